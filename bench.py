@@ -1,0 +1,170 @@
+#!/usr/bin/env python3
+"""Batch-1 greedy decode throughput of Qwen3-0.6B FP16 on one MI355X.
+
+Workload (one "step" = one decode token through all 28 layers, the tied
+lm_head and the device argmax): seeded random-init FP16 weights (pack seed 0,
+N(0, 0.02), norm gains 1.0), the 85-token prompt (ids seed 0) prefilled, then
+W untimed and K timed greedy steps. Weights, KV cache and activations are
+resident in HBM before the timed region. Also reported: TTFT for the 85-,
+1024- and 3968-token prompts, per-kernel times, the roofline of the dominant
+kernel, and the oracle CPU engine timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / 'tests'))
+
+HBM_PEAK_GBS = 8000.0
+KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head']
+# Algorithmic bytes per launch: FP16 weights + FP32 vectors read/written.
+KERNEL_BYTES = {
+    'qkv': 4096 * 1024 * 2 + 1024 * 4 * 2 + 4096 * 4,
+    'o': 1024 * 2048 * 2 + 2048 * 4 + 1024 * 4 * 2,
+    'gate_up': 6144 * 1024 * 2 + 1024 * 4 * 2 + 3072 * 4,
+    'down': 1024 * 3072 * 2 + 3072 * 4 + 1024 * 4 * 2,
+    'lm_head': 151936 * 1024 * 2 + 1024 * 4 * 2 + 151936 * 4,
+}
+
+
+def attention_bytes(n):
+    """K and V rows of 8 heads x 128 FP16 for n positions, plus q/k/v in and out."""
+    return 8 * n * 128 * 2 * 2 + 4096 * 4 + 2048 * 4
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(pack, prompt, seconds):
+    """Oracle engine (CPU restatement) on this host: 12 decode / 6 prefill workers."""
+    from oracle_binding import OracleLib
+    cores = os.cpu_count() or 1
+    decode_threads, prefill_threads = min(12, cores), min(6, cores)
+    oracle = OracleLib().model(pack, decode_threads, prefill_threads, 4096)
+    try:
+        oracle.prefill(prompt)
+        token = int(oracle.logits().argmax())
+        oracle.step(token)  # warmup
+        token = int(oracle.logits().argmax())
+        steps, start = 0, time.perf_counter()
+        while time.perf_counter() - start < seconds:
+            oracle.step(token)
+            token = int(oracle.logits().argmax())
+            steps += 1
+        elapsed = time.perf_counter() - start
+    finally:
+        oracle.close()
+    return dict(value=steps / elapsed, unit='tok/s', cores=decode_threads, kind='port',
+                sample=f'85-token prompt, then {steps} greedy decode steps ({elapsed:.1f} s) with '
+                       f'{decode_threads} decode / {prefill_threads} prefill workers on {cores} host cores')
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument('--gpus', type=int, default=1)
+    parser.add_argument('--steps', type=int, default=256)
+    parser.add_argument('--warmup', type=int, default=16)
+    parser.add_argument('--cpu-seconds', type=float, default=12.0)
+    parser.add_argument('--no-cpu-baseline', action='store_true')
+    parser.add_argument('--no-ttft', action='store_true')
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}); this engine is single-GPU '
+              'batch-1 decode and has no multi-GPU path to time.', file=sys.stderr)
+        return 2
+    if 85 + args.warmup + args.steps > 4096:
+        print('warmup + steps exceed the 4096-token context', file=sys.stderr)
+        return 2
+
+    from conftest import GOLDEN, PACK_CACHE, load_package
+    q = load_package()
+    prompts = json.loads((GOLDEN / 'prompts.json').read_text())
+    pack = q.ensure_random_pack(PACK_CACHE / 'seed0', seed=0)
+    log('pack ready', pack)
+    model = q.Model(pack, context=4096)
+    prompt = prompts['decode_85']
+
+    t0 = time.perf_counter()
+    model.prefill(prompt)
+    token = model.greedy()
+    ttft_85 = time.perf_counter() - t0
+    for _ in range(args.warmup):
+        model.step(token)
+        token = model.greedy()
+    log('warmup done')
+    # Timed region: exactly K greedy steps; each step returns after the device
+    # has finished (stream synchronized inside the engine).
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        model.step(token)
+        token = model.greedy()
+    elapsed = time.perf_counter() - start
+    decode_tps = args.steps / elapsed
+    log(f'decode {decode_tps:.1f} tok/s')
+    context_end = model.position()
+
+    # Per-kernel average durations with HIP events on the engine stream, at
+    # the context length reached by the timed region.
+    kernel_ms = {}
+    for which, name in enumerate(KERNELS):
+        model.reset()
+        model.prefill(prompt)
+        for _ in range(context_end - len(prompt)):
+            model.step(0)
+        kernel_ms[name] = model.time_kernel(which, 200)
+    per_token_ms = {k: v * (1 if k == 'lm_head' else 28) for k, v in kernel_ms.items()}
+    dominant = max(per_token_ms, key=per_token_ms.get)
+    nbytes = attention_bytes(context_end) if dominant == 'attention' else KERNEL_BYTES[dominant]
+    achieved = nbytes / (kernel_ms[dominant] * 1e-3) / 1e9
+    log('kernel ms', kernel_ms)
+
+    ttft = {'85': ttft_85}
+    if not args.no_ttft:
+        for key, name in (('1024', 'prefill_1024'), ('3968', 'long_3968')):
+            model.reset()
+            t0 = time.perf_counter()
+            model.prefill(prompts[name])
+            model.greedy()
+            ttft[key] = time.perf_counter() - t0
+            log(f'ttft {key}: {ttft[key]:.4f} s')
+    model.close()
+
+    baseline = None if args.no_cpu_baseline else cpu_baseline(pack, prompt, args.cpu_seconds)
+    weight_bytes = 1191968768
+    kv_bytes = 114688 * (85 + args.warmup + args.steps / 2)
+    result = {
+        'metric': 'decode tok/s (batch-1 greedy, Qwen3-0.6B FP16, 85-token prompt)',
+        'value': decode_tps,
+        'unit': 'tok/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': 1000.0 / decode_tps,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f16 weights/KV, f32 activations and accumulation',
+        'data': 'synthetic: random-init FP16 weights N(0,0.02) seed 0; prompt ids uniform seed 0',
+        'config': {'workload': 'Qwen3-0.6B FP16 batch-1 greedy decode after an 85-token prompt',
+                   'prompt_tokens': 85, 'context': 4096, 'parallelism': 'none (1 GPU)'},
+        'ttft_s': ttft,
+        'decode_hbm_fraction': (weight_bytes + kv_bytes) * decode_tps / 1e9 / HBM_PEAK_GBS,
+        'kernel_ms': kernel_ms,
+        'roofline': {'kernel': dominant, 'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': None,
+                     'bytes_per_launch': nbytes},
+        'cpu_baseline': baseline,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == '__main__':
+    sys.exit(main())

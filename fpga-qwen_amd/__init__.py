@@ -1,0 +1,230 @@
+"""Python host side of the MI355X Qwen3-0.6B engine (ctypes over the C ABI).
+
+``Model`` mirrors the reference engine API ``qwen_cpu::Model``
+(engine/core.hpp:25-56): reset, truncate, prefill, step, verify_two,
+commit_verified, logits, hidden, position. Errors raise ``RuntimeError`` with
+the engine's message, as the C++ API throws ``std::runtime_error``.
+All inference runs in ``build/libqwen_gpu.so``; there is no CPU fallback:
+importing this module without the built library raises.
+"""
+import ctypes
+import json
+import os
+from pathlib import Path
+
+import numpy as np
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+BUILD_DIR = PACKAGE_DIR / 'build'
+LIBRARY_PATH = BUILD_DIR / 'libqwen_gpu.so'
+CLI_PATH = BUILD_DIR / 'qwen_gpu'
+VOCABULARY = 151936
+HIDDEN = 1024
+PREFIX_REUSE_CHUNK = 512
+EOS = (151643, 151645)
+
+# Every exported symbol of include/qwen_gpu.h with its ctypes signature.
+_c_float_p = ctypes.POINTER(ctypes.c_float)
+_c_int_p = ctypes.POINTER(ctypes.c_int)
+_c_size_p = ctypes.POINTER(ctypes.c_size_t)
+
+
+class Options(ctypes.Structure):
+    """qwen_cpu::Options (engine/core.hpp:11-15)."""
+    _fields_ = [('decode_threads', ctypes.c_int), ('prefill_threads', ctypes.c_int), ('context', ctypes.c_int)]
+
+
+SIGNATURES = {
+    'qwen_gpu_last_error': (ctypes.c_char_p, []),
+    'qwen_gpu_create': (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(Options), ctypes.POINTER(ctypes.c_void_p)]),
+    'qwen_gpu_destroy': (None, [ctypes.c_void_p]),
+    'qwen_gpu_reset': (ctypes.c_int, [ctypes.c_void_p]),
+    'qwen_gpu_truncate': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    'qwen_gpu_prefill': (ctypes.c_int, [ctypes.c_void_p, _c_int_p, ctypes.c_size_t]),
+    'qwen_gpu_step': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    'qwen_gpu_verify_two': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                           ctypes.POINTER(_c_float_p), ctypes.POINTER(_c_float_p), _c_int_p]),
+    'qwen_gpu_commit_verified': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    'qwen_gpu_logits': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_c_float_p), _c_size_p]),
+    'qwen_gpu_hidden': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_c_float_p), _c_size_p]),
+    'qwen_gpu_position': (ctypes.c_int, [ctypes.c_void_p]),
+    'qwen_gpu_lossless_bf16_cache_bytes': (ctypes.c_size_t, [ctypes.c_void_p]),
+    'qwen_gpu_get_options': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Options)]),
+    'qwen_gpu_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
+    'qwen_gpu_verify_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_int_p]),
+    'qwen_gpu_write_random_pack': (ctypes.c_int, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_double, ctypes.c_int]),
+    'qwen_gpu_op_tile_matrix': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_op_gemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_time_kernel': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_float_p]),
+}
+
+
+def load_library(path=LIBRARY_PATH):
+    """Load the engine library; raises if it has not been built."""
+    path = Path(path)
+    if not path.is_file():
+        raise RuntimeError(f'qwen_gpu library not built: {path} (run __graft_entry__.build())')
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+_LIB = load_library()
+
+
+def _check(status):
+    if status != 0:
+        raise RuntimeError(_LIB.qwen_gpu_last_error().decode())
+
+
+class VerificationRows:
+    """qwen_cpu::VerificationRows (engine/core.hpp:16-22), copied to NumPy."""
+
+    def __init__(self, logits, hidden, base_position):
+        self.logits, self.hidden, self.base_position = logits, hidden, base_position
+
+
+class Model:
+    """qwen_cpu::Model on the GPU (engine/core.hpp:25-56)."""
+
+    def __init__(self, weights_file, decode_threads=12, prefill_threads=6, context=4096):
+        handle = ctypes.c_void_p()
+        options = Options(decode_threads, prefill_threads, context)
+        _check(_LIB.qwen_gpu_create(str(weights_file).encode(), ctypes.byref(options), ctypes.byref(handle)))
+        self._handle = handle
+
+    def close(self):
+        if self._handle:
+            _LIB.qwen_gpu_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def reset(self):
+        _check(_LIB.qwen_gpu_reset(self._handle))
+
+    def truncate(self, position):
+        _check(_LIB.qwen_gpu_truncate(self._handle, int(position)))
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        _check(_LIB.qwen_gpu_prefill(self._handle, ids.ctypes.data_as(_c_int_p), ids.size))
+
+    def step(self, token):
+        _check(_LIB.qwen_gpu_step(self._handle, int(token)))
+
+    def verify_two(self, first, second):
+        logits, hidden, base = _c_float_p(), _c_float_p(), ctypes.c_int()
+        _check(_LIB.qwen_gpu_verify_two(self._handle, int(first), int(second), ctypes.byref(logits),
+                                        ctypes.byref(hidden), ctypes.byref(base)))
+        return VerificationRows(np.ctypeslib.as_array(logits, (2, VOCABULARY)).copy(),
+                                np.ctypeslib.as_array(hidden, (2, HIDDEN)).copy(), base.value)
+
+    def commit_verified(self, count):
+        _check(_LIB.qwen_gpu_commit_verified(self._handle, int(count)))
+
+    def logits(self):
+        """Copy of the current FP32 logits; an empty array when there are none."""
+        data, count = _c_float_p(), ctypes.c_size_t()
+        _check(_LIB.qwen_gpu_logits(self._handle, ctypes.byref(data), ctypes.byref(count)))
+        if not count.value:
+            return np.zeros(0, dtype=np.float32)
+        return np.ctypeslib.as_array(data, (count.value,)).copy()
+
+    def hidden(self):
+        data, count = _c_float_p(), ctypes.c_size_t()
+        _check(_LIB.qwen_gpu_hidden(self._handle, ctypes.byref(data), ctypes.byref(count)))
+        return np.ctypeslib.as_array(data, (count.value,)).copy()
+
+    def position(self):
+        return _LIB.qwen_gpu_position(self._handle)
+
+    def lossless_bf16_cache_bytes(self):
+        return _LIB.qwen_gpu_lossless_bf16_cache_bytes(self._handle)
+
+    def options(self):
+        o = Options()
+        _check(_LIB.qwen_gpu_get_options(self._handle, ctypes.byref(o)))
+        return dict(decode_threads=o.decode_threads, prefill_threads=o.prefill_threads, context=o.context)
+
+    def greedy(self):
+        token = ctypes.c_int()
+        _check(_LIB.qwen_gpu_greedy(self._handle, ctypes.byref(token)))
+        return token.value
+
+    def verify_greedy(self):
+        a, b = ctypes.c_int(), ctypes.c_int()
+        _check(_LIB.qwen_gpu_verify_greedy(self._handle, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
+
+    def time_kernel(self, which, iterations):
+        ms = ctypes.c_float()
+        _check(_LIB.qwen_gpu_time_kernel(self._handle, int(which), int(iterations), ctypes.byref(ms)))
+        return ms.value
+
+
+def write_random_pack(path, seed=0, stddev=0.02, threads=None):
+    """Seeded QWCPU01 pack: matrices N(0, stddev) in FP16, norm gains 1.0."""
+    threads = threads or min(16, os.cpu_count() or 1)
+    _check(_LIB.qwen_gpu_write_random_pack(str(path).encode(), int(seed), float(stddev), int(threads)))
+    return Path(path)
+
+
+def ensure_random_pack(directory, seed=0, stddev=0.02):
+    """Reuse ``directory/weights.bin`` when its manifest records the same seed."""
+    directory = Path(directory)
+    directory.mkdir(parents=True, exist_ok=True)
+    path = directory / 'weights.bin'
+    manifest = Path(str(path) + '.manifest.json')
+    if manifest.is_file():
+        info = json.loads(manifest.read_text())
+        synthetic = info.get('synthetic', {})
+        if info.get('completed') and synthetic.get('seed') == seed and synthetic.get('stddev') == stddev:
+            return path
+        raise RuntimeError(f'{manifest} holds a different pack; choose another directory')
+    return write_random_pack(path, seed, stddev)
+
+
+# ---- kernel-level entry points on torch device tensors (memory plumbing) ----
+
+def _ptr(tensor):
+    return ctypes.c_void_p(tensor.data_ptr()) if tensor is not None else None
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def tile_matrix(first, second=None):
+    """Natural FP16 [rows, cols] device tensor(s) -> chain-tiled GEMV layout."""
+    import torch
+    rows, cols = first.shape
+    out_rows = 2 * rows if second is not None else rows
+    out = torch.empty(out_rows * cols, dtype=torch.float16, device=first.device)
+    _check(_LIB.qwen_gpu_op_tile_matrix(_ptr(first), _ptr(second), _ptr(out), rows, cols, _stream()))
+    return out
+
+
+def gemv(tiled, x, rows):
+    """y = W x with the reference dot's chain order (W chain-tiled)."""
+    import torch
+    cols = x.numel()
+    y = torch.empty(rows, dtype=torch.float32, device=x.device)
+    _check(_LIB.qwen_gpu_op_gemv(_ptr(tiled), _ptr(x), _ptr(y), rows, cols, _stream()))
+    return y

@@ -1,0 +1,195 @@
+// extern "C" boundary: exceptions become status codes + a thread-local message.
+#include "qwen_gpu.h"
+
+#include <string>
+
+#include "engine.hpp"
+#include "pack.hpp"
+
+struct qwen_gpu_model {
+    qwen_hip::Engine engine;
+    qwen_gpu_model(const std::string& path, const qwen_hip::Options& o) : engine(path, o) {}
+};
+
+namespace {
+thread_local std::string last_error;
+
+template <class Fn>
+int guarded(Fn&& fn) {
+    try {
+        fn();
+        last_error.clear();
+        return QWEN_GPU_OK;
+    } catch (const std::exception& e) {
+        last_error = e.what();
+    } catch (...) {
+        last_error = "Unknown error";
+    }
+    return QWEN_GPU_ERROR;
+}
+
+void need(const void* p, const char* what) {
+    if (!p) throw std::runtime_error(std::string("Null argument: ") + what);
+}
+}  // namespace
+
+extern "C" {
+
+const char* qwen_gpu_last_error(void) { return last_error.c_str(); }
+
+int qwen_gpu_create(const char* weights, const qwen_gpu_options* options, qwen_gpu_model** out) {
+    return guarded([&] {
+        need(weights, "weights");
+        need(out, "out");
+        *out = nullptr;
+        qwen_hip::Options o;
+        if (options) {
+            o.decode_threads = options->decode_threads;
+            o.prefill_threads = options->prefill_threads;
+            o.context = options->context;
+        }
+        *out = new qwen_gpu_model(weights, o);
+    });
+}
+
+void qwen_gpu_destroy(qwen_gpu_model* model) { delete model; }
+
+int qwen_gpu_reset(qwen_gpu_model* m) {
+    return guarded([&] {
+        need(m, "model");
+        m->engine.reset();
+    });
+}
+
+int qwen_gpu_truncate(qwen_gpu_model* m, int position) {
+    return guarded([&] {
+        need(m, "model");
+        m->engine.truncate(position);
+    });
+}
+
+int qwen_gpu_prefill(qwen_gpu_model* m, const int* ids, size_t count) {
+    return guarded([&] {
+        need(m, "model");
+        if (count) need(ids, "ids");
+        m->engine.prefill(ids, count);
+    });
+}
+
+int qwen_gpu_step(qwen_gpu_model* m, int token) {
+    return guarded([&] {
+        need(m, "model");
+        m->engine.step(token);
+    });
+}
+
+int qwen_gpu_verify_two(qwen_gpu_model* m, int first, int second, const float** logits, const float** hidden,
+                        int* base_position) {
+    return guarded([&] {
+        need(m, "model");
+        need(logits, "logits");
+        need(hidden, "hidden");
+        need(base_position, "base_position");
+        m->engine.verify_two(first, second, logits, hidden, base_position);
+    });
+}
+
+int qwen_gpu_commit_verified(qwen_gpu_model* m, int count) {
+    return guarded([&] {
+        need(m, "model");
+        m->engine.commit_verified(count);
+    });
+}
+
+int qwen_gpu_logits(qwen_gpu_model* m, const float** data, size_t* count) {
+    return guarded([&] {
+        need(m, "model");
+        need(data, "data");
+        need(count, "count");
+        *data = m->engine.logits();
+        *count = *data ? size_t(qwen_hip::kVocab) : 0;
+    });
+}
+
+int qwen_gpu_hidden(qwen_gpu_model* m, const float** data, size_t* count) {
+    return guarded([&] {
+        need(m, "model");
+        need(data, "data");
+        need(count, "count");
+        const float* h = m->engine.hidden();
+        qwen_hip::require(h != nullptr, "No current hidden state");
+        *data = h;
+        *count = size_t(qwen_hip::kHidden);
+    });
+}
+
+int qwen_gpu_position(const qwen_gpu_model* m) { return m ? m->engine.position() : 0; }
+
+size_t qwen_gpu_lossless_bf16_cache_bytes(const qwen_gpu_model*) { return 0; }
+
+int qwen_gpu_get_options(const qwen_gpu_model* m, qwen_gpu_options* options) {
+    return guarded([&] {
+        need(m, "model");
+        need(options, "options");
+        const auto& o = m->engine.options();
+        options->decode_threads = o.decode_threads;
+        options->prefill_threads = o.prefill_threads;
+        options->context = o.context;
+    });
+}
+
+int qwen_gpu_greedy(qwen_gpu_model* m, int* token) {
+    return guarded([&] {
+        need(m, "model");
+        need(token, "token");
+        *token = m->engine.greedy();
+    });
+}
+
+int qwen_gpu_verify_greedy(qwen_gpu_model* m, int* first, int* second) {
+    return guarded([&] {
+        need(m, "model");
+        need(first, "first");
+        need(second, "second");
+        m->engine.verify_greedy(first, second);
+    });
+}
+
+int qwen_gpu_write_random_pack(const char* path, uint64_t seed, double stddev, int threads) {
+    return guarded([&] {
+        need(path, "path");
+        qwen_hip::write_random_pack(path, seed, stddev, threads);
+    });
+}
+
+int qwen_gpu_op_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t* dst, int rows, int cols,
+                            void* stream) {
+    return guarded([&] {
+        need(first, "first");
+        need(dst, "dst");
+        qwen_hip::launch_tile_matrix(first, second, dst, rows, cols, static_cast<hipStream_t>(stream));
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(e));
+    });
+}
+
+int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, int cols, void* stream) {
+    return guarded([&] {
+        need(tiled, "tiled");
+        need(x, "x");
+        need(y, "y");
+        qwen_hip::launch_gemv_plain(tiled, x, y, rows, cols, static_cast<hipStream_t>(stream));
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(e));
+    });
+}
+
+int qwen_gpu_time_kernel(qwen_gpu_model* m, int which, int iterations, float* milliseconds) {
+    return guarded([&] {
+        need(m, "model");
+        need(milliseconds, "milliseconds");
+        *milliseconds = m->engine.time_kernel(which, iterations);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,365 @@
+// Engine: device state, weight upload, captured decode graphs and the
+// qwen_cpu::Model semantics (engine/core.cpp:707-758) on top of them.
+#include "engine.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "pack.hpp"
+
+#define HIP_CHECK(expr)                                                                                  \
+    do {                                                                                                 \
+        const hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess) throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(e_) + \
+                                                       " (" #expr ")");                                  \
+    } while (0)
+
+namespace qwen_hip {
+
+template <class T>
+T* Engine::device_alloc(size_t count) {
+    void* p = nullptr;
+    HIP_CHECK(hipMalloc(&p, count * sizeof(T)));
+    allocations_.push_back(p);
+    return static_cast<T*>(p);
+}
+
+Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
+    // Same check order as the reference constructor: map, option ranges,
+    // header/index (engine/core.cpp:235-276).
+    Pack pack(weights);
+    require(opt.decode_threads >= 1 && opt.decode_threads <= 64 && opt.prefill_threads >= 1 &&
+                opt.prefill_threads <= 64,
+            "Threads must be in 1..64");
+    require(opt.context >= 1 && opt.context <= kMaxContext, "Context must be in 1..4096");
+    pack.validate();
+
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices < 1)
+        throw std::runtime_error("No HIP device available");
+    try {
+        HIP_CHECK(hipSetDevice(0));
+        HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+        const int ctx = opt.context;
+
+        // Embedding: natural copy (gather) and chain-tiled copy (tied head).
+        const PackTensor& emb = pack.tensor("model.embed_tokens.weight");
+        embed_ = device_alloc<uint16_t>(size_t(kVocab) * kHidden);
+        HIP_CHECK(hipMemcpy(embed_, emb.half, size_t(kVocab) * kHidden * 2, hipMemcpyHostToDevice));
+        lm_t_ = device_alloc<uint16_t>(size_t(kVocab) * kHidden);
+        launch_tile_matrix(embed_, nullptr, lm_t_, kVocab, kHidden, stream_);
+        final_norm_ = device_alloc<float>(kHidden);
+        HIP_CHECK(hipMemcpy(final_norm_, pack.tensor("model.norm.weight").norm, kHidden * 4, hipMemcpyHostToDevice));
+
+        // Layer matrices go through a natural-layout staging buffer, then into
+        // their chain-tiled homes.
+        uint16_t* stage = device_alloc<uint16_t>(size_t(2 * kFFN) * kHidden);
+        auto upload = [&](uint16_t* dst, const PackTensor& t) {
+            HIP_CHECK(hipMemcpy(dst, t.half, size_t(t.rows) * t.cols * 2, hipMemcpyHostToDevice));
+        };
+        auto upload_norm = [&](const PackTensor& t) {
+            float* d = device_alloc<float>(t.rows);
+            HIP_CHECK(hipMemcpy(d, t.norm, size_t(t.rows) * 4, hipMemcpyHostToDevice));
+            return d;
+        };
+        layers_.resize(kLayers);
+        for (int l = 0; l < kLayers; ++l) {
+            LayerDevice& L = layers_[l];
+            uint16_t* qkv_t = device_alloc<uint16_t>(size_t(kQKVRows) * kHidden);
+            upload(stage, pack.layer(l, "self_attn.q_proj.weight"));
+            upload(stage + size_t(kQDim) * kHidden, pack.layer(l, "self_attn.k_proj.weight"));
+            upload(stage + size_t(kQDim + kKVDim) * kHidden, pack.layer(l, "self_attn.v_proj.weight"));
+            launch_tile_matrix(stage, nullptr, qkv_t, kQKVRows, kHidden, stream_);
+            HIP_CHECK(hipStreamSynchronize(stream_));
+            uint16_t* o_t = device_alloc<uint16_t>(size_t(kHidden) * kQDim);
+            upload(stage, pack.layer(l, "self_attn.o_proj.weight"));
+            launch_tile_matrix(stage, nullptr, o_t, kHidden, kQDim, stream_);
+            HIP_CHECK(hipStreamSynchronize(stream_));
+            uint16_t* gu_t = device_alloc<uint16_t>(size_t(2 * kFFN) * kHidden);
+            upload(stage, pack.layer(l, "mlp.gate_proj.weight"));
+            upload(stage + size_t(kFFN) * kHidden, pack.layer(l, "mlp.up_proj.weight"));
+            launch_tile_matrix(stage, stage + size_t(kFFN) * kHidden, gu_t, kFFN, kHidden, stream_);
+            HIP_CHECK(hipStreamSynchronize(stream_));
+            uint16_t* down_t = device_alloc<uint16_t>(size_t(kHidden) * kFFN);
+            upload(stage, pack.layer(l, "mlp.down_proj.weight"));
+            launch_tile_matrix(stage, nullptr, down_t, kHidden, kFFN, stream_);
+            HIP_CHECK(hipStreamSynchronize(stream_));
+            L.qkv_t = qkv_t;
+            L.o_t = o_t;
+            L.gateup_t = gu_t;
+            L.down_t = down_t;
+            L.in_norm = upload_norm(pack.layer(l, "input_layernorm.weight"));
+            L.post_norm = upload_norm(pack.layer(l, "post_attention_layernorm.weight"));
+            L.q_norm = upload_norm(pack.layer(l, "self_attn.q_norm.weight"));
+            L.k_norm = upload_norm(pack.layer(l, "self_attn.k_norm.weight"));
+            L.keys = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
+            L.values = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
+        }
+
+        // RoPE tables in double, stored as FP32 (engine/core.cpp:287-288).
+        std::vector<float> cs(size_t(ctx) * 64), sn(cs.size());
+        for (int p = 0; p < ctx; ++p)
+            for (int j = 0; j < 64; ++j) {
+                const double angle = p / std::pow(1000000.0, 2.0 * j / kHeadDim);
+                cs[size_t(p) * 64 + j] = float(std::cos(angle));
+                sn[size_t(p) * 64 + j] = float(std::sin(angle));
+            }
+        cosines_ = device_alloc<float>(cs.size());
+        sines_ = device_alloc<float>(sn.size());
+        HIP_CHECK(hipMemcpy(cosines_, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(sines_, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+
+        DecodeScratch& s = scratch_;
+        s.x = device_alloc<float>(kHidden);
+        s.qkv = device_alloc<float>(kQKVRows);
+        s.attended = device_alloc<float>(kQDim);
+        s.act = device_alloc<float>(kFFN);
+        s.logits = device_alloc<float>(kVocab);
+        s.hidden = device_alloc<float>(kHidden);
+        s.attn_partial = device_alloc<float>(size_t(kKVHeads) * kAttnSplits * kAttnPartial);
+        s.attn_count = device_alloc<unsigned>(kKVHeads);
+        s.lm_value = device_alloc<float>(kLmGroups);
+        s.lm_index = device_alloc<int>(kLmGroups);
+        s.lm_bad = device_alloc<int>(kLmGroups);
+        s.lm_count = device_alloc<unsigned>(1);
+        s.result = device_alloc<ArgmaxResult>(1);
+        HIP_CHECK(hipMemset(s.attn_count, 0, kKVHeads * sizeof(unsigned)));
+        HIP_CHECK(hipMemset(s.lm_count, 0, sizeof(unsigned)));
+        ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
+        ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
+        base_logits_ = device_alloc<float>(kVocab);
+        base_hidden_ = device_alloc<float>(kHidden);
+        params_dev_ = device_alloc<StepParams>(1);
+        void* pinned = nullptr;
+        HIP_CHECK(hipHostMalloc(&pinned, sizeof(StepParams) * size_t(ctx), hipHostMallocDefault));
+        params_host_ = static_cast<StepParams*>(pinned);
+        HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
+        result_host_ = static_cast<ArgmaxResult*>(pinned);
+        std::memset(result_host_, 0, sizeof(ArgmaxResult) * 3);
+        HIP_CHECK(hipStreamSynchronize(stream_));
+        HIP_CHECK(hipFree(stage));
+        allocations_.erase(std::find(allocations_.begin(), allocations_.end(), static_cast<void*>(stage)));
+
+        // Capture: all 28 layers in one graph, the head in another. Kernels
+        // read position/token from params_dev_, so each graph is replayed as is.
+        HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+        for (int l = 0; l < kLayers; ++l)
+            launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, params_dev_, cosines_, sines_, ctx, scratch_,
+                                stream_);
+        HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[0]));
+        HIP_CHECK(hipGraphInstantiate(&layer_graph_, graphs_[0], nullptr, nullptr, 0));
+        HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+        launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
+        HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[1]));
+        HIP_CHECK(hipGraphInstantiate(&head_graph_, graphs_[1], nullptr, nullptr, 0));
+        HIP_CHECK(hipGetLastError());
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+void Engine::release() {
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (layer_graph_) (void)hipGraphExecDestroy(layer_graph_);
+    if (head_graph_) (void)hipGraphExecDestroy(head_graph_);
+    for (hipGraph_t g : graphs_)
+        if (g) (void)hipGraphDestroy(g);
+    for (void* p : allocations_) (void)hipFree(p);
+    if (params_host_) (void)hipHostFree(params_host_);
+    if (result_host_) (void)hipHostFree(result_host_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+    layer_graph_ = head_graph_ = nullptr;
+    graphs_[0] = graphs_[1] = nullptr;
+    allocations_.clear();
+    params_host_ = nullptr;
+    result_host_ = nullptr;
+    stream_ = nullptr;
+}
+
+Engine::~Engine() { release(); }
+
+void Engine::sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
+
+void Engine::invalidate() {
+    has_logits_ = false;
+    host_logits_valid_ = host_hidden_valid_ = false;
+}
+
+// engine/core.cpp:718-721
+void Engine::reset() {
+    pos_ = 0;
+    pending_ = false;
+    invalidate();
+}
+
+// engine/core.cpp:722-727
+void Engine::truncate(int position) {
+    require(position >= 0 && position <= pos_, "Rewind position out of range");
+    pos_ = position;
+    pending_ = false;
+    invalidate();
+}
+
+void Engine::run_token(int token, bool head, int result_slot) {
+    StepParams& slot = params_host_[pos_];
+    slot.pos = pos_;
+    slot.token = token;
+    HIP_CHECK(hipMemcpyAsync(params_dev_, &slot, sizeof(StepParams), hipMemcpyHostToDevice, stream_));
+    HIP_CHECK(hipGraphLaunch(layer_graph_, stream_));
+    if (head) {
+        HIP_CHECK(hipGraphLaunch(head_graph_, stream_));
+        HIP_CHECK(hipMemcpyAsync(result_host_ + result_slot, scratch_.result, sizeof(ArgmaxResult),
+                                 hipMemcpyDeviceToHost, stream_));
+    }
+    ++pos_;
+}
+
+// engine/core.cpp:707-714: validate everything before mutating, then run.
+void Engine::append(const int* ids, size_t count) {
+    require(!pending_, "Commit or discard pending verification before inference");
+    require(count > 0, "Empty token input");
+    require(count <= size_t(options_.context - pos_), "Context capacity exceeded");
+    for (size_t i = 0; i < count; ++i) require(ids[i] >= 0 && ids[i] < kVocab, "Token ID out of range");
+    invalidate();
+    for (size_t i = 0; i < count; ++i) run_token(ids[i], i + 1 == count, 0);
+    sync();
+    has_logits_ = true;
+}
+
+void Engine::prefill(const int* ids, size_t count) { append(ids, count); }
+void Engine::step(int token) { append(&token, 1); }
+
+const float* Engine::logits() {
+    if (!has_logits_) return nullptr;
+    if (!host_logits_valid_) {
+        host_logits_.resize(kVocab);
+        HIP_CHECK(hipMemcpy(host_logits_.data(), scratch_.logits, size_t(kVocab) * 4, hipMemcpyDeviceToHost));
+        host_logits_valid_ = true;
+    }
+    return host_logits_.data();
+}
+
+const float* Engine::hidden() {
+    if (!has_logits_ || pos_ <= 0) return nullptr;
+    if (!host_hidden_valid_) {
+        host_hidden_.resize(kHidden);
+        HIP_CHECK(hipMemcpy(host_hidden_.data(), scratch_.hidden, size_t(kHidden) * 4, hipMemcpyDeviceToHost));
+        host_hidden_valid_ = true;
+    }
+    return host_hidden_.data();
+}
+
+int Engine::greedy() {
+    require(has_logits_, "No current full-vocabulary logits");
+    if (result_host_[0].nonfinite) throw std::runtime_error("Nonfinite model logits");
+    return result_host_[0].token;
+}
+
+// engine/core.cpp:729-741: two B1 steps; public state stays at the base.
+void Engine::verify_two(int first, int second, const float** logits, const float** hidden, int* base) {
+    require(!pending_, "Verification already pending");
+    require(first >= 0 && first < kVocab && second >= 0 && second < kVocab, "Token ID out of range");
+    require(pos_ <= options_.context - 2, "Context capacity exceeded");
+    const int start = pos_;
+    try {
+        if (has_logits_) {
+            HIP_CHECK(hipMemcpyAsync(base_logits_, scratch_.logits, size_t(kVocab) * 4, hipMemcpyDeviceToDevice,
+                                     stream_));
+            HIP_CHECK(hipMemcpyAsync(base_hidden_, scratch_.hidden, size_t(kHidden) * 4, hipMemcpyDeviceToDevice,
+                                     stream_));
+        }
+        const int ids[2] = {first, second};
+        for (int row = 0; row < 2; ++row) {
+            run_token(ids[row], true, 1 + row);
+            HIP_CHECK(hipMemcpyAsync(ver_logits_ + size_t(row) * kVocab, scratch_.logits, size_t(kVocab) * 4,
+                                     hipMemcpyDeviceToDevice, stream_));
+            HIP_CHECK(hipMemcpyAsync(ver_hidden_ + size_t(row) * kHidden, scratch_.hidden, size_t(kHidden) * 4,
+                                     hipMemcpyDeviceToDevice, stream_));
+        }
+        if (has_logits_) {
+            HIP_CHECK(hipMemcpyAsync(scratch_.logits, base_logits_, size_t(kVocab) * 4, hipMemcpyDeviceToDevice,
+                                     stream_));
+            HIP_CHECK(hipMemcpyAsync(scratch_.hidden, base_hidden_, size_t(kHidden) * 4, hipMemcpyDeviceToDevice,
+                                     stream_));
+        }
+        host_ver_logits_.resize(size_t(2) * kVocab);
+        host_ver_hidden_.resize(size_t(2) * kHidden);
+        HIP_CHECK(hipMemcpyAsync(host_ver_logits_.data(), ver_logits_, size_t(2) * kVocab * 4, hipMemcpyDeviceToHost,
+                                 stream_));
+        HIP_CHECK(hipMemcpyAsync(host_ver_hidden_.data(), ver_hidden_, size_t(2) * kHidden * 4,
+                                 hipMemcpyDeviceToHost, stream_));
+        sync();
+        pos_ = start;
+        pending_ = true;
+    } catch (...) {
+        reset();
+        throw;
+    }
+    *logits = host_ver_logits_.data();
+    *hidden = host_ver_hidden_.data();
+    *base = start;
+}
+
+void Engine::verify_greedy(int* first, int* second) {
+    require(pending_, "No verification pending");
+    for (int row = 0; row < 2; ++row)
+        if (result_host_[1 + row].nonfinite) throw std::runtime_error("Nonfinite model logits");
+    *first = result_host_[1].token;
+    *second = result_host_[2].token;
+}
+
+// engine/core.cpp:742-752
+void Engine::commit_verified(int count) {
+    require(pending_, "No verification pending");
+    require(count == 1 || count == 2, "Commit count must be one or two");
+    try {
+        const int row = count - 1;
+        HIP_CHECK(hipMemcpyAsync(scratch_.logits, ver_logits_ + size_t(row) * kVocab, size_t(kVocab) * 4,
+                                 hipMemcpyDeviceToDevice, stream_));
+        HIP_CHECK(hipMemcpyAsync(scratch_.hidden, ver_hidden_ + size_t(row) * kHidden, size_t(kHidden) * 4,
+                                 hipMemcpyDeviceToDevice, stream_));
+        sync();
+        result_host_[0] = result_host_[1 + row];
+        invalidate();
+        has_logits_ = true;
+        pos_ += count;
+        pending_ = false;
+    } catch (...) {
+        reset();
+        throw;
+    }
+}
+
+float Engine::time_kernel(int which, int iterations) {
+    require(pos_ > 0 && !pending_, "time_kernel needs a current position");
+    require(which >= 0 && which <= 5 && iterations > 0, "time_kernel: bad arguments");
+    // Replays kernels of the last processed position; the state is reset afterwards.
+    StepParams& slot = params_host_[pos_ - 1];
+    HIP_CHECK(hipMemcpyAsync(params_dev_, &slot, sizeof(StepParams), hipMemcpyHostToDevice, stream_));
+    const int layer = kLayers / 2;
+    auto launch = [&] {
+        if (which == 5)
+            launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
+        else
+            launch_layer_kernel(which, layers_[layer], nullptr, params_dev_, cosines_, sines_, options_.context,
+                                scratch_, stream_);
+    };
+    launch();
+    hipEvent_t start, stop;
+    HIP_CHECK(hipEventCreate(&start));
+    HIP_CHECK(hipEventCreate(&stop));
+    HIP_CHECK(hipEventRecord(start, stream_));
+    for (int i = 0; i < iterations; ++i) launch();
+    HIP_CHECK(hipEventRecord(stop, stream_));
+    HIP_CHECK(hipEventSynchronize(stop));
+    float ms = 0.f;
+    HIP_CHECK(hipEventElapsedTime(&ms, start, stop));
+    (void)hipEventDestroy(start);
+    (void)hipEventDestroy(stop);
+    reset();
+    return ms / float(iterations);
+}
+
+}  // namespace qwen_hip

@@ -1,0 +1,87 @@
+// HIP engine for the Qwen3-0.6B FP16 path: the device-side replacement of
+// qwen_cpu::Model::Impl (engine/core.cpp:220-758).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+
+namespace qwen_hip {
+
+struct Options {
+    int decode_threads = 12;   // accepted and echoed (engine/core.hpp:11-15)
+    int prefill_threads = 6;
+    int context = 4096;
+};
+
+class Engine {
+public:
+    Engine(const std::string& weights, Options options);
+    ~Engine();
+    Engine(const Engine&) = delete;
+    Engine& operator=(const Engine&) = delete;
+
+    void reset();
+    void truncate(int position);
+    void prefill(const int* ids, size_t count);
+    void step(int token);
+    // Two consumed ids with B1 arithmetic; rows stay pending until commit.
+    void verify_two(int first, int second, const float** logits, const float** hidden, int* base);
+    void commit_verified(int count);
+    // Host copies of the current logits/hidden (nullptr when none).
+    const float* logits();
+    const float* hidden();
+    int position() const { return pos_; }
+    // Device greedy selection of the current logits (engine/main.cpp:51-59).
+    int greedy();
+    // Greedy selections of the pending verification rows.
+    void verify_greedy(int* first, int* second);
+    const Options& options() const { return options_; }
+
+    // Average duration (ms) of one standalone launch of a decode kernel,
+    // timed with HIP events on the engine stream. which: 0 qkv, 1 attention,
+    // 2 o, 3 gate/up, 4 down, 5 lm_head. Requires position() > 0.
+    float time_kernel(int which, int iterations);
+    hipStream_t stream() const { return stream_; }
+
+private:
+    void append(const int* ids, size_t count);
+    void run_token(int token, bool head, int result_slot);
+    void release();
+    void sync();
+    void invalidate();
+
+    Options options_;
+    hipStream_t stream_ = nullptr;
+    std::vector<void*> allocations_;
+    std::vector<LayerDevice> layers_;
+    uint16_t* embed_ = nullptr;     // natural [vocab x 1024]
+    uint16_t* lm_t_ = nullptr;      // chain-tiled embedding
+    float* final_norm_ = nullptr;
+    float* cosines_ = nullptr;
+    float* sines_ = nullptr;
+    DecodeScratch scratch_{};
+    StepParams* params_host_ = nullptr;  // pinned ring, one slot per position
+    StepParams* params_dev_ = nullptr;   // device slot read by the captured kernels
+    ArgmaxResult* result_host_ = nullptr;  // pinned [3]: current, verify row 0, verify row 1
+    hipGraphExec_t layer_graph_ = nullptr;  // 28 decode layers
+    hipGraphExec_t head_graph_ = nullptr;   // final norm + lm_head + argmax
+    hipGraph_t graphs_[2] = {nullptr, nullptr};
+    float* ver_logits_ = nullptr;   // device [2 x vocab]
+    float* ver_hidden_ = nullptr;   // device [2 x 1024]
+    float* base_logits_ = nullptr;  // public logits saved across a verification
+    float* base_hidden_ = nullptr;
+    int pos_ = 0;
+    bool has_logits_ = false;
+    bool pending_ = false;
+    std::vector<float> host_logits_, host_hidden_, host_ver_logits_, host_ver_hidden_;
+    bool host_logits_valid_ = false, host_hidden_valid_ = false;
+
+    template <class T>
+    T* device_alloc(size_t count);
+};
+
+}  // namespace qwen_hip

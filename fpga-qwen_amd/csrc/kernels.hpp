@@ -1,0 +1,99 @@
+// Device-side data layout and kernel launchers of the decode engine.
+//
+// Chain-tiled matrix layout (for batch-1 GEMV). The reference dot product
+// (engine/core.cpp:119-127) accumulates column j of a row into FP32 chain
+// c = j % 8 with fused multiply-adds in ascending j, then combines
+// ((c0+c4)+(c1+c5)) + ((c2+c6)+(c3+c7)). A GEMV thread owns one chain of one
+// row. Rows are grouped in tiles of 8; within a tile, block b holds, for each
+// thread t = 8*r + c, the 8 halves {W[8T+r][64b + 8i + c] : i = 0..7}
+// contiguously (16 bytes). One wavefront therefore reads 1 KiB contiguous per
+// 16-byte load, and each thread's halves arrive in its chain order.
+//   tiled[(((T * NB) + b) * 64 + t) * 8 + i],  NB = cols / 64.
+//
+// KV cache: [layer][kv head][position][128] FP16 (engine/core.cpp:350-352).
+// Key rows are stored chain-permuted, key'[c*16 + s] = key[8s + c], so the
+// 8 threads scoring one position each read 32 contiguous bytes in chain
+// order. Value rows are stored in natural channel order.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "qwen_common.hpp"
+
+namespace qwen_hip {
+
+// Per-step scalars, device resident so captured graphs are position independent.
+struct StepParams {
+    int pos;    // position being written (tokens before it are cached)
+    int token;  // input token id
+};
+
+// Greedy selection result of the lm_head kernel.
+struct ArgmaxResult {
+    int token;
+    int nonfinite;
+};
+
+inline constexpr int kAttnSplits = 32;          // max position splits per KV head
+inline constexpr int kAttnPartial = 2 * 132;    // per split: 2 heads x (128 o + m + l + pad)
+inline constexpr int kLmWaves = 4;              // lm_head workgroup waves
+inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 4748 workgroups
+static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
+
+struct LayerDevice {
+    const uint16_t* qkv_t;     // tiled [4096 x 1024]: q rows, k rows, v rows
+    const uint16_t* o_t;       // tiled [1024 x 2048]
+    const uint16_t* gateup_t;  // tiled [6144 x 1024]: tile T = gate rows 4T..4T+3, up rows 4T..4T+3
+    const uint16_t* down_t;    // tiled [1024 x 3072]
+    const float* in_norm;      // [1024]
+    const float* post_norm;    // [1024]
+    const float* q_norm;       // [128]
+    const float* k_norm;       // [128]
+    uint16_t* keys;            // [8][context][128], chain-permuted rows
+    uint16_t* values;          // [8][context][128]
+};
+
+struct DecodeScratch {
+    float* x;             // [1024] residual stream
+    float* qkv;           // [4096] raw projections
+    float* attended;      // [2048]
+    float* act;           // [3072]
+    float* logits;        // [151936]
+    float* hidden;        // [1024] final normalized hidden
+    float* attn_partial;  // [8][kAttnSplits][kAttnPartial]
+    unsigned* attn_count; // [8], zero between launches
+    float* lm_value;      // [kLmGroups]
+    int* lm_index;        // [kLmGroups]
+    int* lm_bad;          // [kLmGroups]
+    unsigned* lm_count;   // [1], zero between launches
+    ArgmaxResult* result; // [1]
+};
+
+// Layout conversion: natural row-major FP16 [rows x cols] -> chain-tiled.
+// When `second` is non-null the tiles interleave two matrices of equal shape:
+// tile T holds rows 4T..4T+3 of `first` then rows 4T..4T+3 of `second`.
+void launch_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t* dst, int rows, int cols,
+                        hipStream_t stream);
+
+// y[r] = dot(x, W[r]) with the reference chain order; W chain-tiled, cols in
+// {1024, 2048, 3072}, rows a multiple of 8 * waves (waves = 2).
+void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, int cols, hipStream_t stream);
+
+// One decode layer (five kernels): norm+QKV, attention (+q/k norm, RoPE, KV
+// write, split combine), O (+residual), norm+gate/up (+SwiGLU), down (+residual).
+// When `embed` is non-null (first layer) x is first loaded from embed[token].
+void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, const StepParams* params,
+                         const float* cosines, const float* sines, int context, const DecodeScratch& s,
+                         hipStream_t stream);
+
+// One kernel of a decode layer: 0 norm+QKV, 1 attention, 2 O, 3 norm+gate/up, 4 down.
+void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, const StepParams* params,
+                         const float* cosines, const float* sines, int context, const DecodeScratch& s,
+                         hipStream_t stream);
+
+// Final norm + tied lm_head GEMV + greedy argmax (lowest id on ties,
+// nonfinite flagged). Also writes the final hidden vector.
+void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, hipStream_t stream);
+
+}  // namespace qwen_hip

@@ -1,0 +1,105 @@
+/* qwen_gpu: C ABI of the MI355X (gfx950) Qwen3-0.6B FP16 engine.
+ *
+ * Drop-in boundary for the reference's native engine API, qwen_cpu::Model
+ * (engine/core.hpp:8-56), exported as plain C: opaque handle, plain pointers
+ * and sizes, integer status codes, no exceptions and no C++/torch types.
+ * Every function returns QWEN_GPU_OK (0) on success; on failure it returns
+ * QWEN_GPU_ERROR and qwen_gpu_last_error() (per calling thread) holds the
+ * message, using the reference's wording (engine/core.cpp:235-276, 707-752).
+ * One caller at a time per model (engine/core.hpp:23).
+ */
+#ifndef QWEN_GPU_H
+#define QWEN_GPU_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWEN_GPU_OK 0
+#define QWEN_GPU_ERROR 1
+#define QWEN_GPU_VOCABULARY 151936          /* qwen_cpu::vocabulary, engine/core.hpp:9 */
+#define QWEN_GPU_HIDDEN 1024
+#define QWEN_GPU_PREFIX_REUSE_CHUNK 512     /* qwen_cpu::prefix_reuse_chunk, engine/core.hpp:10 */
+
+typedef struct qwen_gpu_model qwen_gpu_model;
+
+/* qwen_cpu::Options (engine/core.hpp:11-15). Thread counts are validated
+ * (1..64) and echoed; context is 1..4096. */
+typedef struct qwen_gpu_options {
+    int decode_threads;
+    int prefill_threads;
+    int context;
+} qwen_gpu_options;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* qwen_gpu_last_error(void);
+
+/* qwen_cpu::Model::Model(weights_file, Options), engine/core.hpp:28 and
+ * engine/core.cpp:235-290: maps and validates the QWCPU01 pack, then uploads
+ * it to GPU 0. options == NULL means {12, 6, 4096}. */
+int qwen_gpu_create(const char* weights, const qwen_gpu_options* options, qwen_gpu_model** out);
+/* qwen_cpu::Model::~Model, engine/core.hpp:29. NULL is ignored. */
+void qwen_gpu_destroy(qwen_gpu_model* model);
+
+/* Model::reset, engine/core.hpp:32; engine/core.cpp:718-721. */
+int qwen_gpu_reset(qwen_gpu_model* model);
+/* Model::truncate(position), engine/core.hpp:35; engine/core.cpp:722-727. */
+int qwen_gpu_truncate(qwen_gpu_model* model, int position);
+/* Model::prefill(ids), engine/core.hpp:37; engine/core.cpp:727,707-714. */
+int qwen_gpu_prefill(qwen_gpu_model* model, const int* ids, size_t count);
+/* Model::step(token), engine/core.hpp:38; engine/core.cpp:728. */
+int qwen_gpu_step(qwen_gpu_model* model, int token);
+/* Model::verify_two(first, second) -> VerificationRows, engine/core.hpp:17-22,43;
+ * engine/core.cpp:729-741. Borrowed row-major [2 x 151936] logits and
+ * [2 x 1024] hidden, valid until commit/reset/truncate or another mutation. */
+int qwen_gpu_verify_two(qwen_gpu_model* model, int first, int second, const float** logits,
+                        const float** hidden, int* base_position);
+/* Model::commit_verified(count), engine/core.hpp:46; engine/core.cpp:742-752. */
+int qwen_gpu_commit_verified(qwen_gpu_model* model, int count);
+/* Model::logits(), engine/core.hpp:47; engine/core.cpp:753. Borrowed FP32
+ * [151936] valid until the next mutation; *count is 0 when there are none. */
+int qwen_gpu_logits(qwen_gpu_model* model, const float** data, size_t* count);
+/* Model::hidden(), engine/core.hpp:48-50; engine/core.cpp:754-757. Fails with
+ * "No current hidden state" when there are no current logits. */
+int qwen_gpu_hidden(qwen_gpu_model* model, const float** data, size_t* count);
+/* Model::position(), engine/core.hpp:51. Returns the position (not a status). */
+int qwen_gpu_position(const qwen_gpu_model* model);
+/* Model::lossless_bf16_cache_bytes(), engine/core.hpp:53; always 0 (engine/core.cpp:759). */
+size_t qwen_gpu_lossless_bf16_cache_bytes(const qwen_gpu_model* model);
+/* Options actually in effect (echoed by the protocol handshake, engine/main.cpp:71-79). */
+int qwen_gpu_get_options(const qwen_gpu_model* model, qwen_gpu_options* options);
+
+/* Greedy Sampler::select of the current logits (engine/main.cpp:51-59):
+ * lowest id among maxima, computed on the GPU without copying the logits.
+ * Fails with "Nonfinite model logits" or "No current full-vocabulary logits". */
+int qwen_gpu_greedy(qwen_gpu_model* model, int* token);
+/* Greedy selections of both pending verification rows (engine/main.cpp:138,142). */
+int qwen_gpu_verify_greedy(qwen_gpu_model* model, int* first, int* second);
+
+/* Synthetic QWCPU01 pack (format: engine/INTERFACE.md:8-21; tensor order of
+ * tools/export_native_cpu_weights.py:29-39): matrices N(0, stddev) rounded to
+ * FP16 from a counter-based splitmix64 Box-Muller stream, norm gains 1.0.
+ * Writes PATH, PATH.index and PATH.manifest.json; refuses existing outputs. */
+int qwen_gpu_write_random_pack(const char* path, uint64_t seed, double stddev, int threads);
+
+/* Kernel-level entry points on caller-owned device memory (stream may be
+ * NULL for the default stream); used by parity tests and the GEMV microbench.
+ * Converts natural row-major FP16 [rows x cols] to the engine's chain-tiled
+ * GEMV layout; second != NULL interleaves two equal-shape matrices by 4 rows. */
+int qwen_gpu_op_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t* dst, int rows, int cols,
+                            void* stream);
+/* y[r] = dot(x, W[r]) with the reference dot's chain order (engine/core.cpp:119-147),
+ * W chain-tiled; cols in {1024, 2048, 3072}; rows a multiple of 16. */
+int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, int cols, void* stream);
+/* Average milliseconds of one standalone launch of a decode kernel on the
+ * model's stream, timed with HIP events (which: 0 norm+QKV, 1 attention,
+ * 2 O, 3 norm+gate/up, 4 down, 5 lm_head). Needs position() > 0; resets the
+ * model afterwards. */
+int qwen_gpu_time_kernel(qwen_gpu_model* model, int which, int iterations, float* milliseconds);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

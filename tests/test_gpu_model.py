@@ -1,0 +1,167 @@
+"""Whole-model parity and lifecycle invariants of the GPU engine.
+
+Parity follows the reference's oracle pipeline (tools/check_native_logits.py):
+the GPU trajectory's consumed ids are replayed through the oracle and every
+position's full-vocabulary logits must pass max-abs 1e-2, RMS 2e-3 and greedy
+identity (tools/check_native_saved_oracle.py:36). Lifecycle invariants follow
+tools/native_verify_check.cpp and tools/check_native_cpu_robustness.py:
+bit-identical repeats, verify == two steps, validation before mutation.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_binding import compare_logits
+
+PROMPTS = json.loads((Path(__file__).parent / 'golden' / 'prompts.json').read_text())
+V = 151936
+
+
+@pytest.fixture(scope='module')
+def gpu_model(qpkg, pack0):
+    model = qpkg.Model(pack0, context=4096)
+    yield model
+    model.close()
+
+
+@pytest.fixture(scope='module')
+def oracle_model(oracle_lib, pack0):
+    model = oracle_lib.model(pack0, 16, 16, 4096)
+    yield model
+    model.close()
+
+
+def greedy_trajectory(model, prompt, steps):
+    model.reset()
+    model.prefill(prompt)
+    rows = []
+    token = model.greedy()
+    rows.append((model.logits(), token))
+    for _ in range(steps - 1):
+        model.step(token)
+        token = model.greedy()
+        rows.append((model.logits(), token))
+    return rows
+
+
+@pytest.mark.gpu
+def test_decode_85_matches_oracle(gpu_model, oracle_model):
+    """85-token prompt (seed 0) + 32 greedy tokens: every position in the gate."""
+    prompt = PROMPTS['decode_85']
+    rows = greedy_trajectory(gpu_model, prompt, 32)
+    assert gpu_model.position() == 85 + 31
+    oracle_model.reset()
+    oracle_model.prefill(prompt)
+    worst = dict(max_abs=0.0, rms=0.0)
+    for i, (logits, token) in enumerate(rows):
+        if i:
+            oracle_model.step(rows[i - 1][1])
+        assert token == int(np.argmax(logits)), 'device greedy disagrees with the logits'
+        result = compare_logits(logits, oracle_model.logits())
+        worst = dict(max_abs=max(worst['max_abs'], result['max_abs']), rms=max(worst['rms'], result['rms']))
+        assert result['passed'], (i, result)
+    print('worst', worst)
+
+
+@pytest.mark.gpu
+def test_repeat_is_bit_identical(gpu_model):
+    prompt = PROMPTS['decode_85'][:20]
+    a = greedy_trajectory(gpu_model, prompt, 4)
+    b = greedy_trajectory(gpu_model, prompt, 4)
+    for (la, ta), (lb, tb) in zip(a, b):
+        assert ta == tb
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_prefill_equals_steps_and_truncate(gpu_model):
+    """Token-at-a-time equivalence and rewind: KV before the cut is retained."""
+    prompt = PROMPTS['decode_85'][:12]
+    gpu_model.reset()
+    gpu_model.prefill(prompt)
+    full = gpu_model.logits()
+    gpu_model.truncate(7)
+    assert gpu_model.position() == 7 and gpu_model.logits().size == 0
+    with pytest.raises(RuntimeError, match='No current hidden state'):
+        gpu_model.hidden()
+    gpu_model.prefill(prompt[7:])
+    assert np.array_equal(gpu_model.logits().view(np.uint32), full.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('prefix,commit', [(0, 1), (0, 2), (1, 1), (1, 2), (513, 2)])
+def test_verify_two_equals_two_steps(qpkg, pack0, gpu_model, prefix, commit):
+    """tools/native_verify_check.cpp normal_case, against a second model."""
+    ids = [32 + (i * 37) % 1000 for i in range(prefix)]
+    ref = qpkg.Model(pack0, context=4096)
+    try:
+        for m in (gpu_model, ref):
+            m.reset()
+            if prefix:
+                m.prefill(ids)
+        base_logits = gpu_model.logits()
+        for bad in ((-1, 11), (9707, V)):
+            with pytest.raises(RuntimeError, match='Token ID out of range'):
+                gpu_model.verify_two(*bad)
+        with pytest.raises(RuntimeError, match='No verification pending'):
+            gpu_model.commit_verified(1)
+        rows = gpu_model.verify_two(9707, 11)
+        assert rows.base_position == prefix and rows.logits.shape == (2, V) and rows.hidden.shape == (2, 1024)
+        assert gpu_model.position() == prefix
+        assert np.array_equal(gpu_model.logits().view(np.uint32), base_logits.view(np.uint32))
+        ref.step(9707)
+        first = (ref.logits(), ref.hidden())
+        ref.step(11)
+        second = (ref.logits(), ref.hidden())
+        for row, (l, h) in enumerate((first, second)):
+            assert np.array_equal(rows.logits[row].view(np.uint32), l.view(np.uint32))
+            assert np.array_equal(rows.hidden[row].view(np.uint32), h.view(np.uint32))
+        assert gpu_model.verify_greedy() == (int(np.argmax(first[0])), int(np.argmax(second[0])))
+        for blocked in (lambda: gpu_model.step(12), lambda: gpu_model.prefill([12])):
+            with pytest.raises(RuntimeError, match='Commit or discard pending verification'):
+                blocked()
+        with pytest.raises(RuntimeError, match='Verification already pending'):
+            gpu_model.verify_two(12, 13)
+        for count in (-1, 0, 3):
+            with pytest.raises(RuntimeError, match='Commit count must be one or two'):
+                gpu_model.commit_verified(count)
+        gpu_model.commit_verified(commit)
+        expected = first if commit == 1 else second
+        assert gpu_model.position() == prefix + commit
+        assert np.array_equal(gpu_model.logits().view(np.uint32), expected[0].view(np.uint32))
+        assert np.array_equal(gpu_model.hidden().view(np.uint32), expected[1].view(np.uint32))
+        if commit == 1:
+            ref.truncate(prefix + 1)
+        gpu_model.step(42)
+        ref.step(42)
+        assert np.array_equal(gpu_model.logits().view(np.uint32), ref.logits().view(np.uint32))
+    finally:
+        ref.close()
+
+
+@pytest.mark.gpu
+def test_validation_before_mutation(qpkg, pack0):
+    """Capacity/id/range errors leave state unchanged (engine/core.cpp:707-732)."""
+    m = qpkg.Model(pack0, context=4)
+    try:
+        m.prefill([1, 2, 3])
+        before = m.logits()
+        for call, message in ((lambda: m.prefill([4, 5]), 'Context capacity exceeded'),
+                              (lambda: m.step(V), 'Token ID out of range'),
+                              (lambda: m.step(-1), 'Token ID out of range'),
+                              (lambda: m.prefill([]), 'Empty token input'),
+                              (lambda: m.truncate(4), 'Rewind position out of range'),
+                              (lambda: m.truncate(-1), 'Rewind position out of range'),
+                              (lambda: m.verify_two(1, 2), 'Context capacity exceeded')):
+            with pytest.raises(RuntimeError, match=message):
+                call()
+            assert m.position() == 3
+            assert np.array_equal(m.logits().view(np.uint32), before.view(np.uint32))
+        m.step(4)
+        assert m.position() == 4
+        with pytest.raises(RuntimeError, match='Context capacity exceeded'):
+            m.step(5)
+    finally:
+        m.close()
