@@ -53,6 +53,11 @@ SIGNATURES = {
     'qwen_gpu_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
     'qwen_gpu_verify_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_int_p]),
     'qwen_gpu_write_random_pack': (ctypes.c_int, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_double, ctypes.c_int]),
+    'qwen_gpu_device_malloc': (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
+    'qwen_gpu_device_free': (ctypes.c_int, [ctypes.c_void_p]),
+    'qwen_gpu_memcpy_to_device': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    'qwen_gpu_memcpy_to_host': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
+    'qwen_gpu_device_synchronize': (ctypes.c_int, []),
     'qwen_gpu_op_tile_matrix': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -200,31 +205,62 @@ def ensure_random_pack(directory, seed=0, stddev=0.02):
     return write_random_pack(path, seed, stddev)
 
 
-# ---- kernel-level entry points on torch device tensors (memory plumbing) ----
+# ---- kernel-level entry points on device memory of this library's runtime ----
 
-def _ptr(tensor):
-    return ctypes.c_void_p(tensor.data_ptr()) if tensor is not None else None
+class DeviceBuffer:
+    """Device allocation made through the engine's own HIP runtime."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        ptr = ctypes.c_void_p()
+        _check(_LIB.qwen_gpu_device_malloc(self.nbytes, ctypes.byref(ptr)))
+        self.ptr = ptr
+
+    @classmethod
+    def from_array(cls, array):
+        array = np.ascontiguousarray(array)
+        buf = cls(array.nbytes)
+        _check(_LIB.qwen_gpu_memcpy_to_device(buf.ptr, array.ctypes.data_as(ctypes.c_void_p), array.nbytes))
+        return buf
+
+    def to_array(self, dtype, count):
+        out = np.empty(count, dtype=dtype)
+        _check(_LIB.qwen_gpu_memcpy_to_host(out.ctypes.data_as(ctypes.c_void_p), self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            _check(_LIB.qwen_gpu_device_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
-def _stream():
-    import torch
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+def synchronize():
+    _check(_LIB.qwen_gpu_device_synchronize())
 
 
 def tile_matrix(first, second=None):
-    """Natural FP16 [rows, cols] device tensor(s) -> chain-tiled GEMV layout."""
-    import torch
+    """Natural FP16 [rows, cols] array(s) -> chain-tiled GEMV layout on the device."""
+    first = np.ascontiguousarray(first, np.float16)
     rows, cols = first.shape
-    out_rows = 2 * rows if second is not None else rows
-    out = torch.empty(out_rows * cols, dtype=torch.float16, device=first.device)
-    _check(_LIB.qwen_gpu_op_tile_matrix(_ptr(first), _ptr(second), _ptr(out), rows, cols, _stream()))
+    a = DeviceBuffer.from_array(first)
+    b = DeviceBuffer.from_array(np.ascontiguousarray(second, np.float16)) if second is not None else None
+    out = DeviceBuffer(first.nbytes * (2 if second is not None else 1))
+    _check(_LIB.qwen_gpu_op_tile_matrix(a.ptr, b.ptr if b else None, out.ptr, rows, cols, None))
+    synchronize()
     return out
 
 
 def gemv(tiled, x, rows):
-    """y = W x with the reference dot's chain order (W chain-tiled)."""
-    import torch
-    cols = x.numel()
-    y = torch.empty(rows, dtype=torch.float32, device=x.device)
-    _check(_LIB.qwen_gpu_op_gemv(_ptr(tiled), _ptr(x), _ptr(y), rows, cols, _stream()))
-    return y
+    """y = W x with the reference dot's chain order (W chain-tiled DeviceBuffer)."""
+    x = np.ascontiguousarray(x, np.float32)
+    xd = DeviceBuffer.from_array(x)
+    yd = DeviceBuffer(rows * 4)
+    _check(_LIB.qwen_gpu_op_gemv(tiled.ptr, xd.ptr, yd.ptr, rows, x.size, None))
+    synchronize()
+    return yd.to_array(np.float32, rows)

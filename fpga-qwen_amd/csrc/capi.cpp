@@ -162,6 +162,30 @@ int qwen_gpu_write_random_pack(const char* path, uint64_t seed, double stddev, i
     });
 }
 
+static void hip_ok(hipError_t e) {
+    if (e != hipSuccess) throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(e));
+}
+
+int qwen_gpu_device_malloc(size_t bytes, void** pointer) {
+    return guarded([&] {
+        need(pointer, "pointer");
+        *pointer = nullptr;
+        hip_ok(hipMalloc(pointer, bytes));
+    });
+}
+
+int qwen_gpu_device_free(void* pointer) { return guarded([&] { hip_ok(hipFree(pointer)); }); }
+
+int qwen_gpu_memcpy_to_device(void* device, const void* host, size_t bytes) {
+    return guarded([&] { hip_ok(hipMemcpy(device, host, bytes, hipMemcpyHostToDevice)); });
+}
+
+int qwen_gpu_memcpy_to_host(void* host, const void* device, size_t bytes) {
+    return guarded([&] { hip_ok(hipMemcpy(host, device, bytes, hipMemcpyDeviceToHost)); });
+}
+
+int qwen_gpu_device_synchronize(void) { return guarded([&] { hip_ok(hipDeviceSynchronize()); }); }
+
 int qwen_gpu_op_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t* dst, int rows, int cols,
                             void* stream) {
     return guarded([&] {

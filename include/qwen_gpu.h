@@ -84,6 +84,15 @@ int qwen_gpu_verify_greedy(qwen_gpu_model* model, int* first, int* second);
  * Writes PATH, PATH.index and PATH.manifest.json; refuses existing outputs. */
 int qwen_gpu_write_random_pack(const char* path, uint64_t seed, double stddev, int threads);
 
+/* Device memory plumbing for callers that hold no other GPU runtime (the
+ * op-level entry points below take device pointers). No reference counterpart:
+ * they exist so tests and C callers need not load a second HIP runtime. */
+int qwen_gpu_device_malloc(size_t bytes, void** pointer);
+int qwen_gpu_device_free(void* pointer);
+int qwen_gpu_memcpy_to_device(void* device, const void* host, size_t bytes);
+int qwen_gpu_memcpy_to_host(void* host, const void* device, size_t bytes);
+int qwen_gpu_device_synchronize(void);
+
 /* Kernel-level entry points on caller-owned device memory (stream may be
  * NULL for the default stream); used by parity tests and the GEMV microbench.
  * Converts natural row-major FP16 [rows x cols] to the engine's chain-tiled
