@@ -114,26 +114,26 @@ __device__ __forceinline__ void copy_to_lds(const float* __restrict__ x, float* 
     }
 }
 
-// Chain dot of one 8-row tile against the permuted LDS vector.
+// Weights of one 8-row tile for this lane: NB 16-byte blocks. Issued before
+// the input vector is ready (weights do not depend on it), so the HBM round
+// trip overlaps the prologue.
 template <int N>
-__device__ __forceinline__ float tile_dot(const uint16_t* __restrict__ w_t, const float* xs, size_t tile, int lane) {
+__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ w_t, size_t tile, int lane, u32x4 (&wv)[N / 64]) {
     constexpr int NB = N / 64;
-    constexpr int U = NB < 16 ? NB : 16;
     const u32x4* wp = reinterpret_cast<const u32x4*>(w_t) + tile * (NB * 64) + lane;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) wv[b] = __builtin_nontemporal_load(wp + b * 64);
+}
+
+// Chain dot of the loaded tile against the permuted LDS vector.
+template <int N>
+__device__ __forceinline__ float tile_dot(const u32x4 (&wv)[N / 64], const float* xs, int lane) {
+    constexpr int NB = N / 64;
     const float4* xs4 = reinterpret_cast<const float4*>(xs);
     const int c = lane & 7;
     float acc = 0.f;
 #pragma unroll
-    for (int b0 = 0; b0 < NB; b0 += U) {
-        u32x4 wv[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) wv[u] = __builtin_nontemporal_load(wp + (b0 + u) * 64);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int b = b0 + u;
-            acc = chain8(acc, wv[u], xs4[16 * b + 2 * c], xs4[16 * b + 2 * c + 1]);
-        }
-    }
+    for (int b = 0; b < NB; ++b) acc = chain8(acc, wv[b], xs4[16 * b + 2 * c], xs4[16 * b + 2 * c + 1]);
     return combine_chains(acc);
 }
 
@@ -151,8 +151,6 @@ struct GemvArgs {
     float* lm_value;
     int* lm_index;
     int* lm_bad;
-    unsigned* lm_count;
-    ArgmaxResult* result;
 };
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
@@ -164,6 +162,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     __shared__ double red[WAVES];
     float* xs = reinterpret_cast<float*>(xs4);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t tile = size_t(blockIdx.x) * WAVES + wave;
+    u32x4 wv[N / 64];
+    load_tile<N>(a.w, tile, lane, wv);
 
     if constexpr (MODE == kQKV) {
         const float* src = a.in;
@@ -184,13 +185,63 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         norm_to_lds<N, THREADS>(a.in, a.norm_w, xs, red, nullptr);
     } else if constexpr (MODE == kLmHead) {
         norm_to_lds<N, THREADS>(a.in, a.norm_w, xs, red, blockIdx.x == 0 ? a.hidden : nullptr);
+    } else if constexpr (MODE == kO) {
+        // Merge the attention splits of all 16 heads (flash-decoding merge,
+        // fixed split order): o = sum_s w_s o_s / sum_s w_s l_s with
+        // w_s = exp(m_s - max); unused splits carry m = -inf, so w_s = 0.
+        // All statistics and split outputs load in one round.
+        static_assert(THREADS == 128 && kQHeads * kAttnSplits <= THREADS, "O prologue layout");
+        __shared__ float cw[kQHeads][kAttnSplits];
+        __shared__ float cl[kQHeads];
+        float part_o[N / THREADS][kAttnSplits];
+#pragma unroll
+        for (int k = 0; k < N / THREADS; ++k)  // output j = tid + 128 k belongs to head k
+#pragma unroll
+            for (int sp = 0; sp < kAttnSplits; ++sp)
+                part_o[k][sp] = a.in[(size_t(k >> 1) * kAttnSplits + sp) * kAttnPartial + (k & 1) * 132 + tid];
+        float m_s = -INFINITY, l_s = 0.f;
+        const int sh = tid / kAttnSplits, ss = tid % kAttnSplits;
+        if (tid < kQHeads * kAttnSplits) {
+            const float* st = a.in + (size_t(sh >> 1) * kAttnSplits + ss) * kAttnPartial + (sh & 1) * 132;
+            m_s = st[128];
+            l_s = st[129];
+        }
+        __shared__ float stat[kQHeads][kAttnSplits][2];
+        if (tid < kQHeads * kAttnSplits) {
+            stat[sh][ss][0] = m_s;
+            stat[sh][ss][1] = l_s;
+        }
+        __syncthreads();
+        if (tid < kQHeads) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < kAttnSplits; ++k) mx = fmaxf(mx, stat[tid][k][0]);
+            float l = 0.f;
+#pragma unroll
+            for (int k = 0; k < kAttnSplits; ++k) {
+                const float w = stat[tid][k][0] == -INFINITY ? 0.f : expf(stat[tid][k][0] - mx);
+                cw[tid][k] = w;
+                l += w * stat[tid][k][1];
+            }
+            cl[tid] = l;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < N / THREADS; ++k) {
+            float o = 0.f;
+#pragma unroll
+            for (int sp = 0; sp < kAttnSplits; ++sp) {
+                const float w = cw[k][sp];
+                o += w != 0.f ? w * part_o[k][sp] : 0.f;
+            }
+            xs[xperm(tid + k * THREADS)] = o / cl[k];
+        }
     } else {
         copy_to_lds<N, THREADS>(a.in, xs);
     }
     __syncthreads();
 
-    const size_t tile = size_t(blockIdx.x) * WAVES + wave;
-    const float y = tile_dot<N>(a.w, xs, tile, lane);
+    const float y = tile_dot<N>(wv, xs, lane);
     const int c = lane & 7, r = lane >> 3;
     const int row = int(tile) * 8 + r;
 
@@ -225,7 +276,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         }
         __shared__ float wv[WAVES];
         __shared__ int wi[WAVES], wb[WAVES];
-        __shared__ int last;
         if (lane == 0) { wv[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
         __syncthreads();
         if (tid == 0) {
@@ -233,45 +283,54 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
                 bad |= wb[k];
                 if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
             }
-            __hip_atomic_store(a.lm_value + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.lm_index + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.lm_bad + blockIdx.x, bad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __threadfence();
-            const unsigned prev = __hip_atomic_fetch_add(a.lm_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            last = prev == gridDim.x - 1;
-        }
-        __syncthreads();
-        if (!last) return;
-        __threadfence();
-        bv = -INFINITY;
-        bi = INT_MAX;
-        bad = 0;
-        for (int k = tid; k < int(gridDim.x); k += THREADS) {
-            const float v = __hip_atomic_load(a.lm_value + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const int i = __hip_atomic_load(a.lm_index + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            bad |= __hip_atomic_load(a.lm_bad + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            bad |= __shfl_xor(bad, off);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-        }
-        __syncthreads();
-        if (lane == 0) { wv[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
-        __syncthreads();
-        if (tid == 0) {
-            for (int k = 1; k < WAVES; ++k) {
-                bad |= wb[k];
-                if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
-            }
-            a.result->token = bi;
-            a.result->nonfinite = bad;
-            __hip_atomic_store(a.lm_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a.lm_value[blockIdx.x] = bv;
+            a.lm_index[blockIdx.x] = bi;
+            a.lm_bad[blockIdx.x] = bad;
         }
     }
+}
+
+// Second pass of the greedy selection: one workgroup reduces the per-group
+// (max, lowest id, nonfinite) partials of the lm_head kernel.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ value, const int* __restrict__ index,
+                                                      const int* __restrict__ bad_in, int groups,
+                                                      ArgmaxResult* result, ArgmaxResult* host_result,
+                                                      const StepParams* params) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    int bi = INT_MAX, bad = 0;
+    for (int k = tid; k < groups; k += 1024) {
+        bad |= bad_in[k];
+        if (better(value[k], index[k], bv, bi)) { bv = value[k]; bi = index[k]; }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        bad |= __shfl_xor(bad, off);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    __shared__ float wv[16];
+    __shared__ int wi[16], wb[16];
+    if (lane == 0) { wv[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int k = 1; k < 16; ++k) {
+            bad |= wb[k];
+            if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
+        }
+        result->token = bi;
+        result->nonfinite = bad;
+        ArgmaxResult* h = host_result + params->slot;
+        h->token = bi;
+        h->nonfinite = bad;
+    }
+}
+
+__global__ void set_step_kernel(StepParams* params, int pos, int token, int slot) {
+    params->pos = pos;
+    params->token = token;
+    params->slot = slot;
 }
 
 struct AttnArgs {
@@ -284,8 +343,6 @@ struct AttnArgs {
     uint16_t* values;
     const StepParams* params;
     float* partial;        // [8][kAttnSplits][kAttnPartial]
-    unsigned* counters;    // [8]
-    float* attended;       // [2048]
     int context;
     float scale;           // 1.0f / sqrt(128.0f)
 };
@@ -318,73 +375,112 @@ __device__ __forceinline__ float head_norm_rope(float raw, const float* w, const
     return out;
 }
 
-__global__ __launch_bounds__(256) void attn_decode_kernel(const AttnArgs a) {
+// One workgroup = one KV head g (GQA query heads 2g, 2g+1) x one split of
+// positions, walked in tiles of 256 with an online softmax (running max and
+// sum rescaled per tile). 512 threads: scores use 8 threads per position
+// (64 positions per pass); P.V uses 4 waves per head, lane = 8-channel group
+// + position lane (16 position lanes). Writes the split's unnormalized
+// output, max and sum; the O projection's prologue merges the splits.
+__global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     const int s = blockIdx.x, g = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = a.params->pos, n = pos + 1;
-    int chunk = (n + kAttnSplits - 1) / kAttnSplits;
-    chunk = max(64, (chunk + 63) & ~63);
-    const int ns = (n + chunk - 1) / chunk;
-    if (s >= ns) return;
-    const int t0 = s * chunk, m = min(n, t0 + chunk) - t0;  // 1 <= m <= 128
-    const bool owner = t0 + m == n;
+    int chunk, ns;
+    attn_split(n, chunk, ns);
+    if (s >= ns) {  // unused split: contributes nothing to the merge
+        if (threadIdx.x < 2) {
+            float* part = a.partial + (size_t(g) * kAttnSplits + s) * kAttnPartial + threadIdx.x * 132;
+            part[128] = -INFINITY;
+            part[129] = 0.f;
+        }
+        return;
+    }
+    const int t_begin = s * chunk, t_end = min(n, t_begin + chunk);
+    const size_t head_base = size_t(g) * a.context;
+    const int quarter = tid >> 7, j = tid & 127, c = tid & 7;
+    const int hv = wave >> 2, cg = lane & 15, pl = ((wave & 3) << 2) | (lane >> 4);
+
+    u32x4 kreg[4][2];
+    u32x4 vreg[16];
+    auto load_tile = [&](int t0, int m) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int tl = p * 64 + (tid >> 3), t = t0 + tl;
+            if (tl < m && t != pos) {
+                const u32x4* kp = reinterpret_cast<const u32x4*>(a.keys + (head_base + t) * 128 + c * 16);
+                kreg[p][0] = kp[0];
+                kreg[p][1] = kp[1];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int tl = pl + 16 * k, t = t0 + tl;
+            if (tl < m && t != pos)
+                vreg[k] = *reinterpret_cast<const u32x4*>(a.values + (head_base + t) * 128 + cg * 8);
+        }
+    };
+    // Raw q/k/v and the first tile's cached K/V rows are loaded first.
+    const float raw = quarter < 2 ? a.qkv[(2 * g + quarter) * 128 + j] : a.qkv[2048 + g * 128 + j];
+    const float raw_v = a.qkv[3072 + g * 128 + j];
+    load_tile(t_begin, min(kAttnTile, t_end - t_begin));
 
     __shared__ float qp[2][128];
-    __shared__ float buf[2][128];
-    __shared__ float sc[2][128];
-    __shared__ float opart[2][2][128];
+    __shared__ float buf[4][128];
+    __shared__ float sc[2][kAttnTile];
+    __shared__ float opart[4][2][128];
     __shared__ uint16_t kcur[128], vcur[128];
-    __shared__ double red[2][2];
-    __shared__ float redm[4], reds[4];
-    __shared__ int last;
+    __shared__ double red[4][2];
+    __shared__ float redm[8], reds[8];
+    __shared__ float run_max[2], run_sum[2], run_scale[2];
 
-    const float* cs = a.cosines + size_t(pos) * 64;
-    const float* sn = a.sines + size_t(pos) * 64;
-    const size_t head_base = size_t(g) * a.context;
-
-    {  // q heads 2g, 2g+1: one head per pair of waves
-        const int h = tid >> 7, j = tid & 127;
-        const float raw = a.qkv[(2 * g + h) * 128 + j];
-        const float q = head_norm_rope(raw, a.q_norm, cs, sn, red[h], buf[h], j);
-        qp[h][kperm(j)] = q;
-    }
-    if (owner) {  // current k and v into the cache and LDS (owner is block-uniform)
-        __syncthreads();
-        // Both wave pairs normalize the same k head into separate buffers so
-        // every wave meets the same barriers; pair 0 stores k, pair 1 stores v.
-        const int h = tid >> 7, j = tid & 127;
-        const float raw = a.qkv[2048 + g * 128 + j];
-        const float k = head_norm_rope(raw, a.k_norm, cs, sn, red[h], buf[h], j);
-        if (h == 0) {
-            const uint16_t bits = f2h(k);
+    // QK-norm + RoPE: quarters 0-1 the two q heads, quarters 2-3 both the k
+    // head (same barriers for every wave); quarter 2 keeps k, quarter 3 v.
+    {
+        const float* cs = a.cosines + size_t(pos) * 64;
+        const float* sn = a.sines + size_t(pos) * 64;
+        const float r = head_norm_rope(raw, quarter < 2 ? a.q_norm : a.k_norm, cs, sn, red[quarter], buf[quarter], j);
+        const bool owner = t_end == n;
+        if (quarter < 2) {
+            qp[quarter][kperm(j)] = r;
+        } else if (quarter == 2) {
+            const uint16_t bits = f2h(r);
             kcur[kperm(j)] = bits;
-            a.keys[(head_base + pos) * 128 + kperm(j)] = bits;
+            if (owner) a.keys[(head_base + pos) * 128 + kperm(j)] = bits;
         } else {
-            const uint16_t bits = f2h(a.qkv[3072 + g * 128 + j]);
+            const uint16_t bits = f2h(raw_v);
             vcur[j] = bits;
-            a.values[(head_base + pos) * 128 + j] = bits;
+            if (owner) a.values[(head_base + pos) * 128 + j] = bits;
+        }
+        if (tid < 2) {
+            run_max[tid] = -INFINITY;
+            run_sum[tid] = 0.f;
         }
     }
     __syncthreads();
 
-    // Scores: 8 threads per position, thread c runs chain c over the 16
-    // steps of the 128-long dot for both query heads (engine/core.cpp:612).
-    {
-        const int c = tid & 7;
-        for (int base = 0; base < m; base += 32) {
-            const int tl = base + (tid >> 3);
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+
+    for (int t0 = t_begin; t0 < t_end; t0 += kAttnTile) {
+        const int m = min(kAttnTile, t_end - t0);
+        if (t0 != t_begin) load_tile(t0, m);
+        // Scores in the reference dot's chain order (engine/core.cpp:612).
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int base = p * 64;
+            if (base >= m) break;  // block-uniform
+            const int tl = base + (tid >> 3), t = t0 + tl;
             float acc0 = 0.f, acc1 = 0.f;
             if (tl < m) {
-                const int t = t0 + tl;
                 uint32_t kw[8];
                 if (t == pos) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) kw[i] = uint32_t(kcur[c * 16 + 2 * i]) | (uint32_t(kcur[c * 16 + 2 * i + 1]) << 16);
+                    for (int i = 0; i < 8; ++i)
+                        kw[i] = uint32_t(kcur[c * 16 + 2 * i]) | (uint32_t(kcur[c * 16 + 2 * i + 1]) << 16);
                 } else {
-                    const u32x4* kp = reinterpret_cast<const u32x4*>(a.keys + (head_base + t) * 128 + c * 16);
-                    const u32x4 lo = kp[0], hi = kp[1];
-                    kw[0] = lo.x; kw[1] = lo.y; kw[2] = lo.z; kw[3] = lo.w;
-                    kw[4] = hi.x; kw[5] = hi.y; kw[6] = hi.z; kw[7] = hi.w;
+                    kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
+                    kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
                 }
                 const float* q0 = &qp[0][c * 16];
                 const float* q1 = &qp[1][c * 16];
@@ -403,96 +499,76 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnArgs a) {
                 sc[1][tl] = d1 * a.scale;
             }
         }
+        __syncthreads();
+        {  // online softmax: threads 0-255 head 0, 256-511 head 1
+            const int h = tid >> 8, i = tid & 255;
+            const float v = i < m ? sc[h][i] : -INFINITY;
+            const float mx = wave_max(v);
+            if (lane == 0) redm[wave] = mx;
+            __syncthreads();
+            const float tile_max = fmaxf(fmaxf(redm[4 * h], redm[4 * h + 1]), fmaxf(redm[4 * h + 2], redm[4 * h + 3]));
+            const float old_max = run_max[h];
+            const float new_max = fmaxf(old_max, tile_max);
+            const float p = i < m ? expf(v - new_max) : 0.f;
+            if (i < m) sc[h][i] = p;
+            const float sm = wave_sum(p);
+            if (lane == 0) reds[wave] = sm;
+            __syncthreads();
+            if (i == 0) {
+                const float scale = old_max == -INFINITY ? 0.f : expf(old_max - new_max);
+                run_scale[h] = scale;
+                run_sum[h] = run_sum[h] * scale + ((reds[4 * h] + reds[4 * h + 1]) + (reds[4 * h + 2] + reds[4 * h + 3]));
+                run_max[h] = new_max;
+            }
+            __syncthreads();
+        }
+        {  // unnormalized P.V, rescaled by the change of running max
+            const float scale = run_scale[hv];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] *= scale;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int tl = pl + 16 * k, t = t0 + tl;
+                if (tl < m) {
+                    const float p = sc[hv][tl];
+                    uint32_t vw[4];
+                    if (t == pos) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            vw[i] = uint32_t(vcur[cg * 8 + 2 * i]) | (uint32_t(vcur[cg * 8 + 2 * i + 1]) << 16);
+                    } else {
+                        vw[0] = vreg[k].x; vw[1] = vreg[k].y; vw[2] = vreg[k].z; vw[3] = vreg[k].w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc[2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p, acc[2 * i]);
+                        acc[2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p, acc[2 * i + 1]);
+                    }
+                }
+            }
+        }
+        __syncthreads();  // sc is rewritten by the next tile
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        acc[i] += __shfl_xor(acc[i], 16);
+        acc[i] += __shfl_xor(acc[i], 32);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) opart[wave & 3][hv][cg * 8 + i] = acc[i];
     }
     __syncthreads();
-
-    // Split-local softmax statistics per head.
-    float head_max, head_sum;
-    {
-        const int h = tid >> 7, i = tid & 127;
-        const float v = i < m ? sc[h][i] : -INFINITY;
-        const float mx = wave_max(v);
-        if (lane == 0) redm[wave] = mx;
-        __syncthreads();
-        head_max = fmaxf(redm[2 * h], redm[2 * h + 1]);
-        const float p = i < m ? expf(v - head_max) : 0.f;
-        if (i < m) sc[h][i] = p;
-        const float sm = wave_sum(p);
-        if (lane == 0) reds[wave] = sm;
-        __syncthreads();
-        head_sum = reds[2 * h] + reds[2 * h + 1];
-    }
-
-    // P.V: wave pair per head; lane = channel group (8 channels) + position lane.
-    {
-        const int h = wave >> 1, cg = lane & 15, pl = ((wave & 1) << 2) | (lane >> 4);
-        float acc[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-        for (int tl = pl; tl < m; tl += 8) {
-            const int t = t0 + tl;
-            const float p = sc[h][tl];
-            uint32_t vw[4];
-            if (t == pos) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) vw[i] = uint32_t(vcur[cg * 8 + 2 * i]) | (uint32_t(vcur[cg * 8 + 2 * i + 1]) << 16);
-            } else {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(a.values + (head_base + t) * 128 + cg * 8);
-                vw[0] = v.x; vw[1] = v.y; vw[2] = v.z; vw[3] = v.w;
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p, acc[2 * i]);
-                acc[2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p, acc[2 * i + 1]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            acc[i] += __shfl_xor(acc[i], 16);
-            acc[i] += __shfl_xor(acc[i], 32);
-        }
-        if (lane < 16) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) opart[wave & 1][h][cg * 8 + i] = acc[i];
-        }
-    }
-    __syncthreads();
-
-    float* part = a.partial + (size_t(g) * kAttnSplits + s) * kAttnPartial;
-    {
-        const int h = tid >> 7, j = tid & 127;
-        const float o = opart[0][h][j] + opart[1][h][j];
-        __hip_atomic_store(part + h * 132 + j, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < 256) {
+        const int h = tid >> 7;
+        const float o = (opart[0][h][j] + opart[1][h][j]) + (opart[2][h][j] + opart[3][h][j]);
+        float* part = a.partial + (size_t(g) * kAttnSplits + s) * kAttnPartial + h * 132;
+        part[j] = o;
         if (j == 0) {
-            __hip_atomic_store(part + h * 132 + 128, head_max, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(part + h * 132 + 129, head_sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            part[128] = run_max[h];
+            part[129] = run_sum[h];
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = prev == unsigned(ns - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    {  // combine splits in fixed order
-        const int h = tid >> 7, j = tid & 127;
-        const float* base = a.partial + size_t(g) * kAttnSplits * kAttnPartial + h * 132;
-        float mx = -INFINITY;
-        for (int k = 0; k < ns; ++k)
-            mx = fmaxf(mx, __hip_atomic_load(base + k * kAttnPartial + 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        float o = 0.f, l = 0.f;
-        for (int k = 0; k < ns; ++k) {
-            const float* p = base + k * kAttnPartial;
-            const float w = expf(__hip_atomic_load(p + 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - mx);
-            o += w * __hip_atomic_load(p + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            l += w * __hip_atomic_load(p + 129, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        a.attended[(2 * g + h) * 128 + j] = o / l;
-    }
-    if (tid == 0) __hip_atomic_store(a.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* __restrict__ second,
@@ -576,17 +652,16 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             at.values = L.values;
             at.params = params;
             at.partial = s.attn_partial;
-            at.counters = s.attn_count;
-            at.attended = s.attended;
             at.context = context;
             at.scale = 1.0f / std::sqrt(128.0f);
-            attn_decode_kernel<<<dim3(kAttnSplits, kKVHeads), 256, 0, stream>>>(at);
+            attn_decode_kernel<<<dim3(kAttnSplits, kKVHeads), 512, 0, stream>>>(at);
             break;
         }
         case 2: {
             GemvArgs o{};
             o.w = L.o_t;
-            o.in = s.attended;
+            o.in = s.attn_partial;
+            o.params = params;
             o.x = s.x;
             launch_gemv<kQDim, kO>(o, kHidden, stream);
             break;
@@ -628,9 +703,13 @@ void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeS
     a.lm_value = s.lm_value;
     a.lm_index = s.lm_index;
     a.lm_bad = s.lm_bad;
-    a.lm_count = s.lm_count;
-    a.result = s.result;
     gemv_kernel<kHidden, kLmWaves, kLmHead><<<kLmGroups, 64 * kLmWaves, 0, stream>>>(a);
+    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, s.host_result,
+                                          s.params);
+}
+
+void launch_set_step(StepParams* params, int pos, int token, int slot, hipStream_t stream) {
+    set_step_kernel<<<1, 1, 0, stream>>>(params, pos, token, slot);
 }
 
 }  // namespace qwen_hip

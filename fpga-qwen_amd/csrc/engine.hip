@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 #include "pack.hpp"
@@ -113,46 +114,45 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
         DecodeScratch& s = scratch_;
         s.x = device_alloc<float>(kHidden);
         s.qkv = device_alloc<float>(kQKVRows);
-        s.attended = device_alloc<float>(kQDim);
         s.act = device_alloc<float>(kFFN);
         s.logits = device_alloc<float>(kVocab);
         s.hidden = device_alloc<float>(kHidden);
         s.attn_partial = device_alloc<float>(size_t(kKVHeads) * kAttnSplits * kAttnPartial);
-        s.attn_count = device_alloc<unsigned>(kKVHeads);
         s.lm_value = device_alloc<float>(kLmGroups);
         s.lm_index = device_alloc<int>(kLmGroups);
         s.lm_bad = device_alloc<int>(kLmGroups);
-        s.lm_count = device_alloc<unsigned>(1);
         s.result = device_alloc<ArgmaxResult>(1);
-        HIP_CHECK(hipMemset(s.attn_count, 0, kKVHeads * sizeof(unsigned)));
-        HIP_CHECK(hipMemset(s.lm_count, 0, sizeof(unsigned)));
         ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
         ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
         base_logits_ = device_alloc<float>(kVocab);
         base_hidden_ = device_alloc<float>(kHidden);
         params_dev_ = device_alloc<StepParams>(1);
+        HIP_CHECK(hipMemset(params_dev_, 0, sizeof(StepParams)));
         void* pinned = nullptr;
-        HIP_CHECK(hipHostMalloc(&pinned, sizeof(StepParams) * size_t(ctx), hipHostMallocDefault));
-        params_host_ = static_cast<StepParams*>(pinned);
         HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
         result_host_ = static_cast<ArgmaxResult*>(pinned);
         std::memset(result_host_, 0, sizeof(ArgmaxResult) * 3);
+        s.host_result = result_host_;
+        s.params = params_dev_;
         HIP_CHECK(hipStreamSynchronize(stream_));
         HIP_CHECK(hipFree(stage));
         allocations_.erase(std::find(allocations_.begin(), allocations_.end(), static_cast<void*>(stage)));
 
         // Capture: all 28 layers in one graph, the head in another. Kernels
         // read position/token from params_dev_, so each graph is replayed as is.
-        HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-        for (int l = 0; l < kLayers; ++l)
-            launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, params_dev_, cosines_, sines_, ctx, scratch_,
-                                stream_);
-        HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[0]));
-        HIP_CHECK(hipGraphInstantiate(&layer_graph_, graphs_[0], nullptr, nullptr, 0));
-        HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-        launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
-        HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[1]));
-        HIP_CHECK(hipGraphInstantiate(&head_graph_, graphs_[1], nullptr, nullptr, 0));
+        // QWEN_GPU_GRAPHS=0 launches the same kernels directly instead.
+        const char* graphs_env = std::getenv("QWEN_GPU_GRAPHS");
+        use_graphs_ = !(graphs_env && std::string(graphs_env) == "0");
+        if (use_graphs_) {
+            HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+            launch_layers();
+            HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[0]));
+            HIP_CHECK(hipGraphInstantiate(&layer_graph_, graphs_[0], nullptr, nullptr, 0));
+            HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+            launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
+            HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[1]));
+            HIP_CHECK(hipGraphInstantiate(&head_graph_, graphs_[1], nullptr, nullptr, 0));
+        }
         HIP_CHECK(hipGetLastError());
     } catch (...) {
         release();
@@ -167,13 +167,11 @@ void Engine::release() {
     for (hipGraph_t g : graphs_)
         if (g) (void)hipGraphDestroy(g);
     for (void* p : allocations_) (void)hipFree(p);
-    if (params_host_) (void)hipHostFree(params_host_);
     if (result_host_) (void)hipHostFree(result_host_);
     if (stream_) (void)hipStreamDestroy(stream_);
     layer_graph_ = head_graph_ = nullptr;
     graphs_[0] = graphs_[1] = nullptr;
     allocations_.clear();
-    params_host_ = nullptr;
     result_host_ = nullptr;
     stream_ = nullptr;
 }
@@ -202,16 +200,23 @@ void Engine::truncate(int position) {
     invalidate();
 }
 
+void Engine::launch_layers() {
+    for (int l = 0; l < kLayers; ++l)
+        launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, params_dev_, cosines_, sines_, options_.context,
+                            scratch_, stream_);
+}
+
 void Engine::run_token(int token, bool head, int result_slot) {
-    StepParams& slot = params_host_[pos_];
-    slot.pos = pos_;
-    slot.token = token;
-    HIP_CHECK(hipMemcpyAsync(params_dev_, &slot, sizeof(StepParams), hipMemcpyHostToDevice, stream_));
-    HIP_CHECK(hipGraphLaunch(layer_graph_, stream_));
+    launch_set_step(params_dev_, pos_, token, result_slot, stream_);
+    if (use_graphs_)
+        HIP_CHECK(hipGraphLaunch(layer_graph_, stream_));
+    else
+        launch_layers();
     if (head) {
-        HIP_CHECK(hipGraphLaunch(head_graph_, stream_));
-        HIP_CHECK(hipMemcpyAsync(result_host_ + result_slot, scratch_.result, sizeof(ArgmaxResult),
-                                 hipMemcpyDeviceToHost, stream_));
+        if (use_graphs_)
+            HIP_CHECK(hipGraphLaunch(head_graph_, stream_));
+        else
+            launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
     }
     ++pos_;
 }
@@ -336,8 +341,7 @@ float Engine::time_kernel(int which, int iterations) {
     require(pos_ > 0 && !pending_, "time_kernel needs a current position");
     require(which >= 0 && which <= 5 && iterations > 0, "time_kernel: bad arguments");
     // Replays kernels of the last processed position; the state is reset afterwards.
-    StepParams& slot = params_host_[pos_ - 1];
-    HIP_CHECK(hipMemcpyAsync(params_dev_, &slot, sizeof(StepParams), hipMemcpyHostToDevice, stream_));
+    launch_set_step(params_dev_, pos_ - 1, 0, 0, stream_);
     const int layer = kLayers / 2;
     auto launch = [&] {
         if (which == 5)

@@ -27,6 +27,7 @@ namespace qwen_hip {
 struct StepParams {
     int pos;    // position being written (tokens before it are cached)
     int token;  // input token id
+    int slot;   // index of the host result slot the argmax writes
 };
 
 // Greedy selection result of the lm_head kernel.
@@ -35,8 +36,22 @@ struct ArgmaxResult {
     int nonfinite;
 };
 
-inline constexpr int kAttnSplits = 32;          // max position splits per KV head
+inline constexpr int kAttnSplits = 4;           // max position splits per KV head
+inline constexpr int kAttnTile = 256;           // positions per attention tile (online softmax)
 inline constexpr int kAttnPartial = 2 * 132;    // per split: 2 heads x (128 o + m + l + pad)
+
+// Position splitting of decode attention over n = pos + 1 cached positions:
+// up to 512 positions, chunks of 128 (<= 4 splits); beyond, 4 chunks of a
+// multiple of 256 positions (<= 1024 for a 4096 context).
+__host__ __device__ inline void attn_split(int n, int& chunk, int& splits) {
+    if (n <= 512) {
+        chunk = 128;
+    } else {
+        chunk = (n + kAttnSplits - 1) / kAttnSplits;
+        chunk = (chunk + kAttnTile - 1) / kAttnTile * kAttnTile;
+    }
+    splits = (n + chunk - 1) / chunk;
+}
 inline constexpr int kLmWaves = 4;              // lm_head workgroup waves
 inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 4748 workgroups
 static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
@@ -57,17 +72,17 @@ struct LayerDevice {
 struct DecodeScratch {
     float* x;             // [1024] residual stream
     float* qkv;           // [4096] raw projections
-    float* attended;      // [2048]
     float* act;           // [3072]
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
-    float* attn_partial;  // [8][kAttnSplits][kAttnPartial]
-    unsigned* attn_count; // [8], zero between launches
+    float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split;
+                          // every launch writes all splits (unused: max = -inf, sum = 0)
     float* lm_value;      // [kLmGroups]
     int* lm_index;        // [kLmGroups]
     int* lm_bad;          // [kLmGroups]
-    unsigned* lm_count;   // [1], zero between launches
-    ArgmaxResult* result; // [1]
+    ArgmaxResult* result; // [1] device copy of the selection
+    ArgmaxResult* host_result;  // pinned host slots, indexed by StepParams::slot
+    const StepParams* params;
 };
 
 // Layout conversion: natural row-major FP16 [rows x cols] -> chain-tiled.
@@ -81,7 +96,8 @@ void launch_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t*
 void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, int cols, hipStream_t stream);
 
 // One decode layer (five kernels): norm+QKV, attention (+q/k norm, RoPE, KV
-// write, split combine), O (+residual), norm+gate/up (+SwiGLU), down (+residual).
+// write) into per-split partials, O (+split combine prologue, +residual),
+// norm+gate/up (+SwiGLU), down (+residual).
 // When `embed` is non-null (first layer) x is first loaded from embed[token].
 void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, const StepParams* params,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
@@ -91,6 +107,9 @@ void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, const 
 void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, const StepParams* params,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
+
+// Writes the step scalars with one tiny kernel (no host-to-device copy).
+void launch_set_step(StepParams* params, int pos, int token, int slot, hipStream_t stream);
 
 // Final norm + tied lm_head GEMV + greedy argmax (lowest id on ties,
 // nonfinite flagged). Also writes the final hidden vector.

@@ -1,0 +1,67 @@
+"""Long-context decode parity (the 3968-token workload, seed 3).
+
+Decode attention splits the cached positions into up to 16 chunks whose
+partial softmax statistics are merged in the O projection's prologue; these
+tests exercise many splits and the 512-position chunk boundaries against the
+oracle's sequential softmax (engine/core.cpp:606-624), teacher-forced like
+tools/check_native_logits.py, under the gate of
+tools/check_native_saved_oracle.py:36.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_binding import compare_logits
+
+PROMPTS = json.loads((Path(__file__).parent / 'golden' / 'prompts.json').read_text())
+
+
+def check_trajectory(gpu, oracle, prompt, steps):
+    gpu.reset()
+    gpu.prefill(prompt)
+    oracle.reset()
+    oracle.prefill(prompt)
+    results = []
+    for i in range(steps):
+        logits = gpu.logits()
+        token = gpu.greedy()
+        result = compare_logits(logits, oracle.logits())
+        results.append(result)
+        assert result['passed'], (len(prompt) + i, result)
+        if i + 1 < steps:
+            gpu.step(token)
+            oracle.step(token)
+    return results
+
+
+@pytest.mark.gpu
+def test_context_1100_matches_oracle(qpkg, pack0, oracle_lib):
+    gpu = qpkg.Model(pack0, context=4096)
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    try:
+        results = check_trajectory(gpu, oracle, PROMPTS['long_3968'][:1100], 4)
+        print('max_abs', max(r['max_abs'] for r in results), 'rms', max(r['rms'] for r in results))
+    finally:
+        gpu.close()
+        oracle.close()
+
+
+@pytest.mark.gpu
+def test_context_3968_matches_oracle(qpkg, pack0, oracle_lib):
+    gpu = qpkg.Model(pack0, context=4096)
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    try:
+        results = check_trajectory(gpu, oracle, PROMPTS['long_3968'], 6)
+        print('max_abs', max(r['max_abs'] for r in results), 'rms', max(r['rms'] for r in results))
+        # Fill the cache to its last slot: capacity then rejects a further step.
+        gpu.reset()
+        gpu.prefill(PROMPTS['long_3968'])
+        gpu.prefill(list(range(128)))
+        assert gpu.position() == 4096 and np.isfinite(gpu.logits()).all()
+        with pytest.raises(RuntimeError, match='Context capacity exceeded'):
+            gpu.step(0)
+    finally:
+        gpu.close()
+        oracle.close()
