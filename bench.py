@@ -74,7 +74,19 @@ def main():
     parser.add_argument('--cpu-seconds', type=float, default=12.0)
     parser.add_argument('--no-cpu-baseline', action='store_true')
     parser.add_argument('--no-ttft', action='store_true')
+    parser.add_argument('--copy-calibration', type=int, metavar='MIB',
+                        help='only run a plain device copy of MIB MiB, 5 times (HBM byte-counter calibration)')
     args = parser.parse_args()
+    if args.copy_calibration:
+        from conftest import load_package
+        q = load_package()
+        nbytes = args.copy_calibration << 20
+        src, dst = q.DeviceBuffer(nbytes), q.DeviceBuffer(nbytes)
+        for _ in range(5):
+            q.copy_device(src, dst, nbytes)
+        q.synchronize()
+        print(json.dumps({'copy_calibration_bytes': nbytes, 'launches': 5}))
+        return 0
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (asked for --gpus {args.gpus}); this engine is single-GPU '
               'batch-1 decode and has no multi-GPU path to time.', file=sys.stderr)

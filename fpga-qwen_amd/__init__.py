@@ -62,6 +62,7 @@ SIGNATURES = {
                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_op_copy': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     'qwen_gpu_time_kernel': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_float_p]),
 }
 
@@ -264,3 +265,8 @@ def gemv(tiled, x, rows):
     _check(_LIB.qwen_gpu_op_gemv(tiled.ptr, xd.ptr, yd.ptr, rows, x.size, None))
     synchronize()
     return yd.to_array(np.float32, rows)
+
+
+def copy_device(src, dst, nbytes):
+    """Plain device copy between DeviceBuffers (counter calibration)."""
+    _check(_LIB.qwen_gpu_op_copy(src.ptr, dst.ptr, int(nbytes), None))

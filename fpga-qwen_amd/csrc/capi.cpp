@@ -208,6 +208,15 @@ int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, 
     });
 }
 
+int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream) {
+    return guarded([&] {
+        need(src, "src");
+        need(dst, "dst");
+        qwen_hip::launch_copy(src, dst, bytes, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
 int qwen_gpu_time_kernel(qwen_gpu_model* m, int which, int iterations, float* milliseconds) {
     return guarded([&] {
         need(m, "model");

@@ -18,6 +18,7 @@
 // cache (engine/core.cpp:395-406) and uses them from LDS.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <climits>
 
@@ -712,4 +713,20 @@ void launch_set_step(StepParams* params, int pos, int token, int slot, hipStream
     set_step_kernel<<<1, 1, 0, stream>>>(params, pos, token, slot);
 }
 
+}  // namespace qwen_hip
+
+namespace qwen_hip {
+namespace {
+__global__ void copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+        dst[i] = src[i];
+}
+}  // namespace
+
+void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream) {
+    require(bytes % 16 == 0, "copy: bytes must be a multiple of 16");
+    const size_t n = bytes / 16;
+    const unsigned blocks = unsigned(std::min<size_t>((n + 255) / 256, 8192));
+    if (n) copy_kernel<<<blocks, 256, 0, stream>>>(static_cast<const uint4*>(src), static_cast<uint4*>(dst), n);
+}
 }  // namespace qwen_hip

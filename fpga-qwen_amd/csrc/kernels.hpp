@@ -108,6 +108,9 @@ void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* em
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
 
+// Plain device copy (bytes a multiple of 16), for counter calibration.
+void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);
+
 // Writes the step scalars with one tiny kernel (no host-to-device copy).
 void launch_set_step(StepParams* params, int pos, int token, int slot, hipStream_t stream);
 

@@ -102,6 +102,9 @@ int qwen_gpu_op_tile_matrix(const uint16_t* first, const uint16_t* second, uint1
 /* y[r] = dot(x, W[r]) with the reference dot's chain order (engine/core.cpp:119-147),
  * W chain-tiled; cols in {1024, 2048, 3072}; rows a multiple of 16. */
 int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, int cols, void* stream);
+/* Plain 16-byte-per-thread device copy (bytes a multiple of 16). No reference
+ * counterpart: a kernel of known traffic for calibrating HBM byte counters. */
+int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream);
 /* Average milliseconds of one standalone launch of a decode kernel on the
  * model's stream, timed with HIP events (which: 0 norm+QKV, 1 attention,
  * 2 O, 3 norm+gate/up, 4 down, 5 lm_head). Needs position() > 0; resets the
