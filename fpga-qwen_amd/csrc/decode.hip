@@ -145,7 +145,9 @@ struct GemvArgs {
     const float* in;          // input vector (plain/O/down), residual x (norm modes)
     const float* norm_w;      // RMSNorm weights (QKV, gate/up, lm_head)
     const uint16_t* embed;    // natural embedding, first layer only (QKV)
-    const StepParams* params; // token for the embedding gather
+    const float* in2;         // O: normalized attention output when splits == 1
+    int token;                // first-layer QKV: embedding row
+    int splits;               // O: attention splits to merge (1: copy in2)
     float* out;               // plain/QKV: y; gate/up: activation; lm_head: logits
     float* x;                 // residual stream (O/down add, first-layer QKV store)
     float* hidden;            // lm_head: final normalized hidden
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         if (a.embed) {
             // First layer: x = fp32(E[token]) (engine/core.cpp:382-383), kept as the residual.
             __shared__ float xe[N];
-            const uint16_t* row = a.embed + size_t(a.params->token) * N;
+            const uint16_t* row = a.embed + size_t(a.token) * N;
             for (int j = tid; j < N; j += THREADS) {
                 const float v = h2f(row[j]);
                 xe[j] = v;
@@ -187,6 +189,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     } else if constexpr (MODE == kLmHead) {
         norm_to_lds<N, THREADS>(a.in, a.norm_w, xs, red, blockIdx.x == 0 ? a.hidden : nullptr);
     } else if constexpr (MODE == kO) {
+      if (a.splits == 1) {
+        copy_to_lds<N, THREADS>(a.in2, xs);
+      } else {
         // Merge the attention splits of all 16 heads (flash-decoding merge,
         // fixed split order): o = sum_s w_s o_s / sum_s w_s l_s with
         // w_s = exp(m_s - max); unused splits carry m = -inf, so w_s = 0.
@@ -237,6 +242,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
             }
             xs[xperm(tid + k * THREADS)] = o / cl[k];
         }
+      }
     } else {
         copy_to_lds<N, THREADS>(a.in, xs);
     }
@@ -295,8 +301,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
 // (max, lowest id, nonfinite) partials of the lm_head kernel.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ value, const int* __restrict__ index,
                                                       const int* __restrict__ bad_in, int groups,
-                                                      ArgmaxResult* result, ArgmaxResult* host_result,
-                                                      const StepParams* params) {
+                                                      ArgmaxResult* result, ArgmaxResult* host_out) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float bv = -INFINITY;
     int bi = INT_MAX, bad = 0;
@@ -322,16 +327,9 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
         }
         result->token = bi;
         result->nonfinite = bad;
-        ArgmaxResult* h = host_result + params->slot;
-        h->token = bi;
-        h->nonfinite = bad;
+        host_out->token = bi;
+        host_out->nonfinite = bad;
     }
-}
-
-__global__ void set_step_kernel(StepParams* params, int pos, int token, int slot) {
-    params->pos = pos;
-    params->token = token;
-    params->slot = slot;
 }
 
 struct AttnArgs {
@@ -342,8 +340,9 @@ struct AttnArgs {
     const float* sines;
     uint16_t* keys;        // layer base [8][context][128]
     uint16_t* values;
-    const StepParams* params;
+    int pos;               // position being written
     float* partial;        // [8][kAttnSplits][kAttnPartial]
+    float* attended;       // [2048], written instead when there is one split
     int context;
     float scale;           // 1.0f / sqrt(128.0f)
 };
@@ -385,7 +384,7 @@ __device__ __forceinline__ float head_norm_rope(float raw, const float* w, const
 __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     const int s = blockIdx.x, g = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = a.params->pos, n = pos + 1;
+    const int pos = a.pos, n = pos + 1;
     int chunk, ns;
     attn_split(n, chunk, ns);
     if (s >= ns) {  // unused split: contributes nothing to the merge
@@ -563,6 +562,10 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     if (tid < 256) {
         const int h = tid >> 7;
         const float o = (opart[0][h][j] + opart[1][h][j]) + (opart[2][h][j] + opart[3][h][j]);
+        if (ns == 1) {  // nothing to merge: normalize here
+            a.attended[(2 * g + h) * 128 + j] = o / run_sum[h];
+            return;
+        }
         float* part = a.partial + (size_t(g) * kAttnSplits + s) * kAttnPartial + h * 132;
         part[j] = o;
         if (j == 0) {
@@ -626,7 +629,7 @@ void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, 
     }
 }
 
-void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed, const StepParams* params,
+void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream) {
     switch (which) {
@@ -636,7 +639,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             q.in = s.x;
             q.norm_w = L.in_norm;
             q.embed = embed;
-            q.params = params;
+            q.token = token;
             q.out = s.qkv;
             q.x = s.x;
             launch_gemv<kHidden, kQKV>(q, kQKVRows, stream);
@@ -651,8 +654,9 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             at.sines = sines;
             at.keys = L.keys;
             at.values = L.values;
-            at.params = params;
+            at.pos = pos;
             at.partial = s.attn_partial;
+            at.attended = s.attended;
             at.context = context;
             at.scale = 1.0f / std::sqrt(128.0f);
             attn_decode_kernel<<<dim3(kAttnSplits, kKVHeads), 512, 0, stream>>>(at);
@@ -662,7 +666,12 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             GemvArgs o{};
             o.w = L.o_t;
             o.in = s.attn_partial;
-            o.params = params;
+            o.in2 = s.attended;
+            {
+                int chunk, splits;
+                attn_split(pos + 1, chunk, splits);
+                o.splits = splits;
+            }
             o.x = s.x;
             launch_gemv<kQDim, kO>(o, kHidden, stream);
             break;
@@ -688,13 +697,14 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
     }
 }
 
-void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, const StepParams* params, const float* cosines,
+void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,
                          const float* sines, int context, const DecodeScratch& s, hipStream_t stream) {
     for (int which = 0; which < 5; ++which)
-        launch_layer_kernel(which, L, which == 0 ? embed : nullptr, params, cosines, sines, context, s, stream);
+        launch_layer_kernel(which, L, which == 0 ? embed : nullptr, pos, token, cosines, sines, context, s, stream);
 }
 
-void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, hipStream_t stream) {
+void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, ArgmaxResult* host_out,
+                    hipStream_t stream) {
     GemvArgs a{};
     a.w = lm_t;
     a.in = s.x;
@@ -705,12 +715,7 @@ void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeS
     a.lm_index = s.lm_index;
     a.lm_bad = s.lm_bad;
     gemv_kernel<kHidden, kLmWaves, kLmHead><<<kLmGroups, 64 * kLmWaves, 0, stream>>>(a);
-    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, s.host_result,
-                                          s.params);
-}
-
-void launch_set_step(StepParams* params, int pos, int token, int slot, hipStream_t stream) {
-    set_step_kernel<<<1, 1, 0, stream>>>(params, pos, token, slot);
+    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, host_out);
 }
 
 }  // namespace qwen_hip

@@ -1,10 +1,9 @@
-// Engine: device state, weight upload, captured decode graphs and the
+// Engine: device state, weight upload, the per-token kernel sequence and the
 // qwen_cpu::Model semantics (engine/core.cpp:707-758) on top of them.
 #include "engine.hpp"
 
 #include <algorithm>
 #include <cmath>
-#include <cstdlib>
 #include <cstring>
 
 #include "pack.hpp"
@@ -114,6 +113,7 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
         DecodeScratch& s = scratch_;
         s.x = device_alloc<float>(kHidden);
         s.qkv = device_alloc<float>(kQKVRows);
+        s.attended = device_alloc<float>(kQDim);
         s.act = device_alloc<float>(kFFN);
         s.logits = device_alloc<float>(kVocab);
         s.hidden = device_alloc<float>(kHidden);
@@ -126,34 +126,14 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
         ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
         base_logits_ = device_alloc<float>(kVocab);
         base_hidden_ = device_alloc<float>(kHidden);
-        params_dev_ = device_alloc<StepParams>(1);
-        HIP_CHECK(hipMemset(params_dev_, 0, sizeof(StepParams)));
         void* pinned = nullptr;
         HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
         result_host_ = static_cast<ArgmaxResult*>(pinned);
         std::memset(result_host_, 0, sizeof(ArgmaxResult) * 3);
-        s.host_result = result_host_;
-        s.params = params_dev_;
         HIP_CHECK(hipStreamSynchronize(stream_));
         HIP_CHECK(hipFree(stage));
         allocations_.erase(std::find(allocations_.begin(), allocations_.end(), static_cast<void*>(stage)));
 
-        // Capture: all 28 layers in one graph, the head in another. Kernels
-        // read position/token from params_dev_, so each graph is replayed as is.
-        // Direct launches are the default (measured as fast as graph replay);
-        // QWEN_GPU_GRAPHS=1 replays the captured graphs instead.
-        const char* graphs_env = std::getenv("QWEN_GPU_GRAPHS");
-        use_graphs_ = graphs_env && std::string(graphs_env) == "1";
-        if (use_graphs_) {
-            HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-            launch_layers();
-            HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[0]));
-            HIP_CHECK(hipGraphInstantiate(&layer_graph_, graphs_[0], nullptr, nullptr, 0));
-            HIP_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-            launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
-            HIP_CHECK(hipStreamEndCapture(stream_, &graphs_[1]));
-            HIP_CHECK(hipGraphInstantiate(&head_graph_, graphs_[1], nullptr, nullptr, 0));
-        }
         HIP_CHECK(hipGetLastError());
     } catch (...) {
         release();
@@ -163,15 +143,9 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
 
 void Engine::release() {
     if (stream_) (void)hipStreamSynchronize(stream_);
-    if (layer_graph_) (void)hipGraphExecDestroy(layer_graph_);
-    if (head_graph_) (void)hipGraphExecDestroy(head_graph_);
-    for (hipGraph_t g : graphs_)
-        if (g) (void)hipGraphDestroy(g);
     for (void* p : allocations_) (void)hipFree(p);
     if (result_host_) (void)hipHostFree(result_host_);
     if (stream_) (void)hipStreamDestroy(stream_);
-    layer_graph_ = head_graph_ = nullptr;
-    graphs_[0] = graphs_[1] = nullptr;
     allocations_.clear();
     result_host_ = nullptr;
     stream_ = nullptr;
@@ -201,24 +175,15 @@ void Engine::truncate(int position) {
     invalidate();
 }
 
-void Engine::launch_layers() {
-    for (int l = 0; l < kLayers; ++l)
-        launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, params_dev_, cosines_, sines_, options_.context,
-                            scratch_, stream_);
-}
-
+// One token through the 28 layers (5 kernels each) and, when `head`, the
+// final norm, tied lm_head and greedy argmax into host result slot
+// `result_slot`. The step scalars are kernel arguments.
 void Engine::run_token(int token, bool head, int result_slot) {
-    launch_set_step(params_dev_, pos_, token, result_slot, stream_);
-    if (use_graphs_)
-        HIP_CHECK(hipGraphLaunch(layer_graph_, stream_));
-    else
-        launch_layers();
-    if (head) {
-        if (use_graphs_)
-            HIP_CHECK(hipGraphLaunch(head_graph_, stream_));
-        else
-            launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
-    }
+    for (int l = 0; l < kLayers; ++l)
+        launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, pos_, token, cosines_, sines_, options_.context,
+                            scratch_, stream_);
+    if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
+    HIP_CHECK(hipGetLastError());
     ++pos_;
 }
 
@@ -345,13 +310,12 @@ float Engine::time_kernel(int which, int iterations) {
     // afterwards. Layer kernels rotate over all 28 layers so that, as in a
     // real step, their weights (about 880 MB in total) stream from HBM rather
     // than from the 256 MB Infinity Cache.
-    launch_set_step(params_dev_, pos_ - 1, 0, 0, stream_);
     int layer = 0;
     auto launch = [&] {
         if (which == 5)
-            launch_lm_head(lm_t_, final_norm_, scratch_, stream_);
+            launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
         else
-            launch_layer_kernel(which, layers_[layer], nullptr, params_dev_, cosines_, sines_, options_.context,
+            launch_layer_kernel(which, layers_[layer], nullptr, pos_ - 1, 0, cosines_, sines_, options_.context,
                                 scratch_, stream_);
         layer = (layer + 1) % kLayers;
     };

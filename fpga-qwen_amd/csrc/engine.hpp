@@ -51,7 +51,6 @@ private:
     void append(const int* ids, size_t count);
     void run_token(int token, bool head, int result_slot);
     void release();
-    void launch_layers();
     void sync();
     void invalidate();
 
@@ -65,16 +64,11 @@ private:
     float* cosines_ = nullptr;
     float* sines_ = nullptr;
     DecodeScratch scratch_{};
-    StepParams* params_dev_ = nullptr;   // device slot read by the captured kernels
     ArgmaxResult* result_host_ = nullptr;  // pinned [3]: current, verify row 0, verify row 1
-    hipGraphExec_t layer_graph_ = nullptr;  // 28 decode layers
-    hipGraphExec_t head_graph_ = nullptr;   // final norm + lm_head + argmax
-    hipGraph_t graphs_[2] = {nullptr, nullptr};
     float* ver_logits_ = nullptr;   // device [2 x vocab]
     float* ver_hidden_ = nullptr;   // device [2 x 1024]
     float* base_logits_ = nullptr;  // public logits saved across a verification
     float* base_hidden_ = nullptr;
-    bool use_graphs_ = true;
     int pos_ = 0;
     bool has_logits_ = false;
     bool pending_ = false;

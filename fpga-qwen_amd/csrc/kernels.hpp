@@ -23,13 +23,6 @@
 
 namespace qwen_hip {
 
-// Per-step scalars, device resident so captured graphs are position independent.
-struct StepParams {
-    int pos;    // position being written (tokens before it are cached)
-    int token;  // input token id
-    int slot;   // index of the host result slot the argmax writes
-};
-
 // Greedy selection result of the lm_head kernel.
 struct ArgmaxResult {
     int token;
@@ -72,6 +65,7 @@ struct LayerDevice {
 struct DecodeScratch {
     float* x;             // [1024] residual stream
     float* qkv;           // [4096] raw projections
+    float* attended;      // [2048] normalized attention output (single-split steps)
     float* act;           // [3072]
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
@@ -81,8 +75,6 @@ struct DecodeScratch {
     int* lm_index;        // [kLmGroups]
     int* lm_bad;          // [kLmGroups]
     ArgmaxResult* result; // [1] device copy of the selection
-    ArgmaxResult* host_result;  // pinned host slots, indexed by StepParams::slot
-    const StepParams* params;
 };
 
 // Layout conversion: natural row-major FP16 [rows x cols] -> chain-tiled.
@@ -98,24 +90,25 @@ void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, 
 // One decode layer (five kernels): norm+QKV, attention (+q/k norm, RoPE, KV
 // write) into per-split partials, O (+split combine prologue, +residual),
 // norm+gate/up (+SwiGLU), down (+residual).
-// When `embed` is non-null (first layer) x is first loaded from embed[token].
-void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, const StepParams* params,
+// pos is the position being written (n = pos + 1 cached positions after
+// it); when `embed` is non-null (first layer) x is first loaded from
+// embed[token]. Step scalars travel as kernel arguments.
+void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
 
 // One kernel of a decode layer: 0 norm+QKV, 1 attention, 2 O, 3 norm+gate/up, 4 down.
-void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, const StepParams* params,
+void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
 
 // Plain device copy (bytes a multiple of 16), for counter calibration.
 void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);
 
-// Writes the step scalars with one tiny kernel (no host-to-device copy).
-void launch_set_step(StepParams* params, int pos, int token, int slot, hipStream_t stream);
-
 // Final norm + tied lm_head GEMV + greedy argmax (lowest id on ties,
-// nonfinite flagged). Also writes the final hidden vector.
-void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, hipStream_t stream);
+// nonfinite flagged). Also writes the final hidden vector; the selection
+// goes to s.result and to `host_out` (pinned host memory).
+void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, ArgmaxResult* host_out,
+                    hipStream_t stream);
 
 }  // namespace qwen_hip
