@@ -62,6 +62,8 @@ SIGNATURES = {
                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_op_gemm': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_copy': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     'qwen_gpu_time_kernel': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_float_p]),
 }
@@ -270,3 +272,17 @@ def gemv(tiled, x, rows):
 def copy_device(src, dst, nbytes):
     """Plain device copy between DeviceBuffers (counter calibration)."""
     _check(_LIB.qwen_gpu_op_copy(src.ptr, dst.ptr, int(nbytes), None))
+
+
+def gemm(a, w, c=None):
+    """C = A W^T (or C += A W^T when C is given) on the matrix cores: A FP32
+    [M, K], W FP16 [N, K] natural layout. Returns C as a NumPy array."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w, np.float16)
+    m, k = a.shape
+    n = w.shape[0]
+    ad, wd = DeviceBuffer.from_array(a), DeviceBuffer.from_array(w)
+    cd = DeviceBuffer.from_array(np.ascontiguousarray(c, np.float32)) if c is not None else DeviceBuffer(m * n * 4)
+    _check(_LIB.qwen_gpu_op_gemm(ad.ptr, wd.ptr, cd.ptr, m, n, k, int(c is not None), None))
+    synchronize()
+    return cd.to_array(np.float32, m * n).reshape(m, n)

@@ -5,6 +5,7 @@
 
 #include "engine.hpp"
 #include "pack.hpp"
+#include "prefill.hpp"
 
 struct qwen_gpu_model {
     qwen_hip::Engine engine;
@@ -205,6 +206,17 @@ int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, 
         qwen_hip::launch_gemv_plain(tiled, x, y, rows, cols, static_cast<hipStream_t>(stream));
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(e));
+    });
+}
+
+int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
+                     void* stream) {
+    return guarded([&] {
+        need(a, "a");
+        need(w, "w");
+        need(c, "c");
+        qwen_hip::launch_gemm(a, w, c, m, n, k, accumulate != 0, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
     });
 }
 

@@ -7,6 +7,7 @@
 #include <cstring>
 
 #include "pack.hpp"
+#include "prefill.hpp"
 
 #define HIP_CHECK(expr)                                                                                  \
     do {                                                                                                 \
@@ -52,9 +53,8 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
         final_norm_ = device_alloc<float>(kHidden);
         HIP_CHECK(hipMemcpy(final_norm_, pack.tensor("model.norm.weight").norm, kHidden * 4, hipMemcpyHostToDevice));
 
-        // Layer matrices go through a natural-layout staging buffer, then into
-        // their chain-tiled homes.
-        uint16_t* stage = device_alloc<uint16_t>(size_t(2 * kFFN) * kHidden);
+        // Layer matrices stay in natural layout (prefill GEMMs) and get a
+        // chain-tiled copy (decode GEMVs).
         auto upload = [&](uint16_t* dst, const PackTensor& t) {
             HIP_CHECK(hipMemcpy(dst, t.half, size_t(t.rows) * t.cols * 2, hipMemcpyHostToDevice));
         };
@@ -64,27 +64,29 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
             return d;
         };
         layers_.resize(kLayers);
+        prefill_layers_.resize(kLayers);
         for (int l = 0; l < kLayers; ++l) {
             LayerDevice& L = layers_[l];
+            PrefillLayer& P = prefill_layers_[l];
+            uint16_t* qkv_n = device_alloc<uint16_t>(size_t(kQKVRows) * kHidden);
+            upload(qkv_n, pack.layer(l, "self_attn.q_proj.weight"));
+            upload(qkv_n + size_t(kQDim) * kHidden, pack.layer(l, "self_attn.k_proj.weight"));
+            upload(qkv_n + size_t(kQDim + kKVDim) * kHidden, pack.layer(l, "self_attn.v_proj.weight"));
+            uint16_t* o_n = device_alloc<uint16_t>(size_t(kHidden) * kQDim);
+            upload(o_n, pack.layer(l, "self_attn.o_proj.weight"));
+            uint16_t* gu_n = device_alloc<uint16_t>(size_t(2 * kFFN) * kHidden);
+            upload(gu_n, pack.layer(l, "mlp.gate_proj.weight"));
+            upload(gu_n + size_t(kFFN) * kHidden, pack.layer(l, "mlp.up_proj.weight"));
+            uint16_t* down_n = device_alloc<uint16_t>(size_t(kHidden) * kFFN);
+            upload(down_n, pack.layer(l, "mlp.down_proj.weight"));
             uint16_t* qkv_t = device_alloc<uint16_t>(size_t(kQKVRows) * kHidden);
-            upload(stage, pack.layer(l, "self_attn.q_proj.weight"));
-            upload(stage + size_t(kQDim) * kHidden, pack.layer(l, "self_attn.k_proj.weight"));
-            upload(stage + size_t(kQDim + kKVDim) * kHidden, pack.layer(l, "self_attn.v_proj.weight"));
-            launch_tile_matrix(stage, nullptr, qkv_t, kQKVRows, kHidden, stream_);
-            HIP_CHECK(hipStreamSynchronize(stream_));
+            launch_tile_matrix(qkv_n, nullptr, qkv_t, kQKVRows, kHidden, stream_);
             uint16_t* o_t = device_alloc<uint16_t>(size_t(kHidden) * kQDim);
-            upload(stage, pack.layer(l, "self_attn.o_proj.weight"));
-            launch_tile_matrix(stage, nullptr, o_t, kHidden, kQDim, stream_);
-            HIP_CHECK(hipStreamSynchronize(stream_));
+            launch_tile_matrix(o_n, nullptr, o_t, kHidden, kQDim, stream_);
             uint16_t* gu_t = device_alloc<uint16_t>(size_t(2 * kFFN) * kHidden);
-            upload(stage, pack.layer(l, "mlp.gate_proj.weight"));
-            upload(stage + size_t(kFFN) * kHidden, pack.layer(l, "mlp.up_proj.weight"));
-            launch_tile_matrix(stage, stage + size_t(kFFN) * kHidden, gu_t, kFFN, kHidden, stream_);
-            HIP_CHECK(hipStreamSynchronize(stream_));
+            launch_tile_matrix(gu_n, gu_n + size_t(kFFN) * kHidden, gu_t, kFFN, kHidden, stream_);
             uint16_t* down_t = device_alloc<uint16_t>(size_t(kHidden) * kFFN);
-            upload(stage, pack.layer(l, "mlp.down_proj.weight"));
-            launch_tile_matrix(stage, nullptr, down_t, kHidden, kFFN, stream_);
-            HIP_CHECK(hipStreamSynchronize(stream_));
+            launch_tile_matrix(down_n, nullptr, down_t, kHidden, kFFN, stream_);
             L.qkv_t = qkv_t;
             L.o_t = o_t;
             L.gateup_t = gu_t;
@@ -95,7 +97,9 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
             L.k_norm = upload_norm(pack.layer(l, "self_attn.k_norm.weight"));
             L.keys = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
             L.values = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
+            P = PrefillLayer{qkv_n, o_n, gu_n, down_n, L.in_norm, L.post_norm, L.q_norm, L.k_norm, L.keys, L.values};
         }
+        HIP_CHECK(hipStreamSynchronize(stream_));
 
         // RoPE tables in double, stored as FP32 (engine/core.cpp:287-288).
         std::vector<float> cs(size_t(ctx) * 64), sn(cs.size());
@@ -130,9 +134,17 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
         HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
         result_host_ = static_cast<ArgmaxResult*>(pinned);
         std::memset(result_host_, 0, sizeof(ArgmaxResult) * 3);
+        PrefillScratch& ps = prefill_;
+        ps.x = device_alloc<float>(size_t(kChunk) * kHidden);
+        ps.h = device_alloc<float>(size_t(kChunk) * kHidden);
+        ps.qkv = device_alloc<float>(size_t(kChunk) * kQKVRows);
+        ps.attended = device_alloc<float>(size_t(kChunk) * kQDim);
+        ps.gu = device_alloc<float>(size_t(kChunk) * 2 * kFFN);
+        ps.act = device_alloc<float>(size_t(kChunk) * kFFN);
+        ids_dev_ = device_alloc<int>(size_t(ctx));
+        HIP_CHECK(hipHostMalloc(&pinned, sizeof(int) * size_t(ctx), hipHostMallocDefault));
+        ids_host_ = static_cast<int*>(pinned);
         HIP_CHECK(hipStreamSynchronize(stream_));
-        HIP_CHECK(hipFree(stage));
-        allocations_.erase(std::find(allocations_.begin(), allocations_.end(), static_cast<void*>(stage)));
 
         HIP_CHECK(hipGetLastError());
     } catch (...) {
@@ -145,6 +157,8 @@ void Engine::release() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     for (void* p : allocations_) (void)hipFree(p);
     if (result_host_) (void)hipHostFree(result_host_);
+    if (ids_host_) (void)hipHostFree(ids_host_);
+    ids_host_ = nullptr;
     if (stream_) (void)hipStreamDestroy(stream_);
     allocations_.clear();
     result_host_ = nullptr;
@@ -194,7 +208,27 @@ void Engine::append(const int* ids, size_t count) {
     require(count <= size_t(options_.context - pos_), "Context capacity exceeded");
     for (size_t i = 0; i < count; ++i) require(ids[i] >= 0 && ids[i] < kVocab, "Token ID out of range");
     invalidate();
-    for (size_t i = 0; i < count; ++i) run_token(ids[i], i + 1 == count, 0);
+    // 512-row chunks counted from the start of this call (engine/core.cpp:712).
+    // A chunk of one row uses the batch-1 path, as in the reference.
+    std::copy(ids, ids + count, ids_host_);
+    HIP_CHECK(hipMemcpyAsync(ids_dev_, ids_host_, count * sizeof(int), hipMemcpyHostToDevice, stream_));
+    for (size_t begin = 0; begin < count; begin += kChunk) {
+        const int rows = int(std::min<size_t>(kChunk, count - begin));
+        const bool last = begin + rows == count;
+        if (rows == 1) {
+            run_token(ids[begin], last, 0);
+            continue;
+        }
+        launch_prefill_chunk(prefill_layers_.data(), embed_, ids_dev_ + begin, rows, pos_, cosines_, sines_,
+                             options_.context, prefill_, stream_);
+        pos_ += rows;
+        if (last) {
+            HIP_CHECK(hipMemcpyAsync(scratch_.x, prefill_.x + size_t(rows - 1) * kHidden, kHidden * sizeof(float),
+                                     hipMemcpyDeviceToDevice, stream_));
+            launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
+        }
+    }
+    HIP_CHECK(hipGetLastError());
     sync();
     has_logits_ = true;
 }

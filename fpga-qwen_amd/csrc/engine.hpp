@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "kernels.hpp"
+#include "prefill.hpp"
 
 namespace qwen_hip {
 
@@ -58,6 +59,10 @@ private:
     hipStream_t stream_ = nullptr;
     std::vector<void*> allocations_;
     std::vector<LayerDevice> layers_;
+    std::vector<PrefillLayer> prefill_layers_;
+    PrefillScratch prefill_{};
+    int* ids_dev_ = nullptr;    // prompt ids of the current call
+    int* ids_host_ = nullptr;   // pinned staging for them
     uint16_t* embed_ = nullptr;     // natural [vocab x 1024]
     uint16_t* lm_t_ = nullptr;      // chain-tiled embedding
     float* final_norm_ = nullptr;

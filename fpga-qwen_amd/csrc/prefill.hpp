@@ -1,0 +1,46 @@
+// Batched prefill (chunks of up to 512 rows; engine/core.cpp:353-646, 712).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "qwen_common.hpp"
+
+namespace qwen_hip {
+
+// Natural row-major FP16 weights of one layer for the matrix-core GEMMs.
+struct PrefillLayer {
+    const uint16_t* qkv_n;     // [4096 x 1024]: q rows, k rows, v rows
+    const uint16_t* o_n;       // [1024 x 2048]
+    const uint16_t* gateup_n;  // [6144 x 1024]: 3072 gate rows then 3072 up rows
+    const uint16_t* down_n;    // [1024 x 3072]
+    const float* in_norm;
+    const float* post_norm;
+    const float* q_norm;
+    const float* k_norm;
+    uint16_t* keys;            // [8][context][128], chain-permuted rows
+    uint16_t* values;          // [8][context][128]
+};
+
+// FP32 activations of one chunk (512 rows each).
+struct PrefillScratch {
+    float* x;         // [512 x 1024] residual stream
+    float* h;         // [512 x 1024] normalized
+    float* qkv;       // [512 x 4096]
+    float* attended;  // [512 x 2048]
+    float* gu;        // [512 x 6144]
+    float* act;       // [512 x 3072]
+};
+
+// C[M x N] (+)= A[M x K] . W[N x K]^T; A FP32 split into FP16 hi + lo on the
+// matrix cores; N, K multiples of 64.
+void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
+                 hipStream_t stream);
+
+// All 28 layers for `rows` prompt ids (device) at positions pos0..pos0+rows-1:
+// K/V land in the cache, the final residual rows in s.x.
+void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, const int* ids_dev, int rows, int pos0,
+                          const float* cosines, const float* sines, int context, const PrefillScratch& s,
+                          hipStream_t stream);
+
+}  // namespace qwen_hip

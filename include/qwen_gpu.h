@@ -102,6 +102,12 @@ int qwen_gpu_op_tile_matrix(const uint16_t* first, const uint16_t* second, uint1
 /* y[r] = dot(x, W[r]) with the reference dot's chain order (engine/core.cpp:119-147),
  * W chain-tiled; cols in {1024, 2048, 3072}; rows a multiple of 16. */
 int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, int cols, void* stream);
+/* Batched projection of the prefill path (engine/core.cpp:292-294, the
+ * cblas_sgemm branch): C[M x N] = A[M x K] . W[N x K]^T, or C += when
+ * accumulate != 0. A is FP32 (split exactly into FP16 hi + lo on the matrix
+ * cores), W natural row-major FP16; N and K multiples of 64, M >= 1. */
+int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
+                     void* stream);
 /* Plain 16-byte-per-thread device copy (bytes a multiple of 16). No reference
  * counterpart: a kernel of known traffic for calibrating HBM byte counters. */
 int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream);

@@ -1,0 +1,90 @@
+"""Batched prefill on the matrix cores (engine/core.cpp:292-294, 353-646).
+
+The reference multiplies FP32 activations by FP32-widened weights
+(cblas_sgemm, closed source, summation order unknown: parity unpinned
+bitwise, held to tolerance). The GPU GEMM splits each activation exactly into
+FP16 hi + lo and accumulates in FP32; it is checked against an FP64 product
+with a bound proportional to sum |a||w|, for row independence from the
+chunk size (needed for exact canonical prefix reuse), and end to end through
+the oracle gate and the reuse-equals-fresh invariant
+(tools/check_native_cpu_prefix.py).
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_binding import compare_logits
+
+PROMPTS = json.loads((Path(__file__).parent / 'golden' / 'prompts.json').read_text())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('m,n,k', [(1, 1024, 1024), (37, 4096, 1024), (85, 1024, 2048), (512, 6144, 1024),
+                                   (129, 1024, 3072)])
+def test_gemm_against_fp64(qpkg, m, n, k):
+    rng = np.random.default_rng(21)
+    a = rng.standard_normal((m, k), dtype=np.float32) * 3
+    w = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float16)
+    got = qpkg.gemm(a, w)
+    ref = a.astype(np.float64) @ w.astype(np.float64).T
+    bound = 4e-6 * (np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T) + 1e-7
+    err = np.abs(got - ref)
+    assert np.all(err <= bound), float((err / bound).max())
+    base = rng.standard_normal((m, n)).astype(np.float32)
+    acc = qpkg.gemm(a, w, base)
+    assert np.array_equal(acc, (base + got).astype(np.float32))
+
+
+@pytest.mark.gpu
+def test_gemm_rows_independent_of_chunk(qpkg):
+    rng = np.random.default_rng(22)
+    a = rng.standard_normal((512, 1024), dtype=np.float32)
+    w = (rng.standard_normal((1024, 1024), dtype=np.float32) * 0.02).astype(np.float16)
+    full = qpkg.gemm(a, w)
+    for rows in (slice(0, 37), slice(100, 101), slice(300, 512)):
+        part = qpkg.gemm(a[rows], w)
+        assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_prefill_1024_matches_oracle(qpkg, pack0, oracle_lib):
+    """The 1024-token prompt (seed 2): two full 512-row chunks."""
+    prompt = PROMPTS['prefill_1024']
+    with qpkg.Model(pack0) as gpu:
+        oracle = oracle_lib.model(pack0, 16, 16, 4096)
+        try:
+            gpu.prefill(prompt)
+            oracle.prefill(prompt)
+            result = compare_logits(gpu.logits(), oracle.logits())
+            print(result)
+            assert result['passed'], result
+            for _ in range(3):
+                token = gpu.greedy()
+                gpu.step(token)
+                oracle.step(token)
+                result = compare_logits(gpu.logits(), oracle.logits())
+                assert result['passed'], result
+        finally:
+            oracle.close()
+
+
+@pytest.mark.gpu
+def test_canonical_prefix_reuse_equals_fresh(qpkg, pack0):
+    """Rewind to a 512 boundary and prefill the rest == one fresh prefill
+    (chunk shapes match; INTERFACE.md:94-111, tools/check_native_cpu_prefix.py)."""
+    prompt = PROMPTS['long_3968'][:1100]
+    with qpkg.Model(pack0) as m:
+        m.prefill(prompt)
+        fresh = (m.logits(), m.hidden())
+        m.step(7)
+        m.truncate(512)
+        m.prefill(prompt[512:])
+        assert np.array_equal(m.logits().view(np.uint32), fresh[0].view(np.uint32))
+        assert np.array_equal(m.hidden().view(np.uint32), fresh[1].view(np.uint32))
+        m.reset()
+        m.prefill(prompt[:1024])
+        m.truncate(1024)
+        m.prefill(prompt[1024:])
+        assert np.array_equal(m.logits().view(np.uint32), fresh[0].view(np.uint32))
