@@ -194,54 +194,62 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
       } else {
         // Merge the attention splits of all 16 heads (flash-decoding merge,
         // fixed split order): o = sum_s w_s o_s / sum_s w_s l_s with
-        // w_s = exp(m_s - max); unused splits carry m = -inf, so w_s = 0.
-        // All statistics and split outputs load in one round.
-        static_assert(THREADS == 128 && kQHeads * kAttnSplits <= THREADS, "O prologue layout");
+        // w_s = exp(m_s - max). The first 4 splits' outputs load together
+        // with all statistics; further splits follow in rounds of 4.
+        static_assert(THREADS == 128 && kQHeads * kAttnSplits == 2 * THREADS, "O prologue layout");
+        constexpr int R = 4;
+        const int ns = a.splits;
         __shared__ float cw[kQHeads][kAttnSplits];
         __shared__ float cl[kQHeads];
-        float part_o[N / THREADS][kAttnSplits];
+        __shared__ float stat[kQHeads][kAttnSplits][2];
+        auto part = [&](int head, int sp) {
+            return a.in + (size_t(head >> 1) * kAttnSplits + sp) * kAttnPartial + (head & 1) * 132;
+        };
+        float po[N / THREADS][R];
 #pragma unroll
         for (int k = 0; k < N / THREADS; ++k)  // output j = tid + 128 k belongs to head k
 #pragma unroll
-            for (int sp = 0; sp < kAttnSplits; ++sp)
-                part_o[k][sp] = a.in[(size_t(k >> 1) * kAttnSplits + sp) * kAttnPartial + (k & 1) * 132 + tid];
-        float m_s = -INFINITY, l_s = 0.f;
-        const int sh = tid / kAttnSplits, ss = tid % kAttnSplits;
-        if (tid < kQHeads * kAttnSplits) {
-            const float* st = a.in + (size_t(sh >> 1) * kAttnSplits + ss) * kAttnPartial + (sh & 1) * 132;
-            m_s = st[128];
-            l_s = st[129];
-        }
-        __shared__ float stat[kQHeads][kAttnSplits][2];
-        if (tid < kQHeads * kAttnSplits) {
-            stat[sh][ss][0] = m_s;
-            stat[sh][ss][1] = l_s;
+            for (int sp = 0; sp < R; ++sp) po[k][sp] = sp < ns ? part(k, sp)[tid] : 0.f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {  // statistics: entry tid + 128 e = (head, split)
+            const int idx = tid + THREADS * e, sh = idx / kAttnSplits, ss = idx % kAttnSplits;
+            stat[sh][ss][0] = ss < ns ? part(sh, ss)[128] : -INFINITY;
+            stat[sh][ss][1] = ss < ns ? part(sh, ss)[129] : 0.f;
         }
         __syncthreads();
         if (tid < kQHeads) {
             float mx = -INFINITY;
-#pragma unroll
-            for (int k = 0; k < kAttnSplits; ++k) mx = fmaxf(mx, stat[tid][k][0]);
+            for (int k = 0; k < ns; ++k) mx = fmaxf(mx, stat[tid][k][0]);
             float l = 0.f;
-#pragma unroll
-            for (int k = 0; k < kAttnSplits; ++k) {
-                const float w = stat[tid][k][0] == -INFINITY ? 0.f : expf(stat[tid][k][0] - mx);
+            for (int k = 0; k < ns; ++k) {
+                const float w = expf(stat[tid][k][0] - mx);
                 cw[tid][k] = w;
                 l += w * stat[tid][k][1];
             }
             cl[tid] = l;
         }
         __syncthreads();
+        float o[N / THREADS];
 #pragma unroll
         for (int k = 0; k < N / THREADS; ++k) {
-            float o = 0.f;
+            o[k] = 0.f;
 #pragma unroll
-            for (int sp = 0; sp < kAttnSplits; ++sp) {
-                const float w = cw[k][sp];
-                o += w != 0.f ? w * part_o[k][sp] : 0.f;
-            }
-            xs[xperm(tid + k * THREADS)] = o / cl[k];
+            for (int sp = 0; sp < R; ++sp)
+                if (sp < ns) o[k] += cw[k][sp] * po[k][sp];
         }
+        for (int s0 = R; s0 < ns; s0 += R) {
+#pragma unroll
+            for (int k = 0; k < N / THREADS; ++k)
+#pragma unroll
+                for (int sp = 0; sp < R; ++sp) po[k][sp] = s0 + sp < ns ? part(k, s0 + sp)[tid] : 0.f;
+#pragma unroll
+            for (int k = 0; k < N / THREADS; ++k)
+#pragma unroll
+                for (int sp = 0; sp < R; ++sp)
+                    if (s0 + sp < ns) o[k] += cw[k][s0 + sp] * po[k][sp];
+        }
+#pragma unroll
+        for (int k = 0; k < N / THREADS; ++k) xs[xperm(tid + k * THREADS)] = o[k] / cl[k];
       }
     } else {
         copy_to_lds<N, THREADS>(a.in, xs);
@@ -387,14 +395,7 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     const int pos = a.pos, n = pos + 1;
     int chunk, ns;
     attn_split(n, chunk, ns);
-    if (s >= ns) {  // unused split: contributes nothing to the merge
-        if (threadIdx.x < 2) {
-            float* part = a.partial + (size_t(g) * kAttnSplits + s) * kAttnPartial + threadIdx.x * 132;
-            part[128] = -INFINITY;
-            part[129] = 0.f;
-        }
-        return;
-    }
+    if (s >= ns) return;  // the grid covers exactly the active splits
     const int t_begin = s * chunk, t_end = min(n, t_begin + chunk);
     const size_t head_base = size_t(g) * a.context;
     const int quarter = tid >> 7, j = tid & 127, c = tid & 7;
@@ -659,7 +660,9 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             at.attended = s.attended;
             at.context = context;
             at.scale = 1.0f / std::sqrt(128.0f);
-            attn_decode_kernel<<<dim3(kAttnSplits, kKVHeads), 512, 0, stream>>>(at);
+            int chunk, splits;
+            attn_split(pos + 1, chunk, splits);
+            attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(at);
             break;
         }
         case 2: {

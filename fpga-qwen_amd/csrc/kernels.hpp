@@ -29,22 +29,17 @@ struct ArgmaxResult {
     int nonfinite;
 };
 
-inline constexpr int kAttnSplits = 4;           // max position splits per KV head
-inline constexpr int kAttnTile = 256;           // positions per attention tile (online softmax)
+inline constexpr int kAttnSplits = 16;          // max position splits per KV head
+inline constexpr int kAttnTile = 256;           // positions per split (one online-softmax tile)
 inline constexpr int kAttnPartial = 2 * 132;    // per split: 2 heads x (128 o + m + l + pad)
 
 // Position splitting of decode attention over n = pos + 1 cached positions:
-// up to 512 positions, chunks of 128 (<= 4 splits); beyond, 4 chunks of a
-// multiple of 256 positions (<= 1024 for a 4096 context).
+// one 256-position tile per split, up to 16 splits for a 4096 context.
 __host__ __device__ inline void attn_split(int n, int& chunk, int& splits) {
-    if (n <= 512) {
-        chunk = 128;
-    } else {
-        chunk = (n + kAttnSplits - 1) / kAttnSplits;
-        chunk = (chunk + kAttnTile - 1) / kAttnTile * kAttnTile;
-    }
-    splits = (n + chunk - 1) / chunk;
+    chunk = kAttnTile;
+    splits = (n + kAttnTile - 1) / kAttnTile;
 }
+
 inline constexpr int kLmWaves = 4;              // lm_head workgroup waves
 inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 4748 workgroups
 static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
@@ -69,8 +64,7 @@ struct DecodeScratch {
     float* act;           // [3072]
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
-    float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split;
-                          // every launch writes all splits (unused: max = -inf, sum = 0)
+    float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
     float* lm_value;      // [kLmGroups]
     int* lm_index;        // [kLmGroups]
     int* lm_bad;          // [kLmGroups]
