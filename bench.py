@@ -33,9 +33,33 @@ KERNEL_BYTES = {
 }
 
 
+# Contexts up to this many positions run attention and the O projection as
+# one kernel (the engine's fused path); the O kernel is then not launched.
+FUSED_ATTENTION_MAX = 512
+
+
 def attention_bytes(n):
-    """K and V rows of 8 heads x 128 FP16 for n positions, plus q/k/v in and out."""
+    """K and V rows of 8 heads x 128 FP16 for n positions, plus q/k/v in and
+    the attention output; on the fused path also the O weights and the
+    8 x 1024 FP32 partial projections written."""
+    if n <= FUSED_ATTENTION_MAX:
+        return 8 * n * 128 * 2 * 2 + 4096 * 4 + 1024 * 2048 * 2 + 8 * 1024 * 4
     return 8 * n * 128 * 2 * 2 + 4096 * 4 + 2048 * 4
+
+
+def measured_traffic(kernel, position):
+    """Calibrated HBM bytes per dispatch from the committed rocprofv3 counter
+    summary (lines 'traffic KERNEL POSITION BYTES'); None when that kernel was
+    not measured at this position."""
+    path = ROOT / 'profiles' / 'decode_hbm_traffic.txt'
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 4 and parts[0] == 'traffic' and parts[1] == kernel:
+            if kernel != 'attention' or int(parts[2]) == position:
+                return float(parts[3])
+    return None
 
 
 def log(*args):
@@ -74,9 +98,27 @@ def main():
     parser.add_argument('--cpu-seconds', type=float, default=12.0)
     parser.add_argument('--no-cpu-baseline', action='store_true')
     parser.add_argument('--no-ttft', action='store_true')
+    parser.add_argument('--pmc-kernel', choices=KERNELS,
+                        help='only run 29 launches of one decode kernel (hardware-counter passes)')
     parser.add_argument('--copy-calibration', type=int, metavar='MIB',
                         help='only run a plain device copy of MIB MiB, 5 times (HBM byte-counter calibration)')
     args = parser.parse_args()
+    if args.pmc_kernel:
+        # Light run for hardware-counter passes (each profiled dispatch is
+        # slow): one batched prefill up to the position the timed region of
+        # the default run ends at, then 28 launches of one decode kernel
+        # there (the same context the per-kernel timings below use).
+        from conftest import GOLDEN, PACK_CACHE, load_package
+        q = load_package()
+        prompts = json.loads((GOLDEN / 'prompts.json').read_text())
+        model = q.Model(q.ensure_random_pack(PACK_CACHE / 'seed0', seed=0), context=4096)
+        position = 85 + args.warmup + args.steps
+        model.prefill(prompts['long_3968'][:position])
+        which = KERNELS.index(args.pmc_kernel)
+        ms = model.time_kernel(which, 28)
+        model.close()
+        print(json.dumps({'pmc_kernel': args.pmc_kernel, 'position': position, 'launches': 29, 'avg_ms': ms}))
+        return 0
     if args.copy_calibration:
         from conftest import load_package
         q = load_package()
@@ -123,15 +165,15 @@ def main():
     context_end = model.position()
 
     # Per-kernel average durations with HIP events on the engine stream, at
-    # the context length reached by the timed region.
+    # the context length reached by the timed region (attention last: timing
+    # it resets the model).
     kernel_ms = {}
-    for which, name in enumerate(KERNELS):
-        model.reset()
-        model.prefill(prompt)
-        for _ in range(context_end - len(prompt)):
-            model.step(0)
-        kernel_ms[name] = model.time_kernel(which, 200)
-    per_token_ms = {k: v * (1 if k == 'lm_head' else 28) for k, v in kernel_ms.items()}
+    for which in (0, 2, 3, 4, 5, 1):
+        kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
+    kernel_ms = {name: kernel_ms[name] for name in KERNELS}
+    if context_end <= FUSED_ATTENTION_MAX:
+        kernel_ms['o'] = None  # inside the attention kernel at this context
+    per_token_ms = {k: v * (1 if k == 'lm_head' else 28) for k, v in kernel_ms.items() if v is not None}
     dominant = max(per_token_ms, key=per_token_ms.get)
     nbytes = attention_bytes(context_end) if dominant == 'attention' else KERNEL_BYTES[dominant]
     achieved = nbytes / (kernel_ms[dominant] * 1e-3) / 1e9
@@ -170,7 +212,8 @@ def main():
         'decode_hbm_fraction': (weight_bytes + kv_bytes) * decode_tps / 1e9 / HBM_PEAK_GBS,
         'kernel_ms': kernel_ms,
         'roofline': {'kernel': dominant, 'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
-                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': None,
+                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS,
+                     'traffic': measured_traffic(dominant, context_end),
                      'bytes_per_launch': nbytes},
         'cpu_baseline': baseline,
     }

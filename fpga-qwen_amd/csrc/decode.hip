@@ -75,17 +75,24 @@ __device__ __forceinline__ float wave_max(float v) {
 // stored at 64b + 8c + i, so chain c reads its 8 values contiguously.
 __device__ __forceinline__ int xperm(int j) { return (j & ~63) | ((j & 7) << 3) | ((j >> 3) & 7); }
 
-// RMSNorm of x[0..N) into permuted LDS (and optionally to `copy`).
+// Residual stream entry x + the 8 per-KV-head partial O projections of the
+// fused attention kernel, summed in a fixed tree order (every kernel that
+// reads the entry gets the same value).
+__device__ __forceinline__ float fold_parts(float x, const float (&p)[kKVHeads]) {
+    return x + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+}
+
+// RMSNorm (engine/core.cpp:207-215) of N values held PER = N / THREADS per
+// thread (element j = tid + k THREADS), with their norm weights, into
+// permuted LDS (and optionally to `copy`).
 template <int N, int THREADS>
-__device__ __forceinline__ void norm_to_lds(const float* __restrict__ x, const float* __restrict__ w, float* xs,
+__device__ __forceinline__ void norm_to_lds(const float (&v)[N / THREADS], const float (&w)[N / THREADS], float* xs,
                                             double* red, float* copy) {
     constexpr int PER = N / THREADS;
     const int tid = threadIdx.x;
-    float v[PER];
     double part = 0.0;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        v[k] = x[tid + k * THREADS];
         const float square = v[k] * v[k];
         part += static_cast<double>(square);
     }
@@ -100,24 +107,15 @@ __device__ __forceinline__ void norm_to_lds(const float* __restrict__ x, const f
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int j = tid + k * THREADS;
-        const float o = (v[k] * inv) * w[j];
+        const float o = (v[k] * inv) * w[k];
         xs[xperm(j)] = o;
         if (copy) copy[j] = o;
     }
 }
 
-template <int N, int THREADS>
-__device__ __forceinline__ void copy_to_lds(const float* __restrict__ x, float* xs) {
-#pragma unroll
-    for (int k = 0; k < N / THREADS; ++k) {
-        const int j = threadIdx.x + k * THREADS;
-        xs[xperm(j)] = x[j];
-    }
-}
-
-// Weights of one 8-row tile for this lane: NB 16-byte blocks. Issued before
-// the input vector is ready (weights do not depend on it), so the HBM round
-// trip overlaps the prologue.
+// Weights of one 8-row tile for this lane: NB 16-byte blocks. Issued right
+// after the (small) prologue inputs, so the HBM round trip overlaps the
+// prologue.
 template <int N>
 __device__ __forceinline__ void load_tile(const uint16_t* __restrict__ w_t, size_t tile, int lane, u32x4 (&wv)[N / 64]) {
     constexpr int NB = N / 64;
@@ -146,6 +144,7 @@ struct GemvArgs {
     const float* norm_w;      // RMSNorm weights (QKV, gate/up, lm_head)
     const uint16_t* embed;    // natural embedding, first layer only (QKV)
     const float* in2;         // O: normalized attention output when splits == 1
+    const float* parts;       // gate/up, down: pending [8][1024] O partials (fused attention), or null
     int token;                // first-layer QKV: embedding row
     int splits;               // O: attention splits to merge (1: copy in2)
     float* out;               // plain/QKV: y; gate/up: activation; lm_head: logits
@@ -158,63 +157,126 @@ struct GemvArgs {
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-template <int N, int WAVES, int MODE>
+// PARTS (gate/up, down): the residual stream still has the fused attention
+// kernel's 8 partial O projections pending in a.parts.
+template <int N, int WAVES, int MODE, bool PARTS = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
-    constexpr int THREADS = WAVES * 64;
+    constexpr int THREADS = WAVES * 64, PER = N / THREADS;
+    constexpr bool kNorm = MODE == kQKV || MODE == kGateUp || MODE == kLmHead;
     __shared__ float4 xs4[N / 4];
     __shared__ double red[WAVES];
     float* xs = reinterpret_cast<float*>(xs4);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t tile = size_t(blockIdx.x) * WAVES + wave;
-    u32x4 wv[N / 64];
-    load_tile<N>(a.w, tile, lane, wv);
+    const int c = lane & 7, r = lane >> 3;
+    const int row = int(tile) * 8 + r;
 
+    // Every load of the prologue and epilogue is issued before the weights:
+    // loads complete in issue order, so one issued after the weight tile
+    // would wait for all of it.
+    float v[PER], wn[PER];
     if constexpr (MODE == kQKV) {
-        const float* src = a.in;
-        if (a.embed) {
-            // First layer: x = fp32(E[token]) (engine/core.cpp:382-383), kept as the residual.
-            __shared__ float xe[N];
-            const uint16_t* row = a.embed + size_t(a.token) * N;
-            for (int j = tid; j < N; j += THREADS) {
-                const float v = h2f(row[j]);
-                xe[j] = v;
-                if (blockIdx.x == 0) a.x[j] = v;
-            }
-            __syncthreads();
-            src = xe;
+        if (a.embed) {  // first layer: x = fp32(E[token]) (engine/core.cpp:382-383)
+            const uint16_t* erow = a.embed + size_t(a.token) * N;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) v[k] = h2f(erow[tid + k * THREADS]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
         }
-        norm_to_lds<N, THREADS>(src, a.norm_w, xs, red, nullptr);
     } else if constexpr (MODE == kGateUp) {
-        norm_to_lds<N, THREADS>(a.in, a.norm_w, xs, red, nullptr);
-    } else if constexpr (MODE == kLmHead) {
-        norm_to_lds<N, THREADS>(a.in, a.norm_w, xs, red, blockIdx.x == 0 ? a.hidden : nullptr);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
     } else if constexpr (MODE == kO) {
-      if (a.splits == 1) {
-        copy_to_lds<N, THREADS>(a.in2, xs);
-      } else {
-        // Merge the attention splits of all 16 heads (flash-decoding merge,
-        // fixed split order): o = sum_s w_s o_s / sum_s w_s l_s with
-        // w_s = exp(m_s - max). The first 4 splits' outputs load together
-        // with all statistics; further splits follow in rounds of 4.
+        if (a.splits == 1) {
+#pragma unroll
+            for (int k = 0; k < PER; ++k) v[k] = a.in2[tid + k * THREADS];
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
+    }
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) wn[k] = a.norm_w[tid + k * THREADS];
+    }
+    // Pending O partials: of this thread's inputs (gate/up) or of this
+    // lane's output row (down).
+    float pin[PARTS && MODE == kGateUp ? PER : 1][kKVHeads], prow[kKVHeads];
+    if constexpr (PARTS && MODE == kGateUp) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k)
+#pragma unroll
+            for (int g = 0; g < kKVHeads; ++g) pin[k][g] = a.parts[g * kHidden + tid + k * THREADS];
+    }
+    float xres = 0.f;  // residual entry of this lane's row (O, down)
+    if constexpr (MODE == kO || MODE == kDown) xres = a.x[row];
+    if constexpr (PARTS && MODE == kDown) {
+#pragma unroll
+        for (int g = 0; g < kKVHeads; ++g) prow[g] = a.parts[g * kHidden + row];
+    }
+
+    // O with several attention splits: the first round of partial outputs
+    // and all statistics (flash-decoding merge, fixed split order).
+    constexpr int R = 4;
+    constexpr int kOPer = MODE == kO ? PER : 1;
+    float po[kOPer][R], st_m[2], st_l[2];
+    auto part = [&](int head, int sp) {
+        return a.in + (size_t(head >> 1) * kAttnSplits + sp) * kAttnPartial + (head & 1) * 132;
+    };
+    if constexpr (MODE == kO) {
         static_assert(THREADS == 128 && kQHeads * kAttnSplits == 2 * THREADS, "O prologue layout");
-        constexpr int R = 4;
         const int ns = a.splits;
+        if (ns > 1) {
+#pragma unroll
+            for (int k = 0; k < PER; ++k)  // output j = tid + 128 k belongs to head k
+#pragma unroll
+                for (int sp = 0; sp < R; ++sp) po[k][sp] = sp < ns ? part(k, sp)[tid] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {  // statistics: entry tid + 128 e = (head, split)
+                const int idx = tid + THREADS * e, sh = idx / kAttnSplits, ss = idx % kAttnSplits;
+                st_m[e] = ss < ns ? part(sh, ss)[128] : -INFINITY;
+                st_l[e] = ss < ns ? part(sh, ss)[129] : 0.f;
+            }
+        }
+    }
+
+    // The scheduling barriers keep the weight loads after the prologue loads
+    // and ahead of every instruction that waits for those.
+    u32x4 wv[N / 64];
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile<N>(a.w, tile, lane, wv);
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (PARTS && MODE == kGateUp) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = fold_parts(v[k], pin[k]);
+    }
+    if constexpr (PARTS && MODE == kDown) xres = fold_parts(xres, prow);
+    if constexpr (kNorm) {
+        if constexpr (MODE == kQKV) {
+            if (a.embed && blockIdx.x == 0) {  // kept as the residual stream
+#pragma unroll
+                for (int k = 0; k < PER; ++k) a.x[tid + k * THREADS] = v[k];
+            }
+        }
+        norm_to_lds<N, THREADS>(v, wn, xs, red, MODE == kLmHead && blockIdx.x == 0 ? a.hidden : nullptr);
+    } else if constexpr (MODE == kO) {
+      const int ns = a.splits;
+      if (ns == 1) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[k];
+      } else {
+        // o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max);
+        // splits beyond the first 4 follow in rounds of 4.
         __shared__ float cw[kQHeads][kAttnSplits];
         __shared__ float cl[kQHeads];
         __shared__ float stat[kQHeads][kAttnSplits][2];
-        auto part = [&](int head, int sp) {
-            return a.in + (size_t(head >> 1) * kAttnSplits + sp) * kAttnPartial + (head & 1) * 132;
-        };
-        float po[N / THREADS][R];
 #pragma unroll
-        for (int k = 0; k < N / THREADS; ++k)  // output j = tid + 128 k belongs to head k
-#pragma unroll
-            for (int sp = 0; sp < R; ++sp) po[k][sp] = sp < ns ? part(k, sp)[tid] : 0.f;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {  // statistics: entry tid + 128 e = (head, split)
+        for (int e = 0; e < 2; ++e) {
             const int idx = tid + THREADS * e, sh = idx / kAttnSplits, ss = idx % kAttnSplits;
-            stat[sh][ss][0] = ss < ns ? part(sh, ss)[128] : -INFINITY;
-            stat[sh][ss][1] = ss < ns ? part(sh, ss)[129] : 0.f;
+            stat[sh][ss][0] = st_m[e];
+            stat[sh][ss][1] = st_l[e];
         }
         __syncthreads();
         if (tid < kQHeads) {
@@ -229,9 +291,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
             cl[tid] = l;
         }
         __syncthreads();
-        float o[N / THREADS];
+        float o[PER];
 #pragma unroll
-        for (int k = 0; k < N / THREADS; ++k) {
+        for (int k = 0; k < PER; ++k) {
             o[k] = 0.f;
 #pragma unroll
             for (int sp = 0; sp < R; ++sp)
@@ -239,31 +301,30 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         }
         for (int s0 = R; s0 < ns; s0 += R) {
 #pragma unroll
-            for (int k = 0; k < N / THREADS; ++k)
+            for (int k = 0; k < PER; ++k)
 #pragma unroll
                 for (int sp = 0; sp < R; ++sp) po[k][sp] = s0 + sp < ns ? part(k, s0 + sp)[tid] : 0.f;
 #pragma unroll
-            for (int k = 0; k < N / THREADS; ++k)
+            for (int k = 0; k < PER; ++k)
 #pragma unroll
                 for (int sp = 0; sp < R; ++sp)
                     if (s0 + sp < ns) o[k] += cw[k][s0 + sp] * po[k][sp];
         }
 #pragma unroll
-        for (int k = 0; k < N / THREADS; ++k) xs[xperm(tid + k * THREADS)] = o[k] / cl[k];
+        for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = o[k] / cl[k];
       }
     } else {
-        copy_to_lds<N, THREADS>(a.in, xs);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[k];
     }
     __syncthreads();
 
     const float y = tile_dot<N>(wv, xs, lane);
-    const int c = lane & 7, r = lane >> 3;
-    const int row = int(tile) * 8 + r;
 
     if constexpr (MODE == kPlain || MODE == kQKV) {
         if (c == 0) a.out[row] = y;
     } else if constexpr (MODE == kO || MODE == kDown) {
-        if (c == 0) a.x[row] = a.x[row] + y;
+        if (c == 0) a.x[row] = xres + y;
     } else if constexpr (MODE == kGateUp) {
         // Tile rows 0-3 are gate rows 4T..4T+3, rows 4-7 the matching up rows.
         const float up = __shfl(y, (lane + 32) & 63);
@@ -351,16 +412,46 @@ struct AttnArgs {
     int pos;               // position being written
     float* partial;        // [8][kAttnSplits][kAttnPartial]
     float* attended;       // [2048], written instead when there is one split
+    const uint16_t* o_n;   // fused: natural O weights [1024 x 2048]
+    float* o_part;         // fused: [8][1024] partial O projections
     int context;
     float scale;           // 1.0f / sqrt(128.0f)
 };
 
-__device__ __forceinline__ int kperm(int j) { return ((j & 7) << 4) | (j >> 3); }
+// Two 16-byte pieces of a chain-permuted key row as the 8 chain steps each
+// of lane c: pieces c and c + 8 (see kperm).
+__device__ __forceinline__ void key_pieces(const uint16_t* row, int c, u32x4& lo, u32x4& hi) {
+    const u32x4* kp = reinterpret_cast<const u32x4*>(row);
+    lo = kp[c];
+    hi = kp[c + 8];
+}
+
+// The same 16 halves of the current key row, from LDS.
+__device__ __forceinline__ void key_pieces_lds(const uint16_t* kcur, int c, uint32_t (&kw)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int base = (i < 4 ? 8 * c : 64 + 8 * c) + 2 * (i & 3);
+        kw[i] = uint32_t(kcur[base]) | (uint32_t(kcur[base + 1]) << 16);
+    }
+}
+
+// Chain c of q . k for one key: steps s = 0..15 in order; q in kperm order.
+__device__ __forceinline__ float key_chain(const float* qperm, int c, const uint32_t (&kw)[8], float acc) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int base = (i < 4 ? 8 * c : 64 + 8 * c) + 2 * (i & 3);
+        acc = __builtin_fmaf(qperm[base], h2f(kw[i] & 0xffffu), acc);
+        acc = __builtin_fmaf(qperm[base + 1], h2f(kw[i] >> 16), acc);
+    }
+    return acc;
+}
 
 // RMSNorm over 128 values held one per thread by two consecutive waves
-// (engine/core.cpp:397-398), then rotate-half RoPE (216-218).
-__device__ __forceinline__ float head_norm_rope(float raw, const float* w, const float* cs, const float* sn,
-                                                double* red2, float* buf, int j) {
+// (engine/core.cpp:397-398), then rotate-half RoPE (216-218). w, cs, sn are
+// this thread's norm weight and the cosine / sine of its rotation pair
+// (index j % 64), loaded by the caller ahead of its other loads.
+__device__ __forceinline__ float head_norm_rope(float raw, float w, float cs, float sn, double* red2, float* buf,
+                                                int j) {
     const int lane = threadIdx.x & 63;
     const float square = raw * raw;
     const double part = wave_sum(static_cast<double>(square));
@@ -368,17 +459,17 @@ __device__ __forceinline__ float head_norm_rope(float raw, const float* w, const
     __syncthreads();
     const float sum = static_cast<float>(red2[0] + red2[1]);
     const float inv = 1.0f / __builtin_sqrtf(sum / 128.0f + 1e-6f);
-    const float normed = (raw * inv) * w[j];
+    const float normed = (raw * inv) * w;
     buf[j] = normed;
     __syncthreads();
     float out;
     if (j < 64) {
         const float x0 = buf[j], x1 = buf[j + 64];
-        out = x0 * cs[j] - x1 * sn[j];
+        out = x0 * cs - x1 * sn;
     } else {
         const int jj = j - 64;
         const float x0 = buf[jj], x1 = buf[j];
-        out = x1 * cs[jj] + x0 * sn[jj];
+        out = x1 * cs + x0 * sn;
     }
     return out;
 }
@@ -407,11 +498,7 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const int tl = p * 64 + (tid >> 3), t = t0 + tl;
-            if (tl < m && t != pos) {
-                const u32x4* kp = reinterpret_cast<const u32x4*>(a.keys + (head_base + t) * 128 + c * 16);
-                kreg[p][0] = kp[0];
-                kreg[p][1] = kp[1];
-            }
+            if (tl < m && t != pos) key_pieces(a.keys + (head_base + t) * 128, c, kreg[p][0], kreg[p][1]);
         }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -423,7 +510,13 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     // Raw q/k/v and the first tile's cached K/V rows are loaded first.
     const float raw = quarter < 2 ? a.qkv[(2 * g + quarter) * 128 + j] : a.qkv[2048 + g * 128 + j];
     const float raw_v = a.qkv[3072 + g * 128 + j];
+    // quarter is uniform per wave; selecting the pointer on a scalar keeps it
+    // out of vector registers (no per-lane load of the kernel argument).
+    const float nw = (__builtin_amdgcn_readfirstlane(quarter) < 2 ? a.q_norm : a.k_norm)[j];
+    const float rc = a.cosines[size_t(pos) * 64 + (j & 63)], rs = a.sines[size_t(pos) * 64 + (j & 63)];
+    __builtin_amdgcn_sched_barrier(0);
     load_tile(t_begin, min(kAttnTile, t_end - t_begin));
+    __builtin_amdgcn_sched_barrier(0);
 
     __shared__ float qp[2][128];
     __shared__ float buf[4][128];
@@ -437,9 +530,7 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     // QK-norm + RoPE: quarters 0-1 the two q heads, quarters 2-3 both the k
     // head (same barriers for every wave); quarter 2 keeps k, quarter 3 v.
     {
-        const float* cs = a.cosines + size_t(pos) * 64;
-        const float* sn = a.sines + size_t(pos) * 64;
-        const float r = head_norm_rope(raw, quarter < 2 ? a.q_norm : a.k_norm, cs, sn, red[quarter], buf[quarter], j);
+        const float r = head_norm_rope(raw, nw, rc, rs, red[quarter], buf[quarter], j);
         const bool owner = t_end == n;
         if (quarter < 2) {
             qp[quarter][kperm(j)] = r;
@@ -476,23 +567,13 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
             if (tl < m) {
                 uint32_t kw[8];
                 if (t == pos) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        kw[i] = uint32_t(kcur[c * 16 + 2 * i]) | (uint32_t(kcur[c * 16 + 2 * i + 1]) << 16);
+                    key_pieces_lds(kcur, c, kw);
                 } else {
                     kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
                     kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
                 }
-                const float* q0 = &qp[0][c * 16];
-                const float* q1 = &qp[1][c * 16];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float k0 = h2f(kw[i] & 0xffffu), k1 = h2f(kw[i] >> 16);
-                    acc0 = __builtin_fmaf(q0[2 * i], k0, acc0);
-                    acc1 = __builtin_fmaf(q1[2 * i], k0, acc1);
-                    acc0 = __builtin_fmaf(q0[2 * i + 1], k1, acc0);
-                    acc1 = __builtin_fmaf(q1[2 * i + 1], k1, acc1);
-                }
+                acc0 = key_chain(qp[0], c, kw, acc0);
+                acc1 = key_chain(qp[1], c, kw, acc1);
             }
             const float d0 = combine_chains(acc0), d1 = combine_chains(acc1);
             if (c == 0 && tl < m) {
@@ -576,6 +657,217 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     }
 }
 
+// Fused attention + O projection for n <= kFusedMaxPositions. Workgroup
+// (g, rb), g = blockIdx.x % 8 so the workgroups of one KV head share an XCD
+// (and its L2 copy of the head's K/V rows), rb = blockIdx.x / 8. Every
+// workgroup of head g computes that head's attention over all n positions
+// (scores in the reference dot's chain order, engine/core.cpp:612; softmax
+// and P.V as in 613-620), then its kAttnORows rows of O against the 256
+// attention outputs of query heads 2g, 2g+1: o_part[g][row] =
+// sum_i O[row][256g + i] * att[i].
+// 512 threads, PASSES = ceil(n / 64) passes of 64 positions (a template
+// parameter so that every load is unconditional and the compiler waits for
+// exactly the loads each phase needs). Wave w owns positions 64p + 8w + i,
+// i < 8: its lanes 8i..8i+7 score position i (lane c = chain c), then the
+// wave runs a softmax over its own positions (max m_w, sum l_w) and its P.V
+// with 4 positions x 16 channel groups per load; the 8 waves' partials are
+// merged with weights exp(m_w - max_w m_w), as in a split-softmax merge.
+template <int PASSES>
+__global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
+    const int g = blockIdx.x % kKVHeads, rb = blockIdx.x / kKVHeads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = a.pos, n = pos + 1;
+    const size_t head_base = size_t(g) * a.context;
+    const int quarter = tid >> 7, j = tid & 127, c = tid & 7, grp = tid >> 3;
+    const int vsub = lane >> 4, vcg = lane & 15;  // P.V: position within a group of 4, channel group
+
+    // Loads complete in issue order per wave, so they are issued in the
+    // order they are needed: this step's q/k/v with their norm weights and
+    // rotation, cached K rows, V rows, then this workgroup's O weights. Rows
+    // past n or at pos (taken from LDS) load row 0 instead and are not used.
+    const float raw = quarter < 2 ? a.qkv[(2 * g + quarter) * 128 + j] : a.qkv[2048 + g * 128 + j];
+    const float raw_v = a.qkv[3072 + g * 128 + j];
+    // quarter is uniform per wave; selecting the pointer on a scalar keeps it
+    // out of vector registers (no per-lane load of the kernel argument).
+    const float nw = (__builtin_amdgcn_readfirstlane(quarter) < 2 ? a.q_norm : a.k_norm)[j];
+    const float rc = a.cosines[size_t(pos) * 64 + (j & 63)], rs = a.sines[size_t(pos) * 64 + (j & 63)];
+    u32x4 kreg[PASSES][2], vreg[PASSES][2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int t = p * 64 + grp;
+        const int tl = t < n && t != pos ? t : 0;
+        key_pieces(a.keys + (head_base + tl) * 128, c, kreg[p][0], kreg[p][1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int t = p * 64 + 8 * wave + 4 * hf + vsub;
+            const int tl = t < n && t != pos ? t : 0;
+            vreg[p][hf] = reinterpret_cast<const u32x4*>(a.values + (head_base + tl) * 128)[vcg];
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    // O rows: kThreadsPerRow threads per row; load i of thread part q holds
+    // the 8 columns 8 (q + kThreadsPerRow i) .. +7 of the head's 256, so the
+    // lanes of one row read consecutive 16-byte pieces.
+    constexpr int kThreadsPerRow = 512 / kAttnORows, kLoads = 256 / 8 / kThreadsPerRow;
+    const int orow = rb * kAttnORows + tid / kThreadsPerRow, opart_id = tid % kThreadsPerRow;
+    u32x4 ow[kLoads];
+    {
+        const u32x4* op = reinterpret_cast<const u32x4*>(a.o_n + size_t(orow) * kQDim + 256 * g) + opart_id;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) ow[i] = __builtin_nontemporal_load(op + kThreadsPerRow * i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    __shared__ float qp[2][128];
+    __shared__ float buf[4][128];
+    __shared__ float prob[2][kFusedMaxPositions];
+    __shared__ float opart[8][4][2][128];
+    __shared__ __align__(16) float att[256];
+    __shared__ uint16_t kcur[128], vcur[128];
+    __shared__ double red[4][2];
+    __shared__ float wmax[8][2], wsum[8][2];
+
+    // QK-norm + RoPE (engine/core.cpp:395-402); workgroup rb == 0 writes the
+    // new K/V row (403-406). The others only read rows t != pos.
+    {
+        const float r = head_norm_rope(raw, nw, rc, rs, red[quarter], buf[quarter], j);
+        const bool owner = rb == 0;
+        if (quarter < 2) {
+            qp[quarter][kperm(j)] = r;
+        } else if (quarter == 2) {
+            const uint16_t bits = f2h(r);
+            kcur[kperm(j)] = bits;
+            if (owner) a.keys[(head_base + pos) * 128 + kperm(j)] = bits;
+        } else {
+            const uint16_t bits = f2h(raw_v);
+            vcur[j] = bits;
+            if (owner) a.values[(head_base + pos) * 128 + j] = bits;
+        }
+    }
+    __syncthreads();
+
+    // Scores of this wave's positions (every lane of a position's group of 8
+    // holds the combined value) and the wave's running maximum.
+    float s0[PASSES], s1[PASSES];
+    float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int t = p * 64 + grp;
+        uint32_t kw[8];
+        if (t == pos) {
+            key_pieces_lds(kcur, c, kw);
+        } else {
+            kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
+            kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+        }
+        const float d0 = combine_chains(key_chain(qp[0], c, kw, 0.f)) * a.scale;
+        const float d1 = combine_chains(key_chain(qp[1], c, kw, 0.f)) * a.scale;
+        s0[p] = t < n ? d0 : -INFINITY;
+        s1[p] = t < n ? d1 : -INFINITY;
+        m0 = fmaxf(m0, s0[p]);
+        m1 = fmaxf(m1, s1[p]);
+    }
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        m0 = fmaxf(m0, __shfl_xor(m0, off));
+        m1 = fmaxf(m1, __shfl_xor(m1, off));
+    }
+    // Probabilities relative to the wave maximum (a wave without positions
+    // keeps m = -inf and contributes nothing).
+    float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int t = p * 64 + grp;
+        const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
+        const float p1 = t < n ? expf(s1[p] - m1) : 0.f;
+        l0 += p0;
+        l1 += p1;
+        if (c == 0) {
+            prob[0][t] = p0;
+            prob[1][t] = p1;
+        }
+    }
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        l0 += __shfl_xor(l0, off);
+        l1 += __shfl_xor(l1, off);
+    }
+    // prob[][t] of this wave's positions is written and read by this wave only.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float acc[2][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[0][i] = acc[1][i] = 0.f;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int t = p * 64 + 8 * wave + 4 * hf + vsub;
+            if (t < n) {
+                const float p0 = prob[0][t], p1 = prob[1][t];
+                uint32_t vw[4];
+                if (t == pos) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        vw[i] = uint32_t(vcur[vcg * 8 + 2 * i]) | (uint32_t(vcur[vcg * 8 + 2 * i + 1]) << 16);
+                } else {
+                    vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
+                    acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
+                    acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
+                    acc[1][2 * i] = __builtin_fmaf(v0, p1, acc[1][2 * i]);
+                    acc[1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[1][2 * i + 1]);
+                }
+            }
+        }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) opart[wave][vsub][h][vcg * 8 + i] = acc[h][i];
+    if (lane == 0) {
+        wmax[wave][0] = m0;
+        wmax[wave][1] = m1;
+        wsum[wave][0] = l0;
+        wsum[wave][1] = l1;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        const int h = tid >> 7;
+        float mx = wmax[0][h];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w][h]);
+        float l = 0.f, o = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const float e = wmax[w][h] == -INFINITY ? 0.f : expf(wmax[w][h] - mx);
+            const float ow4 = (opart[w][0][h][j] + opart[w][1][h][j]) + (opart[w][2][h][j] + opart[w][3][h][j]);
+            l = __builtin_fmaf(e, wsum[w][h], l);
+            o = __builtin_fmaf(e, ow4, o);
+        }
+        att[tid] = o / l;
+    }
+    __syncthreads();
+
+    // This workgroup's rows of O against the 256 outputs of the KV head's
+    // query heads.
+    float y = 0.f;
+    const float4* at4 = reinterpret_cast<const float4*>(att) + 2 * opart_id;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
+#pragma unroll
+    for (int off = 1; off < kThreadsPerRow; off <<= 1) y += __shfl_xor(y, off);
+    if (opart_id == 0) a.o_part[g * kHidden + orow] = y;
+}
+
 __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* __restrict__ second,
                             uint16_t* __restrict__ dst, int rows, int cols) {
     const int nb = cols / 64;
@@ -599,11 +891,27 @@ __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* 
     *reinterpret_cast<u32x4*>(dst + idx * 8) = out;
 }
 
+// Waves (8-row tiles) per workgroup of each layer GEMV. The O projection's
+// split-merge prologue is laid out for exactly 2 waves.
 constexpr int kLayerWaves = 2;
+template <int MODE>
+constexpr int gemv_waves() {
+    if constexpr (MODE == kQKV) return 2;
+    else if constexpr (MODE == kGateUp) return 4;
+    else if constexpr (MODE == kDown) return 1;
+    else return kLayerWaves;
+}
 
 template <int N, int MODE>
 void launch_gemv(const GemvArgs& a, int rows, hipStream_t stream) {
-    gemv_kernel<N, kLayerWaves, MODE><<<rows / (8 * kLayerWaves), 64 * kLayerWaves, 0, stream>>>(a);
+    constexpr int W = gemv_waves<MODE>();
+    if constexpr (MODE == kGateUp || MODE == kDown) {
+        if (a.parts) {
+            gemv_kernel<N, W, MODE, true><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
+            return;
+        }
+    }
+    gemv_kernel<N, W, MODE><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
 }
 
 }  // namespace
@@ -660,12 +968,29 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             at.attended = s.attended;
             at.context = context;
             at.scale = 1.0f / std::sqrt(128.0f);
+            at.o_n = L.o_n;
+            at.o_part = s.o_part;
+            if (attn_fused(pos + 1)) {
+                switch ((pos + 64) / 64) {  // passes of 64 positions over n = pos + 1
+                    case 1: attn_o_kernel<1><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    case 2: attn_o_kernel<2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    case 3: attn_o_kernel<3><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    case 4: attn_o_kernel<4><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    case 5: attn_o_kernel<5><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    case 6: attn_o_kernel<6><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    case 7: attn_o_kernel<7><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    case 8: attn_o_kernel<8><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+                    default: throw std::runtime_error("fused attention: context beyond 512 positions");
+                }
+                break;
+            }
             int chunk, splits;
             attn_split(pos + 1, chunk, splits);
             attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(at);
             break;
         }
         case 2: {
+            if (attn_fused(pos + 1)) break;  // O is part of the attention kernel
             GemvArgs o{};
             o.w = L.o_t;
             o.in = s.attn_partial;
@@ -684,6 +1009,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             gu.w = L.gateup_t;
             gu.in = s.x;
             gu.norm_w = L.post_norm;
+            gu.parts = attn_fused(pos + 1) ? s.o_part : nullptr;
             gu.out = s.act;
             launch_gemv<kHidden, kGateUp>(gu, 2 * kFFN, stream);
             break;
@@ -692,6 +1018,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             GemvArgs d{};
             d.w = L.down_t;
             d.in = s.act;
+            d.parts = attn_fused(pos + 1) ? s.o_part : nullptr;
             d.x = s.x;
             launch_gemv<kFFN, kDown>(d, kHidden, stream);
             break;

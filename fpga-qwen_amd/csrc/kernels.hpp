@@ -11,9 +11,12 @@
 //   tiled[(((T * NB) + b) * 64 + t) * 8 + i],  NB = cols / 64.
 //
 // KV cache: [layer][kv head][position][128] FP16 (engine/core.cpp:350-352).
-// Key rows are stored chain-permuted, key'[c*16 + s] = key[8s + c], so the
-// 8 threads scoring one position each read 32 contiguous bytes in chain
-// order. Value rows are stored in natural channel order.
+// Key rows are stored chain-permuted: element j = 8s + c (chain c, step s of
+// the reference dot) sits at kperm(j) = 64 (s / 8) + 8c + s % 8, so 16-byte
+// piece c of the row holds steps 0..7 of chain c and piece c + 8 steps
+// 8..15. The 8 threads scoring one position (thread c = chain c) read pieces
+// c and c + 8: 128 contiguous bytes per load instruction and group. Value
+// rows are stored in natural channel order.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -22,6 +25,8 @@
 #include "qwen_common.hpp"
 
 namespace qwen_hip {
+
+__host__ __device__ constexpr int kperm(int j) { return (j & ~63) | ((j & 7) << 3) | ((j >> 3) & 7); }
 
 // Greedy selection result of the lm_head kernel.
 struct ArgmaxResult {
@@ -40,6 +45,18 @@ __host__ __device__ inline void attn_split(int n, int& chunk, int& splits) {
     splits = (n + kAttnTile - 1) / kAttnTile;
 }
 
+// Contexts of up to 512 positions take the fused attention + O-projection
+// kernel: one workgroup per (KV head, block of kAttnORows O rows) attends
+// over all positions of its head (K/V rows are re-read from L2 by the 32
+// workgroups of a head, which share an XCD), then multiplies its two query
+// heads' 256 attention outputs into its rows of O. The 8 per-head partial
+// sums of O.att land in o_part and are added to the residual stream by the
+// gate/up prologue and the down epilogue, in a fixed order.
+inline constexpr int kFusedMaxPositions = 512;
+inline constexpr int kAttnORows = 32;
+inline constexpr int kAttnOGroups = kKVHeads * (kHidden / kAttnORows);  // 256 workgroups
+__host__ __device__ inline bool attn_fused(int n) { return n <= kFusedMaxPositions; }
+
 inline constexpr int kLmWaves = 4;              // lm_head workgroup waves
 inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 4748 workgroups
 static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
@@ -47,6 +64,7 @@ static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabu
 struct LayerDevice {
     const uint16_t* qkv_t;     // tiled [4096 x 1024]: q rows, k rows, v rows
     const uint16_t* o_t;       // tiled [1024 x 2048]
+    const uint16_t* o_n;       // natural [1024 x 2048] (fused attention + O)
     const uint16_t* gateup_t;  // tiled [6144 x 1024]: tile T = gate rows 4T..4T+3, up rows 4T..4T+3
     const uint16_t* down_t;    // tiled [1024 x 3072]
     const float* in_norm;      // [1024]
@@ -65,6 +83,7 @@ struct DecodeScratch {
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
+    float* o_part;        // [8][1024]: per-KV-head partial O projections (fused path)
     float* lm_value;      // [kLmGroups]
     int* lm_index;        // [kLmGroups]
     int* lm_bad;          // [kLmGroups]
@@ -81,9 +100,10 @@ void launch_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t*
 // {1024, 2048, 3072}, rows a multiple of 8 * waves (waves = 2).
 void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, int cols, hipStream_t stream);
 
-// One decode layer (five kernels): norm+QKV, attention (+q/k norm, RoPE, KV
-// write) into per-split partials, O (+split combine prologue, +residual),
-// norm+gate/up (+SwiGLU), down (+residual).
+// One decode layer: norm+QKV, attention (+q/k norm, RoPE, KV write), O
+// (+split combine prologue, +residual), norm+gate/up (+SwiGLU), down
+// (+residual). With n = pos + 1 <= kFusedMaxPositions attention and O are one
+// kernel and the O kernel is not launched (four kernels per layer).
 // pos is the position being written (n = pos + 1 cached positions after
 // it); when `embed` is non-null (first layer) x is first loaded from
 // embed[token]. Step scalars travel as kernel arguments.
@@ -91,7 +111,8 @@ void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, int po
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
 
-// One kernel of a decode layer: 0 norm+QKV, 1 attention, 2 O, 3 norm+gate/up, 4 down.
+// One kernel of a decode layer: 0 norm+QKV, 1 attention (fused with O when
+// attn_fused(pos + 1)), 2 O (nothing when fused), 3 norm+gate/up, 4 down.
 void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);

@@ -14,6 +14,7 @@
 
 #include <cfloat>
 
+#include "kernels.hpp"
 #include "prefill.hpp"
 
 namespace qwen_hip {
@@ -134,8 +135,6 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
         out[size_t(b) * kHidden + j] = (v[k] * inv) * w[j];
     }
 }
-
-__device__ __forceinline__ int kperm(int j) { return ((j & 7) << 4) | (j >> 3); }
 
 // Per (row, head): QK-norm + RoPE for the 16 q heads (written back in the
 // key's chain-permuted order) and the 8 k heads (FP16 into the cache), V to

@@ -1,11 +1,14 @@
 """Long-context decode parity (the 3968-token workload, seed 3).
 
-Decode attention splits the cached positions into up to 16 chunks whose
-partial softmax statistics are merged in the O projection's prologue; these
-tests exercise many splits and the 512-position chunk boundaries against the
-oracle's sequential softmax (engine/core.cpp:606-624), teacher-forced like
-tools/check_native_logits.py, under the gate of
-tools/check_native_saved_oracle.py:36.
+Up to 512 cached positions decode attention runs fused with the O
+projection (one workgroup per KV head and block of O rows, partial
+projections folded into the residual stream by the next kernels); beyond
+that it splits the positions into up to 16 chunks of 256 whose partial
+softmax statistics are merged in the O projection's prologue. These tests
+cover the switch between the two paths, many splits and the 512-row prefill
+chunk boundaries against the oracle's sequential softmax
+(engine/core.cpp:606-624), teacher-forced like tools/check_native_logits.py,
+under the gate of tools/check_native_saved_oracle.py:36.
 """
 import json
 from pathlib import Path
@@ -34,6 +37,20 @@ def check_trajectory(gpu, oracle, prompt, steps):
             gpu.step(token)
             oracle.step(token)
     return results
+
+
+@pytest.mark.gpu
+def test_fused_to_split_attention_matches_oracle(qpkg, pack0, oracle_lib):
+    # Steps at n = 506 .. 517 cached positions: fused attention + O up to 512,
+    # split attention with the O-prologue merge from 513 on.
+    gpu = qpkg.Model(pack0, context=4096)
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    try:
+        results = check_trajectory(gpu, oracle, PROMPTS['long_3968'][:505], 13)
+        print('max_abs', max(r['max_abs'] for r in results), 'rms', max(r['rms'] for r in results))
+    finally:
+        gpu.close()
+        oracle.close()
 
 
 @pytest.mark.gpu
