@@ -62,6 +62,59 @@ def measured_traffic(kernel, position):
     return None
 
 
+def long_context_decode(model, token, steps=128):
+    """128 greedy steps after the 3968-token prompt (positions 3968..4095),
+    then per-kernel times at the full 4096 context: attention and O are
+    separate kernels here (position splits merged in the O prologue)."""
+    start = time.perf_counter()
+    for _ in range(steps):
+        model.step(token)
+        token = model.greedy()
+    elapsed = time.perf_counter() - start
+    n = model.position()
+    kernel_ms = {}
+    for which in (0, 2, 3, 4, 5, 1):
+        kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
+    gbs = {k: (attention_bytes(n) if k == 'attention' else KERNEL_BYTES[k]) / (v * 1e-3) / 1e9
+           for k, v in kernel_ms.items()}
+    log(f'long-context decode {steps / elapsed:.1f} tok/s')
+    return {'prompt_tokens': 3968, 'steps': steps, 'decode_tok_s': steps / elapsed, 'context_end': n,
+            'kernel_ms': kernel_ms, 'kernel_gbs': gbs}
+
+
+# Decode projection shapes (in, out) of the isolated GEMV microbenchmark.
+GEMV_SHAPES = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 151936)]
+
+
+def gemv_microbench(q, seed=1, rotate_bytes=640 << 20):
+    """Plain chain-ordered GEMV at each decode shape: W ~ N(0, 0.02) FP16,
+    x ~ N(0, 1) FP32 (seed 1), cycling through enough weight copies (at least
+    640 MB) that they stream from HBM instead of the Infinity Cache. Bytes
+    per call: 2 in out + 4 in + 4 out."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    out = {}
+    for n_in, n_out in GEMV_SHAPES:
+        w = (rng.standard_normal((n_out, n_in), dtype=np.float32) * 0.02).astype(np.float16)
+        x = rng.standard_normal(n_in, dtype=np.float32)
+        tiled = q.tile_matrix(w)
+        del w
+        size = n_out * n_in * 2
+        copies = max(2, -(-rotate_bytes // size))
+        copies_buf = q.DeviceBuffer(size * copies)
+        for i in range(copies):
+            q.copy_device(tiled, q.DeviceView(copies_buf, i * size), size)
+        q.synchronize()
+        xd, yd = q.DeviceBuffer.from_array(x), q.DeviceBuffer(n_out * 4)
+        iterations = max(copies, 20 if n_out > 100000 else 400)
+        ms = q.gemv_time(copies_buf, size, copies, xd, yd, n_out, n_in, iterations)
+        nbytes = 2 * n_in * n_out + 4 * n_in + 4 * n_out
+        out[f'{n_in}x{n_out}'] = {'us': ms * 1e3, 'gbs': nbytes / (ms * 1e-3) / 1e9, 'copies': copies}
+        log(f'gemv {n_in}->{n_out}: {ms * 1e3:.2f} us, {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s')
+        del tiled, copies_buf, xd, yd
+    return out
+
+
 def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
@@ -97,9 +150,12 @@ def main():
     parser.add_argument('--warmup', type=int, default=16)
     parser.add_argument('--cpu-seconds', type=float, default=12.0)
     parser.add_argument('--no-cpu-baseline', action='store_true')
-    parser.add_argument('--no-ttft', action='store_true')
+    parser.add_argument('--no-ttft', action='store_true', help='skip the 1024/3968 prefills and long-context decode')
+    parser.add_argument('--no-gemv', action='store_true', help='skip the isolated GEMV microbenchmark')
     parser.add_argument('--pmc-kernel', choices=KERNELS,
                         help='only run 29 launches of one decode kernel (hardware-counter passes)')
+    parser.add_argument('--pmc-prefill', action='store_true',
+                        help='only run one batched prefill of the 1024-token prompt (hardware-counter passes)')
     parser.add_argument('--copy-calibration', type=int, metavar='MIB',
                         help='only run a plain device copy of MIB MiB, 5 times (HBM byte-counter calibration)')
     args = parser.parse_args()
@@ -118,6 +174,17 @@ def main():
         ms = model.time_kernel(which, 28)
         model.close()
         print(json.dumps({'pmc_kernel': args.pmc_kernel, 'position': position, 'launches': 29, 'avg_ms': ms}))
+        return 0
+    if args.pmc_prefill:
+        from conftest import GOLDEN, PACK_CACHE, load_package
+        q = load_package()
+        prompts = json.loads((GOLDEN / 'prompts.json').read_text())
+        model = q.Model(q.ensure_random_pack(PACK_CACHE / 'seed0', seed=0), context=4096)
+        t0 = time.perf_counter()
+        model.prefill(prompts['prefill_1024'])
+        token = model.greedy()
+        model.close()
+        print(json.dumps({'pmc_prefill': 1024, 'seconds': time.perf_counter() - t0, 'token': token}))
         return 0
     if args.copy_calibration:
         from conftest import load_package
@@ -180,15 +247,18 @@ def main():
     log('kernel ms', kernel_ms)
 
     ttft = {'85': ttft_85}
+    long_context = None
     if not args.no_ttft:
         for key, name in (('1024', 'prefill_1024'), ('3968', 'long_3968')):
             model.reset()
             t0 = time.perf_counter()
             model.prefill(prompts[name])
-            model.greedy()
+            token = model.greedy()
             ttft[key] = time.perf_counter() - t0
             log(f'ttft {key}: {ttft[key]:.4f} s')
+        long_context = long_context_decode(model, token)
     model.close()
+    gemv = None if args.no_gemv else gemv_microbench(q)
 
     baseline = None if args.no_cpu_baseline else cpu_baseline(pack, prompt, args.cpu_seconds)
     weight_bytes = 1191968768
@@ -216,6 +286,8 @@ def main():
                      'traffic': measured_traffic(dominant, context_end),
                      'bytes_per_launch': nbytes},
         'cpu_baseline': baseline,
+        'long_context_decode': long_context,
+        'gemv_microbench': gemv,
     }
     print(json.dumps(result), flush=True)
     return 0

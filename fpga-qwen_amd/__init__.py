@@ -64,6 +64,8 @@ SIGNATURES = {
                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemm': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_op_gemv_time': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
+                                             ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_float_p]),
     'qwen_gpu_op_copy': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     'qwen_gpu_time_kernel': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_float_p]),
 }
@@ -243,6 +245,18 @@ class DeviceBuffer:
             pass
 
 
+class DeviceView:
+    """A byte range inside a DeviceBuffer (keeps the buffer alive; never frees)."""
+
+    def __init__(self, base, offset, nbytes=None):
+        offset = int(offset)
+        nbytes = base.nbytes - offset if nbytes is None else int(nbytes)
+        if offset < 0 or nbytes < 0 or offset + nbytes > base.nbytes:
+            raise ValueError('DeviceView outside its buffer')
+        self.base, self.nbytes = base, nbytes
+        self.ptr = ctypes.c_void_p(base.ptr.value + offset)
+
+
 def synchronize():
     _check(_LIB.qwen_gpu_device_synchronize())
 
@@ -267,6 +281,15 @@ def gemv(tiled, x, rows):
     _check(_LIB.qwen_gpu_op_gemv(tiled.ptr, xd.ptr, yd.ptr, rows, x.size, None))
     synchronize()
     return yd.to_array(np.float32, rows)
+
+
+def gemv_time(tiled, copy_stride, copies, x, y, rows, cols, iterations):
+    """Average ms of one GEMV launch cycling through `copies` tiled weight
+    copies `copy_stride` bytes apart in DeviceBuffer `tiled` (x, y DeviceBuffers)."""
+    ms = ctypes.c_float()
+    _check(_LIB.qwen_gpu_op_gemv_time(tiled.ptr, int(copy_stride), int(copies), x.ptr, y.ptr, int(rows), int(cols),
+                                      int(iterations), ctypes.byref(ms)))
+    return ms.value
 
 
 def copy_device(src, dst, nbytes):

@@ -220,6 +220,38 @@ int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, 
     });
 }
 
+int qwen_gpu_op_gemv_time(const uint16_t* tiled, size_t copy_stride, int copies, const float* x, float* y, int rows,
+                          int cols, int iterations, float* milliseconds) {
+    return guarded([&] {
+        need(tiled, "tiled");
+        need(x, "x");
+        need(y, "y");
+        need(milliseconds, "milliseconds");
+        if (copies < 1 || iterations < 1) throw std::runtime_error("gemv_time: copies and iterations must be positive");
+        if (copy_stride < size_t(rows) * size_t(cols) * 2 && copies > 1)
+            throw std::runtime_error("gemv_time: copy_stride smaller than one matrix");
+        auto launch = [&](int i) {
+            const auto* w = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(tiled) +
+                                                              size_t(i % copies) * copy_stride);
+            qwen_hip::launch_gemv_plain(w, x, y, rows, cols, nullptr);
+        };
+        for (int i = 0; i < copies; ++i) launch(i);  // warm: code, TLB
+        hipEvent_t start, stop;
+        hip_ok(hipEventCreate(&start));
+        hip_ok(hipEventCreate(&stop));
+        hip_ok(hipEventRecord(start, nullptr));
+        for (int i = 0; i < iterations; ++i) launch(i);
+        hip_ok(hipEventRecord(stop, nullptr));
+        hip_ok(hipEventSynchronize(stop));
+        float ms = 0.f;
+        hip_ok(hipEventElapsedTime(&ms, start, stop));
+        (void)hipEventDestroy(start);
+        (void)hipEventDestroy(stop);
+        hip_ok(hipGetLastError());
+        *milliseconds = ms / float(iterations);
+    });
+}
+
 int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream) {
     return guarded([&] {
         need(src, "src");

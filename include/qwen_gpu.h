@@ -108,6 +108,13 @@ int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, 
  * cores), W natural row-major FP16; N and K multiples of 64, M >= 1. */
 int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
                      void* stream);
+/* Isolated GEMV microbenchmark: average milliseconds of one op_gemv launch
+ * over `iterations` back-to-back launches on the default stream, timed with
+ * HIP events, cycling through `copies` chain-tiled weight copies laid
+ * `copy_stride` bytes apart (enough copies keep the weights streaming from
+ * HBM rather than the 256 MB Infinity Cache). No reference counterpart. */
+int qwen_gpu_op_gemv_time(const uint16_t* tiled, size_t copy_stride, int copies, const float* x, float* y, int rows,
+                          int cols, int iterations, float* milliseconds);
 /* Plain 16-byte-per-thread device copy (bytes a multiple of 16). No reference
  * counterpart: a kernel of known traffic for calibrating HBM byte counters. */
 int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream);
