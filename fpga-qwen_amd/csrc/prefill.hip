@@ -180,94 +180,188 @@ __global__ __launch_bounds__(128) void qk_rope_kv_kernel(float* __restrict__ QKV
     }
 }
 
-// Causal attention for a chunk (engine/core.cpp:407-605): workgroup = 16
-// query rows x the two query heads of KV head g; keys in tiles of 64 from
-// the FP16 cache, online softmax per query. q rows hold the chain-permuted
-// order of the cached keys, so plain index order gives the same dot.
-constexpr int kQRows = 16, kKeyTile = 64;
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ QKV,
-                                                           const uint16_t* __restrict__ keys,
-                                                           const uint16_t* __restrict__ values,
-                                                           float* __restrict__ attended, int rows, int pos0,
-                                                           int context, float scale) {
-    __shared__ float qs[2 * kQRows][kHeadDim];
-    __shared__ uint16_t ks[kKeyTile][kHeadDim + 8];
-    __shared__ uint16_t vs[kKeyTile][kHeadDim];
-    __shared__ float ps[2 * kQRows][kKeyTile];
-    const int b0 = blockIdx.x * kQRows, g = blockIdx.y, tid = threadIdx.x;
-    const int nrows = min(kQRows, rows - b0);
-    // query vector qi = 2 * row + head
-    for (int i = tid; i < 2 * kQRows * kHeadDim; i += 256) {
-        const int qi = i / kHeadDim, d = i % kHeadDim, r = qi >> 1;
-        qs[qi][d] = r < nrows ? QKV[size_t(b0 + r) * kQKVRows + (2 * g + (qi & 1)) * kHeadDim + d] : 0.f;
-    }
-    const int qi = tid >> 3, sub = tid & 7, row = qi >> 1;
-    const int qpos = pos0 + b0 + row;  // causal limit for this query
-    const int last = pos0 + b0 + nrows - 1;
-    const size_t head_base = size_t(g) * context;
-    float m_run = -INFINITY, l_run = 0.f;
-    float acc[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+// Causal attention for a prefill chunk on the matrix cores (engine/core.cpp:
+// 407-605, same math as the decode path): workgroup = 32 consecutive query
+// rows x one query head; its 4 waves take every 4th tile of 32 keys, each
+// with its own online softmax, and merge (max, sum, output) at the end.
+//   S^T = K Q^T  (A = 32 keys x 16 dims straight from the cache, B = Q^T as
+//                 FP16 hi + lo of the FP32 q, so products are exact)
+//   O^T += V^T P^T (A = V^T through a per-wave LDS transpose, B = P^T as
+//                 FP16 hi + lo of the FP32 probabilities)
+// With S^T in the 32x32 accumulator layout each lane holds 16 keys of one
+// query (lane % 32), so the softmax statistics stay in the lane: one
+// exchange with lane ^ 32 per tile. q and the cached keys share the
+// chain-permuted channel order, which leaves q . k unchanged.
+constexpr int kFaRows = 32, kFaKeys = 32, kFaWaves = 4, kVtPitch = 40, kFaccPitch = 132;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
-    for (int t0 = 0; t0 <= last; t0 += kKeyTile) {
-        __syncthreads();
-        for (int i = tid; i < kKeyTile * 16; i += 256) {  // 16-byte pieces
-            const int key = i >> 4, piece = i & 15, t = t0 + key;
-            u32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-            if (t <= last) {
-                kv = reinterpret_cast<const u32x4*>(keys + (head_base + t) * kHeadDim)[piece];
-                vv = reinterpret_cast<const u32x4*>(values + (head_base + t) * kHeadDim)[piece];
-            }
-            *reinterpret_cast<u32x4*>(&ks[key][piece * 8]) = kv;
-            *reinterpret_cast<u32x4*>(&vs[key][piece * 8]) = vv;
-        }
-        __syncthreads();
-        float s[8];
-        float tile_max = -INFINITY;
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __restrict__ QKV,
+                                                                const uint16_t* __restrict__ keys,
+                                                                const uint16_t* __restrict__ values,
+                                                                float* __restrict__ attended, int rows, int pos0,
+                                                                int context, float scale) {
+    // LDS: per-wave V^T tiles during the key loop, then the 4 waves' outputs.
+    __shared__ __align__(16) unsigned char lds[kFaWaves * kFaRows * kFaccPitch * 4];
+    __shared__ float fm[kFaWaves][kFaRows], fl[kFaWaves][kFaRows];
+    const int qb = blockIdx.x, head = blockIdx.y, g = head >> 1;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hf = lane >> 5;
+    const int b0 = qb * kFaRows, nrows = min(kFaRows, rows - b0);
+    const int last = pos0 + b0 + nrows - 1;  // last key any query of the block attends to
+    const int ntiles = last / kFaKeys + 1;
+    const size_t head_base = size_t(g) * context;
+    const int qpos = pos0 + b0 + col;        // causal limit of this lane's query
+    uint16_t(*vt)[kVtPitch] = reinterpret_cast<uint16_t(*)[kVtPitch]>(lds + wave * 128 * kVtPitch * 2);
+
+    // Q^T operand: query b0 + col (rows past the chunk repeat its last row
+    // and are never written), channels 16s + 8hf .. +7.
+    half8 qh[8], ql[8];
+    {
+        const float* qrow = QKV + size_t(b0 + min(col, nrows - 1)) * kQKVRows + head * kHeadDim + 8 * hf;
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const int key = sub + 8 * jj, t = t0 + key;
-            float dotv = 0.f;
-#pragma unroll 8
-            for (int d = 0; d < kHeadDim; ++d) dotv = __builtin_fmaf(qs[qi][d], h2f(ks[key][d]), dotv);
-            s[jj] = (t <= qpos && row < nrows) ? dotv * scale : -INFINITY;
-            tile_max = fmaxf(tile_max, s[jj]);
-        }
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) tile_max = fmaxf(tile_max, __shfl_xor(tile_max, off));
-        const float m_new = fmaxf(m_run, tile_max);
-        const float rescale = m_new == -INFINITY ? 1.f : (m_run == -INFINITY ? 0.f : expf(m_run - m_new));
-        float psum = 0.f;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const float p = s[jj] == -INFINITY ? 0.f : expf(s[jj] - m_new);
-            ps[qi][sub + 8 * jj] = p;
-            psum += p;
-        }
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) psum += __shfl_xor(psum, off);
-        l_run = l_run * rescale + psum;
-        m_run = m_new;
-        // ps[qi] is written and read by the same 8 lanes of one wave.
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] *= rescale;
-        for (int key = 0; key < kKeyTile; ++key) {
-            const float p = ps[qi][key];
-            const u32x4 v0 = *reinterpret_cast<const u32x4*>(&vs[key][sub * 16]);
-            const u32x4 v1 = *reinterpret_cast<const u32x4*>(&vs[key][sub * 16 + 8]);
-            const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        for (int s = 0; s < 8; ++s) {
+            const float4 x0 = reinterpret_cast<const float4*>(qrow + 16 * s)[0];
+            const float4 x1 = reinterpret_cast<const float4*>(qrow + 16 * s)[1];
+            const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                acc[2 * i] = __builtin_fmaf(h2f(uint16_t(w[i] & 0xffffu)), p, acc[2 * i]);
-                acc[2 * i + 1] = __builtin_fmaf(h2f(uint16_t(w[i] >> 16)), p, acc[2 * i + 1]);
+                const _Float16 h = static_cast<_Float16>(v[i]);
+                qh[s][i] = h;
+                ql[s][i] = static_cast<_Float16>(v[i] - static_cast<float>(h));
             }
         }
     }
-    if (row < nrows) {
-        float* out = attended + size_t(b0 + row) * kQDim + (2 * g + (qi & 1)) * kHeadDim + sub * 16;
+    float m = -INFINITY, l = 0.f;
+    floatx16 acc[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) out[i] = acc[i] / l_run;
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+
+    const int vp = lane & 15, vg = lane >> 4;  // V^T fill: key pair vp, channel group vg
+    for (int kt = wave; kt < ntiles; kt += kFaWaves) {
+        const int t0 = kt * kFaKeys;
+        // Keys past `last` load row `last` and are masked below.
+        const u32x4* krow = reinterpret_cast<const u32x4*>(keys + (head_base + min(t0 + col, last)) * kHeadDim);
+        half8 ka[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) ka[s] = __builtin_bit_cast(half8, krow[2 * s + hf]);
+        const u32x4* va_row = reinterpret_cast<const u32x4*>(values + (head_base + min(t0 + 2 * vp, last)) * kHeadDim);
+        const u32x4* vb_row =
+            reinterpret_cast<const u32x4*>(values + (head_base + min(t0 + 2 * vp + 1, last)) * kHeadDim);
+        u32x4 va[4], vb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            va[r] = va_row[vg + 4 * r];
+            vb[r] = vb_row[vg + 4 * r];
+        }
+        floatx16 st;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[s], qh[s], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[s], ql[s], st, 0, 0, 0);
+        }
+        // V^T: channel 32r + 8vg + e, keys 2vp (low half) and 2vp + 1 (high half).
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t aw[4] = {va[r].x, va[r].y, va[r].z, va[r].w};
+            const uint32_t bw[4] = {vb[r].x, vb[r].y, vb[r].z, vb[r].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ch = 32 * r + 8 * vg + 2 * i;
+                *reinterpret_cast<uint32_t*>(&vt[ch][2 * vp]) = (aw[i] & 0xffffu) | (bw[i] << 16);
+                *reinterpret_cast<uint32_t*>(&vt[ch + 1][2 * vp]) = (aw[i] >> 16) | (bw[i] & 0xffff0000u);
+            }
+        }
+        // Online softmax; register r holds key t0 + 8(r/4) + 4hf + r%4.
+        float sv[16];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            sv[r] = t <= qpos ? st[r] * scale : -INFINITY;
+            tmax = fmaxf(tmax, sv[r]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mnew = fmaxf(m, tmax);
+        const float factor = m == -INFINITY ? 0.f : expf(m - mnew);
+        half8 ph[2], pl[2];
+        float psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mnew);
+            psum += p;
+            const _Float16 h = static_cast<_Float16>(p);
+            ph[r >> 3][r & 7] = h;
+            pl[r >> 3][r & 7] = static_cast<_Float16>(p - static_cast<float>(h));
+        }
+        psum += __shfl_xor(psum, 32);
+        l = l * factor + psum;
+        m = mnew;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[dt][r] *= factor;
+        // vt is written and read by this wave only.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const uint16_t* vrow = vt[32 * dt + col];
+                const half4 lo4 = *reinterpret_cast<const half4*>(vrow + 16 * j + 4 * hf);
+                const half4 hi4 = *reinterpret_cast<const half4*>(vrow + 16 * j + 8 + 4 * hf);
+                const half8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph[j], acc[dt], 0, 0, 0);
+                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[j], acc[dt], 0, 0, 0);
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // Merge the 4 waves: O^T register r of tile dt is channel 32dt + 8(r/4) + 4hf + r%4 of query col.
+    __syncthreads();  // every wave is done with its V^T tile
+    float(*facc)[kFaccPitch] = reinterpret_cast<float(*)[kFaccPitch]>(lds + wave * kFaRows * kFaccPitch * 4);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) facc[col][32 * dt + 8 * (r >> 2) + 4 * hf + (r & 3)] = acc[dt][r];
+    if (hf == 0) {
+        fm[wave][col] = m;
+        fl[wave][col] = l;
+    }
+    __syncthreads();
+    const int q = tid >> 3, c0 = (tid & 7) * 16;
+    if (q < nrows) {
+        float mx = fm[0][q];
+#pragma unroll
+        for (int w = 1; w < kFaWaves; ++w) mx = fmaxf(mx, fm[w][q]);
+        float e[kFaWaves], lsum = 0.f;
+#pragma unroll
+        for (int w = 0; w < kFaWaves; ++w) {
+            e[w] = fm[w][q] == -INFINITY ? 0.f : expf(fm[w][q] - mx);
+            lsum = __builtin_fmaf(e[w], fl[w][q], lsum);
+        }
+        float* out = attended + size_t(b0 + q) * kQDim + head * kHeadDim + c0;
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+            float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < kFaWaves; ++w) {
+                const float4 v = *reinterpret_cast<const float4*>(
+                    reinterpret_cast<const float*>(lds + w * kFaRows * kFaccPitch * 4) + q * kFaccPitch + c0 + 4 * k4);
+                o[0] = __builtin_fmaf(e[w], v.x, o[0]);
+                o[1] = __builtin_fmaf(e[w], v.y, o[1]);
+                o[2] = __builtin_fmaf(e[w], v.z, o[2]);
+                o[3] = __builtin_fmaf(e[w], v.w, o[3]);
+            }
+            reinterpret_cast<float4*>(out)[k4] = make_float4(o[0] / lsum, o[1] / lsum, o[2] / lsum, o[3] / lsum);
+        }
     }
 }
 
@@ -312,7 +406,7 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
         gemm<0>(s.h, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream);
         qk_rope_kv_kernel<<<dim3(rows, kQHeads + kKVHeads), 128, 0, stream>>>(s.qkv, L.q_norm, L.k_norm, cosines, sines,
                                                                              L.keys, L.values, pos0, context);
-        attn_prefill_kernel<<<dim3((rows + kQRows - 1) / kQRows, kKVHeads), 256, 0, stream>>>(
+        attn_prefill_mfma_kernel<<<dim3((rows + kFaRows - 1) / kFaRows, kQHeads), 256, 0, stream>>>(
             s.qkv, L.keys, L.values, s.attended, rows, pos0, context, scale);
         gemm<1>(s.attended, L.o_n, s.x, rows, kHidden, kQDim, stream);
         rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h);
