@@ -82,6 +82,56 @@ def long_context_decode(model, token, steps=128):
             'kernel_ms': kernel_ms, 'kernel_gbs': gbs}
 
 
+def prefix_reuse_batch(model, prompts, steps=128):
+    """Prefix-reuse workload: the canonical 512-token prefix is prefilled once;
+    8 sequences on the same weights reuse its K/V (device copy of the rewound
+    prefix), prefill their own 1536-token suffix (positions 512..2047) and
+    decode 128 greedy tokens each as one batch of 8 (skinny GEMMs on the
+    matrix cores). Also times one sequence stepping alone at that context."""
+    prefix, suffixes = prompts['prefix_512'], prompts['suffix_1536']
+    base = model.share()
+    seqs = [model.share() for _ in suffixes]
+    q = sys.modules['fpga_qwen_amd']
+    try:
+        t0 = time.perf_counter()
+        base.prefill(prefix)
+        prefix_s = time.perf_counter() - t0
+        suffix_s = []
+        for m, suffix in zip(seqs, suffixes):
+            t0 = time.perf_counter()
+            m.copy_prefix(base, len(prefix))
+            m.prefill(suffix)
+            suffix_s.append(time.perf_counter() - t0)
+        tokens = [m.greedy() for m in seqs]
+        q.step_batch(seqs, tokens)  # warmup step
+        tokens = [m.greedy() for m in seqs]
+        start = time.perf_counter()
+        for _ in range(steps - 1):
+            q.step_batch(seqs, tokens)
+            tokens = [m.greedy() for m in seqs]
+        elapsed = time.perf_counter() - start
+        aggregate = len(seqs) * (steps - 1) / elapsed
+        # The same context stepped one sequence at a time (batch-1 path).
+        single = seqs[0]
+        single.truncate(single.position() - 16)
+        token = 0
+        t0 = time.perf_counter()
+        for _ in range(16):
+            single.step(token)
+            token = single.greedy()
+        single_tps = 16 / (time.perf_counter() - t0)
+        context_end = seqs[1].position()
+    finally:
+        for m in seqs + [base]:
+            m.close()
+    log(f'prefix reuse: {aggregate:.0f} tok/s aggregate over {len(seqs)} sequences')
+    return {'sequences': len(suffixes), 'prefix_tokens': len(prefix), 'suffix_tokens': len(suffixes[0]),
+            'steps': steps, 'timed_steps': steps - 1, 'aggregate_tok_s': aggregate,
+            'step_ms': elapsed / (steps - 1) * 1e3, 'context_end': context_end,
+            'prefix_prefill_ms': prefix_s * 1e3, 'suffix_prefill_ms': sorted(suffix_s)[len(suffix_s) // 2] * 1e3,
+            'single_sequence_tok_s': single_tps}
+
+
 # Decode projection shapes (in, out) of the isolated GEMV microbenchmark.
 GEMV_SHAPES = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 151936)]
 
@@ -152,10 +202,12 @@ def main():
     parser.add_argument('--no-cpu-baseline', action='store_true')
     parser.add_argument('--no-ttft', action='store_true', help='skip the 1024/3968 prefills and long-context decode')
     parser.add_argument('--no-gemv', action='store_true', help='skip the isolated GEMV microbenchmark')
+    parser.add_argument('--no-batch', action='store_true', help='skip the 8-sequence prefix-reuse workload')
     parser.add_argument('--pmc-kernel', choices=KERNELS,
                         help='only run 29 launches of one decode kernel (hardware-counter passes)')
-    parser.add_argument('--pmc-prefill', action='store_true',
-                        help='only run one batched prefill of the 1024-token prompt (hardware-counter passes)')
+    parser.add_argument('--pmc-prefill', type=int, nargs='?', const=1024, choices=(1024, 3968),
+                        help='only run one batched prefill of the 1024- (default) or 3968-token prompt '
+                             '(hardware-counter passes)')
     parser.add_argument('--copy-calibration', type=int, metavar='MIB',
                         help='only run a plain device copy of MIB MiB, 5 times (HBM byte-counter calibration)')
     args = parser.parse_args()
@@ -180,11 +232,12 @@ def main():
         q = load_package()
         prompts = json.loads((GOLDEN / 'prompts.json').read_text())
         model = q.Model(q.ensure_random_pack(PACK_CACHE / 'seed0', seed=0), context=4096)
+        name = 'prefill_1024' if args.pmc_prefill == 1024 else 'long_3968'
         t0 = time.perf_counter()
-        model.prefill(prompts['prefill_1024'])
+        model.prefill(prompts[name])
         token = model.greedy()
         model.close()
-        print(json.dumps({'pmc_prefill': 1024, 'seconds': time.perf_counter() - t0, 'token': token}))
+        print(json.dumps({'pmc_prefill': args.pmc_prefill, 'seconds': time.perf_counter() - t0, 'token': token}))
         return 0
     if args.copy_calibration:
         from conftest import load_package
@@ -257,6 +310,7 @@ def main():
             ttft[key] = time.perf_counter() - t0
             log(f'ttft {key}: {ttft[key]:.4f} s')
         long_context = long_context_decode(model, token)
+    batch = None if args.no_batch else prefix_reuse_batch(model, prompts)
     model.close()
     gemv = None if args.no_gemv else gemv_microbench(q)
 
@@ -287,6 +341,7 @@ def main():
                      'bytes_per_launch': nbytes},
         'cpu_baseline': baseline,
         'long_context_decode': long_context,
+        'prefix_reuse_batch': batch,
         'gemv_microbench': gemv,
     }
     print(json.dumps(result), flush=True)

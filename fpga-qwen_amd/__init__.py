@@ -64,6 +64,12 @@ SIGNATURES = {
                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemm': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_create_sharing': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Options),
+                                               ctypes.POINTER(ctypes.c_void_p)]),
+    'qwen_gpu_copy_prefix': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
+    'qwen_gpu_step_batch': (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _c_int_p, ctypes.c_int]),
+    'qwen_gpu_op_bgemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemv_time': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
                                              ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_float_p]),
     'qwen_gpu_op_copy': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
@@ -107,6 +113,26 @@ class Model:
         options = Options(decode_threads, prefill_threads, context)
         _check(_LIB.qwen_gpu_create(str(weights_file).encode(), ctypes.byref(options), ctypes.byref(handle)))
         self._handle = handle
+
+    @classmethod
+    def _from_handle(cls, handle):
+        model = cls.__new__(cls)
+        model._handle = handle
+        return model
+
+    def share(self, decode_threads=None, prefill_threads=None, context=None):
+        """A further model on this model's uploaded weights, with its own K/V
+        cache and state (options default to this model's)."""
+        own = self.options()
+        options = Options(decode_threads or own['decode_threads'], prefill_threads or own['prefill_threads'],
+                          context or own['context'])
+        handle = ctypes.c_void_p()
+        _check(_LIB.qwen_gpu_create_sharing(self._handle, ctypes.byref(options), ctypes.byref(handle)))
+        return Model._from_handle(handle)
+
+    def copy_prefix(self, src, positions):
+        """Become `src` truncated to `positions` (K/V rows copied on the device)."""
+        _check(_LIB.qwen_gpu_copy_prefix(self._handle, src._handle, int(positions)))
 
     def close(self):
         if self._handle:
@@ -186,6 +212,16 @@ class Model:
         ms = ctypes.c_float()
         _check(_LIB.qwen_gpu_time_kernel(self._handle, int(which), int(iterations), ctypes.byref(ms)))
         return ms.value
+
+
+def step_batch(models, tokens):
+    """One decode step for each model (1..8, sharing weights): models[i]
+    consumes tokens[i], all projections batched on the matrix cores."""
+    handles = (ctypes.c_void_p * len(models))(*[m._handle for m in models])
+    toks = np.ascontiguousarray(tokens, dtype=np.int32)
+    if toks.size != len(models):
+        raise ValueError('one token per model')
+    _check(_LIB.qwen_gpu_step_batch(handles, toks.ctypes.data_as(_c_int_p), len(models)))
 
 
 def write_random_pack(path, seed=0, stddev=0.02, threads=None):
@@ -295,6 +331,19 @@ def gemv_time(tiled, copy_stride, copies, x, y, rows, cols, iterations):
 def copy_device(src, dst, nbytes):
     """Plain device copy between DeviceBuffers (counter calibration)."""
     _check(_LIB.qwen_gpu_op_copy(src.ptr, dst.ptr, int(nbytes), None))
+
+
+def bgemv(w, x):
+    """Y = X W^T for 1..8 rows on the matrix cores (batched decode projection):
+    W FP16 natural [rows, cols], X FP32 [batch, cols]. Returns Y [batch, rows]."""
+    w = np.ascontiguousarray(w, np.float16)
+    x = np.ascontiguousarray(x, np.float32)
+    batch, cols = x.shape
+    rows = w.shape[0]
+    wd, xd, yd = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x), DeviceBuffer(batch * rows * 4)
+    _check(_LIB.qwen_gpu_op_bgemv(wd.ptr, xd.ptr, yd.ptr, batch, rows, cols, None))
+    synchronize()
+    return yd.to_array(np.float32, batch * rows).reshape(batch, rows)
 
 
 def gemm(a, w, c=None):

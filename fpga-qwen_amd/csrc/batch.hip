@@ -1,0 +1,386 @@
+// Batched decode: one step for up to 8 independent sequences that share the
+// weights (the prefix-reuse serving workload). The reference is
+// single-stream; per sequence this computes what qwen_cpu::Model::step does
+// (engine/core.cpp:353-646, 707-714), but every projection reads each weight
+// matrix once for all rows: a skinny GEMM on the matrix cores instead of one
+// GEMV per sequence.
+//
+// Skinny GEMM (bgemv_kernel): Y[b][o] = sum_k X[b][k] W[o][k], W natural
+// row-major FP16, b < 8. Workgroup = 16 output rows (one 16x16x32 MFMA tile,
+// A = W rows, B = X^T with the 8 sequences in columns 0..7) and 4 waves, each
+// a quarter of K; the quarters are summed in LDS in a fixed order. X enters
+// the matrix cores as FP16 hi + lo (hi = fp16(x), lo = fp16(x - hi)), so the
+// products are exact and the sums FP32, as in the prefill GEMMs. Each lane
+// streams 64 contiguous bytes of its weight row per 128-wide K block (the
+// summation order inside a block is a fixed permutation of k, applied to A
+// and B alike). RMSNorm prologues (FP32 squares, FP64 sums per row) and the
+// residual / SwiGLU / argmax epilogues are fused as in the batch-1 kernels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+
+#include "batch.hpp"
+
+namespace qwen_hip {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+
+__device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+enum BatchMode { kBPlain, kBQKV, kBO, kBGateUp, kBDown, kBLmHead };
+
+struct BatchGemvArgs {
+    const uint16_t* w;                 // natural [rows x K]; gate/up: 3072 gate rows then 3072 up rows
+    const float* norm_w;               // RMSNorm weights (QKV, gate/up, lm_head)
+    const float* in[kMaxBatch];        // input rows: x (norm modes), attention output (O), activation (down)
+    const uint16_t* embed[kMaxBatch];  // QKV of the first layer: embedding rows instead of x
+    float* out[kMaxBatch];             // output rows (plain, QKV, gate/up: activation, lm_head: logits)
+    float* x[kMaxBatch];               // residual rows (O and down add; first layer stores E[token])
+    float* hidden[kMaxBatch];          // lm_head: final normalized rows
+    float* lm_value;                   // lm_head argmax partials [groups][kMaxBatch]
+    int* lm_index;
+    int* lm_bad;
+    int batch;
+};
+
+template <int K, int MODE>
+__global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
+    constexpr bool kNorm = MODE == kBQKV || MODE == kBGateUp || MODE == kBLmHead;
+    constexpr int kTiles = MODE == kBGateUp ? 2 : 1;  // gate/up: a gate tile and the matching up tile
+    constexpr int KW = K / kWaves, kBlocks = KW / 128, PER = K / 256;
+    static_assert(KW % 128 == 0, "each wave takes whole 128-wide K blocks");
+    __shared__ __align__(16) _Float16 xh[kMaxBatch][K + 8];
+    __shared__ __align__(16) _Float16 xl[kMaxBatch][K + 8];
+    __shared__ double red[kWaves][kMaxBatch];
+    __shared__ float inv_s[kMaxBatch];
+    __shared__ float part[kWaves][kTiles][64][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, quad = lane >> 4;
+    const int B = a.batch, o0 = blockIdx.x * kBatchRows;
+    // Epilogue element of this thread: row 4 (l / 16) + r, column l % 16 of
+    // the 16x16 accumulator (r = wave, l = lane).
+    const int eb = lane & 15, eo = o0 + 4 * (lane >> 4) + wave;
+
+    // Loads complete in issue order per wave: inputs first (rows past the
+    // batch repeat row B - 1 and are never used), then residual entries,
+    // then the weights.
+    float v[kMaxBatch][PER], wn[PER];
+#pragma unroll
+    for (int b = 0; b < kMaxBatch; ++b) {
+        const int bb = min(b, B - 1);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int j = tid + 256 * k;
+            if constexpr (MODE == kBQKV)
+                v[b][k] = a.embed[bb] ? h2f(a.embed[bb][j]) : a.in[bb][j];
+            else
+                v[b][k] = a.in[bb][j];
+        }
+    }
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) wn[k] = a.norm_w[tid + 256 * k];
+    }
+    float xres = 0.f;
+    if constexpr (MODE == kBO || MODE == kBDown) xres = a.x[min(eb, B - 1)][eo];
+    u32x4 wa[kTiles][kBlocks][4];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int row = o0 + col + (t ? kFFN : 0);
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(row) * K + wave * KW) + 4 * quad;
+#pragma unroll
+        for (int blk = 0; blk < kBlocks; ++blk)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) wa[t][blk][s] = __builtin_nontemporal_load(wp + 16 * blk + s);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (kNorm) {
+        // RMSNorm per row (engine/core.cpp:207-215).
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) {
+            double sq = 0.0;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const float square = v[b][k] * v[b][k];
+                sq += static_cast<double>(square);
+            }
+            sq = wave_sum(sq);
+            if (lane == 0) red[wave][b] = sq;
+        }
+        __syncthreads();
+        if (tid < kMaxBatch) {
+            const double total = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+            inv_s[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(K) + 1e-6f);
+        }
+        __syncthreads();
+        if constexpr (MODE == kBQKV) {
+            if (blockIdx.x == 0) {  // first layer: keep fp32(E[token]) as the residual stream
+#pragma unroll
+                for (int b = 0; b < kMaxBatch; ++b)
+                    if (b < B && a.embed[b]) {
+#pragma unroll
+                        for (int k = 0; k < PER; ++k) a.x[b][tid + 256 * k] = v[b][k];
+                    }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b) {
+            const float inv = inv_s[b];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) v[b][k] = (v[b][k] * inv) * wn[k];
+        }
+        if constexpr (MODE == kBLmHead) {
+            if (blockIdx.x == 0) {
+#pragma unroll
+                for (int b = 0; b < kMaxBatch; ++b)
+                    if (b < B) {
+#pragma unroll
+                        for (int k = 0; k < PER; ++k) a.hidden[b][tid + 256 * k] = v[b][k];
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kMaxBatch; ++b)
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const _Float16 h = static_cast<_Float16>(v[b][k]);
+            xh[b][tid + 256 * k] = h;
+            xl[b][tid + 256 * k] = static_cast<_Float16>(v[b][k] - static_cast<float>(h));
+        }
+    __syncthreads();
+
+    floatx4 acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int blk = 0; blk < kBlocks; ++blk)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            // k slot (quad, i) of step s holds k = 128 blk + 32 quad + 8 s + i of this wave's range.
+            const int k = wave * KW + 128 * blk + 32 * quad + 8 * s;
+            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
+            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t) {
+                const half8 w8 = __builtin_bit_cast(half8, wa[t][blk][s]);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[wave][t][lane][r] = acc[t][r];
+    __syncthreads();
+
+    // Epilogue: thread (wave r, lane l) owns accumulator register r of lane l:
+    // output row eo = o0 + 4 (l / 16) + r, sequence eb = l % 16.
+    float y[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t)
+        y[t] = (part[0][t][lane][wave] + part[1][t][lane][wave]) + (part[2][t][lane][wave] + part[3][t][lane][wave]);
+    const bool live = eb < B;
+    if constexpr (MODE == kBPlain || MODE == kBQKV) {
+        if (live) a.out[eb][eo] = y[0];
+    } else if constexpr (MODE == kBO || MODE == kBDown) {
+        if (live) a.x[eb][eo] = xres + y[0];
+    } else if constexpr (MODE == kBGateUp) {
+        if (live) {  // SwiGLU (engine/core.cpp:636-639)
+            const float gate = y[0], up = y[1];
+            const float half_gate = gate * 0.5f;
+            const float th = tanhf(half_gate);
+            a.out[eb][eo] = gate * (0.5f + 0.5f * th) * up;
+        }
+    } else if constexpr (MODE == kBLmHead) {
+        if (live) a.out[eb][eo] = y[0];
+        // Per-sequence argmax over this workgroup's 16 rows: lowest id among
+        // maxima, nonfinite values flagged (engine/main.cpp:51-59).
+        float bv = live ? y[0] : -INFINITY;
+        int bi = live ? eo : INT_MAX, bad = live && !__builtin_isfinite(y[0]);
+#pragma unroll
+        for (int off = 16; off < 64; off <<= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            bad |= __shfl_xor(bad, off);
+            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        __shared__ float mv[kWaves][16];
+        __shared__ int mi[kWaves][16], mb[kWaves][16];
+        if (lane < 16) { mv[wave][lane] = bv; mi[wave][lane] = bi; mb[wave][lane] = bad; }
+        __syncthreads();
+        if (tid < B) {
+            float v0 = mv[0][tid];
+            int i0 = mi[0][tid], b0 = mb[0][tid];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) {
+                b0 |= mb[w][tid];
+                if (better(mv[w][tid], mi[w][tid], v0, i0)) { v0 = mv[w][tid]; i0 = mi[w][tid]; }
+            }
+            const size_t slot = size_t(blockIdx.x) * kMaxBatch + tid;
+            a.lm_value[slot] = v0;
+            a.lm_index[slot] = i0;
+            a.lm_bad[slot] = b0;
+        }
+    }
+}
+
+// Second pass of the per-sequence greedy selection.
+struct BatchResults {
+    ArgmaxResult* device[kMaxBatch];
+    ArgmaxResult* host[kMaxBatch];
+};
+
+__global__ __launch_bounds__(1024) void batch_argmax_kernel(const float* __restrict__ value,
+                                                            const int* __restrict__ index,
+                                                            const int* __restrict__ bad_in, BatchResults out) {
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    int bi = INT_MAX, bad = 0;
+    for (int k = tid; k < kBatchLmGroups; k += 1024) {
+        const size_t slot = size_t(k) * kMaxBatch + b;
+        bad |= bad_in[slot];
+        if (better(value[slot], index[slot], bv, bi)) { bv = value[slot]; bi = index[slot]; }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        bad |= __shfl_xor(bad, off);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    __shared__ float wv[16];
+    __shared__ int wi[16], wb[16];
+    if (lane == 0) { wv[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int k = 1; k < 16; ++k) {
+            bad |= wb[k];
+            if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
+        }
+        out.device[b]->token = bi;
+        out.device[b]->nonfinite = bad;
+        out.host[b]->token = bi;
+        out.host[b]->nonfinite = bad;
+    }
+}
+
+template <int K, int MODE>
+void bgemv(const BatchGemvArgs& a, int rows, hipStream_t stream) {
+    require(a.batch >= 1 && a.batch <= kMaxBatch, "batched GEMV: 1..8 rows");
+    require(rows % kBatchRows == 0 && rows > 0, "batched GEMV: rows must be a positive multiple of 16");
+    bgemv_kernel<K, MODE><<<rows / kBatchRows, 256, 0, stream>>>(a);
+}
+
+}  // namespace
+
+void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols,
+                        hipStream_t stream) {
+    BatchGemvArgs a{};
+    a.w = w;
+    a.batch = batch;
+    for (int b = 0; b < batch; ++b) {
+        a.in[b] = x + size_t(b) * cols;
+        a.out[b] = y + size_t(b) * rows;
+    }
+    switch (cols) {
+        case 1024: bgemv<1024, kBPlain>(a, rows, stream); break;
+        case 2048: bgemv<2048, kBPlain>(a, rows, stream); break;
+        case 3072: bgemv<3072, kBPlain>(a, rows, stream); break;
+        default: throw std::runtime_error("batched GEMV: cols must be 1024, 2048 or 3072");
+    }
+}
+
+void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const float* final_norm,
+                         const float* cosines, const float* sines, hipStream_t stream) {
+    require(count >= 1 && count <= kMaxBatch, "batched decode: 1..8 sequences");
+    for (int l = 0; l < kLayers; ++l) {
+        const LayerDevice& W = seqs[0].layers[l];  // weights are shared; K/V are per sequence
+        BatchGemvArgs q{};
+        q.w = W.qkv_n;
+        q.norm_w = W.in_norm;
+        q.batch = count;
+        for (int b = 0; b < count; ++b) {
+            const DecodeScratch& s = seqs[b].s;
+            q.in[b] = s.x;
+            q.embed[b] = l == 0 ? embed + size_t(seqs[b].token) * kHidden : nullptr;
+            q.out[b] = s.qkv;
+            q.x[b] = s.x;
+        }
+        bgemv<kHidden, kBQKV>(q, kQKVRows, stream);
+
+        AttnSeq as[kMaxBatch];
+        for (int b = 0; b < count; ++b) {
+            const DecodeScratch& s = seqs[b].s;
+            as[b] = AttnSeq{s.qkv,          seqs[b].layers[l].keys, seqs[b].layers[l].values, s.attn_partial,
+                            s.attended,     seqs[b].pos,            seqs[b].context};
+        }
+        launch_attention_batch(as, count, W.q_norm, W.k_norm, cosines, sines, stream);
+
+        BatchGemvArgs o{};
+        o.w = W.o_n;
+        o.batch = count;
+        for (int b = 0; b < count; ++b) {
+            o.in[b] = seqs[b].s.attended;
+            o.x[b] = seqs[b].s.x;
+        }
+        bgemv<kQDim, kBO>(o, kHidden, stream);
+
+        BatchGemvArgs gu{};
+        gu.w = W.gateup_n;
+        gu.norm_w = W.post_norm;
+        gu.batch = count;
+        for (int b = 0; b < count; ++b) {
+            gu.in[b] = seqs[b].s.x;
+            gu.out[b] = seqs[b].s.act;
+        }
+        bgemv<kHidden, kBGateUp>(gu, kFFN, stream);
+
+        BatchGemvArgs d{};
+        d.w = W.down_n;
+        d.batch = count;
+        for (int b = 0; b < count; ++b) {
+            d.in[b] = seqs[b].s.act;
+            d.x[b] = seqs[b].s.x;
+        }
+        bgemv<kFFN, kBDown>(d, kHidden, stream);
+    }
+    BatchGemvArgs lm{};
+    lm.w = embed;  // tied head (engine/core.cpp:643-645)
+    lm.norm_w = final_norm;
+    lm.batch = count;
+    const DecodeScratch& s0 = seqs[0].s;
+    lm.lm_value = s0.lm_value;
+    lm.lm_index = s0.lm_index;
+    lm.lm_bad = s0.lm_bad;
+    BatchResults res{};
+    for (int b = 0; b < count; ++b) {
+        lm.in[b] = seqs[b].s.x;
+        lm.out[b] = seqs[b].s.logits;
+        lm.hidden[b] = seqs[b].s.hidden;
+        res.device[b] = seqs[b].s.result;
+        res.host[b] = seqs[b].host_out;
+    }
+    bgemv<kHidden, kBLmHead>(lm, kVocab, stream);
+    batch_argmax_kernel<<<count, 1024, 0, stream>>>(s0.lm_value, s0.lm_index, s0.lm_bad, res);
+}
+
+}  // namespace qwen_hip

@@ -1,0 +1,35 @@
+// Batched decode of up to 8 sequences sharing the weights (no reference
+// counterpart: the reference is single-stream; see batch.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.hpp"
+
+namespace qwen_hip {
+
+// One sequence of a batched step.
+struct BatchSeq {
+    const LayerDevice* layers;  // [28]: shared weights, this sequence's K/V cache
+    DecodeScratch s;            // this sequence's decode buffers
+    int pos;                    // position being written
+    int token;                  // id consumed at pos
+    int context;                // K/V cache capacity
+    ArgmaxResult* host_out;     // pinned slot for the greedy selection
+};
+
+// One decode step for each sequence: 28 x (norm+QKV skinny GEMM, batched
+// attention, O skinny GEMM + residual, norm+gate/up skinny GEMM + SwiGLU,
+// down skinny GEMM + residual), final norm + tied lm_head + per-sequence
+// argmax. Logits, hidden and selections land in each sequence's buffers.
+void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const float* final_norm,
+                         const float* cosines, const float* sines, hipStream_t stream);
+
+// Y[b] = W X[b] for b < batch on the matrix cores (W natural row-major
+// [rows x cols] FP16, X [batch x cols] FP32, Y [batch x rows] FP32); rows a
+// multiple of 16, cols in {1024, 2048, 3072}.
+void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols,
+                        hipStream_t stream);
+
+}  // namespace qwen_hip

@@ -3,6 +3,7 @@
 
 #include <string>
 
+#include "batch.hpp"
 #include "engine.hpp"
 #include "pack.hpp"
 #include "prefill.hpp"
@@ -10,6 +11,7 @@
 struct qwen_gpu_model {
     qwen_hip::Engine engine;
     qwen_gpu_model(const std::string& path, const qwen_hip::Options& o) : engine(path, o) {}
+    qwen_gpu_model(std::shared_ptr<qwen_hip::Weights> w, const qwen_hip::Options& o) : engine(std::move(w), o) {}
 };
 
 namespace {
@@ -54,6 +56,43 @@ int qwen_gpu_create(const char* weights, const qwen_gpu_options* options, qwen_g
 }
 
 void qwen_gpu_destroy(qwen_gpu_model* model) { delete model; }
+
+int qwen_gpu_create_sharing(const qwen_gpu_model* owner, const qwen_gpu_options* options, qwen_gpu_model** out) {
+    return guarded([&] {
+        need(owner, "owner");
+        need(out, "out");
+        *out = nullptr;
+        qwen_hip::Options o = owner->engine.options();
+        if (options) {
+            o.decode_threads = options->decode_threads;
+            o.prefill_threads = options->prefill_threads;
+            o.context = options->context;
+        }
+        *out = new qwen_gpu_model(owner->engine.weights(), o);
+    });
+}
+
+int qwen_gpu_copy_prefix(qwen_gpu_model* dst, const qwen_gpu_model* src, int positions) {
+    return guarded([&] {
+        need(dst, "dst");
+        need(src, "src");
+        dst->engine.copy_prefix(src->engine, positions);
+    });
+}
+
+int qwen_gpu_step_batch(qwen_gpu_model* const* models, const int* tokens, int count) {
+    return guarded([&] {
+        need(models, "models");
+        need(tokens, "tokens");
+        if (count < 1 || count > 8) throw std::runtime_error("Batch must hold 1..8 sequences");
+        qwen_hip::Engine* engines[8];
+        for (int i = 0; i < count; ++i) {
+            need(models[i], "model");
+            engines[i] = &models[i]->engine;
+        }
+        qwen_hip::Engine::step_batch(engines, tokens, count);
+    });
+}
 
 int qwen_gpu_reset(qwen_gpu_model* m) {
     return guarded([&] {
@@ -216,6 +255,16 @@ int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, 
         need(w, "w");
         need(c, "c");
         qwen_hip::launch_gemm(a, w, c, m, n, k, accumulate != 0, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
+int qwen_gpu_op_bgemv(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols, void* stream) {
+    return guarded([&] {
+        need(w, "w");
+        need(x, "x");
+        need(y, "y");
+        qwen_hip::launch_bgemv_plain(w, x, y, batch, rows, cols, static_cast<hipStream_t>(stream));
         hip_ok(hipGetLastError());
     });
 }

@@ -479,9 +479,9 @@ __device__ __forceinline__ float head_norm_rope(float raw, float w, float cs, fl
 // sum rescaled per tile). 512 threads: scores use 8 threads per position
 // (64 positions per pass); P.V uses 4 waves per head, lane = 8-channel group
 // + position lane (16 position lanes). Writes the split's unnormalized
-// output, max and sum; the O projection's prologue merges the splits.
-__global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
-    const int s = blockIdx.x, g = blockIdx.y;
+// output, max and sum; the O projection's prologue (or attn_merge_kernel)
+// merges the splits.
+__device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = a.pos, n = pos + 1;
     int chunk, ns;
@@ -655,6 +655,42 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
             part[129] = run_sum[h];
         }
     }
+}
+
+__global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
+    attn_split_body(a, blockIdx.x, blockIdx.y);
+}
+
+// Several sequences in one launch (blockIdx.z = sequence); each has its own
+// position, K/V cache and buffers.
+struct AttnBatch {
+    AttnArgs seq[kMaxBatch];
+};
+
+__global__ __launch_bounds__(512) void attn_decode_batch_kernel(const AttnBatch b) {
+    attn_split_body(b.seq[blockIdx.z], blockIdx.x, blockIdx.y);
+}
+
+// Merge of the position splits of one (sequence, query head), in the same
+// order and arithmetic as the O projection's prologue: o = sum_s w_s o_s /
+// sum_s w_s l_s with w_s = exp(m_s - max_s m_s). One split: attention already
+// wrote the normalized output.
+__global__ __launch_bounds__(128) void attn_merge_batch_kernel(const AttnBatch b) {
+    const AttnArgs& a = b.seq[blockIdx.y];
+    const int head = blockIdx.x, j = threadIdx.x;
+    int chunk, ns;
+    attn_split(a.pos + 1, chunk, ns);
+    if (ns == 1) return;
+    const float* base = a.partial + size_t(head >> 1) * kAttnSplits * kAttnPartial + (head & 1) * 132;
+    float mx = -INFINITY;
+    for (int k = 0; k < ns; ++k) mx = fmaxf(mx, base[k * kAttnPartial + 128]);
+    float l = 0.f, o = 0.f;
+    for (int k = 0; k < ns; ++k) {
+        const float w = expf(base[k * kAttnPartial + 128] - mx);
+        l += w * base[k * kAttnPartial + 129];
+        o += w * base[k * kAttnPartial + j];
+    }
+    a.attended[head * 128 + j] = o / l;
 }
 
 // Fused attention + O projection for n <= kFusedMaxPositions. Workgroup
@@ -1025,6 +1061,34 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
         }
         default: throw std::runtime_error("unknown decode kernel");
     }
+}
+
+void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
+                            const float* cosines, const float* sines, hipStream_t stream) {
+    require(count >= 1 && count <= kMaxBatch, "attention batch: 1..8 sequences");
+    AttnBatch b{};
+    int max_splits = 1;
+    for (int i = 0; i < count; ++i) {
+        AttnArgs& a = b.seq[i];
+        a.qkv = seqs[i].qkv;
+        a.q_norm = q_norm;
+        a.k_norm = k_norm;
+        a.cosines = cosines;
+        a.sines = sines;
+        a.keys = seqs[i].keys;
+        a.values = seqs[i].values;
+        a.pos = seqs[i].pos;
+        a.partial = seqs[i].partial;
+        a.attended = seqs[i].attended;
+        a.context = seqs[i].context;
+        a.scale = 1.0f / std::sqrt(128.0f);
+        require(a.pos >= 0 && a.pos < a.context, "attention batch: position outside the cache");
+        int chunk, splits;
+        attn_split(a.pos + 1, chunk, splits);
+        max_splits = std::max(max_splits, splits);
+    }
+    attn_decode_batch_kernel<<<dim3(max_splits, kKVHeads, count), 512, 0, stream>>>(b);
+    if (max_splits > 1) attn_merge_batch_kernel<<<dim3(kQHeads, count), 128, 0, stream>>>(b);
 }
 
 void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,

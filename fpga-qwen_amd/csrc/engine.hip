@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstring>
 
+#include "batch.hpp"
 #include "pack.hpp"
 #include "prefill.hpp"
 
@@ -26,14 +27,107 @@ T* Engine::device_alloc(size_t count) {
     return static_cast<T*>(p);
 }
 
-Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
-    // Same check order as the reference constructor: map, option ranges,
-    // header/index (engine/core.cpp:235-276).
-    Pack pack(weights);
+Weights::~Weights() {
+    for (void* p : allocations) (void)hipFree(p);
+}
+
+// Uploads a validated pack: natural copies of every matrix (gather, prefill
+// GEMMs, batched decode), chain-tiled copies (batch-1 GEMVs), norms and the
+// RoPE tables for the full 4096-position range.
+static std::shared_ptr<Weights> load_weights(const Pack& pack, hipStream_t stream) {
+    auto w = std::make_shared<Weights>();
+    auto alloc = [&](size_t bytes) {
+        void* p = nullptr;
+        HIP_CHECK(hipMalloc(&p, bytes));
+        w->allocations.push_back(p);
+        return p;
+    };
+    auto alloc_half = [&](size_t count) { return static_cast<uint16_t*>(alloc(count * 2)); };
+    auto upload = [&](uint16_t* dst, const PackTensor& t) {
+        HIP_CHECK(hipMemcpy(dst, t.half, size_t(t.rows) * t.cols * 2, hipMemcpyHostToDevice));
+    };
+    auto upload_norm = [&](const PackTensor& t) {
+        float* d = static_cast<float*>(alloc(size_t(t.rows) * 4));
+        HIP_CHECK(hipMemcpy(d, t.norm, size_t(t.rows) * 4, hipMemcpyHostToDevice));
+        return d;
+    };
+
+    // Embedding: natural copy (gather) and chain-tiled copy (tied head).
+    const PackTensor& emb = pack.tensor("model.embed_tokens.weight");
+    w->embed = alloc_half(size_t(kVocab) * kHidden);
+    HIP_CHECK(hipMemcpy(w->embed, emb.half, size_t(kVocab) * kHidden * 2, hipMemcpyHostToDevice));
+    w->lm_t = alloc_half(size_t(kVocab) * kHidden);
+    launch_tile_matrix(w->embed, nullptr, w->lm_t, kVocab, kHidden, stream);
+    w->final_norm = upload_norm(pack.tensor("model.norm.weight"));
+
+    w->layers.resize(kLayers);
+    w->prefill.resize(kLayers);
+    for (int l = 0; l < kLayers; ++l) {
+        LayerDevice& L = w->layers[l];
+        uint16_t* qkv_n = alloc_half(size_t(kQKVRows) * kHidden);
+        upload(qkv_n, pack.layer(l, "self_attn.q_proj.weight"));
+        upload(qkv_n + size_t(kQDim) * kHidden, pack.layer(l, "self_attn.k_proj.weight"));
+        upload(qkv_n + size_t(kQDim + kKVDim) * kHidden, pack.layer(l, "self_attn.v_proj.weight"));
+        uint16_t* o_n = alloc_half(size_t(kHidden) * kQDim);
+        upload(o_n, pack.layer(l, "self_attn.o_proj.weight"));
+        uint16_t* gu_n = alloc_half(size_t(2 * kFFN) * kHidden);
+        upload(gu_n, pack.layer(l, "mlp.gate_proj.weight"));
+        upload(gu_n + size_t(kFFN) * kHidden, pack.layer(l, "mlp.up_proj.weight"));
+        uint16_t* down_n = alloc_half(size_t(kHidden) * kFFN);
+        upload(down_n, pack.layer(l, "mlp.down_proj.weight"));
+        uint16_t* qkv_t = alloc_half(size_t(kQKVRows) * kHidden);
+        launch_tile_matrix(qkv_n, nullptr, qkv_t, kQKVRows, kHidden, stream);
+        uint16_t* o_t = alloc_half(size_t(kHidden) * kQDim);
+        launch_tile_matrix(o_n, nullptr, o_t, kHidden, kQDim, stream);
+        uint16_t* gu_t = alloc_half(size_t(2 * kFFN) * kHidden);
+        launch_tile_matrix(gu_n, gu_n + size_t(kFFN) * kHidden, gu_t, kFFN, kHidden, stream);
+        uint16_t* down_t = alloc_half(size_t(kHidden) * kFFN);
+        launch_tile_matrix(down_n, nullptr, down_t, kHidden, kFFN, stream);
+        L.qkv_t = qkv_t;
+        L.o_t = o_t;
+        L.o_n = o_n;
+        L.qkv_n = qkv_n;
+        L.gateup_n = gu_n;
+        L.down_n = down_n;
+        L.gateup_t = gu_t;
+        L.down_t = down_t;
+        L.in_norm = upload_norm(pack.layer(l, "input_layernorm.weight"));
+        L.post_norm = upload_norm(pack.layer(l, "post_attention_layernorm.weight"));
+        L.q_norm = upload_norm(pack.layer(l, "self_attn.q_norm.weight"));
+        L.k_norm = upload_norm(pack.layer(l, "self_attn.k_norm.weight"));
+        w->prefill[l] = PrefillLayer{qkv_n, o_n, gu_n, down_n, L.in_norm, L.post_norm, L.q_norm, L.k_norm,
+                                     nullptr, nullptr};
+    }
+    HIP_CHECK(hipStreamSynchronize(stream));
+
+    // RoPE tables in double, stored as FP32 (engine/core.cpp:287-288).
+    std::vector<float> cs(size_t(kMaxContext) * 64), sn(cs.size());
+    for (int p = 0; p < kMaxContext; ++p)
+        for (int j = 0; j < 64; ++j) {
+            const double angle = p / std::pow(1000000.0, 2.0 * j / kHeadDim);
+            cs[size_t(p) * 64 + j] = float(std::cos(angle));
+            sn[size_t(p) * 64 + j] = float(std::sin(angle));
+        }
+    w->cosines = static_cast<float*>(alloc(cs.size() * 4));
+    w->sines = static_cast<float*>(alloc(sn.size() * 4));
+    HIP_CHECK(hipMemcpy(w->cosines, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(w->sines, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    HIP_CHECK(hipGetLastError());
+    return w;
+}
+
+static void check_options(const Options& opt) {
     require(opt.decode_threads >= 1 && opt.decode_threads <= 64 && opt.prefill_threads >= 1 &&
                 opt.prefill_threads <= 64,
             "Threads must be in 1..64");
     require(opt.context >= 1 && opt.context <= kMaxContext, "Context must be in 1..4096");
+}
+
+Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
+    // Same check order as the reference constructor: map, option ranges,
+    // header/index (engine/core.cpp:235-276).
+    Pack pack(weights);
+    check_options(opt);
     pack.validate();
 
     int devices = 0;
@@ -42,117 +136,80 @@ Engine::Engine(const std::string& weights, Options opt) : options_(opt) {
     try {
         HIP_CHECK(hipSetDevice(0));
         HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
-        const int ctx = opt.context;
-
-        // Embedding: natural copy (gather) and chain-tiled copy (tied head).
-        const PackTensor& emb = pack.tensor("model.embed_tokens.weight");
-        embed_ = device_alloc<uint16_t>(size_t(kVocab) * kHidden);
-        HIP_CHECK(hipMemcpy(embed_, emb.half, size_t(kVocab) * kHidden * 2, hipMemcpyHostToDevice));
-        lm_t_ = device_alloc<uint16_t>(size_t(kVocab) * kHidden);
-        launch_tile_matrix(embed_, nullptr, lm_t_, kVocab, kHidden, stream_);
-        final_norm_ = device_alloc<float>(kHidden);
-        HIP_CHECK(hipMemcpy(final_norm_, pack.tensor("model.norm.weight").norm, kHidden * 4, hipMemcpyHostToDevice));
-
-        // Layer matrices stay in natural layout (prefill GEMMs) and get a
-        // chain-tiled copy (decode GEMVs).
-        auto upload = [&](uint16_t* dst, const PackTensor& t) {
-            HIP_CHECK(hipMemcpy(dst, t.half, size_t(t.rows) * t.cols * 2, hipMemcpyHostToDevice));
-        };
-        auto upload_norm = [&](const PackTensor& t) {
-            float* d = device_alloc<float>(t.rows);
-            HIP_CHECK(hipMemcpy(d, t.norm, size_t(t.rows) * 4, hipMemcpyHostToDevice));
-            return d;
-        };
-        layers_.resize(kLayers);
-        prefill_layers_.resize(kLayers);
-        for (int l = 0; l < kLayers; ++l) {
-            LayerDevice& L = layers_[l];
-            PrefillLayer& P = prefill_layers_[l];
-            uint16_t* qkv_n = device_alloc<uint16_t>(size_t(kQKVRows) * kHidden);
-            upload(qkv_n, pack.layer(l, "self_attn.q_proj.weight"));
-            upload(qkv_n + size_t(kQDim) * kHidden, pack.layer(l, "self_attn.k_proj.weight"));
-            upload(qkv_n + size_t(kQDim + kKVDim) * kHidden, pack.layer(l, "self_attn.v_proj.weight"));
-            uint16_t* o_n = device_alloc<uint16_t>(size_t(kHidden) * kQDim);
-            upload(o_n, pack.layer(l, "self_attn.o_proj.weight"));
-            uint16_t* gu_n = device_alloc<uint16_t>(size_t(2 * kFFN) * kHidden);
-            upload(gu_n, pack.layer(l, "mlp.gate_proj.weight"));
-            upload(gu_n + size_t(kFFN) * kHidden, pack.layer(l, "mlp.up_proj.weight"));
-            uint16_t* down_n = device_alloc<uint16_t>(size_t(kHidden) * kFFN);
-            upload(down_n, pack.layer(l, "mlp.down_proj.weight"));
-            uint16_t* qkv_t = device_alloc<uint16_t>(size_t(kQKVRows) * kHidden);
-            launch_tile_matrix(qkv_n, nullptr, qkv_t, kQKVRows, kHidden, stream_);
-            uint16_t* o_t = device_alloc<uint16_t>(size_t(kHidden) * kQDim);
-            launch_tile_matrix(o_n, nullptr, o_t, kHidden, kQDim, stream_);
-            uint16_t* gu_t = device_alloc<uint16_t>(size_t(2 * kFFN) * kHidden);
-            launch_tile_matrix(gu_n, gu_n + size_t(kFFN) * kHidden, gu_t, kFFN, kHidden, stream_);
-            uint16_t* down_t = device_alloc<uint16_t>(size_t(kHidden) * kFFN);
-            launch_tile_matrix(down_n, nullptr, down_t, kHidden, kFFN, stream_);
-            L.qkv_t = qkv_t;
-            L.o_t = o_t;
-            L.o_n = o_n;
-            L.gateup_t = gu_t;
-            L.down_t = down_t;
-            L.in_norm = upload_norm(pack.layer(l, "input_layernorm.weight"));
-            L.post_norm = upload_norm(pack.layer(l, "post_attention_layernorm.weight"));
-            L.q_norm = upload_norm(pack.layer(l, "self_attn.q_norm.weight"));
-            L.k_norm = upload_norm(pack.layer(l, "self_attn.k_norm.weight"));
-            L.keys = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
-            L.values = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
-            P = PrefillLayer{qkv_n, o_n, gu_n, down_n, L.in_norm, L.post_norm, L.q_norm, L.k_norm, L.keys, L.values};
-        }
-        HIP_CHECK(hipStreamSynchronize(stream_));
-
-        // RoPE tables in double, stored as FP32 (engine/core.cpp:287-288).
-        std::vector<float> cs(size_t(ctx) * 64), sn(cs.size());
-        for (int p = 0; p < ctx; ++p)
-            for (int j = 0; j < 64; ++j) {
-                const double angle = p / std::pow(1000000.0, 2.0 * j / kHeadDim);
-                cs[size_t(p) * 64 + j] = float(std::cos(angle));
-                sn[size_t(p) * 64 + j] = float(std::sin(angle));
-            }
-        cosines_ = device_alloc<float>(cs.size());
-        sines_ = device_alloc<float>(sn.size());
-        HIP_CHECK(hipMemcpy(cosines_, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
-        HIP_CHECK(hipMemcpy(sines_, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-
-        DecodeScratch& s = scratch_;
-        s.x = device_alloc<float>(kHidden);
-        s.qkv = device_alloc<float>(kQKVRows);
-        s.attended = device_alloc<float>(kQDim);
-        s.act = device_alloc<float>(kFFN);
-        s.logits = device_alloc<float>(kVocab);
-        s.hidden = device_alloc<float>(kHidden);
-        s.attn_partial = device_alloc<float>(size_t(kKVHeads) * kAttnSplits * kAttnPartial);
-        s.o_part = device_alloc<float>(size_t(kKVHeads) * kHidden);
-        s.lm_value = device_alloc<float>(kLmGroups);
-        s.lm_index = device_alloc<int>(kLmGroups);
-        s.lm_bad = device_alloc<int>(kLmGroups);
-        s.result = device_alloc<ArgmaxResult>(1);
-        ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
-        ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
-        base_logits_ = device_alloc<float>(kVocab);
-        base_hidden_ = device_alloc<float>(kHidden);
-        void* pinned = nullptr;
-        HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
-        result_host_ = static_cast<ArgmaxResult*>(pinned);
-        std::memset(result_host_, 0, sizeof(ArgmaxResult) * 3);
-        PrefillScratch& ps = prefill_;
-        ps.x = device_alloc<float>(size_t(kChunk) * kHidden);
-        ps.h = device_alloc<float>(size_t(kChunk) * kHidden);
-        ps.qkv = device_alloc<float>(size_t(kChunk) * kQKVRows);
-        ps.attended = device_alloc<float>(size_t(kChunk) * kQDim);
-        ps.gu = device_alloc<float>(size_t(kChunk) * 2 * kFFN);
-        ps.act = device_alloc<float>(size_t(kChunk) * kFFN);
-        ids_dev_ = device_alloc<int>(size_t(ctx));
-        HIP_CHECK(hipHostMalloc(&pinned, sizeof(int) * size_t(ctx), hipHostMallocDefault));
-        ids_host_ = static_cast<int*>(pinned);
-        HIP_CHECK(hipStreamSynchronize(stream_));
-
-        HIP_CHECK(hipGetLastError());
+        weights_ = load_weights(pack, stream_);
+        init_state();
     } catch (...) {
         release();
         throw;
     }
+}
+
+Engine::Engine(std::shared_ptr<Weights> weights, Options opt) : options_(opt) {
+    check_options(opt);
+    require(weights != nullptr, "No weights to share");
+    try {
+        HIP_CHECK(hipSetDevice(0));
+        HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+        weights_ = std::move(weights);
+        init_state();
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+// Per-sequence state: KV cache, decode and prefill scratch, pinned staging.
+void Engine::init_state() {
+    const int ctx = options_.context;
+    const Weights& w = *weights_;
+    embed_ = w.embed;
+    lm_t_ = w.lm_t;
+    final_norm_ = w.final_norm;
+    cosines_ = w.cosines;
+    sines_ = w.sines;
+    layers_ = w.layers;
+    prefill_layers_ = w.prefill;
+    for (int l = 0; l < kLayers; ++l) {
+        layers_[l].keys = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
+        layers_[l].values = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
+        prefill_layers_[l].keys = layers_[l].keys;
+        prefill_layers_[l].values = layers_[l].values;
+    }
+
+    DecodeScratch& s = scratch_;
+    s.x = device_alloc<float>(kHidden);
+    s.qkv = device_alloc<float>(kQKVRows);
+    s.attended = device_alloc<float>(kQDim);
+    s.act = device_alloc<float>(kFFN);
+    s.logits = device_alloc<float>(kVocab);
+    s.hidden = device_alloc<float>(kHidden);
+    s.attn_partial = device_alloc<float>(size_t(kKVHeads) * kAttnSplits * kAttnPartial);
+    s.o_part = device_alloc<float>(size_t(kKVHeads) * kHidden);
+    s.lm_value = device_alloc<float>(size_t(kBatchLmGroups) * kMaxBatch);
+    s.lm_index = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
+    s.lm_bad = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
+    s.result = device_alloc<ArgmaxResult>(1);
+    ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
+    ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
+    base_logits_ = device_alloc<float>(kVocab);
+    base_hidden_ = device_alloc<float>(kHidden);
+    void* pinned = nullptr;
+    HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
+    result_host_ = static_cast<ArgmaxResult*>(pinned);
+    std::memset(result_host_, 0, sizeof(ArgmaxResult) * 3);
+    PrefillScratch& ps = prefill_;
+    const size_t prows = size_t(std::max(2, std::min(ctx, kPrefillRows)));  // a call never exceeds the context
+    ps.x = device_alloc<float>(prows * kHidden);
+    ps.h = device_alloc<float>(prows * kHidden);
+    ps.qkv = device_alloc<float>(prows * kQKVRows);
+    ps.attended = device_alloc<float>(prows * kQDim);
+    ps.gu = device_alloc<float>(prows * 2 * kFFN);
+    ps.act = device_alloc<float>(prows * kFFN);
+    ids_dev_ = device_alloc<int>(size_t(ctx));
+    HIP_CHECK(hipHostMalloc(&pinned, sizeof(int) * size_t(ctx), hipHostMallocDefault));
+    ids_host_ = static_cast<int*>(pinned);
+    HIP_CHECK(hipStreamSynchronize(stream_));
+    HIP_CHECK(hipGetLastError());
 }
 
 void Engine::release() {
@@ -210,26 +267,28 @@ void Engine::append(const int* ids, size_t count) {
     require(count <= size_t(options_.context - pos_), "Context capacity exceeded");
     for (size_t i = 0; i < count; ++i) require(ids[i] >= 0 && ids[i] < kVocab, "Token ID out of range");
     invalidate();
-    // 512-row chunks counted from the start of this call (engine/core.cpp:712).
-    // A chunk of one row uses the batch-1 path, as in the reference.
+    // The reference splits a call into 512-row chunks counted from its start
+    // and runs a one-row chunk on the batch-1 path (engine/core.cpp:712). Every
+    // row of the batched path is computed independently of the rows grouped
+    // with it (GEMM rows, row kernels, and causal attention whose key split
+    // follows absolute positions), so consecutive 512-row chunks run as one
+    // batched pass; only a trailing one-row chunk takes the batch-1 path.
     std::copy(ids, ids + count, ids_host_);
     HIP_CHECK(hipMemcpyAsync(ids_dev_, ids_host_, count * sizeof(int), hipMemcpyHostToDevice, stream_));
-    for (size_t begin = 0; begin < count; begin += kChunk) {
-        const int rows = int(std::min<size_t>(kChunk, count - begin));
-        const bool last = begin + rows == count;
-        if (rows == 1) {
-            run_token(ids[begin], last, 0);
-            continue;
-        }
-        launch_prefill_chunk(prefill_layers_.data(), embed_, ids_dev_ + begin, rows, pos_, cosines_, sines_,
+    const size_t batched = count % kChunk == 1 ? count - 1 : count;
+    require(batched <= size_t(kPrefillRows), "prefill: call longer than the batched pass");
+    if (batched > 0) {
+        const int rows = int(batched);
+        launch_prefill_chunk(prefill_layers_.data(), embed_, ids_dev_, rows, pos_, cosines_, sines_,
                              options_.context, prefill_, stream_);
         pos_ += rows;
-        if (last) {
+        if (batched == count) {
             HIP_CHECK(hipMemcpyAsync(scratch_.x, prefill_.x + size_t(rows - 1) * kHidden, kHidden * sizeof(float),
                                      hipMemcpyDeviceToDevice, stream_));
             launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
         }
     }
+    if (batched < count) run_token(ids[count - 1], true, 0);
     HIP_CHECK(hipGetLastError());
     sync();
     has_logits_ = true;
@@ -256,6 +315,61 @@ const float* Engine::hidden() {
         host_hidden_valid_ = true;
     }
     return host_hidden_.data();
+}
+
+// The reference rewinds one model to a 512-token boundary and prefills a new
+// suffix (engine/INTERFACE.md:94-103); for several sequences that share a
+// prefix the same rewind is applied to a copy: src's K/V rows
+// 0..positions-1 on the device, as computed by src.
+void Engine::copy_prefix(const Engine& src, int positions) {
+    require(!pending_, "Commit or discard pending verification before inference");
+    require(src.weights_ == weights_, "Sequences do not share weights");
+    require(positions >= 0 && positions <= src.pos_, "Rewind position out of range");
+    require(positions <= options_.context, "Context capacity exceeded");
+    invalidate();
+    pos_ = 0;
+    const size_t row = size_t(kHeadDim) * sizeof(uint16_t);
+    if (positions > 0 && &src != this) {
+        HIP_CHECK(hipStreamSynchronize(src.stream_));
+        for (int l = 0; l < kLayers; ++l) {
+            HIP_CHECK(hipMemcpy2DAsync(layers_[l].keys, row * options_.context, src.layers_[l].keys,
+                                       row * src.options_.context, row * positions, kKVHeads,
+                                       hipMemcpyDeviceToDevice, stream_));
+            HIP_CHECK(hipMemcpy2DAsync(layers_[l].values, row * options_.context, src.layers_[l].values,
+                                       row * src.options_.context, row * positions, kKVHeads,
+                                       hipMemcpyDeviceToDevice, stream_));
+        }
+        sync();
+    }
+    pos_ = positions;
+}
+
+// Validates every sequence before running any (as append does for one).
+void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
+    require(count >= 1 && count <= kMaxBatch, "Batch must hold 1..8 sequences");
+    for (int i = 0; i < count; ++i) {
+        require(seqs[i] != nullptr, "Null sequence in batch");
+        for (int j = 0; j < i; ++j) require(seqs[j] != seqs[i], "Sequence repeated in batch");
+        require(seqs[i]->weights_ == seqs[0]->weights_, "Sequences do not share weights");
+        require(!seqs[i]->pending_, "Commit or discard pending verification before inference");
+        require(seqs[i]->pos_ < seqs[i]->options_.context, "Context capacity exceeded");
+        require(tokens[i] >= 0 && tokens[i] < kVocab, "Token ID out of range");
+    }
+    BatchSeq bs[kMaxBatch];
+    for (int i = 0; i < count; ++i) {
+        Engine& e = *seqs[i];
+        e.invalidate();
+        HIP_CHECK(hipStreamSynchronize(e.stream_));
+        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_};
+    }
+    Engine& lead = *seqs[0];
+    launch_decode_batch(bs, count, lead.embed_, lead.final_norm_, lead.cosines_, lead.sines_, lead.stream_);
+    HIP_CHECK(hipGetLastError());
+    lead.sync();
+    for (int i = 0; i < count; ++i) {
+        ++seqs[i]->pos_;
+        seqs[i]->has_logits_ = true;
+    }
 }
 
 int Engine::greedy() {

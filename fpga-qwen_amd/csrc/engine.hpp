@@ -18,9 +18,29 @@ struct Options {
     int context = 4096;
 };
 
+// Device weights of one pack, shared by every sequence created from it
+// (freed when the last one goes).
+struct Weights {
+    Weights() = default;
+    Weights(const Weights&) = delete;
+    Weights& operator=(const Weights&) = delete;
+    ~Weights();
+    std::vector<void*> allocations;
+    std::vector<LayerDevice> layers;    // keys/values unset
+    std::vector<PrefillLayer> prefill;  // keys/values unset
+    uint16_t* embed = nullptr;          // natural [vocab x 1024]
+    uint16_t* lm_t = nullptr;           // chain-tiled embedding
+    float* final_norm = nullptr;
+    float* cosines = nullptr;           // [4096][64]
+    float* sines = nullptr;
+};
+
 class Engine {
 public:
     Engine(const std::string& weights, Options options);
+    // A further sequence on already uploaded weights: own KV cache and state.
+    Engine(std::shared_ptr<Weights> weights, Options options);
+    const std::shared_ptr<Weights>& weights() const { return weights_; }
     ~Engine();
     Engine(const Engine&) = delete;
     Engine& operator=(const Engine&) = delete;
@@ -48,7 +68,15 @@ public:
     float time_kernel(int which, int iterations);
     hipStream_t stream() const { return stream_; }
 
+    // This sequence becomes `src` truncated to `positions`: K/V rows
+    // 0..positions-1 copied on the device, no current logits.
+    void copy_prefix(const Engine& src, int positions);
+    // One decode step for each of `count` sequences sharing weights, from one
+    // read of every weight matrix (tokens[i] is consumed by seqs[i]).
+    static void step_batch(Engine* const* seqs, const int* tokens, int count);
+
 private:
+    void init_state();
     void append(const int* ids, size_t count);
     void run_token(int token, bool head, int result_slot);
     void release();
@@ -56,6 +84,7 @@ private:
     void invalidate();
 
     Options options_;
+    std::shared_ptr<Weights> weights_;
     hipStream_t stream_ = nullptr;
     std::vector<void*> allocations_;
     std::vector<LayerDevice> layers_;
@@ -63,8 +92,8 @@ private:
     PrefillScratch prefill_{};
     int* ids_dev_ = nullptr;    // prompt ids of the current call
     int* ids_host_ = nullptr;   // pinned staging for them
-    uint16_t* embed_ = nullptr;     // natural [vocab x 1024]
-    uint16_t* lm_t_ = nullptr;      // chain-tiled embedding
+    uint16_t* embed_ = nullptr;     // the shared weights' pointers, for brevity
+    uint16_t* lm_t_ = nullptr;
     float* final_norm_ = nullptr;
     float* cosines_ = nullptr;
     float* sines_ = nullptr;

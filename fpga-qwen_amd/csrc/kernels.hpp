@@ -57,6 +57,11 @@ inline constexpr int kAttnORows = 32;
 inline constexpr int kAttnOGroups = kKVHeads * (kHidden / kAttnORows);  // 256 workgroups
 __host__ __device__ inline bool attn_fused(int n) { return n <= kFusedMaxPositions; }
 
+inline constexpr int kMaxBatch = 8;             // sequences per batched decode step
+inline constexpr int kBatchRows = 16;           // output rows per batched-GEMV workgroup (one MFMA tile)
+inline constexpr int kBatchLmGroups = kVocab / kBatchRows;  // 9496 lm_head workgroups
+static_assert(kVocab % kBatchRows == 0, "batched lm_head tiles must cover the vocabulary");
+
 inline constexpr int kLmWaves = 4;              // lm_head workgroup waves
 inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 4748 workgroups
 static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
@@ -64,7 +69,10 @@ static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabu
 struct LayerDevice {
     const uint16_t* qkv_t;     // tiled [4096 x 1024]: q rows, k rows, v rows
     const uint16_t* o_t;       // tiled [1024 x 2048]
-    const uint16_t* o_n;       // natural [1024 x 2048] (fused attention + O)
+    const uint16_t* o_n;       // natural [1024 x 2048] (fused attention + O, batched decode)
+    const uint16_t* qkv_n;     // natural [4096 x 1024] (batched decode)
+    const uint16_t* gateup_n;  // natural [6144 x 1024]: gate rows then up rows (batched decode)
+    const uint16_t* down_n;    // natural [1024 x 3072] (batched decode)
     const uint16_t* gateup_t;  // tiled [6144 x 1024]: tile T = gate rows 4T..4T+3, up rows 4T..4T+3
     const uint16_t* down_t;    // tiled [1024 x 3072]
     const float* in_norm;      // [1024]
@@ -84,9 +92,9 @@ struct DecodeScratch {
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
     float* o_part;        // [8][1024]: per-KV-head partial O projections (fused path)
-    float* lm_value;      // [kLmGroups]
-    int* lm_index;        // [kLmGroups]
-    int* lm_bad;          // [kLmGroups]
+    float* lm_value;      // [kBatchLmGroups x kMaxBatch] argmax partials (batch-1 uses kLmGroups)
+    int* lm_index;
+    int* lm_bad;
     ArgmaxResult* result; // [1] device copy of the selection
 };
 
@@ -116,6 +124,24 @@ void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, int po
 void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
+
+// One sequence of a batched attention launch.
+struct AttnSeq {
+    const float* qkv;   // raw projections [4096]
+    uint16_t* keys;     // this layer's cache [8][context][128]
+    uint16_t* values;
+    float* partial;     // [8][kAttnSplits][kAttnPartial]
+    float* attended;    // [2048] normalized output
+    int pos;            // position being written
+    int context;
+};
+
+// Decode attention of up to kMaxBatch sequences in one launch (split
+// attention for every context length) plus the merge of their splits into
+// `attended`; per sequence the same arithmetic as the split path of one
+// sequence.
+void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
+                            const float* cosines, const float* sines, hipStream_t stream);
 
 // Plain device copy (bytes a multiple of 16), for counter calibration.
 void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);

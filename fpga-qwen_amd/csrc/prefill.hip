@@ -397,7 +397,7 @@ void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int 
 void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, const int* ids_dev, int rows, int pos0,
                           const float* cosines, const float* sines, int context, const PrefillScratch& s,
                           hipStream_t stream) {
-    require(rows >= 1 && rows <= kChunk, "prefill chunk: bad row count");
+    require(rows >= 1 && rows <= kPrefillRows, "prefill chunk: bad row count");
     embed_rows_kernel<<<rows, 256, 0, stream>>>(ids_dev, embed, s.x);
     const float scale = 1.0f / std::sqrt(128.0f);
     for (int l = 0; l < kLayers; ++l) {

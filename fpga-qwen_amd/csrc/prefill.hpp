@@ -1,4 +1,4 @@
-// Batched prefill (chunks of up to 512 rows; engine/core.cpp:353-646, 712).
+// Batched prefill (up to kPrefillRows rows per pass; engine/core.cpp:353-646, 712).
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -22,7 +22,7 @@ struct PrefillLayer {
     uint16_t* values;          // [8][context][128]
 };
 
-// FP32 activations of one chunk (512 rows each).
+// FP32 activations of one batched pass (up to kPrefillRows rows each).
 struct PrefillScratch {
     float* x;         // [512 x 1024] residual stream
     float* h;         // [512 x 1024] normalized

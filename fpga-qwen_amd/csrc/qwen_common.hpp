@@ -15,7 +15,8 @@ inline constexpr int kKVHeads = 8;        // K
 inline constexpr int kFFN = 3072;         // F
 inline constexpr int kLayers = 28;        // L
 inline constexpr int kVocab = 151936;     // vocabulary
-inline constexpr int kChunk = 512;        // prefix_reuse_chunk / prefill chunk
+inline constexpr int kChunk = 512;        // prefix_reuse_chunk / the reference's prefill chunk
+inline constexpr int kPrefillRows = 4096; // rows of one batched prefill launch sequence
 inline constexpr int kMaxContext = 4096;  // Options::context upper bound
 inline constexpr int kQDim = kQHeads * kHeadDim;    // 2048
 inline constexpr int kKVDim = kKVHeads * kHeadDim;  // 1024

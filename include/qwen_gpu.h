@@ -43,6 +43,29 @@ int qwen_gpu_create(const char* weights, const qwen_gpu_options* options, qwen_g
 /* qwen_cpu::Model::~Model, engine/core.hpp:29. NULL is ignored. */
 void qwen_gpu_destroy(qwen_gpu_model* model);
 
+/* A further model on the device weights already uploaded for `owner` (no
+ * second upload): its own K/V cache, position and buffers. options == NULL
+ * copies owner's. The weights stay until the last model using them is
+ * destroyed. No reference counterpart (the reference is single-stream): it
+ * backs the batched decode below for callers serving several sequences. */
+int qwen_gpu_create_sharing(const qwen_gpu_model* owner, const qwen_gpu_options* options, qwen_gpu_model** out);
+/* dst becomes src truncated to `positions`: K/V rows 0..positions-1 copied on
+ * the device as src computed them, no current logits. The canonical
+ * prefix-reuse rewind (engine/INTERFACE.md:94-103; Model::truncate,
+ * engine/core.cpp:722-727) applied to a copy; both models share weights.
+ * Fails with "Rewind position out of range" unless 0 <= positions <= src's
+ * position. */
+int qwen_gpu_copy_prefix(qwen_gpu_model* dst, const qwen_gpu_model* src, int positions);
+/* One decode step for each of `count` (1..8) distinct models that share
+ * weights: models[i] consumes tokens[i] (Model::step, engine/core.hpp:38),
+ * with every projection reading each weight matrix once for all rows (FP16
+ * matrix cores, FP32 activations split into FP16 hi + lo, FP32 sums) and the
+ * same attention arithmetic as a batch-1 step past 512 positions. Every model
+ * is validated (pending verification, capacity, token range) before any
+ * runs. Afterwards each model has current logits and qwen_gpu_greedy works
+ * as after a step. No reference counterpart. */
+int qwen_gpu_step_batch(qwen_gpu_model* const* models, const int* tokens, int count);
+
 /* Model::reset, engine/core.hpp:32; engine/core.cpp:718-721. */
 int qwen_gpu_reset(qwen_gpu_model* model);
 /* Model::truncate(position), engine/core.hpp:35; engine/core.cpp:722-727. */
@@ -108,6 +131,11 @@ int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, 
  * cores), W natural row-major FP16; N and K multiples of 64, M >= 1. */
 int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
                      void* stream);
+/* Batched projection of the multi-sequence decode: y[b] = W x[b] for b <
+ * batch (1..8) on the matrix cores; W natural row-major FP16 [rows x cols],
+ * x FP32 [batch x cols], y FP32 [batch x rows]; rows a multiple of 16, cols
+ * in {1024, 2048, 3072}. No reference counterpart (parity-test entry). */
+int qwen_gpu_op_bgemv(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols, void* stream);
 /* Isolated GEMV microbenchmark: average milliseconds of one op_gemv launch
  * over `iterations` back-to-back launches on the default stream, timed with
  * HIP events, cycling through `copies` chain-tiled weight copies laid

@@ -1,0 +1,151 @@
+"""Batched decode of several sequences that share the weights (the
+prefix-reuse workload: a canonical prefix rewound and reused, distinct
+suffixes, greedy decode as a batch on one GPU).
+
+The reference is single-stream, so parity is per sequence: every sequence
+of a batched step must match the same sequence stepped alone (Model::step,
+engine/core.cpp:707-714) and the oracle trajectory, under the gate of
+tools/check_native_saved_oracle.py:36 (max-abs 1e-2, RMS 2e-3, greedy
+identity). The batched projections run on the matrix cores (FP32
+activations as FP16 hi + lo), so they are held to that gate and to an FP64
+bound, not to bit equality with the batch-1 GEMVs.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_binding import compare_logits
+
+PROMPTS = json.loads((Path(__file__).parent / 'golden' / 'prompts.json').read_text())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('rows,cols', [(4096, 1024), (1024, 2048), (1024, 3072), (6144, 1024)])
+@pytest.mark.parametrize('batch', [1, 3, 8])
+def test_bgemv_against_fp64(qpkg, rows, cols, batch):
+    rng = np.random.default_rng(1000 + rows + cols + batch)
+    w = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02).astype(np.float16)
+    x = rng.standard_normal((batch, cols), dtype=np.float32)
+    y = qpkg.bgemv(w, x)
+    w64, x64 = w.astype(np.float64), x.astype(np.float64)
+    ref = x64 @ w64.T
+    bound = 4e-6 * (np.abs(x64) @ np.abs(w64).T) + 1e-7
+    err = np.abs(y.astype(np.float64) - ref)
+    assert (err <= bound).all(), float((err / bound).max())
+
+
+def _seed_sequences(qpkg, pack0):
+    """A base model with a 300-token prefix; three sequences reuse it with
+    suffixes of 20, 37 and 5 tokens, a fourth runs its own 600-token prompt
+    (past 512 positions). Returns (base, batch sequences, twins stepped alone)."""
+    prompt = PROMPTS['long_3968']
+    base = qpkg.Model(pack0, context=4096)
+    base.prefill(prompt[:300])
+    batch, alone = [], []
+    for suffix in (prompt[300:320], prompt[300:337], prompt[1000:1005]):
+        for group in (batch, alone):
+            m = base.share()
+            m.copy_prefix(base, 300)
+            m.prefill(suffix)
+            group.append(m)
+    for group in (batch, alone):
+        m = base.share()
+        m.prefill(prompt[2000:2600])
+        group.append(m)
+    return base, batch, alone
+
+
+@pytest.mark.gpu
+def test_step_batch_equals_single_steps(qpkg, pack0):
+    base, batch, alone = _seed_sequences(qpkg, pack0)
+    try:
+        tokens = [m.greedy() for m in batch]
+        assert tokens == [m.greedy() for m in alone]
+        worst = 0.0
+        for _ in range(6):
+            qpkg.step_batch(batch, tokens)
+            for m, t in zip(alone, tokens):
+                m.step(t)
+            for b, a in zip(batch, alone):
+                assert b.position() == a.position()
+                result = compare_logits(b.logits(), a.logits())
+                assert result['passed'], result
+                worst = max(worst, result['max_abs'])
+                assert np.array_equal(b.hidden().shape, (1024,))
+            tokens = [m.greedy() for m in batch]
+            assert tokens == [m.greedy() for m in alone]
+        print('max_abs batched vs alone', worst)
+    finally:
+        for m in batch + alone + [base]:
+            m.close()
+
+
+@pytest.mark.gpu
+def test_step_batch_matches_oracle(qpkg, pack0, oracle_lib):
+    prompt = PROMPTS['long_3968']
+    base = qpkg.Model(pack0, context=4096)
+    other = base.share()
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    try:
+        base.prefill(prompt[:85])
+        other.prefill(prompt[500:530])
+        oracle.prefill(prompt[:85])
+        tokens = [base.greedy(), other.greedy()]
+        for _ in range(8):
+            qpkg.step_batch([base, other], tokens)
+            oracle.step(tokens[0])
+            result = compare_logits(base.logits(), oracle.logits())
+            assert result['passed'], result
+            tokens = [base.greedy(), other.greedy()]
+    finally:
+        oracle.close()
+        other.close()
+        base.close()
+
+
+@pytest.mark.gpu
+def test_copy_prefix_equals_truncate(qpkg, pack0):
+    prompt = PROMPTS['long_3968']
+    with qpkg.Model(pack0) as a:
+        b = a.share(context=1024)
+        try:
+            a.prefill(prompt[:700])
+            b.copy_prefix(a, 512)
+            assert b.position() == 512 and b.logits().size == 0
+            b.prefill(prompt[512:800])
+            a.truncate(512)
+            a.prefill(prompt[512:800])
+            assert np.array_equal(a.logits().view(np.uint32), b.logits().view(np.uint32))
+            with pytest.raises(RuntimeError, match='Rewind position out of range'):
+                b.copy_prefix(a, 801)
+        finally:
+            b.close()
+
+
+@pytest.mark.gpu
+def test_step_batch_validates_before_running(qpkg, pack0):
+    prompt = PROMPTS['long_3968']
+    with qpkg.Model(pack0) as a, qpkg.Model(pack0) as stranger:
+        b = a.share()
+        try:
+            a.prefill(prompt[:10])
+            b.prefill(prompt[10:30])
+            stranger.prefill(prompt[:5])
+            before = (a.position(), b.position(), a.logits().copy())
+            for models, tokens, message in (
+                    ([a, stranger], [1, 2], 'do not share weights'),
+                    ([a, b], [1, 151936], 'Token ID out of range'),
+                    ([a, a], [1, 2], 'repeated'),
+                    ([a] * 9, [1] * 9, '1..8')):
+                with pytest.raises(RuntimeError, match=message):
+                    qpkg.step_batch(models, tokens)
+                assert (a.position(), b.position()) == before[:2]
+            assert np.array_equal(a.logits(), before[2])
+            b.verify_two(3, 4)
+            with pytest.raises(RuntimeError, match='Commit or discard pending verification'):
+                qpkg.step_batch([a, b], [1, 2])
+            assert (a.position(), b.position()) == before[:2]
+        finally:
+            b.close()

@@ -88,3 +88,27 @@ def test_canonical_prefix_reuse_equals_fresh(qpkg, pack0):
         m.truncate(1024)
         m.prefill(prompt[1024:])
         assert np.array_equal(m.logits().view(np.uint32), fresh[0].view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_prefill_rows_independent_of_grouping(qpkg, pack0):
+    """A call runs its consecutive 512-row chunks as one batched pass; that is
+    only legal because every batched row is computed alone. Any split of a
+    prompt into calls of two or more rows must give the same bits, and a
+    trailing one-row chunk takes the batch-1 path like a step
+    (engine/core.cpp:712)."""
+    prompt = PROMPTS['long_3968'][:1025]
+    with qpkg.Model(pack0) as m:
+        m.prefill(prompt[:700])
+        whole = m.logits().view(np.uint32).copy()
+        m.reset()
+        m.prefill(prompt[:300])
+        m.prefill(prompt[300:700])
+        assert np.array_equal(m.logits().view(np.uint32), whole)
+        m.reset()
+        m.prefill(prompt)  # 1024 batched rows + one batch-1 row
+        tail = m.logits().view(np.uint32).copy()
+        m.reset()
+        m.prefill(prompt[:1024])
+        m.step(prompt[1024])
+        assert np.array_equal(m.logits().view(np.uint32), tail)
