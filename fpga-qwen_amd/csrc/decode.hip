@@ -9,13 +9,14 @@
 // FP64), epilogues fuse the residual add (626, 641), SwiGLU (636-639) and the
 // greedy argmax (engine/main.cpp:51-59).
 //
-// Attention: flash-decoding over position splits. Each workgroup owns one KV
-// head (both GQA query heads 2g, 2g+1 share every K/V row it loads) and a
-// contiguous range of positions; the last split to finish combines the
-// (max, sum, output) partials in fixed split order, so results do not depend
-// on scheduling. The workgroup holding the current position also applies
-// QK-norm + RoPE to k and writes K/V (FP16, round-to-nearest-even) into the
-// cache (engine/core.cpp:395-406) and uses them from LDS.
+// Attention: up to 512 cached positions, one kernel fuses attention with the
+// O projection (attn_o_kernel); beyond that, flash-decoding over splits of
+// 128 positions (attn_split_body) whose (max, sum, output) partials a small
+// merge kernel combines in fixed split order, so results do not depend on
+// scheduling. Each workgroup owns one KV head (both GQA query heads 2g, 2g+1
+// share every K/V row it loads); the one holding the current position also
+// applies QK-norm + RoPE to k and writes K/V (FP16, round-to-nearest-even)
+// into the cache (engine/core.cpp:395-406), and all use them from LDS.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -140,13 +141,11 @@ enum GemvMode { kPlain, kQKV, kO, kGateUp, kDown, kLmHead };
 
 struct GemvArgs {
     const uint16_t* w;        // chain-tiled weights
-    const float* in;          // input vector (plain/O/down), residual x (norm modes)
+    const float* in;          // input vector (plain; O: attention output; down), residual x (norm modes)
     const float* norm_w;      // RMSNorm weights (QKV, gate/up, lm_head)
     const uint16_t* embed;    // natural embedding, first layer only (QKV)
-    const float* in2;         // O: normalized attention output when splits == 1
     const float* parts;       // gate/up, down: pending [8][1024] O partials (fused attention), or null
     int token;                // first-layer QKV: embedding row
-    int splits;               // O: attention splits to merge (1: copy in2)
     float* out;               // plain/QKV: y; gate/up: activation; lm_head: logits
     float* x;                 // residual stream (O/down add, first-layer QKV store)
     float* hidden;            // lm_head: final normalized hidden
@@ -187,11 +186,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     } else if constexpr (MODE == kGateUp) {
 #pragma unroll
         for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
-    } else if constexpr (MODE == kO) {
-        if (a.splits == 1) {
-#pragma unroll
-            for (int k = 0; k < PER; ++k) v[k] = a.in2[tid + k * THREADS];
-        }
     } else {
 #pragma unroll
         for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
@@ -216,31 +210,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         for (int g = 0; g < kKVHeads; ++g) prow[g] = a.parts[g * kHidden + row];
     }
 
-    // O with several attention splits: the first round of partial outputs
-    // and all statistics (flash-decoding merge, fixed split order).
-    constexpr int R = 4;
-    constexpr int kOPer = MODE == kO ? PER : 1;
-    float po[kOPer][R], st_m[2], st_l[2];
-    auto part = [&](int head, int sp) {
-        return a.in + (size_t(head >> 1) * kAttnSplits + sp) * kAttnPartial + (head & 1) * 132;
-    };
-    if constexpr (MODE == kO) {
-        static_assert(THREADS == 128 && kQHeads * kAttnSplits == 2 * THREADS, "O prologue layout");
-        const int ns = a.splits;
-        if (ns > 1) {
-#pragma unroll
-            for (int k = 0; k < PER; ++k)  // output j = tid + 128 k belongs to head k
-#pragma unroll
-                for (int sp = 0; sp < R; ++sp) po[k][sp] = sp < ns ? part(k, sp)[tid] : 0.f;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {  // statistics: entry tid + 128 e = (head, split)
-                const int idx = tid + THREADS * e, sh = idx / kAttnSplits, ss = idx % kAttnSplits;
-                st_m[e] = ss < ns ? part(sh, ss)[128] : -INFINITY;
-                st_l[e] = ss < ns ? part(sh, ss)[129] : 0.f;
-            }
-        }
-    }
-
     // The scheduling barriers keep the weight loads after the prologue loads
     // and ahead of every instruction that waits for those.
     u32x4 wv[N / 64];
@@ -261,58 +230,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
             }
         }
         norm_to_lds<N, THREADS>(v, wn, xs, red, MODE == kLmHead && blockIdx.x == 0 ? a.hidden : nullptr);
-    } else if constexpr (MODE == kO) {
-      const int ns = a.splits;
-      if (ns == 1) {
-#pragma unroll
-        for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[k];
-      } else {
-        // o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max);
-        // splits beyond the first 4 follow in rounds of 4.
-        __shared__ float cw[kQHeads][kAttnSplits];
-        __shared__ float cl[kQHeads];
-        __shared__ float stat[kQHeads][kAttnSplits][2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int idx = tid + THREADS * e, sh = idx / kAttnSplits, ss = idx % kAttnSplits;
-            stat[sh][ss][0] = st_m[e];
-            stat[sh][ss][1] = st_l[e];
-        }
-        __syncthreads();
-        if (tid < kQHeads) {
-            float mx = -INFINITY;
-            for (int k = 0; k < ns; ++k) mx = fmaxf(mx, stat[tid][k][0]);
-            float l = 0.f;
-            for (int k = 0; k < ns; ++k) {
-                const float w = expf(stat[tid][k][0] - mx);
-                cw[tid][k] = w;
-                l += w * stat[tid][k][1];
-            }
-            cl[tid] = l;
-        }
-        __syncthreads();
-        float o[PER];
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            o[k] = 0.f;
-#pragma unroll
-            for (int sp = 0; sp < R; ++sp)
-                if (sp < ns) o[k] += cw[k][sp] * po[k][sp];
-        }
-        for (int s0 = R; s0 < ns; s0 += R) {
-#pragma unroll
-            for (int k = 0; k < PER; ++k)
-#pragma unroll
-                for (int sp = 0; sp < R; ++sp) po[k][sp] = s0 + sp < ns ? part(k, s0 + sp)[tid] : 0.f;
-#pragma unroll
-            for (int k = 0; k < PER; ++k)
-#pragma unroll
-                for (int sp = 0; sp < R; ++sp)
-                    if (s0 + sp < ns) o[k] += cw[k][s0 + sp] * po[k][sp];
-        }
-#pragma unroll
-        for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = o[k] / cl[k];
-      }
     } else {
 #pragma unroll
         for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[k];
@@ -475,63 +392,65 @@ __device__ __forceinline__ float head_norm_rope(float raw, float w, float cs, fl
 }
 
 // One workgroup = one KV head g (GQA query heads 2g, 2g+1) x one split of
-// positions, walked in tiles of 256 with an online softmax (running max and
-// sum rescaled per tile). 512 threads: scores use 8 threads per position
-// (64 positions per pass); P.V uses 4 waves per head, lane = 8-channel group
-// + position lane (16 position lanes). Writes the split's unnormalized
-// output, max and sum; the O projection's prologue (or attn_merge_kernel)
-// merges the splits.
+// up to kAttnTile = 128 positions (2 passes of 64), with the lane layout of
+// the fused kernel: the 8 lanes of position t score it (lane c = chain c of
+// the reference dot, engine/core.cpp:612) and multiply its V row by both
+// probabilities; each wave keeps its own softmax (max, sum, output) over its
+// positions, and the 8 waves are merged in LDS with weights exp(m_w - max).
+// A single split writes the normalized output; several write (output, max,
+// sum) partials that attn_merge_kernel combines. Every load is issued up
+// front and unconditionally (positions outside the split read row 0 and are
+// masked), in the order the phases need them.
 __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g) {
+    constexpr int kPasses = kAttnTile / 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = a.pos, n = pos + 1;
     int chunk, ns;
     attn_split(n, chunk, ns);
-    if (s >= ns) return;  // the grid covers exactly the active splits
+    if (s >= ns) return;  // the grid covers the largest split count of a batch
     const int t_begin = s * chunk, t_end = min(n, t_begin + chunk);
     const size_t head_base = size_t(g) * a.context;
-    const int quarter = tid >> 7, j = tid & 127, c = tid & 7;
-    const int hv = wave >> 2, cg = lane & 15, pl = ((wave & 3) << 2) | (lane >> 4);
+    const int quarter = tid >> 7, j = tid & 127, c = tid & 7, grp = tid >> 3;
+    const int vsub = lane >> 4, vcg = lane & 15;
 
-    u32x4 kreg[4][2];
-    u32x4 vreg[16];
-    auto load_tile = [&](int t0, int m) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int tl = p * 64 + (tid >> 3), t = t0 + tl;
-            if (tl < m && t != pos) key_pieces(a.keys + (head_base + t) * 128, c, kreg[p][0], kreg[p][1]);
-        }
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int tl = pl + 16 * k, t = t0 + tl;
-            if (tl < m && t != pos)
-                vreg[k] = *reinterpret_cast<const u32x4*>(a.values + (head_base + t) * 128 + cg * 8);
-        }
-    };
-    // Raw q/k/v and the first tile's cached K/V rows are loaded first.
     const float raw = quarter < 2 ? a.qkv[(2 * g + quarter) * 128 + j] : a.qkv[2048 + g * 128 + j];
     const float raw_v = a.qkv[3072 + g * 128 + j];
     // quarter is uniform per wave; selecting the pointer on a scalar keeps it
     // out of vector registers (no per-lane load of the kernel argument).
     const float nw = (__builtin_amdgcn_readfirstlane(quarter) < 2 ? a.q_norm : a.k_norm)[j];
     const float rc = a.cosines[size_t(pos) * 64 + (j & 63)], rs = a.sines[size_t(pos) * 64 + (j & 63)];
+    u32x4 kreg[kPasses][2], vreg[kPasses][2];
     __builtin_amdgcn_sched_barrier(0);
-    load_tile(t_begin, min(kAttnTile, t_end - t_begin));
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        const int t = t_begin + p * 64 + grp;
+        const int tl = t < t_end && t != pos ? t : 0;
+        key_pieces(a.keys + (head_base + tl) * 128, c, kreg[p][0], kreg[p][1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int t = t_begin + p * 64 + 8 * wave + 4 * hf + vsub;
+            const int tl = t < t_end && t != pos ? t : 0;
+            vreg[p][hf] = reinterpret_cast<const u32x4*>(a.values + (head_base + tl) * 128)[vcg];
+        }
     __builtin_amdgcn_sched_barrier(0);
 
     __shared__ float qp[2][128];
     __shared__ float buf[4][128];
-    __shared__ float sc[2][kAttnTile];
-    __shared__ float opart[4][2][128];
+    __shared__ float prob[2][kAttnTile];
+    __shared__ float opart[8][4][2][128];
     __shared__ uint16_t kcur[128], vcur[128];
     __shared__ double red[4][2];
-    __shared__ float redm[8], reds[8];
-    __shared__ float run_max[2], run_sum[2], run_scale[2];
+    __shared__ float wmax[8][2], wsum[8][2];
 
-    // QK-norm + RoPE: quarters 0-1 the two q heads, quarters 2-3 both the k
-    // head (same barriers for every wave); quarter 2 keeps k, quarter 3 v.
+    // QK-norm + RoPE (engine/core.cpp:395-402); the split holding pos writes
+    // the new K/V row (403-406) and every split reads only rows t != pos.
     {
         const float r = head_norm_rope(raw, nw, rc, rs, red[quarter], buf[quarter], j);
-        const bool owner = t_end == n;
+        const bool owner = s == ns - 1;
         if (quarter < 2) {
             qp[quarter][kperm(j)] = r;
         } else if (quarter == 2) {
@@ -543,116 +462,117 @@ __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g)
             vcur[j] = bits;
             if (owner) a.values[(head_base + pos) * 128 + j] = bits;
         }
-        if (tid < 2) {
-            run_max[tid] = -INFINITY;
-            run_sum[tid] = 0.f;
-        }
     }
     __syncthreads();
 
-    float acc[8];
+    float s0[kPasses], s1[kPasses];
+    float m0 = -INFINITY, m1 = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    for (int p = 0; p < kPasses; ++p) {
+        const int t = t_begin + p * 64 + grp;
+        uint32_t kw[8];
+        if (t == pos) {
+            key_pieces_lds(kcur, c, kw);
+        } else {
+            kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
+            kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+        }
+        const float d0 = combine_chains(key_chain(qp[0], c, kw, 0.f)) * a.scale;
+        const float d1 = combine_chains(key_chain(qp[1], c, kw, 0.f)) * a.scale;
+        s0[p] = t < t_end ? d0 : -INFINITY;
+        s1[p] = t < t_end ? d1 : -INFINITY;
+        m0 = fmaxf(m0, s0[p]);
+        m1 = fmaxf(m1, s1[p]);
+    }
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        m0 = fmaxf(m0, __shfl_xor(m0, off));
+        m1 = fmaxf(m1, __shfl_xor(m1, off));
+    }
+    float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        const int t = t_begin + p * 64 + grp;
+        const float p0 = t < t_end ? expf(s0[p] - m0) : 0.f;
+        const float p1 = t < t_end ? expf(s1[p] - m1) : 0.f;
+        l0 += p0;
+        l1 += p1;
+        if (c == 0) {
+            prob[0][p * 64 + grp] = p0;
+            prob[1][p * 64 + grp] = p1;
+        }
+    }
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        l0 += __shfl_xor(l0, off);
+        l1 += __shfl_xor(l1, off);
+    }
+    // prob[][] of this wave's positions is written and read by this wave only.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    for (int t0 = t_begin; t0 < t_end; t0 += kAttnTile) {
-        const int m = min(kAttnTile, t_end - t0);
-        if (t0 != t_begin) load_tile(t0, m);
-        // Scores in the reference dot's chain order (engine/core.cpp:612).
+    float acc[2][8];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int base = p * 64;
-            if (base >= m) break;  // block-uniform
-            const int tl = base + (tid >> 3), t = t0 + tl;
-            float acc0 = 0.f, acc1 = 0.f;
-            if (tl < m) {
-                uint32_t kw[8];
+    for (int i = 0; i < 8; ++i) acc[0][i] = acc[1][i] = 0.f;
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int tl = p * 64 + 8 * wave + 4 * hf + vsub, t = t_begin + tl;
+            if (t < t_end) {
+                const float p0 = prob[0][tl], p1 = prob[1][tl];
+                uint32_t vw[4];
                 if (t == pos) {
-                    key_pieces_lds(kcur, c, kw);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        vw[i] = uint32_t(vcur[vcg * 8 + 2 * i]) | (uint32_t(vcur[vcg * 8 + 2 * i + 1]) << 16);
                 } else {
-                    kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
-                    kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+                    vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
                 }
-                acc0 = key_chain(qp[0], c, kw, acc0);
-                acc1 = key_chain(qp[1], c, kw, acc1);
-            }
-            const float d0 = combine_chains(acc0), d1 = combine_chains(acc1);
-            if (c == 0 && tl < m) {
-                sc[0][tl] = d0 * a.scale;
-                sc[1][tl] = d1 * a.scale;
-            }
-        }
-        __syncthreads();
-        {  // online softmax: threads 0-255 head 0, 256-511 head 1
-            const int h = tid >> 8, i = tid & 255;
-            const float v = i < m ? sc[h][i] : -INFINITY;
-            const float mx = wave_max(v);
-            if (lane == 0) redm[wave] = mx;
-            __syncthreads();
-            const float tile_max = fmaxf(fmaxf(redm[4 * h], redm[4 * h + 1]), fmaxf(redm[4 * h + 2], redm[4 * h + 3]));
-            const float old_max = run_max[h];
-            const float new_max = fmaxf(old_max, tile_max);
-            const float p = i < m ? expf(v - new_max) : 0.f;
-            if (i < m) sc[h][i] = p;
-            const float sm = wave_sum(p);
-            if (lane == 0) reds[wave] = sm;
-            __syncthreads();
-            if (i == 0) {
-                const float scale = old_max == -INFINITY ? 0.f : expf(old_max - new_max);
-                run_scale[h] = scale;
-                run_sum[h] = run_sum[h] * scale + ((reds[4 * h] + reds[4 * h + 1]) + (reds[4 * h + 2] + reds[4 * h + 3]));
-                run_max[h] = new_max;
-            }
-            __syncthreads();
-        }
-        {  // unnormalized P.V, rescaled by the change of running max
-            const float scale = run_scale[hv];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] *= scale;
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int tl = pl + 16 * k, t = t0 + tl;
-                if (tl < m) {
-                    const float p = sc[hv][tl];
-                    uint32_t vw[4];
-                    if (t == pos) {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            vw[i] = uint32_t(vcur[cg * 8 + 2 * i]) | (uint32_t(vcur[cg * 8 + 2 * i + 1]) << 16);
-                    } else {
-                        vw[0] = vreg[k].x; vw[1] = vreg[k].y; vw[2] = vreg[k].z; vw[3] = vreg[k].w;
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        acc[2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p, acc[2 * i]);
-                        acc[2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p, acc[2 * i + 1]);
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
+                    acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
+                    acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
+                    acc[1][2 * i] = __builtin_fmaf(v0, p1, acc[1][2 * i]);
+                    acc[1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[1][2 * i + 1]);
                 }
             }
         }
-        __syncthreads();  // sc is rewritten by the next tile
-    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        acc[i] += __shfl_xor(acc[i], 16);
-        acc[i] += __shfl_xor(acc[i], 32);
-    }
-    if (lane < 16) {
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) opart[wave & 3][hv][cg * 8 + i] = acc[i];
+        for (int i = 0; i < 8; ++i) opart[wave][vsub][h][vcg * 8 + i] = acc[h][i];
+    if (lane == 0) {
+        wmax[wave][0] = m0;
+        wmax[wave][1] = m1;
+        wsum[wave][0] = l0;
+        wsum[wave][1] = l1;
     }
     __syncthreads();
     if (tid < 256) {
         const int h = tid >> 7;
-        const float o = (opart[0][h][j] + opart[1][h][j]) + (opart[2][h][j] + opart[3][h][j]);
+        float mx = wmax[0][h];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w][h]);
+        float l = 0.f, o = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const float e = wmax[w][h] == -INFINITY ? 0.f : expf(wmax[w][h] - mx);
+            const float ow4 = (opart[w][0][h][j] + opart[w][1][h][j]) + (opart[w][2][h][j] + opart[w][3][h][j]);
+            l = __builtin_fmaf(e, wsum[w][h], l);
+            o = __builtin_fmaf(e, ow4, o);
+        }
         if (ns == 1) {  // nothing to merge: normalize here
-            a.attended[(2 * g + h) * 128 + j] = o / run_sum[h];
+            a.attended[(2 * g + h) * 128 + j] = o / l;
             return;
         }
         float* part = a.partial + (size_t(g) * kAttnSplits + s) * kAttnPartial + h * 132;
         part[j] = o;
         if (j == 0) {
-            part[128] = run_max[h];
-            part[129] = run_sum[h];
+            part[128] = mx;
+            part[129] = l;
         }
     }
 }
@@ -671,26 +591,44 @@ __global__ __launch_bounds__(512) void attn_decode_batch_kernel(const AttnBatch 
     attn_split_body(b.seq[blockIdx.z], blockIdx.x, blockIdx.y);
 }
 
-// Merge of the position splits of one (sequence, query head), in the same
-// order and arithmetic as the O projection's prologue: o = sum_s w_s o_s /
-// sum_s w_s l_s with w_s = exp(m_s - max_s m_s). One split: attention already
-// wrote the normalized output.
-__global__ __launch_bounds__(128) void attn_merge_batch_kernel(const AttnBatch b) {
-    const AttnArgs& a = b.seq[blockIdx.y];
-    const int head = blockIdx.x, j = threadIdx.x;
+// Merge of the position splits of one query head (flash-decoding, fixed
+// split order): o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max).
+// One split: attention already wrote the normalized output.
+// All partials are loaded up front (entries past ns read split 0 and are
+// skipped), so the merge costs one memory round trip.
+__device__ __forceinline__ void attn_merge_body(const AttnArgs& a, int head) {
+    const int j = threadIdx.x;
     int chunk, ns;
     attn_split(a.pos + 1, chunk, ns);
     if (ns == 1) return;
     const float* base = a.partial + size_t(head >> 1) * kAttnSplits * kAttnPartial + (head & 1) * 132;
-    float mx = -INFINITY;
-    for (int k = 0; k < ns; ++k) mx = fmaxf(mx, base[k * kAttnPartial + 128]);
-    float l = 0.f, o = 0.f;
-    for (int k = 0; k < ns; ++k) {
-        const float w = expf(base[k * kAttnPartial + 128] - mx);
-        l += w * base[k * kAttnPartial + 129];
-        o += w * base[k * kAttnPartial + j];
+    float mv[kAttnSplits], lv[kAttnSplits], ov[kAttnSplits];
+#pragma unroll
+    for (int k = 0; k < kAttnSplits; ++k) {
+        const float* e = base + (k < ns ? k : 0) * kAttnPartial;
+        mv[k] = e[128];
+        lv[k] = e[129];
+        ov[k] = e[j];
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kAttnSplits; ++k)
+        if (k < ns) mx = fmaxf(mx, mv[k]);
+    float l = 0.f, o = 0.f;
+#pragma unroll
+    for (int k = 0; k < kAttnSplits; ++k)
+        if (k < ns) {
+            const float w = expf(mv[k] - mx);
+            l += w * lv[k];
+            o += w * ov[k];
+        }
     a.attended[head * 128 + j] = o / l;
+}
+
+__global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) { attn_merge_body(a, blockIdx.x); }
+
+__global__ __launch_bounds__(128) void attn_merge_batch_kernel(const AttnBatch b) {
+    attn_merge_body(b.seq[blockIdx.y], blockIdx.x);
 }
 
 // Fused attention + O projection for n <= kFusedMaxPositions. Workgroup
@@ -927,8 +865,7 @@ __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* 
     *reinterpret_cast<u32x4*>(dst + idx * 8) = out;
 }
 
-// Waves (8-row tiles) per workgroup of each layer GEMV. The O projection's
-// split-merge prologue is laid out for exactly 2 waves.
+// Waves (8-row tiles) per workgroup of each layer GEMV (measured best).
 constexpr int kLayerWaves = 2;
 template <int MODE>
 constexpr int gemv_waves() {
@@ -1023,19 +960,14 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             int chunk, splits;
             attn_split(pos + 1, chunk, splits);
             attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(at);
+            if (splits > 1) attn_merge_kernel<<<kQHeads, 128, 0, stream>>>(at);
             break;
         }
         case 2: {
             if (attn_fused(pos + 1)) break;  // O is part of the attention kernel
             GemvArgs o{};
             o.w = L.o_t;
-            o.in = s.attn_partial;
-            o.in2 = s.attended;
-            {
-                int chunk, splits;
-                attn_split(pos + 1, chunk, splits);
-                o.splits = splits;
-            }
+            o.in = s.attended;
             o.x = s.x;
             launch_gemv<kQDim, kO>(o, kHidden, stream);
             break;

@@ -34,12 +34,12 @@ struct ArgmaxResult {
     int nonfinite;
 };
 
-inline constexpr int kAttnSplits = 16;          // max position splits per KV head
-inline constexpr int kAttnTile = 256;           // positions per split (one online-softmax tile)
+inline constexpr int kAttnSplits = 32;          // max position splits per KV head
+inline constexpr int kAttnTile = 128;           // positions per split
 inline constexpr int kAttnPartial = 2 * 132;    // per split: 2 heads x (128 o + m + l + pad)
 
 // Position splitting of decode attention over n = pos + 1 cached positions:
-// one 256-position tile per split, up to 16 splits for a 4096 context.
+// 128 positions per split, up to 32 splits for a 4096 context.
 __host__ __device__ inline void attn_split(int n, int& chunk, int& splits) {
     chunk = kAttnTile;
     splits = (n + kAttnTile - 1) / kAttnTile;

@@ -3,8 +3,8 @@
 Up to 512 cached positions decode attention runs fused with the O
 projection (one workgroup per KV head and block of O rows, partial
 projections folded into the residual stream by the next kernels); beyond
-that it splits the positions into up to 16 chunks of 256 whose partial
-softmax statistics are merged in the O projection's prologue. These tests
+that it splits the positions into up to 32 chunks of 128 whose partial
+softmax statistics a merge kernel combines before the O projection. These tests
 cover the switch between the two paths, many splits and the 512-row prefill
 chunk boundaries against the oracle's sequential softmax
 (engine/core.cpp:606-624), teacher-forced like tools/check_native_logits.py,
