@@ -33,71 +33,102 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-constexpr int kTileM = 64, kTileN = 64, kTileK = 64;
+// C[M x N] (+)= A[M x K] . W[N x K]^T on the matrix cores. Workgroup tile TM
+// x 128 (TM = 64 or 32), K in steps of 64; 4 waves, each owning 32 rows x
+// (64 or 32) columns of C as 32x32 MFMA tiles. A (FP32) enters LDS as
+// FP16 hi = fp16(a) and lo = fp16(a - hi), W as its FP16 values; every
+// product runs twice (hi, lo), so products are exact and sums FP32. The next
+// K step's global loads are issued before the current step's MFMAs. Each
+// output element accumulates its K terms in the same order whatever TM and
+// its row position, so results do not depend on M or on how rows are grouped.
+constexpr int kTileN = 128, kTileK = 64;
 constexpr int kLdsRow = kTileK + 8;  // halves per LDS row (padding against bank conflicts)
 
 // Epilogue: 0 store, 1 add into C (residual).
-template <int EPI>
+template <int TM, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, const uint16_t* __restrict__ W,
                                                    float* __restrict__ C, int M, int N, int K) {
-    __shared__ _Float16 a_hi[kTileM][kLdsRow];
-    __shared__ _Float16 a_lo[kTileM][kLdsRow];
-    __shared__ _Float16 b_s[kTileN][kLdsRow];
+    static_assert(TM == 64 || TM == 32, "tile height");
+    constexpr int kWaveRows = TM / 32, kWaveCols = 4 / kWaveRows;  // wave grid
+    constexpr int kColTiles = kTileN / kWaveCols / 32;              // 32-column MFMA tiles per wave
+    constexpr int kAThreadsPerRow = 256 / TM;   // threads loading one A row of the K step
+    constexpr int kAF4 = kTileK / 4 / kAThreadsPerRow;  // float4 loads per thread
+    __shared__ __align__(16) _Float16 a_hi[TM][kLdsRow];
+    __shared__ __align__(16) _Float16 a_lo[TM][kLdsRow];
+    __shared__ __align__(16) _Float16 b_s[kTileN][kLdsRow];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
-    const int wm = wave & 1, wn = wave >> 1;
-    // Tile loads: thread -> (row, 16 consecutive k).
-    const int lr = tid >> 2, lk = (tid & 3) * 16;
-    const bool a_ok = m0 + lr < M;
-    const float* a_row = A + size_t(m0 + lr) * K + lk;
-    const uint16_t* b_row = W + size_t(n0 + lr) * K + lk;
-    floatx16 acc;
+    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * kTileN;
+    const int wm = wave % kWaveRows, wn = wave / kWaveRows;
+    // Global loads: A row ar (rows past M repeat row M - 1 and are not
+    // stored), 4 * kAF4 consecutive k; W row br, 32 consecutive k.
+    const int ar = tid / kAThreadsPerRow, ak = (tid % kAThreadsPerRow) * 4 * kAF4;
+    const int br = tid >> 1, bk = (tid & 1) * 32;
+    const float* a_row = A + size_t(min(m0 + ar, M - 1)) * K + ak;
+    const uint16_t* b_row = W + size_t(n0 + br) * K + bk;
+    float4 av[kAF4];
+    u32x4 bv[4];
+    auto load = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        for (int i = 0; i < kAF4; ++i) av[i] = reinterpret_cast<const float4*>(a_row + k0)[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bv[i] = reinterpret_cast<const u32x4*>(b_row + k0)[i];
+    };
+    floatx16 acc[kColTiles];
+#pragma unroll
+    for (int jt = 0; jt < kColTiles; ++jt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[jt][r] = 0.f;
 
+    load(0);
+    const int fr = lane & 31, fk = (lane >> 5) * 8;
     for (int k0 = 0; k0 < K; k0 += kTileK) {
-        float4 av[4];
+        __syncthreads();  // the previous step's fragments are consumed
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            av[i] = a_ok ? reinterpret_cast<const float4*>(a_row + k0)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const u32x4 bv0 = reinterpret_cast<const u32x4*>(b_row + k0)[0];
-        const u32x4 bv1 = reinterpret_cast<const u32x4*>(b_row + k0)[1];
-        __syncthreads();  // previous tile fully consumed
+        for (int i = 0; i < kAF4; i += 2) {  // 8 values -> one 16-byte store per plane
+            const float v[8] = {av[i].x, av[i].y, av[i].z, av[i].w, av[i + 1].x, av[i + 1].y, av[i + 1].z, av[i + 1].w};
+            half8 hi8, lo8;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float v[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int e = 0; e < 8; ++e) {
                 const _Float16 hi = static_cast<_Float16>(v[e]);
-                const _Float16 lo = static_cast<_Float16>(v[e] - static_cast<float>(hi));
-                a_hi[lr][lk + 4 * i + e] = hi;
-                a_lo[lr][lk + 4 * i + e] = lo;
+                hi8[e] = hi;
+                lo8[e] = static_cast<_Float16>(v[e] - static_cast<float>(hi));
             }
+            *reinterpret_cast<half8*>(&a_hi[ar][ak + 4 * i]) = hi8;
+            *reinterpret_cast<half8*>(&a_lo[ar][ak + 4 * i]) = lo8;
         }
-        *reinterpret_cast<u32x4*>(&b_s[lr][lk]) = bv0;
-        *reinterpret_cast<u32x4*>(&b_s[lr][lk + 8]) = bv1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&b_s[br][bk + 8 * i]) = bv[i];
         __syncthreads();
-        const int fr = lane & 31, fk = (lane >> 5) * 8;
+        if (k0 + kTileK < K) load(k0 + kTileK);
 #pragma unroll
         for (int ks = 0; ks < kTileK; ks += 16) {
             const half8 ah = *reinterpret_cast<const half8*>(&a_hi[wm * 32 + fr][ks + fk]);
             const half8 al = *reinterpret_cast<const half8*>(&a_lo[wm * 32 + fr][ks + fk]);
-            const half8 bb = *reinterpret_cast<const half8*>(&b_s[wn * 32 + fr][ks + fk]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bb, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bb, acc, 0, 0, 0);
+            half8 bb[kColTiles];
+#pragma unroll
+            for (int jt = 0; jt < kColTiles; ++jt)
+                bb[jt] = *reinterpret_cast<const half8*>(&b_s[wn * 32 * kColTiles + 32 * jt + fr][ks + fk]);
+#pragma unroll
+            for (int jt = 0; jt < kColTiles; ++jt) {
+                acc[jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bb[jt], acc[jt], 0, 0, 0);
+                acc[jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bb[jt], acc[jt], 0, 0, 0);
+            }
         }
     }
     // D layout: lane -> column (lane & 31); register r -> row 8(r/4) + 4(lane/32) + r%4.
-    const int n = n0 + wn * 32 + (lane & 31);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < M) {
-            float* c = C + size_t(m) * N + n;
-            if constexpr (EPI == 1)
-                *c = *c + acc[r];
-            else
-                *c = acc[r];
+    for (int jt = 0; jt < kColTiles; ++jt) {
+        const int n = n0 + wn * 32 * kColTiles + 32 * jt + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < M) {
+                float* c = C + size_t(m) * N + n;
+                if constexpr (EPI == 1)
+                    *c = *c + acc[jt][r];
+                else
+                    *c = acc[jt][r];
+            }
         }
     }
 }
@@ -378,10 +409,14 @@ __global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restric
     act[idx] = gate * (0.5f + 0.5f * t) * up;
 }
 
+// 64-row tiles when they give every CU a workgroup, else 32-row tiles.
 template <int EPI>
 void gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, hipStream_t stream) {
     require(N % kTileN == 0 && K % kTileK == 0 && M > 0, "gemm: unsupported shape");
-    gemm_kernel<EPI><<<dim3(N / kTileN, (M + kTileM - 1) / kTileM), 256, 0, stream>>>(A, W, C, M, N, K);
+    if ((M + 63) / 64 * (N / kTileN) >= 256)
+        gemm_kernel<64, EPI><<<dim3(N / kTileN, (M + 63) / 64), 256, 0, stream>>>(A, W, C, M, N, K);
+    else
+        gemm_kernel<32, EPI><<<dim3(N / kTileN, (M + 31) / 32), 256, 0, stream>>>(A, W, C, M, N, K);
 }
 
 }  // namespace

@@ -22,7 +22,7 @@ PROMPTS = json.loads((Path(__file__).parent / 'golden' / 'prompts.json').read_te
 
 @pytest.mark.gpu
 @pytest.mark.parametrize('m,n,k', [(1, 1024, 1024), (37, 4096, 1024), (85, 1024, 2048), (512, 6144, 1024),
-                                   (129, 1024, 3072)])
+                                   (129, 1024, 3072), (1000, 4096, 1024), (1100, 6144, 1024)])
 def test_gemm_against_fp64(qpkg, m, n, k):
     rng = np.random.default_rng(21)
     a = rng.standard_normal((m, k), dtype=np.float32) * 3
@@ -39,11 +39,14 @@ def test_gemm_against_fp64(qpkg, m, n, k):
 
 @pytest.mark.gpu
 def test_gemm_rows_independent_of_chunk(qpkg):
+    """Row results do not depend on M, on the row's position in a tile or on
+    the tile height chosen for the launch (128-row tiles for 1200 x 4096,
+    64-row tiles for the smaller calls)."""
     rng = np.random.default_rng(22)
-    a = rng.standard_normal((512, 1024), dtype=np.float32)
-    w = (rng.standard_normal((1024, 1024), dtype=np.float32) * 0.02).astype(np.float16)
+    a = rng.standard_normal((1200, 1024), dtype=np.float32)
+    w = (rng.standard_normal((4096, 1024), dtype=np.float32) * 0.02).astype(np.float16)
     full = qpkg.gemm(a, w)
-    for rows in (slice(0, 37), slice(100, 101), slice(300, 512)):
+    for rows in (slice(0, 37), slice(100, 101), slice(300, 512), slice(1100, 1200)):
         part = qpkg.gemm(a[rows], w)
         assert np.array_equal(part.view(np.uint32), full[rows].view(np.uint32))
 
