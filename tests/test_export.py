@@ -1,0 +1,196 @@
+"""Checkpoint -> QWCPU01 pack export (the counterpart of the reference's
+tools/export_native_cpu_weights.py; format engine/INTERFACE.md:6-21).
+
+No Qwen3 checkpoint exists in this environment, so the known answer that
+needs one (`prefill 9707` -> 21806, tools/check_native_cpu_interface.py:50-62)
+stays out of reach; these tests pin the conversion and every validation on
+synthetic BF16 safetensors files instead, and check that a full-shape export
+passes the engine's own pack validator.
+"""
+import importlib.util
+import json
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+spec = importlib.util.spec_from_file_location('export_pack', ROOT / 'fpga-qwen_amd' / 'export_pack.py')
+export_pack = importlib.util.module_from_spec(spec)
+spec.loader.exec_module(export_pack)
+
+SMALL = {'model.embed_tokens.weight': (8, 4), 'model.norm.weight': (4,),
+         'model.layers.0.a.weight': (3, 4), 'model.layers.0.n.weight': (2,)}
+
+
+def bf16(values):
+    """Exact BF16 bit patterns of float32 values that are BF16-representable."""
+    bits = np.asarray(values, np.float32).view(np.uint32)
+    assert np.all(bits & 0xffff == 0)
+    return (bits >> 16).astype('<u2')
+
+
+def write_checkpoint(path, tensors, order=None, tail=b''):
+    """tensors: name -> BF16 uint16 array (with its shape). Writes a
+    safetensors file with regions in `order` (default: insertion order)."""
+    names = order or list(tensors)
+    header, blobs, cursor = {}, [], 0
+    for name in names:
+        data = tensors[name].astype('<u2').tobytes()
+        header[name] = dict(dtype='BF16', shape=list(tensors[name].shape), data_offsets=[cursor, cursor + len(data)])
+        blobs.append(data)
+        cursor += len(data)
+    raw = json.dumps(header).encode()
+    path.write_bytes(struct.pack('<Q', len(raw)) + raw + b''.join(blobs) + tail)
+    return path
+
+
+def small_tensors(rng):
+    out = {}
+    for name, shape in SMALL.items():
+        wide = rng.standard_normal(shape).astype(np.float32)
+        out[name] = bf16((wide.view(np.uint32) & 0xffff0000).view(np.float32)).reshape(shape)
+    out['lm_head.weight'] = out['model.embed_tokens.weight'].copy()
+    return out
+
+
+def test_small_export_layout_and_values(tmp_path):
+    rng = np.random.default_rng(5)
+    t = small_tensors(rng)
+    # BF16 keeps fewer significand bits than FP16, so rounding happens only
+    # below FP16's normal range: ties at half the subnormal step go to even
+    # (2^-25 -> 0, 3*2^-25 -> 2*2^-24, 5*2^-25 -> 2*2^-24); also the largest
+    # BF16 value under FP16's maximum (65280), -0 and normal values.
+    special = np.array([2.0 ** -25, 3 * 2.0 ** -25, 5 * 2.0 ** -25, 2.0 ** -24, 65280.0, -0.0, 0.5, -3.0,
+                        2.0 ** -14, 1.0, 2.0, 4.0], np.float32)
+    t['model.layers.0.a.weight'] = bf16(special).reshape(3, 4)
+    ckpt = write_checkpoint(tmp_path / 'model.safetensors', t, order=list(reversed(list(t))))
+    manifest = export_pack.export(tmp_path, tmp_path / 'out' / 'weights.bin', shapes=SMALL)
+    pack = (tmp_path / 'out' / 'weights.bin').read_bytes()
+    assert pack[:64] == b'QWCPU01' + bytes(57)
+    lines = (tmp_path / 'out' / 'weights.bin.index').read_text().splitlines()
+    assert lines[0] == 'QWCPU01 4'
+    meta = json.loads(manifest.read_text())
+    assert meta['format'] == 'QWCPU01' and meta['completed'] is True and meta['tensor_count'] == 4
+    assert meta['tied_lm_head_verified'] is True
+    for line, (name, shape) in zip(lines[1:], SMALL.items()):
+        n, dtype, rows, cols, off, length = line.split()
+        assert n == name and int(off) % 64 == 0
+        wide = (t[name].astype(np.uint32) << 16).view(np.float32).reshape(-1)
+        if len(shape) == 2:
+            assert dtype == 'F16' and (int(rows), int(cols)) == shape
+            got = np.frombuffer(pack[int(off):int(off) + int(length)], '<f2')
+            assert np.array_equal(got.view(np.uint16), wide.astype(np.float16).view(np.uint16))
+        else:
+            assert dtype == 'F32' and (int(rows), int(cols)) == (shape[0], 1)
+            got = np.frombuffer(pack[int(off):int(off) + int(length)], '<f4')
+            assert np.array_equal(got.view(np.uint32), wide.view(np.uint32))
+    off = int(lines[3].split()[4])
+    got = np.frombuffer(pack[off:off + 24], '<u2')
+    expected = [0x0000, 0x0002, 0x0002, 0x0001, 0x7BF8, 0x8000, 0x3800, 0xC200, 0x0400, 0x3C00, 0x4000, 0x4400]
+    assert got.tolist() == expected
+    # Outputs are immutable.
+    with pytest.raises(FileExistsError):
+        export_pack.export(ckpt, tmp_path / 'out' / 'weights.bin', shapes=SMALL)
+
+
+@pytest.mark.parametrize('case, message', [
+    ('missing', 'exactly the expected'),
+    ('extra', 'exactly the expected'),
+    ('dtype', 'dtype/shape'),
+    ('shape', 'dtype/shape'),
+    ('hole', 'overlap, contain holes'),
+    ('tail', 'overlap, contain holes'),
+    ('overlap', 'bounds/length|overlap'),
+    ('untied', 'not bit-identical'),
+    ('nan', 'Nonfinite'),
+    ('overflow', 'FP16 overflow'),
+    ('duplicate', 'Duplicate JSON key'),
+])
+def test_rejections(tmp_path, case, message):
+    rng = np.random.default_rng(6)
+    t = small_tensors(rng)
+    kwargs = {}
+    path = tmp_path / 'model.safetensors'
+    if case == 'missing':
+        del t['model.norm.weight']
+    elif case == 'extra':
+        t['model.extra.weight'] = bf16(np.ones(2, np.float32))
+    elif case == 'untied':
+        t['lm_head.weight'] = t['lm_head.weight'].copy()
+        t['lm_head.weight'][0, 0] ^= 1
+    elif case == 'nan':
+        t['model.norm.weight'][1] = 0x7FC0
+    elif case == 'overflow':
+        t['model.layers.0.a.weight'][0, 0] = 0x4789  # 70144: beyond FP16's range
+    elif case == 'tail':
+        kwargs['tail'] = b'\0\0'
+    if case in ('dtype', 'shape', 'hole', 'overlap', 'duplicate'):
+        write_checkpoint(path, t)
+        n = struct.unpack('<Q', path.read_bytes()[:8])[0]
+        header = json.loads(path.read_bytes()[8:8 + n])
+        data = path.read_bytes()[8 + n:]
+        if case == 'dtype':
+            header['model.norm.weight']['dtype'] = 'F32'
+        elif case == 'shape':
+            header['model.layers.0.a.weight']['shape'] = [4, 3]
+        elif case == 'hole':
+            for name in header:
+                b, e = header[name]['data_offsets']
+                header[name]['data_offsets'] = [b + 2, e + 2]
+            data = b'\0\0' + data
+        elif case == 'overlap':
+            b, e = header['model.norm.weight']['data_offsets']
+            header['model.norm.weight']['data_offsets'] = [b - 2, e - 2]
+        raw = json.dumps(header).encode()
+        if case == 'duplicate':
+            raw = raw[:-1] + b', "model.norm.weight": {"dtype": "BF16", "shape": [4], "data_offsets": [0, 8]}}'
+        path.write_bytes(struct.pack('<Q', len(raw)) + raw + data)
+    else:
+        write_checkpoint(path, t, **kwargs)
+    with pytest.raises(ValueError, match=message):
+        export_pack.export(path, tmp_path / 'out' / 'weights.bin', shapes=SMALL)
+    assert not (tmp_path / 'out' / 'weights.bin').exists()
+
+
+def test_full_shape_export_passes_engine_validation(tmp_path, qpkg):
+    """A synthetic BF16 checkpoint with the exact Qwen3-0.6B tensor set: the
+    exported pack must pass the engine's validator (on a host without a GPU
+    the constructor then stops at the device check)."""
+    shapes = export_pack.pack_shapes()
+    rng = np.random.default_rng(7)
+    wide = rng.standard_normal(1 << 19).astype(np.float32) * 0.02
+    pattern = bf16((wide.view(np.uint32) & 0xffff0000).view(np.float32))
+    ones = bf16(np.ones(1, np.float32))[0]
+    names = list(shapes) + ['lm_head.weight']
+    header, cursor = {}, 0
+    for name in names:
+        shape = shapes['model.embed_tokens.weight'] if name == 'lm_head.weight' else shapes[name]
+        size = 2 * int(np.prod(shape))
+        header[name] = dict(dtype='BF16', shape=list(shape), data_offsets=[cursor, cursor + size])
+        cursor += size
+    raw = json.dumps(header).encode()
+    path = tmp_path / 'model.safetensors'
+    with path.open('wb') as f:
+        f.write(struct.pack('<Q', len(raw)) + raw)
+        for name in names:
+            shape = shapes['model.embed_tokens.weight'] if name == 'lm_head.weight' else shapes[name]
+            count = int(np.prod(shape))
+            if len(shape) == 1:
+                f.write(np.full(count, ones, '<u2').tobytes())
+                continue
+            reps = -(-count // pattern.size)
+            f.write(np.tile(pattern, reps)[:count].tobytes())
+    out = tmp_path / 'pack' / 'weights.bin'
+    export_pack.export(path, out)
+    index = out.with_name('weights.bin.index').read_text().splitlines()
+    assert index[0] == 'QWCPU01 310' and len(index) == 311
+    try:
+        model = qpkg.Model(out, context=64)
+    except RuntimeError as error:
+        assert 'No HIP device available' in str(error), error
+    else:
+        with model:
+            model.prefill([9707])
+            assert model.logits().size == 151936
