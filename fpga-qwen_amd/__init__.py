@@ -52,6 +52,7 @@ SIGNATURES = {
     'qwen_gpu_get_options': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Options)]),
     'qwen_gpu_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
     'qwen_gpu_verify_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_int_p]),
+    'qwen_gpu_verify_two_greedy': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_int_p, _c_int_p]),
     'qwen_gpu_write_random_pack': (ctypes.c_int, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_double, ctypes.c_int]),
     'qwen_gpu_device_malloc': (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
     'qwen_gpu_device_free': (ctypes.c_int, [ctypes.c_void_p]),
@@ -206,6 +207,13 @@ class Model:
     def verify_greedy(self):
         a, b = ctypes.c_int(), ctypes.c_int()
         _check(_LIB.qwen_gpu_verify_greedy(self._handle, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
+
+    def verify_two_greedy(self, first, second):
+        """verify_two + verify_greedy without copying the rows to the host."""
+        a, b = ctypes.c_int(), ctypes.c_int()
+        _check(_LIB.qwen_gpu_verify_two_greedy(self._handle, int(first), int(second), ctypes.byref(a),
+                                               ctypes.byref(b)))
         return a.value, b.value
 
     def time_kernel(self, which, iterations):

@@ -130,7 +130,18 @@ int qwen_gpu_verify_two(qwen_gpu_model* m, int first, int second, const float** 
         need(logits, "logits");
         need(hidden, "hidden");
         need(base_position, "base_position");
-        m->engine.verify_two(first, second, logits, hidden, base_position);
+        m->engine.verify_two(first, second);
+        m->engine.verification_rows(logits, hidden, base_position);
+    });
+}
+
+int qwen_gpu_verify_two_greedy(qwen_gpu_model* m, int first, int second, int* first_choice, int* second_choice) {
+    return guarded([&] {
+        need(m, "model");
+        need(first_choice, "first_choice");
+        need(second_choice, "second_choice");
+        m->engine.verify_two(first, second);
+        m->engine.verify_greedy(first_choice, second_choice);
     });
 }
 

@@ -139,13 +139,17 @@ __device__ __forceinline__ float tile_dot(const u32x4 (&wv)[N / 64], const float
 
 enum GemvMode { kPlain, kQKV, kO, kGateUp, kDown, kLmHead };
 
+// With ROWS input vectors (two-token verification), row q of each per-row
+// buffer starts q strides in: in + q N, x / hidden + q 1024, parts +
+// q 8192, out + q out_stride, lm partials + q gridDim.x.
 struct GemvArgs {
     const uint16_t* w;        // chain-tiled weights
     const float* in;          // input vector (plain; O: attention output; down), residual x (norm modes)
     const float* norm_w;      // RMSNorm weights (QKV, gate/up, lm_head)
     const uint16_t* embed;    // natural embedding, first layer only (QKV)
     const float* parts;       // gate/up, down: pending [8][1024] O partials (fused attention), or null
-    int token;                // first-layer QKV: embedding row
+    int token[2];             // first-layer QKV: embedding row of each input row
+    int out_stride;           // ROWS > 1: distance between the rows' outputs
     float* out;               // plain/QKV: y; gate/up: activation; lm_head: logits
     float* x;                 // residual stream (O/down add, first-layer QKV store)
     float* hidden;            // lm_head: final normalized hidden
@@ -158,13 +162,15 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { retur
 
 // PARTS (gate/up, down): the residual stream still has the fused attention
 // kernel's 8 partial O projections pending in a.parts.
-template <int N, int WAVES, int MODE, bool PARTS = false>
+// ROWS input vectors share every weight load: lane (row, chain) keeps one
+// chain per input with the same FMA order, so each row's result is the one
+// a single-row launch gives.
+template <int N, int WAVES, int MODE, bool PARTS = false, int ROWS = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     constexpr int THREADS = WAVES * 64, PER = N / THREADS;
     constexpr bool kNorm = MODE == kQKV || MODE == kGateUp || MODE == kLmHead;
-    __shared__ float4 xs4[N / 4];
-    __shared__ double red[WAVES];
-    float* xs = reinterpret_cast<float*>(xs4);
+    __shared__ float4 xs4[ROWS][N / 4];
+    __shared__ double red[ROWS][WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t tile = size_t(blockIdx.x) * WAVES + wave;
     const int c = lane & 7, r = lane >> 3;
@@ -173,22 +179,22 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     // Every load of the prologue and epilogue is issued before the weights:
     // loads complete in issue order, so one issued after the weight tile
     // would wait for all of it.
-    float v[PER], wn[PER];
-    if constexpr (MODE == kQKV) {
-        if (a.embed) {  // first layer: x = fp32(E[token]) (engine/core.cpp:382-383)
-            const uint16_t* erow = a.embed + size_t(a.token) * N;
+    float v[ROWS][PER], wn[PER];
 #pragma unroll
-            for (int k = 0; k < PER; ++k) v[k] = h2f(erow[tid + k * THREADS]);
+    for (int q = 0; q < ROWS; ++q) {
+        if constexpr (MODE == kQKV) {
+            if (a.embed) {  // first layer: x = fp32(E[token]) (engine/core.cpp:382-383)
+                const uint16_t* erow = a.embed + size_t(a.token[q]) * N;
+#pragma unroll
+                for (int k = 0; k < PER; ++k) v[q][k] = h2f(erow[tid + k * THREADS]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < PER; ++k) v[q][k] = a.in[q * N + tid + k * THREADS];
+            }
         } else {
 #pragma unroll
-            for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
+            for (int k = 0; k < PER; ++k) v[q][k] = a.in[q * N + tid + k * THREADS];
         }
-    } else if constexpr (MODE == kGateUp) {
-#pragma unroll
-        for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
-    } else {
-#pragma unroll
-        for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
     }
     if constexpr (kNorm) {
 #pragma unroll
@@ -196,18 +202,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     }
     // Pending O partials: of this thread's inputs (gate/up) or of this
     // lane's output row (down).
-    float pin[PARTS && MODE == kGateUp ? PER : 1][kKVHeads], prow[kKVHeads];
+    float pin[ROWS][PARTS && MODE == kGateUp ? PER : 1][kKVHeads], prow[ROWS][kKVHeads];
     if constexpr (PARTS && MODE == kGateUp) {
 #pragma unroll
-        for (int k = 0; k < PER; ++k)
+        for (int q = 0; q < ROWS; ++q)
 #pragma unroll
-            for (int g = 0; g < kKVHeads; ++g) pin[k][g] = a.parts[g * kHidden + tid + k * THREADS];
+            for (int k = 0; k < PER; ++k)
+#pragma unroll
+                for (int g = 0; g < kKVHeads; ++g)
+                    pin[q][k][g] = a.parts[(q * kKVHeads + g) * kHidden + tid + k * THREADS];
     }
-    float xres = 0.f;  // residual entry of this lane's row (O, down)
-    if constexpr (MODE == kO || MODE == kDown) xres = a.x[row];
-    if constexpr (PARTS && MODE == kDown) {
+    float xres[ROWS];  // residual entry of this lane's row (O, down)
 #pragma unroll
-        for (int g = 0; g < kKVHeads; ++g) prow[g] = a.parts[g * kHidden + row];
+    for (int q = 0; q < ROWS; ++q) {
+        xres[q] = 0.f;
+        if constexpr (MODE == kO || MODE == kDown) xres[q] = a.x[q * kHidden + row];
+        if constexpr (PARTS && MODE == kDown) {
+#pragma unroll
+            for (int g = 0; g < kKVHeads; ++g) prow[q][g] = a.parts[(q * kKVHeads + g) * kHidden + row];
+        }
     }
 
     // The scheduling barriers keep the weight loads after the prologue loads
@@ -217,68 +230,80 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     load_tile<N>(a.w, tile, lane, wv);
     __builtin_amdgcn_sched_barrier(0);
 
-    if constexpr (PARTS && MODE == kGateUp) {
 #pragma unroll
-        for (int k = 0; k < PER; ++k) v[k] = fold_parts(v[k], pin[k]);
-    }
-    if constexpr (PARTS && MODE == kDown) xres = fold_parts(xres, prow);
-    if constexpr (kNorm) {
-        if constexpr (MODE == kQKV) {
-            if (a.embed && blockIdx.x == 0) {  // kept as the residual stream
+    for (int q = 0; q < ROWS; ++q) {
+        float* xs = reinterpret_cast<float*>(xs4[q]);
+        if constexpr (PARTS && MODE == kGateUp) {
 #pragma unroll
-                for (int k = 0; k < PER; ++k) a.x[tid + k * THREADS] = v[k];
-            }
+            for (int k = 0; k < PER; ++k) v[q][k] = fold_parts(v[q][k], pin[q][k]);
         }
-        norm_to_lds<N, THREADS>(v, wn, xs, red, MODE == kLmHead && blockIdx.x == 0 ? a.hidden : nullptr);
-    } else {
+        if constexpr (PARTS && MODE == kDown) xres[q] = fold_parts(xres[q], prow[q]);
+        if constexpr (kNorm) {
+            if constexpr (MODE == kQKV) {
+                if (a.embed && blockIdx.x == 0) {  // kept as the residual stream
 #pragma unroll
-        for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[k];
+                    for (int k = 0; k < PER; ++k) a.x[q * kHidden + tid + k * THREADS] = v[q][k];
+                }
+            }
+            norm_to_lds<N, THREADS>(v[q], wn, xs, red[q],
+                                    MODE == kLmHead && blockIdx.x == 0 ? a.hidden + q * kHidden : nullptr);
+        } else {
+#pragma unroll
+            for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[q][k];
+        }
     }
     __syncthreads();
 
-    const float y = tile_dot<N>(wv, xs, lane);
-
-    if constexpr (MODE == kPlain || MODE == kQKV) {
-        if (c == 0) a.out[row] = y;
-    } else if constexpr (MODE == kO || MODE == kDown) {
-        if (c == 0) a.x[row] = xres + y;
-    } else if constexpr (MODE == kGateUp) {
-        // Tile rows 0-3 are gate rows 4T..4T+3, rows 4-7 the matching up rows.
-        const float up = __shfl(y, (lane + 32) & 63);
-        if (lane < 32 && c == 0) {
-            const float gate = y;
-            const float half_gate = gate * 0.5f;
-            const float t = tanhf(half_gate);
-            a.out[int(tile) * 4 + r] = gate * (0.5f + 0.5f * t) * up;
-        }
-    } else if constexpr (MODE == kLmHead) {
-        if (c == 0) a.out[row] = y;
-        // Workgroup argmax: lowest id among maxima; any nonfinite value flagged.
-        float bv = -INFINITY;
-        int bi = INT_MAX, bad = 0;
-        if (c == 0) {
-            bad = !__builtin_isfinite(y);
-            if (better(y, row, bv, bi)) { bv = y; bi = row; }
-        }
+    float y[ROWS];
 #pragma unroll
-        for (int off = 8; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            bad |= __shfl_xor(bad, off);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-        }
-        __shared__ float wv[WAVES];
-        __shared__ int wi[WAVES], wb[WAVES];
-        if (lane == 0) { wv[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
-        __syncthreads();
-        if (tid == 0) {
-            for (int k = 1; k < WAVES; ++k) {
-                bad |= wb[k];
-                if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
+    for (int q = 0; q < ROWS; ++q) y[q] = tile_dot<N>(wv, reinterpret_cast<const float*>(xs4[q]), lane);
+
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        float* out = a.out + size_t(q) * a.out_stride;
+        if constexpr (MODE == kPlain || MODE == kQKV) {
+            if (c == 0) out[row] = y[q];
+        } else if constexpr (MODE == kO || MODE == kDown) {
+            if (c == 0) a.x[q * kHidden + row] = xres[q] + y[q];
+        } else if constexpr (MODE == kGateUp) {
+            // Tile rows 0-3 are gate rows 4T..4T+3, rows 4-7 the matching up rows.
+            const float up = __shfl(y[q], (lane + 32) & 63);
+            if (lane < 32 && c == 0) {
+                const float gate = y[q];
+                const float half_gate = gate * 0.5f;
+                const float t = tanhf(half_gate);
+                out[int(tile) * 4 + r] = gate * (0.5f + 0.5f * t) * up;
             }
-            a.lm_value[blockIdx.x] = bv;
-            a.lm_index[blockIdx.x] = bi;
-            a.lm_bad[blockIdx.x] = bad;
+        } else if constexpr (MODE == kLmHead) {
+            if (c == 0) out[row] = y[q];
+            // Workgroup argmax: lowest id among maxima; any nonfinite value flagged.
+            float bv = -INFINITY;
+            int bi = INT_MAX, bad = 0;
+            if (c == 0) {
+                bad = !__builtin_isfinite(y[q]);
+                if (better(y[q], row, bv, bi)) { bv = y[q]; bi = row; }
+            }
+#pragma unroll
+            for (int off = 8; off < 64; off <<= 1) {
+                const float ov = __shfl_xor(bv, off);
+                const int oi = __shfl_xor(bi, off);
+                bad |= __shfl_xor(bad, off);
+                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
+            __shared__ float wbest[ROWS][WAVES];
+            __shared__ int wi[ROWS][WAVES], wb[ROWS][WAVES];
+            if (lane == 0) { wbest[q][wave] = bv; wi[q][wave] = bi; wb[q][wave] = bad; }
+            __syncthreads();
+            if (tid == 0) {
+                for (int k = 1; k < WAVES; ++k) {
+                    bad |= wb[q][k];
+                    if (better(wbest[q][k], wi[q][k], bv, bi)) { bv = wbest[q][k]; bi = wi[q][k]; }
+                }
+                const int slot = q * gridDim.x + blockIdx.x;
+                a.lm_value[slot] = bv;
+                a.lm_index[slot] = bi;
+                a.lm_bad[slot] = bad;
+            }
         }
     }
 }
@@ -646,11 +671,16 @@ __global__ __launch_bounds__(128) void attn_merge_batch_kernel(const AttnBatch b
 // wave runs a softmax over its own positions (max m_w, sum l_w) and its P.V
 // with 4 positions x 16 channel groups per load; the 8 waves' partials are
 // merged with weights exp(m_w - max_w m_w), as in a split-softmax merge.
-template <int PASSES>
+// ROWS = 2 (two-token verification): row q is the step at position pos + q
+// and attends over its pos + q + 1 positions; both rows share every K/V and
+// O load, row 1 takes position pos (row 0's new K/V) from LDS, and each
+// row's arithmetic is the single-row kernel's (extra masked positions add
+// exact zeros), so its output equals a single-row launch at its position.
+template <int PASSES, int ROWS = 1>
 __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     const int g = blockIdx.x % kKVHeads, rb = blockIdx.x / kKVHeads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = a.pos, n = pos + 1;
+    const int pos = a.pos;
     const size_t head_base = size_t(g) * a.context;
     const int quarter = tid >> 7, j = tid & 127, c = tid & 7, grp = tid >> 3;
     const int vsub = lane >> 4, vcg = lane & 15;  // P.V: position within a group of 4, channel group
@@ -658,19 +688,29 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     // Loads complete in issue order per wave, so they are issued in the
     // order they are needed: this step's q/k/v with their norm weights and
     // rotation, cached K rows, V rows, then this workgroup's O weights. Rows
-    // past n or at pos (taken from LDS) load row 0 instead and are not used.
-    const float raw = quarter < 2 ? a.qkv[(2 * g + quarter) * 128 + j] : a.qkv[2048 + g * 128 + j];
-    const float raw_v = a.qkv[3072 + g * 128 + j];
+    // from pos on (taken from LDS) or past them load row 0 instead and are
+    // not used.
+    float raw[ROWS], raw_v[ROWS], rc[ROWS], rs[ROWS];
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        const float* qkv = a.qkv + q * kQKVRows;
+        raw[q] = quarter < 2 ? qkv[(2 * g + quarter) * 128 + j] : qkv[2048 + g * 128 + j];
+        raw_v[q] = qkv[3072 + g * 128 + j];
+    }
     // quarter is uniform per wave; selecting the pointer on a scalar keeps it
     // out of vector registers (no per-lane load of the kernel argument).
     const float nw = (__builtin_amdgcn_readfirstlane(quarter) < 2 ? a.q_norm : a.k_norm)[j];
-    const float rc = a.cosines[size_t(pos) * 64 + (j & 63)], rs = a.sines[size_t(pos) * 64 + (j & 63)];
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        rc[q] = a.cosines[size_t(pos + q) * 64 + (j & 63)];
+        rs[q] = a.sines[size_t(pos + q) * 64 + (j & 63)];
+    }
     u32x4 kreg[PASSES][2], vreg[PASSES][2];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int t = p * 64 + grp;
-        const int tl = t < n && t != pos ? t : 0;
+        const int tl = t < pos ? t : 0;
         key_pieces(a.keys + (head_base + tl) * 128, c, kreg[p][0], kreg[p][1]);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -679,7 +719,7 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             const int t = p * 64 + 8 * wave + 4 * hf + vsub;
-            const int tl = t < n && t != pos ? t : 0;
+            const int tl = t < pos ? t : 0;
             vreg[p][hf] = reinterpret_cast<const u32x4*>(a.values + (head_base + tl) * 128)[vcg];
         }
     __builtin_amdgcn_sched_barrier(0);
@@ -696,150 +736,162 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    __shared__ float qp[2][128];
-    __shared__ float buf[4][128];
-    __shared__ float prob[2][kFusedMaxPositions];
+    __shared__ float qp[ROWS][2][128];
+    __shared__ float buf[ROWS][4][128];
+    __shared__ float prob[ROWS][2][kFusedMaxPositions];
     __shared__ float opart[8][4][2][128];
-    __shared__ __align__(16) float att[256];
-    __shared__ uint16_t kcur[128], vcur[128];
-    __shared__ double red[4][2];
+    __shared__ __align__(16) float att[ROWS][256];
+    __shared__ uint16_t kcur[ROWS][128], vcur[ROWS][128];
+    __shared__ double red[ROWS][4][2];
     __shared__ float wmax[8][2], wsum[8][2];
 
     // QK-norm + RoPE (engine/core.cpp:395-402); workgroup rb == 0 writes the
-    // new K/V row (403-406). The others only read rows t != pos.
-    {
-        const float r = head_norm_rope(raw, nw, rc, rs, red[quarter], buf[quarter], j);
-        const bool owner = rb == 0;
+    // new K/V rows (403-406). The others only read rows t < pos.
+    const bool owner = rb == 0;
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        const float r = head_norm_rope(raw[q], nw, rc[q], rs[q], red[q][quarter], buf[q][quarter], j);
         if (quarter < 2) {
-            qp[quarter][kperm(j)] = r;
+            qp[q][quarter][kperm(j)] = r;
         } else if (quarter == 2) {
             const uint16_t bits = f2h(r);
-            kcur[kperm(j)] = bits;
-            if (owner) a.keys[(head_base + pos) * 128 + kperm(j)] = bits;
+            kcur[q][kperm(j)] = bits;
+            if (owner) a.keys[(head_base + pos + q) * 128 + kperm(j)] = bits;
         } else {
-            const uint16_t bits = f2h(raw_v);
-            vcur[j] = bits;
-            if (owner) a.values[(head_base + pos) * 128 + j] = bits;
+            const uint16_t bits = f2h(raw_v[q]);
+            vcur[q][j] = bits;
+            if (owner) a.values[(head_base + pos + q) * 128 + j] = bits;
         }
     }
     __syncthreads();
 
-    // Scores of this wave's positions (every lane of a position's group of 8
-    // holds the combined value) and the wave's running maximum.
-    float s0[PASSES], s1[PASSES];
-    float m0 = -INFINITY, m1 = -INFINITY;
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-        const int t = p * 64 + grp;
-        uint32_t kw[8];
-        if (t == pos) {
-            key_pieces_lds(kcur, c, kw);
-        } else {
-            kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
-            kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+    for (int q = 0; q < ROWS; ++q) {
+        const int n = pos + q + 1;
+        // Scores of this wave's positions (every lane of a position's group
+        // of 8 holds the combined value) and the wave's running maximum.
+        float s0[PASSES], s1[PASSES];
+        float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = p * 64 + grp, cur = t - pos;
+            uint32_t kw[8];
+            if (cur >= 0 && cur <= q) {
+                key_pieces_lds(kcur[cur], c, kw);
+            } else {
+                kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
+                kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+            }
+            const float d0 = combine_chains(key_chain(qp[q][0], c, kw, 0.f)) * a.scale;
+            const float d1 = combine_chains(key_chain(qp[q][1], c, kw, 0.f)) * a.scale;
+            s0[p] = t < n ? d0 : -INFINITY;
+            s1[p] = t < n ? d1 : -INFINITY;
+            m0 = fmaxf(m0, s0[p]);
+            m1 = fmaxf(m1, s1[p]);
         }
-        const float d0 = combine_chains(key_chain(qp[0], c, kw, 0.f)) * a.scale;
-        const float d1 = combine_chains(key_chain(qp[1], c, kw, 0.f)) * a.scale;
-        s0[p] = t < n ? d0 : -INFINITY;
-        s1[p] = t < n ? d1 : -INFINITY;
-        m0 = fmaxf(m0, s0[p]);
-        m1 = fmaxf(m1, s1[p]);
-    }
 #pragma unroll
-    for (int off = 8; off < 64; off <<= 1) {
-        m0 = fmaxf(m0, __shfl_xor(m0, off));
-        m1 = fmaxf(m1, __shfl_xor(m1, off));
-    }
-    // Probabilities relative to the wave maximum (a wave without positions
-    // keeps m = -inf and contributes nothing).
-    float l0 = 0.f, l1 = 0.f;
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-        const int t = p * 64 + grp;
-        const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
-        const float p1 = t < n ? expf(s1[p] - m1) : 0.f;
-        l0 += p0;
-        l1 += p1;
-        if (c == 0) {
-            prob[0][t] = p0;
-            prob[1][t] = p1;
+        for (int off = 8; off < 64; off <<= 1) {
+            m0 = fmaxf(m0, __shfl_xor(m0, off));
+            m1 = fmaxf(m1, __shfl_xor(m1, off));
         }
-    }
+        // Probabilities relative to the wave maximum (a wave without
+        // positions keeps m = -inf and contributes nothing).
+        float l0 = 0.f, l1 = 0.f;
 #pragma unroll
-    for (int off = 8; off < 64; off <<= 1) {
-        l0 += __shfl_xor(l0, off);
-        l1 += __shfl_xor(l1, off);
-    }
-    // prob[][t] of this wave's positions is written and read by this wave only.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    float acc[2][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[0][i] = acc[1][i] = 0.f;
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int t = p * 64 + 8 * wave + 4 * hf + vsub;
-            if (t < n) {
-                const float p0 = prob[0][t], p1 = prob[1][t];
-                uint32_t vw[4];
-                if (t == pos) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        vw[i] = uint32_t(vcur[vcg * 8 + 2 * i]) | (uint32_t(vcur[vcg * 8 + 2 * i + 1]) << 16);
-                } else {
-                    vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
-                    acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
-                    acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
-                    acc[1][2 * i] = __builtin_fmaf(v0, p1, acc[1][2 * i]);
-                    acc[1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[1][2 * i + 1]);
-                }
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = p * 64 + grp;
+            const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
+            const float p1 = t < n ? expf(s1[p] - m1) : 0.f;
+            l0 += p0;
+            l1 += p1;
+            if (c == 0) {
+                prob[q][0][t] = p0;
+                prob[q][1][t] = p1;
             }
         }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) opart[wave][vsub][h][vcg * 8 + i] = acc[h][i];
-    if (lane == 0) {
-        wmax[wave][0] = m0;
-        wmax[wave][1] = m1;
-        wsum[wave][0] = l0;
-        wsum[wave][1] = l1;
-    }
-    __syncthreads();
-    if (tid < 256) {
-        const int h = tid >> 7;
-        float mx = wmax[0][h];
-#pragma unroll
-        for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w][h]);
-        float l = 0.f, o = 0.f;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const float e = wmax[w][h] == -INFINITY ? 0.f : expf(wmax[w][h] - mx);
-            const float ow4 = (opart[w][0][h][j] + opart[w][1][h][j]) + (opart[w][2][h][j] + opart[w][3][h][j]);
-            l = __builtin_fmaf(e, wsum[w][h], l);
-            o = __builtin_fmaf(e, ow4, o);
+        for (int off = 8; off < 64; off <<= 1) {
+            l0 += __shfl_xor(l0, off);
+            l1 += __shfl_xor(l1, off);
         }
-        att[tid] = o / l;
+        // prob[q][][t] of this wave's positions is written and read by this
+        // wave only.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        float acc[2][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[0][i] = acc[1][i] = 0.f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int t = p * 64 + 8 * wave + 4 * hf + vsub, cur = t - pos;
+                if (t < n) {
+                    const float p0 = prob[q][0][t], p1 = prob[q][1][t];
+                    uint32_t vw[4];
+                    if (cur >= 0) {  // cur <= q here since t < n
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            vw[i] = uint32_t(vcur[cur][vcg * 8 + 2 * i]) |
+                                    (uint32_t(vcur[cur][vcg * 8 + 2 * i + 1]) << 16);
+                    } else {
+                        vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
+                        acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
+                        acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
+                        acc[1][2 * i] = __builtin_fmaf(v0, p1, acc[1][2 * i]);
+                        acc[1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[1][2 * i + 1]);
+                    }
+                }
+            }
+        if (q > 0) __syncthreads();  // the previous row's merge has read opart / wmax / wsum
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) opart[wave][vsub][h][vcg * 8 + i] = acc[h][i];
+        if (lane == 0) {
+            wmax[wave][0] = m0;
+            wmax[wave][1] = m1;
+            wsum[wave][0] = l0;
+            wsum[wave][1] = l1;
+        }
+        __syncthreads();
+        if (tid < 256) {
+            const int h = tid >> 7;
+            float mx = wmax[0][h];
+#pragma unroll
+            for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w][h]);
+            float l = 0.f, o = 0.f;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const float e = wmax[w][h] == -INFINITY ? 0.f : expf(wmax[w][h] - mx);
+                const float ow4 = (opart[w][0][h][j] + opart[w][1][h][j]) + (opart[w][2][h][j] + opart[w][3][h][j]);
+                l = __builtin_fmaf(e, wsum[w][h], l);
+                o = __builtin_fmaf(e, ow4, o);
+            }
+            att[q][tid] = o / l;
+        }
     }
     __syncthreads();
 
     // This workgroup's rows of O against the 256 outputs of the KV head's
     // query heads.
-    float y = 0.f;
-    const float4* at4 = reinterpret_cast<const float4*>(att) + 2 * opart_id;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
+    for (int q = 0; q < ROWS; ++q) {
+        float y = 0.f;
+        const float4* at4 = reinterpret_cast<const float4*>(att[q]) + 2 * opart_id;
 #pragma unroll
-    for (int off = 1; off < kThreadsPerRow; off <<= 1) y += __shfl_xor(y, off);
-    if (opart_id == 0) a.o_part[g * kHidden + orow] = y;
+        for (int i = 0; i < kLoads; ++i)
+            y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
+#pragma unroll
+        for (int off = 1; off < kThreadsPerRow; off <<= 1) y += __shfl_xor(y, off);
+        if (opart_id == 0) a.o_part[(q * kKVHeads + g) * kHidden + orow] = y;
+    }
 }
 
 __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* __restrict__ second,
@@ -887,6 +939,26 @@ void launch_gemv(const GemvArgs& a, int rows, hipStream_t stream) {
     gemv_kernel<N, W, MODE><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
 }
 
+// Two-row launches (verification pairs): waves per workgroup of each mode.
+template <int MODE>
+constexpr int gemv_pair_waves() {
+    if constexpr (MODE == kGateUp || MODE == kLmHead) return 4;
+    else if constexpr (MODE == kDown) return 1;
+    else return 2;
+}
+
+template <int N, int MODE>
+void launch_gemv_pair(const GemvArgs& a, int rows, hipStream_t stream) {
+    constexpr int W = gemv_pair_waves<MODE>();
+    if constexpr (MODE == kGateUp || MODE == kDown) {
+        if (a.parts) {
+            gemv_kernel<N, W, MODE, true, 2><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
+            return;
+        }
+    }
+    gemv_kernel<N, W, MODE, false, 2><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
+}
+
 }  // namespace
 
 void launch_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t* dst, int rows, int cols,
@@ -921,7 +993,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             q.in = s.x;
             q.norm_w = L.in_norm;
             q.embed = embed;
-            q.token = token;
+            q.token[0] = token;
             q.out = s.qkv;
             q.x = s.x;
             launch_gemv<kHidden, kQKV>(q, kQKVRows, stream);
@@ -993,6 +1065,109 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
         }
         default: throw std::runtime_error("unknown decode kernel");
     }
+}
+
+bool pair_supported(int pos) { return attn_fused(pos + 2) || !attn_fused(pos + 1); }
+
+void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int pos, const int (&tokens)[2],
+                              const float* cosines, const float* sines, int context, const DecodeScratch& s,
+                              const PairScratch& pr, hipStream_t stream) {
+    require(pair_supported(pos) && pos >= 0 && pos + 2 <= context, "verification pair: unsupported position");
+    const bool fused = attn_fused(pos + 2);
+    GemvArgs q{};
+    q.w = L.qkv_t;
+    q.in = pr.x;
+    q.norm_w = L.in_norm;
+    q.embed = embed;
+    q.token[0] = tokens[0];
+    q.token[1] = tokens[1];
+    q.out = pr.qkv;
+    q.out_stride = kQKVRows;
+    q.x = pr.x;
+    launch_gemv_pair<kHidden, kQKV>(q, kQKVRows, stream);
+
+    AttnArgs at{};
+    at.qkv = pr.qkv;
+    at.q_norm = L.q_norm;
+    at.k_norm = L.k_norm;
+    at.cosines = cosines;
+    at.sines = sines;
+    at.keys = L.keys;
+    at.values = L.values;
+    at.pos = pos;
+    at.partial = s.attn_partial;
+    at.context = context;
+    at.scale = 1.0f / std::sqrt(128.0f);
+    at.o_n = L.o_n;
+    at.o_part = pr.o_part;
+    if (fused) {
+        switch ((pos + 2 + 63) / 64) {  // passes of 64 positions over n = pos + 2
+            case 1: attn_o_kernel<1, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            case 2: attn_o_kernel<2, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            case 3: attn_o_kernel<3, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            case 4: attn_o_kernel<4, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            case 5: attn_o_kernel<5, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            case 6: attn_o_kernel<6, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            case 7: attn_o_kernel<7, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            case 8: attn_o_kernel<8, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
+            default: throw std::runtime_error("fused attention: context beyond 512 positions");
+        }
+    } else {
+        // Both rows past the fused range: the single-row split kernels, row 0
+        // first (it writes the K/V row that row 1 reads from the cache).
+        for (int row = 0; row < 2; ++row) {
+            AttnArgs ar = at;
+            ar.qkv = pr.qkv + row * kQKVRows;
+            ar.pos = pos + row;
+            ar.attended = pr.attended + row * kQDim;
+            int chunk, splits;
+            attn_split(ar.pos + 1, chunk, splits);
+            attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(ar);
+            attn_merge_kernel<<<kQHeads, 128, 0, stream>>>(ar);
+        }
+        GemvArgs o{};
+        o.w = L.o_t;
+        o.in = pr.attended;
+        o.x = pr.x;
+        launch_gemv_pair<kQDim, kO>(o, kHidden, stream);
+    }
+
+    GemvArgs gu{};
+    gu.w = L.gateup_t;
+    gu.in = pr.x;
+    gu.norm_w = L.post_norm;
+    gu.parts = fused ? pr.o_part : nullptr;
+    gu.out = pr.act;
+    gu.out_stride = kFFN;
+    launch_gemv_pair<kHidden, kGateUp>(gu, 2 * kFFN, stream);
+
+    GemvArgs d{};
+    d.w = L.down_t;
+    d.in = pr.act;
+    d.parts = fused ? pr.o_part : nullptr;
+    d.x = pr.x;
+    launch_gemv_pair<kFFN, kDown>(d, kHidden, stream);
+}
+
+void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
+                         const PairScratch& pr, ArgmaxResult* host_out, hipStream_t stream) {
+    GemvArgs a{};
+    a.w = lm_t;
+    a.in = pr.x;
+    a.norm_w = final_norm;
+    a.out = pr.logits;
+    a.out_stride = kVocab;
+    a.hidden = pr.hidden;
+    a.lm_value = s.lm_value;
+    a.lm_index = s.lm_index;
+    a.lm_bad = s.lm_bad;
+    constexpr int W = gemv_pair_waves<kLmHead>();
+    static_assert(W == kLmWaves, "pair lm_head partials use the single-row group count");
+    gemv_kernel<kHidden, W, kLmHead, false, 2><<<kLmGroups, 64 * W, 0, stream>>>(a);
+    for (int row = 0; row < 2; ++row)
+        argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value + row * kLmGroups, s.lm_index + row * kLmGroups,
+                                              s.lm_bad + row * kLmGroups, kLmGroups, pr.result + row,
+                                              host_out + row);
 }
 
 void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,

@@ -193,7 +193,17 @@ void Engine::init_state() {
     ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
     base_logits_ = device_alloc<float>(kVocab);
     base_hidden_ = device_alloc<float>(kHidden);
+    pair_.x = device_alloc<float>(2 * kHidden);
+    pair_.qkv = device_alloc<float>(2 * kQKVRows);
+    pair_.attended = device_alloc<float>(2 * kQDim);
+    pair_.act = device_alloc<float>(2 * kFFN);
+    pair_.o_part = device_alloc<float>(size_t(2) * kKVHeads * kHidden);
+    pair_.logits = ver_logits_;
+    pair_.hidden = ver_hidden_;
+    pair_.result = device_alloc<ArgmaxResult>(2);
     void* pinned = nullptr;
+    HIP_CHECK(hipHostMalloc(&pinned, sizeof(float) * 2 * (size_t(kVocab) + kHidden), hipHostMallocDefault));
+    ver_host_ = static_cast<float*>(pinned);
     HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
     result_host_ = static_cast<ArgmaxResult*>(pinned);
     std::memset(result_host_, 0, sizeof(ArgmaxResult) * 3);
@@ -216,6 +226,8 @@ void Engine::release() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     for (void* p : allocations_) (void)hipFree(p);
     if (result_host_) (void)hipHostFree(result_host_);
+    if (ver_host_) (void)hipHostFree(ver_host_);
+    ver_host_ = nullptr;
     if (ids_host_) (void)hipHostFree(ids_host_);
     ids_host_ = nullptr;
     if (stream_) (void)hipStreamDestroy(stream_);
@@ -378,49 +390,73 @@ int Engine::greedy() {
     return result_host_[0].token;
 }
 
-// engine/core.cpp:729-741: two B1 steps; public state stays at the base.
-void Engine::verify_two(int first, int second, const float** logits, const float** hidden, int* base) {
+// Both verification rows through the 28 layers and the head in one pass
+// over the weights; K/V rows written at pos_ and pos_ + 1, pos_ unchanged.
+void Engine::run_pair(int first, int second) {
+    const int tokens[2] = {first, second};
+    for (int l = 0; l < kLayers; ++l)
+        launch_decode_layer_pair(layers_[l], l == 0 ? embed_ : nullptr, pos_, tokens, cosines_, sines_,
+                                 options_.context, scratch_, pair_, stream_);
+    launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, stream_);
+    HIP_CHECK(hipGetLastError());
+}
+
+// engine/core.cpp:729-741: the rows of two B1 steps; public state stays at
+// the base.
+void Engine::verify_two(int first, int second) {
     require(!pending_, "Verification already pending");
     require(first >= 0 && first < kVocab && second >= 0 && second < kVocab, "Token ID out of range");
     require(pos_ <= options_.context - 2, "Context capacity exceeded");
     const int start = pos_;
     try {
-        if (has_logits_) {
-            HIP_CHECK(hipMemcpyAsync(base_logits_, scratch_.logits, size_t(kVocab) * 4, hipMemcpyDeviceToDevice,
-                                     stream_));
-            HIP_CHECK(hipMemcpyAsync(base_hidden_, scratch_.hidden, size_t(kHidden) * 4, hipMemcpyDeviceToDevice,
-                                     stream_));
+        if (pair_supported(start)) {
+            run_pair(first, second);
+        } else {
+            // The two positions straddle the fused-attention limit: two single
+            // steps, with the public logits saved and restored around them.
+            if (has_logits_) {
+                HIP_CHECK(hipMemcpyAsync(base_logits_, scratch_.logits, size_t(kVocab) * 4,
+                                         hipMemcpyDeviceToDevice, stream_));
+                HIP_CHECK(hipMemcpyAsync(base_hidden_, scratch_.hidden, size_t(kHidden) * 4,
+                                         hipMemcpyDeviceToDevice, stream_));
+            }
+            const int ids[2] = {first, second};
+            for (int row = 0; row < 2; ++row) {
+                run_token(ids[row], true, 1 + row);
+                HIP_CHECK(hipMemcpyAsync(ver_logits_ + size_t(row) * kVocab, scratch_.logits, size_t(kVocab) * 4,
+                                         hipMemcpyDeviceToDevice, stream_));
+                HIP_CHECK(hipMemcpyAsync(ver_hidden_ + size_t(row) * kHidden, scratch_.hidden,
+                                         size_t(kHidden) * 4, hipMemcpyDeviceToDevice, stream_));
+            }
+            if (has_logits_) {
+                HIP_CHECK(hipMemcpyAsync(scratch_.logits, base_logits_, size_t(kVocab) * 4,
+                                         hipMemcpyDeviceToDevice, stream_));
+                HIP_CHECK(hipMemcpyAsync(scratch_.hidden, base_hidden_, size_t(kHidden) * 4,
+                                         hipMemcpyDeviceToDevice, stream_));
+            }
         }
-        const int ids[2] = {first, second};
-        for (int row = 0; row < 2; ++row) {
-            run_token(ids[row], true, 1 + row);
-            HIP_CHECK(hipMemcpyAsync(ver_logits_ + size_t(row) * kVocab, scratch_.logits, size_t(kVocab) * 4,
-                                     hipMemcpyDeviceToDevice, stream_));
-            HIP_CHECK(hipMemcpyAsync(ver_hidden_ + size_t(row) * kHidden, scratch_.hidden, size_t(kHidden) * 4,
-                                     hipMemcpyDeviceToDevice, stream_));
-        }
-        if (has_logits_) {
-            HIP_CHECK(hipMemcpyAsync(scratch_.logits, base_logits_, size_t(kVocab) * 4, hipMemcpyDeviceToDevice,
-                                     stream_));
-            HIP_CHECK(hipMemcpyAsync(scratch_.hidden, base_hidden_, size_t(kHidden) * 4, hipMemcpyDeviceToDevice,
-                                     stream_));
-        }
-        host_ver_logits_.resize(size_t(2) * kVocab);
-        host_ver_hidden_.resize(size_t(2) * kHidden);
-        HIP_CHECK(hipMemcpyAsync(host_ver_logits_.data(), ver_logits_, size_t(2) * kVocab * 4, hipMemcpyDeviceToHost,
-                                 stream_));
-        HIP_CHECK(hipMemcpyAsync(host_ver_hidden_.data(), ver_hidden_, size_t(2) * kHidden * 4,
-                                 hipMemcpyDeviceToHost, stream_));
         sync();
         pos_ = start;
         pending_ = true;
+        ver_host_valid_ = false;
     } catch (...) {
         reset();
         throw;
     }
-    *logits = host_ver_logits_.data();
-    *hidden = host_ver_hidden_.data();
-    *base = start;
+}
+
+void Engine::verification_rows(const float** logits, const float** hidden, int* base) {
+    require(pending_, "No verification pending");
+    if (!ver_host_valid_) {
+        HIP_CHECK(hipMemcpyAsync(ver_host_, ver_logits_, size_t(2) * kVocab * 4, hipMemcpyDeviceToHost, stream_));
+        HIP_CHECK(hipMemcpyAsync(ver_host_ + size_t(2) * kVocab, ver_hidden_, size_t(2) * kHidden * 4,
+                                 hipMemcpyDeviceToHost, stream_));
+        sync();
+        ver_host_valid_ = true;
+    }
+    *logits = ver_host_;
+    *hidden = ver_host_ + size_t(2) * kVocab;
+    *base = pos_;
 }
 
 void Engine::verify_greedy(int* first, int* second) {

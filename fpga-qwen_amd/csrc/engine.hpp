@@ -50,7 +50,12 @@ public:
     void prefill(const int* ids, size_t count);
     void step(int token);
     // Two consumed ids with B1 arithmetic; rows stay pending until commit.
-    void verify_two(int first, int second, const float** logits, const float** hidden, int* base);
+    // Both rows run as one pass over the weights when the two positions take
+    // the same attention path (pair_supported), else as two single steps.
+    void verify_two(int first, int second);
+    // Host copies of the pending rows ([2 x vocab] logits, [2 x 1024]
+    // hidden), copied on first access, and the base position.
+    void verification_rows(const float** logits, const float** hidden, int* base);
     void commit_verified(int count);
     // Host copies of the current logits/hidden (nullptr when none).
     const float* logits();
@@ -79,6 +84,7 @@ private:
     void init_state();
     void append(const int* ids, size_t count);
     void run_token(int token, bool head, int result_slot);
+    void run_pair(int first, int second);
     void release();
     void sync();
     void invalidate();
@@ -101,12 +107,15 @@ private:
     ArgmaxResult* result_host_ = nullptr;  // pinned [3]: current, verify row 0, verify row 1
     float* ver_logits_ = nullptr;   // device [2 x vocab]
     float* ver_hidden_ = nullptr;   // device [2 x 1024]
-    float* base_logits_ = nullptr;  // public logits saved across a verification
+    float* base_logits_ = nullptr;  // public logits saved across a two-step verification
     float* base_hidden_ = nullptr;
+    PairScratch pair_{};            // one-pass verification buffers (logits/hidden = ver_*)
+    float* ver_host_ = nullptr;     // pinned [2 x vocab] logits then [2 x 1024] hidden
+    bool ver_host_valid_ = false;
     int pos_ = 0;
     bool has_logits_ = false;
     bool pending_ = false;
-    std::vector<float> host_logits_, host_hidden_, host_ver_logits_, host_ver_hidden_;
+    std::vector<float> host_logits_, host_hidden_;
     bool host_logits_valid_ = false, host_hidden_valid_ = false;
 
     template <class T>

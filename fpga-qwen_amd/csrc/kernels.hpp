@@ -125,6 +125,36 @@ void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* em
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
 
+// Buffers of a two-token verification (rows at positions pos and pos + 1).
+struct PairScratch {
+    float* x;             // [2][1024] residual streams
+    float* qkv;           // [2][4096]
+    float* attended;      // [2][2048] (split attention)
+    float* act;           // [2][3072]
+    float* o_part;        // [2][8][1024] (fused attention)
+    float* logits;        // [2][151936]
+    float* hidden;        // [2][1024]
+    ArgmaxResult* result; // [2] device copies of the selections
+};
+
+// True when the steps at pos and pos + 1 take the same attention path
+// (both fused or both split), which the pair launch requires.
+bool pair_supported(int pos);
+
+// Verification (engine/core.cpp:729-741): one decode layer for the steps at
+// positions pos and pos + 1 with tokens[0], tokens[1], every weight matrix
+// read once for both rows; each row gets the arithmetic of
+// launch_decode_layer at its position, so results are bit-identical to two
+// single steps. Writes K/V at pos and pos + 1.
+void launch_decode_layer_pair(const LayerDevice& layer, const uint16_t* embed, int pos, const int (&tokens)[2],
+                              const float* cosines, const float* sines, int context, const DecodeScratch& s,
+                              const PairScratch& pair, hipStream_t stream);
+
+// Final norm + lm_head + greedy argmax of both verification rows (uses the
+// lm partial buffers of s); selections to pair.result and host_out[0..1].
+void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
+                         const PairScratch& pair, ArgmaxResult* host_out, hipStream_t stream);
+
 // One sequence of a batched attention launch.
 struct AttnSeq {
     const float* qkv;   // raw projections [4096]

@@ -195,8 +195,7 @@ int main(int argc, char** argv) {
                     if (history.size() != size_t(model.position()))
                         throw std::runtime_error("Consumed history does not match model position");
                     const auto start = Clock::now();
-                    (void)model.verify_two(pending, draft);
-                    const auto [first, bonus] = model.verify_greedy();
+                    const auto [first, bonus] = model.verify_two_greedy(pending, draft);
                     const bool accepted = first == draft;
                     const int committed = accepted && !is_eos(first) ? 2 : 1;
                     const int second = committed == 2 ? bonus : -1;

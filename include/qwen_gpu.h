@@ -100,6 +100,12 @@ int qwen_gpu_get_options(const qwen_gpu_model* model, qwen_gpu_options* options)
 int qwen_gpu_greedy(qwen_gpu_model* model, int* token);
 /* Greedy selections of both pending verification rows (engine/main.cpp:138,142). */
 int qwen_gpu_verify_greedy(qwen_gpu_model* model, int* first, int* second);
+/* verify_two followed by verify_greedy, without copying the rows to host
+ * memory: what the protocol's verify-greedy command needs (engine/main.cpp:
+ * 128-147 calls verify_two and selects from the returned rows). The rows stay
+ * pending for qwen_gpu_commit_verified. No counterpart in the reference class. */
+int qwen_gpu_verify_two_greedy(qwen_gpu_model* model, int first, int second, int* first_choice,
+                               int* second_choice);
 
 /* Synthetic QWCPU01 pack (format: engine/INTERFACE.md:8-21; tensor order of
  * tools/export_native_cpu_weights.py:29-39): matrices N(0, stddev) rounded to

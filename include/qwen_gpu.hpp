@@ -98,6 +98,13 @@ public:
         detail::check(qwen_gpu_verify_greedy(handle_.get(), &a, &b));
         return {a, b};
     }
+    // verify_two + verify_greedy without copying the rows to the host.
+    std::pair<int, int> verify_two_greedy(int first, int second) {
+        int a = 0, b = 0;
+        logits_.clear();
+        detail::check(qwen_gpu_verify_two_greedy(handle_.get(), first, second, &a, &b));
+        return {a, b};
+    }
 
 private:
     struct Deleter {

@@ -91,9 +91,15 @@ def test_prefill_equals_steps_and_truncate(gpu_model):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('prefix,commit', [(0, 1), (0, 2), (1, 1), (1, 2), (513, 2)])
+# Prefixes cover the one-pass pair kernels (fused attention: 0, 1, 62, 63
+# where row 1 needs one more 64-position pass than row 0, 510 at the fused
+# limit; split attention: 513, 700) and the two-step fallback (511: row 0
+# fused, row 1 split).
+@pytest.mark.parametrize('prefix,commit', [(0, 1), (0, 2), (1, 1), (1, 2), (62, 2), (63, 1), (510, 2), (511, 2),
+                                           (513, 2), (700, 1)])
 def test_verify_two_equals_two_steps(qpkg, pack0, gpu_model, prefix, commit):
-    """tools/native_verify_check.cpp normal_case, against a second model."""
+    """tools/native_verify_check.cpp normal_case, against a second model:
+    every row bit-identical to single steps."""
     ids = [32 + (i * 37) % 1000 for i in range(prefix)]
     ref = qpkg.Model(pack0, context=4096)
     try:
@@ -139,6 +145,27 @@ def test_verify_two_equals_two_steps(qpkg, pack0, gpu_model, prefix, commit):
         assert np.array_equal(gpu_model.logits().view(np.uint32), ref.logits().view(np.uint32))
     finally:
         ref.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('prefix', [5, 511, 600])
+def test_verify_two_greedy_matches_rows(qpkg, pack0, gpu_model, prefix):
+    """The no-host-copy verification selects what verify_two's rows give and
+    leaves the same pending state."""
+    ids = [100 + (i * 53) % 5000 for i in range(prefix)]
+    gpu_model.reset()
+    gpu_model.prefill(ids)
+    rows = gpu_model.verify_two(77, 78)
+    expected = (int(np.argmax(rows.logits[0])), int(np.argmax(rows.logits[1])))
+    gpu_model.commit_verified(2)
+    after = gpu_model.logits()
+    gpu_model.truncate(prefix)  # same cache contents, no current logits
+    assert gpu_model.verify_two_greedy(77, 78) == expected
+    with pytest.raises(RuntimeError, match='Verification already pending'):
+        gpu_model.verify_two_greedy(77, 78)
+    gpu_model.commit_verified(2)
+    assert gpu_model.position() == prefix + 2
+    assert np.array_equal(gpu_model.logits().view(np.uint32), after.view(np.uint32))
 
 
 @pytest.mark.gpu
