@@ -132,6 +132,29 @@ def prefix_reuse_batch(model, prompts, steps=128):
             'single_sequence_tok_s': single_tps}
 
 
+def verification_pairs(model, token, pairs=32):
+    """Two-token greedy verification as a drafting loop uses it (the
+    protocol's verify-greedy): `pairs` calls of verify_two_greedy, each
+    committing both positions, against the same positions stepped one at a
+    time. The pair runs both rows in one pass over the weights."""
+    start_pos = model.position()
+    t0 = time.perf_counter()
+    for _ in range(pairs):
+        _, token = model.verify_two_greedy(token, token)
+        model.commit_verified(2)
+    pair_ms = (time.perf_counter() - t0) / pairs * 1e3
+    model.truncate(start_pos)
+    t0 = time.perf_counter()
+    for _ in range(pairs):
+        model.step(token)
+        model.step(token)
+    steps_ms = (time.perf_counter() - t0) / pairs * 1e3
+    model.truncate(start_pos)
+    log(f'verification pair {pair_ms:.3f} ms vs two steps {steps_ms:.3f} ms')
+    return {'positions': [start_pos, start_pos + 2 * pairs], 'pairs': pairs, 'pair_ms': pair_ms,
+            'two_steps_ms': steps_ms, 'speedup': steps_ms / pair_ms}
+
+
 # Decode projection shapes (in, out) of the isolated GEMV microbenchmark.
 GEMV_SHAPES = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 151936)]
 
@@ -283,6 +306,7 @@ def main():
     decode_tps = args.steps / elapsed
     log(f'decode {decode_tps:.1f} tok/s')
     context_end = model.position()
+    verification = verification_pairs(model, token)
 
     # Per-kernel average durations with HIP events on the engine stream, at
     # the context length reached by the timed region (attention last: timing
@@ -340,6 +364,7 @@ def main():
                      'traffic': measured_traffic(dominant, context_end),
                      'bytes_per_launch': nbytes},
         'cpu_baseline': baseline,
+        'verification_pair': verification,
         'long_context_decode': long_context,
         'prefix_reuse_batch': batch,
         'gemv_microbench': gemv,

@@ -52,6 +52,9 @@ SIGNATURES = {
     'qwen_gpu_get_options': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Options)]),
     'qwen_gpu_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
     'qwen_gpu_verify_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p, _c_int_p]),
+    'qwen_gpu_top_scores': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_int,
+                                           _c_float_p, _c_int_p]),
+    'qwen_gpu_update_penalized': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, ctypes.c_size_t]),
     'qwen_gpu_verify_two_greedy': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_int_p, _c_int_p]),
     'qwen_gpu_write_random_pack': (ctypes.c_int, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_double, ctypes.c_int]),
     'qwen_gpu_device_malloc': (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
@@ -215,6 +218,21 @@ class Model:
         _check(_LIB.qwen_gpu_verify_two_greedy(self._handle, int(first), int(second), ctypes.byref(a),
                                                ctypes.byref(b)))
         return a.value, b.value
+
+    def top_scores(self, penalty=1.5, temperature=0.7, k=20):
+        """Chat-mode candidates of the current logits: (values, ids) of the k
+        best (logit - (penalized ? penalty : 0)) / temperature, value
+        descending then id ascending."""
+        values = np.zeros(k, dtype=np.float32)
+        ids = np.zeros(k, dtype=np.int32)
+        _check(_LIB.qwen_gpu_top_scores(self._handle, float(penalty), float(temperature), int(k),
+                                        values.ctypes.data_as(_c_float_p), ids.ctypes.data_as(_c_int_p)))
+        return values, ids
+
+    def update_penalized(self, ids=(), clear=False):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        _check(_LIB.qwen_gpu_update_penalized(self._handle, 1 if clear else 0, ids.ctypes.data_as(_c_int_p),
+                                              ids.size))
 
     def time_kernel(self, which, iterations):
         ms = ctypes.c_float()

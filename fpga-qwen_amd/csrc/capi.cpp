@@ -206,6 +206,23 @@ int qwen_gpu_verify_greedy(qwen_gpu_model* m, int* first, int* second) {
     });
 }
 
+int qwen_gpu_top_scores(qwen_gpu_model* m, float penalty, float temperature, int k, float* values, int* ids) {
+    return guarded([&] {
+        need(m, "model");
+        need(values, "values");
+        need(ids, "ids");
+        m->engine.top_scores(penalty, temperature, k, values, ids);
+    });
+}
+
+int qwen_gpu_update_penalized(qwen_gpu_model* m, int clear, const int* ids, size_t count) {
+    return guarded([&] {
+        need(m, "model");
+        if (count) need(ids, "ids");
+        m->engine.update_penalized(clear != 0, ids, count);
+    });
+}
+
 int qwen_gpu_write_random_pack(const char* path, uint64_t seed, double stddev, int threads) {
     return guarded([&] {
         need(path, "path");

@@ -201,7 +201,12 @@ void Engine::init_state() {
     pair_.logits = ver_logits_;
     pair_.hidden = ver_hidden_;
     pair_.result = device_alloc<ArgmaxResult>(2);
+    penalized_ = device_alloc<uint8_t>(kVocab);
+    top_scratch_ = device_alloc<uint8_t>(top_scores_scratch_bytes());
+    top_device_ = device_alloc<TopScores>(1);
     void* pinned = nullptr;
+    HIP_CHECK(hipHostMalloc(&pinned, sizeof(TopScores), hipHostMallocDefault));
+    top_host_ = static_cast<TopScores*>(pinned);
     HIP_CHECK(hipHostMalloc(&pinned, sizeof(float) * 2 * (size_t(kVocab) + kHidden), hipHostMallocDefault));
     ver_host_ = static_cast<float*>(pinned);
     HIP_CHECK(hipHostMalloc(&pinned, sizeof(ArgmaxResult) * 3, hipHostMallocDefault));
@@ -218,6 +223,7 @@ void Engine::init_state() {
     ids_dev_ = device_alloc<int>(size_t(ctx));
     HIP_CHECK(hipHostMalloc(&pinned, sizeof(int) * size_t(ctx), hipHostMallocDefault));
     ids_host_ = static_cast<int*>(pinned);
+    launch_mark_penalized(penalized_, true, nullptr, 0, stream_);
     HIP_CHECK(hipStreamSynchronize(stream_));
     HIP_CHECK(hipGetLastError());
 }
@@ -228,6 +234,8 @@ void Engine::release() {
     if (result_host_) (void)hipHostFree(result_host_);
     if (ver_host_) (void)hipHostFree(ver_host_);
     ver_host_ = nullptr;
+    if (top_host_) (void)hipHostFree(top_host_);
+    top_host_ = nullptr;
     if (ids_host_) (void)hipHostFree(ids_host_);
     ids_host_ = nullptr;
     if (stream_) (void)hipStreamDestroy(stream_);
@@ -465,6 +473,36 @@ void Engine::verify_greedy(int* first, int* second) {
         if (result_host_[1 + row].nonfinite) throw std::runtime_error("Nonfinite model logits");
     *first = result_host_[1].token;
     *second = result_host_[2].token;
+}
+
+void Engine::top_scores(float penalty, float temperature, int k, float* values, int* ids) {
+    require(k >= 1 && k <= kTopMax, "top scores: k must be 1..32");
+    require(std::isfinite(penalty) && std::isfinite(temperature) && temperature > 0.f,
+            "top scores: penalty and temperature must be finite, temperature positive");
+    require(has_logits_, "No current full-vocabulary logits");
+    if (result_host_[0].nonfinite) throw std::runtime_error("Nonfinite model logits");
+    launch_top_scores(scratch_.logits, penalized_, penalty, temperature, k, top_scratch_, top_device_, top_host_,
+                      stream_);
+    HIP_CHECK(hipGetLastError());
+    sync();
+    std::copy(top_host_->value, top_host_->value + k, values);
+    std::copy(top_host_->id, top_host_->id + k, ids);
+}
+
+void Engine::update_penalized(bool clear, const int* ids, size_t count) {
+    for (size_t i = 0; i < count; ++i) require(ids[i] >= 0 && ids[i] < kVocab, "Token ID out of range");
+    if (clear) launch_mark_penalized(penalized_, true, nullptr, 0, stream_);
+    // Staged through the prompt-id buffers, one context-sized piece at a time.
+    const size_t piece = size_t(options_.context);
+    for (size_t done = 0; done < count; done += piece) {
+        const size_t n = std::min(piece, count - done);
+        std::copy(ids + done, ids + done + n, ids_host_);
+        HIP_CHECK(hipMemcpyAsync(ids_dev_, ids_host_, n * sizeof(int), hipMemcpyHostToDevice, stream_));
+        launch_mark_penalized(penalized_, false, ids_dev_, int(n), stream_);
+        sync();
+    }
+    HIP_CHECK(hipGetLastError());
+    sync();
 }
 
 // engine/core.cpp:742-752

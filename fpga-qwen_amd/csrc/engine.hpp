@@ -9,6 +9,7 @@
 
 #include "kernels.hpp"
 #include "prefill.hpp"
+#include "sampler.hpp"
 
 namespace qwen_hip {
 
@@ -65,6 +66,13 @@ public:
     int greedy();
     // Greedy selections of the pending verification rows.
     void verify_greedy(int* first, int* second);
+    // Chat-mode candidates of the current logits (engine/main.cpp:51-62):
+    // the k best (logit - (penalized ? penalty : 0)) / temperature, value
+    // descending then id ascending; k in 1..kTopMax.
+    void top_scores(float penalty, float temperature, int k, float* values, int* ids);
+    // The penalized-token flags (the sampler's consumed ids): cleared first
+    // when `clear`, then ids[0..count) set.
+    void update_penalized(bool clear, const int* ids, size_t count);
     const Options& options() const { return options_; }
 
     // Average duration (ms) of one standalone launch of a decode kernel,
@@ -105,6 +113,10 @@ private:
     float* sines_ = nullptr;
     DecodeScratch scratch_{};
     ArgmaxResult* result_host_ = nullptr;  // pinned [3]: current, verify row 0, verify row 1
+    uint8_t* penalized_ = nullptr;         // device [vocab] flags of the chat sampler
+    void* top_scratch_ = nullptr;          // device candidates of top_scores
+    TopScores* top_device_ = nullptr;
+    TopScores* top_host_ = nullptr;        // pinned
     float* ver_logits_ = nullptr;   // device [2 x vocab]
     float* ver_hidden_ = nullptr;   // device [2 x 1024]
     float* base_logits_ = nullptr;  // public logits saved across a two-step verification

@@ -57,44 +57,53 @@ bool is_eos(int id) { return id == 151643 || id == 151645; }
 // Sampler semantics of engine/main.cpp:40-70: greedy = argmax (lowest id on
 // ties); chat = presence penalty 1.5, temperature 0.7, top-k 20, top-p 0.8,
 // mt19937_64 seeded per request.
+// engine/main.cpp:40-70. The seen set (presence penalty) is kept here and
+// mirrored into the model's device flags; the scores and their partial sort
+// run on the GPU (qwen_gpu_top_scores), and only the 20 candidates come back
+// for the top-p draw below, which is the reference's arithmetic.
 class Sampler {
 public:
-    void reset() { std::fill(seen_.begin(), seen_.end(), 0); }
+    void reset() {
+        std::fill(seen_.begin(), seen_.end(), 0);
+        clear_ = true;
+        fresh_.clear();
+    }
     void mode(bool chat, uint64_t seed) {
         chat_ = chat;
         rng_.seed(seed);
     }
-    void consumed(int id) { seen_.at(size_t(id)) = 1; }
+    void consumed(int id) {
+        if (!seen_.at(size_t(id))) fresh_.push_back(id);
+        seen_[size_t(id)] = 1;
+    }
     bool greedy() const { return !chat_; }
-    int chat_select(const std::vector<float>& logits) {
-        if (logits.size() != size_t(kV)) throw std::runtime_error("No current full-vocabulary logits");
-        for (int id = 0; id < kV; ++id) {
-            if (!std::isfinite(logits[id])) throw std::runtime_error("Nonfinite model logits");
-            scores_[id] = {(logits[id] - (seen_[id] ? 1.5f : 0.f)) / .7f, id};
+    int chat_select(qwen_gpu::Model& model) {
+        if (clear_ || !fresh_.empty()) {
+            model.update_penalized(clear_, fresh_);
+            clear_ = false;
+            fresh_.clear();
         }
-        std::partial_sort(scores_.begin(), scores_.begin() + 20, scores_.end(), [](const Score& a, const Score& b) {
-            return a.value > b.value || (a.value == b.value && a.id < b.id);
-        });
-        double p[20], total = 0;
-        for (int i = 0; i < 20; ++i) total += (p[i] = std::exp(double(scores_[i].value) - scores_[0].value));
+        float value[kTop];
+        int id[kTop];
+        model.top_scores(1.5f, .7f, kTop, value, id);
+        double p[kTop], total = 0;
+        for (int i = 0; i < kTop; ++i) total += (p[i] = std::exp(double(value[i]) - value[0]));
         double kept = 0;
         int count = 0;
         do {
             kept += p[count++];
-        } while (count < 20 && kept < .8 * total);
+        } while (count < kTop && kept < .8 * total);
         double draw = std::generate_canonical<double, 53>(rng_) * kept;
         for (int i = 0; i < count; ++i)
-            if ((draw -= p[i]) < 0) return scores_[i].id;
-        return scores_[count - 1].id;
+            if ((draw -= p[i]) < 0) return id[i];
+        return id[count - 1];
     }
 
 private:
-    struct Score {
-        float value;
-        int id;
-    };
+    static constexpr int kTop = 20;
     std::vector<unsigned char> seen_ = std::vector<unsigned char>(size_t(kV), 0);
-    std::vector<Score> scores_ = std::vector<Score>(size_t(kV));
+    std::vector<int> fresh_;  // seen since the last upload
+    bool clear_ = true;       // the device flags predate the last reset
     std::mt19937_64 rng_{0};
     bool chat_ = false;
 };
@@ -139,7 +148,7 @@ int main(int argc, char** argv) {
         std::vector<int> history;
         history.reserve(size_t(options.context));
         handshake(options, model);
-        auto select = [&]() { return sampler.greedy() ? model.greedy() : sampler.chat_select(model.logits()); };
+        auto select = [&]() { return sampler.greedy() ? model.greedy() : sampler.chat_select(model); };
         std::string line;
         while (std::getline(std::cin, line)) {
             try {

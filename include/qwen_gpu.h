@@ -107,6 +107,21 @@ int qwen_gpu_verify_greedy(qwen_gpu_model* model, int* first, int* second);
 int qwen_gpu_verify_two_greedy(qwen_gpu_model* model, int first, int second, int* first_choice,
                                int* second_choice);
 
+/* Chat-mode candidates of the current logits on the GPU (engine/main.cpp:
+ * 51-62: score = (logit - (seen ? 1.5 : 0)) / 0.7, partial sort of the 20
+ * best by value descending, id ascending): the k (1..32) best scores
+ * (logit - (penalized ? penalty : 0)) / temperature in that order, with their
+ * ids. Only these leave the device; the caller draws from them. Fails with
+ * "No current full-vocabulary logits" or "Nonfinite model logits" like the
+ * reference's select. */
+int qwen_gpu_top_scores(qwen_gpu_model* model, float penalty, float temperature, int k, float* values,
+                        int* ids);
+/* The model's penalized-token flags, the device copy of the sampler's seen
+ * set (engine/main.cpp:42,47-49): cleared when `clear` is nonzero, then
+ * ids[0..count) set. All flags start clear; reset/truncate leave them as
+ * they are (the sampler owns them, as in the reference). */
+int qwen_gpu_update_penalized(qwen_gpu_model* model, int clear, const int* ids, size_t count);
+
 /* Synthetic QWCPU01 pack (format: engine/INTERFACE.md:8-21; tensor order of
  * tools/export_native_cpu_weights.py:29-39): matrices N(0, stddev) rounded to
  * FP16 from a counter-based splitmix64 Box-Muller stream, norm gains 1.0.

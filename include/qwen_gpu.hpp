@@ -98,6 +98,13 @@ public:
         detail::check(qwen_gpu_verify_greedy(handle_.get(), &a, &b));
         return {a, b};
     }
+    // Chat-mode candidates (qwen_gpu_top_scores): fills values/ids[0..k).
+    void top_scores(float penalty, float temperature, int k, float* values, int* ids) const {
+        detail::check(qwen_gpu_top_scores(handle_.get(), penalty, temperature, k, values, ids));
+    }
+    void update_penalized(bool clear, const std::vector<int>& ids) {
+        detail::check(qwen_gpu_update_penalized(handle_.get(), clear ? 1 : 0, ids.data(), ids.size()));
+    }
     // verify_two + verify_greedy without copying the rows to the host.
     std::pair<int, int> verify_two_greedy(int first, int second) {
         int a = 0, b = 0;
