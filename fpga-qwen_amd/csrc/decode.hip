@@ -308,6 +308,80 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     }
 }
 
+// Long-row GEMV (O: 2048 columns, down: 3072) with each chain split into
+// SEG consecutive segments of its blocks. A workgroup covers half a tile
+// (4 rows x 8 chains = 32 lanes per segment); segment s sits in wave s / 2,
+// lanes 32 (s % 2) .. +31. Every lane loads only its segment's blocks, so
+// twice (SEG = 2) or four times (SEG = 4, two waves) as many lanes stream
+// the matrix as in gemv_kernel, spread over twice the workgroups. The
+// running sum moves from segment to segment (lane l -> l + 32 inside a
+// wave, through LDS between waves), so each chain performs exactly the
+// reference's FMA sequence and the result equals gemv_kernel's bit for bit.
+template <int N, int SEG, int MODE, bool PARTS = false>
+__global__ __launch_bounds__(SEG * 32) void gemv_seg_kernel(const GemvArgs a) {
+    static_assert(SEG == 2 || SEG == 4, "segments: 2 or 4");
+    static_assert(MODE == kPlain || MODE == kO || MODE == kDown, "long-row modes only");
+    constexpr int THREADS = SEG * 32, WAVES = SEG / 2, PER = N / THREADS, NB = N / 64, NBS = NB / SEG;
+    static_assert(NB % SEG == 0, "segments must split the blocks evenly");
+    __shared__ float4 xs4[N / 4];
+    __shared__ float hand[32];
+    float* xs = reinterpret_cast<float*>(xs4);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = blockIdx.x >> 1, half = blockIdx.x & 1;
+    const int l32 = lane & 31, c = l32 & 7, r = l32 >> 3;
+    const int seg = 2 * wave + (lane >> 5);
+    const int row = tile * 8 + 4 * half + r;
+
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
+    float xres = 0.f, prow[kKVHeads];
+    if constexpr (MODE == kO || MODE == kDown) xres = a.x[row];
+    if constexpr (PARTS) {
+#pragma unroll
+        for (int g = 0; g < kKVHeads; ++g) prow[g] = a.parts[g * kHidden + row];
+    }
+    u32x4 wv[NBS];
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w) + (size_t(tile) * NB + size_t(seg) * NBS) * 64 +
+                          32 * half + l32;
+#pragma unroll
+        for (int b = 0; b < NBS; ++b) wv[b] = __builtin_nontemporal_load(wp + b * 64);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PARTS) xres = fold_parts(xres, prow);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[k];
+    __syncthreads();
+
+    // Phase p of wave w runs segment 2w + p: the lanes of that segment hold
+    // the true running sum, the other half of the wave computes a discarded
+    // value with the same instructions.
+    const float4* x4 = xs4 + 16 * (seg * NBS) + 2 * c;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+        if (wave == w) {
+            if (w > 0) acc = hand[l32];
+#pragma unroll
+            for (int b = 0; b < NBS; ++b) acc = chain8(acc, wv[b], x4[16 * b], x4[16 * b + 1]);
+            acc = __shfl_xor(acc, 32);  // lower half's sum to the upper half
+#pragma unroll
+            for (int b = 0; b < NBS; ++b) acc = chain8(acc, wv[b], x4[16 * b], x4[16 * b + 1]);
+            if (w + 1 < WAVES && lane >= 32) hand[l32] = acc;
+        }
+        if (w + 1 < WAVES) __syncthreads();
+    }
+    if (wave == WAVES - 1) {
+        const float y = combine_chains(acc);
+        if (lane >= 32 && c == 0) {
+            if constexpr (MODE == kPlain) a.out[row] = y;
+            else a.x[row] = xres + y;
+        }
+    }
+}
+
 // Second pass of the greedy selection: one workgroup reduces the per-group
 // (max, lowest id, nonfinite) partials of the lm_head kernel.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ value, const int* __restrict__ index,
@@ -923,12 +997,21 @@ template <int MODE>
 constexpr int gemv_waves() {
     if constexpr (MODE == kQKV) return 2;
     else if constexpr (MODE == kGateUp) return 4;
-    else if constexpr (MODE == kDown) return 1;
     else return kLayerWaves;
 }
 
 template <int N, int MODE>
 void launch_gemv(const GemvArgs& a, int rows, hipStream_t stream) {
+    if constexpr (N > kHidden) {  // long rows (O, down, plain 2048/3072): two-segment chains
+        if constexpr (MODE == kDown) {
+            if (a.parts) {
+                gemv_seg_kernel<N, 2, MODE, true><<<rows / 4, 64, 0, stream>>>(a);
+                return;
+            }
+        }
+        gemv_seg_kernel<N, 2, MODE><<<rows / 4, 64, 0, stream>>>(a);
+        return;
+    }
     constexpr int W = gemv_waves<MODE>();
     if constexpr (MODE == kGateUp || MODE == kDown) {
         if (a.parts) {
