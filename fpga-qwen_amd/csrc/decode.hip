@@ -66,11 +66,13 @@ __device__ __forceinline__ double wave_sum(double v) {
 // stored at 64b + 8c + i, so chain c reads its 8 values contiguously.
 __device__ __forceinline__ int xperm(int j) { return (j & ~63) | ((j & 7) << 3) | ((j >> 3) & 7); }
 
-// Residual stream entry x + the 8 per-KV-head partial O projections of the
-// fused attention kernel, summed in a fixed tree order (every kernel that
-// reads the entry gets the same value).
-__device__ __forceinline__ float fold_parts(float x, const float (&p)[kKVHeads]) {
-    return x + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+// Residual stream entry x + the 16 per-query-head partial O projections of
+// the fused attention kernel, summed in a fixed tree order (every kernel
+// that reads the entry gets the same value).
+__device__ __forceinline__ float fold_parts(float x, const float (&p)[kOParts]) {
+    const float lo = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    const float hi = ((p[8] + p[9]) + (p[10] + p[11])) + ((p[12] + p[13]) + (p[14] + p[15]));
+    return x + (lo + hi);
 }
 
 // RMSNorm (engine/core.cpp:207-215) of N values held PER = N / THREADS per
@@ -131,13 +133,13 @@ enum GemvMode { kPlain, kQKV, kO, kGateUp, kDown, kLmHead };
 
 // With ROWS input vectors (two-token verification), row q of each per-row
 // buffer starts q strides in: in + q N, x / hidden + q 1024, parts +
-// q 8192, out + q out_stride, lm partials + q gridDim.x.
+// q 16384, out + q out_stride, lm partials + q gridDim.x.
 struct GemvArgs {
     const uint16_t* w;        // chain-tiled weights
     const float* in;          // input vector (plain; O: attention output; down), residual x (norm modes)
     const float* norm_w;      // RMSNorm weights (QKV, gate/up, lm_head)
     const uint16_t* embed;    // natural embedding, first layer only (QKV)
-    const float* parts;       // gate/up, down: pending [8][1024] O partials (fused attention), or null
+    const float* parts;       // gate/up, down: pending [16][1024] O partials (fused attention), or null
     int token[2];             // first-layer QKV: embedding row of each input row
     int out_stride;           // ROWS > 1: distance between the rows' outputs
     float* out;               // plain/QKV: y; gate/up: activation; lm_head: logits
@@ -192,15 +194,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     }
     // Pending O partials: of this thread's inputs (gate/up) or of this
     // lane's output row (down).
-    float pin[ROWS][PARTS && MODE == kGateUp ? PER : 1][kKVHeads], prow[ROWS][kKVHeads];
+    float pin[ROWS][PARTS && MODE == kGateUp ? PER : 1][kOParts], prow[ROWS][kOParts];
     if constexpr (PARTS && MODE == kGateUp) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q)
 #pragma unroll
             for (int k = 0; k < PER; ++k)
 #pragma unroll
-                for (int g = 0; g < kKVHeads; ++g)
-                    pin[q][k][g] = a.parts[(q * kKVHeads + g) * kHidden + tid + k * THREADS];
+                for (int g = 0; g < kOParts; ++g)
+                    pin[q][k][g] = a.parts[(q * kOParts + g) * kHidden + tid + k * THREADS];
     }
     float xres[ROWS];  // residual entry of this lane's row (O, down)
 #pragma unroll
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         if constexpr (MODE == kO || MODE == kDown) xres[q] = a.x[q * kHidden + row];
         if constexpr (PARTS && MODE == kDown) {
 #pragma unroll
-            for (int g = 0; g < kKVHeads; ++g) prow[q][g] = a.parts[(q * kKVHeads + g) * kHidden + row];
+            for (int g = 0; g < kOParts; ++g) prow[q][g] = a.parts[(q * kOParts + g) * kHidden + row];
         }
     }
 
@@ -325,11 +327,11 @@ __global__ __launch_bounds__(SEG * 32) void gemv_seg_kernel(const GemvArgs a) {
     float v[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
-    float xres = 0.f, prow[kKVHeads];
+    float xres = 0.f, prow[kOParts];
     if constexpr (MODE == kO || MODE == kDown) xres = a.x[row];
     if constexpr (PARTS) {
 #pragma unroll
-        for (int g = 0; g < kKVHeads; ++g) prow[g] = a.parts[g * kHidden + row];
+        for (int g = 0; g < kOParts; ++g) prow[g] = a.parts[g * kHidden + row];
     }
     u32x4 wv[NBS];
     __builtin_amdgcn_sched_barrier(0);
@@ -419,7 +421,7 @@ struct AttnArgs {
     float* partial;        // [8][kAttnSplits][kAttnPartial]
     float* attended;       // [2048], written instead when there is one split
     const uint16_t* o_n;   // fused: natural O weights [1024 x 2048]
-    float* o_part;         // fused: [8][1024] partial O projections
+    float* o_part;         // fused: [16][1024] partial O projections
     int context;
     float scale;           // 1.0f / sqrt(128.0f)
 };
@@ -721,13 +723,13 @@ __global__ __launch_bounds__(128) void attn_merge_batch_kernel(const AttnBatch b
 }
 
 // Fused attention + O projection for n <= kFusedMaxPositions. Workgroup
-// (g, rb), g = blockIdx.x % 8 so the workgroups of one KV head share an XCD
-// (and its L2 copy of the head's K/V rows), rb = blockIdx.x / 8. Every
-// workgroup of head g computes that head's attention over all n positions
-// (scores in the reference dot's chain order, engine/core.cpp:612; softmax
-// and P.V as in 613-620), then its kAttnORows rows of O against the 256
-// attention outputs of query heads 2g, 2g+1: o_part[g][row] =
-// sum_i O[row][256g + i] * att[i].
+// blockIdx = 8m + g: KV head g (so the 32 workgroups reading one head's K/V
+// rows share an XCD and its L2 copy of them), query head h = 2g + m % 2,
+// block rb = m / 2 of kAttnORows O rows. Every workgroup computes its query
+// head's attention over all n positions (scores in the reference dot's chain
+// order, engine/core.cpp:612; softmax and P.V as in 613-620), then its rows
+// of O against the head's 128 attention outputs:
+// o_part[h][row] = sum_i O[row][128h + i] * att[i].
 // 512 threads, PASSES = ceil(n / 64) passes of 64 positions (a template
 // parameter so that every load is unconditional and the compiler waits for
 // exactly the loads each phase needs). Wave w owns positions 64p + 8w + i,
@@ -742,10 +744,13 @@ __global__ __launch_bounds__(128) void attn_merge_batch_kernel(const AttnBatch b
 // exact zeros), so its output equals a single-row launch at its position.
 template <int PASSES, int ROWS = 1>
 __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
-    const int g = blockIdx.x % kKVHeads, rb = blockIdx.x / kKVHeads;
+    const int g = blockIdx.x % kKVHeads, m = blockIdx.x / kKVHeads;
+    const int h = 2 * g + (m & 1), rb = m >> 1;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = a.pos;
     const size_t head_base = size_t(g) * a.context;
+    // Threads 0-127: q of head h, 128-255: k, 256-383: v (384-511 repeat v
+    // and write nothing).
     const int quarter = tid >> 7, j = tid & 127, c = tid & 7, grp = tid >> 3;
     const int vsub = lane >> 4, vcg = lane & 15;  // P.V: position within a group of 4, channel group
 
@@ -754,16 +759,13 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     // rotation, cached K rows, V rows, then this workgroup's O weights. Rows
     // from pos on (taken from LDS) or past them load row 0 instead and are
     // not used.
-    float raw[ROWS], raw_v[ROWS], rc[ROWS], rs[ROWS];
+    float raw[ROWS], rc[ROWS], rs[ROWS];
+    const int src = quarter == 0 ? h * 128 + j : (quarter == 1 ? 2048 : 3072) + g * 128 + j;
 #pragma unroll
-    for (int q = 0; q < ROWS; ++q) {
-        const float* qkv = a.qkv + q * kQKVRows;
-        raw[q] = quarter < 2 ? qkv[(2 * g + quarter) * 128 + j] : qkv[2048 + g * 128 + j];
-        raw_v[q] = qkv[3072 + g * 128 + j];
-    }
+    for (int q = 0; q < ROWS; ++q) raw[q] = a.qkv[q * kQKVRows + src];
     // quarter is uniform per wave; selecting the pointer on a scalar keeps it
     // out of vector registers (no per-lane load of the kernel argument).
-    const float nw = (__builtin_amdgcn_readfirstlane(quarter) < 2 ? a.q_norm : a.k_norm)[j];
+    const float nw = (__builtin_amdgcn_readfirstlane(quarter) == 0 ? a.q_norm : a.k_norm)[j];
 #pragma unroll
     for (int q = 0; q < ROWS; ++q) {
         rc[q] = a.cosines[size_t(pos + q) * 64 + (j & 63)];
@@ -788,41 +790,42 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
         }
     __builtin_amdgcn_sched_barrier(0);
     // O rows: kThreadsPerRow threads per row; load i of thread part q holds
-    // the 8 columns 8 (q + kThreadsPerRow i) .. +7 of the head's 256, so the
+    // the 8 columns 8 (q + kThreadsPerRow i) .. +7 of the head's 128, so the
     // lanes of one row read consecutive 16-byte pieces.
-    constexpr int kThreadsPerRow = 512 / kAttnORows, kLoads = 256 / 8 / kThreadsPerRow;
+    constexpr int kThreadsPerRow = 512 / kAttnORows, kLoads = 128 / 8 / kThreadsPerRow;
     const int orow = rb * kAttnORows + tid / kThreadsPerRow, opart_id = tid % kThreadsPerRow;
     u32x4 ow[kLoads];
     {
-        const u32x4* op = reinterpret_cast<const u32x4*>(a.o_n + size_t(orow) * kQDim + 256 * g) + opart_id;
+        const u32x4* op = reinterpret_cast<const u32x4*>(a.o_n + size_t(orow) * kQDim + 128 * h) + opart_id;
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) ow[i] = __builtin_nontemporal_load(op + kThreadsPerRow * i);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    __shared__ float qp[ROWS][2][128];
+    __shared__ float qp[ROWS][128];
     __shared__ float buf[ROWS][4][128];
-    __shared__ float prob[ROWS][2][kFusedMaxPositions];
-    __shared__ float opart[8][4][2][128];
-    __shared__ __align__(16) float att[ROWS][256];
+    __shared__ float prob[ROWS][kFusedMaxPositions];
+    __shared__ float opart[8][4][128];
+    __shared__ __align__(16) float att[ROWS][128];
     __shared__ uint16_t kcur[ROWS][128], vcur[ROWS][128];
     __shared__ double red[ROWS][4][2];
-    __shared__ float wmax[8][2], wsum[8][2];
+    __shared__ float wmax[8], wsum[8];
 
-    // QK-norm + RoPE (engine/core.cpp:395-402); workgroup rb == 0 writes the
-    // new K/V rows (403-406). The others only read rows t < pos.
-    const bool owner = rb == 0;
+    // QK-norm + RoPE (engine/core.cpp:395-402); one workgroup per KV head
+    // (m == 0) writes the new K/V rows (403-406). The others only read rows
+    // t < pos.
+    const bool owner = m == 0;
 #pragma unroll
     for (int q = 0; q < ROWS; ++q) {
         const float r = head_norm_rope(raw[q], nw, rc[q], rs[q], red[q][quarter], buf[q][quarter], j);
-        if (quarter < 2) {
-            qp[q][quarter][kperm(j)] = r;
-        } else if (quarter == 2) {
+        if (quarter == 0) {
+            qp[q][kperm(j)] = r;
+        } else if (quarter == 1) {
             const uint16_t bits = f2h(r);
             kcur[q][kperm(j)] = bits;
             if (owner) a.keys[(head_base + pos + q) * 128 + kperm(j)] = bits;
-        } else {
-            const uint16_t bits = f2h(raw_v[q]);
+        } else if (quarter == 2) {
+            const uint16_t bits = f2h(raw[q]);
             vcur[q][j] = bits;
             if (owner) a.values[(head_base + pos + q) * 128 + j] = bits;
         }
@@ -834,8 +837,8 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
         const int n = pos + q + 1;
         // Scores of this wave's positions (every lane of a position's group
         // of 8 holds the combined value) and the wave's running maximum.
-        float s0[PASSES], s1[PASSES];
-        float m0 = -INFINITY, m1 = -INFINITY;
+        float s0[PASSES];
+        float m0 = -INFINITY;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int t = p * 64 + grp, cur = t - pos;
@@ -846,54 +849,40 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
                 kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
                 kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
             }
-            const float d0 = combine_chains(key_chain(qp[q][0], c, kw, 0.f)) * a.scale;
-            const float d1 = combine_chains(key_chain(qp[q][1], c, kw, 0.f)) * a.scale;
+            const float d0 = combine_chains(key_chain(qp[q], c, kw, 0.f)) * a.scale;
             s0[p] = t < n ? d0 : -INFINITY;
-            s1[p] = t < n ? d1 : -INFINITY;
             m0 = fmaxf(m0, s0[p]);
-            m1 = fmaxf(m1, s1[p]);
         }
 #pragma unroll
-        for (int off = 8; off < 64; off <<= 1) {
-            m0 = fmaxf(m0, __shfl_xor(m0, off));
-            m1 = fmaxf(m1, __shfl_xor(m1, off));
-        }
+        for (int off = 8; off < 64; off <<= 1) m0 = fmaxf(m0, __shfl_xor(m0, off));
         // Probabilities relative to the wave maximum (a wave without
         // positions keeps m = -inf and contributes nothing).
-        float l0 = 0.f, l1 = 0.f;
+        float l0 = 0.f;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int t = p * 64 + grp;
             const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
-            const float p1 = t < n ? expf(s1[p] - m1) : 0.f;
             l0 += p0;
-            l1 += p1;
-            if (c == 0) {
-                prob[q][0][t] = p0;
-                prob[q][1][t] = p1;
-            }
+            if (c == 0) prob[q][t] = p0;
         }
 #pragma unroll
-        for (int off = 8; off < 64; off <<= 1) {
-            l0 += __shfl_xor(l0, off);
-            l1 += __shfl_xor(l1, off);
-        }
-        // prob[q][][t] of this wave's positions is written and read by this
+        for (int off = 8; off < 64; off <<= 1) l0 += __shfl_xor(l0, off);
+        // prob[q][t] of this wave's positions is written and read by this
         // wave only.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        float acc[2][8];
+        float acc[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[0][i] = acc[1][i] = 0.f;
+        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p)
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
                 const int t = p * 64 + 8 * wave + 4 * hf + vsub, cur = t - pos;
                 if (t < n) {
-                    const float p0 = prob[q][0][t], p1 = prob[q][1][t];
+                    const float p0 = prob[q][t];
                     uint32_t vw[4];
                     if (cur >= 0) {  // cur <= q here since t < n
 #pragma unroll
@@ -905,37 +894,29 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
                     }
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
-                        acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
-                        acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
-                        acc[1][2 * i] = __builtin_fmaf(v0, p1, acc[1][2 * i]);
-                        acc[1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[1][2 * i + 1]);
+                        acc[2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p0, acc[2 * i]);
+                        acc[2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p0, acc[2 * i + 1]);
                     }
                 }
             }
         if (q > 0) __syncthreads();  // the previous row's merge has read opart / wmax / wsum
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) opart[wave][vsub][h][vcg * 8 + i] = acc[h][i];
+        for (int i = 0; i < 8; ++i) opart[wave][vsub][vcg * 8 + i] = acc[i];
         if (lane == 0) {
-            wmax[wave][0] = m0;
-            wmax[wave][1] = m1;
-            wsum[wave][0] = l0;
-            wsum[wave][1] = l1;
+            wmax[wave] = m0;
+            wsum[wave] = l0;
         }
         __syncthreads();
-        if (tid < 256) {
-            const int h = tid >> 7;
-            float mx = wmax[0][h];
+        if (tid < 128) {
+            float mx = wmax[0];
 #pragma unroll
-            for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w][h]);
+            for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w]);
             float l = 0.f, o = 0.f;
 #pragma unroll
             for (int w = 0; w < 8; ++w) {
-                const float e = wmax[w][h] == -INFINITY ? 0.f : expf(wmax[w][h] - mx);
-                const float ow4 = (opart[w][0][h][j] + opart[w][1][h][j]) + (opart[w][2][h][j] + opart[w][3][h][j]);
-                l = __builtin_fmaf(e, wsum[w][h], l);
+                const float e = wmax[w] == -INFINITY ? 0.f : expf(wmax[w] - mx);
+                const float ow4 = (opart[w][0][tid] + opart[w][1][tid]) + (opart[w][2][tid] + opart[w][3][tid]);
+                l = __builtin_fmaf(e, wsum[w], l);
                 o = __builtin_fmaf(e, ow4, o);
             }
             att[q][tid] = o / l;
@@ -943,8 +924,7 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     }
     __syncthreads();
 
-    // This workgroup's rows of O against the 256 outputs of the KV head's
-    // query heads.
+    // This workgroup's rows of O against the head's 128 attention outputs.
 #pragma unroll
     for (int q = 0; q < ROWS; ++q) {
         float y = 0.f;
@@ -954,7 +934,7 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
             y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
 #pragma unroll
         for (int off = 1; off < kThreadsPerRow; off <<= 1) y += __shfl_xor(y, off);
-        if (opart_id == 0) a.o_part[(q * kKVHeads + g) * kHidden + orow] = y;
+        if (opart_id == 0) a.o_part[(q * kOParts + h) * kHidden + orow] = y;
     }
 }
 

@@ -184,7 +184,7 @@ void Engine::init_state() {
     s.logits = device_alloc<float>(kVocab);
     s.hidden = device_alloc<float>(kHidden);
     s.attn_partial = device_alloc<float>(size_t(kKVHeads) * kAttnSplits * kAttnPartial);
-    s.o_part = device_alloc<float>(size_t(kKVHeads) * kHidden);
+    s.o_part = device_alloc<float>(size_t(kOParts) * kHidden);
     s.lm_value = device_alloc<float>(size_t(kBatchLmGroups) * kMaxBatch);
     s.lm_index = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
     s.lm_bad = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
@@ -197,7 +197,7 @@ void Engine::init_state() {
     pair_.qkv = device_alloc<float>(2 * kQKVRows);
     pair_.attended = device_alloc<float>(2 * kQDim);
     pair_.act = device_alloc<float>(2 * kFFN);
-    pair_.o_part = device_alloc<float>(size_t(2) * kKVHeads * kHidden);
+    pair_.o_part = device_alloc<float>(size_t(2) * kOParts * kHidden);
     pair_.logits = ver_logits_;
     pair_.hidden = ver_hidden_;
     pair_.result = device_alloc<ArgmaxResult>(2);

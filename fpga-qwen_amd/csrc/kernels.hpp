@@ -46,15 +46,16 @@ __host__ __device__ inline void attn_split(int n, int& chunk, int& splits) {
 }
 
 // Contexts of up to 512 positions take the fused attention + O-projection
-// kernel: one workgroup per (KV head, block of kAttnORows O rows) attends
-// over all positions of its head (K/V rows are re-read from L2 by the 32
-// workgroups of a head, which share an XCD), then multiplies its two query
-// heads' 256 attention outputs into its rows of O. The 8 per-head partial
+// kernel: one workgroup per (query head, block of kAttnORows O rows) attends
+// over all positions of the head (K/V rows are re-read from L2 by the 32
+// workgroups of a KV head, which share an XCD), then multiplies the head's
+// 128 attention outputs into its rows of O. The kOParts per-head partial
 // sums of O.att land in o_part and are added to the residual stream by the
 // gate/up prologue and the down epilogue, in a fixed order.
 inline constexpr int kFusedMaxPositions = 512;
-inline constexpr int kAttnORows = 32;
-inline constexpr int kAttnOGroups = kKVHeads * (kHidden / kAttnORows);  // 256 workgroups
+inline constexpr int kAttnORows = 64;
+inline constexpr int kOParts = kQHeads;                                // 16 partial O projections
+inline constexpr int kAttnOGroups = kQHeads * (kHidden / kAttnORows);  // 256 workgroups
 __host__ __device__ inline bool attn_fused(int n) { return n <= kFusedMaxPositions; }
 
 inline constexpr int kMaxBatch = 8;             // sequences per batched decode step
@@ -91,7 +92,7 @@ struct DecodeScratch {
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
-    float* o_part;        // [8][1024]: per-KV-head partial O projections (fused path)
+    float* o_part;        // [16][1024]: per-query-head partial O projections (fused path)
     float* lm_value;      // [kBatchLmGroups x kMaxBatch] argmax partials (batch-1 uses kLmGroups)
     int* lm_index;
     int* lm_bad;
@@ -131,7 +132,7 @@ struct PairScratch {
     float* qkv;           // [2][4096]
     float* attended;      // [2][2048] (split attention)
     float* act;           // [2][3072]
-    float* o_part;        // [2][8][1024] (fused attention)
+    float* o_part;        // [2][16][1024] (fused attention)
     float* logits;        // [2][151936]
     float* hidden;        // [2][1024]
     ArgmaxResult* result; // [2] device copies of the selections
