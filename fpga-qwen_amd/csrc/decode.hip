@@ -76,9 +76,9 @@ __device__ __forceinline__ float fold_parts(float x, const float (&p)[kOParts]) 
 }
 
 // RMSNorm (engine/core.cpp:207-215) of N values held PER = N / THREADS per
-// thread (element j = tid + k THREADS), with their norm weights, into
-// permuted LDS (and optionally to `copy`).
-template <int N, int THREADS>
+// thread (element j = tid + k THREADS, or j = PER tid + k when CONTIG), with
+// their norm weights, into permuted LDS (and optionally to `copy`).
+template <int N, int THREADS, bool CONTIG = false>
 __device__ __forceinline__ void norm_to_lds(const float (&v)[N / THREADS], const float (&w)[N / THREADS], float* xs,
                                             double* red, float* copy) {
     constexpr int PER = N / THREADS;
@@ -99,7 +99,7 @@ __device__ __forceinline__ void norm_to_lds(const float (&v)[N / THREADS], const
     const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(N) + 1e-6f);
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int j = tid + k * THREADS;
+        const int j = CONTIG ? PER * tid + k : tid + k * THREADS;
         const float o = (v[k] * inv) * w[k];
         xs[xperm(j)] = o;
         if (copy) copy[j] = o;
@@ -170,39 +170,53 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
 
     // Every load of the prologue and epilogue is issued before the weights:
     // loads complete in issue order, so one issued after the weight tile
-    // would wait for all of it.
+    // would wait for all of it. The normalized inputs (QKV, gate/up,
+    // lm_head) are held PER consecutive values per thread (j = PER tid + k)
+    // and loaded 16 bytes at a time; the others as j = tid + k THREADS.
+    constexpr bool kContig = kNorm && PER % 4 == 0;
+    static_assert(MODE != kQKV || kContig, "the embedding row is read as consecutive pairs");
+    const int jbase = kContig ? PER * tid : tid;
+    constexpr int kStride = kContig ? 1 : THREADS;
+    auto load_f = [&](const float* src, float (&dst)[PER]) {
+        if constexpr (kContig) {
+#pragma unroll
+            for (int k = 0; k < PER; k += 4) {
+                const float4 f = *reinterpret_cast<const float4*>(src + jbase + k);
+                dst[k] = f.x; dst[k + 1] = f.y; dst[k + 2] = f.z; dst[k + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < PER; ++k) dst[k] = src[jbase + k * kStride];
+        }
+    };
     float v[ROWS][PER], wn[PER];
 #pragma unroll
     for (int q = 0; q < ROWS; ++q) {
         if constexpr (MODE == kQKV) {
             if (a.embed) {  // first layer: x = fp32(E[token]) (engine/core.cpp:382-383)
-                const uint16_t* erow = a.embed + size_t(a.token[q]) * N;
+                const uint16_t* erow = a.embed + size_t(a.token[q]) * N + jbase;
 #pragma unroll
-                for (int k = 0; k < PER; ++k) v[q][k] = h2f(erow[tid + k * THREADS]);
+                for (int k = 0; k < PER; k += 2) {
+                    const uint32_t pair = *reinterpret_cast<const uint32_t*>(erow + k);
+                    v[q][k] = h2f(pair & 0xffffu);
+                    v[q][k + 1] = h2f(pair >> 16);
+                }
             } else {
-#pragma unroll
-                for (int k = 0; k < PER; ++k) v[q][k] = a.in[q * N + tid + k * THREADS];
+                load_f(a.in + q * N, v[q]);
             }
         } else {
-#pragma unroll
-            for (int k = 0; k < PER; ++k) v[q][k] = a.in[q * N + tid + k * THREADS];
+            load_f(a.in + q * N, v[q]);
         }
     }
-    if constexpr (kNorm) {
-#pragma unroll
-        for (int k = 0; k < PER; ++k) wn[k] = a.norm_w[tid + k * THREADS];
-    }
+    if constexpr (kNorm) load_f(a.norm_w, wn);
     // Pending O partials: of this thread's inputs (gate/up) or of this
     // lane's output row (down).
-    float pin[ROWS][PARTS && MODE == kGateUp ? PER : 1][kOParts], prow[ROWS][kOParts];
+    float pin[ROWS][kOParts][PARTS && MODE == kGateUp ? PER : 1], prow[ROWS][kOParts];
     if constexpr (PARTS && MODE == kGateUp) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q)
 #pragma unroll
-            for (int k = 0; k < PER; ++k)
-#pragma unroll
-                for (int g = 0; g < kOParts; ++g)
-                    pin[q][k][g] = a.parts[(q * kOParts + g) * kHidden + tid + k * THREADS];
+            for (int g = 0; g < kOParts; ++g) load_f(a.parts + (q * kOParts + g) * kHidden, pin[q][g]);
     }
     float xres[ROWS];  // residual entry of this lane's row (O, down)
 #pragma unroll
@@ -227,21 +241,26 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         float* xs = reinterpret_cast<float*>(xs4[q]);
         if constexpr (PARTS && MODE == kGateUp) {
 #pragma unroll
-            for (int k = 0; k < PER; ++k) v[q][k] = fold_parts(v[q][k], pin[q][k]);
+            for (int k = 0; k < PER; ++k) {
+                float pk[kOParts];
+#pragma unroll
+                for (int g = 0; g < kOParts; ++g) pk[g] = pin[q][g][k];
+                v[q][k] = fold_parts(v[q][k], pk);
+            }
         }
         if constexpr (PARTS && MODE == kDown) xres[q] = fold_parts(xres[q], prow[q]);
         if constexpr (kNorm) {
             if constexpr (MODE == kQKV) {
                 if (a.embed && blockIdx.x == 0) {  // kept as the residual stream
 #pragma unroll
-                    for (int k = 0; k < PER; ++k) a.x[q * kHidden + tid + k * THREADS] = v[q][k];
+                    for (int k = 0; k < PER; ++k) a.x[q * kHidden + jbase + k * kStride] = v[q][k];
                 }
             }
-            norm_to_lds<N, THREADS>(v[q], wn, xs, red[q],
-                                    MODE == kLmHead && blockIdx.x == 0 ? a.hidden + q * kHidden : nullptr);
+            norm_to_lds<N, THREADS, kContig>(v[q], wn, xs, red[q],
+                                             MODE == kLmHead && blockIdx.x == 0 ? a.hidden + q * kHidden : nullptr);
         } else {
 #pragma unroll
-            for (int k = 0; k < PER; ++k) xs[xperm(tid + k * THREADS)] = v[q][k];
+            for (int k = 0; k < PER; ++k) xs[xperm(jbase + k * kStride)] = v[q][k];
         }
     }
     __syncthreads();
