@@ -1014,7 +1014,8 @@ void launch_gemv(const GemvArgs& a, int rows, hipStream_t stream) {
 // Two-row launches (verification pairs): waves per workgroup of each mode.
 template <int MODE>
 constexpr int gemv_pair_waves() {
-    if constexpr (MODE == kGateUp || MODE == kLmHead) return 4;
+    if constexpr (MODE == kLmHead) return kLmWaves;
+    else if constexpr (MODE == kGateUp) return 4;
     else if constexpr (MODE == kDown) return 1;
     else return 2;
 }

@@ -63,8 +63,8 @@ inline constexpr int kBatchRows = 16;           // output rows per batched-GEMV 
 inline constexpr int kBatchLmGroups = kVocab / kBatchRows;  // 9496 lm_head workgroups
 static_assert(kVocab % kBatchRows == 0, "batched lm_head tiles must cover the vocabulary");
 
-inline constexpr int kLmWaves = 4;              // lm_head workgroup waves
-inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 4748 workgroups
+inline constexpr int kLmWaves = 8;              // lm_head workgroup waves
+inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 2374 workgroups
 static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
 
 struct LayerDevice {
