@@ -220,6 +220,7 @@ void Engine::init_state() {
     ps.attended = device_alloc<float>(prows * kQDim);
     ps.gu = device_alloc<float>(prows * 2 * kFFN);
     ps.act = device_alloc<float>(prows * kFFN);
+    ps.part = device_alloc<float>(3 * prows * kHidden);
     ids_dev_ = device_alloc<int>(size_t(ctx));
     HIP_CHECK(hipHostMalloc(&pinned, sizeof(int) * size_t(ctx), hipHostMallocDefault));
     ids_host_ = static_cast<int*>(pinned);

@@ -44,7 +44,8 @@ __device__ __forceinline__ double wave_sum(double v) {
 constexpr int kTileN = 128, kTileK = 64;
 constexpr int kLdsRow = kTileK + 8;  // halves per LDS row (padding against bank conflicts)
 
-// Epilogue: 0 store, 1 add into C (residual).
+// Epilogue: 0 store, 1 add into C (residual), 2 store the partial product
+// of K range blockIdx.z (K / gridDim.z columns) at C + blockIdx.z M N.
 template <int TM, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, const uint16_t* __restrict__ W,
                                                    float* __restrict__ C, int M, int N, int K) {
@@ -63,8 +64,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
     // stored), 4 * kAF4 consecutive k; W row br, 32 consecutive k.
     const int ar = tid / kAThreadsPerRow, ak = (tid % kAThreadsPerRow) * 4 * kAF4;
     const int br = tid >> 1, bk = (tid & 1) * 32;
-    const float* a_row = A + size_t(min(m0 + ar, M - 1)) * K + ak;
-    const uint16_t* b_row = W + size_t(n0 + br) * K + bk;
+    const int ks = K / gridDim.z, kz = blockIdx.z * ks;  // this workgroup's K range
+    const float* a_row = A + size_t(min(m0 + ar, M - 1)) * K + kz + ak;
+    const uint16_t* b_row = W + size_t(n0 + br) * K + kz + bk;
     float4 av[kAF4];
     u32x4 bv[4];
     auto load = [&](int k0) {
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
 
     load(0);
     const int fr = lane & 31, fk = (lane >> 5) * 8;
-    for (int k0 = 0; k0 < K; k0 += kTileK) {
+    for (int k0 = 0; k0 < ks; k0 += kTileK) {
         __syncthreads();  // the previous step's fragments are consumed
 #pragma unroll
         for (int i = 0; i < kAF4; i += 2) {  // 8 values -> one 16-byte store per plane
@@ -99,7 +101,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
 #pragma unroll
         for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&b_s[br][bk + 8 * i]) = bv[i];
         __syncthreads();
-        if (k0 + kTileK < K) load(k0 + kTileK);
+        if (k0 + kTileK < ks) load(k0 + kTileK);
 #pragma unroll
         for (int ks = 0; ks < kTileK; ks += 16) {
             const half8 ah = *reinterpret_cast<const half8*>(&a_hi[wm * 32 + fr][ks + fk]);
@@ -123,7 +125,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
         for (int r = 0; r < 16; ++r) {
             const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m < M) {
-                float* c = C + size_t(m) * N + n;
+                float* c = C + (size_t(blockIdx.z) * M + m) * N + n;
                 if constexpr (EPI == 1)
                     *c = *c + acc[jt][r];
                 else
@@ -141,16 +143,33 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const int* __restrict__
     for (int j = threadIdx.x; j < kHidden; j += 256) X[size_t(b) * kHidden + j] = h2f(row[j]);
 }
 
+// x + the SPLITS partial products of a K-split GEMM in a fixed order.
+template <int SPLITS>
+__device__ __forceinline__ float fold_splits(float x, const float* p, size_t stride) {
+    if constexpr (SPLITS == 0) return x;
+    else if constexpr (SPLITS == 2) return x + (p[0] + p[stride]);
+    else return x + ((p[0] + p[stride]) + p[2 * stride]);
+}
+
 // out[b] = RMSNorm(x[b]) (engine/core.cpp:207-215): FP32 squares, FP64 sum.
-__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ X, const float* __restrict__ w,
-                                                           float* __restrict__ out) {
+// With SPLITS > 0 the residual first absorbs the pending partial products of
+// a K-split GEMM (parts[z][b], z < SPLITS) and is written back.
+template <int SPLITS = 0>
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X, const float* __restrict__ w,
+                                                           float* __restrict__ out, const float* __restrict__ parts,
+                                                           int rows) {
     const int b = blockIdx.x, tid = threadIdx.x;
-    const float* x = X + size_t(b) * kHidden;
+    float* x = X + size_t(b) * kHidden;
     float v[4];
     double part = 0.0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        v[k] = x[tid + 256 * k];
+        const int j = tid + 256 * k;
+        v[k] = x[j];
+        if constexpr (SPLITS > 0) {
+            v[k] = fold_splits<SPLITS>(v[k], parts + size_t(b) * kHidden + j, size_t(rows) * kHidden);
+            x[j] = v[k];
+        }
         const float square = v[k] * v[k];
         part += static_cast<double>(square);
     }
@@ -409,14 +428,24 @@ __global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restric
     act[idx] = gate * (0.5f + 0.5f * t) * up;
 }
 
+// X[b] += the SPLITS partial products of a K-split GEMM (rows x 1024).
+template <int SPLITS>
+__global__ __launch_bounds__(256) void fold_rows_kernel(float* __restrict__ X, const float* __restrict__ parts,
+                                                        int rows) {
+    const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (idx < size_t(rows) * kHidden) X[idx] = fold_splits<SPLITS>(X[idx], parts + idx, size_t(rows) * kHidden);
+}
+
 // 64-row tiles when they give every CU a workgroup, else 32-row tiles.
+// `splits` K ranges (EPI 2) count towards the workgroups.
 template <int EPI>
-void gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, hipStream_t stream) {
-    require(N % kTileN == 0 && K % kTileK == 0 && M > 0, "gemm: unsupported shape");
-    if ((M + 63) / 64 * (N / kTileN) >= 256)
-        gemm_kernel<64, EPI><<<dim3(N / kTileN, (M + 63) / 64), 256, 0, stream>>>(A, W, C, M, N, K);
+void gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, hipStream_t stream, int splits = 1) {
+    require(N % kTileN == 0 && K % (kTileK * splits) == 0 && M > 0 && (splits == 1 || EPI == 2),
+            "gemm: unsupported shape");
+    if ((M + 63) / 64 * (N / kTileN) * splits >= 256)
+        gemm_kernel<64, EPI><<<dim3(N / kTileN, (M + 63) / 64, splits), 256, 0, stream>>>(A, W, C, M, N, K);
     else
-        gemm_kernel<32, EPI><<<dim3(N / kTileN, (M + 31) / 32), 256, 0, stream>>>(A, W, C, M, N, K);
+        gemm_kernel<32, EPI><<<dim3(N / kTileN, (M + 31) / 32, splits), 256, 0, stream>>>(A, W, C, M, N, K);
 }
 
 }  // namespace
@@ -435,20 +464,29 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
     require(rows >= 1 && rows <= kPrefillRows, "prefill chunk: bad row count");
     embed_rows_kernel<<<rows, 256, 0, stream>>>(ids_dev, embed, s.x);
     const float scale = 1.0f / std::sqrt(128.0f);
+    // The O and down GEMMs (1024 output columns, K = 2048 / 3072) split K
+    // into 1024-wide ranges for parallelism at any row count; the row kernel
+    // after each adds the partials to the residual in a fixed order, so a
+    // row's result still does not depend on the rows around it.
+    constexpr int kOSplits = kQDim / 1024, kDownSplits = kFFN / 1024;
     for (int l = 0; l < kLayers; ++l) {
         const PrefillLayer& L = layers[l];
-        rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h);
+        if (l == 0)
+            rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h, nullptr, rows);
+        else
+            rmsnorm_rows_kernel<kDownSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h, s.part, rows);
         gemm<0>(s.h, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream);
         qk_rope_kv_kernel<<<dim3(rows, kQHeads + kKVHeads), 128, 0, stream>>>(s.qkv, L.q_norm, L.k_norm, cosines, sines,
                                                                              L.keys, L.values, pos0, context);
         attn_prefill_mfma_kernel<<<dim3((rows + kFaRows - 1) / kFaRows, kQHeads), 256, 0, stream>>>(
             s.qkv, L.keys, L.values, s.attended, rows, pos0, context, scale);
-        gemm<1>(s.attended, L.o_n, s.x, rows, kHidden, kQDim, stream);
-        rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h);
+        gemm<2>(s.attended, L.o_n, s.part, rows, kHidden, kQDim, stream, kOSplits);
+        rmsnorm_rows_kernel<kOSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h, s.part, rows);
         gemm<0>(s.h, L.gateup_n, s.gu, rows, 2 * kFFN, kHidden, stream);
         swiglu_rows_kernel<<<(rows * kFFN + 255) / 256, 256, 0, stream>>>(s.gu, s.act, rows * kFFN);
-        gemm<1>(s.act, L.down_n, s.x, rows, kHidden, kFFN, stream);
+        gemm<2>(s.act, L.down_n, s.part, rows, kHidden, kFFN, stream, kDownSplits);
     }
+    fold_rows_kernel<kDownSplits><<<(rows * kHidden + 255) / 256, 256, 0, stream>>>(s.x, s.part, rows);
 }
 
 }  // namespace qwen_hip

@@ -24,12 +24,13 @@ struct PrefillLayer {
 
 // FP32 activations of one batched pass (up to kPrefillRows rows each).
 struct PrefillScratch {
-    float* x;         // [512 x 1024] residual stream
-    float* h;         // [512 x 1024] normalized
-    float* qkv;       // [512 x 4096]
-    float* attended;  // [512 x 2048]
-    float* gu;        // [512 x 6144]
-    float* act;       // [512 x 3072]
+    float* x;         // [rows x 1024] residual stream
+    float* h;         // [rows x 1024] normalized
+    float* qkv;       // [rows x 4096]
+    float* attended;  // [rows x 2048]
+    float* gu;        // [rows x 6144]
+    float* act;       // [rows x 3072]
+    float* part;      // [3 x rows x 1024] K-split partial products of the O and down GEMMs
 };
 
 // C[M x N] (+)= A[M x K] . W[N x K]^T; A FP32 split into FP16 hi + lo on the
