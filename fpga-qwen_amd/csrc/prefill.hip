@@ -242,10 +242,12 @@ __global__ __launch_bounds__(128) void qk_rope_kv_kernel(float* __restrict__ QKV
 // query (lane % 32), so the softmax statistics stay in the lane: one
 // exchange with lane ^ 32 per tile. q and the cached keys share the
 // chain-permuted channel order, which leaves q . k unchanged.
-constexpr int kFaRows = 32, kFaKeys = 32, kFaWaves = 4, kVtPitch = 40, kFaccPitch = 132;
+constexpr int kFaRows = 32, kFaKeys = 32, kFaWaves = 4, kVtPitch = 36, kFaccPitch = 132;
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __restrict__ QKV,
+// Two waves per SIMD (at most 256 registers per lane, two workgroups per
+// CU): one wave's softmax and V^T work overlaps the other's matrix ops.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_mfma_kernel(const float* __restrict__ QKV,
                                                                 const uint16_t* __restrict__ keys,
                                                                 const uint16_t* __restrict__ values,
                                                                 float* __restrict__ attended, int rows, int pos0,
@@ -261,6 +263,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
     const int ntiles = last / kFaKeys + 1;
     const size_t head_base = size_t(g) * context;
     const int qpos = pos0 + b0 + col;        // causal limit of this lane's query
+    // Softmax in base 2: scores scaled by log2(e) / sqrt(128), weights 2^(s - m)
+    // = e^(scaled score - max) from the hardware exp2.
+    const float scale2 = scale * 1.4426950408889634f;
     uint16_t(*vt)[kVtPitch] = reinterpret_cast<uint16_t(*)[kVtPitch]>(lds + wave * 128 * kVtPitch * 2);
 
     // Q^T operand: query b0 + col (rows past the chunk repeat its last row
@@ -331,17 +336,17 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = t0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-            sv[r] = t <= qpos ? st[r] * scale : -INFINITY;
+            sv[r] = t <= qpos ? st[r] * scale2 : -INFINITY;
             tmax = fmaxf(tmax, sv[r]);
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const float mnew = fmaxf(m, tmax);
-        const float factor = m == -INFINITY ? 0.f : expf(m - mnew);
+        const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
         half8 ph[2], pl[2];
         float psum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float p = sv[r] == -INFINITY ? 0.f : expf(sv[r] - mnew);
+            const float p = sv[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[r] - mnew);
             psum += p;
             const _Float16 h = static_cast<_Float16>(p);
             ph[r >> 3][r & 7] = h;
@@ -349,11 +354,14 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
         }
         psum += __shfl_xor(psum, 32);
         l = l * factor + psum;
+        // Rescaling by 1 changes nothing; skip it when no lane's maximum moved.
+        if (__builtin_amdgcn_ballot_w64(mnew != m) != 0) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[dt][r] *= factor;
+        }
         m = mnew;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[dt][r] *= factor;
         // vt is written and read by this wave only.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -394,7 +402,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float* __r
         float e[kFaWaves], lsum = 0.f;
 #pragma unroll
         for (int w = 0; w < kFaWaves; ++w) {
-            e[w] = fm[w][q] == -INFINITY ? 0.f : expf(fm[w][q] - mx);
+            e[w] = fm[w][q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fm[w][q] - mx);
             lsum = __builtin_fmaf(e[w], fl[w][q], lsum);
         }
         float* out = attended + size_t(b0 + q) * kQDim + head * kHeadDim + c0;
