@@ -218,7 +218,6 @@ void Engine::init_state() {
     ps.h = device_alloc<float>(prows * kHidden);
     ps.qkv = device_alloc<float>(prows * kQKVRows);
     ps.attended = device_alloc<float>(prows * kQDim);
-    ps.gu = device_alloc<float>(prows * 2 * kFFN);
     ps.act = device_alloc<float>(prows * kFFN);
     ps.part = device_alloc<float>(3 * prows * kHidden);
     ids_dev_ = device_alloc<int>(size_t(ctx));

@@ -1,6 +1,8 @@
-// Batched prefill kernels for gfx950: a chunk of up to 512 prompt rows runs
-// through each layer as GEMMs on the matrix cores plus row kernels
-// (engine/core.cpp:353-646 with batch > 1).
+// Batched prefill kernels for gfx950: up to 4096 prompt rows run through
+// each layer as GEMMs on the matrix cores plus row kernels
+// (engine/core.cpp:353-646 with batch > 1). QK-norm, RoPE and the K/V cache
+// writes run in the QKV GEMM's epilogue, SwiGLU in the gate/up GEMM's, and
+// the residual adds of the K-split O and down GEMMs in the next RMSNorm.
 //
 // GEMM: C[M x N] = A[M x K] . W[N x K]^T with natural FP16 weights on
 // v_mfma_f32_32x32x16_f16. The FP32 activations are split exactly into
@@ -44,19 +46,42 @@ __device__ __forceinline__ double wave_sum(double v) {
 constexpr int kTileN = 128, kTileK = 64;
 constexpr int kLdsRow = kTileK + 8;  // halves per LDS row (padding against bank conflicts)
 
+// Per-head work fused into the QKV GEMM (EPI 4): QK-norm, RoPE and the K/V
+// cache writes of engine/core.cpp:395-406.
+struct QkvEpilogue {
+    const float* q_norm;
+    const float* k_norm;
+    const float* cosines;
+    const float* sines;
+    uint16_t* keys;
+    uint16_t* values;
+    int pos0;
+    int context;
+};
+
 // Epilogue: 0 store, 1 add into C (residual), 2 store the partial product
-// of K range blockIdx.z (K / gridDim.z columns) at C + blockIdx.z M N.
+// of K range blockIdx.z (K / gridDim.z columns) at C + blockIdx.z M N,
+// 3 SwiGLU (W = gate rows then up rows, N = 2F: tile t multiplies gate rows
+// 64t.. and up rows F + 64t.. and stores act[m][64t + i], C has F columns),
+// 4 QKV rows (tile t = head t): q heads QK-normed, rotated and stored in the
+// key's chain-permuted order, k heads QK-normed, rotated and written to the
+// cache as FP16, v heads written to the cache. Epilogues 3 and 4 stage the
+// finished tile in LDS.
 template <int TM, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, const uint16_t* __restrict__ W,
-                                                   float* __restrict__ C, int M, int N, int K) {
+                                                   float* __restrict__ C, int M, int N, int K, QkvEpilogue ep) {
     static_assert(TM == 64 || TM == 32, "tile height");
     constexpr int kWaveRows = TM / 32, kWaveCols = 4 / kWaveRows;  // wave grid
     constexpr int kColTiles = kTileN / kWaveCols / 32;              // 32-column MFMA tiles per wave
     constexpr int kAThreadsPerRow = 256 / TM;   // threads loading one A row of the K step
     constexpr int kAF4 = kTileK / 4 / kAThreadsPerRow;  // float4 loads per thread
-    __shared__ __align__(16) _Float16 a_hi[TM][kLdsRow];
-    __shared__ __align__(16) _Float16 a_lo[TM][kLdsRow];
-    __shared__ __align__(16) _Float16 b_s[kTileN][kLdsRow];
+    constexpr int kCPitch = kTileN + 4;                     // floats per row of the staged C tile
+    constexpr int kABytes = TM * kLdsRow * 2, kBBytes = kTileN * kLdsRow * 2;
+    constexpr int kSmem = 2 * kABytes + kBBytes > TM * kCPitch * 4 ? 2 * kABytes + kBBytes : TM * kCPitch * 4;
+    __shared__ __align__(16) unsigned char smem[kSmem];
+    _Float16(*a_hi)[kLdsRow] = reinterpret_cast<_Float16(*)[kLdsRow]>(smem);
+    _Float16(*a_lo)[kLdsRow] = reinterpret_cast<_Float16(*)[kLdsRow]>(smem + kABytes);
+    _Float16(*b_s)[kLdsRow] = reinterpret_cast<_Float16(*)[kLdsRow]>(smem + 2 * kABytes);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m0 = blockIdx.y * TM, n0 = blockIdx.x * kTileN;
     const int wm = wave % kWaveRows, wn = wave / kWaveRows;
@@ -66,7 +91,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
     const int br = tid >> 1, bk = (tid & 1) * 32;
     const int ks = K / gridDim.z, kz = blockIdx.z * ks;  // this workgroup's K range
     const float* a_row = A + size_t(min(m0 + ar, M - 1)) * K + kz + ak;
-    const uint16_t* b_row = W + size_t(n0 + br) * K + kz + bk;
+    const int wr = EPI == 3 ? (br < 64 ? n0 / 2 + br : N / 2 + n0 / 2 + br - 64) : n0 + br;  // W row of tile row br
+    const uint16_t* b_row = W + size_t(wr) * K + kz + bk;
     float4 av[kAF4];
     u32x4 bv[4];
     auto load = [&](int k0) {
@@ -118,18 +144,97 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
         }
     }
     // D layout: lane -> column (lane & 31); register r -> row 8(r/4) + 4(lane/32) + r%4.
+    if constexpr (EPI <= 2) {
 #pragma unroll
-    for (int jt = 0; jt < kColTiles; ++jt) {
-        const int n = n0 + wn * 32 * kColTiles + 32 * jt + (lane & 31);
+        for (int jt = 0; jt < kColTiles; ++jt) {
+            const int n = n0 + wn * 32 * kColTiles + 32 * jt + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (m < M) {
-                float* c = C + (size_t(blockIdx.z) * M + m) * N + n;
-                if constexpr (EPI == 1)
-                    *c = *c + acc[jt][r];
-                else
-                    *c = acc[jt][r];
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < M) {
+                    float* c = C + (size_t(blockIdx.z) * M + m) * N + n;
+                    if constexpr (EPI == 1)
+                        *c = *c + acc[jt][r];
+                    else
+                        *c = acc[jt][r];
+                }
+            }
+        }
+        return;
+    }
+    float(*ct)[kCPitch] = reinterpret_cast<float(*)[kCPitch]>(smem);
+    __syncthreads();  // every wave is done with the operand tiles
+#pragma unroll
+    for (int jt = 0; jt < kColTiles; ++jt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            ct[wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)][wn * 32 * kColTiles + 32 * jt + (lane & 31)] =
+                acc[jt][r];
+    __syncthreads();
+    if constexpr (EPI == 3) {
+        // SwiGLU (engine/core.cpp:636-639): thread -> row tid / 4, outputs 16 (tid % 4) .. +15.
+        const int row = tid >> 2, c0 = (tid & 3) * 16, m = m0 + row;
+        if (row < TM && m < M) {
+            float* out = C + size_t(m) * (N / 2) + n0 / 2 + c0;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float gate = ct[row][c0 + i + e], up = ct[row][64 + c0 + i + e];
+                    const float half_gate = gate * 0.5f;
+                    const float t = tanhf(half_gate);
+                    o[e] = gate * (0.5f + 0.5f * t) * up;
+                }
+                *reinterpret_cast<float4*>(out + i) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        }
+    } else {
+        // Thread -> row tid / 4, channels j in [16 s, 16 s + 16) and j + 64 (s = tid % 4).
+        const int row = tid >> 2, s4 = tid & 3, m = m0 + row, head = blockIdx.x;
+        if (row < TM && m < M) {
+            const int pos = ep.pos0 + m;
+            if (head >= kQHeads + kKVHeads) {  // v: FP16 into the cache
+                uint16_t* vrow = ep.values + (size_t(head - kQHeads - kKVHeads) * ep.context + pos) * kHeadDim;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    vrow[16 * s4 + i] = f2h(ct[row][16 * s4 + i]);
+                    vrow[64 + 16 * s4 + i] = f2h(ct[row][64 + 16 * s4 + i]);
+                }
+            } else {
+                const bool is_q = head < kQHeads;
+                const float* w = is_q ? ep.q_norm : ep.k_norm;
+                float x0[16], x1[16];
+                double part = 0.0;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    x0[i] = ct[row][16 * s4 + i];
+                    x1[i] = ct[row][64 + 16 * s4 + i];
+                    const float s0 = x0[i] * x0[i], s1 = x1[i] * x1[i];
+                    part += static_cast<double>(s0);
+                    part += static_cast<double>(s1);
+                }
+                part += __shfl_xor(part, 1);
+                part += __shfl_xor(part, 2);
+                const float inv = 1.0f / __builtin_sqrtf(static_cast<float>(part) / 128.0f + 1e-6f);
+                const float* cs = ep.cosines + size_t(pos) * 64;
+                const float* sn = ep.sines + size_t(pos) * 64;
+                float* qrow = C + size_t(m) * N + head * kHeadDim;
+                uint16_t* krow = ep.keys + (size_t(head - kQHeads) * ep.context + pos) * kHeadDim;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int j = 16 * s4 + i;
+                    const float n0v = (x0[i] * inv) * w[j], n1v = (x1[i] * inv) * w[j + 64];
+                    const float o0 = n0v * cs[j] - n1v * sn[j];
+                    const float o1 = n1v * cs[j] + n0v * sn[j];
+                    if (is_q) {
+                        qrow[kperm(j)] = o0;
+                        qrow[kperm(j + 64)] = o1;
+                    } else {
+                        krow[kperm(j)] = f2h(o0);
+                        krow[kperm(j + 64)] = f2h(o1);
+                    }
+                }
             }
         }
     }
@@ -183,50 +288,6 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
     for (int k = 0; k < 4; ++k) {
         const int j = tid + 256 * k;
         out[size_t(b) * kHidden + j] = (v[k] * inv) * w[j];
-    }
-}
-
-// Per (row, head): QK-norm + RoPE for the 16 q heads (written back in the
-// key's chain-permuted order) and the 8 k heads (FP16 into the cache), V to
-// the cache (engine/core.cpp:395-406). Grid (rows, 24), 128 threads.
-__global__ __launch_bounds__(128) void qk_rope_kv_kernel(float* __restrict__ QKV, const float* __restrict__ q_norm,
-                                                         const float* __restrict__ k_norm,
-                                                         const float* __restrict__ cosines,
-                                                         const float* __restrict__ sines, uint16_t* __restrict__ keys,
-                                                         uint16_t* __restrict__ values, int pos0, int context) {
-    const int b = blockIdx.x, head = blockIdx.y, j = threadIdx.x, lane = j & 63;
-    const int pos = pos0 + b;
-    float* row = QKV + size_t(b) * kQKVRows;
-    const bool is_q = head < kQHeads;
-    const int kh = head - kQHeads;
-    float* src = is_q ? row + head * kHeadDim : row + kQDim + kh * kHeadDim;
-    const float raw = src[j];
-    const float square = raw * raw;
-    const double part = wave_sum(static_cast<double>(square));
-    __shared__ double red[2];
-    __shared__ float buf[128];
-    if (lane == 0) red[j >> 6] = part;
-    __syncthreads();
-    const float sum = static_cast<float>(red[0] + red[1]);
-    const float inv = 1.0f / __builtin_sqrtf(sum / 128.0f + 1e-6f);
-    buf[j] = (raw * inv) * (is_q ? q_norm : k_norm)[j];
-    __syncthreads();
-    const float* cs = cosines + size_t(pos) * 64;
-    const float* sn = sines + size_t(pos) * 64;
-    float out;
-    if (j < 64) {
-        out = buf[j] * cs[j] - buf[j + 64] * sn[j];
-    } else {
-        const int jj = j - 64;
-        out = buf[j] * cs[jj] + buf[jj] * sn[jj];
-    }
-    if (is_q) {
-        __syncthreads();  // all raw values read before the in-place write
-        src[kperm(j)] = out;
-    } else {
-        const size_t slot = (size_t(kh) * context + pos) * kHeadDim;
-        keys[slot + kperm(j)] = f2h(out);
-        values[slot + j] = f2h(row[kQDim + kKVDim + kh * kHeadDim + j]);
     }
 }
 
@@ -423,19 +484,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-// act[b][i] = g * (0.5 + 0.5 * tanh(0.5 g)) * u with g = GU[b][i], u = GU[b][3072 + i]
-// (engine/core.cpp:636-639).
-__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restrict__ GU, float* __restrict__ act,
-                                                          int total) {
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= total) return;
-    const int b = idx / kFFN, i = idx % kFFN;
-    const float gate = GU[size_t(b) * 2 * kFFN + i], up = GU[size_t(b) * 2 * kFFN + kFFN + i];
-    const float half_gate = gate * 0.5f;
-    const float t = tanhf(half_gate);
-    act[idx] = gate * (0.5f + 0.5f * t) * up;
-}
-
 // X[b] += the SPLITS partial products of a K-split GEMM (rows x 1024).
 template <int SPLITS>
 __global__ __launch_bounds__(256) void fold_rows_kernel(float* __restrict__ X, const float* __restrict__ parts,
@@ -447,13 +495,14 @@ __global__ __launch_bounds__(256) void fold_rows_kernel(float* __restrict__ X, c
 // 64-row tiles when they give every CU a workgroup, else 32-row tiles.
 // `splits` K ranges (EPI 2) count towards the workgroups.
 template <int EPI>
-void gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, hipStream_t stream, int splits = 1) {
+void gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, hipStream_t stream, int splits = 1,
+          const QkvEpilogue& ep = {}) {
     require(N % kTileN == 0 && K % (kTileK * splits) == 0 && M > 0 && (splits == 1 || EPI == 2),
             "gemm: unsupported shape");
     if ((M + 63) / 64 * (N / kTileN) * splits >= 256)
-        gemm_kernel<64, EPI><<<dim3(N / kTileN, (M + 63) / 64, splits), 256, 0, stream>>>(A, W, C, M, N, K);
+        gemm_kernel<64, EPI><<<dim3(N / kTileN, (M + 63) / 64, splits), 256, 0, stream>>>(A, W, C, M, N, K, ep);
     else
-        gemm_kernel<32, EPI><<<dim3(N / kTileN, (M + 31) / 32, splits), 256, 0, stream>>>(A, W, C, M, N, K);
+        gemm_kernel<32, EPI><<<dim3(N / kTileN, (M + 31) / 32, splits), 256, 0, stream>>>(A, W, C, M, N, K, ep);
 }
 
 }  // namespace
@@ -483,15 +532,13 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
             rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h, nullptr, rows);
         else
             rmsnorm_rows_kernel<kDownSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h, s.part, rows);
-        gemm<0>(s.h, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream);
-        qk_rope_kv_kernel<<<dim3(rows, kQHeads + kKVHeads), 128, 0, stream>>>(s.qkv, L.q_norm, L.k_norm, cosines, sines,
-                                                                             L.keys, L.values, pos0, context);
+        const QkvEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context};
+        gemm<4>(s.h, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream, 1, ep);
         attn_prefill_mfma_kernel<<<dim3((rows + kFaRows - 1) / kFaRows, kQHeads), 256, 0, stream>>>(
             s.qkv, L.keys, L.values, s.attended, rows, pos0, context, scale);
         gemm<2>(s.attended, L.o_n, s.part, rows, kHidden, kQDim, stream, kOSplits);
         rmsnorm_rows_kernel<kOSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h, s.part, rows);
-        gemm<0>(s.h, L.gateup_n, s.gu, rows, 2 * kFFN, kHidden, stream);
-        swiglu_rows_kernel<<<(rows * kFFN + 255) / 256, 256, 0, stream>>>(s.gu, s.act, rows * kFFN);
+        gemm<3>(s.h, L.gateup_n, s.act, rows, 2 * kFFN, kHidden, stream);
         gemm<2>(s.act, L.down_n, s.part, rows, kHidden, kFFN, stream, kDownSplits);
     }
     fold_rows_kernel<kDownSplits><<<(rows * kHidden + 255) / 256, 256, 0, stream>>>(s.x, s.part, rows);

@@ -28,7 +28,6 @@ struct PrefillScratch {
     float* h;         // [rows x 1024] normalized
     float* qkv;       // [rows x 4096]
     float* attended;  // [rows x 2048]
-    float* gu;        // [rows x 6144]
     float* act;       // [rows x 3072]
     float* part;      // [3 x rows x 1024] K-split partial products of the O and down GEMMs
 };
