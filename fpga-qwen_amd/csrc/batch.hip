@@ -6,15 +6,16 @@
 // GEMV per sequence.
 //
 // Skinny GEMM (bgemv_kernel): Y[b][o] = sum_k X[b][k] W[o][k], W natural
-// row-major FP16, b < 8. Workgroup = 16 output rows (one 16x16x32 MFMA tile,
-// A = W rows, B = X^T with the 8 sequences in columns 0..7) and 4 waves, each
-// a quarter of K; the quarters are summed in LDS in a fixed order. X enters
-// the matrix cores as FP16 hi + lo (hi = fp16(x), lo = fp16(x - hi)), so the
-// products are exact and the sums FP32, as in the prefill GEMMs. Each lane
-// streams 64 contiguous bytes of its weight row per 128-wide K block (the
-// summation order inside a block is a fixed permutation of k, applied to A
-// and B alike). RMSNorm prologues (FP32 squares, FP64 sums per row) and the
-// residual / SwiGLU / argmax epilogues are fused as in the batch-1 kernels.
+// row-major FP16, b < 8. Workgroup = 16 output rows per MFMA tile (one
+// 16x16x32 tile, A = W rows, B = X^T with the 8 sequences in columns 0..7;
+// the lm_head takes 4 tiles per workgroup) and 4 waves, each a quarter of K;
+// the quarters are summed in LDS in a fixed order. X enters the matrix cores
+// as FP16 hi + lo (hi = fp16(x), lo = fp16(x - hi)), so the products are
+// exact and the sums FP32, as in the prefill GEMMs. In each weight load the 4
+// lanes of a tile row read 64 contiguous bytes (the summation order inside a
+// 128-wide K block is a fixed permutation of k, applied to A and B alike).
+// RMSNorm prologues (FP32 squares, FP64 sums per row) and the residual /
+// SwiGLU / argmax epilogues are fused as in the batch-1 kernels.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -27,18 +28,13 @@ namespace qwen_hip {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 
 __device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
-
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
@@ -58,76 +54,95 @@ struct BatchGemvArgs {
     int batch;
 };
 
-template <int K, int MODE>
+// RT = 16-row MFMA tiles per workgroup (gate/up: the gate tile and the
+// matching up tile). The prologue loads every input row as float4 (thread t
+// holds elements 4 (t + 256 i) .. + 3), sums the squares of all rows in one
+// pass (one barrier for the 8 norms) and stages FP16 hi / lo with 8-byte LDS
+// stores; the weights are issued right after the inputs, so their HBM round
+// trip overlaps the prologue.
+template <int K, int MODE, int RT = 1>
 __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
     constexpr bool kNorm = MODE == kBQKV || MODE == kBGateUp || MODE == kBLmHead;
-    constexpr int kTiles = MODE == kBGateUp ? 2 : 1;  // gate/up: a gate tile and the matching up tile
-    constexpr int KW = K / kWaves, kBlocks = KW / 128, PER = K / 256;
-    static_assert(KW % 128 == 0, "each wave takes whole 128-wide K blocks");
+    constexpr int kTiles = MODE == kBGateUp ? 2 : RT;
+    static_assert(MODE == kBGateUp ? RT == 1 : RT >= 1, "gate/up pairs one gate tile with one up tile");
+    constexpr int KW = K / kWaves, kBlocks = KW / 128, F4 = K / 1024;
+    static_assert(KW % 128 == 0 && K % 1024 == 0, "each wave takes whole 128-wide K blocks");
     __shared__ __align__(16) _Float16 xh[kMaxBatch][K + 8];
     __shared__ __align__(16) _Float16 xl[kMaxBatch][K + 8];
     __shared__ double red[kWaves][kMaxBatch];
-    __shared__ float inv_s[kMaxBatch];
     __shared__ float part[kWaves][kTiles][64][4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, quad = lane >> 4;
-    const int B = a.batch, o0 = blockIdx.x * kBatchRows;
-    // Epilogue element of this thread: row 4 (l / 16) + r, column l % 16 of
-    // the 16x16 accumulator (r = wave, l = lane).
-    const int eb = lane & 15, eo = o0 + 4 * (lane >> 4) + wave;
+    const int B = a.batch, o0 = blockIdx.x * (kBatchRows * RT);
+    // Epilogue elements of this thread: row o0 + 16 t + 4 (l / 16) + r,
+    // sequence l % 16 of each 16x16 accumulator (r = wave, l = lane).
+    const int eb = lane & 15, erow = 4 * (lane >> 4) + wave;
 
     // Loads complete in issue order per wave: inputs first (rows past the
-    // batch repeat row B - 1 and are never used), then residual entries,
-    // then the weights.
-    float v[kMaxBatch][PER], wn[PER];
+    // batch repeat row B - 1 and are never stored), then norm weights and
+    // residual entries, then the weights.
+    float4 v[kMaxBatch][F4];
 #pragma unroll
     for (int b = 0; b < kMaxBatch; ++b) {
         const int bb = min(b, B - 1);
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int j = tid + 256 * k;
-            if constexpr (MODE == kBQKV)
-                v[b][k] = a.embed[bb] ? h2f(a.embed[bb][j]) : a.in[bb][j];
-            else
-                v[b][k] = a.in[bb][j];
+        for (int i = 0; i < F4; ++i) {
+            const int j4 = tid + 256 * i;
+            if constexpr (MODE == kBQKV) {
+                if (a.embed[bb]) {
+                    const uint2 e = reinterpret_cast<const uint2*>(a.embed[bb])[j4];
+                    v[b][i] = make_float4(h2f(e.x & 0xffffu), h2f(e.x >> 16), h2f(e.y & 0xffffu), h2f(e.y >> 16));
+                    continue;
+                }
+            }
+            v[b][i] = reinterpret_cast<const float4*>(a.in[bb])[j4];
         }
     }
+    float4 wn[F4];
     if constexpr (kNorm) {
 #pragma unroll
-        for (int k = 0; k < PER; ++k) wn[k] = a.norm_w[tid + 256 * k];
+        for (int i = 0; i < F4; ++i) wn[i] = reinterpret_cast<const float4*>(a.norm_w)[tid + 256 * i];
     }
     float xres = 0.f;
-    if constexpr (MODE == kBO || MODE == kBDown) xres = a.x[min(eb, B - 1)][eo];
+    if constexpr (MODE == kBO || MODE == kBDown) xres = a.x[min(eb, B - 1)][o0 + erow];
     u32x4 wa[kTiles][kBlocks][4];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
-        const int row = o0 + col + (t ? kFFN : 0);
-        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(row) * K + wave * KW) + 4 * quad;
+        const int row = MODE == kBGateUp ? o0 + col + (t ? kFFN : 0) : o0 + kBatchRows * t + col;
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(row) * K + wave * KW) + quad;
 #pragma unroll
         for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) wa[t][blk][s] = __builtin_nontemporal_load(wp + 16 * blk + s);
+            for (int s = 0; s < 4; ++s) wa[t][blk][s] = __builtin_nontemporal_load(wp + 16 * blk + 4 * s);
     }
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (kNorm) {
-        // RMSNorm per row (engine/core.cpp:207-215).
+        // RMSNorm per row (engine/core.cpp:207-215): FP32 squares summed in
+        // FP64, all rows reduced together.
+        double sq[kMaxBatch];
 #pragma unroll
         for (int b = 0; b < kMaxBatch; ++b) {
-            double sq = 0.0;
+            double s = 0.0;
 #pragma unroll
-            for (int k = 0; k < PER; ++k) {
-                const float square = v[b][k] * v[b][k];
-                sq += static_cast<double>(square);
+            for (int i = 0; i < F4; ++i) {
+                const float e[4] = {v[b][i].x, v[b][i].y, v[b][i].z, v[b][i].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float square = e[k] * e[k];
+                    s += static_cast<double>(square);
+                }
             }
-            sq = wave_sum(sq);
-            if (lane == 0) red[wave][b] = sq;
+            sq[b] = s;
         }
-        __syncthreads();
-        if (tid < kMaxBatch) {
-            const double total = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
-            inv_s[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(K) + 1e-6f);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+            for (int b = 0; b < kMaxBatch; ++b) sq[b] += __shfl_xor(sq[b], off);
+        if (lane == 0) {
+#pragma unroll
+            for (int b = 0; b < kMaxBatch; ++b) red[wave][b] = sq[b];
         }
         __syncthreads();
         if constexpr (MODE == kBQKV) {
@@ -136,15 +151,21 @@ __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
                 for (int b = 0; b < kMaxBatch; ++b)
                     if (b < B && a.embed[b]) {
 #pragma unroll
-                        for (int k = 0; k < PER; ++k) a.x[b][tid + 256 * k] = v[b][k];
+                        for (int i = 0; i < F4; ++i) reinterpret_cast<float4*>(a.x[b])[tid + 256 * i] = v[b][i];
                     }
             }
         }
 #pragma unroll
         for (int b = 0; b < kMaxBatch; ++b) {
-            const float inv = inv_s[b];
+            const double total = (red[0][b] + red[1][b]) + (red[2][b] + red[3][b]);
+            const float inv = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(K) + 1e-6f);
 #pragma unroll
-            for (int k = 0; k < PER; ++k) v[b][k] = (v[b][k] * inv) * wn[k];
+            for (int i = 0; i < F4; ++i) {
+                v[b][i].x = (v[b][i].x * inv) * wn[i].x;
+                v[b][i].y = (v[b][i].y * inv) * wn[i].y;
+                v[b][i].z = (v[b][i].z * inv) * wn[i].z;
+                v[b][i].w = (v[b][i].w * inv) * wn[i].w;
+            }
         }
         if constexpr (MODE == kBLmHead) {
             if (blockIdx.x == 0) {
@@ -152,7 +173,7 @@ __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
                 for (int b = 0; b < kMaxBatch; ++b)
                     if (b < B) {
 #pragma unroll
-                        for (int k = 0; k < PER; ++k) a.hidden[b][tid + 256 * k] = v[b][k];
+                        for (int i = 0; i < F4; ++i) reinterpret_cast<float4*>(a.hidden[b])[tid + 256 * i] = v[b][i];
                     }
             }
         }
@@ -160,10 +181,17 @@ __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
 #pragma unroll
     for (int b = 0; b < kMaxBatch; ++b)
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const _Float16 h = static_cast<_Float16>(v[b][k]);
-            xh[b][tid + 256 * k] = h;
-            xl[b][tid + 256 * k] = static_cast<_Float16>(v[b][k] - static_cast<float>(h));
+        for (int i = 0; i < F4; ++i) {
+            const float e[4] = {v[b][i].x, v[b][i].y, v[b][i].z, v[b][i].w};
+            half4 hi, lo;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                hi[k] = static_cast<_Float16>(e[k]);
+                lo[k] = static_cast<_Float16>(e[k] - static_cast<float>(hi[k]));
+            }
+            const int j = 4 * (tid + 256 * i);
+            *reinterpret_cast<half4*>(&xh[b][j]) = hi;
+            *reinterpret_cast<half4*>(&xl[b][j]) = lo;
         }
     __syncthreads();
 
@@ -175,8 +203,9 @@ __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
     for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            // k slot (quad, i) of step s holds k = 128 blk + 32 quad + 8 s + i of this wave's range.
-            const int k = wave * KW + 128 * blk + 32 * quad + 8 * s;
+            // k slot (quad, i) of step s holds k = 128 blk + 32 s + 8 quad + i of this wave's range
+            // (each weight load reads 64 contiguous bytes of every tile row).
+            const int k = wave * KW + 128 * blk + 32 * s + 8 * quad;
             const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
             const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
 #pragma unroll
@@ -192,13 +221,13 @@ __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
         for (int r = 0; r < 4; ++r) part[wave][t][lane][r] = acc[t][r];
     __syncthreads();
 
-    // Epilogue: thread (wave r, lane l) owns accumulator register r of lane l:
-    // output row eo = o0 + 4 (l / 16) + r, sequence eb = l % 16.
+    // The four K quarters of each output, summed in a fixed order.
     float y[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t)
         y[t] = (part[0][t][lane][wave] + part[1][t][lane][wave]) + (part[2][t][lane][wave] + part[3][t][lane][wave]);
     const bool live = eb < B;
+    const int eo = o0 + erow;
     if constexpr (MODE == kBPlain || MODE == kBQKV) {
         if (live) a.out[eb][eo] = y[0];
     } else if constexpr (MODE == kBO || MODE == kBDown) {
@@ -211,11 +240,19 @@ __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
             a.out[eb][eo] = gate * (0.5f + 0.5f * th) * up;
         }
     } else if constexpr (MODE == kBLmHead) {
-        if (live) a.out[eb][eo] = y[0];
-        // Per-sequence argmax over this workgroup's 16 rows: lowest id among
+        // Per-sequence argmax over this workgroup's rows: lowest id among
         // maxima, nonfinite values flagged (engine/main.cpp:51-59).
-        float bv = live ? y[0] : -INFINITY;
-        int bi = live ? eo : INT_MAX, bad = live && !__builtin_isfinite(y[0]);
+        float bv = -INFINITY;
+        int bi = INT_MAX, bad = 0;
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            const int row = eo + kBatchRows * t;
+            if (live) {
+                a.out[eb][row] = y[t];
+                bad |= !__builtin_isfinite(y[t]);
+                if (better(y[t], row, bv, bi)) { bv = y[t]; bi = row; }
+            }
+        }
 #pragma unroll
         for (int off = 16; off < 64; off <<= 1) {
             const float ov = __shfl_xor(bv, off);
@@ -283,11 +320,11 @@ __global__ __launch_bounds__(1024) void batch_argmax_kernel(const float* __restr
     }
 }
 
-template <int K, int MODE>
+template <int K, int MODE, int RT = 1>
 void bgemv(const BatchGemvArgs& a, int rows, hipStream_t stream) {
     require(a.batch >= 1 && a.batch <= kMaxBatch, "batched GEMV: 1..8 rows");
-    require(rows % kBatchRows == 0 && rows > 0, "batched GEMV: rows must be a positive multiple of 16");
-    bgemv_kernel<K, MODE><<<rows / kBatchRows, 256, 0, stream>>>(a);
+    require(rows % (kBatchRows * RT) == 0 && rows > 0, "batched GEMV: rows must be a positive multiple of the tile rows");
+    bgemv_kernel<K, MODE, RT><<<rows / (kBatchRows * RT), 256, 0, stream>>>(a);
 }
 
 }  // namespace
@@ -379,7 +416,7 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
         res.device[b] = seqs[b].s.result;
         res.host[b] = seqs[b].host_out;
     }
-    bgemv<kHidden, kBLmHead>(lm, kVocab, stream);
+    bgemv<kHidden, kBLmHead, kBatchLmTiles>(lm, kVocab, stream);
     batch_argmax_kernel<<<count, 1024, 0, stream>>>(s0.lm_value, s0.lm_index, s0.lm_bad, res);
 }
 

@@ -59,9 +59,10 @@ inline constexpr int kAttnOGroups = kQHeads * (kHidden / kAttnORows);  // 256 wo
 __host__ __device__ inline bool attn_fused(int n) { return n <= kFusedMaxPositions; }
 
 inline constexpr int kMaxBatch = 8;             // sequences per batched decode step
-inline constexpr int kBatchRows = 16;           // output rows per batched-GEMV workgroup (one MFMA tile)
-inline constexpr int kBatchLmGroups = kVocab / kBatchRows;  // 9496 lm_head workgroups
-static_assert(kVocab % kBatchRows == 0, "batched lm_head tiles must cover the vocabulary");
+inline constexpr int kBatchRows = 16;           // output rows of one batched-GEMV MFMA tile
+inline constexpr int kBatchLmTiles = 4;         // MFMA tiles per batched lm_head workgroup
+inline constexpr int kBatchLmGroups = kVocab / (kBatchRows * kBatchLmTiles);  // 2374 lm_head workgroups
+static_assert(kVocab % (kBatchRows * kBatchLmTiles) == 0, "batched lm_head tiles must cover the vocabulary");
 
 inline constexpr int kLmWaves = 8;              // lm_head workgroup waves
 inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 2374 workgroups
