@@ -215,11 +215,14 @@ void Engine::init_state() {
     PrefillScratch& ps = prefill_;
     const size_t prows = size_t(std::max(2, std::min(ctx, kPrefillRows)));  // a call never exceeds the context
     ps.x = device_alloc<float>(prows * kHidden);
-    ps.h = device_alloc<float>(prows * kHidden);
+    ps.h_hi = device_alloc<uint16_t>(prows * kHidden);
+    ps.h_lo = device_alloc<uint16_t>(prows * kHidden);
     ps.qkv = device_alloc<float>(prows * kQKVRows);
-    ps.attended = device_alloc<float>(prows * kQDim);
-    ps.act = device_alloc<float>(prows * kFFN);
-    ps.part = device_alloc<float>(3 * prows * kHidden);
+    ps.att_hi = device_alloc<uint16_t>(prows * kQDim);
+    ps.att_lo = device_alloc<uint16_t>(prows * kQDim);
+    ps.act_hi = device_alloc<uint16_t>(prows * kFFN);
+    ps.act_lo = device_alloc<uint16_t>(prows * kFFN);
+    ps.part = device_alloc<float>(4 * prows * kHidden);
     ids_dev_ = device_alloc<int>(size_t(ctx));
     HIP_CHECK(hipHostMalloc(&pinned, sizeof(int) * size_t(ctx), hipHostMallocDefault));
     ids_host_ = static_cast<int*>(pinned);

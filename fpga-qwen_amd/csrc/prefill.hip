@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <type_traits>
 
 #include "kernels.hpp"
 #include "prefill.hpp"
@@ -23,6 +24,7 @@ namespace qwen_hip {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -35,20 +37,45 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// C[M x N] (+)= A[M x K] . W[N x K]^T on the matrix cores. Workgroup tile TM
-// x 128 (TM = 64 or 32), K in steps of 64; 4 waves, each owning 32 rows x
-// (64 or 32) columns of C as 32x32 MFMA tiles. A (FP32) enters LDS as
-// FP16 hi = fp16(a) and lo = fp16(a - hi), W as its FP16 values; every
-// product runs twice (hi, lo), so products are exact and sums FP32. The next
-// K step's global loads are issued before the current step's MFMAs. Each
-// output element accumulates its K terms in the same order whatever TM and
-// its row position, so results do not depend on M or on how rows are grouped.
+// C[M x N] (+)= A[M x K] . W[N x K]^T on the matrix cores
+// (v_mfma_f32_32x32x16_f16). A arrives as two FP16 planes written by the
+// kernel that produced it, hi = fp16(a) and lo = fp16(a - hi) (a - hi is
+// exact in FP32), W as its FP16 values; every product runs twice (hi, lo), so
+// products are exact and sums FP32. Workgroup tile BM x 128 (BM = 128, 64 or
+// 32), K in steps of 64 through a ring of LDS stages filled by direct global
+// -> LDS loads (global_load_lds_dwordx4) one or two steps ahead of the matrix
+// cores, one barrier per step. A wave retires roughly one 1 KiB load
+// instruction per 240 cycles on this chip, so the loads are spread over 16
+// (BM = 128) or 8 waves per workgroup; 4 (BM = 64: 8) of them also run the
+// MFMAs, each on 64x64 (BM = 128) or 32x32 tiles of C. Epilogues stage C in LDS and write 16 bytes per
+// lane. Each output element accumulates its K terms in the same order
+// whatever BM and its row position, so results do not depend on M or on how
+// rows are grouped.
 constexpr int kTileN = 128, kTileK = 64;
-constexpr int kLdsRow = kTileK + 8;  // halves per LDS row (padding against bank conflicts)
 
-// Per-head work fused into the QKV GEMM (EPI 4): QK-norm, RoPE and the K/V
-// cache writes of engine/core.cpp:395-406.
-struct QkvEpilogue {
+template <int BM>
+struct GemmShape {
+    static constexpr int kWaves = BM == 128 ? 16 : 8;            // waves per workgroup (all load)
+    static constexpr int kMma = BM == 64 ? 8 : 4;                // waves running the MFMAs
+    static constexpr int TI = BM == 128 ? 2 : 1;                 // 32-row tiles per MFMA wave
+    static constexpr int WR = BM / 32 / TI, WC = kMma / WR;      // MFMA wave grid
+    static constexpr int TJ = kTileN / WC / 32;                  // 32-column tiles per MFMA wave
+    static constexpr int kASlots = BM * 8, kBSlots = kTileN * 8; // 16-byte slots per stage
+    static constexpr int kStageBytes = (2 * kASlots + kBSlots) * 16;
+    static constexpr int kLoads = (2 * kASlots + kBSlots) / (64 * kWaves);  // per thread per stage
+    static constexpr int kStages = BM == 128 ? 3 : 4;
+    static_assert(kLoads * 64 * kWaves == 2 * kASlots + kBSlots, "stage loads split evenly over the waves");
+};
+
+// LDS operand tiles hold rows of 64 halves (eight 16-byte pieces): piece p of
+// row r sits in 16-byte slot 8 r + (p ^ swz(r)), so the 8 (or 16) lanes
+// served in one LDS cycle read distinct banks.
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
+// Work fused into the epilogue. QKV (EPI 4): QK-norm, RoPE and the K/V cache
+// writes of engine/core.cpp:395-406. Gate/up (EPI 3): SwiGLU, written as the
+// FP16 hi / lo planes the down GEMM reads.
+struct GemmEpilogue {
     const float* q_norm;
     const float* k_norm;
     const float* cosines;
@@ -57,184 +84,257 @@ struct QkvEpilogue {
     uint16_t* values;
     int pos0;
     int context;
+    uint16_t* act_hi;
+    uint16_t* act_lo;
 };
+
+// FP32 value -> the FP16 hi / lo pair the GEMMs read (hi = fp16(v), lo = fp16(v - hi)).
+__device__ __forceinline__ void split_store(float v, uint16_t* hi, uint16_t* lo, size_t i) {
+    const _Float16 h = static_cast<_Float16>(v);
+    hi[i] = __builtin_bit_cast(uint16_t, h);
+    lo[i] = f2h(v - static_cast<float>(h));
+}
+
+// 16 bytes per lane from global memory straight into LDS at
+// lds + 16 lane (lds wave-uniform); counted by vmcnt like any load.
+__device__ __forceinline__ void load_lds16(const void* src, unsigned char* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
+// vmcnt <= n (expcnt and lgkmcnt unconstrained).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without a memory fence: the waits before it already
+// cover the direct-to-LDS loads (a fenced barrier would wait for every load
+// in flight, including the later stages). The empty asm statements keep the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 // Epilogue: 0 store, 1 add into C (residual), 2 store the partial product
 // of K range blockIdx.z (K / gridDim.z columns) at C + blockIdx.z M N,
 // 3 SwiGLU (W = gate rows then up rows, N = 2F: tile t multiplies gate rows
-// 64t.. and up rows F + 64t.. and stores act[m][64t + i], C has F columns),
+// 64t.. and up rows F + 64t.. and stores act[m][64t + i] as FP16 hi / lo),
 // 4 QKV rows (tile t = head t): q heads QK-normed, rotated and stored in the
 // key's chain-permuted order, k heads QK-normed, rotated and written to the
-// cache as FP16, v heads written to the cache. Epilogues 3 and 4 stage the
-// finished tile in LDS.
-template <int TM, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, const uint16_t* __restrict__ W,
-                                                   float* __restrict__ C, int M, int N, int K, QkvEpilogue ep) {
-    static_assert(TM == 64 || TM == 32, "tile height");
-    constexpr int kWaveRows = TM / 32, kWaveCols = 4 / kWaveRows;  // wave grid
-    constexpr int kColTiles = kTileN / kWaveCols / 32;              // 32-column MFMA tiles per wave
-    constexpr int kAThreadsPerRow = 256 / TM;   // threads loading one A row of the K step
-    constexpr int kAF4 = kTileK / 4 / kAThreadsPerRow;  // float4 loads per thread
-    constexpr int kCPitch = kTileN + 4;                     // floats per row of the staged C tile
-    constexpr int kABytes = TM * kLdsRow * 2, kBBytes = kTileN * kLdsRow * 2;
-    constexpr int kSmem = 2 * kABytes + kBBytes > TM * kCPitch * 4 ? 2 * kABytes + kBBytes : TM * kCPitch * 4;
+// cache as FP16, v heads written to the cache.
+template <int BM, int EPI>
+__global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
+    const uint16_t* __restrict__ Ah, const uint16_t* __restrict__ Al, const uint16_t* __restrict__ W,
+    float* __restrict__ C, int M, int N, int K, GemmEpilogue ep) {
+    using S = GemmShape<BM>;
+    constexpr int kStages = S::kStages, kLoads = S::kLoads, kStageBytes = S::kStageBytes;
+    constexpr int kASlots = S::kASlots, WR = S::WR, TI = S::TI, TJ = S::TJ;
+    constexpr int kThreads = S::kWaves * 64;
+    constexpr int kCPitch = kTileN + 4;  // floats per row of the staged C tile
+    constexpr int kEpiBytes = BM * kCPitch * 4 + (EPI == 4 ? BM * kHeadDim * 2 : 0);
+    constexpr int kSmem = kStages * kStageBytes > kEpiBytes ? kStages * kStageBytes : kEpiBytes;
     __shared__ __align__(16) unsigned char smem[kSmem];
-    _Float16(*a_hi)[kLdsRow] = reinterpret_cast<_Float16(*)[kLdsRow]>(smem);
-    _Float16(*a_lo)[kLdsRow] = reinterpret_cast<_Float16(*)[kLdsRow]>(smem + kABytes);
-    _Float16(*b_s)[kLdsRow] = reinterpret_cast<_Float16(*)[kLdsRow]>(smem + 2 * kABytes);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * kTileN;
-    const int wm = wave % kWaveRows, wn = wave / kWaveRows;
-    // Global loads: A row ar (rows past M repeat row M - 1 and are not
-    // stored), 4 * kAF4 consecutive k; W row br, 32 consecutive k.
-    const int ar = tid / kAThreadsPerRow, ak = (tid % kAThreadsPerRow) * 4 * kAF4;
-    const int br = tid >> 1, bk = (tid & 1) * 32;
-    const int ks = K / gridDim.z, kz = blockIdx.z * ks;  // this workgroup's K range
-    const float* a_row = A + size_t(min(m0 + ar, M - 1)) * K + kz + ak;
-    const int wr = EPI == 3 ? (br < 64 ? n0 / 2 + br : N / 2 + n0 / 2 + br - 64) : n0 + br;  // W row of tile row br
-    const uint16_t* b_row = W + size_t(wr) * K + kz + bk;
-    float4 av[kAF4];
-    u32x4 bv[4];
-    auto load = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < kAF4; ++i) av[i] = reinterpret_cast<const float4*>(a_row + k0)[i];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) bv[i] = reinterpret_cast<const u32x4*>(b_row + k0)[i];
-    };
-    floatx16 acc[kColTiles];
-#pragma unroll
-    for (int jt = 0; jt < kColTiles; ++jt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[jt][r] = 0.f;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kTileN;
+    const bool mma = wave < S::kMma;
+    const int wm = wave % WR, wn = wave / WR;
+    const int ks = K / gridDim.z, kz = blockIdx.z * ks, nk = ks / kTileK;  // this workgroup's K range
 
-    load(0);
-    const int fr = lane & 31, fk = (lane >> 5) * 8;
-    for (int k0 = 0; k0 < ks; k0 += kTileK) {
-        __syncthreads();  // the previous step's fragments are consumed
+    // Load j of this thread fills slot 64 (wave + kWaves j) + lane of a
+    // stage: a wave-uniform operand plane (A hi, A lo, W) and one 16-byte
+    // piece of a row. A rows past M repeat row M - 1 and are never stored.
+    const uint16_t* src[kLoads];
 #pragma unroll
-        for (int i = 0; i < kAF4; i += 2) {  // 8 values -> one 16-byte store per plane
-            const float v[8] = {av[i].x, av[i].y, av[i].z, av[i].w, av[i + 1].x, av[i + 1].y, av[i + 1].z, av[i + 1].w};
-            half8 hi8, lo8;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const _Float16 hi = static_cast<_Float16>(v[e]);
-                hi8[e] = hi;
-                lo8[e] = static_cast<_Float16>(v[e] - static_cast<float>(hi));
-            }
-            *reinterpret_cast<half8*>(&a_hi[ar][ak + 4 * i]) = hi8;
-            *reinterpret_cast<half8*>(&a_lo[ar][ak + 4 * i]) = lo8;
+    for (int j = 0; j < kLoads; ++j) {
+        const int q = 64 * (wave + S::kWaves * j) + lane;
+        if (q < 2 * kASlots) {
+            const int qa = q < kASlots ? q : q - kASlots, r = qa >> 3, p = (qa & 7) ^ swz(r);
+            src[j] = (q < kASlots ? Ah : Al) + size_t(min(m0 + r, M - 1)) * K + kz + 8 * p;
+        } else {
+            const int qb = q - 2 * kASlots, r = qb >> 3, p = (qb & 7) ^ swz(r);
+            const int wr = EPI == 3 ? (r < 64 ? n0 / 2 + r : N / 2 + n0 / 2 + r - 64) : n0 + r;
+            src[j] = W + size_t(wr) * K + kz + 8 * p;
         }
+    }
+    auto issue = [&](int kt) {
+        unsigned char* stage = smem + (kt % kStages) * kStageBytes;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&b_s[br][bk + 8 * i]) = bv[i];
-        __syncthreads();
-        if (k0 + kTileK < ks) load(k0 + kTileK);
+        for (int j = 0; j < kLoads; ++j) load_lds16(src[j] + kt * kTileK, stage + 1024 * (wave + S::kWaves * j));
+    };
+
+    floatx16 acc[TI][TJ];
 #pragma unroll
-        for (int ks = 0; ks < kTileK; ks += 16) {
-            const half8 ah = *reinterpret_cast<const half8*>(&a_hi[wm * 32 + fr][ks + fk]);
-            const half8 al = *reinterpret_cast<const half8*>(&a_lo[wm * 32 + fr][ks + fk]);
-            half8 bb[kColTiles];
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-            for (int jt = 0; jt < kColTiles; ++jt)
-                bb[jt] = *reinterpret_cast<const half8*>(&b_s[wn * 32 * kColTiles + 32 * jt + fr][ks + fk]);
+        for (int jt = 0; jt < TJ; ++jt)
 #pragma unroll
-            for (int jt = 0; jt < kColTiles; ++jt) {
-                acc[jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bb[jt], acc[jt], 0, 0, 0);
-                acc[jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bb[jt], acc[jt], 0, 0, 0);
+            for (int r = 0; r < 16; ++r) acc[i][jt][r] = 0.f;
+
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s)
+        if (s < nk) issue(s);
+    const int fr = lane & 31;
+    for (int kt = 0; kt < nk; ++kt) {
+        // Step kt has landed once no more than the later steps' loads are
+        // pending; the barrier then also tells every wave that all waves are
+        // done reading the stage the next issue overwrites.
+        if (kt + kStages - 2 < nk)
+            wait_vmcnt<(kStages - 2) * kLoads>();
+        else
+            wait_vmcnt<0>();
+        stage_barrier();
+        if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
+        if (mma) {
+            const unsigned char* stage = smem + (kt % kStages) * kStageBytes;
+#pragma unroll
+            for (int sub = 0; sub < 4; ++sub) {
+                const int p = 2 * sub + (lane >> 5);  // k = 16 sub + 8 (lane / 32) .. + 7 of the step
+                half8 ah[TI], al[TI], bb[TJ];
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const int ra = (wm * TI + i) * 32 + fr, sa = 8 * ra + (p ^ swz(ra));
+                    ah[i] = *reinterpret_cast<const half8*>(stage + 16 * sa);
+                    al[i] = *reinterpret_cast<const half8*>(stage + 16 * (kASlots + sa));
+                }
+#pragma unroll
+                for (int jt = 0; jt < TJ; ++jt) {
+                    const int rb = wn * (kTileN / S::WC) + 32 * jt + fr;
+                    bb[jt] = *reinterpret_cast<const half8*>(stage + 16 * (2 * kASlots + 8 * rb + (p ^ swz(rb))));
+                }
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int jt = 0; jt < TJ; ++jt) {
+                        acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bb[jt], acc[i][jt], 0, 0, 0);
+                        acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bb[jt], acc[i][jt], 0, 0, 0);
+                    }
             }
         }
     }
-    // D layout: lane -> column (lane & 31); register r -> row 8(r/4) + 4(lane/32) + r%4.
+
+    // Stage C in LDS. D layout: lane -> column (lane & 31); register r ->
+    // row 8(r/4) + 4(lane/32) + r%4 of the wave's 32-row tile.
+    float(*ct)[kCPitch] = reinterpret_cast<float(*)[kCPitch]>(smem);
+    stage_barrier();  // every wave is done with the operand stages (all loads were waited for)
+    if (mma) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int jt = 0; jt < TJ; ++jt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    ct[(wm * TI + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)]
+                      [wn * (kTileN / S::WC) + 32 * jt + fr] = acc[i][jt][r];
+    }
+    __syncthreads();
     if constexpr (EPI <= 2) {
+        // 16-byte pieces: row q / 32, columns 4 (q % 32) .. + 3.
 #pragma unroll
-        for (int jt = 0; jt < kColTiles; ++jt) {
-            const int n = n0 + wn * 32 * kColTiles + 32 * jt + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M) {
-                    float* c = C + (size_t(blockIdx.z) * M + m) * N + n;
-                    if constexpr (EPI == 1)
-                        *c = *c + acc[jt][r];
-                    else
-                        *c = acc[jt][r];
+        for (int q = tid; q < BM * 32; q += kThreads) {
+            const int row = q >> 5, c4 = q & 31, m = m0 + row;
+            if (m < M) {
+                float4* c = reinterpret_cast<float4*>(C + (size_t(blockIdx.z) * M + m) * N + n0) + c4;
+                const float4 v = *reinterpret_cast<const float4*>(&ct[row][4 * c4]);
+                if constexpr (EPI == 1) {
+                    const float4 o = *c;
+                    *c = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+                } else {
+                    *c = v;
                 }
             }
         }
-        return;
-    }
-    float(*ct)[kCPitch] = reinterpret_cast<float(*)[kCPitch]>(smem);
-    __syncthreads();  // every wave is done with the operand tiles
+    } else if constexpr (EPI == 3) {
+        // SwiGLU (engine/core.cpp:636-639): task q = row q / 8, act columns
+        // n0 / 2 + 8 (q % 8) .. + 7, stored as one 16-byte piece per plane.
 #pragma unroll
-    for (int jt = 0; jt < kColTiles; ++jt)
+        for (int q = tid; q < BM * 8; q += kThreads) {
+            const int row = q >> 3, c8 = 8 * (q & 7), m = m0 + row;
+            if (m < M) {
+                half8 hi, lo;
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            ct[wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)][wn * 32 * kColTiles + 32 * jt + (lane & 31)] =
-                acc[jt][r];
-    __syncthreads();
-    if constexpr (EPI == 3) {
-        // SwiGLU (engine/core.cpp:636-639): thread -> row tid / 4, outputs 16 (tid % 4) .. +15.
-        const int row = tid >> 2, c0 = (tid & 3) * 16, m = m0 + row;
-        if (row < TM && m < M) {
-            float* out = C + size_t(m) * (N / 2) + n0 / 2 + c0;
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                float o[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float gate = ct[row][c0 + i + e], up = ct[row][64 + c0 + i + e];
+                for (int e = 0; e < 8; ++e) {
+                    const float gate = ct[row][c8 + e], up = ct[row][64 + c8 + e];
                     const float half_gate = gate * 0.5f;
                     const float t = tanhf(half_gate);
-                    o[e] = gate * (0.5f + 0.5f * t) * up;
+                    const float o = gate * (0.5f + 0.5f * t) * up;
+                    hi[e] = static_cast<_Float16>(o);
+                    lo[e] = static_cast<_Float16>(o - static_cast<float>(hi[e]));
                 }
-                *reinterpret_cast<float4*>(out + i) = make_float4(o[0], o[1], o[2], o[3]);
+                const size_t at = size_t(m) * (N / 2) + n0 / 2 + c8;
+                *reinterpret_cast<half8*>(ep.act_hi + at) = hi;
+                *reinterpret_cast<half8*>(ep.act_lo + at) = lo;
             }
         }
     } else {
-        // Thread -> row tid / 4, channels j in [16 s, 16 s + 16) and j + 64 (s = tid % 4).
-        const int row = tid >> 2, s4 = tid & 3, m = m0 + row, head = blockIdx.x;
-        if (row < TM && m < M) {
-            const int pos = ep.pos0 + m;
-            if (head >= kQHeads + kKVHeads) {  // v: FP16 into the cache
-                uint16_t* vrow = ep.values + (size_t(head - kQHeads - kKVHeads) * ep.context + pos) * kHeadDim;
+        // Per row (one wave per row, rows wave, wave + kWaves, ...; lane l on
+        // channels l and l + 64): QK-norm and RoPE in place, the row left in
+        // LDS in its stored order (q: FP32 chain-permuted; k: FP16
+        // chain-permuted; v: FP16), then written out 16 bytes per lane.
+        uint16_t(*ht)[kHeadDim] = reinterpret_cast<uint16_t(*)[kHeadDim]>(smem + BM * kCPitch * 4);
+        const int head = blockIdx.x, j = lane;
+        const bool is_q = head < kQHeads, is_v = head >= kQHeads + kKVHeads;
+        constexpr int kRows = BM / S::kWaves;
+        if (is_v) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    vrow[16 * s4 + i] = f2h(ct[row][16 * s4 + i]);
-                    vrow[64 + 16 * s4 + i] = f2h(ct[row][64 + 16 * s4 + i]);
-                }
-            } else {
-                const bool is_q = head < kQHeads;
-                const float* w = is_q ? ep.q_norm : ep.k_norm;
-                float x0[16], x1[16];
-                double part = 0.0;
+            for (int k = 0; k < kRows; ++k) {
+                const int rr = wave + S::kWaves * k;
+                ht[rr][j] = f2h(ct[rr][j]);
+                ht[rr][j + 64] = f2h(ct[rr][j + 64]);
+            }
+        } else {
+            const float* w = is_q ? ep.q_norm : ep.k_norm;
+            const float w0 = w[j], w1 = w[j + 64];
+            float rc[kRows], rs[kRows];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    x0[i] = ct[row][16 * s4 + i];
-                    x1[i] = ct[row][64 + 16 * s4 + i];
-                    const float s0 = x0[i] * x0[i], s1 = x1[i] * x1[i];
-                    part += static_cast<double>(s0);
-                    part += static_cast<double>(s1);
-                }
-                part += __shfl_xor(part, 1);
-                part += __shfl_xor(part, 2);
+            for (int k = 0; k < kRows; ++k) {
+                const int pos = ep.pos0 + min(m0 + wave + S::kWaves * k, M - 1);
+                rc[k] = ep.cosines[size_t(pos) * 64 + j];
+                rs[k] = ep.sines[size_t(pos) * 64 + j];
+            }
+#pragma unroll
+            for (int k = 0; k < kRows; ++k) {
+                const int rr = wave + S::kWaves * k;
+                const float x0 = ct[rr][j], x1 = ct[rr][j + 64];
+                const float s0 = x0 * x0, s1 = x1 * x1;
+                double part = static_cast<double>(s0) + static_cast<double>(s1);
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
                 const float inv = 1.0f / __builtin_sqrtf(static_cast<float>(part) / 128.0f + 1e-6f);
-                const float* cs = ep.cosines + size_t(pos) * 64;
-                const float* sn = ep.sines + size_t(pos) * 64;
-                float* qrow = C + size_t(m) * N + head * kHeadDim;
-                uint16_t* krow = ep.keys + (size_t(head - kQHeads) * ep.context + pos) * kHeadDim;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int j = 16 * s4 + i;
-                    const float n0v = (x0[i] * inv) * w[j], n1v = (x1[i] * inv) * w[j + 64];
-                    const float o0 = n0v * cs[j] - n1v * sn[j];
-                    const float o1 = n1v * cs[j] + n0v * sn[j];
-                    if (is_q) {
-                        qrow[kperm(j)] = o0;
-                        qrow[kperm(j + 64)] = o1;
-                    } else {
-                        krow[kperm(j)] = f2h(o0);
-                        krow[kperm(j + 64)] = f2h(o1);
-                    }
+                const float n0v = (x0 * inv) * w0, n1v = (x1 * inv) * w1;
+                const float o0 = n0v * rc[k] - n1v * rs[k];
+                const float o1 = n1v * rc[k] + n0v * rs[k];
+                if (is_q) {
+                    ct[rr][kperm(j)] = o0;  // the row's reads above came first
+                    ct[rr][kperm(j + 64)] = o1;
+                } else {
+                    ht[rr][kperm(j)] = f2h(o0);
+                    ht[rr][kperm(j + 64)] = f2h(o1);
                 }
+            }
+        }
+        __syncthreads();
+        if (is_q) {
+#pragma unroll
+            for (int q = tid; q < BM * 32; q += kThreads) {
+                const int row = q >> 5, c4 = q & 31, m = m0 + row;
+                if (m < M)
+                    reinterpret_cast<float4*>(C + size_t(m) * N + head * kHeadDim)[c4] =
+                        *reinterpret_cast<const float4*>(&ct[row][4 * c4]);
+            }
+        } else {
+            uint16_t* cache = (is_v ? ep.values + size_t(head - kQHeads - kKVHeads) * ep.context * kHeadDim
+                                    : ep.keys + size_t(head - kQHeads) * ep.context * kHeadDim);
+#pragma unroll
+            for (int q = tid; q < BM * 16; q += kThreads) {
+                const int row = q >> 4, c8 = q & 15, m = m0 + row;
+                if (m < M)
+                    reinterpret_cast<u32x4*>(cache + size_t(ep.pos0 + m) * kHeadDim)[c8] =
+                        *reinterpret_cast<const u32x4*>(&ht[row][8 * c8]);
             }
         }
     }
@@ -251,18 +351,21 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const int* __restrict__
 // x + the SPLITS partial products of a K-split GEMM in a fixed order.
 template <int SPLITS>
 __device__ __forceinline__ float fold_splits(float x, const float* p, size_t stride) {
+    static_assert(SPLITS == 0 || SPLITS == 4, "K-split GEMMs use 4 ranges");
     if constexpr (SPLITS == 0) return x;
-    else if constexpr (SPLITS == 2) return x + (p[0] + p[stride]);
-    else return x + ((p[0] + p[stride]) + p[2 * stride]);
+    else return x + ((p[0] + p[stride]) + (p[2 * stride] + p[3 * stride]));
 }
 
-// out[b] = RMSNorm(x[b]) (engine/core.cpp:207-215): FP32 squares, FP64 sum.
+
+// out[b] = RMSNorm(x[b]) (engine/core.cpp:207-215): FP32 squares, FP64 sum,
+// written as the FP16 hi / lo planes of the next GEMM's A operand.
 // With SPLITS > 0 the residual first absorbs the pending partial products of
 // a K-split GEMM (parts[z][b], z < SPLITS) and is written back.
 template <int SPLITS = 0>
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X, const float* __restrict__ w,
-                                                           float* __restrict__ out, const float* __restrict__ parts,
-                                                           int rows) {
+                                                           uint16_t* __restrict__ out_hi,
+                                                           uint16_t* __restrict__ out_lo,
+                                                           const float* __restrict__ parts, int rows) {
     const int b = blockIdx.x, tid = threadIdx.x;
     float* x = X + size_t(b) * kHidden;
     float v[4];
@@ -287,7 +390,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int j = tid + 256 * k;
-        out[size_t(b) * kHidden + j] = (v[k] * inv) * w[j];
+        split_store((v[k] * inv) * w[j], out_hi, out_lo, size_t(b) * kHidden + j);
     }
 }
 
@@ -304,14 +407,14 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
 // exchange with lane ^ 32 per tile. q and the cached keys share the
 // chain-permuted channel order, which leaves q . k unchanged.
 constexpr int kFaRows = 32, kFaKeys = 32, kFaWaves = 4, kVtPitch = 36, kFaccPitch = 132;
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
 // Two waves per SIMD (at most 256 registers per lane, two workgroups per
 // CU): one wave's softmax and V^T work overlaps the other's matrix ops.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_mfma_kernel(const float* __restrict__ QKV,
                                                                 const uint16_t* __restrict__ keys,
                                                                 const uint16_t* __restrict__ values,
-                                                                float* __restrict__ attended, int rows, int pos0,
+                                                                uint16_t* __restrict__ att_hi,
+                                                                uint16_t* __restrict__ att_lo, int rows, int pos0,
                                                                 int context, float scale) {
     // LDS: per-wave V^T tiles during the key loop, then the 4 waves' outputs.
     __shared__ __align__(16) unsigned char lds[kFaWaves * kFaRows * kFaccPitch * 4];
@@ -466,7 +569,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             e[w] = fm[w][q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fm[w][q] - mx);
             lsum = __builtin_fmaf(e[w], fl[w][q], lsum);
         }
-        float* out = attended + size_t(b0 + q) * kQDim + head * kHeadDim + c0;
+        const size_t out = size_t(b0 + q) * kQDim + head * kHeadDim + c0;
 #pragma unroll
         for (int k4 = 0; k4 < 4; ++k4) {
             float o[4] = {0.f, 0.f, 0.f, 0.f};
@@ -479,7 +582,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 o[2] = __builtin_fmaf(e[w], v.z, o[2]);
                 o[3] = __builtin_fmaf(e[w], v.w, o[3]);
             }
-            reinterpret_cast<float4*>(out)[k4] = make_float4(o[0] / lsum, o[1] / lsum, o[2] / lsum, o[3] / lsum);
+            half4 hi, lo;  // the O GEMM's A operand as FP16 hi / lo
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const float v = o[e4] / lsum;
+                hi[e4] = static_cast<_Float16>(v);
+                lo[e4] = static_cast<_Float16>(v - static_cast<float>(hi[e4]));
+            }
+            *reinterpret_cast<half4*>(att_hi + out + 4 * k4) = hi;
+            *reinterpret_cast<half4*>(att_lo + out + 4 * k4) = lo;
         }
     }
 }
@@ -492,27 +603,54 @@ __global__ __launch_bounds__(256) void fold_rows_kernel(float* __restrict__ X, c
     if (idx < size_t(rows) * kHidden) X[idx] = fold_splits<SPLITS>(X[idx], parts + idx, size_t(rows) * kHidden);
 }
 
-// 64-row tiles when they give every CU a workgroup, else 32-row tiles.
-// `splits` K ranges (EPI 2) count towards the workgroups.
+// The tallest tile (128, 64 or 32 rows) that still gives every CU a
+// workgroup; `splits` K ranges (EPI 2) count towards the workgroups.
 template <int EPI>
-void gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, hipStream_t stream, int splits = 1,
-          const QkvEpilogue& ep = {}) {
+void gemm(const uint16_t* Ah, const uint16_t* Al, const uint16_t* W, float* C, int M, int N, int K,
+          hipStream_t stream, int splits = 1, const GemmEpilogue& ep = {}) {
     require(N % kTileN == 0 && K % (kTileK * splits) == 0 && M > 0 && (splits == 1 || EPI == 2),
             "gemm: unsupported shape");
-    if ((M + 63) / 64 * (N / kTileN) * splits >= 256)
-        gemm_kernel<64, EPI><<<dim3(N / kTileN, (M + 63) / 64, splits), 256, 0, stream>>>(A, W, C, M, N, K, ep);
+    const int tiles = N / kTileN * splits;
+    auto launch = [&](auto bm) {
+        constexpr int BM = decltype(bm)::value;
+        gemm_kernel<BM, EPI><<<dim3(N / kTileN, (M + BM - 1) / BM, splits), GemmShape<BM>::kWaves * 64, 0, stream>>>(
+            Ah, Al, W, C, M, N, K, ep);
+    };
+    if ((M + 127) / 128 * tiles >= 256)
+        launch(std::integral_constant<int, 128>{});
+    else if ((M + 63) / 64 * tiles >= 256)
+        launch(std::integral_constant<int, 64>{});
     else
-        gemm_kernel<32, EPI><<<dim3(N / kTileN, (M + 31) / 32, splits), 256, 0, stream>>>(A, W, C, M, N, K, ep);
+        launch(std::integral_constant<int, 32>{});
+}
+
+// FP32 rows -> FP16 hi / lo planes (GEMM operands handed over as FP32).
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ A, uint16_t* __restrict__ hi,
+                                                         uint16_t* __restrict__ lo, size_t n) {
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
+        split_store(A[i], hi, lo, i);
 }
 
 }  // namespace
 
 void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
                  hipStream_t stream) {
+    require(M > 0 && K > 0, "gemm: unsupported shape");
+    // Operand planes for this call (an operator entry point for tests and
+    // benchmarks, not on the inference path).
+    const size_t n = size_t(M) * K;
+    auto check = [](hipError_t e, const char* what) {
+        require(e == hipSuccess, std::string("HIP error: ") + hipGetErrorString(e) + " (" + what + ")");
+    };
+    uint16_t* planes = nullptr;
+    check(hipMalloc(&planes, 2 * n * sizeof(uint16_t)), "hipMalloc");
+    split_rows_kernel<<<unsigned(std::min<size_t>((n + 255) / 256, 4096)), 256, 0, stream>>>(A, planes, planes + n, n);
     if (accumulate)
-        gemm<1>(A, W, C, M, N, K, stream);
+        gemm<1>(planes, planes + n, W, C, M, N, K, stream);
     else
-        gemm<0>(A, W, C, M, N, K, stream);
+        gemm<0>(planes, planes + n, W, C, M, N, K, stream);
+    check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    check(hipFree(planes), "hipFree");
 }
 
 void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, const int* ids_dev, int rows, int pos0,
@@ -522,26 +660,26 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
     embed_rows_kernel<<<rows, 256, 0, stream>>>(ids_dev, embed, s.x);
     const float scale = 1.0f / std::sqrt(128.0f);
     // The O and down GEMMs (1024 output columns, K = 2048 / 3072) split K
-    // into 1024-wide ranges for parallelism at any row count; the row kernel
-    // after each adds the partials to the residual in a fixed order, so a
-    // row's result still does not depend on the rows around it.
-    constexpr int kOSplits = kQDim / 1024, kDownSplits = kFFN / 1024;
+    // into 4 ranges for parallelism at any row count; the row kernel after
+    // each adds the partials to the residual in a fixed order, so a row's
+    // result still does not depend on the rows around it.
+    constexpr int kSplits = 4;
     for (int l = 0; l < kLayers; ++l) {
         const PrefillLayer& L = layers[l];
         if (l == 0)
-            rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h, nullptr, rows);
+            rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, nullptr, rows);
         else
-            rmsnorm_rows_kernel<kDownSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h, s.part, rows);
-        const QkvEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context};
-        gemm<4>(s.h, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream, 1, ep);
+            rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, s.part, rows);
+        const GemmEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context, s.act_hi, s.act_lo};
+        gemm<4>(s.h_hi, s.h_lo, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream, 1, ep);
         attn_prefill_mfma_kernel<<<dim3((rows + kFaRows - 1) / kFaRows, kQHeads), 256, 0, stream>>>(
-            s.qkv, L.keys, L.values, s.attended, rows, pos0, context, scale);
-        gemm<2>(s.attended, L.o_n, s.part, rows, kHidden, kQDim, stream, kOSplits);
-        rmsnorm_rows_kernel<kOSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h, s.part, rows);
-        gemm<3>(s.h, L.gateup_n, s.act, rows, 2 * kFFN, kHidden, stream);
-        gemm<2>(s.act, L.down_n, s.part, rows, kHidden, kFFN, stream, kDownSplits);
+            s.qkv, L.keys, L.values, s.att_hi, s.att_lo, rows, pos0, context, scale);
+        gemm<2>(s.att_hi, s.att_lo, L.o_n, s.part, rows, kHidden, kQDim, stream, kSplits);
+        rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h_hi, s.h_lo, s.part, rows);
+        gemm<3>(s.h_hi, s.h_lo, L.gateup_n, nullptr, rows, 2 * kFFN, kHidden, stream, 1, ep);
+        gemm<2>(s.act_hi, s.act_lo, L.down_n, s.part, rows, kHidden, kFFN, stream, kSplits);
     }
-    fold_rows_kernel<kDownSplits><<<(rows * kHidden + 255) / 256, 256, 0, stream>>>(s.x, s.part, rows);
+    fold_rows_kernel<kSplits><<<(rows * kHidden + 255) / 256, 256, 0, stream>>>(s.x, s.part, rows);
 }
 
 }  // namespace qwen_hip

@@ -22,18 +22,22 @@ struct PrefillLayer {
     uint16_t* values;          // [8][context][128]
 };
 
-// FP32 activations of one batched pass (up to kPrefillRows rows each).
+// Activations of one batched pass (up to kPrefillRows rows each). GEMM
+// inputs are kept as FP16 hi / lo planes (hi = fp16(v), lo = fp16(v - hi)).
 struct PrefillScratch {
-    float* x;         // [rows x 1024] residual stream
-    float* h;         // [rows x 1024] normalized
-    float* qkv;       // [rows x 4096]
-    float* attended;  // [rows x 2048]
-    float* act;       // [rows x 3072]
-    float* part;      // [3 x rows x 1024] K-split partial products of the O and down GEMMs
+    float* x;           // [rows x 1024] residual stream (FP32)
+    uint16_t* h_hi;     // [rows x 1024] normalized
+    uint16_t* h_lo;
+    float* qkv;         // [rows x 4096] (FP32; q heads normed and rotated)
+    uint16_t* att_hi;   // [rows x 2048] attention output
+    uint16_t* att_lo;
+    uint16_t* act_hi;   // [rows x 3072] SwiGLU output
+    uint16_t* act_lo;
+    float* part;        // [4 x rows x 1024] K-split partial products of the O and down GEMMs
 };
 
 // C[M x N] (+)= A[M x K] . W[N x K]^T; A FP32 split into FP16 hi + lo on the
-// matrix cores; N, K multiples of 64.
+// matrix cores; N a multiple of 128, K of 32.
 void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
                  hipStream_t stream);
 
