@@ -419,7 +419,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // LDS: per-wave V^T tiles during the key loop, then the 4 waves' outputs.
     __shared__ __align__(16) unsigned char lds[kFaWaves * kFaRows * kFaccPitch * 4];
     __shared__ float fm[kFaWaves][kFaRows], fl[kFaWaves][kFaRows];
-    const int qb = blockIdx.x, head = blockIdx.y, g = head >> 1;
+    // Workgroup w runs on XCD w % 8 (round-robin dispatch): KV head g = w % 8
+    // keeps every workgroup reading one head's K/V rows on one XCD, so they
+    // stay in its L2 (2 MiB per head at 4096 positions); the query blocks
+    // run heaviest (latest) first.
+    const int nqb = gridDim.x / (2 * kKVHeads), k = blockIdx.x / kKVHeads;
+    const int g = blockIdx.x % kKVHeads, head = 2 * g + (k & 1), qb = nqb - 1 - (k >> 1);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hf = lane >> 5;
     const int b0 = qb * kFaRows, nrows = min(kFaRows, rows - b0);
@@ -672,7 +677,7 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
             rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, s.part, rows);
         const GemmEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context, s.act_hi, s.act_lo};
         gemm<4>(s.h_hi, s.h_lo, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream, 1, ep);
-        attn_prefill_mfma_kernel<<<dim3((rows + kFaRows - 1) / kFaRows, kQHeads), 256, 0, stream>>>(
+        attn_prefill_mfma_kernel<<<(rows + kFaRows - 1) / kFaRows * kQHeads, 256, 0, stream>>>(
             s.qkv, L.keys, L.values, s.att_hi, s.att_lo, rows, pos0, context, scale);
         gemm<2>(s.att_hi, s.att_lo, L.o_n, s.part, rows, kHidden, kQDim, stream, kSplits);
         rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h_hi, s.h_lo, s.part, rows);
