@@ -395,47 +395,99 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
 }
 
 // Causal attention for a prefill chunk on the matrix cores (engine/core.cpp:
-// 407-605, same math as the decode path): workgroup = 32 consecutive query
-// rows x one query head; its 4 waves take every 4th tile of 32 keys, each
-// with its own online softmax, and merge (max, sum, output) at the end.
-//   S^T = K Q^T  (A = 32 keys x 16 dims straight from the cache, B = Q^T as
-//                 FP16 hi + lo of the FP32 q, so products are exact)
-//   O^T += V^T P^T (A = V^T through a per-wave LDS transpose, B = P^T as
-//                 FP16 hi + lo of the FP32 probabilities)
+// 407-605, same math as the decode path):
+//   S^T = K Q^T  (A = 32 keys x 16 dims, B = Q^T as FP16 hi + lo of the FP32
+//                 q, so products are exact)
+//   O^T += V^T P^T (A = V^T, B = P^T as FP16 hi + lo of the FP32
+//                 probabilities)
 // With S^T in the 32x32 accumulator layout each lane holds 16 keys of one
 // query (lane % 32), so the softmax statistics stay in the lane: one
 // exchange with lane ^ 32 per tile. q and the cached keys share the
 // chain-permuted channel order, which leaves q . k unchanged.
-constexpr int kFaRows = 32, kFaKeys = 32, kFaWaves = 4, kVtPitch = 36, kFaccPitch = 132;
+constexpr int kFaRows = 32, kFaKeys = 32, kFaccPitch = 132;
 
-// Two waves per SIMD (at most 256 registers per lane, two workgroups per
-// CU): one wave's softmax and V^T work overlaps the other's matrix ops.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_mfma_kernel(const float* __restrict__ QKV,
-                                                                const uint16_t* __restrict__ keys,
-                                                                const uint16_t* __restrict__ values,
-                                                                uint16_t* __restrict__ att_hi,
-                                                                uint16_t* __restrict__ att_lo, int rows, int pos0,
-                                                                int context, float scale) {
-    // LDS: per-wave V^T tiles during the key loop, then the 4 waves' outputs.
-    __shared__ __align__(16) unsigned char lds[kFaWaves * kFaRows * kFaccPitch * 4];
-    __shared__ float fm[kFaWaves][kFaRows], fl[kFaWaves][kFaRows];
+// Workgroup = 32 consecutive query rows x one KV head g, 8 waves: wave
+// (h, s) = (wave & 1, wave >> 1) runs query head 2g + h over the key tiles
+// kt = s (mod 4) with its own online softmax, and the 4 key splits of each
+// head are merged at the end. The two waves of a split use the same tiles:
+// they load each K/V tile together (direct global -> LDS loads, 8 KiB each)
+// into a double-buffered LDS ring, one tile ahead of the matrix cores, so a
+// wave streams half a tile per step instead of a whole one (a wave retires
+// only about 10 GB/s of loads). K is read from LDS as the S^T operand and V^T
+// with the LDS transpose load (ds_read_b64_tr_b16), so V needs no transpose
+// pass through registers.
+constexpr int kFbTileBytes = kFaKeys * kHeadDim * 2;        // one K or V tile (8 KiB)
+constexpr int kFbSplitBytes = 2 * kFbTileBytes;             // K then V of one split
+constexpr int kFbStageBytes = 4 * kFbSplitBytes;            // the 4 splits' tiles of one step
+constexpr int kFbMergeBytes = 8 * kFaRows * kFaccPitch * 4; // 8 waves' outputs
+constexpr int kFbLds = 2 * kFbStageBytes > kFbMergeBytes ? 2 * kFbStageBytes : kFbMergeBytes;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// K and V tiles in LDS: rows of 128 halves (sixteen 16-byte pieces), piece p
+// of key row r in 16-byte slot 16 r + (p ^ (r & 15)), so the lanes of one
+// LDS access cycle read distinct banks.
+__device__ __forceinline__ int fb_slot(int r, int p) { return 16 * r + (p ^ (r & 15)); }
+
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane 4a + b
+// receives element b of the 8-byte chunks addressed by lanes a, a + 4,
+// a + 8 and a + 12, in that order.
+__device__ __forceinline__ short4_t lds_read_tr16(const unsigned char* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) short4_t*)(const_cast<unsigned char*>(p)));
+#else
+    (void)p;
+    return short4_t{0, 0, 0, 0};
+#endif
+}
+
+__global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __restrict__ QKV,
+                                                                  const uint16_t* __restrict__ keys,
+                                                                  const uint16_t* __restrict__ values,
+                                                                  uint16_t* __restrict__ att_hi,
+                                                                  uint16_t* __restrict__ att_lo, int rows, int pos0,
+                                                                  int context, float scale) {
+    __shared__ __align__(16) unsigned char lds[kFbLds];
+    __shared__ float fm[8][kFaRows], fl[8][kFaRows];
     // Workgroup w runs on XCD w % 8 (round-robin dispatch): KV head g = w % 8
     // keeps every workgroup reading one head's K/V rows on one XCD, so they
-    // stay in its L2 (2 MiB per head at 4096 positions); the query blocks
-    // run heaviest (latest) first.
-    const int nqb = gridDim.x / (2 * kKVHeads), k = blockIdx.x / kKVHeads;
-    const int g = blockIdx.x % kKVHeads, head = 2 * g + (k & 1), qb = nqb - 1 - (k >> 1);
+    // stay in its L2; the query blocks run heaviest (latest) first.
+    const int nqb = gridDim.x / kKVHeads;
+    const int g = blockIdx.x % kKVHeads, qb = nqb - 1 - blockIdx.x / kKVHeads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = wave & 1, sp = wave >> 1, head = 2 * g + h;
     const int col = lane & 31, hf = lane >> 5;
     const int b0 = qb * kFaRows, nrows = min(kFaRows, rows - b0);
     const int last = pos0 + b0 + nrows - 1;  // last key any query of the block attends to
     const int ntiles = last / kFaKeys + 1;
+    const int nsteps = (ntiles + 3) / 4;     // steps of 4 tiles (one per split)
     const size_t head_base = size_t(g) * context;
     const int qpos = pos0 + b0 + col;        // causal limit of this lane's query
-    // Softmax in base 2: scores scaled by log2(e) / sqrt(128), weights 2^(s - m)
-    // = e^(scaled score - max) from the hardware exp2.
     const float scale2 = scale * 1.4426950408889634f;
-    uint16_t(*vt)[kVtPitch] = reinterpret_cast<uint16_t(*)[kVtPitch]>(lds + wave * 128 * kVtPitch * 2);
+
+    // Direct loads of step i: split sp's tile kt = 4 i + sp; load j of this
+    // wave fills 16-byte slot 64 (2 j + h) + lane of the split's K tile
+    // (j < 4) or V tile; rows past `last` repeat row `last` (masked).
+    int ld_row[8], ld_col[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = (64 * (2 * j + h) + lane) & 511, r = q >> 4;
+        ld_row[j] = r;
+        ld_col[j] = 8 * ((q & 15) ^ (r & 15));
+    }
+    auto issue = [&](int step) {
+        const int kt = 4 * step + sp;
+        unsigned char* dst = lds + (step & 1) * kFbStageBytes + sp * kFbSplitBytes;
+        if (kt < ntiles) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = min(kt * kFaKeys + ld_row[j], last);
+                const uint16_t* src = (j < 4 ? keys : values) + (head_base + key) * kHeadDim + ld_col[j];
+                load_lds16(src, dst + 1024 * (2 * j + h));
+            }
+        }
+    };
+    issue(0);
 
     // Q^T operand: query b0 + col (rows past the chunk repeat its last row
     // and are never written), channels 16s + 8hf .. +7.
@@ -449,9 +501,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const _Float16 h = static_cast<_Float16>(v[i]);
-                qh[s][i] = h;
-                ql[s][i] = static_cast<_Float16>(v[i] - static_cast<float>(h));
+                const _Float16 hh = static_cast<_Float16>(v[i]);
+                qh[s][i] = hh;
+                ql[s][i] = static_cast<_Float16>(v[i] - static_cast<float>(hh));
             }
         }
     }
@@ -462,42 +514,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-    const int vp = lane & 15, vg = lane >> 4;  // V^T fill: key pair vp, channel group vg
-    for (int kt = wave; kt < ntiles; kt += kFaWaves) {
-        const int t0 = kt * kFaKeys;
-        // Keys past `last` load row `last` and are masked below.
-        const u32x4* krow = reinterpret_cast<const u32x4*>(keys + (head_base + min(t0 + col, last)) * kHeadDim);
-        half8 ka[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) ka[s] = __builtin_bit_cast(half8, krow[2 * s + hf]);
-        const u32x4* va_row = reinterpret_cast<const u32x4*>(values + (head_base + min(t0 + 2 * vp, last)) * kHeadDim);
-        const u32x4* vb_row =
-            reinterpret_cast<const u32x4*>(values + (head_base + min(t0 + 2 * vp + 1, last)) * kHeadDim);
-        u32x4 va[4], vb[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            va[r] = va_row[vg + 4 * r];
-            vb[r] = vb_row[vg + 4 * r];
-        }
+    // Transpose-load addresses in a V tile: lane j of 16-lane group G hands
+    // over key row 8 hh + 4 (G / 2) + jj / 4 (+ 16 per key step), channels
+    // 32 dt + 16 (G % 2) + 4 (jj % 4) (jj = j % 16).
+    const int grp = lane >> 4, jj = lane & 15;
+    const int tr_row = 4 * (grp >> 1) + (jj >> 2), tr_ch = 16 * (grp & 1) + 4 * (jj & 3);
+    for (int step = 0; step < nsteps; ++step) {
+        wait_vmcnt<0>();       // this wave's loads of the step have landed
+        stage_barrier();       // everyone's have; the other buffer is free again
+        if (step + 1 < nsteps) issue(step + 1);
+        const int kt = 4 * step + sp, t0 = kt * kFaKeys;
+        if (kt >= ntiles) continue;  // wave-uniform: this split has no tile in the last step
+        const unsigned char* k_lds = lds + (step & 1) * kFbStageBytes + sp * kFbSplitBytes;
+        const unsigned char* v_lds = k_lds + kFbTileBytes;
         floatx16 st;
 #pragma unroll
         for (int r = 0; r < 16; ++r) st[r] = 0.f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[s], qh[s], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[s], ql[s], st, 0, 0, 0);
-        }
-        // V^T: channel 32r + 8vg + e, keys 2vp (low half) and 2vp + 1 (high half).
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t aw[4] = {va[r].x, va[r].y, va[r].z, va[r].w};
-            const uint32_t bw[4] = {vb[r].x, vb[r].y, vb[r].z, vb[r].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int ch = 32 * r + 8 * vg + 2 * i;
-                *reinterpret_cast<uint32_t*>(&vt[ch][2 * vp]) = (aw[i] & 0xffffu) | (bw[i] << 16);
-                *reinterpret_cast<uint32_t*>(&vt[ch + 1][2 * vp]) = (aw[i] >> 16) | (bw[i] & 0xffff0000u);
-            }
+            const half8 ka = *reinterpret_cast<const half8*>(k_lds + 16 * fb_slot(col, 2 * s + hf));
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[s], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[s], st, 0, 0, 0);
         }
         // Online softmax; register r holds key t0 + 8(r/4) + 4hf + r%4.
         float sv[16];
@@ -517,9 +554,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int r = 0; r < 16; ++r) {
             const float p = sv[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[r] - mnew);
             psum += p;
-            const _Float16 h = static_cast<_Float16>(p);
-            ph[r >> 3][r & 7] = h;
-            pl[r >> 3][r & 7] = static_cast<_Float16>(p - static_cast<float>(h));
+            const _Float16 hh = static_cast<_Float16>(p);
+            ph[r >> 3][r & 7] = hh;
+            pl[r >> 3][r & 7] = static_cast<_Float16>(p - static_cast<float>(hh));
         }
         psum += __shfl_xor(psum, 32);
         l = l * factor + psum;
@@ -531,28 +568,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 for (int r = 0; r < 16; ++r) acc[dt][r] *= factor;
         }
         m = mnew;
-        // vt is written and read by this wave only.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // P^T k slot 8 hf + i of key step j is key 16 j + 8 (i / 4) + 4 hf + i % 4;
+        // transpose load hh covers keys 16 j + 8 hh + 4 hf + 0..3 of channel
+        // 32 dt + lane % 32, the same order.
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const uint16_t* vrow = vt[32 * dt + col];
-                const half4 lo4 = *reinterpret_cast<const half4*>(vrow + 16 * j + 4 * hf);
-                const half4 hi4 = *reinterpret_cast<const half4*>(vrow + 16 * j + 8 + 4 * hf);
-                const half8 a = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+                const int c = 32 * dt + tr_ch;
+                const int r0 = 16 * j + tr_row, r1 = r0 + 8;
+                const short4_t lo4 = lds_read_tr16(v_lds + 16 * fb_slot(r0, c >> 3) + 2 * (c & 7));
+                const short4_t hi4 = lds_read_tr16(v_lds + 16 * fb_slot(r1, c >> 3) + 2 * (c & 7));
+                const half8 a = __builtin_bit_cast(half8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph[j], acc[dt], 0, 0, 0);
                 acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl[j], acc[dt], 0, 0, 0);
             }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
-    // Merge the 4 waves: O^T register r of tile dt is channel 32dt + 8(r/4) + 4hf + r%4 of query col.
-    __syncthreads();  // every wave is done with its V^T tile
+    // Merge the 4 splits of each head: O^T register r of tile dt is channel
+    // 32dt + 8(r/4) + 4hf + r%4 of query col.
+    stage_barrier();  // every wave is done with the K/V stages (all loads were waited for)
     float(*facc)[kFaccPitch] = reinterpret_cast<float(*)[kFaccPitch]>(lds + wave * kFaRows * kFaccPitch * 4);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -563,40 +598,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         fl[wave][col] = l;
     }
     __syncthreads();
-    const int q = tid >> 3, c0 = (tid & 7) * 16;
+    // Thread -> head hm = tid / 256, query q, channels c0 .. c0 + 15.
+    const int hm = tid >> 8, q = (tid >> 3) & 31, c0 = (tid & 7) * 16;
     if (q < nrows) {
-        float mx = fm[0][q];
+        float mx = fm[hm][q];
 #pragma unroll
-        for (int w = 1; w < kFaWaves; ++w) mx = fmaxf(mx, fm[w][q]);
-        float e[kFaWaves], lsum = 0.f;
+        for (int s = 1; s < 4; ++s) mx = fmaxf(mx, fm[2 * s + hm][q]);
+        float e[4], lsum = 0.f;
 #pragma unroll
-        for (int w = 0; w < kFaWaves; ++w) {
-            e[w] = fm[w][q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fm[w][q] - mx);
-            lsum = __builtin_fmaf(e[w], fl[w][q], lsum);
+        for (int s = 0; s < 4; ++s) {
+            const int w = 2 * s + hm;
+            e[s] = fm[w][q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fm[w][q] - mx);
+            lsum = __builtin_fmaf(e[s], fl[w][q], lsum);
         }
-        const size_t out = size_t(b0 + q) * kQDim + head * kHeadDim + c0;
+        const size_t out = size_t(b0 + q) * kQDim + (2 * g + hm) * kHeadDim + c0;
+        half8 hi[2], lo[2];
 #pragma unroll
         for (int k4 = 0; k4 < 4; ++k4) {
             float o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int w = 0; w < kFaWaves; ++w) {
+            for (int s = 0; s < 4; ++s) {
                 const float4 v = *reinterpret_cast<const float4*>(
-                    reinterpret_cast<const float*>(lds + w * kFaRows * kFaccPitch * 4) + q * kFaccPitch + c0 + 4 * k4);
-                o[0] = __builtin_fmaf(e[w], v.x, o[0]);
-                o[1] = __builtin_fmaf(e[w], v.y, o[1]);
-                o[2] = __builtin_fmaf(e[w], v.z, o[2]);
-                o[3] = __builtin_fmaf(e[w], v.w, o[3]);
+                    reinterpret_cast<const float*>(lds + (2 * s + hm) * kFaRows * kFaccPitch * 4) + q * kFaccPitch +
+                    c0 + 4 * k4);
+                o[0] = __builtin_fmaf(e[s], v.x, o[0]);
+                o[1] = __builtin_fmaf(e[s], v.y, o[1]);
+                o[2] = __builtin_fmaf(e[s], v.z, o[2]);
+                o[3] = __builtin_fmaf(e[s], v.w, o[3]);
             }
-            half4 hi, lo;  // the O GEMM's A operand as FP16 hi / lo
 #pragma unroll
-            for (int e4 = 0; e4 < 4; ++e4) {
+            for (int e4 = 0; e4 < 4; ++e4) {  // the O GEMM's A operand as FP16 hi / lo
                 const float v = o[e4] / lsum;
-                hi[e4] = static_cast<_Float16>(v);
-                lo[e4] = static_cast<_Float16>(v - static_cast<float>(hi[e4]));
+                const _Float16 hh = static_cast<_Float16>(v);
+                hi[k4 >> 1][4 * (k4 & 1) + e4] = hh;
+                lo[k4 >> 1][4 * (k4 & 1) + e4] = static_cast<_Float16>(v - static_cast<float>(hh));
             }
-            *reinterpret_cast<half4*>(att_hi + out + 4 * k4) = hi;
-            *reinterpret_cast<half4*>(att_lo + out + 4 * k4) = lo;
         }
+        *reinterpret_cast<half8*>(att_hi + out) = hi[0];
+        *reinterpret_cast<half8*>(att_hi + out + 8) = hi[1];
+        *reinterpret_cast<half8*>(att_lo + out) = lo[0];
+        *reinterpret_cast<half8*>(att_lo + out + 8) = lo[1];
     }
 }
 
@@ -677,7 +718,7 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
             rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, s.part, rows);
         const GemmEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context, s.act_hi, s.act_lo};
         gemm<4>(s.h_hi, s.h_lo, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream, 1, ep);
-        attn_prefill_mfma_kernel<<<(rows + kFaRows - 1) / kFaRows * kQHeads, 256, 0, stream>>>(
+        attn_prefill_mfma_kernel<<<(rows + kFaRows - 1) / kFaRows * kKVHeads, 512, 0, stream>>>(
             s.qkv, L.keys, L.values, s.att_hi, s.att_lo, rows, pos0, context, scale);
         gemm<2>(s.att_hi, s.att_lo, L.o_n, s.part, rows, kHidden, kQDim, stream, kSplits);
         rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h_hi, s.h_lo, s.part, rows);
