@@ -704,40 +704,67 @@ __global__ __launch_bounds__(512) void attn_decode_batch_kernel(const AttnBatch 
 // Merge of the position splits of one query head (flash-decoding, fixed
 // split order): o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max).
 // One split: attention already wrote the normalized output.
-// All partials are loaded up front (entries past ns read split 0 and are
-// skipped), so the merge costs one memory round trip.
+// 512 threads: group q = tid / 128 merges splits 8q .. 8q + 7 against its own
+// maximum (thread j = channel j), then the 4 group results are combined with
+// weights exp(m_q - max): the same sums, reassociated in a fixed order. Each
+// wave loads 8 splits' entries (a wave retires only about 10 GB/s of loads,
+// so they are spread over 8 waves), all issued up front (entries past ns
+// read split 0 and are skipped).
+constexpr int kMergeGroups = 4, kMergePer = kAttnSplits / kMergeGroups;
+static_assert(kAttnSplits % kMergeGroups == 0, "merge groups split the splits evenly");
 __device__ __forceinline__ void attn_merge_body(const AttnArgs& a, int head) {
-    const int j = threadIdx.x;
+    const int tid = threadIdx.x, j = tid & 127, grp = tid >> 7;
     int chunk, ns;
     attn_split(a.pos + 1, chunk, ns);
     if (ns == 1) return;
     const float* base = a.partial + size_t(head >> 1) * kAttnSplits * kAttnPartial + (head & 1) * 132;
-    float mv[kAttnSplits], lv[kAttnSplits], ov[kAttnSplits];
+    float mv[kMergePer], lv[kMergePer], ov[kMergePer];
 #pragma unroll
-    for (int k = 0; k < kAttnSplits; ++k) {
-        const float* e = base + (k < ns ? k : 0) * kAttnPartial;
+    for (int k = 0; k < kMergePer; ++k) {
+        const int sidx = grp * kMergePer + k;
+        const float* e = base + (sidx < ns ? sidx : 0) * kAttnPartial;
         mv[k] = e[128];
         lv[k] = e[129];
         ov[k] = e[j];
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kAttnSplits; ++k)
-        if (k < ns) mx = fmaxf(mx, mv[k]);
+    for (int k = 0; k < kMergePer; ++k)
+        if (grp * kMergePer + k < ns) mx = fmaxf(mx, mv[k]);
     float l = 0.f, o = 0.f;
 #pragma unroll
-    for (int k = 0; k < kAttnSplits; ++k)
-        if (k < ns) {
+    for (int k = 0; k < kMergePer; ++k)
+        if (grp * kMergePer + k < ns) {
             const float w = expf(mv[k] - mx);
             l += w * lv[k];
             o += w * ov[k];
         }
-    a.attended[head * 128 + j] = o / l;
+    __shared__ float gm[kMergeGroups], gl[kMergeGroups], go[kMergeGroups][128];
+    if (j == 0) {
+        gm[grp] = mx;
+        gl[grp] = l;
+    }
+    go[grp][j] = o;
+    __syncthreads();
+    if (grp == 0) {
+        float m2 = gm[0];
+#pragma unroll
+        for (int q = 1; q < kMergeGroups; ++q) m2 = fmaxf(m2, gm[q]);
+        float lt = 0.f, ot = 0.f;
+#pragma unroll
+        for (int q = 0; q < kMergeGroups; ++q)
+            if (gm[q] != -INFINITY) {  // a group without splits adds nothing
+                const float w = expf(gm[q] - m2);
+                lt += w * gl[q];
+                ot += w * go[q][j];
+            }
+        a.attended[head * 128 + j] = ot / lt;
+    }
 }
 
-__global__ __launch_bounds__(128) void attn_merge_kernel(const AttnArgs a) { attn_merge_body(a, blockIdx.x); }
+__global__ __launch_bounds__(512) void attn_merge_kernel(const AttnArgs a) { attn_merge_body(a, blockIdx.x); }
 
-__global__ __launch_bounds__(128) void attn_merge_batch_kernel(const AttnBatch b) {
+__global__ __launch_bounds__(512) void attn_merge_batch_kernel(const AttnBatch b) {
     attn_merge_body(b.seq[blockIdx.y], blockIdx.x);
 }
 
@@ -1105,7 +1132,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             int chunk, splits;
             attn_split(pos + 1, chunk, splits);
             attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(at);
-            if (splits > 1) attn_merge_kernel<<<kQHeads, 128, 0, stream>>>(at);
+            if (splits > 1) attn_merge_kernel<<<kQHeads, 512, 0, stream>>>(at);
             break;
         }
         case 2: {
@@ -1196,7 +1223,7 @@ void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int p
             int chunk, splits;
             attn_split(ar.pos + 1, chunk, splits);
             attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(ar);
-            attn_merge_kernel<<<kQHeads, 128, 0, stream>>>(ar);
+            attn_merge_kernel<<<kQHeads, 512, 0, stream>>>(ar);
         }
         GemvArgs o{};
         o.w = L.o_t;
@@ -1268,7 +1295,7 @@ void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm,
         max_splits = std::max(max_splits, splits);
     }
     attn_decode_batch_kernel<<<dim3(max_splits, kKVHeads, count), 512, 0, stream>>>(b);
-    if (max_splits > 1) attn_merge_batch_kernel<<<dim3(kQHeads, count), 128, 0, stream>>>(b);
+    if (max_splits > 1) attn_merge_batch_kernel<<<dim3(kQHeads, count), 512, 0, stream>>>(b);
 }
 
 void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,
