@@ -424,9 +424,13 @@ constexpr int kFbLds = 2 * kFbStageBytes > kFbMergeBytes ? 2 * kFbStageBytes : k
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // K and V tiles in LDS: rows of 128 halves (sixteen 16-byte pieces), piece p
-// of key row r in 16-byte slot 16 r + (p ^ (r & 15)), so the lanes of one
-// LDS access cycle read distinct banks.
-__device__ __forceinline__ int fb_slot(int r, int p) { return 16 * r + (p ^ (r & 15)); }
+// of key row r in 16-byte slot 16 r + (p ^ fb_swz(r)). fb_swz is a bijection
+// of r % 16, so 16 consecutive rows at one piece (the K operand reads) fill
+// 16 distinct slots of a 256-byte bank cycle, and 4 consecutive rows (r % 4
+// in bits 2-3) at 4 aligned pieces (bits 0-1) -- what 32 lanes of the V^T
+// transpose load touch -- also fill 16 distinct slots.
+__device__ __forceinline__ int fb_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int fb_slot(int r, int p) { return 16 * r + (p ^ fb_swz(r)); }
 
 // ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane 4a + b
 // receives element b of the 8-byte chunks addressed by lanes a, a + 4,
@@ -473,7 +477,7 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
     for (int j = 0; j < 8; ++j) {
         const int q = (64 * (2 * j + h) + lane) & 511, r = q >> 4;
         ld_row[j] = r;
-        ld_col[j] = 8 * ((q & 15) ^ (r & 15));
+        ld_col[j] = 8 * ((q & 15) ^ fb_swz(r));
     }
     auto issue = [&](int step) {
         const int kt = 4 * step + sp;
