@@ -540,28 +540,37 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
             st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[s], st, 0, 0, 0);
             st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[s], st, 0, 0, 0);
         }
-        // Online softmax; register r holds key t0 + 8(r/4) + 4hf + r%4.
-        float sv[16];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = t0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-            sv[r] = t <= qpos ? st[r] * scale2 : -INFINITY;
-            tmax = fmaxf(tmax, sv[r]);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mnew = fmaxf(m, tmax);
-        const float factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+        // Online softmax; register r holds key t0 + 8(r/4) + 4hf + r%4. A
+        // tile entirely at or before the block's first query needs no causal
+        // mask (and its maximum is finite), which saves the per-key compares
+        // and selects on all but the diagonal tiles.
+        float sv[16], mnew, factor, psum = 0.f;
         half8 ph[2], pl[2];
-        float psum = 0.f;
+        auto softmax = [&](auto masked) {
+            constexpr bool kMask = decltype(masked)::value;
+            float tmax = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float p = sv[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[r] - mnew);
-            psum += p;
-            const _Float16 hh = static_cast<_Float16>(p);
-            ph[r >> 3][r & 7] = hh;
-            pl[r >> 3][r & 7] = static_cast<_Float16>(p - static_cast<float>(hh));
-        }
+            for (int r = 0; r < 16; ++r) {
+                const int t = t0 + 8 * (r >> 2) + 4 * hf + (r & 3);
+                sv[r] = !kMask || t <= qpos ? st[r] * scale2 : -INFINITY;
+                tmax = fmaxf(tmax, sv[r]);
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            mnew = fmaxf(m, tmax);
+            factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = kMask && sv[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[r] - mnew);
+                psum += p;
+                const _Float16 hh = static_cast<_Float16>(p);
+                ph[r >> 3][r & 7] = hh;
+                pl[r >> 3][r & 7] = static_cast<_Float16>(p - static_cast<float>(hh));
+            }
+        };
+        if (t0 + kFaKeys - 1 <= pos0 + b0)
+            softmax(std::false_type{});
+        else
+            softmax(std::true_type{});
         psum += __shfl_xor(psum, 32);
         l = l * factor + psum;
         // Rescaling by 1 changes nothing; skip it when no lane's maximum moved.
