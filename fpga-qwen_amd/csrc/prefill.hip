@@ -140,7 +140,16 @@ __global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
     constexpr int kSmem = kStages * kStageBytes > kEpiBytes ? kStages * kStageBytes : kEpiBytes;
     __shared__ __align__(16) unsigned char smem[kSmem];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kTileN;
+    // Tile of this workgroup: workgroup w runs on XCD w % 8 (round-robin
+    // dispatch), which takes row tiles xcd, xcd + 8, ... and walks the column
+    // tiles, so each XCD keeps only its eighth of A resident in its L2 while
+    // W streams through. The grid is rounded up to whole XCD rows; the extra
+    // workgroups have no tile.
+    const int mtiles = (M + BM - 1) / BM, per = (mtiles + 7) / 8;
+    const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+    const int mt = xcd + 8 * (slot % per), nt = slot / per;
+    if (mt >= mtiles) return;
+    const int m0 = mt * BM, n0 = nt * kTileN;
     const bool mma = wave < S::kMma;
     const int wm = wave % WR, wn = wave / WR;
     const int ks = K / gridDim.z, kz = blockIdx.z * ks, nk = ks / kTileK;  // this workgroup's K range
@@ -276,7 +285,7 @@ __global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
         // LDS in its stored order (q: FP32 chain-permuted; k: FP16
         // chain-permuted; v: FP16), then written out 16 bytes per lane.
         uint16_t(*ht)[kHeadDim] = reinterpret_cast<uint16_t(*)[kHeadDim]>(smem + BM * kCPitch * 4);
-        const int head = blockIdx.x, j = lane;
+        const int head = nt, j = lane;
         const bool is_q = head < kQHeads, is_v = head >= kQHeads + kKVHeads;
         constexpr int kRows = BM / S::kWaves;
         if (is_v) {
@@ -672,7 +681,8 @@ void gemm(const uint16_t* Ah, const uint16_t* Al, const uint16_t* W, float* C, i
     const int tiles = N / kTileN * splits;
     auto launch = [&](auto bm) {
         constexpr int BM = decltype(bm)::value;
-        gemm_kernel<BM, EPI><<<dim3(N / kTileN, (M + BM - 1) / BM, splits), GemmShape<BM>::kWaves * 64, 0, stream>>>(
+        const int per = ((M + BM - 1) / BM + 7) / 8;  // row tiles per XCD
+        gemm_kernel<BM, EPI><<<dim3(8 * per * (N / kTileN), 1, splits), GemmShape<BM>::kWaves * 64, 0, stream>>>(
             Ah, Al, W, C, M, N, K, ep);
     };
     if ((M + 127) / 128 * tiles >= 256)
