@@ -1,0 +1,141 @@
+// Device arithmetic of the batch-1 decode kernels (decode.hip): the
+// reference dot's chain steps and combine (engine/core.cpp:119-147), RMSNorm
+// (207-215), QK-norm and rotate-half RoPE (216-218, 395-402), and the
+// chain-permuted key reads.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.hpp"
+
+namespace qwen_hip {
+namespace dev {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+// Eight chain steps from one 16-byte block: halves i = 0..7 with activations xa/xb.
+__device__ __forceinline__ float chain8(float acc, u32x4 w, float4 xa, float4 xb) {
+    acc = __builtin_fmaf(xa.x, h2f(w.x & 0xffffu), acc);
+    acc = __builtin_fmaf(xa.y, h2f(w.x >> 16), acc);
+    acc = __builtin_fmaf(xa.z, h2f(w.y & 0xffffu), acc);
+    acc = __builtin_fmaf(xa.w, h2f(w.y >> 16), acc);
+    acc = __builtin_fmaf(xb.x, h2f(w.z & 0xffffu), acc);
+    acc = __builtin_fmaf(xb.y, h2f(w.z >> 16), acc);
+    acc = __builtin_fmaf(xb.z, h2f(w.w & 0xffffu), acc);
+    acc = __builtin_fmaf(xb.w, h2f(w.w >> 16), acc);
+    return acc;
+}
+
+// Lane c of each 8-lane group holds chain c; returns
+// ((c0+c4)+(c1+c5)) + ((c2+c6)+(c3+c7)) in every lane of the group.
+__device__ __forceinline__ float combine_chains(float acc) {
+    const float t1 = acc + __shfl_xor(acc, 4);
+    const float t2 = t1 + __shfl_xor(t1, 1);
+    return t2 + __shfl_xor(t2, 2);
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Position of activation j in the permuted LDS vector: j = 64b + 8i + c is
+// stored at 64b + 8c + i, so chain c reads its 8 values contiguously.
+__device__ __forceinline__ int xperm(int j) { return (j & ~63) | ((j & 7) << 3) | ((j >> 3) & 7); }
+
+// RMSNorm (engine/core.cpp:207-215) of N values held PER = N / THREADS per
+// thread (element j = tid + k THREADS, or j = PER tid + k when CONTIG), with
+// their norm weights, into permuted LDS (and optionally to `copy`).
+template <int N, int THREADS, bool CONTIG = false>
+__device__ __forceinline__ void norm_to_lds(const float (&v)[N / THREADS], const float (&w)[N / THREADS], float* xs,
+                                            double* red, float* copy) {
+    constexpr int PER = N / THREADS;
+    const int tid = threadIdx.x;
+    double part = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const float square = v[k] * v[k];
+        part += static_cast<double>(square);
+    }
+    part = wave_sum(part);
+    if ((tid & 63) == 0) red[tid >> 6] = part;
+    __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int i = 0; i < THREADS / 64; ++i) total += red[i];
+    const float sum = static_cast<float>(total);
+    const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(N) + 1e-6f);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int j = CONTIG ? PER * tid + k : tid + k * THREADS;
+        const float o = (v[k] * inv) * w[k];
+        xs[xperm(j)] = o;
+        if (copy) copy[j] = o;
+    }
+}
+
+// Two 16-byte pieces of a chain-permuted key row as the 8 chain steps each
+// of lane c: pieces c and c + 8 (see kperm).
+__device__ __forceinline__ void key_pieces(const uint16_t* row, int c, u32x4& lo, u32x4& hi) {
+    const u32x4* kp = reinterpret_cast<const u32x4*>(row);
+    lo = kp[c];
+    hi = kp[c + 8];
+}
+
+// The same 16 halves of the current key row, from LDS.
+__device__ __forceinline__ void key_pieces_lds(const uint16_t* kcur, int c, uint32_t (&kw)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int base = (i < 4 ? 8 * c : 64 + 8 * c) + 2 * (i & 3);
+        kw[i] = uint32_t(kcur[base]) | (uint32_t(kcur[base + 1]) << 16);
+    }
+}
+
+// Chain c of q . k for one key: steps s = 0..15 in order; q in kperm order.
+__device__ __forceinline__ float key_chain(const float* qperm, int c, const uint32_t (&kw)[8], float acc) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int base = (i < 4 ? 8 * c : 64 + 8 * c) + 2 * (i & 3);
+        acc = __builtin_fmaf(qperm[base], h2f(kw[i] & 0xffffu), acc);
+        acc = __builtin_fmaf(qperm[base + 1], h2f(kw[i] >> 16), acc);
+    }
+    return acc;
+}
+
+// RMSNorm over 128 values held one per thread by two consecutive waves
+// (engine/core.cpp:397-398), then rotate-half RoPE (216-218). w, cs, sn are
+// this thread's norm weight and the cosine / sine of its rotation pair
+// (index j % 64), loaded by the caller ahead of its other loads.
+__device__ __forceinline__ float head_norm_rope(float raw, float w, float cs, float sn, double* red2, float* buf,
+                                                int j) {
+    const int lane = threadIdx.x & 63;
+    const float square = raw * raw;
+    const double part = wave_sum(static_cast<double>(square));
+    if (lane == 0) red2[(j >> 6)] = part;
+    __syncthreads();
+    const float sum = static_cast<float>(red2[0] + red2[1]);
+    const float inv = 1.0f / __builtin_sqrtf(sum / 128.0f + 1e-6f);
+    const float normed = (raw * inv) * w;
+    buf[j] = normed;
+    __syncthreads();
+    float out;
+    if (j < 64) {
+        const float x0 = buf[j], x1 = buf[j + 64];
+        out = x0 * cs - x1 * sn;
+    } else {
+        const int jj = j - 64;
+        const float x0 = buf[jj], x1 = buf[j];
+        out = x1 * cs + x0 * sn;
+    }
+    return out;
+}
+
+}  // namespace dev
+}  // namespace qwen_hip
