@@ -34,17 +34,21 @@ KERNEL_BYTES = {
 
 
 # Contexts up to this many positions run attention and the O projection as
-# one kernel (the engine's fused path); the O kernel is then not launched.
+# one kernel (the engine's fused path); beyond it split attention and a
+# merge + O kernel. The O projection is never a kernel of its own.
 FUSED_ATTENTION_MAX = 512
 
 
 def attention_bytes(n):
-    """K and V rows of 8 heads x 128 FP16 for n positions, plus q/k/v in and
-    the attention output; on the fused path also the O weights and the
-    8 x 1024 FP32 partial projections written."""
+    """The attention stage (attention + O partials): K and V rows of 8 heads x
+    128 FP16 for n positions, q/k/v in, the O weights and the 16 x 1024 FP32
+    partial projections written; past the fused range also the split
+    partials written and read back by the merge."""
+    base = 8 * n * 128 * 2 * 2 + 4096 * 4 + 1024 * 2048 * 2 + 16 * 1024 * 4
     if n <= FUSED_ATTENTION_MAX:
-        return 8 * n * 128 * 2 * 2 + 4096 * 4 + 1024 * 2048 * 2 + 8 * 1024 * 4
-    return 8 * n * 128 * 2 * 2 + 4096 * 4 + 2048 * 4
+        return base
+    splits = (n + 127) // 128
+    return base + 2 * 8 * splits * 264 * 4
 
 
 def measured_traffic(kernel, position):
@@ -64,8 +68,8 @@ def measured_traffic(kernel, position):
 
 def long_context_decode(model, token, steps=128):
     """128 greedy steps after the 3968-token prompt (positions 3968..4095),
-    then per-kernel times at the full 4096 context: attention and O are
-    separate kernels here (position splits merged in the O prologue)."""
+    then per-stage times at the full 4096 context (attention: split
+    attention + merge/O kernels)."""
     start = time.perf_counter()
     for _ in range(steps):
         model.step(token)
@@ -73,7 +77,7 @@ def long_context_decode(model, token, steps=128):
     elapsed = time.perf_counter() - start
     n = model.position()
     kernel_ms = {}
-    for which in (0, 2, 3, 4, 5, 1):
+    for which in (0, 3, 4, 5, 1):
         kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
     gbs = {k: (attention_bytes(n) if k == 'attention' else KERNEL_BYTES[k]) / (v * 1e-3) / 1e9
            for k, v in kernel_ms.items()}
@@ -312,11 +316,9 @@ def main():
     # the context length reached by the timed region (attention last: timing
     # it resets the model).
     kernel_ms = {}
-    for which in (0, 2, 3, 4, 5, 1):
+    for which in (0, 3, 4, 5, 1):
         kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
-    kernel_ms = {name: kernel_ms[name] for name in KERNELS}
-    if context_end <= FUSED_ATTENTION_MAX:
-        kernel_ms['o'] = None  # inside the attention kernel at this context
+    kernel_ms = {name: kernel_ms.get(name) for name in KERNELS}  # 'o' runs with the attention
     per_token_ms = {k: v * (1 if k == 'lm_head' else 28) for k, v in kernel_ms.items() if v is not None}
     dominant = max(per_token_ms, key=per_token_ms.get)
     nbytes = attention_bytes(context_end) if dominant == 'attention' else KERNEL_BYTES[dominant]

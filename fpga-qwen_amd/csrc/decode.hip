@@ -63,7 +63,7 @@ __device__ __forceinline__ float tile_dot(const u32x4 (&wv)[N / 64], const float
     return combine_chains(acc);
 }
 
-enum GemvMode { kPlain, kQKV, kO, kGateUp, kDown, kLmHead };
+enum GemvMode { kPlain, kQKV, kGateUp, kDown, kLmHead };
 
 // With ROWS input vectors (two-token verification), row q of each per-row
 // buffer starts q strides in: in + q N, x / hidden + q 1024, parts +
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
 #pragma unroll
     for (int q = 0; q < ROWS; ++q) {
         xres[q] = 0.f;
-        if constexpr (MODE == kO || MODE == kDown) xres[q] = a.x[q * kHidden + row];
+        if constexpr (MODE == kDown) xres[q] = a.x[q * kHidden + row];
         if constexpr (PARTS && MODE == kDown) {
 #pragma unroll
             for (int g = 0; g < kOParts; ++g) prow[q][g] = a.parts[(q * kOParts + g) * kHidden + row];
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
         float* out = a.out + size_t(q) * a.out_stride;
         if constexpr (MODE == kPlain || MODE == kQKV) {
             if (c == 0) out[row] = y[q];
-        } else if constexpr (MODE == kO || MODE == kDown) {
+        } else if constexpr (MODE == kDown) {
             if (c == 0) a.x[q * kHidden + row] = xres[q] + y[q];
         } else if constexpr (MODE == kGateUp) {
             // Tile rows 0-3 are gate rows 4T..4T+3, rows 4-7 the matching up rows.
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
 template <int N, int SEG, int MODE, bool PARTS = false>
 __global__ __launch_bounds__(SEG * 32) void gemv_seg_kernel(const GemvArgs a) {
     static_assert(SEG == 2 || SEG == 4, "segments: 2 or 4");
-    static_assert(MODE == kPlain || MODE == kO || MODE == kDown, "long-row modes only");
+    static_assert(MODE == kPlain || MODE == kDown, "long-row modes only");
     constexpr int THREADS = SEG * 32, WAVES = SEG / 2, PER = N / THREADS, NB = N / 64, NBS = NB / SEG;
     static_assert(NB % SEG == 0, "segments must split the blocks evenly");
     __shared__ float4 xs4[N / 4];
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(SEG * 32) void gemv_seg_kernel(const GemvArgs a) {
 #pragma unroll
     for (int k = 0; k < PER; ++k) v[k] = a.in[tid + k * THREADS];
     float xres = 0.f, prow[kOParts];
-    if constexpr (MODE == kO || MODE == kDown) xres = a.x[row];
+    if constexpr (MODE == kDown) xres = a.x[row];
     if constexpr (PARTS) {
 #pragma unroll
         for (int g = 0; g < kOParts; ++g) prow[g] = a.parts[g * kHidden + row];
@@ -590,7 +590,10 @@ __global__ __launch_bounds__(512) void attn_decode_batch_kernel(const AttnBatch 
 // read split 0 and are skipped).
 constexpr int kMergeGroups = 4, kMergePer = kAttnSplits / kMergeGroups;
 static_assert(kAttnSplits % kMergeGroups == 0, "merge groups split the splits evenly");
-__device__ __forceinline__ void attn_merge_body(const AttnArgs& a, int head) {
+// The merged row goes to out[0..127]; after_loads() runs right after the
+// split entries are issued (the fused O kernel issues its weights there).
+template <class AfterLoads>
+__device__ __forceinline__ void attn_merge_body(const AttnArgs& a, int head, float* out, AfterLoads&& after_loads) {
     const int tid = threadIdx.x, j = tid & 127, grp = tid >> 7;
     int chunk, ns;
     attn_split(a.pos + 1, chunk, ns);
@@ -605,6 +608,7 @@ __device__ __forceinline__ void attn_merge_body(const AttnArgs& a, int head) {
         lv[k] = e[129];
         ov[k] = e[j];
     }
+    after_loads();
     float mx = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kMergePer; ++k)
@@ -636,14 +640,44 @@ __device__ __forceinline__ void attn_merge_body(const AttnArgs& a, int head) {
                 lt += w * gl[q];
                 ot += w * go[q][j];
             }
-        a.attended[head * 128 + j] = ot / lt;
+        out[j] = ot / lt;
     }
 }
 
-__global__ __launch_bounds__(512) void attn_merge_kernel(const AttnArgs a) { attn_merge_body(a, blockIdx.x); }
+// Past kFusedMaxPositions: the merge of query head h's position splits fused
+// with that head's share of the O projection, laid out as the tail of
+// attn_o_kernel. Workgroup blockIdx = 8m + g: h = 2g + m % 2, O rows
+// kAttnORows (m / 2) .. + kAttnORows - 1; o_part[h][row] = sum_i
+// O[row][128h + i] att[i], folded into the residual stream by the gate/up
+// prologue and the down epilogue like the fused kernel's partials.
+__global__ __launch_bounds__(512) void attn_merge_o_kernel(const AttnArgs a) {
+    const int g = blockIdx.x % kKVHeads, m = blockIdx.x / kKVHeads;
+    const int h = 2 * g + (m & 1), rb = m >> 1;
+    const int tid = threadIdx.x;
+    constexpr int kThreadsPerRow = 512 / kAttnORows, kLoads = 128 / 8 / kThreadsPerRow;
+    const int orow = rb * kAttnORows + tid / kThreadsPerRow, opart_id = tid % kThreadsPerRow;
+    __shared__ __align__(16) float att[128];
+    u32x4 ow[kLoads];
+    attn_merge_body(a, h, att, [&] {
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4* op = reinterpret_cast<const u32x4*>(a.o_n + size_t(orow) * kQDim + 128 * h) + opart_id;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) ow[i] = __builtin_nontemporal_load(op + kThreadsPerRow * i);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    __syncthreads();
+    float y = 0.f;
+    const float4* at4 = reinterpret_cast<const float4*>(att) + 2 * opart_id;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
+#pragma unroll
+    for (int off = 1; off < kThreadsPerRow; off <<= 1) y += __shfl_xor(y, off);
+    if (opart_id == 0) a.o_part[h * kHidden + orow] = y;
+}
 
 __global__ __launch_bounds__(512) void attn_merge_batch_kernel(const AttnBatch b) {
-    attn_merge_body(b.seq[blockIdx.y], blockIdx.x);
+    const AttnArgs& a = b.seq[blockIdx.y];
+    attn_merge_body(a, blockIdx.x, a.attended + blockIdx.x * 128, [] {});
 }
 
 // Fused attention + O projection for n <= kFusedMaxPositions. Workgroup
@@ -1009,25 +1043,19 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             }
             int chunk, splits;
             attn_split(pos + 1, chunk, splits);
+            require(splits > 1, "split attention: a single split takes the fused kernel");
             attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(at);
-            if (splits > 1) attn_merge_kernel<<<kQHeads, 512, 0, stream>>>(at);
+            attn_merge_o_kernel<<<kAttnOGroups, 512, 0, stream>>>(at);
             break;
         }
-        case 2: {
-            if (attn_fused(pos + 1)) break;  // O is part of the attention kernel
-            GemvArgs o{};
-            o.w = L.o_t;
-            o.in = s.attended;
-            o.x = s.x;
-            launch_gemv<kQDim, kO>(o, kHidden, stream);
+        case 2:  // O runs with the attention (its per-head partials go to o_part)
             break;
-        }
         case 3: {
             GemvArgs gu{};
             gu.w = L.gateup_t;
             gu.in = s.x;
             gu.norm_w = L.post_norm;
-            gu.parts = attn_fused(pos + 1) ? s.o_part : nullptr;
+            gu.parts = s.o_part;
             gu.out = s.act;
             launch_gemv<kHidden, kGateUp>(gu, 2 * kFFN, stream);
             break;
@@ -1036,7 +1064,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             GemvArgs d{};
             d.w = L.down_t;
             d.in = s.act;
-            d.parts = attn_fused(pos + 1) ? s.o_part : nullptr;
+            d.parts = s.o_part;
             d.x = s.x;
             launch_gemv<kFFN, kDown>(d, kHidden, stream);
             break;
@@ -1091,30 +1119,26 @@ void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int p
             default: throw std::runtime_error("fused attention: context beyond 512 positions");
         }
     } else {
-        // Both rows past the fused range: the single-row split kernels, row 0
-        // first (it writes the K/V row that row 1 reads from the cache).
+        // Both rows past the fused range: the single-row split and merge + O
+        // kernels, row 0 first (it writes the K/V row that row 1 reads from
+        // the cache).
         for (int row = 0; row < 2; ++row) {
             AttnArgs ar = at;
             ar.qkv = pr.qkv + row * kQKVRows;
             ar.pos = pos + row;
-            ar.attended = pr.attended + row * kQDim;
+            ar.o_part = pr.o_part + size_t(row) * kOParts * kHidden;
             int chunk, splits;
             attn_split(ar.pos + 1, chunk, splits);
             attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(ar);
-            attn_merge_kernel<<<kQHeads, 512, 0, stream>>>(ar);
+            attn_merge_o_kernel<<<kAttnOGroups, 512, 0, stream>>>(ar);
         }
-        GemvArgs o{};
-        o.w = L.o_t;
-        o.in = pr.attended;
-        o.x = pr.x;
-        launch_gemv_pair<kQDim, kO>(o, kHidden, stream);
     }
 
     GemvArgs gu{};
     gu.w = L.gateup_t;
     gu.in = pr.x;
     gu.norm_w = L.post_norm;
-    gu.parts = fused ? pr.o_part : nullptr;
+    gu.parts = pr.o_part;
     gu.out = pr.act;
     gu.out_stride = kFFN;
     launch_gemv_pair<kHidden, kGateUp>(gu, 2 * kFFN, stream);
@@ -1122,7 +1146,7 @@ void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int p
     GemvArgs d{};
     d.w = L.down_t;
     d.in = pr.act;
-    d.parts = fused ? pr.o_part : nullptr;
+    d.parts = pr.o_part;
     d.x = pr.x;
     launch_gemv_pair<kFFN, kDown>(d, kHidden, stream);
 }

@@ -77,14 +77,11 @@ static std::shared_ptr<Weights> load_weights(const Pack& pack, hipStream_t strea
         upload(down_n, pack.layer(l, "mlp.down_proj.weight"));
         uint16_t* qkv_t = alloc_half(size_t(kQKVRows) * kHidden);
         launch_tile_matrix(qkv_n, nullptr, qkv_t, kQKVRows, kHidden, stream);
-        uint16_t* o_t = alloc_half(size_t(kHidden) * kQDim);
-        launch_tile_matrix(o_n, nullptr, o_t, kHidden, kQDim, stream);
         uint16_t* gu_t = alloc_half(size_t(2 * kFFN) * kHidden);
         launch_tile_matrix(gu_n, gu_n + size_t(kFFN) * kHidden, gu_t, kFFN, kHidden, stream);
         uint16_t* down_t = alloc_half(size_t(kHidden) * kFFN);
         launch_tile_matrix(down_n, nullptr, down_t, kHidden, kFFN, stream);
         L.qkv_t = qkv_t;
-        L.o_t = o_t;
         L.o_n = o_n;
         L.qkv_n = qkv_n;
         L.gateup_n = gu_n;
@@ -195,7 +192,6 @@ void Engine::init_state() {
     base_hidden_ = device_alloc<float>(kHidden);
     pair_.x = device_alloc<float>(2 * kHidden);
     pair_.qkv = device_alloc<float>(2 * kQKVRows);
-    pair_.attended = device_alloc<float>(2 * kQDim);
     pair_.act = device_alloc<float>(2 * kFFN);
     pair_.o_part = device_alloc<float>(size_t(2) * kOParts * kHidden);
     pair_.logits = ver_logits_;
@@ -534,7 +530,7 @@ float Engine::time_kernel(int which, int iterations) {
     require(pos_ > 0 && !pending_, "time_kernel needs a current position");
     HIP_CHECK(hipStreamSynchronize(stream_));
     require(which >= 0 && which <= 5 && iterations > 0, "time_kernel: bad arguments");
-    if (which == 2 && attn_fused(pos_)) return 0.f;  // O runs inside the attention kernel here
+    if (which == 2) return 0.f;  // O runs with the attention (1)
     // Replays kernels of the last processed position; the state is reset
     // afterwards. Layer kernels rotate over all 28 layers so that, as in a
     // real step, their weights (about 880 MB in total) stream from HBM rather

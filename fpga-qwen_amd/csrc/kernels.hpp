@@ -49,9 +49,12 @@ __host__ __device__ inline void attn_split(int n, int& chunk, int& splits) {
 // kernel: one workgroup per (query head, block of kAttnORows O rows) attends
 // over all positions of the head (K/V rows are re-read from L2 by the 32
 // workgroups of a KV head, which share an XCD), then multiplies the head's
-// 128 attention outputs into its rows of O. The kOParts per-head partial
-// sums of O.att land in o_part and are added to the residual stream by the
-// gate/up prologue and the down epilogue, in a fixed order.
+// 128 attention outputs into its rows of O. Longer contexts split the
+// positions (128 per split) and a merge kernel with the same workgroup
+// layout combines the splits of its head and applies the same O rows. Either
+// way the kOParts per-head partial sums of O.att land in o_part and are added
+// to the residual stream by the gate/up prologue and the down epilogue, in a
+// fixed order.
 inline constexpr int kFusedMaxPositions = 512;
 inline constexpr int kAttnORows = 64;
 inline constexpr int kOParts = kQHeads;                                // 16 partial O projections
@@ -70,8 +73,7 @@ static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabu
 
 struct LayerDevice {
     const uint16_t* qkv_t;     // tiled [4096 x 1024]: q rows, k rows, v rows
-    const uint16_t* o_t;       // tiled [1024 x 2048]
-    const uint16_t* o_n;       // natural [1024 x 2048] (fused attention + O, batched decode)
+    const uint16_t* o_n;       // natural [1024 x 2048] (attention + O kernels, batched decode)
     const uint16_t* qkv_n;     // natural [4096 x 1024] (batched decode)
     const uint16_t* gateup_n;  // natural [6144 x 1024]: gate rows then up rows (batched decode)
     const uint16_t* down_n;    // natural [1024 x 3072] (batched decode)
@@ -88,12 +90,12 @@ struct LayerDevice {
 struct DecodeScratch {
     float* x;             // [1024] residual stream
     float* qkv;           // [4096] raw projections
-    float* attended;      // [2048] normalized attention output (single-split steps)
+    float* attended;      // [2048] normalized attention output (batched decode)
     float* act;           // [3072]
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
-    float* o_part;        // [16][1024]: per-query-head partial O projections (fused path)
+    float* o_part;        // [16][1024]: per-query-head partial O projections
     float* lm_value;      // [kBatchLmGroups x kMaxBatch] argmax partials (batch-1 uses kLmGroups)
     int* lm_index;
     int* lm_bad;
@@ -110,10 +112,11 @@ void launch_tile_matrix(const uint16_t* first, const uint16_t* second, uint16_t*
 // {1024, 2048, 3072}, rows a multiple of 8 * waves (waves = 2).
 void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, int cols, hipStream_t stream);
 
-// One decode layer: norm+QKV, attention (+q/k norm, RoPE, KV write), O
-// (+split combine prologue, +residual), norm+gate/up (+SwiGLU), down
-// (+residual). With n = pos + 1 <= kFusedMaxPositions attention and O are one
-// kernel and the O kernel is not launched (four kernels per layer).
+// One decode layer: norm+QKV, attention (+q/k norm, RoPE, KV write) with the
+// per-head O partials, norm+gate/up (+O partials, +SwiGLU), down (+O
+// partials, +residual). With n = pos + 1 <= kFusedMaxPositions attention is
+// one kernel (four kernels per layer), beyond it split attention + merge/O
+// (five).
 // pos is the position being written (n = pos + 1 cached positions after
 // it); when `embed` is non-null (first layer) x is first loaded from
 // embed[token]. Step scalars travel as kernel arguments.
@@ -121,8 +124,9 @@ void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, int po
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
 
-// One kernel of a decode layer: 0 norm+QKV, 1 attention (fused with O when
-// attn_fused(pos + 1)), 2 O (nothing when fused), 3 norm+gate/up, 4 down.
+// One stage of a decode layer: 0 norm+QKV, 1 attention with the O partials
+// (one kernel up to kFusedMaxPositions, split + merge/O beyond), 2 nothing
+// (O runs with the attention), 3 norm+gate/up, 4 down.
 void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          hipStream_t stream);
@@ -131,9 +135,8 @@ void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* em
 struct PairScratch {
     float* x;             // [2][1024] residual streams
     float* qkv;           // [2][4096]
-    float* attended;      // [2][2048] (split attention)
     float* act;           // [2][3072]
-    float* o_part;        // [2][16][1024] (fused attention)
+    float* o_part;        // [2][16][1024]
     float* logits;        // [2][151936]
     float* hidden;        // [2][1024]
     ArgmaxResult* result; // [2] device copies of the selections
