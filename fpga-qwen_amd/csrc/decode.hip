@@ -73,7 +73,7 @@ struct GemvArgs {
     const float* in;          // input vector (plain; O: attention output; down), residual x (norm modes)
     const float* norm_w;      // RMSNorm weights (QKV, gate/up, lm_head)
     const uint16_t* embed;    // natural embedding, first layer only (QKV)
-    const float* parts;       // gate/up, down: pending [16][1024] O partials (fused attention), or null
+    const float* parts;       // gate/up, down: pending [16][1024] per-head O partials, or null
     int token[2];             // first-layer QKV: embedding row of each input row
     int out_stride;           // ROWS > 1: distance between the rows' outputs
     float* out;               // plain/QKV: y; gate/up: activation; lm_head: logits
@@ -386,7 +386,7 @@ struct AttnArgs {
 // probabilities; each wave keeps its own softmax (max, sum, output) over its
 // positions, and the 8 waves are merged in LDS with weights exp(m_w - max).
 // A single split writes the normalized output; several write (output, max,
-// sum) partials that attn_merge_kernel combines. Every load is issued up
+// sum) partials that the merge kernels combine. Every load is issued up
 // front and unconditionally (positions outside the split read row 0 and are
 // masked), in the order the phases need them.
 __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g) {
