@@ -53,17 +53,21 @@ __device__ __forceinline__ double wave_sum(double v) {
 // rows are grouped.
 constexpr int kTileN = 128, kTileK = 64;
 
-template <int BM>
+// BN = 256 (only with BM = 128): twice the columns per workgroup, so every
+// A byte streamed feeds twice the MFMA work; 8 MFMA waves on 64x64 tiles and
+// 2 stages of 64 KiB (the LDS holds no third).
+template <int BM, int BN = kTileN>
 struct GemmShape {
+    static_assert(BN == kTileN || (BN == 2 * kTileN && BM == 128), "256-column tiles with 128 rows only");
     static constexpr int kWaves = BM == 128 ? 16 : 8;            // waves per workgroup (all load)
-    static constexpr int kMma = BM == 64 ? 8 : 4;                // waves running the MFMAs
+    static constexpr int kMma = BM == 64 || BN == 256 ? 8 : 4;   // waves running the MFMAs
     static constexpr int TI = BM == 128 ? 2 : 1;                 // 32-row tiles per MFMA wave
     static constexpr int WR = BM / 32 / TI, WC = kMma / WR;      // MFMA wave grid
-    static constexpr int TJ = kTileN / WC / 32;                  // 32-column tiles per MFMA wave
-    static constexpr int kASlots = BM * 8, kBSlots = kTileN * 8; // 16-byte slots per stage
+    static constexpr int TJ = BN / WC / 32;                      // 32-column tiles per MFMA wave
+    static constexpr int kASlots = BM * 8, kBSlots = BN * 8;     // 16-byte slots per stage
     static constexpr int kStageBytes = (2 * kASlots + kBSlots) * 16;
     static constexpr int kLoads = (2 * kASlots + kBSlots) / (64 * kWaves);  // per thread per stage
-    static constexpr int kStages = BM == 128 ? 3 : 4;
+    static constexpr int kStages = BN == 256 ? 2 : (BM == 128 ? 3 : 4);
     static_assert(kLoads * 64 * kWaves == 2 * kASlots + kBSlots, "stage loads split evenly over the waves");
 };
 
@@ -127,15 +131,16 @@ __device__ __forceinline__ void stage_barrier() {
 // 4 QKV rows (tile t = head t): q heads QK-normed, rotated and stored in the
 // key's chain-permuted order, k heads QK-normed, rotated and written to the
 // cache as FP16, v heads written to the cache.
-template <int BM, int EPI>
-__global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
+template <int BM, int EPI, int BN = kTileN>
+__global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
     const uint16_t* __restrict__ Ah, const uint16_t* __restrict__ Al, const uint16_t* __restrict__ W,
     float* __restrict__ C, int M, int N, int K, GemmEpilogue ep) {
-    using S = GemmShape<BM>;
+    using S = GemmShape<BM, BN>;
+    static_assert(EPI != 4 || BN == kTileN, "the QKV epilogue takes one head per tile");
     constexpr int kStages = S::kStages, kLoads = S::kLoads, kStageBytes = S::kStageBytes;
     constexpr int kASlots = S::kASlots, WR = S::WR, TI = S::TI, TJ = S::TJ;
     constexpr int kThreads = S::kWaves * 64;
-    constexpr int kCPitch = kTileN + 4;  // floats per row of the staged C tile
+    constexpr int kCPitch = BN + 4;  // floats per row of the staged C tile
     constexpr int kEpiBytes = BM * kCPitch * 4 + (EPI == 4 ? BM * kHeadDim * 2 : 0);
     constexpr int kSmem = kStages * kStageBytes > kEpiBytes ? kStages * kStageBytes : kEpiBytes;
     __shared__ __align__(16) unsigned char smem[kSmem];
@@ -149,7 +154,7 @@ __global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
     const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
     const int mt = xcd + 8 * (slot % per), nt = slot / per;
     if (mt >= mtiles) return;
-    const int m0 = mt * BM, n0 = nt * kTileN;
+    const int m0 = mt * BM, n0 = nt * BN;
     const bool mma = wave < S::kMma;
     const int wm = wave % WR, wn = wave / WR;
     const int ks = K / gridDim.z, kz = blockIdx.z * ks, nk = ks / kTileK;  // this workgroup's K range
@@ -166,7 +171,7 @@ __global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
             src[j] = (q < kASlots ? Ah : Al) + size_t(min(m0 + r, M - 1)) * K + kz + 8 * p;
         } else {
             const int qb = q - 2 * kASlots, r = qb >> 3, p = (qb & 7) ^ swz(r);
-            const int wr = EPI == 3 ? (r < 64 ? n0 / 2 + r : N / 2 + n0 / 2 + r - 64) : n0 + r;
+            const int wr = EPI == 3 ? (r < BN / 2 ? n0 / 2 + r : N / 2 + n0 / 2 + r - BN / 2) : n0 + r;
             src[j] = W + size_t(wr) * K + kz + 8 * p;
         }
     }
@@ -212,7 +217,7 @@ __global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
                 }
 #pragma unroll
                 for (int jt = 0; jt < TJ; ++jt) {
-                    const int rb = wn * (kTileN / S::WC) + 32 * jt + fr;
+                    const int rb = wn * (BN / S::WC) + 32 * jt + fr;
                     bb[jt] = *reinterpret_cast<const half8*>(stage + 16 * (2 * kASlots + 8 * rb + (p ^ swz(rb))));
                 }
 #pragma unroll
@@ -238,14 +243,14 @@ __global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     ct[(wm * TI + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)]
-                      [wn * (kTileN / S::WC) + 32 * jt + fr] = acc[i][jt][r];
+                      [wn * (BN / S::WC) + 32 * jt + fr] = acc[i][jt][r];
     }
     __syncthreads();
     if constexpr (EPI <= 2) {
-        // 16-byte pieces: row q / 32, columns 4 (q % 32) .. + 3.
+        // 16-byte pieces: row q / (BN / 4), columns 4 (q % (BN / 4)) .. + 3.
 #pragma unroll
-        for (int q = tid; q < BM * 32; q += kThreads) {
-            const int row = q >> 5, c4 = q & 31, m = m0 + row;
+        for (int q = tid; q < BM * (BN / 4); q += kThreads) {
+            const int row = q / (BN / 4), c4 = q % (BN / 4), m = m0 + row;
             if (m < M) {
                 float4* c = reinterpret_cast<float4*>(C + (size_t(blockIdx.z) * M + m) * N + n0) + c4;
                 const float4 v = *reinterpret_cast<const float4*>(&ct[row][4 * c4]);
@@ -258,16 +263,17 @@ __global__ __launch_bounds__(GemmShape<BM>::kWaves * 64) void gemm_kernel(
             }
         }
     } else if constexpr (EPI == 3) {
-        // SwiGLU (engine/core.cpp:636-639): task q = row q / 8, act columns
-        // n0 / 2 + 8 (q % 8) .. + 7, stored as one 16-byte piece per plane.
+        // SwiGLU (engine/core.cpp:636-639): task q = row q / (BN / 16), act
+        // columns n0 / 2 + 8 (q % (BN / 16)) .. + 7, stored as one 16-byte
+        // piece per plane (gate in tile columns 0 .. BN / 2 - 1, up after).
 #pragma unroll
-        for (int q = tid; q < BM * 8; q += kThreads) {
-            const int row = q >> 3, c8 = 8 * (q & 7), m = m0 + row;
+        for (int q = tid; q < BM * (BN / 16); q += kThreads) {
+            const int row = q / (BN / 16), c8 = 8 * (q % (BN / 16)), m = m0 + row;
             if (m < M) {
                 half8 hi, lo;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float gate = ct[row][c8 + e], up = ct[row][64 + c8 + e];
+                    const float gate = ct[row][c8 + e], up = ct[row][BN / 2 + c8 + e];
                     const float half_gate = gate * 0.5f;
                     const float t = tanhf(half_gate);
                     const float o = gate * (0.5f + 0.5f * t) * up;
@@ -679,18 +685,27 @@ void gemm(const uint16_t* Ah, const uint16_t* Al, const uint16_t* W, float* C, i
     require(N % kTileN == 0 && K % (kTileK * splits) == 0 && M > 0 && (splits == 1 || EPI == 2),
             "gemm: unsupported shape");
     const int tiles = N / kTileN * splits;
-    auto launch = [&](auto bm) {
-        constexpr int BM = decltype(bm)::value;
+    auto launch = [&](auto bm, auto bn) {
+        constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value;
         const int per = ((M + BM - 1) / BM + 7) / 8;  // row tiles per XCD
-        gemm_kernel<BM, EPI><<<dim3(8 * per * (N / kTileN), 1, splits), GemmShape<BM>::kWaves * 64, 0, stream>>>(
+        gemm_kernel<BM, EPI, BN><<<dim3(8 * per * (N / BN), 1, splits), GemmShape<BM, BN>::kWaves * 64, 0, stream>>>(
             Ah, Al, W, C, M, N, K, ep);
     };
+    using I128 = std::integral_constant<int, 128>;
+    // 256-column tiles where they still give every CU a workgroup (O, down
+    // and gate/up of long prompts); the QKV epilogue takes one head per tile.
+    if constexpr (EPI != 4) {
+        if (N % 256 == 0 && (M + 127) / 128 * (tiles / 2) >= 256) {
+            launch(I128{}, std::integral_constant<int, 256>{});
+            return;
+        }
+    }
     if ((M + 127) / 128 * tiles >= 256)
-        launch(std::integral_constant<int, 128>{});
+        launch(I128{}, I128{});
     else if ((M + 63) / 64 * tiles >= 256)
-        launch(std::integral_constant<int, 64>{});
+        launch(std::integral_constant<int, 64>{}, I128{});
     else
-        launch(std::integral_constant<int, 32>{});
+        launch(std::integral_constant<int, 32>{}, I128{});
 }
 
 // FP32 rows -> FP16 hi / lo planes (GEMM operands handed over as FP32).
