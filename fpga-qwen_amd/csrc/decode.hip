@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <climits>
+#include <type_traits>
 
 #include "decode_dev.hpp"
 #include "kernels.hpp"
@@ -228,13 +229,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
                 bad = !__builtin_isfinite(y[q]);
                 if (better(y[q], row, bv, bi)) { bv = y[q]; bi = row; }
             }
-#pragma unroll
-            for (int off = 8; off < 64; off <<= 1) {
-                const float ov = __shfl_xor(bv, off);
-                const int oi = __shfl_xor(bi, off);
-                bad |= __shfl_xor(bad, off);
+            auto step = [&](auto off) {
+                constexpr int kOff = decltype(off)::value;
+                const float ov = xor_lanes<kOff>(bv);
+                const int oi = xor_lanes<kOff>(bi);
+                bad |= xor_lanes<kOff>(bad);
                 if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            }
+            };
+            step(std::integral_constant<int, 8>{});
+            step(std::integral_constant<int, 16>{});
+            step(std::integral_constant<int, 32>{});
             __shared__ float wbest[ROWS][WAVES];
             __shared__ int wi[ROWS][WAVES], wb[ROWS][WAVES];
             if (lane == 0) { wbest[q][wave] = bv; wi[q][wave] = bi; wb[q][wave] = bad; }
@@ -339,13 +343,19 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
         bad |= bad_in[k];
         if (better(value[k], index[k], bv, bi)) { bv = value[k]; bi = index[k]; }
     }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        bad |= __shfl_xor(bad, off);
+    auto step = [&](auto off) {
+        constexpr int kOff = decltype(off)::value;
+        const float ov = xor_lanes<kOff>(bv);
+        const int oi = xor_lanes<kOff>(bi);
+        bad |= xor_lanes<kOff>(bad);
         if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
+    };
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 4>{});
+    step(std::integral_constant<int, 8>{});
+    step(std::integral_constant<int, 16>{});
+    step(std::integral_constant<int, 32>{});
     __shared__ float wv[16];
     __shared__ int wi[16], wb[16];
     if (lane == 0) { wv[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
@@ -472,11 +482,12 @@ __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g)
         m0 = fmaxf(m0, s0[p]);
         m1 = fmaxf(m1, s1[p]);
     }
-#pragma unroll
-    for (int off = 8; off < 64; off <<= 1) {
-        m0 = fmaxf(m0, __shfl_xor(m0, off));
-        m1 = fmaxf(m1, __shfl_xor(m1, off));
-    }
+    m0 = fmaxf(m0, xor_lanes<8>(m0));
+    m1 = fmaxf(m1, xor_lanes<8>(m1));
+    m0 = fmaxf(m0, xor_lanes<16>(m0));
+    m1 = fmaxf(m1, xor_lanes<16>(m1));
+    m0 = fmaxf(m0, xor_lanes<32>(m0));
+    m1 = fmaxf(m1, xor_lanes<32>(m1));
     float l0 = 0.f, l1 = 0.f;
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
@@ -490,11 +501,12 @@ __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g)
             prob[1][p * 64 + grp] = p1;
         }
     }
-#pragma unroll
-    for (int off = 8; off < 64; off <<= 1) {
-        l0 += __shfl_xor(l0, off);
-        l1 += __shfl_xor(l1, off);
-    }
+    l0 += xor_lanes<8>(l0);
+    l1 += xor_lanes<8>(l1);
+    l0 += xor_lanes<16>(l0);
+    l1 += xor_lanes<16>(l1);
+    l0 += xor_lanes<32>(l0);
+    l1 += xor_lanes<32>(l1);
     // prob[][] of this wave's positions is written and read by this wave only.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -670,8 +682,10 @@ __global__ __launch_bounds__(512) void attn_merge_o_kernel(const AttnArgs a) {
     const float4* at4 = reinterpret_cast<const float4*>(att) + 2 * opart_id;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
-#pragma unroll
-    for (int off = 1; off < kThreadsPerRow; off <<= 1) y += __shfl_xor(y, off);
+    static_assert(kThreadsPerRow == 8, "three lane exchanges");
+    y += xor_lanes<1>(y);
+    y += xor_lanes<2>(y);
+    y += xor_lanes<4>(y);
     if (opart_id == 0) a.o_part[h * kHidden + orow] = y;
 }
 
@@ -811,8 +825,9 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
             s0[p] = t < n ? d0 : -INFINITY;
             m0 = fmaxf(m0, s0[p]);
         }
-#pragma unroll
-        for (int off = 8; off < 64; off <<= 1) m0 = fmaxf(m0, __shfl_xor(m0, off));
+        m0 = fmaxf(m0, xor_lanes<8>(m0));
+        m0 = fmaxf(m0, xor_lanes<16>(m0));
+        m0 = fmaxf(m0, xor_lanes<32>(m0));
         // Probabilities relative to the wave maximum (a wave without
         // positions keeps m = -inf and contributes nothing).
         float l0 = 0.f;
@@ -823,8 +838,9 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
             l0 += p0;
             if (c == 0) prob[q][t] = p0;
         }
-#pragma unroll
-        for (int off = 8; off < 64; off <<= 1) l0 += __shfl_xor(l0, off);
+        l0 += xor_lanes<8>(l0);
+        l0 += xor_lanes<16>(l0);
+        l0 += xor_lanes<32>(l0);
         // prob[q][t] of this wave's positions is written and read by this
         // wave only.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -890,8 +906,10 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i)
             y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
-#pragma unroll
-        for (int off = 1; off < kThreadsPerRow; off <<= 1) y += __shfl_xor(y, off);
+        static_assert(kThreadsPerRow == 8, "three lane exchanges");
+        y += xor_lanes<1>(y);
+        y += xor_lanes<2>(y);
+        y += xor_lanes<4>(y);
         if (opart_id == 0) a.o_part[(q * kOParts + h) * kHidden + orow] = y;
     }
 }

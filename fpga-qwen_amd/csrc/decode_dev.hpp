@@ -32,17 +32,53 @@ __device__ __forceinline__ float chain8(float acc, u32x4 w, float4 xa, float4 xb
     return acc;
 }
 
+// The value of lane (this lane ^ OFF). Inside a 16-lane row the exchange
+// uses DPP row moves (quad_perm for 1 and 2; row_shl / row_shr plus a lane
+// select for 4 and 8) at register speed instead of the cross-lane permute
+// through the LDS unit; 16 and 32 use the permute. Every lane receives the
+// same value as from __shfl_xor, so reductions keep their exact order.
+template <int OFF>
+__device__ __forceinline__ int xor_lanes_bits(int v) {
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "power-of-two lane offset");
+    if constexpr (OFF == 1) {
+        return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (OFF == 2) {
+        return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (OFF == 4 || OFF == 8) {
+        const int up = __builtin_amdgcn_update_dpp(v, v, 0x100 + OFF, 0xF, 0xF, false);  // row_shl: lane + OFF
+        const int down = __builtin_amdgcn_update_dpp(v, v, 0x110 + OFF, 0xF, 0xF, false);  // row_shr: lane - OFF
+        return (threadIdx.x & OFF) ? down : up;
+    } else {
+        return __shfl_xor(v, OFF);
+    }
+}
+template <int OFF>
+__device__ __forceinline__ int xor_lanes(int v) { return xor_lanes_bits<OFF>(v); }
+template <int OFF>
+__device__ __forceinline__ float xor_lanes(float v) { return __int_as_float(xor_lanes_bits<OFF>(__float_as_int(v))); }
+template <int OFF>
+__device__ __forceinline__ double xor_lanes(double v) {
+    const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(xor_lanes_bits<OFF>(static_cast<int>(b & 0xffffffffu)));
+    const unsigned hi = static_cast<unsigned>(xor_lanes_bits<OFF>(static_cast<int>(b >> 32)));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
 // Lane c of each 8-lane group holds chain c; returns
 // ((c0+c4)+(c1+c5)) + ((c2+c6)+(c3+c7)) in every lane of the group.
 __device__ __forceinline__ float combine_chains(float acc) {
-    const float t1 = acc + __shfl_xor(acc, 4);
-    const float t2 = t1 + __shfl_xor(t1, 1);
-    return t2 + __shfl_xor(t2, 2);
+    const float t1 = acc + xor_lanes<4>(acc);
+    const float t2 = t1 + xor_lanes<1>(t1);
+    return t2 + xor_lanes<2>(t2);
 }
 
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    v += xor_lanes<32>(v);
+    v += xor_lanes<16>(v);
+    v += xor_lanes<8>(v);
+    v += xor_lanes<4>(v);
+    v += xor_lanes<2>(v);
+    v += xor_lanes<1>(v);
     return v;
 }
 
