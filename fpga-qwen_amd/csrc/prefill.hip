@@ -420,6 +420,10 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
 // exchange with lane ^ 32 per tile. q and the cached keys share the
 // chain-permuted channel order, which leaves q . k unchanged.
 constexpr int kFaRows = 32, kFaKeys = 32, kFaccPitch = 132;
+// A query keeps the reference maximum of its online softmax until a score
+// exceeds it by more than this (log2 units), so probabilities stay <= 2^8 and
+// most tiles need no rescaling of the output accumulators.
+constexpr float kFaLazyMax = 8.f;
 
 // Workgroup = 32 consecutive query rows x one KV head g, 8 waves: wave
 // (h, s) = (wave & 1, wave >> 1) runs query head 2g + h over the key tiles
@@ -509,7 +513,8 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
     issue(0);
 
     // Q^T operand: query b0 + col (rows past the chunk repeat its last row
-    // and are never written), channels 16s + 8hf .. +7.
+    // and are never written), channels 16s + 8hf .. +7, scaled by
+    // scale * log2(e) so that the scores come out in the exp2 domain.
     half8 qh[8], ql[8];
     {
         const float* qrow = QKV + size_t(b0 + min(col, nrows - 1)) * kQKVRows + head * kHeadDim + 8 * hf;
@@ -517,7 +522,8 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
         for (int s = 0; s < 8; ++s) {
             const float4 x0 = reinterpret_cast<const float4*>(qrow + 16 * s)[0];
             const float4 x1 = reinterpret_cast<const float4*>(qrow + 16 * s)[1];
-            const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const float v[8] = {x0.x * scale2, x0.y * scale2, x0.z * scale2, x0.w * scale2,
+                                x1.x * scale2, x1.y * scale2, x1.z * scale2, x1.w * scale2};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const _Float16 hh = static_cast<_Float16>(v[i]);
@@ -560,6 +566,7 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
         // mask (and its maximum is finite), which saves the per-key compares
         // and selects on all but the diagonal tiles.
         float sv[16], mnew, factor, psum = 0.f;
+        bool grow;
         half8 ph[2], pl[2];
         auto softmax = [&](auto masked) {
             constexpr bool kMask = decltype(masked)::value;
@@ -567,12 +574,13 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int t = t0 + 8 * (r >> 2) + 4 * hf + (r & 3);
-                sv[r] = !kMask || t <= qpos ? st[r] * scale2 : -INFINITY;
+                sv[r] = !kMask || t <= qpos ? st[r] : -INFINITY;
                 tmax = fmaxf(tmax, sv[r]);
             }
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            mnew = fmaxf(m, tmax);
-            factor = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+            grow = tmax > m + kFaLazyMax;  // per query (both halves agree)
+            mnew = grow ? tmax : m;
+            factor = !grow ? 1.f : m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float p = kMask && sv[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[r] - mnew);
@@ -588,8 +596,8 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
             softmax(std::true_type{});
         psum += __shfl_xor(psum, 32);
         l = l * factor + psum;
-        // Rescaling by 1 changes nothing; skip it when no lane's maximum moved.
-        if (__builtin_amdgcn_ballot_w64(mnew != m) != 0) {
+        // Rescaling by 1 changes nothing; skip it when no lane's reference moved.
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
