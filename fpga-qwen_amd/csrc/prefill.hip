@@ -53,22 +53,27 @@ __device__ __forceinline__ double wave_sum(double v) {
 // rows are grouped.
 constexpr int kTileN = 128, kTileK = 64;
 
-// BN = 256 (only with BM = 128): twice the columns per workgroup, so every
-// A byte streamed feeds twice the MFMA work; 8 MFMA waves on 64x64 tiles and
-// 2 stages of 64 KiB (the LDS holds no third).
+// BN = 192 or 256 (only with BM = 128): 1.5x or 2x the columns per
+// workgroup, so every A byte streamed feeds more MFMA work; 6 or 8 MFMA waves
+// on 64x64 tiles and 2 stages of 56 or 64 KiB (the LDS holds no third). At
+// BN = 192 a stage is 56 loads of 1 KiB, so half of the 16 waves issue 4 and
+// half 3 (with two stages every wait is for all of a wave's loads).
 template <int BM, int BN = kTileN>
 struct GemmShape {
-    static_assert(BN == kTileN || (BN == 2 * kTileN && BM == 128), "256-column tiles with 128 rows only");
+    static_assert(BN == kTileN || ((BN == 192 || BN == 256) && BM == 128), "wide tiles with 128 rows only");
     static constexpr int kWaves = BM == 128 ? 16 : 8;            // waves per workgroup (all load)
-    static constexpr int kMma = BM == 64 || BN == 256 ? 8 : 4;   // waves running the MFMAs
+    static constexpr int kMma = BN == 192 ? 6 : BM == 64 || BN == 256 ? 8 : 4;  // waves running the MFMAs
     static constexpr int TI = BM == 128 ? 2 : 1;                 // 32-row tiles per MFMA wave
     static constexpr int WR = BM / 32 / TI, WC = kMma / WR;      // MFMA wave grid
     static constexpr int TJ = BN / WC / 32;                      // 32-column tiles per MFMA wave
     static constexpr int kASlots = BM * 8, kBSlots = BN * 8;     // 16-byte slots per stage
     static constexpr int kStageBytes = (2 * kASlots + kBSlots) * 16;
-    static constexpr int kLoads = (2 * kASlots + kBSlots) / (64 * kWaves);  // per thread per stage
-    static constexpr int kStages = BN == 256 ? 2 : (BM == 128 ? 3 : 4);
-    static_assert(kLoads * 64 * kWaves == 2 * kASlots + kBSlots, "stage loads split evenly over the waves");
+    static constexpr int kStageLoads = (2 * kASlots + kBSlots) / 64;         // 1 KiB loads per stage
+    static constexpr int kLoads = (kStageLoads + kWaves - 1) / kWaves;       // per thread per stage (at most)
+    static constexpr int kStages = BN == kTileN ? (BM == 128 ? 3 : 4) : 2;
+    static_assert(kStageLoads * 64 == 2 * kASlots + kBSlots && WR * WC == kMma && TJ * WC * 32 == BN,
+                  "tile shape");
+    static_assert(kLoads * kWaves == kStageLoads || kStages == 2, "uneven loads need whole-stage waits");
 };
 
 // LDS operand tiles hold rows of 64 halves (eight 16-byte pieces): piece p of
@@ -178,7 +183,9 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
     auto issue = [&](int kt) {
         unsigned char* stage = smem + (kt % kStages) * kStageBytes;
 #pragma unroll
-        for (int j = 0; j < kLoads; ++j) load_lds16(src[j] + kt * kTileK, stage + 1024 * (wave + S::kWaves * j));
+        for (int j = 0; j < kLoads; ++j)
+            if (kLoads * S::kWaves == S::kStageLoads || wave + S::kWaves * j < S::kStageLoads)
+                load_lds16(src[j] + kt * kTileK, stage + 1024 * (wave + S::kWaves * j));
     };
 
     floatx16 acc[TI][TJ];
@@ -700,12 +707,27 @@ void gemm(const uint16_t* Ah, const uint16_t* Al, const uint16_t* W, float* C, i
             Ah, Al, W, C, M, N, K, ep);
     };
     using I128 = std::integral_constant<int, 128>;
-    // 256-column tiles where they still give every CU a workgroup (O, down
-    // and gate/up of long prompts); the QKV epilogue takes one head per tile.
+    // 128-row tiles of 128, 192 or 256 columns (the QKV epilogue takes one
+    // head per tile): the fewest rounds of 256 workgroups, each round priced
+    // at the measured time of one workgroup of that width relative to 128.
     if constexpr (EPI != 4) {
-        if (N % 256 == 0 && (M + 127) / 128 * (tiles / 2) >= 256) {
-            launch(I128{}, std::integral_constant<int, 256>{});
-            return;
+        const int mtiles = (M + 127) / 128;
+        auto cost = [&](int bn, double per_round) {
+            const long groups = long(mtiles) * (N / bn) * splits;
+            return (groups + 255) / 256 * per_round;
+        };
+        if (mtiles * tiles >= 256) {
+            const double c128 = cost(128, 1.0);
+            const double c192 = N % 192 == 0 ? cost(192, 1.45) : 1e30;
+            const double c256 = N % 256 == 0 ? cost(256, 1.91) : 1e30;
+            if (c256 <= c192 && c256 <= c128) {
+                launch(I128{}, std::integral_constant<int, 256>{});
+                return;
+            }
+            if (c192 <= c128) {
+                launch(I128{}, std::integral_constant<int, 192>{});
+                return;
+            }
         }
     }
     if ((M + 127) / 128 * tiles >= 256)

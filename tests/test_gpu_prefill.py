@@ -22,7 +22,8 @@ PROMPTS = json.loads((Path(__file__).parent / 'golden' / 'prompts.json').read_te
 
 @pytest.mark.gpu
 @pytest.mark.parametrize('m,n,k', [(1, 1024, 1024), (37, 4096, 1024), (85, 1024, 2048), (512, 6144, 1024),
-                                   (129, 1024, 3072), (1000, 4096, 1024), (1100, 6144, 1024)])
+                                   (129, 1024, 3072), (1000, 4096, 1024), (1100, 6144, 1024),
+                                   (1024, 6144, 1024)])
 def test_gemm_against_fp64(qpkg, m, n, k):
     rng = np.random.default_rng(21)
     a = rng.standard_normal((m, k), dtype=np.float32) * 3
