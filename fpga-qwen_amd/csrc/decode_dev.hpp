@@ -36,7 +36,9 @@ __device__ __forceinline__ float chain8(float acc, u32x4 w, float4 xa, float4 xb
 // uses DPP row moves (quad_perm for 1 and 2; row_shl / row_shr plus a lane
 // select for 4 and 8) at register speed instead of the cross-lane permute
 // through the LDS unit; 16 and 32 use the permute. Every lane receives the
-// same value as from __shfl_xor, so reductions keep their exact order.
+// same value as from __shfl_xor, so reductions keep their exact order. The
+// lane select reads threadIdx.x, so callers run one-dimensional workgroups
+// (threadIdx.x % 64 is the lane), as every decode kernel does.
 template <int OFF>
 __device__ __forceinline__ int xor_lanes_bits(int v) {
     static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "power-of-two lane offset");
