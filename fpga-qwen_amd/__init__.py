@@ -72,6 +72,9 @@ SIGNATURES = {
                                                ctypes.POINTER(ctypes.c_void_p)]),
     'qwen_gpu_copy_prefix': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
     'qwen_gpu_step_batch': (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _c_int_p, ctypes.c_int]),
+    'qwen_gpu_op_attention_prefill': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                                     ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_bgemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemv_time': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
@@ -370,6 +373,24 @@ def bgemv(w, x):
     _check(_LIB.qwen_gpu_op_bgemv(wd.ptr, xd.ptr, yd.ptr, batch, rows, cols, None))
     synchronize()
     return yd.to_array(np.float32, batch * rows).reshape(batch, rows)
+
+
+def attention_prefill(qkv, keys, values, pos0):
+    """Causal GQA attention of a prefill chunk on the matrix cores: qkv FP32
+    [rows, 4096] (queries in columns 0..2047), keys / values FP16 [8, context,
+    128] holding positions 0 .. pos0 + rows - 1. Returns FP32 [rows, 2048]
+    (the kernel's FP16 hi + lo planes summed)."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    keys = np.ascontiguousarray(keys, np.float16)
+    values = np.ascontiguousarray(values, np.float16)
+    rows, context = qkv.shape[0], keys.shape[1]
+    qd, kd, vd = DeviceBuffer.from_array(qkv), DeviceBuffer.from_array(keys), DeviceBuffer.from_array(values)
+    hi, lo = DeviceBuffer(rows * 2048 * 2), DeviceBuffer(rows * 2048 * 2)
+    _check(_LIB.qwen_gpu_op_attention_prefill(qd.ptr, kd.ptr, vd.ptr, hi.ptr, lo.ptr, rows, pos0, context, None))
+    synchronize()
+    h = hi.to_array(np.float16, rows * 2048).astype(np.float32)
+    l = lo.to_array(np.float16, rows * 2048).astype(np.float32)
+    return (h + l).reshape(rows, 2048)
 
 
 def gemm(a, w, c=None):

@@ -287,6 +287,20 @@ int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, 
     });
 }
 
+int qwen_gpu_op_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,
+                                  uint16_t* att_lo, int rows, int pos0, int context, void* stream) {
+    return guarded([&] {
+        need(qkv, "qkv");
+        need(keys, "keys");
+        need(values, "values");
+        need(att_hi, "att_hi");
+        need(att_lo, "att_lo");
+        qwen_hip::launch_attention_prefill(qkv, keys, values, att_hi, att_lo, rows, pos0, context,
+                                           static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
 int qwen_gpu_op_bgemv(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols, void* stream) {
     return guarded([&] {
         need(w, "w");

@@ -767,12 +767,19 @@ void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int 
     check(hipFree(planes), "hipFree");
 }
 
+void launch_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,
+                              uint16_t* att_lo, int rows, int pos0, int context, hipStream_t stream) {
+    require(rows >= 1 && rows <= kPrefillRows && pos0 >= 0 && context > 0 && pos0 + rows <= context,
+            "attention: bad rows / position / context");
+    attn_prefill_mfma_kernel<<<(rows + kFaRows - 1) / kFaRows * kKVHeads, 512, 0, stream>>>(
+        qkv, keys, values, att_hi, att_lo, rows, pos0, context, 1.0f / std::sqrt(128.0f));
+}
+
 void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, const int* ids_dev, int rows, int pos0,
                           const float* cosines, const float* sines, int context, const PrefillScratch& s,
                           hipStream_t stream) {
     require(rows >= 1 && rows <= kPrefillRows, "prefill chunk: bad row count");
     embed_rows_kernel<<<rows, 256, 0, stream>>>(ids_dev, embed, s.x);
-    const float scale = 1.0f / std::sqrt(128.0f);
     // The O and down GEMMs (1024 output columns, K = 2048 / 3072) split K
     // into 4 ranges for parallelism at any row count; the row kernel after
     // each adds the partials to the residual in a fixed order, so a row's
@@ -786,8 +793,7 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
             rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, s.part, rows);
         const GemmEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context, s.act_hi, s.act_lo};
         gemm<4>(s.h_hi, s.h_lo, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream, 1, ep);
-        attn_prefill_mfma_kernel<<<(rows + kFaRows - 1) / kFaRows * kKVHeads, 512, 0, stream>>>(
-            s.qkv, L.keys, L.values, s.att_hi, s.att_lo, rows, pos0, context, scale);
+        launch_attention_prefill(s.qkv, L.keys, L.values, s.att_hi, s.att_lo, rows, pos0, context, stream);
         gemm<2>(s.att_hi, s.att_lo, L.o_n, s.part, rows, kHidden, kQDim, stream, kSplits);
         rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h_hi, s.h_lo, s.part, rows);
         gemm<3>(s.h_hi, s.h_lo, L.gateup_n, nullptr, rows, 2 * kFFN, kHidden, stream, 1, ep);

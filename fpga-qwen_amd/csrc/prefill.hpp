@@ -41,6 +41,14 @@ struct PrefillScratch {
 void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
                  hipStream_t stream);
 
+// Causal GQA attention of a prefill chunk (the layer step between the QKV
+// and O GEMMs): queries from qkv [rows x 4096] (columns 0..2047, 16 heads),
+// keys / values of positions 0 .. pos0 + rows - 1 from the [8][context][128]
+// caches; output [rows x 2048] as FP16 hi + lo planes. rows in 1..4096 and
+// pos0 + rows <= context.
+void launch_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,
+                              uint16_t* att_lo, int rows, int pos0, int context, hipStream_t stream);
+
 // All 28 layers for `rows` prompt ids (device) at positions pos0..pos0+rows-1:
 // K/V land in the cache, the final residual rows in s.x.
 void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, const int* ids_dev, int rows, int pos0,

@@ -152,6 +152,17 @@ int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, 
  * cores), W natural row-major FP16; N and K multiples of 64, M >= 1. */
 int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
                      void* stream);
+/* Causal GQA attention of a prefill chunk (engine/core.cpp:407-605, the
+ * batched rows' attention): rows queries at positions pos0 .. pos0 + rows - 1
+ * from qkv FP32 [rows x 4096] (columns 0..2047: 16 query heads of 128),
+ * against FP16 keys / values [8 KV heads][context][128] holding positions
+ * 0 .. pos0 + rows - 1 (query head h reads KV head h / 2; q and k channels in
+ * one common order), scale 1/sqrt(128). Output [rows x 2048] as FP16 hi and
+ * lo planes (hi + lo is the FP32 result to 2^-22). rows 1..4096, pos0 + rows
+ * <= context. Parity-test entry for the kernel the prefill runs between its
+ * QKV and O GEMMs. */
+int qwen_gpu_op_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,
+                                  uint16_t* att_lo, int rows, int pos0, int context, void* stream);
 /* Batched projection of the multi-sequence decode: y[b] = W x[b] for b <
  * batch (1..8) on the matrix cores; W natural row-major FP16 [rows x cols],
  * x FP32 [batch x cols], y FP32 [batch x rows]; rows a multiple of 16, cols

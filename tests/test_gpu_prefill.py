@@ -38,6 +38,52 @@ def test_gemm_against_fp64(qpkg, m, n, k):
     assert np.array_equal(acc, (base + got).astype(np.float32))
 
 
+def causal_attention_fp64(q, keys, values, pos0):
+    """softmax(q k^T / sqrt(128)) v per query head over positions 0..pos0 + i,
+    query head h reading KV head h // 2 (engine/core.cpp:407-605), in FP64."""
+    rows = q.shape[0]
+    out = np.empty((rows, 16, 128))
+    k64, v64 = keys.astype(np.float64), values.astype(np.float64)
+    for i in range(rows):
+        n = pos0 + i + 1
+        for h in range(16):
+            s = k64[h // 2, :n] @ q[i, h].astype(np.float64) / np.sqrt(128.0)
+            p = np.exp(s - s.max())
+            out[i, h] = (p @ v64[h // 2, :n]) / p.sum()
+    return out.reshape(rows, 2048)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('rows,pos0,boost', [(1, 0, False), (45, 0, True), (130, 200, True), (300, 37, False),
+                                             (300, 37, True)])
+def test_attention_prefill_against_fp64(qpkg, rows, pos0, boost):
+    """The prefill attention kernel against an FP64 causal softmax. With
+    `boost`, keys at positions 40, 97, 170 and 300 align with a direction
+    every query shares, so their scores beat all earlier ones by about 14, 28,
+    42 and 56 (natural log units), far past the kernel's lazy-rescale margin.
+    Keys 170 and 300 lie in the second and third tiles of key split 1 (tiles
+    of 32 keys, split = tile % 4), so the cases past 170 positions rescale a
+    running output and sum mid-sequence: a CPU emulation of the kernel's
+    order without that rescale misses these two cases by 3.6 and 4.5."""
+    rng = np.random.default_rng(rows + pos0)
+    context = pos0 + rows + 7
+    u = rng.standard_normal(128)
+    u *= 4.0 / np.linalg.norm(u)
+    q = (u + 0.5 * rng.standard_normal((rows, 16, 128))).astype(np.float32)
+    keys = (0.3 * rng.standard_normal((8, context, 128))).astype(np.float16)
+    values = rng.standard_normal((8, context, 128)).astype(np.float16)
+    if boost:
+        for t, alpha in ((40, 10.0), (97, 20.0), (170, 30.0), (300, 40.0)):
+            if t < pos0 + rows:
+                keys[:, t] = (alpha * u).astype(np.float16)
+    qkv = np.zeros((rows, 4096), np.float32)
+    qkv[:, :2048] = q.reshape(rows, 2048)
+    got = qpkg.attention_prefill(qkv, keys, values, pos0)
+    ref = causal_attention_fp64(q, keys, values, pos0)
+    err = np.abs(got - ref)
+    assert np.all(err <= 1e-4 + 1e-4 * np.abs(ref)), float(err.max())
+
+
 @pytest.mark.gpu
 def test_gemm_rows_independent_of_chunk(qpkg):
     """Row results do not depend on M, on the row's position in a tile or on
