@@ -75,6 +75,14 @@ SIGNATURES = {
     'qwen_gpu_op_attention_prefill': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                                      ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_op_gemm_swiglu': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_op_norm_qkv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p]),
+    'qwen_gpu_op_norm_gate_up': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    'qwen_gpu_op_down_residual': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_void_p]),
     'qwen_gpu_op_bgemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemv_time': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
@@ -383,7 +391,15 @@ def attention_prefill(qkv, keys, values, pos0):
     qkv = np.ascontiguousarray(qkv, np.float32)
     keys = np.ascontiguousarray(keys, np.float16)
     values = np.ascontiguousarray(values, np.float16)
+    # The kernel reads qkv rows of 4096 and [8][context][128] caches: shapes
+    # are checked here, before any device copy.
+    if qkv.ndim != 2 or qkv.shape[1] != 4096:
+        raise ValueError(f'qkv must be [rows, 4096], got {qkv.shape}')
+    if keys.ndim != 3 or keys.shape[0] != 8 or keys.shape[2] != 128 or values.shape != keys.shape:
+        raise ValueError(f'keys and values must both be [8, context, 128], got {keys.shape} and {values.shape}')
     rows, context = qkv.shape[0], keys.shape[1]
+    if not (rows >= 1 and 0 <= pos0 and pos0 + rows <= context):
+        raise ValueError(f'need 1 <= rows and 0 <= pos0 with pos0 + rows <= context ({rows}, {pos0}, {context})')
     qd, kd, vd = DeviceBuffer.from_array(qkv), DeviceBuffer.from_array(keys), DeviceBuffer.from_array(values)
     hi, lo = DeviceBuffer(rows * 2048 * 2), DeviceBuffer(rows * 2048 * 2)
     _check(_LIB.qwen_gpu_op_attention_prefill(qd.ptr, kd.ptr, vd.ptr, hi.ptr, lo.ptr, rows, pos0, context, None))
@@ -405,3 +421,69 @@ def gemm(a, w, c=None):
     _check(_LIB.qwen_gpu_op_gemm(ad.ptr, wd.ptr, cd.ptr, m, n, k, int(c is not None), None))
     synchronize()
     return cd.to_array(np.float32, m * n).reshape(m, n)
+
+
+def gemm_swiglu(a, w):
+    """Prefill gate/up GEMM with its SwiGLU epilogue: A FP32 [M, K], W FP16
+    [N, K] holding N / 2 gate rows then N / 2 up rows. Returns the FP32
+    activation [M, N / 2] (the kernel's FP16 hi + lo planes summed)."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w, np.float16)
+    m, k = a.shape
+    n = w.shape[0]
+    if w.shape[1] != k or n % 256 or k % 64:
+        raise ValueError(f'need W [N, K] with N % 256 == 0 and K % 64 == 0, got A {a.shape} W {w.shape}')
+    ad, wd = DeviceBuffer.from_array(a), DeviceBuffer.from_array(w)
+    hi, lo = DeviceBuffer(m * n // 2 * 2), DeviceBuffer(m * n // 2 * 2)
+    _check(_LIB.qwen_gpu_op_gemm_swiglu(ad.ptr, wd.ptr, hi.ptr, lo.ptr, m, n, k, None))
+    synchronize()
+    h = hi.to_array(np.float16, m * n // 2).astype(np.float32)
+    l = lo.to_array(np.float16, m * n // 2).astype(np.float32)
+    return (h + l).reshape(m, n // 2)
+
+
+def _vector(values, size, name):
+    values = np.ascontiguousarray(values, np.float32)
+    if values.shape != (size,):
+        raise ValueError(f'{name} must have shape ({size},), got {values.shape}')
+    return DeviceBuffer.from_array(values)
+
+
+def _parts(parts):
+    if parts is None:
+        return None
+    parts = np.ascontiguousarray(parts, np.float32)
+    if parts.shape != (16, HIDDEN):
+        raise ValueError(f'parts must be [16, 1024], got {parts.shape}')
+    return DeviceBuffer.from_array(parts)
+
+
+def norm_qkv(tiled, norm_weight, x):
+    """Decode QKV projection as a step runs it: W_qkv (chain-tiled [4096 x
+    1024] DeviceBuffer) . RMSNorm(x). Returns qkv [4096]."""
+    nd, xd, out = _vector(norm_weight, HIDDEN, 'norm_weight'), _vector(x, HIDDEN, 'x'), DeviceBuffer(4096 * 4)
+    _check(_LIB.qwen_gpu_op_norm_qkv(tiled.ptr, nd.ptr, xd.ptr, out.ptr, None))
+    synchronize()
+    return out.to_array(np.float32, 4096)
+
+
+def norm_gate_up(tiled, norm_weight, x, parts=None):
+    """Decode gate/up projection + SwiGLU as a step runs it (tiled: gate and
+    up interleaved, tile_matrix(gate, up)); parts: pending [16, 1024] O
+    partials folded into x first, or None. Returns (act [3072], gate [3072],
+    up [3072]), the last two being the kernel's dot products."""
+    nd, xd = _vector(norm_weight, HIDDEN, 'norm_weight'), _vector(x, HIDDEN, 'x')
+    pd, out, raw = _parts(parts), DeviceBuffer(3072 * 4), DeviceBuffer(6144 * 4)
+    _check(_LIB.qwen_gpu_op_norm_gate_up(tiled.ptr, nd.ptr, xd.ptr, pd.ptr if pd else None, out.ptr, raw.ptr, None))
+    synchronize()
+    rows = raw.to_array(np.float32, 6144).reshape(768, 2, 4)  # tile, (gate, up), row in tile
+    return out.to_array(np.float32, 3072), rows[:, 0, :].reshape(3072), rows[:, 1, :].reshape(3072)
+
+
+def down_residual(tiled, act, x, parts=None):
+    """Decode down projection + residual as a step runs it: returns
+    (x + folded parts) + W_down . act, W_down chain-tiled [1024 x 3072]."""
+    ad, xd, pd = _vector(act, 3072, 'act'), _vector(x, HIDDEN, 'x'), _parts(parts)
+    _check(_LIB.qwen_gpu_op_down_residual(tiled.ptr, ad.ptr, pd.ptr if pd else None, xd.ptr, None))
+    synchronize()
+    return xd.to_array(np.float32, HIDDEN)

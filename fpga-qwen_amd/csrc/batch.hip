@@ -23,6 +23,7 @@
 #include <cmath>
 
 #include "batch.hpp"
+#include "half_split.hpp"
 
 namespace qwen_hip {
 namespace {
@@ -186,8 +187,10 @@ __global__ __launch_bounds__(256) void bgemv_kernel(const BatchGemvArgs a) {
             half4 hi, lo;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                hi[k] = static_cast<_Float16>(e[k]);
-                lo[k] = static_cast<_Float16>(e[k] - static_cast<float>(hi[k]));
+                _Float16 h, l;
+                split_half(e[k], h, l);
+                hi[k] = h;
+                lo[k] = l;
             }
             const int j = 4 * (tid + 256 * i);
             *reinterpret_cast<half4*>(&xh[b][j]) = hi;

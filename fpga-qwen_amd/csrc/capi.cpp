@@ -287,6 +287,51 @@ int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, 
     });
 }
 
+int qwen_gpu_op_gemm_swiglu(const float* a, const uint16_t* w, uint16_t* act_hi, uint16_t* act_lo, int m, int n,
+                            int k, void* stream) {
+    return guarded([&] {
+        need(a, "a");
+        need(w, "w");
+        need(act_hi, "act_hi");
+        need(act_lo, "act_lo");
+        qwen_hip::launch_gemm_swiglu(a, w, act_hi, act_lo, m, n, k, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
+int qwen_gpu_op_norm_qkv(const uint16_t* tiled, const float* norm_weight, const float* x, float* qkv, void* stream) {
+    return guarded([&] {
+        need(tiled, "tiled");
+        need(norm_weight, "norm_weight");
+        need(x, "x");
+        need(qkv, "qkv");
+        qwen_hip::launch_norm_qkv(tiled, norm_weight, x, qkv, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
+int qwen_gpu_op_norm_gate_up(const uint16_t* tiled, const float* norm_weight, const float* x, const float* parts,
+                             float* act, float* raw, void* stream) {
+    return guarded([&] {
+        need(tiled, "tiled");
+        need(norm_weight, "norm_weight");
+        need(x, "x");
+        need(act, "act");
+        qwen_hip::launch_norm_gate_up(tiled, norm_weight, x, parts, act, raw, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
+int qwen_gpu_op_down_residual(const uint16_t* tiled, const float* act, const float* parts, float* x, void* stream) {
+    return guarded([&] {
+        need(tiled, "tiled");
+        need(act, "act");
+        need(x, "x");
+        qwen_hip::launch_down_residual(tiled, act, parts, x, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
 int qwen_gpu_op_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,
                                   uint16_t* att_lo, int rows, int pos0, int context, void* stream) {
     return guarded([&] {

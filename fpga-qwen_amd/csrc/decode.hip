@@ -83,6 +83,7 @@ struct GemvArgs {
     float* lm_value;
     int* lm_index;
     int* lm_bad;
+    float* raw;               // gate/up, optional: the dot products in tile row order (parity tests)
 };
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
@@ -213,6 +214,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
             if (c == 0) a.x[q * kHidden + row] = xres[q] + y[q];
         } else if constexpr (MODE == kGateUp) {
             // Tile rows 0-3 are gate rows 4T..4T+3, rows 4-7 the matching up rows.
+            if (a.raw && c == 0) a.raw[size_t(q) * a.out_stride * 2 + row] = y[q];
             const float up = __shfl(y[q], (lane + 32) & 63);
             if (lane < 32 && c == 0) {
                 const float gate = y[q];
@@ -1237,6 +1239,37 @@ void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeS
     a.lm_bad = s.lm_bad;
     gemv_kernel<kHidden, kLmWaves, kLmHead><<<kLmGroups, 64 * kLmWaves, 0, stream>>>(a);
     argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, host_out);
+}
+
+void launch_norm_qkv(const uint16_t* qkv_t, const float* norm_w, const float* x, float* qkv, hipStream_t stream) {
+    GemvArgs q{};
+    q.w = qkv_t;
+    q.in = x;
+    q.norm_w = norm_w;
+    q.out = qkv;
+    launch_gemv<kHidden, kQKV>(q, kQKVRows, stream);
+}
+
+void launch_norm_gate_up(const uint16_t* gateup_t, const float* norm_w, const float* x, const float* parts,
+                         float* act, float* raw, hipStream_t stream) {
+    GemvArgs gu{};
+    gu.raw = raw;
+    gu.w = gateup_t;
+    gu.in = x;
+    gu.norm_w = norm_w;
+    gu.parts = parts;
+    gu.out = act;
+    launch_gemv<kHidden, kGateUp>(gu, 2 * kFFN, stream);
+}
+
+void launch_down_residual(const uint16_t* down_t, const float* act, const float* parts, float* x,
+                          hipStream_t stream) {
+    GemvArgs d{};
+    d.w = down_t;
+    d.in = act;
+    d.parts = parts;
+    d.x = x;
+    launch_gemv<kFFN, kDown>(d, kHidden, stream);
 }
 
 }  // namespace qwen_hip

@@ -7,6 +7,7 @@
 
 #include <cstdint>
 
+#include "half_split.hpp"
 #include "kernels.hpp"
 
 namespace qwen_hip {
@@ -17,7 +18,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float h2f(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return to_half_bits(f); }
 
 // Eight chain steps from one 16-byte block: halves i = 0..7 with activations xa/xb.
 __device__ __forceinline__ float chain8(float acc, u32x4 w, float4 xa, float4 xb) {

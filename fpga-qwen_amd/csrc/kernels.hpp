@@ -178,6 +178,20 @@ struct AttnSeq {
 void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
                             const float* cosines, const float* sines, hipStream_t stream);
 
+// The batch-1 decode projections of one layer as the step runs them, on
+// caller buffers (parity-test entries):
+// qkv[4096] = W_qkv . RMSNorm(x) (norm prologue, one chain-ordered dot per row);
+void launch_norm_qkv(const uint16_t* qkv_t, const float* norm_w, const float* x, float* qkv, hipStream_t stream);
+// act[3072] = SwiGLU(W_gate . h, W_up . h) with h = RMSNorm(x + the 16 pending
+// O partials folded in their fixed tree order; none when parts is null),
+// W chain-tiled with gate / up rows interleaved 4 by 4; raw (optional,
+// [6144]) receives the dot products in that interleaved row order;
+void launch_norm_gate_up(const uint16_t* gateup_t, const float* norm_w, const float* x, const float* parts,
+                         float* act, float* raw, hipStream_t stream);
+// x[r] = (x[r] + folded O partials of row r) + W_down[r] . act (two-segment chains).
+void launch_down_residual(const uint16_t* down_t, const float* act, const float* parts, float* x,
+                          hipStream_t stream);
+
 // Plain device copy (bytes a multiple of 16), for counter calibration.
 void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);
 

@@ -17,6 +17,7 @@
 #include <cfloat>
 #include <type_traits>
 
+#include "half_split.hpp"
 #include "kernels.hpp"
 #include "prefill.hpp"
 
@@ -29,7 +30,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return to_half_bits(f); }
 
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
@@ -99,9 +100,10 @@ struct GemmEpilogue {
 
 // FP32 value -> the FP16 hi / lo pair the GEMMs read (hi = fp16(v), lo = fp16(v - hi)).
 __device__ __forceinline__ void split_store(float v, uint16_t* hi, uint16_t* lo, size_t i) {
-    const _Float16 h = static_cast<_Float16>(v);
+    _Float16 h, l;
+    split_half(v, h, l);
     hi[i] = __builtin_bit_cast(uint16_t, h);
-    lo[i] = f2h(v - static_cast<float>(h));
+    lo[i] = __builtin_bit_cast(uint16_t, l);
 }
 
 // 16 bytes per lane from global memory straight into LDS at
@@ -284,8 +286,10 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
                     const float half_gate = gate * 0.5f;
                     const float t = tanhf(half_gate);
                     const float o = gate * (0.5f + 0.5f * t) * up;
-                    hi[e] = static_cast<_Float16>(o);
-                    lo[e] = static_cast<_Float16>(o - static_cast<float>(hi[e]));
+                    _Float16 h, l;
+                    split_half(o, h, l);
+                    hi[e] = h;
+                    lo[e] = l;
                 }
                 const size_t at = size_t(m) * (N / 2) + n0 / 2 + c8;
                 *reinterpret_cast<half8*>(ep.act_hi + at) = hi;
@@ -533,9 +537,10 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
                                 x1.x * scale2, x1.y * scale2, x1.z * scale2, x1.w * scale2};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const _Float16 hh = static_cast<_Float16>(v[i]);
+                _Float16 hh, ll;
+                split_half(v[i], hh, ll);
                 qh[s][i] = hh;
-                ql[s][i] = static_cast<_Float16>(v[i] - static_cast<float>(hh));
+                ql[s][i] = ll;
             }
         }
     }
@@ -592,9 +597,10 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
             for (int r = 0; r < 16; ++r) {
                 const float p = kMask && sv[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[r] - mnew);
                 psum += p;
-                const _Float16 hh = static_cast<_Float16>(p);
+                _Float16 hh, ll;
+                split_half(p, hh, ll);
                 ph[r >> 3][r & 7] = hh;
-                pl[r >> 3][r & 7] = static_cast<_Float16>(p - static_cast<float>(hh));
+                pl[r >> 3][r & 7] = ll;
             }
         };
         if (t0 + kFaKeys - 1 <= pos0 + b0)
@@ -672,9 +678,10 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
 #pragma unroll
             for (int e4 = 0; e4 < 4; ++e4) {  // the O GEMM's A operand as FP16 hi / lo
                 const float v = o[e4] / lsum;
-                const _Float16 hh = static_cast<_Float16>(v);
+                _Float16 hh, ll;
+                split_half(v, hh, ll);
                 hi[k4 >> 1][4 * (k4 & 1) + e4] = hh;
-                lo[k4 >> 1][4 * (k4 & 1) + e4] = static_cast<_Float16>(v - static_cast<float>(hh));
+                lo[k4 >> 1][4 * (k4 & 1) + e4] = ll;
             }
         }
         *reinterpret_cast<half8*>(att_hi + out) = hi[0];
@@ -747,11 +754,12 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
 
 }  // namespace
 
-void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
-                 hipStream_t stream) {
+// Runs fn(hi, lo) on FP16 hi / lo planes of the FP32 rows A[M x K], held in
+// device memory allocated for this call (an operator entry point for tests
+// and benchmarks, not on the inference path), then waits for the stream.
+template <class F>
+static void with_planes(const float* A, int M, int K, hipStream_t stream, F&& fn) {
     require(M > 0 && K > 0, "gemm: unsupported shape");
-    // Operand planes for this call (an operator entry point for tests and
-    // benchmarks, not on the inference path).
     const size_t n = size_t(M) * K;
     auto check = [](hipError_t e, const char* what) {
         require(e == hipSuccess, std::string("HIP error: ") + hipGetErrorString(e) + " (" + what + ")");
@@ -759,12 +767,33 @@ void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int 
     uint16_t* planes = nullptr;
     check(hipMalloc(&planes, 2 * n * sizeof(uint16_t)), "hipMalloc");
     split_rows_kernel<<<unsigned(std::min<size_t>((n + 255) / 256, 4096)), 256, 0, stream>>>(A, planes, planes + n, n);
-    if (accumulate)
-        gemm<1>(planes, planes + n, W, C, M, N, K, stream);
-    else
-        gemm<0>(planes, planes + n, W, C, M, N, K, stream);
-    check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    fn(planes, planes + n);
+    const hipError_t launched = hipGetLastError();
+    const hipError_t done = hipStreamSynchronize(stream);
     check(hipFree(planes), "hipFree");
+    check(launched, "gemm launch");
+    check(done, "hipStreamSynchronize");
+}
+
+void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
+                 hipStream_t stream) {
+    with_planes(A, M, K, stream, [&](const uint16_t* hi, const uint16_t* lo) {
+        if (accumulate)
+            gemm<1>(hi, lo, W, C, M, N, K, stream);
+        else
+            gemm<0>(hi, lo, W, C, M, N, K, stream);
+    });
+}
+
+void launch_gemm_swiglu(const float* A, const uint16_t* W, uint16_t* act_hi, uint16_t* act_lo, int M, int N, int K,
+                        hipStream_t stream) {
+    require(N % 256 == 0, "gemm swiglu: N must be a multiple of 256");
+    GemmEpilogue ep{};
+    ep.act_hi = act_hi;
+    ep.act_lo = act_lo;
+    with_planes(A, M, K, stream, [&](const uint16_t* hi, const uint16_t* lo) {
+        gemm<3>(hi, lo, W, nullptr, M, N, K, stream, 1, ep);
+    });
 }
 
 void launch_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,

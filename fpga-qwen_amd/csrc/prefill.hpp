@@ -41,6 +41,13 @@ struct PrefillScratch {
 void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
                  hipStream_t stream);
 
+// Gate/up projection with the SwiGLU epilogue of the prefill path: W holds
+// N / 2 gate rows then N / 2 up rows (natural [N x K]); act[m][i] =
+// SwiGLU(gate_i, up_i) of row m, written as FP16 hi / lo planes [M x N / 2].
+// N a multiple of 256, K of 64.
+void launch_gemm_swiglu(const float* A, const uint16_t* W, uint16_t* act_hi, uint16_t* act_lo, int M, int N, int K,
+                        hipStream_t stream);
+
 // Causal GQA attention of a prefill chunk (the layer step between the QKV
 // and O GEMMs): queries from qkv [rows x 4096] (columns 0..2047, 16 heads),
 // keys / values of positions 0 .. pos0 + rows - 1 from the [8][context][128]

@@ -152,6 +152,35 @@ int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, 
  * cores), W natural row-major FP16; N and K multiples of 64, M >= 1. */
 int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
                      void* stream);
+/* Gate/up projection of the prefill path with its SwiGLU epilogue
+ * (engine/core.cpp:630-639 with batch > 1: the gate and up projections, then
+ * gate * (0.5 + 0.5 tanh(gate / 2)) * up): w natural FP16 [n x k] holding
+ * n / 2 gate rows then n / 2 up rows, a FP32 [m x k]; act[m][i] is written
+ * as FP16 hi and lo planes [m x n / 2] (hi + lo is the FP32 result to
+ * 2^-22). n a multiple of 256, k of 64. Parity-test entry for the kernel the
+ * prefill runs between the post-attention norm and the down GEMM. */
+int qwen_gpu_op_gemm_swiglu(const float* a, const uint16_t* w, uint16_t* act_hi, uint16_t* act_lo, int m, int n,
+                            int k, void* stream);
+/* The batch-1 decode projections as a step runs them (parity-test entries;
+ * all weights in the chain-tiled layout of qwen_gpu_op_tile_matrix):
+ * qkv[4096] = W_qkv . RMSNorm(x, norm_weight) with W_qkv = q, k, v rows
+ * stacked [4096 x 1024] (engine/core.cpp:384-386: norm, then project_group<3>
+ * over q/k/v). */
+int qwen_gpu_op_norm_qkv(const uint16_t* tiled, const float* norm_weight, const float* x, float* qkv, void* stream);
+/* act[3072] = SwiGLU(W_gate . h, W_up . h), h = RMSNorm(x + the 16 pending
+ * per-query-head O partials parts[16][1024], added in the engine's fixed
+ * tree order; parts NULL means none), the tiled matrix interleaving gate and
+ * up rows 4 by 4 (qwen_gpu_op_tile_matrix with second = up)
+ * (engine/core.cpp:625-639: residual, norm, project_group<2>, SwiGLU).
+ * raw (NULL to skip, else [6144]) receives the gate and up dot products in
+ * that interleaved row order: 8t + i is gate row 4t + i, 8t + 4 + i up row
+ * 4t + i (i < 4). */
+int qwen_gpu_op_norm_gate_up(const uint16_t* tiled, const float* norm_weight, const float* x, const float* parts,
+                             float* act, float* raw, void* stream);
+/* x[r] = (x[r] + the pending O partials of row r, NULL for none) +
+ * W_down[r] . act, W_down [1024 x 3072] (engine/core.cpp:640-641: project,
+ * then the residual add). */
+int qwen_gpu_op_down_residual(const uint16_t* tiled, const float* act, const float* parts, float* x, void* stream);
 /* Causal GQA attention of a prefill chunk (engine/core.cpp:407-605, the
  * batched rows' attention): rows queries at positions pos0 .. pos0 + rows - 1
  * from qkv FP32 [rows x 4096] (columns 0..2047: 16 query heads of 128),

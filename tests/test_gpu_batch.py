@@ -149,3 +149,61 @@ def test_step_batch_validates_before_running(qpkg, pack0):
             assert (a.position(), b.position()) == before[:2]
         finally:
             b.close()
+
+
+@pytest.mark.gpu
+def test_prefix_reuse_workload_matches_oracle(qpkg, pack0, oracle_lib):
+    """The 8-sequence prefix-reuse workload at its real size
+    (engine/INTERFACE.md:94-103, tools/native_cpu_chat.py:198-216): the
+    canonical 512-token prefix is prefilled once; 8 sequences take a device
+    copy of its K/V (the 512-token rewind), prefill their own 1536-token
+    suffix (positions 512..2047) and decode 8 greedy steps together through
+    step_batch (contexts 2049..2056: 17 position splits per KV head, a grid
+    of 8 sequences). Teacher-forced against the oracle (rewind to 512, prefill
+    the suffix, step the same tokens), every sequence's logits after its
+    prefill and after each batched step pass the reference gate; then each
+    sequence re-steps the same tokens alone from position 2048 (batch-1
+    path), and those rows too pass the gate against its batched rows."""
+    prefix, suffixes = PROMPTS['prefix_512'], PROMPTS['suffix_1536']
+    assert len(prefix) == 512 and len(suffixes) == 8 and all(len(s) == 1536 for s in suffixes)
+    steps = 8
+    base = qpkg.Model(pack0, context=4096)
+    seqs = [base.share(context=2304) for _ in suffixes]
+    try:
+        base.prefill(prefix)
+        for m, suffix in zip(seqs, suffixes):
+            m.copy_prefix(base, len(prefix))
+            m.prefill(suffix)
+        rows = [[(m.logits(), m.greedy())] for m in seqs]
+        for _ in range(steps):
+            qpkg.step_batch(seqs, [r[-1][1] for r in rows])
+            for r, m in zip(rows, seqs):
+                r.append((m.logits(), m.greedy()))
+        assert all(m.position() == 2048 + steps for m in seqs)
+        worst_alone = 0.0
+        for r, m in zip(rows, seqs):
+            m.truncate(2048)
+            for k in range(1, steps + 1):
+                m.step(r[k - 1][1])
+                result = compare_logits(m.logits(), r[k][0])
+                assert result['passed'], ('alone vs batched', k, result)
+                worst_alone = max(worst_alone, result['max_abs'])
+    finally:
+        for m in seqs + [base]:
+            m.close()
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    worst = 0.0
+    try:
+        oracle.prefill(prefix)
+        for i, suffix in enumerate(suffixes):
+            oracle.truncate(len(prefix))
+            oracle.prefill(suffix)
+            for k, (logits, _) in enumerate(rows[i]):
+                if k:
+                    oracle.step(rows[i][k - 1][1])
+                result = compare_logits(logits, oracle.logits())
+                assert result['passed'], ('sequence', i, 'row', k, result)
+                worst = max(worst, result['max_abs'])
+    finally:
+        oracle.close()
+    print('max_abs vs oracle', worst, 'alone vs batched', worst_alone)

@@ -66,19 +66,53 @@ def test_context_1100_matches_oracle(qpkg, pack0, oracle_lib):
 
 
 @pytest.mark.gpu
-def test_context_3968_matches_oracle(qpkg, pack0, oracle_lib):
+def test_context_3968_decode_to_capacity_matches_oracle(qpkg, pack0, oracle_lib):
+    """The long-context workload end to end: the 3968-token prompt, then 128
+    greedy steps over positions 3968..4095 (up to 32 position splits per KV
+    head), every one of the 129 logit rows gated against the oracle
+    teacher-forced (tools/check_native_logits.py samples such rows; here all
+    are taken). The cache is then full: a further step is rejected."""
     gpu = qpkg.Model(pack0, context=4096)
     oracle = oracle_lib.model(pack0, 16, 16, 4096)
     try:
-        results = check_trajectory(gpu, oracle, PROMPTS['long_3968'], 6)
+        results = check_trajectory(gpu, oracle, PROMPTS['long_3968'], 129)
+        assert gpu.position() == 4096
         print('max_abs', max(r['max_abs'] for r in results), 'rms', max(r['rms'] for r in results))
-        # Fill the cache to its last slot: capacity then rejects a further step.
-        gpu.reset()
-        gpu.prefill(PROMPTS['long_3968'])
-        gpu.prefill(list(range(128)))
-        assert gpu.position() == 4096 and np.isfinite(gpu.logits()).all()
         with pytest.raises(RuntimeError, match='Context capacity exceeded'):
             gpu.step(0)
+        assert gpu.position() == 4096 and np.isfinite(gpu.logits()).all()
+    finally:
+        gpu.close()
+        oracle.close()
+
+
+@pytest.mark.gpu
+def test_chunk_boundary_prompts_match_oracle(qpkg, pack0, oracle_lib):
+    """Prompts of 511, 512 and 513 tokens (one batched pass short of, at, and
+    one row past the 512-token chunk, the last row then taking the batch-1
+    path as engine/core.cpp:712 splits it) and of 1024 / 1025 tokens, each
+    prefilled in one call and gated against the oracle at the same position,
+    then 2 greedy steps after the 513- and 1025-token prompts."""
+    prompt = PROMPTS['prefill_1024'] + PROMPTS['long_3968'][:1]
+    gpu = qpkg.Model(pack0, context=4096)
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    try:
+        for start, lengths in ((510, (511, 512, 513)), (1023, (1024, 1025))):
+            oracle.reset()
+            oracle.prefill(prompt[:start])
+            for n in lengths:
+                oracle.step(prompt[n - 1])
+                gpu.reset()
+                gpu.prefill(prompt[:n])
+                assert gpu.position() == n
+                result = compare_logits(gpu.logits(), oracle.logits())
+                assert result['passed'], (n, result)
+            for _ in range(2):
+                token = gpu.greedy()
+                gpu.step(token)
+                oracle.step(token)
+                result = compare_logits(gpu.logits(), oracle.logits())
+                assert result['passed'], (gpu.position(), result)
     finally:
         gpu.close()
         oracle.close()

@@ -90,6 +90,35 @@ def test_prefill_equals_steps_and_truncate(gpu_model):
     assert np.array_equal(gpu_model.logits().view(np.uint32), full.view(np.uint32))
 
 
+VERIFY_IDS = [32 + (i * 37) % 1000 for i in range(700)]
+
+
+class OraclePrefix:
+    """One oracle model walked to prefixes of VERIFY_IDS: rows below the
+    reached prefix always hold those ids, so a test may step past it and a
+    later test truncate back or extend forward."""
+
+    def __init__(self, oracle):
+        self.oracle, self.valid = oracle, 0
+        oracle.reset()
+
+    def at(self, n):
+        if n > self.valid:
+            self.oracle.truncate(self.valid)
+            self.oracle.prefill(VERIFY_IDS[self.valid:n])
+        else:
+            self.oracle.truncate(n)
+        self.valid = n  # the caller's steps overwrite rows from n on
+        return self.oracle
+
+
+@pytest.fixture(scope='module')
+def oracle_prefix(oracle_lib, pack0):
+    model = oracle_lib.model(pack0, 16, 16, 4096)
+    yield OraclePrefix(model)
+    model.close()
+
+
 @pytest.mark.gpu
 # Prefixes cover the one-pass pair kernels (fused attention: 0, 1, 62, 63
 # where row 1 needs one more 64-position pass than row 0, 510 at the fused
@@ -97,10 +126,12 @@ def test_prefill_equals_steps_and_truncate(gpu_model):
 # fused, row 1 split).
 @pytest.mark.parametrize('prefix,commit', [(0, 1), (0, 2), (1, 1), (1, 2), (62, 2), (63, 1), (510, 2), (511, 2),
                                            (513, 2), (700, 1)])
-def test_verify_two_equals_two_steps(qpkg, pack0, gpu_model, prefix, commit):
+def test_verify_two_equals_two_steps(qpkg, pack0, gpu_model, oracle_prefix, prefix, commit):
     """tools/native_verify_check.cpp normal_case, against a second model:
-    every row bit-identical to single steps."""
-    ids = [32 + (i * 37) % 1000 for i in range(prefix)]
+    every row bit-identical to single steps; and both rows (logits and
+    hidden) against the oracle's two steps (engine/core.cpp:729-752) under
+    the reference gate."""
+    ids = VERIFY_IDS[:prefix]
     ref = qpkg.Model(pack0, context=4096)
     try:
         for m in (gpu_model, ref):
@@ -124,6 +155,13 @@ def test_verify_two_equals_two_steps(qpkg, pack0, gpu_model, prefix, commit):
         for row, (l, h) in enumerate((first, second)):
             assert np.array_equal(rows.logits[row].view(np.uint32), l.view(np.uint32))
             assert np.array_equal(rows.hidden[row].view(np.uint32), h.view(np.uint32))
+        oracle = oracle_prefix.at(prefix)
+        for row, token in enumerate((9707, 11)):
+            oracle.step(token)
+            result = compare_logits(rows.logits[row], oracle.logits())
+            assert result['passed'], (prefix, row, result)
+            hidden_err = float(np.abs(rows.hidden[row] - oracle.hidden()).max())
+            assert hidden_err <= 1e-2, (prefix, row, hidden_err)
         assert gpu_model.verify_greedy() == (int(np.argmax(first[0])), int(np.argmax(second[0])))
         for blocked in (lambda: gpu_model.step(12), lambda: gpu_model.prefill([12])):
             with pytest.raises(RuntimeError, match='Commit or discard pending verification'):

@@ -38,6 +38,51 @@ def test_gemm_against_fp64(qpkg, m, n, k):
     assert np.array_equal(acc, (base + got).astype(np.float32))
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize('m', [1024, 100, 3968])
+def test_gemm_swiglu_against_fp64(qpkg, m):
+    """The gate/up GEMM with its SwiGLU epilogue (engine/core.cpp:630-639 at
+    batch > 1). 1024 rows take 128 x 192 tiles (256 workgroups in one round),
+    100 rows narrower 32- or 64-row tiles and 3968 rows 128 x 256 tiles, so
+    each epilogue's gate/up column mapping is exercised. Against FP64:
+    g sigmoid(g) u with g, u the exact products, the GEMM error bound
+    propagated through the activation's partial derivatives, plus the FP16
+    hi + lo rounding of the stored result."""
+    rng = np.random.default_rng(23 + m)
+    a = rng.standard_normal((m, 1024), dtype=np.float32)
+    w = (rng.standard_normal((6144, 1024), dtype=np.float32) * 0.02).astype(np.float16)
+    # Every column, every third row plus the last (the FP64 products of all
+    # 3968 rows would dominate the test's time).
+    rows = np.r_[0:m:3, m - 1]
+    got = qpkg.gemm_swiglu(a, w).astype(np.float64)[rows]
+    a64, w64 = a[rows].astype(np.float64), w.astype(np.float64)
+    g, u = a64 @ w64[:3072].T, a64 @ w64[3072:].T
+    sig = 1.0 / (1.0 + np.exp(-g))
+    ref = g * sig * u
+    bg = 4e-6 * (np.abs(a64) @ np.abs(w64[:3072]).T) + 1e-7
+    bu = 4e-6 * (np.abs(a64) @ np.abs(w64[3072:]).T) + 1e-7
+    bound = (np.abs(sig * (1.0 + g * (1.0 - sig)) * u) * bg + np.abs(g * sig) * bu
+             + 1e-6 * np.abs(ref) + 1e-8)
+    # The epilogue itself: the plain GEMM accumulates every element in the
+    # same K order, so its g and u are the ones the SwiGLU epilogue saw. The
+    # activation must be the reference formula evaluated in FP32 on them, up
+    # to the spread of two tanhf implementations and what FP16 hi + lo holds
+    # (2^-22 relative, half of FP16's subnormal spacing absolute). A hi / lo
+    # pair rounded from two different values misses this by an FP16 ulp.
+    plain = qpkg.gemm(a, w)[rows]
+    g32, u32 = plain[:, :3072], plain[:, 3072:]
+    t32 = np.tanh(np.float32(0.5) * g32).astype(np.float32)
+    emu = (g32 * (np.float32(0.5) + np.float32(0.5) * t32) * u32).astype(np.float64)
+    tol = (np.abs(g32.astype(np.float64) * u32) * 2.0 ** -23 + 4 * np.spacing(np.abs(emu).astype(np.float32))
+           + 2.0 ** -21 * np.abs(emu) + 2.0 ** -24)
+    assert np.all(np.abs(got - emu) <= tol), float((np.abs(got - emu) / tol).max())
+    err = np.abs(got - ref)
+    worst = np.unravel_index(np.argmax(err / bound), err.shape)
+    assert np.all(err <= bound), dict(ratio=float((err / bound).max()), row=int(rows[worst[0]]), col=int(worst[1]),
+                                      g=float(g[worst]), u=float(u[worst]), got=float(got[worst]),
+                                      ref=float(ref[worst]), bound=float(bound[worst]))
+
+
 def causal_attention_fp64(q, keys, values, pos0):
     """softmax(q k^T / sqrt(128)) v per query head over positions 0..pos0 + i,
     query head h reading KV head h // 2 (engine/core.cpp:407-605), in FP64."""
