@@ -75,6 +75,8 @@ SIGNATURES = {
     'qwen_gpu_op_attention_prefill': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                                      ctypes.c_int, ctypes.c_void_p]),
+    'qwen_gpu_op_gemm_static': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                               ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemm_swiglu': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_norm_qkv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -487,3 +489,17 @@ def down_residual(tiled, act, x, parts=None):
     _check(_LIB.qwen_gpu_op_down_residual(tiled.ptr, ad.ptr, pd.ptr if pd else None, xd.ptr, None))
     synchronize()
     return xd.to_array(np.float32, HIDDEN)
+
+
+def gemm_static(a, w, c=None):
+    """gemm() through the entry point that allocates nothing (operand planes
+    in the library's static device array; M x K at most 1048576)."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w, np.float16)
+    m, k = a.shape
+    n = w.shape[0]
+    ad, wd = DeviceBuffer.from_array(a), DeviceBuffer.from_array(w)
+    cd = DeviceBuffer.from_array(np.ascontiguousarray(c, np.float32)) if c is not None else DeviceBuffer(m * n * 4)
+    _check(_LIB.qwen_gpu_op_gemm_static(ad.ptr, wd.ptr, cd.ptr, m, n, k, int(c is not None), None))
+    synchronize()
+    return cd.to_array(np.float32, m * n).reshape(m, n)

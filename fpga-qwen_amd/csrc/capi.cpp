@@ -287,6 +287,17 @@ int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, 
     });
 }
 
+int qwen_gpu_op_gemm_static(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
+                            void* stream) {
+    return guarded([&] {
+        need(a, "a");
+        need(w, "w");
+        need(c, "c");
+        qwen_hip::launch_gemm_static(a, w, c, m, n, k, accumulate != 0, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
 int qwen_gpu_op_gemm_swiglu(const float* a, const uint16_t* w, uint16_t* act_hi, uint16_t* act_lo, int m, int n,
                             int k, void* stream) {
     return guarded([&] {

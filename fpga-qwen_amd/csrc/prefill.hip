@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <mutex>
 #include <type_traits>
 
 #include "half_split.hpp"
@@ -794,6 +795,46 @@ void launch_gemm_swiglu(const float* A, const uint16_t* W, uint16_t* act_hi, uin
     with_planes(A, M, K, stream, [&](const uint16_t* hi, const uint16_t* lo) {
         gemm<3>(hi, lo, W, nullptr, M, N, K, stream, 1, ep);
     });
+}
+
+// Operand planes of launch_gemm_static: a file-scope device array, so the
+// call allocates nothing. Each device holds its own copy at its own address
+// (from hipGetSymbolAddress, taken once per device); host code uses only that
+// address, never the array's name.
+static __device__ __align__(256) uint16_t scratch[2 * kStaticGemmElements];
+
+static uint16_t* static_planes() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex lock;
+    static uint16_t* by_device[kMaxDevices] = {};
+    int device = -1;
+    hipError_t e = hipGetDevice(&device);
+    require(e == hipSuccess && device >= 0 && device < kMaxDevices,
+            std::string("gemm static: no usable current device (") + hipGetErrorString(e) + ")");
+    std::lock_guard<std::mutex> guard(lock);
+    if (!by_device[device]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        require(e == hipSuccess && ptr != nullptr,
+                std::string("gemm static: hipGetSymbolAddress failed (") + hipGetErrorString(e) + ")");
+        by_device[device] = static_cast<uint16_t*>(ptr);
+    }
+    return by_device[device];
+}
+
+void launch_gemm_static(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
+                        hipStream_t stream) {
+    require(M > 0 && K > 0 && N > 0 && N % kTileN == 0 && K % kTileK == 0, "gemm: unsupported shape");
+    require(size_t(M) * size_t(K) <= kStaticGemmElements,
+            "gemm static: M x K exceeds the 1048576 operand elements of the static planes");
+    uint16_t* hi = static_planes();
+    uint16_t* lo = hi + kStaticGemmElements;
+    const size_t n = size_t(M) * K;
+    split_rows_kernel<<<unsigned(std::min<size_t>((n + 255) / 256, 4096)), 256, 0, stream>>>(A, hi, lo, n);
+    if (accumulate)
+        gemm<1>(hi, lo, W, C, M, N, K, stream);
+    else
+        gemm<0>(hi, lo, W, C, M, N, K, stream);
 }
 
 void launch_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,

@@ -41,6 +41,14 @@ struct PrefillScratch {
 void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
                  hipStream_t stream);
 
+// launch_gemm without allocating: the FP16 operand planes live in a static
+// device array of 2 x kStaticGemmElements halves (4 MiB per device, held until
+// the process ends) shared by every call on a device, so calls that overlap
+// on one device race. Enqueues on `stream` and returns (no synchronization).
+inline constexpr size_t kStaticGemmElements = size_t(1) << 20;  // M x K limit
+void launch_gemm_static(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
+                        hipStream_t stream);
+
 // Gate/up projection with the SwiGLU epilogue of the prefill path: W holds
 // N / 2 gate rows then N / 2 up rows (natural [N x K]); act[m][i] =
 // SwiGLU(gate_i, up_i) of row m, written as FP16 hi / lo planes [M x N / 2].

@@ -152,6 +152,18 @@ int qwen_gpu_op_gemv(const uint16_t* tiled, const float* x, float* y, int rows, 
  * cores), W natural row-major FP16; N and K multiples of 64, M >= 1. */
 int qwen_gpu_op_gemm(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
                      void* stream);
+/* qwen_gpu_op_gemm without any device allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. The FP16 operand
+ * planes live in a static device array of the library (4 MiB per device,
+ * held until the process ends), so m * k may be at most 1048576; larger
+ * inputs fail with an error and launch nothing. The call only enqueues work
+ * on `stream` (NULL: the default stream) and returns; the caller synchronizes
+ * before reading c. Every call on one device shares that array: calls that
+ * may overlap on a device (other streams, other threads) race and must be
+ * serialized by the caller. Results are bit-identical to qwen_gpu_op_gemm. */
+int qwen_gpu_op_gemm_static(const float* a, const uint16_t* w, float* c, int m, int n, int k, int accumulate,
+                            void* stream);
 /* Gate/up projection of the prefill path with its SwiGLU epilogue
  * (engine/core.cpp:630-639 with batch > 1: the gate and up projections, then
  * gate * (0.5 + 0.5 tanh(gate / 2)) * up): w natural FP16 [n x k] holding
