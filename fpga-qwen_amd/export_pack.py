@@ -1,241 +1,333 @@
 #!/usr/bin/env python3
-"""Real-checkpoint pack writer: a Qwen3-0.6B BF16 ``model.safetensors`` ->
-the QWCPU01 pack the engine loads (``weights.bin``, ``.index``,
-``.manifest.json``), in the format of engine/INTERFACE.md:6-21 and with the
-checks of the reference's exporter (tools/export_native_cpu_weights.py:49-163):
+"""Writes the engine's weight pack from a Qwen3-0.6B BF16 checkpoint.
 
-* the safetensors header is read once (8-byte little-endian length, JSON
-  without duplicate keys) and must list exactly the 311 expected tensors
-  (310 pack tensors plus ``lm_head.weight``), every one BF16 with its exact
-  shape and length, the regions tiling the data area with no gaps, overlaps
-  or trailing bytes;
-* ``lm_head.weight`` must equal the embedding byte for byte and is then
-  omitted (the engine ties the output head to the embedding);
-* values are widened BF16 -> FP32; 2-D matrices are rounded to FP16
-  (round-to-nearest-even), 1-D norms stay FP32; nonfinite inputs and FP16
-  overflow are rejected;
-* tensors go out in the engine's fixed order at 64-byte aligned offsets
-  after a 64-byte ``QWCPU01`` header; the outputs are immutable: existing
-  files are never replaced, and the three files appear only once complete
-  (hard links from a staging directory, manifest last).
+Input: ``model.safetensors`` (or the directory holding it). Output: the
+QWCPU01 pack of engine/INTERFACE.md:6-21, three files ``weights.bin``,
+``weights.bin.index`` and ``weights.bin.manifest.json``; the binary is the
+same bytes the reference's exporter writes for the same checkpoint.
 
-Streams the checkpoint in 1 MiB blocks; needs no GPU and no Torch.
+How it works:
+
+1. The checkpoint is memory-mapped. Its JSON header (keys must be unique) is
+   checked against the tensor table below: exactly those 310 tensors plus
+   ``lm_head.weight``, all BF16 with the expected shapes, byte ranges that
+   lie inside the file and together cover its data area exactly once.
+2. ``lm_head.weight`` must equal the embedding byte for byte; the engine ties
+   its output head to the embedding, so the pack stores the embedding once.
+3. The pack layout is computed up front: a 64-byte ``QWCPU01`` header, then
+   the tensors in table order at 64-byte aligned offsets. The binary is
+   allocated at its final size and filled through a memory map, one block of
+   rows at a time: BF16 widened exactly to FP32, 2-D matrices rounded to FP16
+   (round to nearest even), 1-D norms kept FP32. A non-finite input value or
+   a matrix value beyond FP16's range stops the export.
+4. Packs are immutable. Each file is written under a temporary name in the
+   output directory, synced, made read-only and then hard-linked to its final
+   name, which fails rather than replace an existing file; the manifest goes
+   last and marks the pack complete. On any failure the files already linked
+   are removed again.
+
+Needs NumPy only (no GPU, no Torch).
 
 Usage: python export_pack.py --checkpoint DIR_OR_FILE --output weights.bin
 """
 import argparse
 import hashlib
 import json
+import mmap
 import os
 import struct
 import tempfile
+from dataclasses import dataclass
 from pathlib import Path
 
 import numpy as np
 
-MAGIC = b'QWCPU01'
+FORMAT = 'QWCPU01'
+HEADER_BYTES = 64
 ALIGN = 64
-BLOCK = 1 << 20
-ROUNDING = ('BF16 widened to FP32; matrices rounded to FP16 round-to-nearest-even; '
-            '1D norms preserved FP32; little endian')
+ROWS_PER_BLOCK = 2048
+ROUNDING = ('BF16 widened exactly to FP32; 2-D matrices rounded to FP16 (round to nearest even); '
+            '1-D norm weights kept FP32; little endian')
 
 
-def pack_shapes():
-    """Pack tensors in the engine's order (name -> shape); matches
-    fpga-qwen_amd/csrc/pack.cpp pack_layout()."""
-    shapes = {'model.embed_tokens.weight': (151936, 1024), 'model.norm.weight': (1024,)}
-    per_layer = [('input_layernorm', (1024,)), ('post_attention_layernorm', (1024,)),
-                 ('self_attn.q_norm', (128,)), ('self_attn.k_norm', (128,)),
-                 ('self_attn.q_proj', (2048, 1024)), ('self_attn.k_proj', (1024, 1024)),
-                 ('self_attn.v_proj', (1024, 1024)), ('self_attn.o_proj', (1024, 2048)),
-                 ('mlp.gate_proj', (3072, 1024)), ('mlp.up_proj', (3072, 1024)),
-                 ('mlp.down_proj', (1024, 3072))]
-    for layer in range(28):
-        for name, shape in per_layer:
-            shapes[f'model.layers.{layer}.{name}.weight'] = shape
-    return shapes
+class PackError(ValueError):
+    """The checkpoint cannot become a pack (the message says why)."""
 
 
-def _sha256(path):
+def qwen3_tensor_table():
+    """The pack's tensors in file order, name -> shape (fpga-qwen_amd/csrc/pack.cpp
+    validates the same table; engine/core.cpp:235-276)."""
+    table = {'model.embed_tokens.weight': (151936, 1024), 'model.norm.weight': (1024,)}
+    layer = (('input_layernorm', (1024,)), ('post_attention_layernorm', (1024,)),
+             ('self_attn.q_norm', (128,)), ('self_attn.k_norm', (128,)),
+             ('self_attn.q_proj', (2048, 1024)), ('self_attn.k_proj', (1024, 1024)),
+             ('self_attn.v_proj', (1024, 1024)), ('self_attn.o_proj', (1024, 2048)),
+             ('mlp.gate_proj', (3072, 1024)), ('mlp.up_proj', (3072, 1024)), ('mlp.down_proj', (1024, 3072)))
+    for index in range(28):
+        table.update((f'model.layers.{index}.{part}.weight', shape) for part, shape in layer)
+    return table
+
+
+@dataclass(frozen=True)
+class Slot:
+    """Where one tensor goes in the pack."""
+    name: str
+    shape: tuple
+    offset: int
+
+    @property
+    def matrix(self):
+        return len(self.shape) == 2
+
+    @property
+    def rows(self):
+        return self.shape[0]
+
+    @property
+    def columns(self):
+        return self.shape[1] if self.matrix else 1
+
+    @property
+    def dtype(self):
+        return 'F16' if self.matrix else 'F32'
+
+    @property
+    def length(self):
+        return self.rows * self.columns * (2 if self.matrix else 4)
+
+
+def plan(table):
+    """Pack slots in table order and the binary's total size."""
+    slots, cursor = [], HEADER_BYTES
+    for name, shape in table.items():
+        cursor = -(-cursor // ALIGN) * ALIGN
+        slots.append(Slot(name, tuple(shape), cursor))
+        cursor += slots[-1].length
+    return slots, cursor
+
+
+def _unique_keys(pairs):
+    seen = {}
+    for key, value in pairs:
+        if key in seen:
+            raise PackError(f'safetensors header repeats the key {key!r}')
+        seen[key] = value
+    return seen
+
+
+class Checkpoint:
+    """A memory-mapped safetensors file and its parsed header."""
+
+    def __init__(self, path):
+        self.path = Path(path)
+        self._file = self.path.open('rb')
+        self.size = os.fstat(self._file.fileno()).st_size
+        if self.size < 8:
+            raise PackError('safetensors file is shorter than its 8-byte header length')
+        self.map = mmap.mmap(self._file.fileno(), 0, access=mmap.ACCESS_READ)
+        (header_bytes,) = struct.unpack_from('<Q', self.map, 0)
+        if not 2 <= header_bytes <= min(self.size - 8, 64 << 20):
+            raise PackError(f'safetensors header length {header_bytes} does not fit the file')
+        try:
+            header = json.loads(self.map[8:8 + header_bytes], object_pairs_hook=_unique_keys)
+        except PackError:
+            raise
+        except ValueError as error:
+            raise PackError(f'safetensors header is not JSON: {error}') from None
+        if not isinstance(header, dict):
+            raise PackError('safetensors header is not a JSON object')
+        header.pop('__metadata__', None)
+        self.header, self.data = header, 8 + header_bytes
+
+    def bf16(self, name):
+        """The tensor's BF16 bit patterns as a read-only uint16 array view."""
+        begin, end = self.header[name]['data_offsets']
+        shape = self.header[name]['shape']
+        return np.frombuffer(self.map, dtype='<u2', count=(end - begin) // 2, offset=self.data + begin).reshape(shape)
+
+    def sha256(self):
+        digest = hashlib.sha256()
+        view = memoryview(self.map)
+        for start in range(0, self.size, 64 << 20):
+            digest.update(view[start:start + (64 << 20)])
+        view.release()
+        return digest.hexdigest()
+
+    def close(self):
+        try:
+            self.map.close()
+        except BufferError:  # an array view is still alive; the map closes when it goes
+            pass
+        self._file.close()
+
+
+def audit(checkpoint, table):
+    """Checks the checkpoint against the table (step 1 and 2 of the module
+    docstring); raises PackError with the first problem found."""
+    expected = dict(table, **{'lm_head.weight': table['model.embed_tokens.weight']})
+    missing = sorted(set(expected) - set(checkpoint.header))
+    unexpected = sorted(set(checkpoint.header) - set(expected))
+    if missing or unexpected:
+        raise PackError(f'checkpoint tensors are not the {len(expected)} of Qwen3-0.6B: '
+                        f'missing {missing[:4]}, unexpected {unexpected[:4]}')
+    spans = []
+    for name, shape in expected.items():
+        entry = checkpoint.header[name]
+        found = (entry.get('dtype'), entry.get('shape')) if isinstance(entry, dict) else (None, None)
+        if found != ('BF16', list(shape)):
+            raise PackError(f'{name}: expected BF16 {list(shape)}, found {found[0]} {found[1]}')
+        offsets = entry.get('data_offsets')
+        if not (isinstance(offsets, list) and len(offsets) == 2 and all(type(v) is int for v in offsets)):
+            raise PackError(f'{name}: data_offsets must be two integers')
+        begin, end = offsets
+        if not (0 <= begin and end - begin == 2 * int(np.prod(shape)) and checkpoint.data + end <= checkpoint.size):
+            raise PackError(f'{name}: byte range [{begin}, {end}) does not hold its {int(np.prod(shape))} '
+                            'BF16 values inside the file')
+        spans.append((begin, end))
+    spans.sort()
+    covered = 0
+    for begin, end in spans:
+        if begin != covered:
+            raise PackError('the tensors do not cover the data area exactly once (a gap or an overlap)')
+        covered = end
+    if checkpoint.data + covered != checkpoint.size:
+        raise PackError('the tensors do not cover the data area exactly once (trailing bytes)')
+    head, embedding = checkpoint.bf16('lm_head.weight'), checkpoint.bf16('model.embed_tokens.weight')
+    for start in range(0, head.shape[0], 8 * ROWS_PER_BLOCK):
+        if not np.array_equal(head[start:start + 8 * ROWS_PER_BLOCK], embedding[start:start + 8 * ROWS_PER_BLOCK]):
+            raise PackError('lm_head.weight differs from model.embed_tokens.weight; the engine needs a tied head')
+
+
+def convert(block, matrix, name):
+    """BF16 bits -> FP16 values (matrix) or FP32 values (norm), checked."""
+    wide = (block.astype(np.uint32) << 16).view(np.float32)
+    if not np.isfinite(wide).all():
+        raise PackError(f'{name}: the checkpoint holds a non-finite value')
+    if not matrix:
+        return wide
+    with np.errstate(over='ignore'):
+        narrow = wide.astype(np.float16)
+    if not np.isfinite(narrow).all():
+        raise PackError(f'{name}: a value lies beyond the FP16 range')
+    return narrow
+
+
+def _file_sha256(path):
     digest = hashlib.sha256()
     with open(path, 'rb') as f:
-        while True:
-            block = f.read(BLOCK)
-            if not block:
-                return digest.hexdigest()
+        for block in iter(lambda: f.read(16 << 20), b''):
             digest.update(block)
+    return digest.hexdigest()
 
 
-def _no_duplicates(pairs):
-    out = {}
-    for key, value in pairs:
-        if key in out:
-            raise ValueError(f'Duplicate JSON key: {key}')
-        out[key] = value
-    return out
-
-
-def read_header(source):
-    """(header dict, data start, file size) of a safetensors file."""
-    size = source.stat().st_size
-    with source.open('rb') as f:
-        raw = f.read(8)
-        if len(raw) != 8:
-            raise ValueError('Truncated safetensors header')
-        length = struct.unpack('<Q', raw)[0]
-        if length < 2 or length > min(64 << 20, size - 8):
-            raise ValueError('Invalid safetensors header length')
-        header = json.loads(f.read(length), object_pairs_hook=_no_duplicates)
-    if not isinstance(header, dict):
-        raise ValueError('Invalid safetensors header')
-    return header, 8 + length, size
-
-
-def check_layout(header, data_start, size, shapes):
-    """Validates names, dtypes, shapes and the tiling of the data area;
-    returns {name: (begin, end)} relative to the data start."""
-    expected = dict(shapes)
-    expected['lm_head.weight'] = shapes['model.embed_tokens.weight']
-    tensors = {k: v for k, v in header.items() if k != '__metadata__'}
-    if set(tensors) != set(expected):
-        raise ValueError(f'Checkpoint must contain exactly the expected {len(expected)} tensors')
-    regions = {}
-    for name, shape in expected.items():
-        spec = tensors[name]
-        if not isinstance(spec, dict) or spec.get('dtype') != 'BF16' or spec.get('shape') != list(shape):
-            raise ValueError(f'Unexpected tensor dtype/shape: {name}')
-        offsets = spec.get('data_offsets')
-        if not isinstance(offsets, list) or len(offsets) != 2 or any(type(v) is not int for v in offsets):
-            raise ValueError(f'Invalid offsets: {name}')
-        begin, end = offsets
-        if begin < 0 or end - begin != 2 * int(np.prod(shape)) or data_start + end > size:
-            raise ValueError(f'Tensor bounds/length mismatch: {name}')
-        regions[name] = (begin, end)
-    spans = sorted(regions.values())
-    if spans[0][0] != 0 or data_start + spans[-1][1] != size or any(
-            a[1] != b[0] for a, b in zip(spans, spans[1:])):
-        raise ValueError('Checkpoint tensor regions overlap, contain holes, or leave trailing bytes')
-    return regions
-
-
-def _same_bytes(path, a, b, length):
-    with open(path, 'rb') as fa, open(path, 'rb') as fb:
-        fa.seek(a)
-        fb.seek(b)
-        while length:
-            n = min(length, BLOCK)
-            if fa.read(n) != fb.read(n):
-                return False
-            length -= n
-    return True
-
-
-def convert_block(raw, matrix, name):
-    """BF16 bytes -> FP16 (matrix) or FP32 (norm) bytes, rejecting nonfinite
-    inputs and FP16 overflow."""
-    if len(raw) % 2:
-        raise ValueError('Truncated tensor during export')
-    wide = (np.frombuffer(raw, dtype='<u2').astype(np.uint32) << 16).view('<f4')
-    if not np.isfinite(wide).all():
-        raise ValueError(f'Nonfinite checkpoint tensor: {name}')
-    if not matrix:
-        return wide.tobytes()
-    with np.errstate(over='ignore'):
-        narrow = wide.astype('<f2')
-    if not np.isfinite(narrow).all():
-        raise ValueError(f'FP16 overflow in tensor: {name}')
-    return narrow.tobytes()
-
-
-def export(checkpoint, output, shapes=None):
-    """Writes OUTPUT, OUTPUT.index and OUTPUT.manifest.json; returns the
-    manifest path. `shapes` replaces the Qwen3-0.6B table (tests only)."""
-    shapes = pack_shapes() if shapes is None else shapes
-    checkpoint, output = Path(checkpoint), Path(output)
-    source = checkpoint / 'model.safetensors' if checkpoint.is_dir() else checkpoint
-    targets = [output, Path(f'{output}.index'), Path(f'{output}.manifest.json')]
+def write_pack(checkpoint_path, output, table=None):
+    """Writes OUTPUT, OUTPUT.index and OUTPUT.manifest.json and returns the
+    manifest's path. `table` replaces the Qwen3-0.6B tensor table (tests)."""
+    table = qwen3_tensor_table() if table is None else table
+    checkpoint_path, output = Path(checkpoint_path), Path(output)
+    source = checkpoint_path / 'model.safetensors' if checkpoint_path.is_dir() else checkpoint_path
+    finals = [output, Path(f'{output}.index'), Path(f'{output}.manifest.json')]
     output.parent.mkdir(parents=True, exist_ok=True)
-    if any(t.exists() or t.is_symlink() for t in targets):
-        raise FileExistsError('Weight pack outputs are immutable; choose a fresh path')
-    source_hash = _sha256(source)
-    header, data_start, size = read_header(source)
-    regions = check_layout(header, data_start, size, shapes)
-    head, embed = regions['lm_head.weight'], regions['model.embed_tokens.weight']
-    if not _same_bytes(source, data_start + head[0], data_start + embed[0], head[1] - head[0]):
-        raise ValueError('lm_head.weight is not bit-identical to the embedding')
+    taken = [p for p in finals if p.exists() or p.is_symlink()]
+    if taken:
+        raise FileExistsError(f'{taken[0]} already exists; packs are never overwritten, choose a new path')
+    before = os.stat(source)
+    checkpoint = Checkpoint(source)
+    temporaries, descriptors = [], []
+    try:
+        audit(checkpoint, table)
+        source_sha = checkpoint.sha256()
+        slots, total = plan(table)
 
-    with tempfile.TemporaryDirectory(prefix='.qwen-pack-', dir=output.parent) as staging:
-        staging = Path(staging)
-        staged = [staging / 'weights.bin', staging / 'weights.bin.index', staging / 'weights.bin.manifest.json']
+        def close(fd):
+            descriptors.remove(fd)
+            os.close(fd)
+
+        def temporary(suffix):
+            fd, name = tempfile.mkstemp(prefix=f'.{output.name}.', suffix=suffix, dir=output.parent)
+            temporaries.append(Path(name))
+            descriptors.append(fd)
+            return fd, Path(name)
+
+        fd, binary = temporary('.bin')
+        os.ftruncate(fd, total)
+        out = np.memmap(binary, dtype=np.uint8, mode='r+', shape=(total,))
+        out[:len(FORMAT)] = np.frombuffer(FORMAT.encode(), np.uint8)
         records = []
-        with source.open('rb') as src, staged[0].open('wb') as dst:
-            dst.write(MAGIC + bytes(ALIGN - len(MAGIC)))
-            for name, shape in shapes.items():
-                matrix = len(shape) == 2
-                offset = -(-dst.tell() // ALIGN) * ALIGN
-                dst.write(bytes(offset - dst.tell()))
-                begin, end = regions[name]
-                src.seek(data_start + begin)
-                seen, written = hashlib.sha256(), hashlib.sha256()
-                left = end - begin
-                while left:
-                    raw = src.read(min(left, BLOCK))
-                    if not raw:
-                        raise ValueError('Truncated tensor during export')
-                    seen.update(raw)
-                    out = convert_block(raw, matrix, name)
-                    written.update(out)
-                    dst.write(out)
-                    left -= len(raw)
-                rows, cols = shape if matrix else (shape[0], 1)
-                length = dst.tell() - offset
-                if length != rows * cols * (2 if matrix else 4):
-                    raise ValueError('Internal converted tensor length mismatch')
-                records.append(dict(name=name, dtype='F16' if matrix else 'F32', rows=rows, columns=cols,
-                                    offset_bytes=offset, length_bytes=length,
-                                    checkpoint_sha256=seen.hexdigest(), sha256=written.hexdigest()))
-            dst.flush()
-            os.fsync(dst.fileno())
-        staged[1].write_text(f'QWCPU01 {len(records)}\n' + ''.join(
-            f"{r['name']} {r['dtype']} {r['rows']} {r['columns']} {r['offset_bytes']} {r['length_bytes']}\n"
-            for r in records))
-        if _sha256(source) != source_hash:
-            raise RuntimeError('Checkpoint changed while exporting')
-        manifest = dict(format='QWCPU01', completed=True, gpu=False, pytorch=False,
-                        checkpoint=dict(path=str(source.resolve()), sha256=source_hash),
-                        exporter_sha256=_sha256(Path(__file__)), numpy_version=np.__version__,
-                        binary=dict(path=output.name, bytes=staged[0].stat().st_size, sha256=_sha256(staged[0])),
-                        index=dict(path=targets[1].name, sha256=_sha256(staged[1])),
-                        tensor_count=len(records), tied_lm_head_verified=True, rounding=ROUNDING,
-                        tensors=records)
-        staged[2].write_text(json.dumps(manifest, indent=2) + '\n')
-        published = []
+        for slot in slots:
+            bits = checkpoint.bf16(slot.name).reshape(slot.rows, -1)
+            target = out[slot.offset:slot.offset + slot.length].view(np.float16 if slot.matrix else np.float32)
+            target = target.reshape(slot.rows, slot.columns)
+            source_digest, pack_digest = hashlib.sha256(), hashlib.sha256()
+            for start in range(0, slot.rows, ROWS_PER_BLOCK):
+                block = bits[start:start + ROWS_PER_BLOCK]
+                values = convert(block, slot.matrix, slot.name).reshape(block.shape[0], slot.columns)
+                target[start:start + block.shape[0]] = values
+                source_digest.update(block.tobytes())
+                pack_digest.update(values.tobytes())
+            records.append(dict(name=slot.name, dtype=slot.dtype, rows=slot.rows, columns=slot.columns,
+                                offset_bytes=slot.offset, length_bytes=slot.length,
+                                source_sha256=source_digest.hexdigest(), sha256=pack_digest.hexdigest()))
+        out.flush()
+        del out, target, bits
+        os.fsync(fd)
+        close(fd)
+
+        fd, index = temporary('.index')
+        lines = [f'{FORMAT} {len(records)}'] + [
+            f"{r['name']} {r['dtype']} {r['rows']} {r['columns']} {r['offset_bytes']} {r['length_bytes']}"
+            for r in records]
+        os.write(fd, ('\n'.join(lines) + '\n').encode())
+        os.fsync(fd)
+        close(fd)
+
+        after = os.stat(source)
+        if (after.st_size, after.st_mtime_ns, after.st_ino) != (before.st_size, before.st_mtime_ns, before.st_ino):
+            raise PackError('the checkpoint changed while the pack was being written')
+        manifest = dict(
+            format=FORMAT, completed=True,
+            producer=dict(tool='fpga-qwen_amd/export_pack.py', sha256=_file_sha256(Path(__file__)),
+                          numpy=np.__version__),
+            source=dict(path=str(source.resolve()), bytes=checkpoint.size, sha256=source_sha),
+            binary=dict(path=output.name, bytes=total, sha256=_file_sha256(binary)),
+            index=dict(path=finals[1].name, sha256=_file_sha256(index)),
+            tensor_count=len(records), tied_lm_head_verified=True, rounding=ROUNDING, tensors=records)
+        fd, manifest_path = temporary('.json')
+        os.write(fd, (json.dumps(manifest, indent=2) + '\n').encode())
+        os.fsync(fd)
+        close(fd)
+
+        linked = []
         try:
-            for path, target in zip(staged, targets):  # manifest last: it marks completion
-                with path.open('rb') as f:
-                    os.fsync(f.fileno())
-                path.chmod(0o444)
-                os.link(path, target)
-                published.append(target)
-            fd = os.open(output.parent, os.O_RDONLY)
+            for staged, final in zip((binary, index, manifest_path), finals):  # the manifest last
+                staged.chmod(0o444)
+                os.link(staged, final)
+                linked.append(final)
+            directory = os.open(output.parent, os.O_RDONLY)
             try:
-                os.fsync(fd)
+                os.fsync(directory)
             finally:
-                os.close(fd)
+                os.close(directory)
         except BaseException:
-            for target in reversed(published):
-                target.unlink()
+            for final in reversed(linked):
+                final.unlink()
             raise
-    return targets[2]
+    finally:
+        for fd in descriptors:
+            os.close(fd)
+        checkpoint.close()
+        for path in temporaries:
+            path.unlink(missing_ok=True)
+    return finals[2]
 
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument('--checkpoint', type=Path, required=True,
-                        help='model.safetensors or the directory holding it')
-    parser.add_argument('--output', type=Path, required=True, help='weights.bin to create')
+                        help='model.safetensors or the directory that holds it')
+    parser.add_argument('--output', type=Path, required=True, help='the weights.bin to create')
     args = parser.parse_args()
-    print(export(args.checkpoint, args.output.resolve()))
+    print(write_pack(args.checkpoint, args.output.resolve()))
 
 
 if __name__ == '__main__':

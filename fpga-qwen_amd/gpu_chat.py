@@ -1,33 +1,40 @@
-"""Chat-side driver of the MI355X engine process (protocol v1,
-engine/INTERFACE.md:40-90): the counterpart of the reference's adapter
-tools/native_cpu_chat.py for callers that switch to ``build/qwen_gpu``.
+"""Chat client of the MI355X engine process (``build/qwen_gpu``, protocol v1 of
+engine/INTERFACE.md:40-90).
 
-It keeps the adapter's contract (tools/native_cpu_chat.py:144-304) and
-differs where the process does: the handshake reports ``"gpu": true``.
-
-* One process per adapter, started lazily; its ready object must report
-  protocol 1, ``gpu`` true, ``pytorch`` false, FP16 weights and KV, FP32
-  norms and activations, the requested worker counts and a 4096 context.
-* Canonical prefix reuse: a request in the same session reuses the longest
-  common prefix with the previous prompt, rounded down to a multiple of 512
-  and capped by the tokens that came from a fresh prompt prefill (never
-  decoded tokens, never the whole prompt), via ``rewind``; otherwise
-  ``reset``. Rows of a 512-aligned rewind equal a fresh prefill's.
-* Greedy B2 drafting (opt-in per request): when a drafter proposes one token
-  after the pending one, ``verify-greedy PENDING DRAFT`` checks both in one
-  call and the adapter consumes only what the engine committed.
-* Any protocol violation, error object or cancellation closes the process
-  and forgets the cached prefix.
-
-Token ids in, token ids out; tokenization and text belong to the caller
+A front end hands it one request at a time (prompt token ids, an output
+budget, greedy or seeded chat decoding, optional one-token drafting) and
+receives the events a chat page consumes: ``loading``, ``start``,
+``prefill``, one ``update`` per emitted token and ``done``, each carrying the
+running metrics. Tokenization and text belong to the caller
 (``protocol.tokenizer.decode``).
+
+The rules it keeps are the reference adapter's contract
+(tools/native_cpu_chat.py:144-304, engine/INTERFACE.md:91-120); the code is
+this project's own:
+
+* the engine consumes only committed inputs; an EOS prediction is reported,
+  never fed back;
+* a new request of the same session reuses its common prefix with what the
+  engine holds, but only whole 512-token chunks that came from a prompt
+  prefill, and never the whole prompt (the last prompt token is always
+  prefilled, its logits give the first output); anything else starts from
+  ``reset``;
+* drafting (greedy only, opt-in per request) proposes one token after the
+  pending one and checks both with ``verify-greedy``; only what the engine
+  committed enters the context;
+* an error object, a malformed or inconsistent response, a time-out or a
+  cancellation ends the process and forgets the context.
+
+It differs where this engine does: the handshake reports ``"gpu": true``.
 """
 import json
 import os
+import queue
 import secrets
-import select
 import subprocess
+import threading
 import time
+from dataclasses import asdict, dataclass, field
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -35,319 +42,485 @@ EOS = frozenset((151643, 151645))
 VOCABULARY = 151936
 CONTEXT = 4096
 CHUNK = 512
+REPLY_TIMEOUT = 180.0
+
+# What the engine's ready line must state (exact values and JSON types).
+HANDSHAKE = dict(ready=True, protocol=1, gpu=True, pytorch=False, weight_precision='f16', kv_precision='f16',
+                 norm_precision='f32', activation_precision='f32', context=CONTEXT)
 
 
-class NativeCancelled(Exception):
-    """The request's cancel event was set."""
+class Cancelled(Exception):
+    """The caller's cancel event was set while a request was running."""
 
 
-class LongestMatchDrafter:
-    """Proposes the tokens that followed the most recent earlier occurrence
-    of the context's longest suffix (min_match..max_match tokens), looking in
-    the context first and then in earlier sequences, newest first. The same
-    rule as the reference's n-gram drafter (tools/suffix.py:4-33): no model,
-    no future tokens."""
+class EngineError(RuntimeError):
+    """The engine answered with an error, broke the protocol or went away."""
+
+
+def _is_token(value):
+    return type(value) is int and 0 <= value < VOCABULARY
+
+
+# ---------------------------------------------------------------- drafting
+
+class NGramDrafter:
+    """Proposes what followed an earlier occurrence of the context's tail.
+
+    Tails of max_match down to min_match tokens are tried, longest first; for
+    each tail the current context is searched first, then the history
+    sequences from the newest; within a sequence the occurrence closest to its
+    end that still has a following token wins. That is the reference
+    drafter's rule (tools/suffix.py:4-29); the search here walks the
+    occurrences of the tail's last token, indexed once per sequence.
+    """
 
     def __init__(self, min_match=2, max_match=12, max_context=CONTEXT, history=()):
-        if not 1 <= min_match <= max_match or max_context < max_match:
-            raise ValueError('Invalid matching limits')
+        if not (1 <= min_match <= max_match) or max_context < max_match:
+            raise ValueError('Drafter limits need 1 <= min_match <= max_match <= max_context')
         self.min_match, self.max_match, self.max_context = min_match, max_match, max_context
-        self.history = [tuple(h) for h in history]
+        self.history = [list(seq) for seq in history]
+
+    @staticmethod
+    def _ends(seq):
+        """token -> end positions (exclusive) that have a following token, newest first."""
+        ends = {}
+        for end in range(len(seq) - 1, 0, -1):
+            ends.setdefault(seq[end - 1], []).append(end)
+        return ends
 
     def propose(self, context, count):
         if count < 0:
-            raise ValueError('Negative proposal length')
-        if count == 0:
+            raise ValueError('Cannot propose a negative number of tokens')
+        context = list(context)[-self.max_context:]
+        if count == 0 or not context:
             return []
-        context = tuple(context[-self.max_context:])
         sources = [context] + self.history[::-1]
+        indexes = [self._ends(seq) for seq in sources]
         for length in range(min(self.max_match, len(context)), self.min_match - 1, -1):
-            suffix = context[-length:]
-            for seq in sources:
-                # Latest occurrence that still has a next token.
-                for start in range(len(seq) - length - 1, -1, -1):
-                    if seq[start:start + length] == suffix:
-                        return list(seq[start + length:start + length + count])
+            tail = context[-length:]
+            for seq, ends in zip(sources, indexes):
+                for end in ends.get(tail[-1], ()):
+                    if end >= length and seq[end - length:end] == tail:
+                        return seq[end:end + count]
         return []
 
 
-class NativeGPUChat:
+# ---------------------------------------------------------------- transport
+
+_CLOSED = object()
+
+
+class ProcessLink:
+    """One engine process. Commands are written to its stdin; a reader thread
+    cuts its stdout into lines and queues them, so waiting for a reply can
+    watch the cancel event and a deadline at the same time."""
+
+    MAX_LINE = 1 << 20
+
+    def __init__(self, argv, log):
+        self.proc = subprocess.Popen(argv, stdin=subprocess.PIPE, stdout=subprocess.PIPE, stderr=log, bufsize=0)
+        self.lines = queue.Queue()
+        self.reader = threading.Thread(target=self._read_lines, daemon=True)
+        self.reader.start()
+
+    def _read_lines(self):
+        pending = bytearray()
+        try:
+            while True:
+                block = os.read(self.proc.stdout.fileno(), 1 << 16)
+                if not block:
+                    break
+                pending += block
+                while (cut := pending.find(b'\n')) >= 0:
+                    self.lines.put(bytes(pending[:cut]))
+                    del pending[:cut + 1]
+                if len(pending) > self.MAX_LINE:
+                    self.lines.put(b'oversized')
+                    break
+        except OSError:
+            pass
+        finally:
+            self.lines.put(_CLOSED)
+
+    def alive(self):
+        return self.proc.poll() is None
+
+    def send(self, line):
+        data = (line + '\n').encode()
+        written = 0
+        while written < len(data):
+            n = self.proc.stdin.write(data[written:])
+            if not n:
+                raise EngineError('Engine stdin closed')
+            written += n
+
+    def receive(self, cancel, timeout):
+        """The next reply as a dict; Cancelled, EngineError or TimeoutError."""
+        deadline = time.monotonic() + timeout
+        while True:
+            if cancel.is_set():
+                raise Cancelled()
+            try:
+                line = self.lines.get(timeout=0.02)
+            except queue.Empty:
+                if time.monotonic() > deadline:
+                    raise TimeoutError('No engine reply before the deadline')
+                continue
+            if line is _CLOSED:
+                raise EngineError('Engine process ended; see its chat.log')
+            try:
+                reply = json.loads(line)
+            except ValueError:
+                raise EngineError(f'Engine wrote a line that is not JSON: {line[:120]!r}') from None
+            if not isinstance(reply, dict):
+                raise EngineError(f'Engine reply is not an object: {reply!r}')
+            if 'error' in reply:
+                raise EngineError(f'Engine error: {reply["error"]}')
+            return reply
+
+    def exchange(self, line, cancel, timeout=REPLY_TIMEOUT):
+        self.send(line)
+        return self.receive(cancel, timeout)
+
+    def shutdown(self):
+        if self.proc.poll() is None:
+            self.proc.terminate()
+            try:
+                self.proc.wait(timeout=2)
+            except subprocess.TimeoutExpired:
+                self.proc.kill()
+                self.proc.wait(timeout=5)
+        for pipe in (self.proc.stdin, self.proc.stdout):
+            try:
+                pipe.close()
+            except OSError:
+                pass
+        self.reader.join(timeout=2)
+
+
+# ---------------------------------------------------------------- context bookkeeping
+
+class ContextLedger:
+    """What the engine holds: the ids it consumed, in order, the session they
+    belong to, and how many leading ids are whole 512-token chunks of a prompt
+    prefill (the only part a later request may keep)."""
+
+    def __init__(self):
+        self.clear()
+
+    def clear(self):
+        self.ids, self.session, self.canonical = [], None, 0
+
+    def reusable(self, session, prompt):
+        """Leading prompt tokens a rewind may keep (a multiple of 512)."""
+        if session != self.session:
+            return 0
+        limit = min(self.canonical, len(prompt) - 1, len(self.ids))
+        common = 0
+        while common < limit and self.ids[common] == prompt[common]:
+            common += 1
+        return common - common % CHUNK
+
+    def prefilled(self, session, prompt):
+        self.ids, self.session = list(prompt), session
+        self.canonical = len(prompt) - len(prompt) % CHUNK
+
+
+@dataclass
+class RequestMetrics:
+    """The running numbers each event carries (names as the chat page reads them)."""
+    prompt_tokens: int = 0
+    reused_prefix_tokens: int = 0
+    evaluated_prompt_tokens: int = 0
+    output_tokens: int = 0
+    rounds: int = 0
+    proposed_tokens: int = 0
+    accepted_tokens: int = 0
+    rejected_tokens: int = 0
+    tokens_per_round: float = 0
+    suffix_enabled: bool = False
+    verification_calls: int = 0
+    verified_positions: int = 0
+    decode_tokens_per_second: float = 0
+    first_token_ms: float = None
+    elapsed_seconds: float = 0
+    kv_tokens: int = 0
+    context_limit: int = CONTEXT
+
+
+@dataclass
+class _Run:
+    request: object
+    began: float = field(default_factory=time.perf_counter)
+    tokens: list = field(default_factory=list)
+    text: str = ''
+    first_at: float = None
+    reason: str = 'length'
+    metrics: RequestMetrics = field(default_factory=RequestMetrics)
+
+    def event(self, kind, **extra):
+        self.metrics.elapsed_seconds = time.perf_counter() - self.began
+        return dict(type=kind, **extra, metrics=asdict(self.metrics))
+
+    def emit(self, token, decode):
+        now = time.perf_counter()
+        self.tokens.append(token)
+        if self.first_at is None:
+            self.first_at = now
+            self.metrics.first_token_ms = (now - self.began) * 1e3
+        self.text = decode(self.tokens, skip_special_tokens=True)
+        m = self.metrics
+        m.output_tokens = len(self.tokens)
+        m.tokens_per_round = m.output_tokens / m.rounds
+        m.decode_tokens_per_second = (len(self.tokens) - 1) / (now - self.first_at) if now > self.first_at else 0
+        return self.event('update', text=self.text, token_ids=list(self.tokens))
+
+    def done(self):
+        m = self.metrics
+        m.tokens_per_round = len(self.tokens) / m.rounds if m.rounds else 0
+        return self.event('done', text=self.text, token_ids=list(self.tokens), finish_reason=self.reason)
+
+
+def _checked_verification(reply, draft, budget, base):
+    """(tokens, accepted, committed) of a verify-greedy reply, after checking it
+    against engine/INTERFACE.md:63-72 and the request's output budget."""
+    def fail(what):
+        raise EngineError(f'Invalid engine B2 verification response: {what}')
+
+    tokens = reply.get('tokens')
+    if not (isinstance(tokens, list) and 1 <= len(tokens) <= 2 and all(map(_is_token, tokens))):
+        fail('tokens')
+    accepted = reply.get('accepted')
+    if type(accepted) is not int or accepted != int(tokens[0] == draft):
+        fail('accepted')
+    committed = reply.get('committed_inputs')
+    if type(committed) is not int or committed != (2 if accepted and tokens[0] not in EOS else 1):
+        fail('committed_inputs')
+    if len(tokens) != committed:
+        fail('one prediction per committed input')
+    if len(tokens) > budget:
+        fail('more predictions than the output budget')
+    if tokens[0] in EOS and len(tokens) > 1:
+        fail('prediction after EOS')
+    position = reply.get('position')
+    if type(position) is not int or position != base + committed:
+        fail('position')
+    if type(reply.get('verified_positions')) is not int or reply['verified_positions'] != 2:
+        fail('verified_positions')
+    if reply.get('finish_reason') != ('eos' if tokens[-1] in EOS else None):
+        fail('finish_reason')
+    return tokens, accepted, committed
+
+
+# ---------------------------------------------------------------- the client
+
+class GPUChatAdapter:
     def __init__(self, protocol, binary=None, weights=None, threads=12, prefill_threads=6, reuse_prefix=True,
-                 drafter_factory=LongestMatchDrafter):
-        if type(reuse_prefix) is not bool:
-            raise ValueError('reuse_prefix must be boolean')
+                 drafter_factory=NGramDrafter, link_factory=None):
+        if not isinstance(reuse_prefix, bool):
+            raise ValueError('reuse_prefix must be True or False')
         self.protocol = protocol
         self.binary = Path(binary or PACKAGE_DIR / 'build' / 'qwen_gpu')
         self.weights = Path(weights or PACKAGE_DIR / 'build' / 'weights.bin')
         self.threads, self.prefill_threads = threads, prefill_threads
         self.reuse_prefix = reuse_prefix
         self.drafter_factory = drafter_factory
-        self.process = None
+        self.link_factory = link_factory or self._spawn
+        self.link = None
         self.ready = None
-        self.log = None
-        self._pending = b''
-        self._forget()
+        self.ledger = ContextLedger()
+        self._log = None
 
-    # -- cached prefix bookkeeping ---------------------------------------
-    def _forget(self):
-        self.cache_ids = []           # inputs the engine has consumed, in order
-        self.cache_session = None
-        self.canonical_reusable_tokens = 0   # prompt tokens a rewind may keep
-
-    def _capable(self, key, value):
-        return bool(self.ready and self.ready.get(key) is True and self.process is not None
-                    and self.process.poll() is None and value)
+    # -- capabilities the running engine advertised
+    def _advertises(self, key, value=True):
+        ready = self.ready or {}
+        return (self.link is not None and self.link.alive() and type(ready.get(key)) is type(value)
+                and ready.get(key) == value)
 
     def prefix_reuse_supported(self):
-        chunk = (self.ready or {}).get('prefix_reuse_chunk')
-        return self._capable('prefix_reuse', type(chunk) is int and chunk == CHUNK)
+        return self._advertises('prefix_reuse') and self._advertises('prefix_reuse_chunk', CHUNK)
 
     def suffix_supported(self):
-        draft = (self.ready or {}).get('max_verified_draft')
-        return self._capable('verify_greedy_b2', type(draft) is int and draft == 1)
+        return self._advertises('verify_greedy_b2') and self._advertises('max_verified_draft', 1)
 
     def available(self):
-        return (self.binary.is_file() and os.access(self.binary, os.X_OK) and self.weights.is_file()
-                and Path(f'{self.weights}.index').is_file() and Path(f'{self.weights}.manifest.json').is_file())
+        files = [self.binary, self.weights, Path(f'{self.weights}.index'), Path(f'{self.weights}.manifest.json')]
+        return all(p.is_file() for p in files) and os.access(self.binary, os.X_OK)
 
     def status(self):
         reuse, suffix = self.prefix_reuse_supported(), self.suffix_supported()
         return dict(model='Qwen3-0.6B', device='gpu', gpu_inference=True, pytorch_loaded=False,
                     precision='FP16 matrices / FP32 norm weights / FP16 KV', context_limit=CONTEXT,
                     decode_workers=self.threads, prefill_workers=self.prefill_threads,
-                    cached_tokens=len(self.cache_ids) if reuse else 0,
-                    prefix_reuse_supported=reuse, prefix_reuse_enabled=self.reuse_prefix and reuse,
-                    canonical_reusable_tokens=self.canonical_reusable_tokens if reuse else 0,
+                    cached_tokens=len(self.ledger.ids) if reuse else 0,
+                    prefix_reuse_supported=reuse, prefix_reuse_enabled=reuse and self.reuse_prefix,
+                    canonical_reusable_tokens=self.ledger.canonical if reuse else 0,
                     canonical_prefix_policy='native_f16_prefill512_v1' if reuse else None,
-                    suffix_supported=suffix, suffix_greedy_only=True, max_verified_draft=1 if suffix else 0)
+                    suffix_supported=suffix, suffix_greedy_only=True, max_verified_draft=int(suffix))
 
-    # -- process ---------------------------------------------------------
-    def close(self):
-        self._forget()
-        process, self.process = self.process, None
-        if process is not None:
-            if process.poll() is None:
-                process.terminate()
-                try:
-                    process.wait(timeout=2)
-                except subprocess.TimeoutExpired:
-                    process.kill()
-                    process.wait(timeout=5)
-            for pipe in (process.stdin, process.stdout):
-                if pipe:
-                    pipe.close()
-        if self.log:
-            self.log.close()
-            self.log = None
-        self._pending = b''
-        self.ready = None
+    # -- process lifetime
+    def _spawn(self):
+        if self._log is None:
+            self._log = (self.binary.parent / 'chat.log').open('ab')
+        return ProcessLink([str(self.binary), '--weights', str(self.weights), '--threads', str(self.threads),
+                            '--prefill-threads', str(self.prefill_threads), '--context', str(CONTEXT)], self._log)
 
     def start(self, cancel):
-        if self.process is not None and self.process.poll() is None:
+        """Starts the engine unless it is running, and checks its ready line."""
+        if self.link is not None and self.link.alive():
             return
         self.close()
         if not self.available():
-            raise RuntimeError('Build the engine and export a weight pack before selecting this backend')
+            raise EngineError('Build the engine and write a weight pack before selecting this backend')
         manifest = json.loads(Path(f'{self.weights}.manifest.json').read_text())
         if manifest.get('format') != 'QWCPU01' or manifest.get('completed') is not True:
-            raise RuntimeError('Weight pack manifest is incomplete')
-        self.log = (self.binary.parent / 'chat.log').open('ab')
-        argv = [str(self.binary), '--weights', str(self.weights), '--threads', str(self.threads),
-                '--prefill-threads', str(self.prefill_threads), '--context', str(CONTEXT)]
+            raise EngineError('The weight pack manifest does not mark a completed QWCPU01 pack')
         try:
-            self.process = subprocess.Popen(argv, stdin=subprocess.PIPE, stdout=subprocess.PIPE, stderr=self.log,
-                                            bufsize=0)
-            ready = self._read(cancel)
-            expected = dict(ready=True, protocol=1, gpu=True, pytorch=False, weight_precision='f16',
-                            kv_precision='f16', norm_precision='f32', activation_precision='f32',
-                            decode_threads=self.threads, prefill_threads=self.prefill_threads, context=CONTEXT)
-            if any(ready.get(key) != value or type(ready.get(key)) is not type(value)
-                   for key, value in expected.items()):
-                raise RuntimeError('Unexpected engine startup handshake')
+            self.link = self.link_factory()
+            ready = self.link.receive(cancel, REPLY_TIMEOUT)
+            wanted = dict(HANDSHAKE, decode_threads=self.threads, prefill_threads=self.prefill_threads)
+            wrong = sorted(k for k, v in wanted.items() if type(ready.get(k)) is not type(v) or ready.get(k) != v)
+            if wrong:
+                raise EngineError(f'Engine handshake differs from this client in: {", ".join(wrong)}')
             self.ready = ready
         except BaseException:
             self.close()
             raise
 
-    def _read(self, cancel, timeout=180):
-        deadline = time.monotonic() + timeout
-        while True:
-            if cancel.is_set():
-                self.close()
-                raise NativeCancelled()
-            line, sep, rest = self._pending.partition(b'\n')
-            if sep:
-                self._pending = rest
-                value = json.loads(line)
-                if not isinstance(value, dict) or value.get('error'):
-                    raise RuntimeError(f'Engine protocol error: {value}')
-                return value
-            if self.process is None or self.process.poll() is not None:
-                raise RuntimeError('Engine process exited; see its chat.log')
-            if time.monotonic() >= deadline:
-                raise TimeoutError('Engine response timed out')
-            if select.select([self.process.stdout], [], [], 0.05)[0]:
-                block = os.read(self.process.stdout.fileno(), 1 << 16)
-                if not block:
-                    raise RuntimeError('Engine stdout closed')
-                self._pending += block
-                if len(self._pending) > 1 << 20:
-                    raise RuntimeError('Oversized engine protocol response')
+    def close(self):
+        self.ledger.clear()
+        link, self.link, self.ready = self.link, None, None
+        if link is not None:
+            link.shutdown()
+        if self._log is not None:
+            self._log.close()
+            self._log = None
 
-    def command(self, command, cancel, *, preserve_cache=False):
-        """Sends one command line and returns its JSON response. Commands that
-        change the context forget the cached prefix unless the caller keeps
-        the bookkeeping itself (preserve_cache)."""
-        if '\n' in command or '\r' in command:
-            raise ValueError('Engine command must occupy one line')
-        op = command.split(' ', 1)[0]
-        if op == 'reset' or (not preserve_cache and op in ('rewind', 'prefill', 'step', 'verify-greedy')):
-            self._forget()
+    def command(self, line, cancel, *, keep_ledger=False):
+        """Sends one protocol command and returns its reply. A command that
+        changes the engine's context clears the ledger unless the caller
+        updates it itself (keep_ledger); any failure ends the process."""
+        if '\n' in line or '\r' in line:
+            raise ValueError('A protocol command is one line')
+        verb = line.split(' ', 1)[0]
+        if verb == 'reset' or (not keep_ledger and verb in ('rewind', 'prefill', 'step', 'verify-greedy')):
+            self.ledger.clear()
         try:
             if cancel.is_set():
-                raise NativeCancelled()
-            data = memoryview((command + '\n').encode())
-            while data:
-                n = self.process.stdin.write(data)
-                if not n:
-                    raise RuntimeError('Engine stdin closed')
-                data = data[n:]
-            self.process.stdin.flush()
-            return self._read(cancel)
+                raise Cancelled()
+            if self.link is None:
+                raise EngineError('Engine not started')
+            return self.link.exchange(line, cancel)
         except BaseException:
             self.close()
             raise
 
-    # -- one request -----------------------------------------------------
-    def _reusable(self, request):
-        if not (self.reuse_prefix and self.prefix_reuse_supported() and self.cache_session == request.session):
-            return 0
-        common = 0
-        for a, b in zip(self.cache_ids, request.ids):
-            if a != b:
-                break
-            common += 1
-        # Keep whole 512-token chunks of an earlier prompt prefill, and always
-        # recompute at least one prompt token so the call yields logits.
-        return min(common, self.canonical_reusable_tokens, len(request.ids) - 1) // CHUNK * CHUNK
-
-    def _check_verification(self, response, draft, remaining):
-        tokens, accepted, committed = response.get('tokens'), response.get('accepted'), response.get('committed_inputs')
-        valid = (isinstance(tokens, list) and tokens and all(type(t) is int and 0 <= t < VOCABULARY for t in tokens)
-                 and type(accepted) is int and accepted == int(tokens[0] == draft)
-                 and type(committed) is int and committed == (2 if accepted and tokens[0] not in EOS else 1)
-                 and len(tokens) == committed and len(tokens) <= remaining
-                 and not any(t in EOS for t in tokens[:-1])
-                 and type(response.get('position')) is int
-                 and response['position'] == len(self.cache_ids) + committed
-                 and response.get('verified_positions') == 2 and type(response.get('verified_positions')) is int
-                 and response.get('finish_reason') == ('eos' if tokens[-1] in EOS else None))
-        if not valid:
-            raise RuntimeError('Invalid engine B2 verification response')
-        return tokens, accepted, committed
-
+    # -- one request
     def stream(self, request, cancel):
-        """Yields loading, start, prefill, update* and done events for one
-        request (ids, max_new, max_draft, decoding 'greedy' or chat, seed,
-        session)."""
-        started = time.perf_counter()
-        out, text, first, reason = [], '', None, 'length'
-        metrics = dict(prompt_tokens=len(request.ids), reused_prefix_tokens=0, output_tokens=0, rounds=0,
-                       proposed_tokens=0, accepted_tokens=0, rejected_tokens=0, tokens_per_round=0,
-                       suffix_enabled=False, verification_calls=0, verified_positions=0,
-                       decode_tokens_per_second=0, first_token_ms=None, elapsed_seconds=0, kv_tokens=0,
-                       context_limit=CONTEXT)
+        """Yields the request's events; request has ids, max_new, max_draft,
+        decoding ('greedy' or chat), seed and session."""
+        run = _Run(request)
+        run.metrics.prompt_tokens = len(request.ids)
         try:
             if request.max_draft and request.decoding != 'greedy':
-                raise ValueError('B2 suffix drafting supports greedy decoding only')
-            yield dict(type='loading', message='Loading the MI355X engine…')
+                raise ValueError('One-token drafting needs greedy decoding')
+            yield run.event('loading', message='Loading the MI355X engine…')
             self.start(cancel)
-            metrics['suffix_enabled'] = bool(request.max_draft > 0 and request.decoding == 'greedy'
-                                             and self.suffix_supported())
-            reuse = self._reusable(request)
-            if reuse:
-                ack = self.command(f'rewind {reuse}', cancel, preserve_cache=True)
-                if ack.get('ok') is not True or ack.get('position') != reuse:
-                    raise RuntimeError('Engine rewind did not keep the reused prefix')
-                self.cache_ids = self.cache_ids[:reuse]
-                self.canonical_reusable_tokens = reuse
-            else:
-                ack = self.command('reset', cancel)
-                if ack.get('ok') is not True or ack.get('position') != 0:
-                    raise RuntimeError('Engine reset did not clear the context')
-            metrics.update(reused_prefix_tokens=reuse, evaluated_prompt_tokens=len(request.ids) - reuse,
-                           kv_tokens=reuse)
-            seed = request.seed if request.seed is not None else secrets.randbits(32)
-            mode = 'mode greedy' if request.decoding == 'greedy' else f'mode chat {seed}'
-            if self.command(mode, cancel).get('ok') is not True:
-                raise RuntimeError('Engine decoding mode was not acknowledged')
-            yield dict(type='start', metrics=dict(metrics))
-            response = self.command('prefill ' + ' '.join(map(str, request.ids[reuse:])), cancel,
-                                    preserve_cache=True)
-            if response.get('position') != len(request.ids):
-                raise RuntimeError('Engine prefill position differs from the full prompt')
-            self.cache_ids, self.cache_session = list(request.ids), request.session
-            self.canonical_reusable_tokens = (len(request.ids) // CHUNK * CHUNK
-                                              if self.prefix_reuse_supported() else 0)
-            metrics.update(elapsed_seconds=time.perf_counter() - started, kv_tokens=len(request.ids))
-            yield dict(type='prefill', processed_tokens=len(request.ids) - reuse, metrics=dict(metrics))
-            drafter = self.drafter_factory() if self.drafter_factory else None
-            produced = [response.get('token')]
-            while len(out) < request.max_new:
-                metrics['rounds'] += 1
-                metrics['kv_tokens'] = len(self.cache_ids)
-                for token in produced:
-                    if cancel.is_set():
-                        raise NativeCancelled()
-                    if type(token) is not int or not 0 <= token < VOCABULARY:
-                        raise RuntimeError('Invalid engine token')
-                    if token in EOS:
-                        reason = 'eos'
-                        break
-                    out.append(token)
-                    now = time.perf_counter()
-                    if first is None:
-                        first = now
-                        metrics['first_token_ms'] = (now - started) * 1e3
-                    text = self.protocol.tokenizer.decode(out, skip_special_tokens=True)
-                    metrics.update(output_tokens=len(out), tokens_per_round=len(out) / metrics['rounds'],
-                                   elapsed_seconds=now - started,
-                                   decode_tokens_per_second=(len(out) - 1) / (now - first) if now > first else 0)
-                    yield dict(type='update', text=text, token_ids=list(out), metrics=dict(metrics))
-                if reason == 'eos' or len(out) >= request.max_new:
-                    break
-                # The last emitted token is pending: it enters cache_ids only
-                # once the engine consumes it. The reuse ceiling stays at the
-                # prompt prefill.
-                pending, remaining = out[-1], request.max_new - len(out)
-                draft = []
-                if (drafter and request.max_draft > 0 and self.suffix_supported() and remaining >= 2
-                        and len(self.cache_ids) + 2 <= CONTEXT):
-                    draft = drafter.propose(self.cache_ids + [pending], 1)
-                if draft:
-                    metrics['proposed_tokens'] += 1
-                    metrics['verification_calls'] += 1
-                    response = self.command(f'verify-greedy {pending} {draft[0]}', cancel, preserve_cache=True)
-                    tokens, accepted, committed = self._check_verification(response, draft[0], remaining)
-                    self.cache_ids.extend([pending, draft[0]][:committed])
-                    metrics['accepted_tokens'] += accepted
-                    metrics['rejected_tokens'] += 1 - accepted
-                    metrics['verified_positions'] += 2
-                    produced = tokens
-                else:
-                    response = self.command(f'step {pending}', cancel, preserve_cache=True)
-                    if response.get('position') != len(self.cache_ids) + 1:
-                        raise RuntimeError('Invalid engine step position')
-                    self.cache_ids.append(pending)
-                    produced = [response.get('token')]
+            run.metrics.suffix_enabled = bool(request.max_draft > 0 and request.decoding == 'greedy'
+                                              and self.suffix_supported())
+            kept = self._open_context(request, cancel)
+            run.metrics.reused_prefix_tokens = kept
+            run.metrics.evaluated_prompt_tokens = len(request.ids) - kept
+            run.metrics.kv_tokens = kept
+            self._choose_mode(request, cancel)
+            yield run.event('start')
+            first = self._prefill(request, kept, cancel)
+            run.metrics.kv_tokens = len(self.ledger.ids)
+            yield run.event('prefill', processed_tokens=len(request.ids) - kept)
+            yield from self._decode(run, first, cancel)
             if cancel.is_set():
-                raise NativeCancelled()
-        except NativeCancelled:
+                raise Cancelled()
+        except Cancelled:
             self.close()
-            reason = 'stopped'
+            run.reason = 'stopped'
         except BaseException:
             self.close()
             raise
-        metrics['elapsed_seconds'] = time.perf_counter() - started
-        metrics['tokens_per_round'] = len(out) / metrics['rounds'] if metrics['rounds'] else 0
-        yield dict(type='done', text=text, token_ids=list(out), metrics=dict(metrics), finish_reason=reason)
+        yield run.done()
+
+    def _open_context(self, request, cancel):
+        keep = self.ledger.reusable(request.session, request.ids) if (
+            self.reuse_prefix and self.prefix_reuse_supported()) else 0
+        if keep:
+            reply = self.command(f'rewind {keep}', cancel, keep_ledger=True)
+            if reply.get('ok') is not True or reply.get('position') != keep:
+                raise EngineError('Engine rewind did not keep the reused prefix')
+            self.ledger.ids = self.ledger.ids[:keep]
+            self.ledger.canonical = keep
+        else:
+            reply = self.command('reset', cancel)
+            if reply.get('ok') is not True or reply.get('position') != 0:
+                raise EngineError('Engine reset did not empty the context')
+        return keep
+
+    def _choose_mode(self, request, cancel):
+        if request.decoding == 'greedy':
+            line = 'mode greedy'
+        else:
+            line = f'mode chat {request.seed if request.seed is not None else secrets.randbits(32)}'
+        if self.command(line, cancel).get('ok') is not True:
+            raise EngineError('Engine did not acknowledge the decoding mode')
+
+    def _prefill(self, request, kept, cancel):
+        reply = self.command('prefill ' + ' '.join(map(str, request.ids[kept:])), cancel, keep_ledger=True)
+        if reply.get('position') != len(request.ids):
+            raise EngineError('Engine position after prefill is not the prompt length')
+        self.ledger.prefilled(request.session, request.ids)
+        if not self.prefix_reuse_supported():
+            self.ledger.canonical = 0
+        return reply.get('token')
+
+    def _decode(self, run, first, cancel):
+        request, decode = run.request, self.protocol.tokenizer.decode
+        drafter = self.drafter_factory() if self.drafter_factory else None
+        fresh = [first]  # predictions not yet shown; the last shown one is pending
+        while len(run.tokens) < request.max_new:
+            run.metrics.rounds += 1
+            run.metrics.kv_tokens = len(self.ledger.ids)
+            for token in fresh:
+                if cancel.is_set():
+                    raise Cancelled()
+                if not _is_token(token):
+                    raise EngineError(f'Engine predicted an invalid token: {token!r}')
+                if token in EOS:
+                    run.reason = 'eos'
+                    return
+                yield run.emit(token, decode)
+            budget = request.max_new - len(run.tokens)
+            if budget <= 0:
+                return
+            fresh = self._advance(run, run.tokens[-1], budget, drafter, cancel)
+
+    def _advance(self, run, pending, budget, drafter, cancel):
+        """Feeds the pending token (and a draft after it, when one is
+        proposed) and returns the engine's new predictions."""
+        draft = []
+        if (drafter is not None and run.request.max_draft > 0 and budget >= 2 and self.suffix_supported()
+                and len(self.ledger.ids) + 2 <= CONTEXT):
+            draft = drafter.propose(self.ledger.ids + [pending], 1)
+        if not draft:
+            reply = self.command(f'step {pending}', cancel, keep_ledger=True)
+            if reply.get('position') != len(self.ledger.ids) + 1:
+                raise EngineError('Engine position after a step is not one past the context')
+            self.ledger.ids.append(pending)
+            return [reply.get('token')]
+        m = run.metrics
+        m.proposed_tokens += 1
+        m.verification_calls += 1
+        reply = self.command(f'verify-greedy {pending} {draft[0]}', cancel, keep_ledger=True)
+        tokens, accepted, committed = _checked_verification(reply, draft[0], budget, len(self.ledger.ids))
+        self.ledger.ids += [pending, draft[0]][:committed]
+        m.accepted_tokens += accepted
+        m.rejected_tokens += 1 - accepted
+        m.verified_positions += 2
+        return tokens

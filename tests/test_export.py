@@ -66,7 +66,7 @@ def test_small_export_layout_and_values(tmp_path):
                         2.0 ** -14, 1.0, 2.0, 4.0], np.float32)
     t['model.layers.0.a.weight'] = bf16(special).reshape(3, 4)
     ckpt = write_checkpoint(tmp_path / 'model.safetensors', t, order=list(reversed(list(t))))
-    manifest = export_pack.export(tmp_path, tmp_path / 'out' / 'weights.bin', shapes=SMALL)
+    manifest = export_pack.write_pack(tmp_path, tmp_path / 'out' / 'weights.bin', table=SMALL)
     pack = (tmp_path / 'out' / 'weights.bin').read_bytes()
     assert pack[:64] == b'QWCPU01' + bytes(57)
     lines = (tmp_path / 'out' / 'weights.bin.index').read_text().splitlines()
@@ -92,21 +92,21 @@ def test_small_export_layout_and_values(tmp_path):
     assert got.tolist() == expected
     # Outputs are immutable.
     with pytest.raises(FileExistsError):
-        export_pack.export(ckpt, tmp_path / 'out' / 'weights.bin', shapes=SMALL)
+        export_pack.write_pack(ckpt, tmp_path / 'out' / 'weights.bin', table=SMALL)
 
 
 @pytest.mark.parametrize('case, message', [
-    ('missing', 'exactly the expected'),
-    ('extra', 'exactly the expected'),
-    ('dtype', 'dtype/shape'),
-    ('shape', 'dtype/shape'),
-    ('hole', 'overlap, contain holes'),
-    ('tail', 'overlap, contain holes'),
-    ('overlap', 'bounds/length|overlap'),
-    ('untied', 'not bit-identical'),
-    ('nan', 'Nonfinite'),
-    ('overflow', 'FP16 overflow'),
-    ('duplicate', 'Duplicate JSON key'),
+    ('missing', 'are not the 5 of Qwen3-0.6B: missing'),
+    ('extra', 'unexpected'),
+    ('dtype', 'expected BF16 \\[4\\], found F32'),
+    ('shape', 'expected BF16 \\[3, 4\\], found BF16 \\[4, 3\\]'),
+    ('hole', 'a gap or an overlap'),
+    ('tail', 'trailing bytes'),
+    ('overlap', 'a gap or an overlap'),
+    ('untied', 'tied head'),
+    ('nan', 'non-finite'),
+    ('overflow', 'beyond the FP16 range'),
+    ('duplicate', 'repeats the key'),
 ])
 def test_rejections(tmp_path, case, message):
     rng = np.random.default_rng(6)
@@ -150,7 +150,7 @@ def test_rejections(tmp_path, case, message):
     else:
         write_checkpoint(path, t, **kwargs)
     with pytest.raises(ValueError, match=message):
-        export_pack.export(path, tmp_path / 'out' / 'weights.bin', shapes=SMALL)
+        export_pack.write_pack(path, tmp_path / 'out' / 'weights.bin', table=SMALL)
     assert not (tmp_path / 'out' / 'weights.bin').exists()
 
 
@@ -158,7 +158,7 @@ def test_full_shape_export_passes_engine_validation(tmp_path, qpkg):
     """A synthetic BF16 checkpoint with the exact Qwen3-0.6B tensor set: the
     exported pack must pass the engine's validator (on a host without a GPU
     the constructor then stops at the device check)."""
-    shapes = export_pack.pack_shapes()
+    shapes = export_pack.qwen3_tensor_table()
     rng = np.random.default_rng(7)
     wide = rng.standard_normal(1 << 19).astype(np.float32) * 0.02
     pattern = bf16((wide.view(np.uint32) & 0xffff0000).view(np.float32))
@@ -183,7 +183,7 @@ def test_full_shape_export_passes_engine_validation(tmp_path, qpkg):
             reps = -(-count // pattern.size)
             f.write(np.tile(pattern, reps)[:count].tobytes())
     out = tmp_path / 'pack' / 'weights.bin'
-    export_pack.export(path, out)
+    export_pack.write_pack(path, out)
     index = out.with_name('weights.bin.index').read_text().splitlines()
     assert index[0] == 'QWCPU01 310' and len(index) == 311
     try:
