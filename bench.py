@@ -52,18 +52,80 @@ def attention_bytes(n):
 
 
 def measured_traffic(kernel, position):
-    """Calibrated HBM bytes per dispatch from the committed rocprofv3 counter
-    summary (lines 'traffic KERNEL POSITION BYTES'); None when that kernel was
-    not measured at this position."""
+    """Calibrated HBM bytes per dispatch of a decode kernel with `position`
+    cached positions (the step writes position - 1), from the committed
+    rocprofv3 counter summary (lines 'traffic KERNEL POSITIONS BYTES').
+    Kernels whose traffic does not depend on the context use their one
+    measurement. The attention stage reads 8 x n x 512 bytes of K/V, so its
+    traffic is linear in n on each attention path (fused up to 512 cached
+    positions, split beyond): the line through the two measurements on the
+    same path is evaluated at n. Returns (bytes, how) or (None, reason)."""
     path = ROOT / 'profiles' / 'decode_hbm_traffic.txt'
     if not path.exists():
-        return None
+        return None, 'no counter summary'
+    points = []
     for line in path.read_text().splitlines():
         parts = line.split()
         if len(parts) == 4 and parts[0] == 'traffic' and parts[1] == kernel:
-            if kernel != 'attention' or int(parts[2]) == position:
-                return float(parts[3])
-    return None
+            points.append((int(parts[2]), float(parts[3])))
+    if kernel != 'attention':
+        return (points[0][1], f'measured at position {points[0][0]}') if points else (None, 'not measured')
+    fused = position <= FUSED_ATTENTION_MAX
+    same = sorted(p for p in points if (p[0] <= FUSED_ATTENTION_MAX) == fused)
+    if any(p[0] == position for p in same):
+        return dict(same)[position], f'measured at position {position}'
+    if len(same) < 2:
+        return None, 'fewer than two measurements on this attention path'
+    (p0, b0), (p1, b1) = same[0], same[-1]
+    return b0 + (b1 - b0) * (position - p0) / (p1 - p0), f'line through positions {p0} and {p1}'
+
+
+def _median_ci(values, seed=0, draws=2000):
+    """Median and a 95% bootstrap interval of the median."""
+    import numpy as np
+    v = np.asarray(values, dtype=np.float64)
+    rng = np.random.default_rng(seed)
+    medians = np.median(rng.choice(v, size=(draws, v.size), replace=True), axis=1)
+    return float(np.median(v)), [float(np.percentile(medians, 2.5)), float(np.percentile(medians, 97.5))]
+
+
+# Prompt, output tokens: the reference's published rows for the 85-, 1024-
+# and 3968-token prompts (32 / 128 / 128 outputs).
+PROTOCOL_CASES = (('85', 'decode_85', 32), ('1024', 'prefill_1024', 128), ('3968', 'long_3968', 128))
+
+
+def generation_protocol(model, ids, outputs, warmups=1, repeats=10):
+    """The reference's request measurement (tools/benchmark_matched.py:39-48,
+    tools/benchmark_native_cpu.py:248-272): per run the model is reset, TTFT
+    is prefill -> first greedy token, then N - 1 greedy steps, and decode is
+    (N - 1) / (t_last - t_first). One unscored warmup, then `repeats` scored
+    runs whose greedy ids must all be the same; medians with 95% bootstrap
+    intervals."""
+    ttft, decode, expected = [], [], None
+    for run in range(warmups + repeats):
+        model.reset()
+        t0 = time.perf_counter()
+        model.prefill(ids)
+        token = model.greedy()
+        t_first = time.perf_counter()
+        produced = [token]
+        for _ in range(outputs - 1):
+            model.step(token)
+            token = model.greedy()
+            produced.append(token)
+        t_last = time.perf_counter()
+        if expected is None:
+            expected = produced
+        elif produced != expected:
+            raise RuntimeError('greedy output changed between runs')
+        if run >= warmups:
+            ttft.append((t_first - t0) * 1e3)
+            decode.append((outputs - 1) / (t_last - t_first))
+    ttft_median, ttft_ci = _median_ci(ttft)
+    decode_median, decode_ci = _median_ci(decode)
+    return dict(prompt_tokens=len(ids), output_tokens=outputs, warmups=warmups, repeats=repeats,
+                ttft_ms_median=ttft_median, ttft_ms_ci95=ttft_ci, decode_tok_s_median=decode_median,
+                decode_tok_s_ci95=decode_ci, ttft_ms=ttft, decode_tok_s=decode)
 
 
 def long_context_decode(model, token, steps=128):
@@ -76,6 +138,7 @@ def long_context_decode(model, token, steps=128):
         token = model.greedy()
     elapsed = time.perf_counter() - start
     n = model.position()
+    assert n == 4096, n
     kernel_ms = {}
     for which in (0, 3, 4, 5, 1):
         kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
@@ -232,6 +295,8 @@ def main():
     parser.add_argument('--no-batch', action='store_true', help='skip the 8-sequence prefix-reuse workload')
     parser.add_argument('--pmc-kernel', choices=KERNELS,
                         help='only run 29 launches of one decode kernel (hardware-counter passes)')
+    parser.add_argument('--pmc-positions', type=int,
+                        help='cached positions for --pmc-kernel (default: where the timed region ends)')
     parser.add_argument('--pmc-prefill', type=int, nargs='?', const=1024, choices=(1024, 3968),
                         help='only run one batched prefill of the 1024- (default) or 3968-token prompt '
                              '(hardware-counter passes)')
@@ -247,8 +312,9 @@ def main():
         q = load_package()
         prompts = json.loads((GOLDEN / 'prompts.json').read_text())
         model = q.Model(q.ensure_random_pack(PACK_CACHE / 'seed0', seed=0), context=4096)
-        position = 85 + args.warmup + args.steps
-        model.prefill(prompts['long_3968'][:position])
+        position = args.pmc_positions or 85 + args.warmup + args.steps
+        prompt = (prompts['long_3968'] + prompts['prefill_1024'])[:position]
+        model.prefill(prompt)
         which = KERNELS.index(args.pmc_kernel)
         ms = model.time_kernel(which, 28)
         model.close()
@@ -323,19 +389,21 @@ def main():
     dominant = max(per_token_ms, key=per_token_ms.get)
     nbytes = attention_bytes(context_end) if dominant == 'attention' else KERNEL_BYTES[dominant]
     achieved = nbytes / (kernel_ms[dominant] * 1e-3) / 1e9
+    # The replays write position context_end - 1 over context_end cached positions.
+    traffic, traffic_source = measured_traffic(dominant, context_end)
     log('kernel ms', kernel_ms)
 
+    protocol, long_context = {}, None
     ttft = {'85': ttft_85}
-    long_context = None
     if not args.no_ttft:
-        for key, name in (('1024', 'prefill_1024'), ('3968', 'long_3968')):
-            model.reset()
-            t0 = time.perf_counter()
-            model.prefill(prompts[name])
-            token = model.greedy()
-            ttft[key] = time.perf_counter() - t0
-            log(f'ttft {key}: {ttft[key]:.4f} s')
-        long_context = long_context_decode(model, token)
+        for key, name, outputs in PROTOCOL_CASES:
+            protocol[key] = generation_protocol(model, prompts[name], outputs)
+            ttft[key] = protocol[key]['ttft_ms_median'] * 1e-3
+            log(f"prompt {key}: TTFT {protocol[key]['ttft_ms_median']:.2f} ms, "
+                f"decode {protocol[key]['decode_tok_s_median']:.0f} tok/s (medians of 10)")
+        model.reset()
+        model.prefill(prompts['long_3968'])
+        long_context = long_context_decode(model, model.greedy())
     batch = None if args.no_batch else prefix_reuse_batch(model, prompts)
     model.close()
     gemv = None if args.no_gemv else gemv_microbench(q)
@@ -362,9 +430,10 @@ def main():
         'decode_hbm_fraction': (weight_bytes + kv_bytes) * decode_tps / 1e9 / HBM_PEAK_GBS,
         'kernel_ms': kernel_ms,
         'roofline': {'kernel': dominant, 'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS,
-                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS,
-                     'traffic': measured_traffic(dominant, context_end),
+                     'unit': 'GB/s', 'frac': achieved / HBM_PEAK_GBS, 'traffic': traffic,
+                     'traffic_source': traffic_source, 'cached_positions': context_end,
                      'bytes_per_launch': nbytes},
+        'reference_protocol': protocol,
         'cpu_baseline': baseline,
         'verification_pair': verification,
         'long_context_decode': long_context,
