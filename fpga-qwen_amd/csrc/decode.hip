@@ -395,9 +395,11 @@ struct AttnArgs {
 // up to kAttnTile = 128 positions (2 passes of 64), with the lane layout of
 // the fused kernel: the 8 lanes of position t score it (lane c = chain c of
 // the reference dot, engine/core.cpp:612) and multiply its V row by both
-// probabilities; each wave keeps its own softmax (max, sum, output) over its
-// positions, and the 8 waves are merged in LDS with weights exp(m_w - max).
-// A single split writes the normalized output; several write (output, max,
+// probabilities. The split's maximum (per head, over the 8 waves' maxima)
+// is shared through LDS first, so every probability is exp(s - max of the
+// split); each wave sums its positions' probabilities and P.V products
+// (the four position groups of a wave folded in registers), and the 8
+// waves' sums are added in LDS in a fixed tree. A single split writes the normalized output; several write (output, max,
 // sum) partials that the merge kernels combine. Every load is issued up
 // front and unconditionally (positions outside the split read row 0 and are
 // masked), in the order the phases need them.
@@ -441,7 +443,7 @@ __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g)
     __shared__ float qp[2][128];
     __shared__ float buf[4][128];
     __shared__ float prob[2][kAttnTile];
-    __shared__ float opart[8][4][2][128];
+    __shared__ __align__(16) float opart[8][2][128];
     __shared__ uint16_t kcur[128], vcur[128];
     __shared__ double red[4][2];
     __shared__ float wmax[8][2], wsum[8][2];
@@ -490,6 +492,20 @@ __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g)
     m1 = fmaxf(m1, xor_lanes<16>(m1));
     m0 = fmaxf(m0, xor_lanes<32>(m0));
     m1 = fmaxf(m1, xor_lanes<32>(m1));
+    // One maximum per head for the whole split: every probability is taken
+    // relative to it, so the waves' partial sums add without rescaling.
+    if (lane == 0) {
+        wmax[wave][0] = m0;
+        wmax[wave][1] = m1;
+    }
+    __syncthreads();
+    m0 = wmax[0][0];
+    m1 = wmax[0][1];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) {
+        m0 = fmaxf(m0, wmax[w][0]);
+        m1 = fmaxf(m1, wmax[w][1]);
+    }
     float l0 = 0.f, l1 = 0.f;
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
@@ -542,30 +558,36 @@ __device__ __forceinline__ void attn_split_body(const AttnArgs& a, int s, int g)
                 }
             }
         }
+    // The wave's four position groups (lanes vcg + 16 vsub) hold partial sums
+    // of the same channels: fold them in registers, then one group writes the
+    // wave's 2 x 128 outputs.
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) opart[wave][vsub][h][vcg * 8 + i] = acc[h][i];
+        for (int i = 0; i < 8; ++i) {
+            acc[h][i] += xor_lanes<16>(acc[h][i]);
+            acc[h][i] += xor_lanes<32>(acc[h][i]);
+        }
+    if (vsub == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 8; i += 4)
+                *reinterpret_cast<float4*>(&opart[wave][h][vcg * 8 + i]) =
+                    make_float4(acc[h][i], acc[h][i + 1], acc[h][i + 2], acc[h][i + 3]);
+    }
     if (lane == 0) {
-        wmax[wave][0] = m0;
-        wmax[wave][1] = m1;
         wsum[wave][0] = l0;
         wsum[wave][1] = l1;
     }
     __syncthreads();
     if (tid < 256) {
         const int h = tid >> 7;
-        float mx = wmax[0][h];
-#pragma unroll
-        for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w][h]);
-        float l = 0.f, o = 0.f;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const float e = wmax[w][h] == -INFINITY ? 0.f : expf(wmax[w][h] - mx);
-            const float ow4 = (opart[w][0][h][j] + opart[w][1][h][j]) + (opart[w][2][h][j] + opart[w][3][h][j]);
-            l = __builtin_fmaf(e, wsum[w][h], l);
-            o = __builtin_fmaf(e, ow4, o);
-        }
+        const float o = ((opart[0][h][j] + opart[1][h][j]) + (opart[2][h][j] + opart[3][h][j])) +
+                        ((opart[4][h][j] + opart[5][h][j]) + (opart[6][h][j] + opart[7][h][j]));
+        const float l = ((wsum[0][h] + wsum[1][h]) + (wsum[2][h] + wsum[3][h])) +
+                        ((wsum[4][h] + wsum[5][h]) + (wsum[6][h] + wsum[7][h]));
+        const float mx = h ? m1 : m0;
         if (ns == 1) {  // nothing to merge: normalize here
             a.attended[(2 * g + h) * 128 + j] = o / l;
             return;
@@ -589,7 +611,9 @@ struct AttnBatch {
     AttnArgs seq[kMaxBatch];
 };
 
-__global__ __launch_bounds__(512) void attn_decode_batch_kernel(const AttnBatch b) {
+// At most 80 VGPRs (6 waves per SIMD): three workgroups share a CU, so the
+// 8-sequence grids (over a thousand workgroups) take fewer rounds.
+__global__ __launch_bounds__(512, 6) void attn_decode_batch_kernel(const AttnBatch b) {
     attn_split_body(b.seq[blockIdx.z], blockIdx.x, blockIdx.y);
 }
 
@@ -707,10 +731,11 @@ __global__ __launch_bounds__(512) void attn_merge_batch_kernel(const AttnBatch b
 // 512 threads, PASSES = ceil(n / 64) passes of 64 positions (a template
 // parameter so that every load is unconditional and the compiler waits for
 // exactly the loads each phase needs). Wave w owns positions 64p + 8w + i,
-// i < 8: its lanes 8i..8i+7 score position i (lane c = chain c), then the
-// wave runs a softmax over its own positions (max m_w, sum l_w) and its P.V
-// with 4 positions x 16 channel groups per load; the 8 waves' partials are
-// merged with weights exp(m_w - max_w m_w), as in a split-softmax merge.
+// i < 8: its lanes 8i..8i+7 score position i (lane c = chain c); the head's
+// maximum over all positions is shared through LDS, then each wave sums the
+// probabilities exp(s - max) and P.V products of its positions (4 positions
+// x 16 channel groups per load, the 4 position groups folded in registers),
+// and the 8 waves' sums are added in LDS in a fixed tree.
 // ROWS = 2 (two-token verification): row q is the step at position pos + q
 // and attends over its pos + q + 1 positions; both rows share every K/V and
 // O load, row 1 takes position pos (row 0's new K/V) from LDS, and each
@@ -779,11 +804,11 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     __shared__ float qp[ROWS][128];
     __shared__ float buf[ROWS][4][128];
     __shared__ float prob[ROWS][kFusedMaxPositions];
-    __shared__ float opart[8][4][128];
+    __shared__ __align__(16) float opart[ROWS][8][128];
     __shared__ __align__(16) float att[ROWS][128];
     __shared__ uint16_t kcur[ROWS][128], vcur[ROWS][128];
     __shared__ double red[ROWS][4][2];
-    __shared__ float wmax[8], wsum[8];
+    __shared__ float wmax[ROWS][8], wsum[ROWS][8];
 
     // QK-norm + RoPE (engine/core.cpp:395-402); one workgroup per KV head
     // (m == 0) writes the new K/V rows (403-406). The others only read rows
@@ -830,8 +855,14 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
         m0 = fmaxf(m0, xor_lanes<8>(m0));
         m0 = fmaxf(m0, xor_lanes<16>(m0));
         m0 = fmaxf(m0, xor_lanes<32>(m0));
-        // Probabilities relative to the wave maximum (a wave without
-        // positions keeps m = -inf and contributes nothing).
+        // The head's maximum over all positions (the 8 waves' maxima through
+        // LDS): every probability is exp(s - max), so the waves' partial sums
+        // add without rescaling.
+        if (lane == 0) wmax[q][wave] = m0;
+        __syncthreads();
+        m0 = wmax[q][0];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) m0 = fmaxf(m0, wmax[q][w]);
         float l0 = 0.f;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
@@ -875,28 +906,27 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
                     }
                 }
             }
-        if (q > 0) __syncthreads();  // the previous row's merge has read opart / wmax / wsum
+        // The wave's four position groups (lanes vcg + 16 vsub) hold partial
+        // sums of the same channels: fold them in registers; one group writes.
 #pragma unroll
-        for (int i = 0; i < 8; ++i) opart[wave][vsub][vcg * 8 + i] = acc[i];
-        if (lane == 0) {
-            wmax[wave] = m0;
-            wsum[wave] = l0;
+        for (int i = 0; i < 8; ++i) {
+            acc[i] += xor_lanes<16>(acc[i]);
+            acc[i] += xor_lanes<32>(acc[i]);
         }
-        __syncthreads();
-        if (tid < 128) {
-            float mx = wmax[0];
-#pragma unroll
-            for (int w = 1; w < 8; ++w) mx = fmaxf(mx, wmax[w]);
-            float l = 0.f, o = 0.f;
-#pragma unroll
-            for (int w = 0; w < 8; ++w) {
-                const float e = wmax[w] == -INFINITY ? 0.f : expf(wmax[w] - mx);
-                const float ow4 = (opart[w][0][tid] + opart[w][1][tid]) + (opart[w][2][tid] + opart[w][3][tid]);
-                l = __builtin_fmaf(e, wsum[w], l);
-                o = __builtin_fmaf(e, ow4, o);
-            }
-            att[q][tid] = o / l;
+        if (vsub == 0) {
+            *reinterpret_cast<float4*>(&opart[q][wave][vcg * 8]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            *reinterpret_cast<float4*>(&opart[q][wave][vcg * 8 + 4]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
         }
+        if (lane == 0) wsum[q][wave] = l0;
+    }
+    __syncthreads();
+    if (tid < 128 * ROWS) {  // the 8 waves' sums in a fixed tree
+        const int q = tid >> 7, ch = tid & 127;
+        const float o = ((opart[q][0][ch] + opart[q][1][ch]) + (opart[q][2][ch] + opart[q][3][ch])) +
+                        ((opart[q][4][ch] + opart[q][5][ch]) + (opart[q][6][ch] + opart[q][7][ch]));
+        const float l = ((wsum[q][0] + wsum[q][1]) + (wsum[q][2] + wsum[q][3])) +
+                        ((wsum[q][4] + wsum[q][5]) + (wsum[q][6] + wsum[q][7]));
+        att[q][ch] = o / l;
     }
     __syncthreads();
 

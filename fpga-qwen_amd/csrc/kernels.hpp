@@ -62,6 +62,7 @@ inline constexpr int kAttnOGroups = kQHeads * (kHidden / kAttnORows);  // 256 wo
 __host__ __device__ inline bool attn_fused(int n) { return n <= kFusedMaxPositions; }
 
 inline constexpr int kMaxBatch = 8;             // sequences per batched decode step
+inline constexpr int kBatchSplitMax = 3;        // K slices of 1024 columns in a batched down projection
 inline constexpr int kBatchRows = 16;           // output rows of one batched-GEMV MFMA tile
 inline constexpr int kBatchLmTiles = 4;         // MFMA tiles per batched lm_head workgroup
 inline constexpr int kBatchLmGroups = kVocab / (kBatchRows * kBatchLmTiles);  // 2374 lm_head workgroups
@@ -95,7 +96,7 @@ struct DecodeScratch {
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
-    float* o_part;        // [16][1024]: per-query-head partial O projections
+    float* o_part;        // [16][1024]: per-query-head partial O projections (batched decode: down K slices)
     float* lm_value;      // [kBatchLmGroups x kMaxBatch] argmax partials (batch-1 uses kLmGroups)
     int* lm_index;
     int* lm_bad;
