@@ -300,6 +300,9 @@ def main():
     parser.add_argument('--pmc-prefill', type=int, nargs='?', const=1024, choices=(1024, 3968),
                         help='only run one batched prefill of the 1024- (default) or 3968-token prompt '
                              '(hardware-counter passes)')
+    parser.add_argument('--pmc-batch', type=int, nargs='?', const=4, metavar='STEPS',
+                        help='only set up the 8-sequence prefix-reuse batch and run STEPS (default 4) batched '
+                             'decode steps after one warmup step (hardware-counter passes)')
     parser.add_argument('--copy-calibration', type=int, metavar='MIB',
                         help='only run a plain device copy of MIB MiB, 5 times (HBM byte-counter calibration)')
     args = parser.parse_args()
@@ -331,6 +334,29 @@ def main():
         token = model.greedy()
         model.close()
         print(json.dumps({'pmc_prefill': args.pmc_prefill, 'seconds': time.perf_counter() - t0, 'token': token}))
+        return 0
+    if args.pmc_batch:
+        from conftest import GOLDEN, PACK_CACHE, load_package
+        q = load_package()
+        prompts = json.loads((GOLDEN / 'prompts.json').read_text())
+        model = q.Model(q.ensure_random_pack(PACK_CACHE / 'seed0', seed=0), context=4096)
+        base = model.share()
+        seqs = [model.share() for _ in prompts['suffix_1536']]
+        try:
+            base.prefill(prompts['prefix_512'])
+            for m, suffix in zip(seqs, prompts['suffix_1536']):
+                m.copy_prefix(base, len(prompts['prefix_512']))
+                m.prefill(suffix)
+            tokens = [m.greedy() for m in seqs]
+            for _ in range(1 + args.pmc_batch):
+                q.step_batch(seqs, tokens)
+                tokens = [m.greedy() for m in seqs]
+            position = seqs[0].position()
+        finally:
+            for m in seqs + [base]:
+                m.close()
+            model.close()
+        print(json.dumps({'pmc_batch_steps': args.pmc_batch, 'sequences': len(seqs), 'position': position}))
         return 0
     if args.copy_calibration:
         from conftest import load_package
