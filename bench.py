@@ -22,14 +22,22 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / 'tests'))
 
 HBM_PEAK_GBS = 8000.0
-KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head']
+# Engine kernel ids (time_kernel): 'ffn' is the fused norm + gate/up +
+# SwiGLU + down kernel that layers 0-26 run; the last layer runs the
+# separate norm+gate/up and down kernels.
+KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head', 'ffn']
+# Launches of each kernel per decode token.
+PER_TOKEN = {'qkv': 28, 'attention': 28, 'gate_up': 1, 'down': 1, 'ffn': 27, 'lm_head': 1}
 # Algorithmic bytes per launch: FP16 weights + FP32 vectors read/written.
 KERNEL_BYTES = {
-    'qkv': 4096 * 1024 * 2 + 1024 * 4 * 2 + 4096 * 4,
+    'qkv': 4096 * 1024 * 2 + 1024 * 4 * 2 + 4096 * 4 + 8 * 1024 * 4,  # + the 8 down slices folded in
     'o': 1024 * 2048 * 2 + 2048 * 4 + 1024 * 4 * 2,
     'gate_up': 6144 * 1024 * 2 + 1024 * 4 * 2 + 3072 * 4,
     'down': 1024 * 3072 * 2 + 3072 * 4 + 1024 * 4 * 2,
     'lm_head': 151936 * 1024 * 2 + 1024 * 4 * 2 + 151936 * 4,
+    # gate/up + down weights, x, norm weights, 16 O partials, xm and the 8
+    # down slices written, the 3072 tagged activations exchanged.
+    'ffn': 6144 * 1024 * 2 + 1024 * 3072 * 2 + 1024 * 4 * 3 + 16 * 1024 * 4 + 8 * 1024 * 4 + 3072 * 8,
 }
 
 
@@ -140,7 +148,7 @@ def long_context_decode(model, token, steps=128):
     n = model.position()
     assert n == 4096, n
     kernel_ms = {}
-    for which in (0, 3, 4, 5, 1):
+    for which in (0, 6, 3, 4, 5, 1):
         kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
     gbs = {k: (attention_bytes(n) if k == 'attention' else KERNEL_BYTES[k]) / (v * 1e-3) / 1e9
            for k, v in kernel_ms.items()}
@@ -408,10 +416,10 @@ def main():
     # the context length reached by the timed region (attention last: timing
     # it resets the model).
     kernel_ms = {}
-    for which in (0, 3, 4, 5, 1):
+    for which in (0, 6, 3, 4, 5, 1):
         kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
     kernel_ms = {name: kernel_ms.get(name) for name in KERNELS}  # 'o' runs with the attention
-    per_token_ms = {k: v * (1 if k == 'lm_head' else 28) for k, v in kernel_ms.items() if v is not None}
+    per_token_ms = {k: v * PER_TOKEN[k] for k, v in kernel_ms.items() if v is not None}
     dominant = max(per_token_ms, key=per_token_ms.get)
     nbytes = attention_bytes(context_end) if dominant == 'attention' else KERNEL_BYTES[dominant]
     achieved = nbytes / (kernel_ms[dominant] * 1e-3) / 1e9

@@ -85,6 +85,8 @@ SIGNATURES = {
                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     'qwen_gpu_op_down_residual': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                  ctypes.c_void_p]),
+    'qwen_gpu_op_fused_ffn': (ctypes.c_int, [ctypes.c_void_p] * 9 + [ctypes.c_uint32, ctypes.c_void_p]),
+    'qwen_gpu_op_norm_qkv_folded': (ctypes.c_int, [ctypes.c_void_p] * 7),
     'qwen_gpu_op_bgemv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemv_time': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
@@ -489,6 +491,47 @@ def down_residual(tiled, act, x, parts=None):
     _check(_LIB.qwen_gpu_op_down_residual(tiled.ptr, ad.ptr, pd.ptr if pd else None, xd.ptr, None))
     synchronize()
     return xd.to_array(np.float32, HIDDEN)
+
+
+class FusedFfn:
+    """The fused decode FFN kernel on caller data (parity-test entry): holds
+    the exchange buffer and the launch tag, as an engine does."""
+
+    def __init__(self):
+        self.exchange = DeviceBuffer.from_array(np.zeros(3072, np.uint64))
+        self.stall = DeviceBuffer.from_array(np.zeros(1, np.int32))
+        self.tag = 0
+
+    def __call__(self, gateup_tiled, down_tiled, norm_weight, x, parts=None):
+        """Returns (xm [1024], dparts [8, 1024], act [3072] as exchanged,
+        stalled)."""
+        nd, xd = _vector(norm_weight, HIDDEN, 'norm_weight'), _vector(x, HIDDEN, 'x')
+        pd = _parts(parts if parts is not None else np.zeros((16, HIDDEN), np.float32))
+        xm, dparts = DeviceBuffer(HIDDEN * 4), DeviceBuffer(8 * HIDDEN * 4)
+        self.tag = self.tag % 0xFFFFFFFF + 1
+        _check(_LIB.qwen_gpu_op_fused_ffn(gateup_tiled.ptr, down_tiled.ptr, nd.ptr, xd.ptr, pd.ptr, xm.ptr, dparts.ptr,
+                                          self.exchange.ptr, self.stall.ptr, self.tag, None))
+        synchronize()
+        words = self.exchange.to_array(np.uint64, 3072)
+        if not np.all((words >> np.uint64(32)) == np.uint64(self.tag)):
+            raise RuntimeError('fused FFN: exchange words do not carry this launch tag')
+        act = (words & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32)
+        stalled = int(self.stall.to_array(np.int32, 1)[0])
+        return (xm.to_array(np.float32, HIDDEN), dparts.to_array(np.float32, 8 * HIDDEN).reshape(8, HIDDEN), act,
+                stalled)
+
+
+def norm_qkv_folded(tiled, norm_weight, xm, dparts):
+    """QKV of a layer after a fused FFN layer: x = xm + the 8 down slices
+    (fixed tree order), qkv = W_qkv . RMSNorm(x). Returns (x, qkv)."""
+    dparts = np.ascontiguousarray(dparts, np.float32)
+    if dparts.shape != (8, HIDDEN):
+        raise ValueError(f'dparts must be [8, 1024], got {dparts.shape}')
+    nd, xmd, dd = _vector(norm_weight, HIDDEN, 'norm_weight'), _vector(xm, HIDDEN, 'xm'), DeviceBuffer.from_array(dparts)
+    xd, out = DeviceBuffer(HIDDEN * 4), DeviceBuffer(4096 * 4)
+    _check(_LIB.qwen_gpu_op_norm_qkv_folded(tiled.ptr, nd.ptr, xmd.ptr, dd.ptr, xd.ptr, out.ptr, None))
+    synchronize()
+    return xd.to_array(np.float32, HIDDEN), out.to_array(np.float32, 4096)
 
 
 def gemm_static(a, w, c=None):

@@ -400,8 +400,10 @@ __global__ __launch_bounds__(1024) void batch_argmax_kernel(const float* __restr
         }
         out.device[b]->token = bi;
         out.device[b]->nonfinite = bad;
+        out.device[b]->stalled = 0;
         out.host[b]->token = bi;
         out.host[b]->nonfinite = bad;
+        out.host[b]->stalled = 0;
     }
 }
 

@@ -343,6 +343,39 @@ int qwen_gpu_op_down_residual(const uint16_t* tiled, const float* act, const flo
     });
 }
 
+int qwen_gpu_op_fused_ffn(const uint16_t* gateup_tiled, const uint16_t* down_tiled, const float* norm_weight,
+                          const float* x, const float* parts, float* xm, float* dparts, uint64_t* exchange, int* stall,
+                          uint32_t tag, void* stream) {
+    return guarded([&] {
+        need(gateup_tiled, "gateup_tiled");
+        need(down_tiled, "down_tiled");
+        need(norm_weight, "norm_weight");
+        need(x, "x");
+        need(parts, "parts");
+        need(xm, "xm");
+        need(dparts, "dparts");
+        need(exchange, "exchange");
+        need(stall, "stall");
+        qwen_hip::launch_fused_ffn(gateup_tiled, down_tiled, norm_weight, x, parts, xm, dparts, exchange, stall, tag,
+                                   static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
+int qwen_gpu_op_norm_qkv_folded(const uint16_t* tiled, const float* norm_weight, const float* xm,
+                                const float* dparts, float* x, float* qkv, void* stream) {
+    return guarded([&] {
+        need(tiled, "tiled");
+        need(norm_weight, "norm_weight");
+        need(xm, "xm");
+        need(dparts, "dparts");
+        need(x, "x");
+        need(qkv, "qkv");
+        qwen_hip::launch_norm_qkv_folded(tiled, norm_weight, xm, dparts, x, qkv, static_cast<hipStream_t>(stream));
+        hip_ok(hipGetLastError());
+    });
+}
+
 int qwen_gpu_op_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,
                                   uint16_t* att_lo, int rows, int pos0, int context, void* stream) {
     return guarded([&] {

@@ -41,6 +41,12 @@ __device__ __forceinline__ float fold_parts(float x, const float (&p)[kOParts]) 
     return x + (lo + hi);
 }
 
+// Residual stream entry xm + the 8 per-slice down products of the fused FFN
+// kernel, summed in a fixed tree order.
+__device__ __forceinline__ float fold_slices(float xm, const float (&d)[kFfnSlices]) {
+    return xm + (((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7])));
+}
+
 // Weights of one 8-row tile for this lane: NB 16-byte blocks. Issued right
 // after the (small) prologue inputs, so the HBM round trip overlaps the
 // prologue.
@@ -89,7 +95,10 @@ struct GemvArgs {
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
 // PARTS (gate/up, down): the residual stream still has the fused attention
-// kernel's 8 partial O projections pending in a.parts.
+// kernel's 16 partial O projections pending in a.parts. PARTS with QKV: the
+// input is the previous layer's s.xm and a.parts holds its 8 down slices;
+// the folded residual is the norm's input and is written to a.x (workgroup
+// b writes entries 4b .. 4b + 3, so a grid of 256 covers all 1024).
 // ROWS input vectors share every weight load: lane (row, chain) keeps one
 // chain per input with the same FMA order, so each row's result is the one
 // a single-row launch gives.
@@ -154,6 +163,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
 #pragma unroll
             for (int g = 0; g < kOParts; ++g) load_f(a.parts + (q * kOParts + g) * kHidden, pin[q][g]);
     }
+    float dsl[ROWS][kFfnSlices][PARTS && MODE == kQKV ? PER : 1];
+    if constexpr (PARTS && MODE == kQKV) {
+        static_assert(PER == 8 && kContig, "QKV folds 8 consecutive entries per thread");
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q)
+#pragma unroll
+            for (int g = 0; g < kFfnSlices; ++g) load_f(a.parts + (q * kFfnSlices + g) * kHidden, dsl[q][g]);
+    }
     float xres[ROWS];  // residual entry of this lane's row (O, down)
 #pragma unroll
     for (int q = 0; q < ROWS; ++q) {
@@ -185,6 +202,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
             }
         }
         if constexpr (PARTS && MODE == kDown) xres[q] = fold_parts(xres[q], prow[q]);
+        if constexpr (PARTS && MODE == kQKV) {
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                float dk[kFfnSlices];
+#pragma unroll
+                for (int g = 0; g < kFfnSlices; ++g) dk[g] = dsl[q][g][k];
+                v[q][k] = fold_slices(v[q][k], dk);
+            }
+            if (tid == int(blockIdx.x >> 1)) {
+                const int h = 4 * (blockIdx.x & 1);
+                *reinterpret_cast<float4*>(a.x + q * kHidden + jbase + h) =
+                    make_float4(v[q][h], v[q][h + 1], v[q][h + 2], v[q][h + 3]);
+            }
+        }
         if constexpr (kNorm) {
             if constexpr (MODE == kQKV) {
                 if (a.embed && blockIdx.x == 0) {  // kept as the residual stream
@@ -333,11 +364,173 @@ __global__ __launch_bounds__(SEG * 32) void gemv_seg_kernel(const GemvArgs a) {
     }
 }
 
+// Exchange between the workgroups of one XCD. A launch's workgroups are
+// dispatched round-robin over the 8 XCDs (workgroup w on XCD w % 8, measured
+// on this chip also right after launches of odd sizes), whose CUs share the
+// XCD's L2. A plain store reaches that L2 (the vector L1 is write-through),
+// and an agent-scope load skips the reader's L1 and finds the line there.
+// (Invalidating L1 with buffer_inv sc0 does not work here: outside
+// thread-group-split mode it leaves the stale line in place.) Each value
+// travels with its launch's tag in one 8-byte store, so a word left by an
+// earlier launch is never taken for a fresh one: placement decides only
+// whether a value arrives, never which value is read. Polls are bounded; a
+// consumer that gives up raises the stall flag, which the step's argmax
+// copies to the host. Measured: 0.40 us per exchange inside an XCD, against
+// 2.37 us per dependent kernel launch.
+constexpr unsigned kExchangeSpins = 1u << 20;
+
+__device__ __forceinline__ void exchange_put(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Two consecutive tagged words; false if they did not both carry `tag`
+// within kExchangeSpins polls.
+__device__ __forceinline__ bool exchange_get2(const uint64_t* p, uint32_t tag, float& a, float& b) {
+    for (unsigned spin = 0; spin < kExchangeSpins; ++spin) {
+        const uint64_t u = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t w = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (uint32_t(u >> 32) == tag && uint32_t(w >> 32) == tag) {
+            a = __uint_as_float(uint32_t(u));
+            b = __uint_as_float(uint32_t(w));
+            return true;
+        }
+    }
+    return false;
+}
+
+struct FfnArgs {
+    const uint16_t* gateup_t;  // chain-tiled gate/up, rows interleaved 4 by 4
+    const uint16_t* down_t;    // chain-tiled down [1024 x 3072]
+    const float* x;            // residual stream before the O partials [ROWS][1024]
+    const float* norm_w;       // post-attention RMSNorm weights
+    const float* parts;        // [ROWS][16][1024] per-query-head O partials
+    float* xm;                 // out: x + folded O partials [ROWS][1024]
+    float* dparts;             // out: [ROWS][8][1024] down products of the 8 activation slices
+    uint64_t* exchange;        // [ROWS][3072] tagged activations
+    int* stall;
+    uint32_t tag;
+};
+
+// Norm + gate/up + SwiGLU + down of one layer in one launch (batch-1
+// decode, engine/core.cpp:627-641). 256 workgroups x 4 waves. Slice g =
+// blockIdx % 8 (one XCD) owns activations 384 g .. 384 g + 383; its 32
+// workgroups (slot s = blockIdx / 8)
+// compute gate/up tiles 96 g + 3 s + w (waves w = 0..2; tile T yields
+// activations 4T..4T+3, wave 3 repeats wave 2's tile and discards it), post
+// the activations to the exchange, and each then multiplies down tiles
+// 4 s + w (rows 32 s + 8 w .. + 7, every wave) over the slice's 384
+// columns. Every gate/up row is the reference's chain-ordered dot
+// (bit-identical to the norm+gate/up kernel); the down row r of slice g is
+// the 8-chain dot over those 384 columns, and the next layer's QKV prologue
+// adds the 8 slices in a fixed tree order. Workgroup b also writes entries
+// 4b .. 4b + 3 of x + O partials to xm (the residual the slices are added
+// to). The down weights are issued before the exchange is polled, so their
+// round trip overlaps the wait.
+template <int ROWS>
+__global__ __launch_bounds__(256) void ffn_kernel(const FfnArgs a) {
+    constexpr int THREADS = 256, PER = kHidden / THREADS;
+    constexpr int kSliceBlocks = kFfnSlice / 64, kDownBlocks = kFFN / 64;
+    static_assert(PER == 4 && kSliceBlocks == 6 && kFfnGroups == 256, "fused FFN shape");
+    __shared__ float4 xs4[ROWS][kHidden / 4];
+    __shared__ float4 as4[ROWS][kFfnSlice / 4];
+    __shared__ double red[ROWS][THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 7, r = lane >> 3;
+    // Slice g = blockIdx % 8: the 32 workgroups of a slice share an XCD.
+    const int g = int(blockIdx.x & 7), slot = int(blockIdx.x >> 3);
+    const int gu_tile = 96 * g + 3 * slot + min(wave, 2);
+    const int down_tile = 4 * slot + wave;
+    const int jbase = PER * tid;
+
+    float v[ROWS][PER], wn[PER], pin[ROWS][kOParts][PER];
+    auto load4 = [&](const float* src, float (&dst)[PER]) {
+        const float4 f = *reinterpret_cast<const float4*>(src + jbase);
+        dst[0] = f.x; dst[1] = f.y; dst[2] = f.z; dst[3] = f.w;
+    };
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) load4(a.x + q * kHidden, v[q]);
+    load4(a.norm_w, wn);
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q)
+#pragma unroll
+        for (int h = 0; h < kOParts; ++h) load4(a.parts + (q * kOParts + h) * kHidden, pin[q][h]);
+
+    u32x4 wv[kHidden / 64];
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile<kHidden>(a.gateup_t, size_t(gu_tile), lane, wv);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            float pk[kOParts];
+#pragma unroll
+            for (int h = 0; h < kOParts; ++h) pk[h] = pin[q][h][k];
+            v[q][k] = fold_parts(v[q][k], pk);
+        }
+        if (tid == int(blockIdx.x))
+            *reinterpret_cast<float4*>(a.xm + q * kHidden + jbase) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+        norm_to_lds<kHidden, THREADS, true>(v[q], wn, reinterpret_cast<float*>(xs4[q]), red[q], nullptr);
+    }
+    __syncthreads();
+
+    // The down weights of this wave's tile over the slice's 6 column blocks.
+    u32x4 dw[kSliceBlocks];
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const u32x4* dp = reinterpret_cast<const u32x4*>(a.down_t) +
+                          (size_t(down_tile) * kDownBlocks + size_t(kSliceBlocks) * g) * 64 + lane;
+#pragma unroll
+        for (int b = 0; b < kSliceBlocks; ++b) dw[b] = __builtin_nontemporal_load(dp + b * 64);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        const float y = tile_dot<kHidden>(wv, reinterpret_cast<const float*>(xs4[q]), lane);
+        // Tile rows 0-3 are gate rows 4T..4T+3, rows 4-7 the matching up rows.
+        const float up = __shfl(y, (lane + 32) & 63);
+        if (wave < 3 && lane < 32 && c == 0) {
+            const float gate = y;
+            const float half_gate = gate * 0.5f;
+            const float t = tanhf(half_gate);
+            exchange_put(a.exchange + q * kFFN + 4 * gu_tile + r, gate * (0.5f + 0.5f * t) * up, a.tag);
+        }
+    }
+
+    // This XCD's 384 activations (two per thread of waves 0-2), permuted for
+    // the chain reads like the GEMV inputs.
+    bool ok = true;
+    if (tid < kFfnSlice / 2) {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            float a0 = 0.f, a1 = 0.f;
+            ok &= exchange_get2(a.exchange + q * kFFN + kFfnSlice * g + 2 * tid, a.tag, a0, a1);
+            float* as = reinterpret_cast<float*>(as4[q]);
+            as[xperm(2 * tid)] = a0;
+            as[xperm(2 * tid + 1)] = a1;
+        }
+    }
+    if (!ok) *a.stall = 1;
+    __syncthreads();
+
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        const float4* as = as4[q];
+        float acc = 0.f;
+#pragma unroll
+        for (int b = 0; b < kSliceBlocks; ++b) acc = chain8(acc, dw[b], as[16 * b + 2 * c], as[16 * b + 2 * c + 1]);
+        const float y = combine_chains(acc);
+        if (c == 0) a.dparts[(q * kFfnSlices + g) * kHidden + 8 * down_tile + r] = y;
+    }
+}
+
 // Second pass of the greedy selection: one workgroup reduces the per-group
 // (max, lowest id, nonfinite) partials of the lm_head kernel.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ value, const int* __restrict__ index,
                                                       const int* __restrict__ bad_in, int groups,
-                                                      ArgmaxResult* result, ArgmaxResult* host_out) {
+                                                      ArgmaxResult* result, ArgmaxResult* host_out, int* stall) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float bv = -INFINITY;
     int bi = INT_MAX, bad = 0;
@@ -367,10 +560,14 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
             bad |= wb[k];
             if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
         }
+        const int stalled = *stall;
+        *stall = 0;
         result->token = bi;
         result->nonfinite = bad;
+        result->stalled = stalled;
         host_out->token = bi;
         host_out->nonfinite = bad;
+        host_out->stalled = stalled;
     }
 }
 
@@ -991,7 +1188,7 @@ void launch_gemv(const GemvArgs& a, int rows, hipStream_t stream) {
         return;
     }
     constexpr int W = gemv_waves<MODE>();
-    if constexpr (MODE == kGateUp || MODE == kDown) {
+    if constexpr (MODE == kGateUp || MODE == kDown || MODE == kQKV) {
         if (a.parts) {
             gemv_kernel<N, W, MODE, true><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
             return;
@@ -1012,13 +1209,38 @@ constexpr int gemv_pair_waves() {
 template <int N, int MODE>
 void launch_gemv_pair(const GemvArgs& a, int rows, hipStream_t stream) {
     constexpr int W = gemv_pair_waves<MODE>();
-    if constexpr (MODE == kGateUp || MODE == kDown) {
+    if constexpr (MODE == kGateUp || MODE == kDown || MODE == kQKV) {
         if (a.parts) {
             gemv_kernel<N, W, MODE, true, 2><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
             return;
         }
     }
     gemv_kernel<N, W, MODE, false, 2><<<rows / (8 * W), 64 * W, 0, stream>>>(a);
+}
+
+template <int ROWS>
+void launch_ffn_rows(const uint16_t* gateup_t, const uint16_t* down_t, const float* norm_w, const float* x,
+                     const float* parts, float* xm, float* dparts, uint64_t* exchange, int* stall, uint32_t tag,
+                     hipStream_t stream) {
+    require(tag != 0, "fused FFN: tag 0 is the cleared exchange");
+    FfnArgs f{};
+    f.gateup_t = gateup_t;
+    f.down_t = down_t;
+    f.x = x;
+    f.norm_w = norm_w;
+    f.parts = parts;
+    f.xm = xm;
+    f.dparts = dparts;
+    f.exchange = exchange;
+    f.stall = stall;
+    f.tag = tag;
+    ffn_kernel<ROWS><<<kFfnGroups, 256, 0, stream>>>(f);
+}
+
+template <int ROWS>
+void launch_ffn(const LayerDevice& L, const float* x, const float* parts, float* xm, float* dparts,
+                uint64_t* exchange, int* stall, uint32_t tag, hipStream_t stream) {
+    launch_ffn_rows<ROWS>(L.gateup_t, L.down_t, L.post_norm, x, parts, xm, dparts, exchange, stall, tag, stream);
 }
 
 }  // namespace
@@ -1047,7 +1269,7 @@ void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, 
 
 void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                         hipStream_t stream) {
+                         LayerFlow flow, hipStream_t stream) {
     switch (which) {
         case 0: {
             GemvArgs q{};
@@ -1058,6 +1280,10 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             q.token[0] = token;
             q.out = s.qkv;
             q.x = s.x;
+            if (flow.fold_input && !embed) {
+                q.in = s.xm;
+                q.parts = s.dparts;
+            }
             launch_gemv<kHidden, kQKV>(q, kQKVRows, stream);
             break;
         }
@@ -1101,6 +1327,10 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
         case 2:  // O runs with the attention (its per-head partials go to o_part)
             break;
         case 3: {
+            if (flow.ffn_tag) {
+                launch_ffn<1>(L, s.x, s.o_part, s.xm, s.dparts, s.exchange, s.stall, flow.ffn_tag, stream);
+                break;
+            }
             GemvArgs gu{};
             gu.w = L.gateup_t;
             gu.in = s.x;
@@ -1111,6 +1341,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             break;
         }
         case 4: {
+            if (flow.ffn_tag) break;  // the fused FFN kernel ran the down projection
             GemvArgs d{};
             d.w = L.down_t;
             d.in = s.act;
@@ -1127,7 +1358,7 @@ bool pair_supported(int pos) { return attn_fused(pos + 2) || !attn_fused(pos + 1
 
 void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int pos, const int (&tokens)[2],
                               const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                              const PairScratch& pr, hipStream_t stream) {
+                              const PairScratch& pr, LayerFlow flow, hipStream_t stream) {
     require(pair_supported(pos) && pos >= 0 && pos + 2 <= context, "verification pair: unsupported position");
     const bool fused = attn_fused(pos + 2);
     GemvArgs q{};
@@ -1140,6 +1371,10 @@ void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int p
     q.out = pr.qkv;
     q.out_stride = kQKVRows;
     q.x = pr.x;
+    if (flow.fold_input && !embed) {
+        q.in = pr.xm;
+        q.parts = pr.dparts;
+    }
     launch_gemv_pair<kHidden, kQKV>(q, kQKVRows, stream);
 
     AttnArgs at{};
@@ -1184,6 +1419,10 @@ void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int p
         }
     }
 
+    if (flow.ffn_tag) {
+        launch_ffn<2>(L, pr.x, pr.o_part, pr.xm, pr.dparts, pr.exchange, s.stall, flow.ffn_tag, stream);
+        return;
+    }
     GemvArgs gu{};
     gu.w = L.gateup_t;
     gu.in = pr.x;
@@ -1219,7 +1458,7 @@ void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const De
     for (int row = 0; row < 2; ++row)
         argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value + row * kLmGroups, s.lm_index + row * kLmGroups,
                                               s.lm_bad + row * kLmGroups, kLmGroups, pr.result + row,
-                                              host_out + row);
+                                              host_out + row, s.stall);
 }
 
 void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
@@ -1251,9 +1490,10 @@ void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm,
 }
 
 void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,
-                         const float* sines, int context, const DecodeScratch& s, hipStream_t stream) {
+                         const float* sines, int context, const DecodeScratch& s, LayerFlow flow, hipStream_t stream) {
     for (int which = 0; which < 5; ++which)
-        launch_layer_kernel(which, L, which == 0 ? embed : nullptr, pos, token, cosines, sines, context, s, stream);
+        launch_layer_kernel(which, L, which == 0 ? embed : nullptr, pos, token, cosines, sines, context, s, flow,
+                            stream);
 }
 
 void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, ArgmaxResult* host_out,
@@ -1268,7 +1508,7 @@ void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeS
     a.lm_index = s.lm_index;
     a.lm_bad = s.lm_bad;
     gemv_kernel<kHidden, kLmWaves, kLmHead><<<kLmGroups, 64 * kLmWaves, 0, stream>>>(a);
-    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, host_out);
+    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, host_out, s.stall);
 }
 
 void launch_norm_qkv(const uint16_t* qkv_t, const float* norm_w, const float* x, float* qkv, hipStream_t stream) {
@@ -1290,6 +1530,24 @@ void launch_norm_gate_up(const uint16_t* gateup_t, const float* norm_w, const fl
     gu.parts = parts;
     gu.out = act;
     launch_gemv<kHidden, kGateUp>(gu, 2 * kFFN, stream);
+}
+
+void launch_fused_ffn(const uint16_t* gateup_t, const uint16_t* down_t, const float* norm_w, const float* x,
+                      const float* parts, float* xm, float* dparts, uint64_t* exchange, int* stall, uint32_t tag,
+                      hipStream_t stream) {
+    launch_ffn_rows<1>(gateup_t, down_t, norm_w, x, parts, xm, dparts, exchange, stall, tag, stream);
+}
+
+void launch_norm_qkv_folded(const uint16_t* qkv_t, const float* norm_w, const float* xm, const float* dparts,
+                            float* x, float* qkv, hipStream_t stream) {
+    GemvArgs q{};
+    q.w = qkv_t;
+    q.in = xm;
+    q.parts = dparts;
+    q.norm_w = norm_w;
+    q.out = qkv;
+    q.x = x;
+    launch_gemv<kHidden, kQKV>(q, kQKVRows, stream);
 }
 
 void launch_down_residual(const uint16_t* down_t, const float* act, const float* parts, float* x,

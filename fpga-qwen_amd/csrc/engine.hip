@@ -4,7 +4,9 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
+#include <string>
 
 #include "batch.hpp"
 #include "pack.hpp"
@@ -186,6 +188,10 @@ void Engine::init_state() {
     s.lm_index = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
     s.lm_bad = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
     s.result = device_alloc<ArgmaxResult>(1);
+    s.xm = device_alloc<float>(kHidden);
+    s.dparts = device_alloc<float>(size_t(kFfnSlices) * kHidden);
+    s.exchange = device_alloc<uint64_t>(kFFN);
+    s.stall = device_alloc<int>(1);
     ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
     ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
     base_logits_ = device_alloc<float>(kVocab);
@@ -197,6 +203,14 @@ void Engine::init_state() {
     pair_.logits = ver_logits_;
     pair_.hidden = ver_hidden_;
     pair_.result = device_alloc<ArgmaxResult>(2);
+    pair_.xm = device_alloc<float>(2 * kHidden);
+    pair_.dparts = device_alloc<float>(size_t(2) * kFfnSlices * kHidden);
+    pair_.exchange = device_alloc<uint64_t>(2 * kFFN);
+    // Exchange words start with tag 0, which no launch uses.
+    HIP_CHECK(hipMemsetAsync(s.exchange, 0, kFFN * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(pair_.exchange, 0, 2 * kFFN * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(s.stall, 0, sizeof(int), stream_));
+    if (const char* env = std::getenv("QWEN_HIP_FUSED_FFN")) fused_ffn_ = std::string(env) != "0";
     penalized_ = device_alloc<uint8_t>(kVocab);
     top_scratch_ = device_alloc<uint8_t>(top_scores_scratch_bytes());
     top_device_ = device_alloc<TopScores>(1);
@@ -270,10 +284,27 @@ void Engine::truncate(int position) {
 // One token through the 28 layers (5 kernels each) and, when `head`, the
 // final norm, tied lm_head and greedy argmax into host result slot
 // `result_slot`. The step scalars are kernel arguments.
+LayerFlow Engine::layer_flow(int layer) {
+    LayerFlow f{};
+    f.fold_input = fused_ffn_ && layer > 0;
+    if (fused_ffn_ && layer < kLayers - 1) {  // the last layer writes the residual the head reads
+        if (++ffn_tag_ == 0) ++ffn_tag_;
+        f.ffn_tag = ffn_tag_;
+    }
+    return f;
+}
+
+// A fused FFN launch whose exchange poll gave up leaves garbage in the
+// residual stream; the argmax of the step reports it.
+void Engine::check_stall(int slot) const {
+    if (result_host_[slot].stalled)
+        throw std::runtime_error("Decode step stalled: a fused FFN exchange did not complete");
+}
+
 void Engine::run_token(int token, bool head, int result_slot) {
     for (int l = 0; l < kLayers; ++l)
         launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, pos_, token, cosines_, sines_, options_.context,
-                            scratch_, stream_);
+                            scratch_, layer_flow(l), stream_);
     if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
     HIP_CHECK(hipGetLastError());
     ++pos_;
@@ -310,6 +341,7 @@ void Engine::append(const int* ids, size_t count) {
     if (batched < count) run_token(ids[count - 1], true, 0);
     HIP_CHECK(hipGetLastError());
     sync();
+    check_stall(0);
     has_logits_ = true;
 }
 
@@ -403,7 +435,7 @@ void Engine::run_pair(int first, int second) {
     const int tokens[2] = {first, second};
     for (int l = 0; l < kLayers; ++l)
         launch_decode_layer_pair(layers_[l], l == 0 ? embed_ : nullptr, pos_, tokens, cosines_, sines_,
-                                 options_.context, scratch_, pair_, stream_);
+                                 options_.context, scratch_, pair_, layer_flow(l), stream_);
     launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, stream_);
     HIP_CHECK(hipGetLastError());
 }
@@ -443,6 +475,8 @@ void Engine::verify_two(int first, int second) {
             }
         }
         sync();
+        check_stall(1);
+        check_stall(2);
         pos_ = start;
         pending_ = true;
         ver_host_valid_ = false;
@@ -529,22 +563,29 @@ void Engine::commit_verified(int count) {
 float Engine::time_kernel(int which, int iterations) {
     require(pos_ > 0 && !pending_, "time_kernel needs a current position");
     HIP_CHECK(hipStreamSynchronize(stream_));
-    require(which >= 0 && which <= 5 && iterations > 0, "time_kernel: bad arguments");
+    require(which >= 0 && which <= 6 && iterations > 0, "time_kernel: bad arguments");
     if (which == 2) return 0.f;  // O runs with the attention (1)
+    require(which != 6 || fused_ffn_, "time_kernel: the fused FFN kernel is switched off");
     // Replays kernels of the last processed position; the state is reset
     // afterwards. Layer kernels rotate over all 28 layers so that, as in a
     // real step, their weights (about 880 MB in total) stream from HBM rather
     // than from the 256 MB Infinity Cache.
+    // 3 and 4 time the norm+gate/up and down kernels (every layer; with the
+    // fused FFN on, a step runs them only in the last layer), 6 the fused
+    // FFN kernel (layers 0-26).
+    const int layers = which == 6 ? kLayers - 1 : kLayers;
     int layer = 0;
     auto launch = [&] {
+        LayerFlow flow = layer_flow(layer);
+        if (which == 3 || which == 4) flow.ffn_tag = 0;
         if (which == 5)
             launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
         else
-            launch_layer_kernel(which, layers_[layer], nullptr, pos_ - 1, 0, cosines_, sines_, options_.context,
-                                scratch_, stream_);
-        layer = (layer + 1) % kLayers;
+            launch_layer_kernel(which == 6 ? 3 : which, layers_[layer], nullptr, pos_ - 1, 0, cosines_, sines_,
+                                options_.context, scratch_, flow, stream_);
+        layer = (layer + 1) % layers;
     };
-    for (int i = 0; i < kLayers; ++i) launch();
+    for (int i = 0; i < layers; ++i) launch();
     hipEvent_t start, stop;
     HIP_CHECK(hipEventCreate(&start));
     HIP_CHECK(hipEventCreate(&stop));

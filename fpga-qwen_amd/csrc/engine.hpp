@@ -93,6 +93,8 @@ private:
     void append(const int* ids, size_t count);
     void run_token(int token, bool head, int result_slot);
     void run_pair(int first, int second);
+    LayerFlow layer_flow(int layer);
+    void check_stall(int slot) const;
     void release();
     void sync();
     void invalidate();
@@ -125,6 +127,11 @@ private:
     float* ver_host_ = nullptr;     // pinned [2 x vocab] logits then [2 x 1024] hidden
     bool ver_host_valid_ = false;
     int pos_ = 0;
+    // Layers 0-26 run the fused FFN kernel (norm + gate/up + SwiGLU + down
+    // slices in one launch) unless QWEN_HIP_FUSED_FFN=0; every fused launch
+    // takes the next tag (never 0, the cleared exchange).
+    bool fused_ffn_ = true;
+    uint32_t ffn_tag_ = 0;
     bool has_logits_ = false;
     bool pending_ = false;
     std::vector<float> host_logits_, host_hidden_;

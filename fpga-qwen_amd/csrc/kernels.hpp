@@ -32,6 +32,7 @@ __host__ __device__ constexpr int kperm(int j) { return (j & ~63) | ((j & 7) << 
 struct ArgmaxResult {
     int token;
     int nonfinite;
+    int stalled;  // a fused FFN launch of this step gave up waiting for an exchange
 };
 
 inline constexpr int kAttnSplits = 32;          // max position splits per KV head
@@ -101,7 +102,18 @@ struct DecodeScratch {
     int* lm_index;
     int* lm_bad;
     ArgmaxResult* result; // [1] device copy of the selection
+    float* xm;            // [1024] residual after the O partials (written by the fused FFN kernel)
+    float* dparts;        // [8][1024] down products of the 8 activation slices (fused FFN kernel)
+    uint64_t* exchange;   // [3072] activations with their launch tag, exchanged inside each XCD
+    int* stall;           // nonzero once a fused FFN poll gave up (cleared by the argmax kernel)
 };
+
+// The fused FFN kernel (norm + gate/up + SwiGLU + down in one launch): XCD
+// g computes activations 384 g .. 384 g + 383 and their share of the down
+// product; the 8 shares are added by the next layer's QKV prologue.
+inline constexpr int kFfnSlices = 8;
+inline constexpr int kFfnSlice = kFFN / kFfnSlices;  // 384 activations per XCD
+inline constexpr int kFfnGroups = 256;               // workgroups (32 per XCD)
 
 // Layout conversion: natural row-major FP16 [rows x cols] -> chain-tiled.
 // When `second` is non-null the tiles interleave two matrices of equal shape:
@@ -121,16 +133,27 @@ void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, 
 // pos is the position being written (n = pos + 1 cached positions after
 // it); when `embed` is non-null (first layer) x is first loaded from
 // embed[token]. Step scalars travel as kernel arguments.
+// How a layer hands its residual stream on. fold_input: the previous layer
+// ran the fused FFN kernel, so QKV reads s.xm plus the 8 down slices and
+// writes their sum to s.x. ffn_tag != 0: this layer runs the fused FFN kernel
+// (that tag must differ from the previous fused launch's on these buffers);
+// 0: the norm+gate/up and down kernels.
+struct LayerFlow {
+    bool fold_input;
+    uint32_t ffn_tag;
+};
+
 void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                         hipStream_t stream);
+                         LayerFlow flow, hipStream_t stream);
 
 // One stage of a decode layer: 0 norm+QKV, 1 attention with the O partials
 // (one kernel up to kFusedMaxPositions, split + merge/O beyond), 2 nothing
-// (O runs with the attention), 3 norm+gate/up, 4 down.
+// (O runs with the attention), 3 norm+gate/up (the fused FFN kernel when
+// flow.ffn_tag != 0), 4 down (nothing after a fused FFN launch).
 void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                         hipStream_t stream);
+                         LayerFlow flow, hipStream_t stream);
 
 // Buffers of a two-token verification (rows at positions pos and pos + 1).
 struct PairScratch {
@@ -141,6 +164,9 @@ struct PairScratch {
     float* logits;        // [2][151936]
     float* hidden;        // [2][1024]
     ArgmaxResult* result; // [2] device copies of the selections
+    float* xm;            // [2][1024]
+    float* dparts;        // [2][8][1024]
+    uint64_t* exchange;   // [2][3072]
 };
 
 // True when the steps at pos and pos + 1 take the same attention path
@@ -154,7 +180,7 @@ bool pair_supported(int pos);
 // single steps. Writes K/V at pos and pos + 1.
 void launch_decode_layer_pair(const LayerDevice& layer, const uint16_t* embed, int pos, const int (&tokens)[2],
                               const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                              const PairScratch& pair, hipStream_t stream);
+                              const PairScratch& pair, LayerFlow flow, hipStream_t stream);
 
 // Final norm + lm_head + greedy argmax of both verification rows (uses the
 // lm partial buffers of s); selections to pair.result and host_out[0..1].
@@ -192,6 +218,18 @@ void launch_norm_gate_up(const uint16_t* gateup_t, const float* norm_w, const fl
 // x[r] = (x[r] + folded O partials of row r) + W_down[r] . act (two-segment chains).
 void launch_down_residual(const uint16_t* down_t, const float* act, const float* parts, float* x,
                           hipStream_t stream);
+// The fused FFN kernel of one layer: xm = x + folded O partials (parts
+// [16][1024]), act = SwiGLU(gate/up . RMSNorm(xm)) posted to exchange[3072]
+// with `tag`, dparts[g][r] = W_down[r][384 g .. 384 g + 383] . act[same]
+// (8-chain dot over the slice). The exchange must hold no word with `tag`
+// (zeroed, or last written with another tag); stall is set if a poll gave up.
+void launch_fused_ffn(const uint16_t* gateup_t, const uint16_t* down_t, const float* norm_w, const float* x,
+                      const float* parts, float* xm, float* dparts, uint64_t* exchange, int* stall, uint32_t tag,
+                      hipStream_t stream);
+// qkv = W_qkv . RMSNorm(x) with x = xm + the 8 down slices dparts[8][1024]
+// added in the fixed tree order; x is also written out.
+void launch_norm_qkv_folded(const uint16_t* qkv_t, const float* norm_w, const float* xm, const float* dparts,
+                            float* x, float* qkv, hipStream_t stream);
 
 // Plain device copy (bytes a multiple of 16), for counter calibration.
 void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);

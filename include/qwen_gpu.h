@@ -193,6 +193,26 @@ int qwen_gpu_op_norm_gate_up(const uint16_t* tiled, const float* norm_weight, co
  * W_down[r] . act, W_down [1024 x 3072] (engine/core.cpp:640-641: project,
  * then the residual add). */
 int qwen_gpu_op_down_residual(const uint16_t* tiled, const float* act, const float* parts, float* x, void* stream);
+/* The FFN of one layer as the fused decode kernel runs it
+ * (engine/core.cpp:625-641, with the down projection split into 8 column
+ * slices): xm = x + the 16 O partials parts[16][1024] (fixed tree order);
+ * act = SwiGLU(W_gate . h, W_up . h), h = RMSNorm(xm), posted to
+ * exchange[3072] as (tag << 32 | FP32 bits); dparts[g][r] = W_down[r][384 g
+ * .. 384 g + 383] . act[384 g .. 384 g + 383] (the reference's 8-chain dot
+ * over that slice), g < 8. The next layer adds xm + the 8 slices (see
+ * qwen_gpu_op_norm_qkv_folded). exchange must hold no word carrying tag
+ * (zero it once; tag != 0 and different from the previous call's); *stall
+ * is set nonzero if a workgroup gave up waiting for the slice's
+ * activations. Parity-test entry. */
+int qwen_gpu_op_fused_ffn(const uint16_t* gateup_tiled, const uint16_t* down_tiled, const float* norm_weight,
+                          const float* x, const float* parts, float* xm, float* dparts, uint64_t* exchange, int* stall,
+                          uint32_t tag, void* stream);
+/* qkv[4096] = W_qkv . RMSNorm(x) where x = xm + the 8 down slices
+ * dparts[8][1024] added in the fixed tree order ((d0+d1)+(d2+d3)) +
+ * ((d4+d5)+(d6+d7)); x[1024] is written out (engine/core.cpp:641 then
+ * 384-386). Parity-test entry. */
+int qwen_gpu_op_norm_qkv_folded(const uint16_t* tiled, const float* norm_weight, const float* xm,
+                                const float* dparts, float* x, float* qkv, void* stream);
 /* Causal GQA attention of a prefill chunk (engine/core.cpp:407-605, the
  * batched rows' attention): rows queries at positions pos0 .. pos0 + rows - 1
  * from qkv FP32 [rows x 4096] (columns 0..2047: 16 query heads of 128),
@@ -221,11 +241,12 @@ int qwen_gpu_op_gemv_time(const uint16_t* tiled, size_t copy_stride, int copies,
 int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream);
 /* Average milliseconds of one standalone launch of a decode kernel on the
  * model's stream, timed with HIP events (which: 0 norm+QKV, 1 attention,
- * 2 O, 3 norm+gate/up, 4 down, 5 lm_head). Needs position() > 0. The O
- * projection runs with the attention (timed as 1: one kernel up to 512
- * positions, split attention + merge/O beyond) and 2 reports 0. Afterwards
- * the current logits are invalid; timing the attention (1) also resets the
- * model, so time it last. */
+ * 2 O, 3 norm+gate/up, 4 down, 5 lm_head, 6 the fused FFN kernel that layers
+ * 0-26 run in place of 3 and 4). Needs position() > 0. The O projection
+ * runs with the attention (timed as 1: one kernel up to 512 positions, split
+ * attention + merge/O beyond) and 2 reports 0. Afterwards the current
+ * logits are invalid; timing the attention (1) also resets the model, so
+ * time it last. */
 int qwen_gpu_time_kernel(qwen_gpu_model* model, int which, int iterations, float* milliseconds);
 
 #ifdef __cplusplus

@@ -123,3 +123,58 @@ def test_down_residual_bit_exact(qpkg, oracle_lib, with_parts):
     base = _fold_parts(x, parts) if with_parts else x
     expected = base + oracle_lib.gemv(w, act, threads=16)
     _assert_same_bits(got, expected, 'x')
+
+
+def _fold_slices(xm, d):
+    """xm + the 8 per-slice down products in the engine's fixed tree order
+    ((d0+d1)+(d2+d3))+((d4+d5)+(d6+d7)), FP32 throughout."""
+    d = np.asarray(d, np.float32)
+    return np.asarray(xm, np.float32) + (((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7])))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('with_parts', [False, True])
+def test_fused_ffn_slices_bit_exact(qpkg, oracle_lib, with_parts):
+    """The fused FFN kernel (norm + gate/up + SwiGLU + down in one launch,
+    engine/core.cpp:625-641 with the down projection split into 8 column
+    slices exchanged inside each XCD): xm is x plus the folded O partials bit
+    for bit; the activations it exchanges are the norm+gate/up kernel's bit
+    for bit; slice g's down product is the oracle's chain-ordered dot over
+    columns 384g .. 384g + 383 bit for bit; and the folded slices lie within
+    the FP32 accumulation bound of the whole product in FP64 (a slice taken
+    from the wrong columns or rows fails all three). Two calls in a row
+    reuse the exchange with a new tag."""
+    rng, gate, x, norm_w, parts = _decode_inputs(16 + with_parts, 3072, 1024)
+    up = (rng.standard_normal((3072, 1024), dtype=np.float32) * 0.02).astype(np.float16)
+    down = (rng.standard_normal((1024, 3072), dtype=np.float32) * 0.02).astype(np.float16)
+    gu_t, down_t = qpkg.tile_matrix(gate, up), qpkg.tile_matrix(down)
+    ffn = qpkg.FusedFfn()
+    p = parts if with_parts else None
+    act_ref, _, _ = qpkg.norm_gate_up(gu_t, norm_w, x, p)
+    for call in range(2):
+        xm, dparts, act, stalled = ffn(gu_t, down_t, norm_w, x, p)
+        assert stalled == 0
+        _assert_same_bits(xm, _fold_parts(x, parts if with_parts else np.zeros((16, 1024), np.float32)), 'xm')
+        _assert_same_bits(act, act_ref, 'act')
+        for g in range(8):
+            cols = slice(384 * g, 384 * (g + 1))
+            expected = oracle_lib.gemv(np.ascontiguousarray(down[:, cols]), np.ascontiguousarray(act[cols]), threads=16)
+            _assert_same_bits(dparts[g], expected, f'down slice {g}')
+        total = _fold_slices(np.zeros(1024, np.float32), dparts).astype(np.float64)
+        ref = down.astype(np.float64) @ act.astype(np.float64)
+        bound = 1e-5 * (np.abs(down.astype(np.float64)) @ np.abs(act.astype(np.float64))) + 1e-7
+        assert np.all(np.abs(total - ref) <= bound), float((np.abs(total - ref) / bound).max())
+
+
+@pytest.mark.gpu
+def test_norm_qkv_folded_bit_exact(qpkg, oracle_lib):
+    """QKV after a fused FFN layer: the residual is xm plus the 8 down slices
+    in the fixed tree order (written out bit for bit), then the oracle's norm
+    and chain-ordered GEMV over the stacked q/k/v rows (engine/core.cpp:641,
+    384-386)."""
+    rng, w, xm, norm_w, _ = _decode_inputs(18, 4096, 1024)
+    d = (0.05 * rng.standard_normal((8, 1024), dtype=np.float32)).astype(np.float32)
+    x, qkv = qpkg.norm_qkv_folded(qpkg.tile_matrix(w), norm_w, xm, d)
+    xf = _fold_slices(xm, d)
+    _assert_same_bits(x, xf, 'x')
+    _assert_same_bits(qkv, oracle_lib.gemv(w, oracle_lib.norm(xf, norm_w), threads=16), 'qkv')

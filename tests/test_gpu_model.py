@@ -76,6 +76,33 @@ def test_repeat_is_bit_identical(gpu_model):
 
 
 @pytest.mark.gpu
+def test_fused_ffn_path_matches_two_kernel_path(qpkg, pack0, gpu_model, monkeypatch):
+    """Layers 0-26 run the fused FFN kernel, whose down projection is 8
+    column slices added by the next layer; QWEN_HIP_FUSED_FFN=0 selects the
+    two-kernel path (norm+gate/up, then down as the reference's dot over all
+    3072 columns). Along greedy trajectories after the 85-token prompt (fused
+    attention) and an 1100-token prompt (split attention) both paths choose
+    the same tokens and their logits agree to 1e-4: the slice sums move each
+    down output by a few FP32 ulps, nothing more (a wrong slice, row or
+    fold would move them by the size of the product, ~1e-1)."""
+    monkeypatch.setenv('QWEN_HIP_FUSED_FFN', '0')
+    plain = qpkg.Model(pack0, context=4096)
+    monkeypatch.delenv('QWEN_HIP_FUSED_FFN')
+    try:
+        for prompt in (PROMPTS['decode_85'], PROMPTS['long_3968'][:1100]):
+            fused_rows = greedy_trajectory(gpu_model, prompt, 12)
+            plain_rows = greedy_trajectory(plain, prompt, 12)
+            worst = 0.0
+            for (lf, tf), (lp, tp) in zip(fused_rows, plain_rows):
+                assert tf == tp
+                worst = max(worst, float(np.max(np.abs(lf - lp))))
+            print(f'prompt {len(prompt)}: fused vs two-kernel max |d logit| {worst:.3e}')
+            assert worst <= 1e-4
+    finally:
+        plain.close()
+
+
+@pytest.mark.gpu
 def test_prefill_equals_steps_and_truncate(gpu_model):
     """Token-at-a-time equivalence and rewind: KV before the cut is retained."""
     prompt = PROMPTS['decode_85'][:12]
