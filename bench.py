@@ -22,12 +22,14 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / 'tests'))
 
 HBM_PEAK_GBS = 8000.0
-# Engine kernel ids (time_kernel): 'ffn' is the fused norm + gate/up +
-# SwiGLU + down kernel that layers 0-26 run; the last layer runs the
-# separate norm+gate/up and down kernels.
-KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head', 'ffn']
+# Engine kernel ids (time_kernel). A decode step runs 'qkv_attention' (norm
+# + QKV + attention + O in one kernel) in every layer, 'ffn' (norm + gate/up
+# + SwiGLU + down) in layers 0-26 and the separate 'gate_up' and 'down'
+# kernels in the last layer; 'qkv' and 'attention' are the separate kernels
+# the fused one replaces (timed for comparison, not run by a step).
+KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head', 'ffn', 'qkv_attention']
 # Launches of each kernel per decode token.
-PER_TOKEN = {'qkv': 28, 'attention': 28, 'gate_up': 1, 'down': 1, 'ffn': 27, 'lm_head': 1}
+PER_TOKEN = {'qkv_attention': 28, 'ffn': 27, 'gate_up': 1, 'down': 1, 'lm_head': 1}
 # Algorithmic bytes per launch: FP16 weights + FP32 vectors read/written.
 KERNEL_BYTES = {
     'qkv': 4096 * 1024 * 2 + 1024 * 4 * 2 + 4096 * 4 + 8 * 1024 * 4,  # + the 8 down slices folded in
@@ -59,15 +61,41 @@ def attention_bytes(n):
     return base + 2 * 8 * splits * 264 * 4
 
 
+def kernel_bytes(kernel, n):
+    """Algorithmic bytes of one launch with n cached positions."""
+    if kernel == 'attention':
+        return attention_bytes(n)
+    if kernel == 'qkv_attention':
+        # QKV and O weights, K/V rows, residual (+ the 8 down slices) in and
+        # out, norm weights, the 16 partial O projections written.
+        return (4096 * 1024 * 2 + 1024 * 2048 * 2 + 8 * n * 128 * 2 * 2 + 1024 * 4 * (2 + 8) + 1024 * 4
+                + 16 * 1024 * 4)
+    return KERNEL_BYTES[kernel]
+
+
+def kernel_replays(model, history, iterations=224):
+    """Average duration of each decode kernel at the model's position (HIP
+    events on the engine stream, launches rotating over the layers). Timing
+    an attention kernel rewrites cached K/V and resets the model, so the
+    context `history` is prefilled again before the fused one."""
+    kernel_ms = {}
+    for which in (0, 6, 3, 4, 5, 1):
+        kernel_ms[KERNELS[which]] = model.time_kernel(which, iterations)
+    model.prefill(history)
+    kernel_ms['qkv_attention'] = model.time_kernel(7, iterations)
+    return kernel_ms
+
+
 def measured_traffic(kernel, position):
     """Calibrated HBM bytes per dispatch of a decode kernel with `position`
     cached positions (the step writes position - 1), from the committed
     rocprofv3 counter summary (lines 'traffic KERNEL POSITIONS BYTES').
     Kernels whose traffic does not depend on the context use their one
-    measurement. The attention stage reads 8 x n x 512 bytes of K/V, so its
-    traffic is linear in n on each attention path (fused up to 512 cached
-    positions, split beyond): the line through the two measurements on the
-    same path is evaluated at n. Returns (bytes, how) or (None, reason)."""
+    measurement. The attention stages read 8 x n x 512 bytes of K/V, so their
+    traffic is linear in n on each path (the separate attention kernels:
+    fused up to 512 cached positions, split beyond; the fused QKV +
+    attention kernel: one path): the line through the two measurements on
+    the same path is evaluated at n. Returns (bytes, how) or (None, reason)."""
     path = ROOT / 'profiles' / 'decode_hbm_traffic.txt'
     if not path.exists():
         return None, 'no counter summary'
@@ -76,10 +104,10 @@ def measured_traffic(kernel, position):
         parts = line.split()
         if len(parts) == 4 and parts[0] == 'traffic' and parts[1] == kernel:
             points.append((int(parts[2]), float(parts[3])))
-    if kernel != 'attention':
+    if kernel not in ('attention', 'qkv_attention'):
         return (points[0][1], f'measured at position {points[0][0]}') if points else (None, 'not measured')
     fused = position <= FUSED_ATTENTION_MAX
-    same = sorted(p for p in points if (p[0] <= FUSED_ATTENTION_MAX) == fused)
+    same = sorted(p for p in points if kernel == 'qkv_attention' or (p[0] <= FUSED_ATTENTION_MAX) == fused)
     if any(p[0] == position for p in same):
         return dict(same)[position], f'measured at position {position}'
     if len(same) < 2:
@@ -136,22 +164,23 @@ def generation_protocol(model, ids, outputs, warmups=1, repeats=10):
                 decode_tok_s_ci95=decode_ci, ttft_ms=ttft, decode_tok_s=decode)
 
 
-def long_context_decode(model, token, steps=128):
+def long_context_decode(model, prompt, steps=128):
     """128 greedy steps after the 3968-token prompt (positions 3968..4095),
-    then per-stage times at the full 4096 context (attention: split
-    attention + merge/O kernels)."""
+    then per-kernel times at the full 4096 context."""
+    model.reset()
+    model.prefill(prompt)
+    token = model.greedy()
+    history = list(prompt)
     start = time.perf_counter()
     for _ in range(steps):
         model.step(token)
+        history.append(token)
         token = model.greedy()
     elapsed = time.perf_counter() - start
     n = model.position()
     assert n == 4096, n
-    kernel_ms = {}
-    for which in (0, 6, 3, 4, 5, 1):
-        kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
-    gbs = {k: (attention_bytes(n) if k == 'attention' else KERNEL_BYTES[k]) / (v * 1e-3) / 1e9
-           for k, v in kernel_ms.items()}
+    kernel_ms = kernel_replays(model, history)
+    gbs = {k: kernel_bytes(k, n) / (v * 1e-3) / 1e9 for k, v in kernel_ms.items()}
     log(f'long-context decode {steps / elapsed:.1f} tok/s')
     return {'prompt_tokens': 3968, 'steps': steps, 'decode_tok_s': steps / elapsed, 'context_end': n,
             'kernel_ms': kernel_ms, 'kernel_gbs': gbs}
@@ -396,8 +425,10 @@ def main():
     model.prefill(prompt)
     token = model.greedy()
     ttft_85 = time.perf_counter() - t0
+    history = list(prompt)  # every id the model has consumed
     for _ in range(args.warmup):
         model.step(token)
+        history.append(token)
         token = model.greedy()
     log('warmup done')
     # Timed region: exactly K greedy steps; each step returns after the device
@@ -405,6 +436,7 @@ def main():
     start = time.perf_counter()
     for _ in range(args.steps):
         model.step(token)
+        history.append(token)
         token = model.greedy()
     elapsed = time.perf_counter() - start
     decode_tps = args.steps / elapsed
@@ -413,15 +445,12 @@ def main():
     verification = verification_pairs(model, token)
 
     # Per-kernel average durations with HIP events on the engine stream, at
-    # the context length reached by the timed region (attention last: timing
-    # it resets the model).
-    kernel_ms = {}
-    for which in (0, 6, 3, 4, 5, 1):
-        kernel_ms[KERNELS[which]] = model.time_kernel(which, 224)
+    # the context length reached by the timed region.
+    kernel_ms = kernel_replays(model, history)
     kernel_ms = {name: kernel_ms.get(name) for name in KERNELS}  # 'o' runs with the attention
-    per_token_ms = {k: v * PER_TOKEN[k] for k, v in kernel_ms.items() if v is not None}
+    per_token_ms = {k: v * PER_TOKEN[k] for k, v in kernel_ms.items() if v is not None and k in PER_TOKEN}
     dominant = max(per_token_ms, key=per_token_ms.get)
-    nbytes = attention_bytes(context_end) if dominant == 'attention' else KERNEL_BYTES[dominant]
+    nbytes = kernel_bytes(dominant, context_end)
     achieved = nbytes / (kernel_ms[dominant] * 1e-3) / 1e9
     # The replays write position context_end - 1 over context_end cached positions.
     traffic, traffic_source = measured_traffic(dominant, context_end)
@@ -435,9 +464,7 @@ def main():
             ttft[key] = protocol[key]['ttft_ms_median'] * 1e-3
             log(f"prompt {key}: TTFT {protocol[key]['ttft_ms_median']:.2f} ms, "
                 f"decode {protocol[key]['decode_tok_s_median']:.0f} tok/s (medians of 10)")
-        model.reset()
-        model.prefill(prompts['long_3968'])
-        long_context = long_context_decode(model, model.greedy())
+        long_context = long_context_decode(model, prompts['long_3968'])
     batch = None if args.no_batch else prefix_reuse_batch(model, prompts)
     model.close()
     gemv = None if args.no_gemv else gemv_microbench(q)

@@ -377,7 +377,7 @@ __global__ __launch_bounds__(SEG * 32) void gemv_seg_kernel(const GemvArgs a) {
 // consumer that gives up raises the stall flag, which the step's argmax
 // copies to the host. Measured: 0.40 us per exchange inside an XCD, against
 // 2.37 us per dependent kernel launch.
-constexpr unsigned kExchangeSpins = 1u << 20;
+constexpr unsigned kExchangeSpins = 1u << 18;  // ~0.1 s of polling; an exchange takes about a microsecond
 
 __device__ __forceinline__ void exchange_put(uint64_t* p, float v, uint32_t tag) {
     __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -506,7 +506,7 @@ __global__ __launch_bounds__(256) void ffn_kernel(const FfnArgs a) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
             float a0 = 0.f, a1 = 0.f;
-            ok &= exchange_get2(a.exchange + q * kFFN + kFfnSlice * g + 2 * tid, a.tag, a0, a1);
+            if (ok) ok = exchange_get2(a.exchange + q * kFFN + kFfnSlice * g + 2 * tid, a.tag, a0, a1);
             float* as = reinterpret_cast<float*>(as4[q]);
             as[xperm(2 * tid)] = a0;
             as[xperm(2 * tid + 1)] = a1;
@@ -1143,6 +1143,572 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     }
 }
 
+// N tagged words at once: every round issues the loads of all words still
+// missing (bit k of `want`), then checks them, so a round costs one L2 round
+// trip however many words there are. False if some word did not carry `tag`
+// within kExchangeSpins rounds.
+template <int N>
+__device__ __forceinline__ bool exchange_gather(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N],
+                                                unsigned want) {
+    for (unsigned spin = 0; want && spin < kExchangeSpins; ++spin) {
+        uint64_t u[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            u[k] = (want >> k) & 1 ? __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
+                out[k] = __uint_as_float(uint32_t(u[k]));
+                want &= ~(1u << k);
+            }
+    }
+    return want == 0;
+}
+
+// Contexts of up to this many 64-position passes take the fused kernel's
+// FULL form (every workgroup attends its head over all positions).
+constexpr int kFullAttnPasses = 4;
+
+// Words per attention partial in the exchange: 128 outputs, max, sum.
+constexpr int kXPart = kHeadDim + 2;
+
+struct QkvAttnArgs {
+    const uint16_t* qkv_t;   // chain-tiled [4096 x 1024]: q rows, k rows, v rows
+    const float* in_norm;    // input RMSNorm weights
+    const float* x;          // residual the layer starts from (when neither embed nor dparts)
+    const float* xm;         // with dparts: the previous fused FFN's residual
+    const float* dparts;     // [8][1024] down slices of the previous layer, or null
+    const uint16_t* embed;   // first layer: natural embedding, or null
+    int token;
+    float* x_out;            // with embed or dparts: the residual, written here
+    const float* q_norm;
+    const float* k_norm;
+    const float* cosines;
+    const float* sines;
+    uint16_t* keys;          // layer base [8][context][128] (keys chain-permuted)
+    uint16_t* values;
+    int pos;
+    int context;
+    float scale;
+    const uint16_t* o_n;     // natural O weights [1024 x 2048]
+    float* o_part;           // [16][1024] per-query-head partial O projections
+    uint64_t* xqkv;          // [8][512] tagged q/k/v rows of each KV head group
+    uint64_t* xpart;         // [8][32][2][kXPart] tagged attention partials
+    int* stall;
+    uint32_t tag;
+};
+
+// Norm + QKV + attention + O of one decode layer in one launch, for every
+// context length. 256 workgroups x 8 waves; KV head g = blockIdx % 8 (one
+// XCD) with slot s = blockIdx / 8:
+// 1. RMSNorm of the residual (engine/core.cpp:384; the previous layer's 8
+//    down slices added first when it ran the fused FFN), then waves 0-1 run
+//    QKV tiles 2s and 2s + 1 of head group g (its 512 rows: q heads 2g and
+//    2g + 1, k head g, v head g; the reference's chain-ordered dot per row)
+//    and post the rows to the XCD's exchange.
+// 2. Every workgroup takes the 512 rows, applies QK-norm and RoPE
+//    (395-402) and attends (606-624) over its 64-position passes s and
+//    s + 32 with the lane layout of the split kernel (one maximum per head
+//    over the workgroup, the 8 waves' sums added in a fixed tree); the pass
+//    holding pos writes the new K/V row (403-406). Each active workgroup
+//    posts its (output, max, sum) partials for both query heads.
+// 3. Workgroup (g, s) merges query head h = 2g + s % 2 over the partials of
+//    workgroups 0 .. min(32, passes) - 1 in a fixed order (4 groups of 8
+//    against their own maximum, then combined) and multiplies the result
+//    into O rows 64 (s / 2) .. + 63: o_part[h][row] = O[row][128h ..] . att.
+// Every wave issues the same loads (QKV weights, K/V rows of its passes,
+// O weights) at the start, so their round trips overlap the norm, the QKV
+// dots and both exchanges, and the compiler's waits stay exact. QKV tile
+// t = wave % 2 is split into 4 segments of 4 column blocks (wave / 2): the
+// segments run in turn, each continuing the chains of the previous one
+// (handed over through LDS), so each row is the reference's FMA sequence.
+// PASSES = 2 once a context needs more than 32 passes (n > 2048); SRC:
+// 0 residual x, 1 embedding row (first layer), 2 xm + down slices.
+// FULL (short contexts, PASSES = passes of the whole context): instead of
+// steps 2-3, workgroup (g, s) attends query head h = 2g + s % 2 over all n
+// positions itself (K/V rows re-read from the XCD's L2 by its 16
+// workgroups) and multiplies the result into its O rows: no partials to
+// exchange.
+template <int PASSES, int SRC, bool FULL>
+__global__ __launch_bounds__(512) void qkv_attn_kernel(const QkvAttnArgs a) {
+    constexpr int PER = 4, kSegBlocks = kHidden / 64 / 4;  // waves 0-3 hold 4 residual entries per thread
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = int(blockIdx.x & 7), s = int(blockIdx.x >> 3);
+    const int pos = a.pos, n = pos + 1, npasses = (n + 63) >> 6;
+    const int active = min(npasses, 32);  // workgroups with positions (split form)
+    const bool mine = FULL || s < active;
+    const int j = tid & 127, c = tid & 7, grp = tid >> 3;
+    const int vsub = lane >> 4, vcg = lane & 15;
+    const size_t head_base = size_t(g) * a.context;
+    // Local QKV tile li of the head group: q tiles 32g + li (li < 32), k
+    // tiles 256 + 16g + li - 32, v tiles 384 + 16g + li - 48.
+    const int ti = wave & 1, seg = wave >> 1;
+    const int li = 2 * s + ti;
+    const int qkv_tile = li < 32 ? 32 * g + li : li < 48 ? 256 + 16 * g + (li - 32) : 384 + 16 * g + (li - 48);
+    // O rows of phase 3.
+    const int hq = s & 1, h = 2 * g + hq, rb = s >> 1;
+    constexpr int kThreadsPerRow = 512 / kAttnORows, kOLoads = kHeadDim / 8 / kThreadsPerRow;
+    const int orow = rb * kAttnORows + tid / kThreadsPerRow, opart_id = tid % kThreadsPerRow;
+    const int jbase = PER * tid;
+    const bool holds = wave < 4;  // wave-uniform: waves 0-3 load and normalize the residual
+
+    // Loads in the order they are needed.
+    float v[PER], wn[PER], dsl[kFfnSlices][PER];
+    if (holds) {
+        auto load4 = [&](const float* src, float (&dst)[PER]) {
+            const float4 f = *reinterpret_cast<const float4*>(src + jbase);
+            dst[0] = f.x; dst[1] = f.y; dst[2] = f.z; dst[3] = f.w;
+        };
+        if constexpr (SRC == 1) {
+            const uint2 e = *reinterpret_cast<const uint2*>(a.embed + size_t(a.token) * kHidden + jbase);
+            v[0] = h2f(e.x & 0xffffu);
+            v[1] = h2f(e.x >> 16);
+            v[2] = h2f(e.y & 0xffffu);
+            v[3] = h2f(e.y >> 16);
+        } else {
+            load4(SRC == 2 ? a.xm : a.x, v);
+            if constexpr (SRC == 2) {
+#pragma unroll
+                for (int k = 0; k < kFfnSlices; ++k) load4(a.dparts + k * kHidden, dsl[k]);
+            }
+        }
+        load4(a.in_norm, wn);
+    }
+    // QK-norm weights and rotation of this lane's channel pair (lane, lane +
+    // 64): waves 0-1 the query heads, wave 2 the key head.
+    const float* hw = __builtin_amdgcn_readfirstlane(wave) == 2 ? a.k_norm : a.q_norm;
+    const float nw0 = hw[lane], nw1 = hw[lane + 64];
+    const float rc = a.cosines[size_t(pos) * 64 + lane], rs = a.sines[size_t(pos) * 64 + lane];
+    u32x4 wv[kSegBlocks];
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.qkv_t) + (size_t(qkv_tile) * (kHidden / 64) +
+                                                                     size_t(kSegBlocks) * seg) * 64 + lane;
+#pragma unroll
+        for (int b = 0; b < kSegBlocks; ++b) wv[b] = __builtin_nontemporal_load(wp + b * 64);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // K/V rows of this workgroup's passes (positions past n, the current
+    // one, and all of an inactive workgroup's read row 0 and are unused).
+    // Pass p covers positions 64 (s + 32 p) .. + 63 (split form) or
+    // 64 p .. + 63 (FULL).
+    auto pass_base = [&](int p) { return FULL ? 64 * p : 64 * (s + 32 * p); };
+    u32x4 kreg[PASSES][2], vreg[PASSES][2];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int t = pass_base(p) + grp;
+        const int tl = mine && t < n && t != pos ? t : 0;
+        key_pieces(a.keys + (head_base + tl) * 128, c, kreg[p][0], kreg[p][1]);
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int t = pass_base(p) + 8 * wave + 4 * hf + vsub;
+            const int tl = mine && t < n && t != pos ? t : 0;
+            vreg[p][hf] = reinterpret_cast<const u32x4*>(a.values + (head_base + tl) * 128)[vcg];
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 ow[kOLoads];
+    {
+        const u32x4* op = reinterpret_cast<const u32x4*>(a.o_n + size_t(orow) * kQDim + 128 * h) + opart_id;
+#pragma unroll
+        for (int i = 0; i < kOLoads; ++i) ow[i] = __builtin_nontemporal_load(op + kThreadsPerRow * i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    __shared__ float4 xs4[kHidden / 4];
+    __shared__ double red4[4];
+    __shared__ float qp[2][128];
+    __shared__ float prob[FULL ? 1 : 2][64 * PASSES];
+    __shared__ __align__(16) float opart[8][FULL ? 1 : 2][128];
+    __shared__ uint16_t kcur[128], vcur[128];
+    __shared__ float wmax[8][2], wsum[8][2];
+    __shared__ float gm[4], gl[4], go[4][128];
+    __shared__ __align__(16) float att[128];
+    __shared__ float hand[2][64];
+
+    // 1. Residual (engine/core.cpp:207-215: FP32 squares summed in FP64),
+    // then the QKV rows of the head group.
+    if (holds) {
+        if constexpr (SRC == 2) {
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                float dk[kFfnSlices];
+#pragma unroll
+                for (int z = 0; z < kFfnSlices; ++z) dk[z] = dsl[z][k];
+                v[k] = fold_slices(v[k], dk);
+            }
+        }
+        if (SRC != 0 && tid == int(blockIdx.x))  // workgroup b writes entries 4b .. 4b + 3
+            *reinterpret_cast<float4*>(a.x_out + jbase) = make_float4(v[0], v[1], v[2], v[3]);
+        double part = 0.0;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const float square = v[k] * v[k];
+            part += static_cast<double>(square);
+        }
+        part = wave_sum(part);
+        if (lane == 0) red4[wave] = part;
+    }
+    __syncthreads();
+    if (holds) {
+        const float sum = static_cast<float>(((red4[0] + red4[1]) + red4[2]) + red4[3]);
+        const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(kHidden) + 1e-6f);
+        float* xs = reinterpret_cast<float*>(xs4);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) xs[xperm(jbase + k)] = (v[k] * inv) * wn[k];
+    }
+    __syncthreads();
+    {
+        float acc = 0.f;
+        const float4* x4 = xs4 + 16 * (kSegBlocks * seg) + 2 * c;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (seg == k) {
+                if (k > 0) acc = hand[ti][lane];
+#pragma unroll
+                for (int b = 0; b < kSegBlocks; ++b) acc = chain8(acc, wv[b], x4[16 * b], x4[16 * b + 1]);
+                if (k < 3) {
+                    hand[ti][lane] = acc;
+                } else {
+                    const float y = combine_chains(acc);
+                    if (c == 0) exchange_put(a.xqkv + g * 512 + 8 * li + (lane >> 3), y, a.tag);
+                }
+            }
+            if (k < 3) __syncthreads();
+        }
+    }
+    // 2. Wave w < 4 takes head-group rows 128 w + lane and 128 w + 64 + lane
+    // (q0, q1, k, v): QK-norm (engine/core.cpp:397-398) and rotate-half RoPE
+    // (216-218) of the pair inside the wave; the pass holding pos writes the
+    // new K/V row (403-406).
+    bool ok = true;
+    if (holds) {
+        const uint64_t* const words[2] = {a.xqkv + g * 512 + 128 * wave + lane, a.xqkv + g * 512 + 128 * wave + 64 + lane};
+        float got[2] = {0.f, 0.f};
+        ok = exchange_gather<2>(words, a.tag, got, 3u);
+        const float x0 = got[0], x1 = got[1];
+        const bool owner = ((pos >> 6) & 31) == s;
+        if (wave < 3) {
+            const float sq0 = x0 * x0, sq1 = x1 * x1;
+            const double lo = wave_sum(static_cast<double>(sq0)), hi = wave_sum(static_cast<double>(sq1));
+            const float sum = static_cast<float>(lo + hi);
+            const float inv = 1.0f / __builtin_sqrtf(sum / 128.0f + 1e-6f);
+            const float n0 = (x0 * inv) * nw0, n1 = (x1 * inv) * nw1;
+            const float r0 = n0 * rc - n1 * rs, r1 = n1 * rc + n0 * rs;
+            if (wave < 2) {
+                qp[wave][kperm(lane)] = r0;
+                qp[wave][kperm(lane + 64)] = r1;
+            } else {
+                const uint16_t b0 = f2h(r0), b1 = f2h(r1);
+                kcur[kperm(lane)] = b0;
+                kcur[kperm(lane + 64)] = b1;
+                if (owner) {
+                    a.keys[(head_base + pos) * 128 + kperm(lane)] = b0;
+                    a.keys[(head_base + pos) * 128 + kperm(lane + 64)] = b1;
+                }
+            }
+        } else {
+            const uint16_t b0 = f2h(x0), b1 = f2h(x1);
+            vcur[lane] = b0;
+            vcur[lane + 64] = b1;
+            if (owner) {
+                a.values[(head_base + pos) * 128 + lane] = b0;
+                a.values[(head_base + pos) * 128 + lane + 64] = b1;
+            }
+        }
+    }
+    __syncthreads();
+
+    if constexpr (FULL) {
+        // Query head hq over all positions (engine/core.cpp:606-624): one
+        // maximum for the head through LDS, then each wave's probabilities and
+        // P.V of its positions, the 8 waves' sums added in a fixed tree.
+        float s0[PASSES];
+        float m0 = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = 64 * p + grp;
+            uint32_t kw[8];
+            if (t == pos) {
+                key_pieces_lds(kcur, c, kw);
+            } else {
+                kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
+                kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+            }
+            const float d0 = combine_chains(key_chain(qp[hq], c, kw, 0.f)) * a.scale;
+            s0[p] = t < n ? d0 : -INFINITY;
+            m0 = fmaxf(m0, s0[p]);
+        }
+        m0 = fmaxf(m0, xor_lanes<8>(m0));
+        m0 = fmaxf(m0, xor_lanes<16>(m0));
+        m0 = fmaxf(m0, xor_lanes<32>(m0));
+        if (lane == 0) wmax[wave][0] = m0;
+        __syncthreads();
+        m0 = wmax[0][0];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) m0 = fmaxf(m0, wmax[w][0]);
+        float l0 = 0.f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = 64 * p + grp;
+            const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
+            l0 += p0;
+            if (c == 0) prob[0][t] = p0;
+        }
+        l0 += xor_lanes<8>(l0);
+        l0 += xor_lanes<16>(l0);
+        l0 += xor_lanes<32>(l0);
+        // prob[0][t] of this wave's positions is written and read by this wave only.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int t = 64 * p + 8 * wave + 4 * hf + vsub;
+                if (t < n) {
+                    const float p0 = prob[0][t];
+                    uint32_t vw[4];
+                    if (t == pos) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            vw[i] = uint32_t(vcur[vcg * 8 + 2 * i]) | (uint32_t(vcur[vcg * 8 + 2 * i + 1]) << 16);
+                    } else {
+                        vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc[2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p0, acc[2 * i]);
+                        acc[2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p0, acc[2 * i + 1]);
+                    }
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            acc[i] += xor_lanes<16>(acc[i]);
+            acc[i] += xor_lanes<32>(acc[i]);
+        }
+        if (vsub == 0) {
+            *reinterpret_cast<float4*>(&opart[wave][0][vcg * 8]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            *reinterpret_cast<float4*>(&opart[wave][0][vcg * 8 + 4]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        }
+        if (lane == 0) wsum[wave][0] = l0;
+        if (!ok) *a.stall = 1;
+        __syncthreads();
+        if (tid < 128) {
+            const float o = ((opart[0][0][tid] + opart[1][0][tid]) + (opart[2][0][tid] + opart[3][0][tid])) +
+                            ((opart[4][0][tid] + opart[5][0][tid]) + (opart[6][0][tid] + opart[7][0][tid]));
+            const float l = ((wsum[0][0] + wsum[1][0]) + (wsum[2][0] + wsum[3][0])) +
+                            ((wsum[4][0] + wsum[5][0]) + (wsum[6][0] + wsum[7][0]));
+            att[tid] = o / l;
+        }
+    } else {
+    if (mine) {
+        float s0[PASSES], s1[PASSES];
+        float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = 64 * (s + 32 * p) + grp;
+            uint32_t kw[8];
+            if (t == pos) {
+                key_pieces_lds(kcur, c, kw);
+            } else {
+                kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
+                kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+            }
+            const float d0 = combine_chains(key_chain(qp[0], c, kw, 0.f)) * a.scale;
+            const float d1 = combine_chains(key_chain(qp[1], c, kw, 0.f)) * a.scale;
+            s0[p] = t < n ? d0 : -INFINITY;
+            s1[p] = t < n ? d1 : -INFINITY;
+            m0 = fmaxf(m0, s0[p]);
+            m1 = fmaxf(m1, s1[p]);
+        }
+        m0 = fmaxf(m0, xor_lanes<8>(m0));
+        m1 = fmaxf(m1, xor_lanes<8>(m1));
+        m0 = fmaxf(m0, xor_lanes<16>(m0));
+        m1 = fmaxf(m1, xor_lanes<16>(m1));
+        m0 = fmaxf(m0, xor_lanes<32>(m0));
+        m1 = fmaxf(m1, xor_lanes<32>(m1));
+        if (lane == 0) {
+            wmax[wave][0] = m0;
+            wmax[wave][1] = m1;
+        }
+        __syncthreads();
+        m0 = wmax[0][0];
+        m1 = wmax[0][1];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) {
+            m0 = fmaxf(m0, wmax[w][0]);
+            m1 = fmaxf(m1, wmax[w][1]);
+        }
+        float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = 64 * (s + 32 * p) + grp;
+            const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
+            const float p1 = t < n ? expf(s1[p] - m1) : 0.f;
+            l0 += p0;
+            l1 += p1;
+            if (c == 0) {
+                prob[0][p * 64 + grp] = p0;
+                prob[1][p * 64 + grp] = p1;
+            }
+        }
+        l0 += xor_lanes<8>(l0);
+        l1 += xor_lanes<8>(l1);
+        l0 += xor_lanes<16>(l0);
+        l1 += xor_lanes<16>(l1);
+        l0 += xor_lanes<32>(l0);
+        l1 += xor_lanes<32>(l1);
+        // prob[][] of this wave's positions is written and read by this wave only.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float acc[2][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[0][i] = acc[1][i] = 0.f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int tl = p * 64 + 8 * wave + 4 * hf + vsub, t = 64 * (s + 32 * p) + 8 * wave + 4 * hf + vsub;
+                if (t < n) {
+                    const float p0 = prob[0][tl], p1 = prob[1][tl];
+                    uint32_t vw[4];
+                    if (t == pos) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            vw[i] = uint32_t(vcur[vcg * 8 + 2 * i]) | (uint32_t(vcur[vcg * 8 + 2 * i + 1]) << 16);
+                    } else {
+                        vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
+                        acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
+                        acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
+                        acc[1][2 * i] = __builtin_fmaf(v0, p1, acc[1][2 * i]);
+                        acc[1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[1][2 * i + 1]);
+                    }
+                }
+            }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                acc[hh][i] += xor_lanes<16>(acc[hh][i]);
+                acc[hh][i] += xor_lanes<32>(acc[hh][i]);
+            }
+        if (vsub == 0) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int i = 0; i < 8; i += 4)
+                    *reinterpret_cast<float4*>(&opart[wave][hh][vcg * 8 + i]) =
+                        make_float4(acc[hh][i], acc[hh][i + 1], acc[hh][i + 2], acc[hh][i + 3]);
+        }
+        if (lane == 0) {
+            wsum[wave][0] = l0;
+            wsum[wave][1] = l1;
+        }
+        __syncthreads();
+        if (tid < 256) {
+            const int hh = tid >> 7;
+            const float o = ((opart[0][hh][j] + opart[1][hh][j]) + (opart[2][hh][j] + opart[3][hh][j])) +
+                            ((opart[4][hh][j] + opart[5][hh][j]) + (opart[6][hh][j] + opart[7][hh][j]));
+            const float l = ((wsum[0][hh] + wsum[1][hh]) + (wsum[2][hh] + wsum[3][hh])) +
+                            ((wsum[4][hh] + wsum[5][hh]) + (wsum[6][hh] + wsum[7][hh]));
+            uint64_t* part = a.xpart + ((size_t(g) * 32 + s) * 2 + hh) * kXPart;
+            exchange_put(part + j, o, a.tag);
+            if (j == 0) {
+                exchange_put(part + 128, hh ? m1 : m0, a.tag);
+                exchange_put(part + 129, l, a.tag);
+            }
+        }
+    }
+
+    // 3. Merge query head h over the active workgroups' partials (group q of
+    // 128 threads: workgroups 8q .. 8q + 7), then its O rows.
+    {
+        const int q = tid >> 7;
+        float mv[8], lv[8], ovl[8];
+        {
+            // The partials of workgroups 8q .. 8q + 7 that have positions:
+            // output j, max and sum of each, gathered in one poll.
+            const uint64_t* words[24];
+            float got[24];
+            unsigned want = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint64_t* part = a.xpart + ((size_t(g) * 32 + 8 * q + k) * 2 + hq) * kXPart;
+                words[k] = part + j;
+                words[8 + k] = part + 128;
+                words[16 + k] = part + 129;
+                got[k] = got[8 + k] = got[16 + k] = 0.f;
+                if (8 * q + k < active) want |= 0x10101u << k;
+            }
+            // After a give-up, stop polling (the step is reported as stalled).
+            if (ok) ok = exchange_gather<24>(words, a.tag, got, want);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                ovl[k] = got[k];
+                mv[k] = 8 * q + k < active ? got[8 + k] : -INFINITY;
+                lv[k] = got[16 + k];
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (8 * q + k < active) mx = fmaxf(mx, mv[k]);
+        float l = 0.f, o = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (8 * q + k < active) {
+                const float w = expf(mv[k] - mx);
+                l += w * lv[k];
+                o += w * ovl[k];
+            }
+        if (j == 0) {
+            gm[q] = mx;
+            gl[q] = l;
+        }
+        go[q][j] = o;
+    }
+    if (!ok) *a.stall = 1;
+    __syncthreads();
+    if (tid < 128) {
+        float m2 = gm[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) m2 = fmaxf(m2, gm[q]);
+        float lt = 0.f, ot = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (gm[q] != -INFINITY) {  // a group without partials adds nothing
+                const float w = expf(gm[q] - m2);
+                lt += w * gl[q];
+                ot += w * go[q][tid];
+            }
+        att[tid] = ot / lt;
+    }
+    }  // split form
+    __syncthreads();
+    float y = 0.f;
+    const float4* at4 = reinterpret_cast<const float4*>(att) + 2 * opart_id;
+#pragma unroll
+    for (int i = 0; i < kOLoads; ++i) y = chain8(y, ow[i], at4[2 * kThreadsPerRow * i], at4[2 * kThreadsPerRow * i + 1]);
+    static_assert(kThreadsPerRow == 8, "three lane exchanges");
+    y += xor_lanes<1>(y);
+    y += xor_lanes<2>(y);
+    y += xor_lanes<4>(y);
+    if (opart_id == 0) a.o_part[h * kHidden + orow] = y;
+}
+
 __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* __restrict__ second,
                             uint16_t* __restrict__ dst, int rows, int cols) {
     const int nb = cols / 64;
@@ -1237,6 +1803,60 @@ void launch_ffn_rows(const uint16_t* gateup_t, const uint16_t* down_t, const flo
     ffn_kernel<ROWS><<<kFfnGroups, 256, 0, stream>>>(f);
 }
 
+// The fused QKV + attention + O kernel of one row at position pos. x: the
+// residual the layer starts from (written there with embed or dparts); xm
+// and dparts: the previous fused FFN's output when dparts is non-null.
+void launch_qkv_attn(const LayerDevice& L, const uint16_t* embed, int token, int pos, const float* cosines,
+                     const float* sines, int context, float* x, const float* xm, const float* dparts, float* o_part,
+                     const DecodeScratch& s, uint32_t tag, hipStream_t stream) {
+    require(tag != 0, "fused attention: tag 0 is the cleared exchange");
+    require(pos >= 0 && pos < context && pos < 64 * 64, "fused attention: position outside the cache");
+    static_assert(kXPartWords == kKVHeads * 32 * 2 * kXPart, "exchange size");
+    QkvAttnArgs q{};
+    q.qkv_t = L.qkv_t;
+    q.in_norm = L.in_norm;
+    q.x = x;
+    q.xm = xm;
+    q.dparts = dparts;
+    q.embed = embed;
+    q.token = token;
+    q.x_out = x;
+    q.q_norm = L.q_norm;
+    q.k_norm = L.k_norm;
+    q.cosines = cosines;
+    q.sines = sines;
+    q.keys = L.keys;
+    q.values = L.values;
+    q.pos = pos;
+    q.context = context;
+    q.scale = 1.0f / std::sqrt(128.0f);
+    q.o_n = L.o_n;
+    q.o_part = o_part;
+    q.xqkv = s.xqkv;
+    q.xpart = s.xpart;
+    q.stall = s.stall;
+    q.tag = tag;
+    const int passes = (pos + 1 + 63) / 64;
+    const int src = embed ? 1 : dparts ? 2 : 0;
+    auto go = [&](auto tag_passes, auto tag_full) {
+        constexpr int P = decltype(tag_passes)::value;
+        constexpr bool F = decltype(tag_full)::value;
+        if (src == 0) qkv_attn_kernel<P, 0, F><<<256, 512, 0, stream>>>(q);
+        else if (src == 1) qkv_attn_kernel<P, 1, F><<<256, 512, 0, stream>>>(q);
+        else qkv_attn_kernel<P, 2, F><<<256, 512, 0, stream>>>(q);
+    };
+    using std::integral_constant;
+    switch (passes <= kFullAttnPasses ? passes : 0) {
+        case 1: go(integral_constant<int, 1>{}, std::true_type{}); break;
+        case 2: go(integral_constant<int, 2>{}, std::true_type{}); break;
+        case 3: go(integral_constant<int, 3>{}, std::true_type{}); break;
+        case 4: go(integral_constant<int, 4>{}, std::true_type{}); break;
+        default:
+            if (passes > 32) go(integral_constant<int, 2>{}, std::false_type{});
+            else go(integral_constant<int, 1>{}, std::false_type{});
+    }
+}
+
 template <int ROWS>
 void launch_ffn(const LayerDevice& L, const float* x, const float* parts, float* xm, float* dparts,
                 uint64_t* exchange, int* stall, uint32_t tag, hipStream_t stream) {
@@ -1272,6 +1892,12 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
                          LayerFlow flow, hipStream_t stream) {
     switch (which) {
         case 0: {
+            if (flow.attn_tag) {
+                const bool fold = flow.fold_input && !embed;
+                launch_qkv_attn(L, embed, token, pos, cosines, sines, context, s.x, s.xm, fold ? s.dparts : nullptr,
+                                s.o_part, s, flow.attn_tag, stream);
+                break;
+            }
             GemvArgs q{};
             q.w = L.qkv_t;
             q.in = s.x;
@@ -1288,6 +1914,7 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
             break;
         }
         case 1: {
+            if (flow.attn_tag) break;  // the fused kernel ran the attention
             AttnArgs at{};
             at.qkv = s.qkv;
             at.q_norm = L.q_norm;
@@ -1356,9 +1983,11 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
 
 bool pair_supported(int pos) { return attn_fused(pos + 2) || !attn_fused(pos + 1); }
 
-void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int pos, const int (&tokens)[2],
-                              const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                              const PairScratch& pr, LayerFlow flow, hipStream_t stream) {
+// The pair's QKV (shared weight loads) and attention kernels (fused for both
+// rows, or split + merge/O per row).
+static void launch_pair_qkv_attention(const LayerDevice& L, const uint16_t* embed, int pos, const int (&tokens)[2],
+                               const float* cosines, const float* sines, int context, const DecodeScratch& s,
+                               const PairScratch& pr, LayerFlow flow, hipStream_t stream) {
     require(pair_supported(pos) && pos >= 0 && pos + 2 <= context, "verification pair: unsupported position");
     const bool fused = attn_fused(pos + 2);
     GemvArgs q{};
@@ -1418,7 +2047,25 @@ void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int p
             attn_merge_o_kernel<<<kAttnOGroups, 512, 0, stream>>>(ar);
         }
     }
+}
 
+void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int pos, const int (&tokens)[2],
+                              const float* cosines, const float* sines, int context, const DecodeScratch& s,
+                              const PairScratch& pr, LayerFlow flow, hipStream_t stream) {
+    if (flow.attn_tag) {
+        // Each row through the fused QKV + attention kernel at its position
+        // (row 0 first: it writes the K/V row that row 1 reads), then the
+        // FFN for both rows with shared weight loads.
+        require(pos >= 0 && pos + 2 <= context, "verification pair: unsupported position");
+        const bool fold = flow.fold_input && !embed;
+        for (int row = 0; row < 2; ++row)
+            launch_qkv_attn(L, embed, tokens[row], pos + row, cosines, sines, context, pr.x + row * kHidden,
+                            pr.xm + row * kHidden, fold ? pr.dparts + size_t(row) * kFfnSlices * kHidden : nullptr,
+                            pr.o_part + size_t(row) * kOParts * kHidden, s, row ? flow.attn_tag2 : flow.attn_tag,
+                            stream);
+    } else {
+        launch_pair_qkv_attention(L, embed, pos, tokens, cosines, sines, context, s, pr, flow, stream);
+    }
     if (flow.ffn_tag) {
         launch_ffn<2>(L, pr.x, pr.o_part, pr.xm, pr.dparts, pr.exchange, s.stall, flow.ffn_tag, stream);
         return;

@@ -192,6 +192,8 @@ void Engine::init_state() {
     s.dparts = device_alloc<float>(size_t(kFfnSlices) * kHidden);
     s.exchange = device_alloc<uint64_t>(kFFN);
     s.stall = device_alloc<int>(1);
+    s.xqkv = device_alloc<uint64_t>(kXqkvWords);
+    s.xpart = device_alloc<uint64_t>(kXPartWords);
     ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
     ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
     base_logits_ = device_alloc<float>(kVocab);
@@ -210,7 +212,10 @@ void Engine::init_state() {
     HIP_CHECK(hipMemsetAsync(s.exchange, 0, kFFN * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(pair_.exchange, 0, 2 * kFFN * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(s.stall, 0, sizeof(int), stream_));
+    HIP_CHECK(hipMemsetAsync(s.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(s.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
     if (const char* env = std::getenv("QWEN_HIP_FUSED_FFN")) fused_ffn_ = std::string(env) != "0";
+    if (const char* env = std::getenv("QWEN_HIP_FUSED_ATTENTION")) fused_attn_ = std::string(env) != "0";
     penalized_ = device_alloc<uint8_t>(kVocab);
     top_scratch_ = device_alloc<uint8_t>(top_scores_scratch_bytes());
     top_device_ = device_alloc<TopScores>(1);
@@ -284,13 +289,21 @@ void Engine::truncate(int position) {
 // One token through the 28 layers (5 kernels each) and, when `head`, the
 // final norm, tied lm_head and greedy argmax into host result slot
 // `result_slot`. The step scalars are kernel arguments.
-LayerFlow Engine::layer_flow(int layer) {
+// Exchange tags: every launch of a fused kernel takes the next one (never 0,
+// the cleared exchange), so no launch reads a word an earlier one wrote.
+uint32_t Engine::next_tag() {
+    if (++ffn_tag_ == 0) ++ffn_tag_;
+    return ffn_tag_;
+}
+
+LayerFlow Engine::layer_flow(int layer, bool pair) {
     LayerFlow f{};
     f.fold_input = fused_ffn_ && layer > 0;
-    if (fused_ffn_ && layer < kLayers - 1) {  // the last layer writes the residual the head reads
-        if (++ffn_tag_ == 0) ++ffn_tag_;
-        f.ffn_tag = ffn_tag_;
+    if (fused_attn_) {
+        f.attn_tag = next_tag();
+        if (pair) f.attn_tag2 = next_tag();
     }
+    if (fused_ffn_ && layer < kLayers - 1) f.ffn_tag = next_tag();  // the last layer writes the residual the head reads
     return f;
 }
 
@@ -435,7 +448,7 @@ void Engine::run_pair(int first, int second) {
     const int tokens[2] = {first, second};
     for (int l = 0; l < kLayers; ++l)
         launch_decode_layer_pair(layers_[l], l == 0 ? embed_ : nullptr, pos_, tokens, cosines_, sines_,
-                                 options_.context, scratch_, pair_, layer_flow(l), stream_);
+                                 options_.context, scratch_, pair_, layer_flow(l, true), stream_);
     launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, stream_);
     HIP_CHECK(hipGetLastError());
 }
@@ -448,7 +461,7 @@ void Engine::verify_two(int first, int second) {
     require(pos_ <= options_.context - 2, "Context capacity exceeded");
     const int start = pos_;
     try {
-        if (pair_supported(start)) {
+        if (fused_attn_ || pair_supported(start)) {
             run_pair(first, second);
         } else {
             // The two positions straddle the fused-attention limit: two single
@@ -563,26 +576,29 @@ void Engine::commit_verified(int count) {
 float Engine::time_kernel(int which, int iterations) {
     require(pos_ > 0 && !pending_, "time_kernel needs a current position");
     HIP_CHECK(hipStreamSynchronize(stream_));
-    require(which >= 0 && which <= 6 && iterations > 0, "time_kernel: bad arguments");
+    require(which >= 0 && which <= 7 && iterations > 0, "time_kernel: bad arguments");
     if (which == 2) return 0.f;  // O runs with the attention (1)
     require(which != 6 || fused_ffn_, "time_kernel: the fused FFN kernel is switched off");
+    require(which != 7 || fused_attn_, "time_kernel: the fused QKV + attention kernel is switched off");
     // Replays kernels of the last processed position; the state is reset
     // afterwards. Layer kernels rotate over all 28 layers so that, as in a
     // real step, their weights (about 880 MB in total) stream from HBM rather
     // than from the 256 MB Infinity Cache.
-    // 3 and 4 time the norm+gate/up and down kernels (every layer; with the
-    // fused FFN on, a step runs them only in the last layer), 6 the fused
-    // FFN kernel (layers 0-26).
+    // 0, 1, 3 and 4 time the separate norm+QKV, attention, norm+gate/up and
+    // down kernels (every layer; with the fused kernels on, a step runs 3 and
+    // 4 only in the last layer and 0 and 1 never), 6 the fused FFN kernel
+    // (layers 0-26), 7 the fused QKV + attention + O kernel.
     const int layers = which == 6 ? kLayers - 1 : kLayers;
     int layer = 0;
     auto launch = [&] {
         LayerFlow flow = layer_flow(layer);
         if (which == 3 || which == 4) flow.ffn_tag = 0;
+        if (which == 0 || which == 1) flow.attn_tag = 0;
         if (which == 5)
             launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
         else
-            launch_layer_kernel(which == 6 ? 3 : which, layers_[layer], nullptr, pos_ - 1, 0, cosines_, sines_,
-                                options_.context, scratch_, flow, stream_);
+            launch_layer_kernel(which == 6 ? 3 : which == 7 ? 0 : which, layers_[layer], nullptr, pos_ - 1, 0,
+                                cosines_, sines_, options_.context, scratch_, flow, stream_);
         layer = (layer + 1) % layers;
     };
     for (int i = 0; i < layers; ++i) launch();
@@ -599,7 +615,7 @@ float Engine::time_kernel(int which, int iterations) {
     (void)hipEventDestroy(stop);
     // The replayed kernels overwrite the residual stream and logits; the
     // attention kernel also rewrites cached K/V, so it resets the model.
-    if (which == 1)
+    if (which == 1 || which == 7)
         reset();
     else
         invalidate();

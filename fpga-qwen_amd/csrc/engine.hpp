@@ -93,7 +93,8 @@ private:
     void append(const int* ids, size_t count);
     void run_token(int token, bool head, int result_slot);
     void run_pair(int first, int second);
-    LayerFlow layer_flow(int layer);
+    LayerFlow layer_flow(int layer, bool pair = false);
+    uint32_t next_tag();
     void check_stall(int slot) const;
     void release();
     void sync();
@@ -131,6 +132,9 @@ private:
     // slices in one launch) unless QWEN_HIP_FUSED_FFN=0; every fused launch
     // takes the next tag (never 0, the cleared exchange).
     bool fused_ffn_ = true;
+    // Norm + QKV + attention + O run as one kernel per layer unless
+    // QWEN_HIP_FUSED_ATTENTION=0; its launches take tags from the same counter.
+    bool fused_attn_ = true;
     uint32_t ffn_tag_ = 0;
     bool has_logits_ = false;
     bool pending_ = false;

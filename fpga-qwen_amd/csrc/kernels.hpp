@@ -105,7 +105,9 @@ struct DecodeScratch {
     float* xm;            // [1024] residual after the O partials (written by the fused FFN kernel)
     float* dparts;        // [8][1024] down products of the 8 activation slices (fused FFN kernel)
     uint64_t* exchange;   // [3072] activations with their launch tag, exchanged inside each XCD
-    int* stall;           // nonzero once a fused FFN poll gave up (cleared by the argmax kernel)
+    int* stall;           // nonzero once an exchange poll gave up (cleared by the argmax kernel)
+    uint64_t* xqkv;       // [8][512] q/k/v rows of each KV head group (fused QKV + attention kernel)
+    uint64_t* xpart;      // [kXPartWords] attention partials of its workgroups
 };
 
 // The fused FFN kernel (norm + gate/up + SwiGLU + down in one launch): XCD
@@ -114,6 +116,10 @@ struct DecodeScratch {
 inline constexpr int kFfnSlices = 8;
 inline constexpr int kFfnSlice = kFFN / kFfnSlices;  // 384 activations per XCD
 inline constexpr int kFfnGroups = 256;               // workgroups (32 per XCD)
+// The fused QKV + attention + O kernel: exchange words for the q/k/v rows and
+// for the (128 outputs, max, sum) partials of 2 heads x 32 workgroups x 8 KV heads.
+inline constexpr int kXqkvWords = kKVHeads * 512;
+inline constexpr int kXPartWords = kKVHeads * 32 * 2 * (kHeadDim + 2);
 
 // Layout conversion: natural row-major FP16 [rows x cols] -> chain-tiled.
 // When `second` is non-null the tiles interleave two matrices of equal shape:
@@ -138,19 +144,26 @@ void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, 
 // writes their sum to s.x. ffn_tag != 0: this layer runs the fused FFN kernel
 // (that tag must differ from the previous fused launch's on these buffers);
 // 0: the norm+gate/up and down kernels.
+// attn_tag != 0: norm + QKV + attention + O run as one kernel with that
+// tag (pairs: attn_tag for row 0, attn_tag2 for row 1); 0: the QKV and
+// attention kernels.
 struct LayerFlow {
     bool fold_input;
     uint32_t ffn_tag;
+    uint32_t attn_tag;
+    uint32_t attn_tag2;
 };
 
 void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          LayerFlow flow, hipStream_t stream);
 
-// One stage of a decode layer: 0 norm+QKV, 1 attention with the O partials
-// (one kernel up to kFusedMaxPositions, split + merge/O beyond), 2 nothing
-// (O runs with the attention), 3 norm+gate/up (the fused FFN kernel when
-// flow.ffn_tag != 0), 4 down (nothing after a fused FFN launch).
+// One stage of a decode layer: 0 norm+QKV (the fused QKV + attention + O
+// kernel when flow.attn_tag != 0), 1 attention with the O partials (one
+// kernel up to kFusedMaxPositions, split + merge/O beyond; nothing after a
+// fused launch), 2 nothing (O runs with the attention), 3 norm+gate/up (the
+// fused FFN kernel when flow.ffn_tag != 0), 4 down (nothing after a fused FFN
+// launch).
 void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* embed, int pos, int token,
                          const float* cosines, const float* sines, int context, const DecodeScratch& s,
                          LayerFlow flow, hipStream_t stream);

@@ -242,11 +242,12 @@ int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream);
 /* Average milliseconds of one standalone launch of a decode kernel on the
  * model's stream, timed with HIP events (which: 0 norm+QKV, 1 attention,
  * 2 O, 3 norm+gate/up, 4 down, 5 lm_head, 6 the fused FFN kernel that layers
- * 0-26 run in place of 3 and 4). Needs position() > 0. The O projection
- * runs with the attention (timed as 1: one kernel up to 512 positions, split
- * attention + merge/O beyond) and 2 reports 0. Afterwards the current
- * logits are invalid; timing the attention (1) also resets the model, so
- * time it last. */
+ * 0-26 run in place of 3 and 4, 7 the fused norm + QKV + attention + O
+ * kernel that every layer runs in place of 0 and 1). Needs position() > 0.
+ * The O projection runs with the attention (timed as 1: one kernel up to 512
+ * positions, split attention + merge/O beyond) and 2 reports 0. Afterwards
+ * the current logits are invalid; timing the attention (1 or 7) also resets
+ * the model, so time it last. */
 int qwen_gpu_time_kernel(qwen_gpu_model* model, int which, int iterations, float* milliseconds);
 
 #ifdef __cplusplus

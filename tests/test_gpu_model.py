@@ -76,27 +76,31 @@ def test_repeat_is_bit_identical(gpu_model):
 
 
 @pytest.mark.gpu
-def test_fused_ffn_path_matches_two_kernel_path(qpkg, pack0, gpu_model, monkeypatch):
-    """Layers 0-26 run the fused FFN kernel, whose down projection is 8
-    column slices added by the next layer; QWEN_HIP_FUSED_FFN=0 selects the
-    two-kernel path (norm+gate/up, then down as the reference's dot over all
-    3072 columns). Along greedy trajectories after the 85-token prompt (fused
-    attention) and an 1100-token prompt (split attention) both paths choose
-    the same tokens and their logits agree to 1e-4: the slice sums move each
-    down output by a few FP32 ulps, nothing more (a wrong slice, row or
-    fold would move them by the size of the product, ~1e-1)."""
-    monkeypatch.setenv('QWEN_HIP_FUSED_FFN', '0')
+@pytest.mark.parametrize('switch', ['QWEN_HIP_FUSED_FFN', 'QWEN_HIP_FUSED_ATTENTION'])
+def test_fused_kernels_match_separate_kernels(qpkg, pack0, gpu_model, monkeypatch, switch):
+    """The step's two fused kernels against the separate kernels they
+    replace. QWEN_HIP_FUSED_FFN=0: norm+gate/up, then down as the reference's
+    dot over all 3072 columns, instead of 8 column slices added by the next
+    layer. QWEN_HIP_FUSED_ATTENTION=0: the QKV kernel and the fused (up to 512
+    positions) or split + merge attention kernels, instead of one kernel whose
+    workgroups attend over 64-position passes and merge their partials. Along
+    greedy trajectories after the 85-token prompt and after 1100- and
+    3000-token prompts both paths choose the same tokens and their logits
+    agree to 1e-4: the different summation orders move outputs by a few FP32
+    ulps, nothing more (a wrong slice, row, head, pass or fold moves them by
+    ~1e-1)."""
+    monkeypatch.setenv(switch, '0')
     plain = qpkg.Model(pack0, context=4096)
-    monkeypatch.delenv('QWEN_HIP_FUSED_FFN')
+    monkeypatch.delenv(switch)
     try:
-        for prompt in (PROMPTS['decode_85'], PROMPTS['long_3968'][:1100]):
+        for prompt in (PROMPTS['decode_85'], PROMPTS['long_3968'][:1100], PROMPTS['long_3968'][:3000]):
             fused_rows = greedy_trajectory(gpu_model, prompt, 12)
             plain_rows = greedy_trajectory(plain, prompt, 12)
             worst = 0.0
             for (lf, tf), (lp, tp) in zip(fused_rows, plain_rows):
                 assert tf == tp
                 worst = max(worst, float(np.max(np.abs(lf - lp))))
-            print(f'prompt {len(prompt)}: fused vs two-kernel max |d logit| {worst:.3e}')
+            print(f'{switch}=0, prompt {len(prompt)}: max |d logit| against the fused kernels {worst:.3e}')
             assert worst <= 1e-4
     finally:
         plain.close()
