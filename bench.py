@@ -23,13 +23,12 @@ sys.path.insert(0, str(ROOT / 'tests'))
 
 HBM_PEAK_GBS = 8000.0
 # Engine kernel ids (time_kernel). A decode step runs 'qkv_attention' (norm
-# + QKV + attention + O in one kernel) in every layer, 'ffn' (norm + gate/up
-# + SwiGLU + down) in layers 0-26 and the separate 'gate_up' and 'down'
-# kernels in the last layer; 'qkv' and 'attention' are the separate kernels
-# the fused one replaces (timed for comparison, not run by a step).
+# + QKV + attention + O in one kernel) and 'ffn' (norm + gate/up + SwiGLU +
+# down) in every layer; 'qkv', 'attention', 'gate_up' and 'down' are the
+# separate kernels those replace (timed for comparison, not run by a step).
 KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head', 'ffn', 'qkv_attention']
 # Launches of each kernel per decode token.
-PER_TOKEN = {'qkv_attention': 28, 'ffn': 27, 'gate_up': 1, 'down': 1, 'lm_head': 1}
+PER_TOKEN = {'qkv_attention': 28, 'ffn': 28, 'lm_head': 1}
 # Algorithmic bytes per launch: FP16 weights + FP32 vectors read/written.
 KERNEL_BYTES = {
     'qkv': 4096 * 1024 * 2 + 1024 * 4 * 2 + 4096 * 4 + 8 * 1024 * 4,  # + the 8 down slices folded in

@@ -384,18 +384,24 @@ __device__ __forceinline__ void exchange_put(uint64_t* p, float v, uint32_t tag)
 }
 
 // Two consecutive tagged words; false if they did not both carry `tag`
-// within kExchangeSpins polls.
+// within kExchangeSpins polls. The loop runs while any lane of the wave still
+// waits (a wave-uniform exit), and each lane's result comes from its own
+// flag: lanes leaving a loop at different iterations would otherwise hand the
+// compiler a divergent loop exit for the result.
 __device__ __forceinline__ bool exchange_get2(const uint64_t* p, uint32_t tag, float& a, float& b) {
-    for (unsigned spin = 0; spin < kExchangeSpins; ++spin) {
-        const uint64_t u = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t w = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (uint32_t(u >> 32) == tag && uint32_t(w >> 32) == tag) {
-            a = __uint_as_float(uint32_t(u));
-            b = __uint_as_float(uint32_t(w));
-            return true;
+    unsigned missing = 1;
+    for (unsigned spin = 0; spin < kExchangeSpins && __any(missing); ++spin) {
+        if (missing) {
+            const uint64_t u = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t w = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (uint32_t(u >> 32) == tag && uint32_t(w >> 32) == tag) {
+                a = __uint_as_float(uint32_t(u));
+                b = __uint_as_float(uint32_t(w));
+                missing = 0;
+            }
         }
     }
-    return false;
+    return missing == 0;
 }
 
 struct FfnArgs {
@@ -1150,7 +1156,8 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
 template <int N>
 __device__ __forceinline__ bool exchange_gather(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N],
                                                 unsigned want) {
-    for (unsigned spin = 0; want && spin < kExchangeSpins; ++spin) {
+    // Wave-uniform loop exit, per-lane result from `want` (see exchange_get2).
+    for (unsigned spin = 0; spin < kExchangeSpins && __any(want != 0); ++spin) {
         uint64_t u[N];
 #pragma unroll
         for (int k = 0; k < N; ++k)
@@ -1803,6 +1810,22 @@ void launch_ffn_rows(const uint16_t* gateup_t, const uint16_t* down_t, const flo
     ffn_kernel<ROWS><<<kFfnGroups, 256, 0, stream>>>(f);
 }
 
+// The attention form and pass count for n = pos + 1 cached positions.
+template <class F>
+void with_attention_form(int pos, F&& go) {
+    const int passes = (pos + 1 + 63) / 64;
+    using std::integral_constant;
+    switch (passes <= kFullAttnPasses ? passes : 0) {
+        case 1: go(integral_constant<int, 1>{}, std::true_type{}); break;
+        case 2: go(integral_constant<int, 2>{}, std::true_type{}); break;
+        case 3: go(integral_constant<int, 3>{}, std::true_type{}); break;
+        case 4: go(integral_constant<int, 4>{}, std::true_type{}); break;
+        default:
+            if (passes > 32) go(integral_constant<int, 2>{}, std::false_type{});
+            else go(integral_constant<int, 1>{}, std::false_type{});
+    }
+}
+
 // The fused QKV + attention + O kernel of one row at position pos. x: the
 // residual the layer starts from (written there with embed or dparts); xm
 // and dparts: the previous fused FFN's output when dparts is non-null.
@@ -1836,25 +1859,14 @@ void launch_qkv_attn(const LayerDevice& L, const uint16_t* embed, int token, int
     q.xpart = s.xpart;
     q.stall = s.stall;
     q.tag = tag;
-    const int passes = (pos + 1 + 63) / 64;
     const int src = embed ? 1 : dparts ? 2 : 0;
-    auto go = [&](auto tag_passes, auto tag_full) {
+    with_attention_form(pos, [&](auto tag_passes, auto tag_full) {
         constexpr int P = decltype(tag_passes)::value;
         constexpr bool F = decltype(tag_full)::value;
         if (src == 0) qkv_attn_kernel<P, 0, F><<<256, 512, 0, stream>>>(q);
         else if (src == 1) qkv_attn_kernel<P, 1, F><<<256, 512, 0, stream>>>(q);
         else qkv_attn_kernel<P, 2, F><<<256, 512, 0, stream>>>(q);
-    };
-    using std::integral_constant;
-    switch (passes <= kFullAttnPasses ? passes : 0) {
-        case 1: go(integral_constant<int, 1>{}, std::true_type{}); break;
-        case 2: go(integral_constant<int, 2>{}, std::true_type{}); break;
-        case 3: go(integral_constant<int, 3>{}, std::true_type{}); break;
-        case 4: go(integral_constant<int, 4>{}, std::true_type{}); break;
-        default:
-            if (passes > 32) go(integral_constant<int, 2>{}, std::false_type{});
-            else go(integral_constant<int, 1>{}, std::false_type{});
-    }
+    });
 }
 
 template <int ROWS>
@@ -2177,6 +2189,24 @@ void launch_norm_gate_up(const uint16_t* gateup_t, const float* norm_w, const fl
     gu.parts = parts;
     gu.out = act;
     launch_gemv<kHidden, kGateUp>(gu, 2 * kFFN, stream);
+}
+
+namespace {
+// x[q][j] = xm[q][j] + the 8 down slices of row j (fixed tree order): the
+// residual after a layer whose FFN ran as the fused kernel.
+__global__ __launch_bounds__(kHidden) void fold_residual_kernel(const float* __restrict__ xm,
+                                                                const float* __restrict__ dparts, float* x) {
+    const int q = blockIdx.x, j = threadIdx.x;
+    float d[kFfnSlices];
+#pragma unroll
+    for (int g = 0; g < kFfnSlices; ++g) d[g] = dparts[(q * kFfnSlices + g) * kHidden + j];
+    x[q * kHidden + j] = fold_slices(xm[q * kHidden + j], d);
+}
+}  // namespace
+
+void launch_fold_residual(const float* xm, const float* dparts, float* x, int rows, hipStream_t stream) {
+    require(rows == 1 || rows == 2, "fold: one or two rows");
+    fold_residual_kernel<<<rows, kHidden, 0, stream>>>(xm, dparts, x);
 }
 
 void launch_fused_ffn(const uint16_t* gateup_t, const uint16_t* down_t, const float* norm_w, const float* x,

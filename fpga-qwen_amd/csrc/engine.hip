@@ -194,6 +194,7 @@ void Engine::init_state() {
     s.stall = device_alloc<int>(1);
     s.xqkv = device_alloc<uint64_t>(kXqkvWords);
     s.xpart = device_alloc<uint64_t>(kXPartWords);
+
     ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
     ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
     base_logits_ = device_alloc<float>(kVocab);
@@ -214,8 +215,10 @@ void Engine::init_state() {
     HIP_CHECK(hipMemsetAsync(s.stall, 0, sizeof(int), stream_));
     HIP_CHECK(hipMemsetAsync(s.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(s.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
+
     if (const char* env = std::getenv("QWEN_HIP_FUSED_FFN")) fused_ffn_ = std::string(env) != "0";
     if (const char* env = std::getenv("QWEN_HIP_FUSED_ATTENTION")) fused_attn_ = std::string(env) != "0";
+
     penalized_ = device_alloc<uint8_t>(kVocab);
     top_scratch_ = device_alloc<uint8_t>(top_scores_scratch_bytes());
     top_device_ = device_alloc<TopScores>(1);
@@ -303,7 +306,7 @@ LayerFlow Engine::layer_flow(int layer, bool pair) {
         f.attn_tag = next_tag();
         if (pair) f.attn_tag2 = next_tag();
     }
-    if (fused_ffn_ && layer < kLayers - 1) f.ffn_tag = next_tag();  // the last layer writes the residual the head reads
+    if (fused_ffn_) f.ffn_tag = next_tag();
     return f;
 }
 
@@ -318,6 +321,7 @@ void Engine::run_token(int token, bool head, int result_slot) {
     for (int l = 0; l < kLayers; ++l)
         launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, pos_, token, cosines_, sines_, options_.context,
                             scratch_, layer_flow(l), stream_);
+    if (fused_ffn_) launch_fold_residual(scratch_.xm, scratch_.dparts, scratch_.x, 1, stream_);
     if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
     HIP_CHECK(hipGetLastError());
     ++pos_;
@@ -449,6 +453,7 @@ void Engine::run_pair(int first, int second) {
     for (int l = 0; l < kLayers; ++l)
         launch_decode_layer_pair(layers_[l], l == 0 ? embed_ : nullptr, pos_, tokens, cosines_, sines_,
                                  options_.context, scratch_, pair_, layer_flow(l, true), stream_);
+    if (fused_ffn_) launch_fold_residual(pair_.xm, pair_.dparts, pair_.x, 2, stream_);
     launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, stream_);
     HIP_CHECK(hipGetLastError());
 }
@@ -585,10 +590,9 @@ float Engine::time_kernel(int which, int iterations) {
     // real step, their weights (about 880 MB in total) stream from HBM rather
     // than from the 256 MB Infinity Cache.
     // 0, 1, 3 and 4 time the separate norm+QKV, attention, norm+gate/up and
-    // down kernels (every layer; with the fused kernels on, a step runs 3 and
-    // 4 only in the last layer and 0 and 1 never), 6 the fused FFN kernel
-    // (layers 0-26), 7 the fused QKV + attention + O kernel.
-    const int layers = which == 6 ? kLayers - 1 : kLayers;
+    // down kernels (with the fused kernels on, a step runs none of them), 6
+    // the fused FFN kernel, 7 the fused QKV + attention + O kernel.
+    const int layers = kLayers;
     int layer = 0;
     auto launch = [&] {
         LayerFlow flow = layer_flow(layer);

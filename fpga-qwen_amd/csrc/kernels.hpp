@@ -142,7 +142,8 @@ void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, 
 // How a layer hands its residual stream on. fold_input: the previous layer
 // ran the fused FFN kernel, so QKV reads s.xm plus the 8 down slices and
 // writes their sum to s.x. ffn_tag != 0: this layer runs the fused FFN kernel
-// (that tag must differ from the previous fused launch's on these buffers);
+// (that tag must differ from the previous fused launch's on these buffers;
+// after the last layer the caller folds s.xm and the slices into s.x);
 // 0: the norm+gate/up and down kernels.
 // attn_tag != 0: norm + QKV + attention + O run as one kernel with that
 // tag (pairs: attn_tag for row 0, attn_tag2 for row 1); 0: the QKV and
@@ -239,6 +240,8 @@ void launch_down_residual(const uint16_t* down_t, const float* act, const float*
 void launch_fused_ffn(const uint16_t* gateup_t, const uint16_t* down_t, const float* norm_w, const float* x,
                       const float* parts, float* xm, float* dparts, uint64_t* exchange, int* stall, uint32_t tag,
                       hipStream_t stream);
+// x[q] = xm[q] + the 8 down slices dparts[q][8][1024] (fixed tree order), q < rows (1 or 2).
+void launch_fold_residual(const float* xm, const float* dparts, float* x, int rows, hipStream_t stream);
 // qkv = W_qkv . RMSNorm(x) with x = xm + the 8 down slices dparts[8][1024]
 // added in the fixed tree order; x is also written out.
 void launch_norm_qkv_folded(const uint16_t* qkv_t, const float* norm_w, const float* xm, const float* dparts,
