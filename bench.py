@@ -46,6 +46,9 @@ KERNEL_BYTES = {
 # one kernel (the engine's fused path); beyond it split attention and a
 # merge + O kernel. The O projection is never a kernel of its own.
 FUSED_ATTENTION_MAX = 512
+# Up to this many cached positions every workgroup of the fused QKV +
+# attention kernel attends its head over all positions.
+FULL_ATTENTION_MAX = 256
 
 
 def attention_bytes(n):
@@ -93,8 +96,9 @@ def measured_traffic(kernel, position):
     measurement. The attention stages read 8 x n x 512 bytes of K/V, so their
     traffic is linear in n on each path (the separate attention kernels:
     fused up to 512 cached positions, split beyond; the fused QKV +
-    attention kernel: one path): the line through the two measurements on
-    the same path is evaluated at n. Returns (bytes, how) or (None, reason)."""
+    attention kernel: whole-context workgroups up to 256, passes beyond):
+    the line through the two measurements on the same path is evaluated at
+    n. Returns (bytes, how) or (None, reason)."""
     path = ROOT / 'profiles' / 'decode_hbm_traffic.txt'
     if not path.exists():
         return None, 'no counter summary'
@@ -103,10 +107,13 @@ def measured_traffic(kernel, position):
         parts = line.split()
         if len(parts) == 4 and parts[0] == 'traffic' and parts[1] == kernel:
             points.append((int(parts[2]), float(parts[3])))
-    if kernel not in ('attention', 'qkv_attention'):
+    if kernel not in ('attention', 'qkv_attention'):  # no dependence on the context
         return (points[0][1], f'measured at position {points[0][0]}') if points else (None, 'not measured')
-    fused = position <= FUSED_ATTENTION_MAX
-    same = sorted(p for p in points if kernel == 'qkv_attention' or (p[0] <= FUSED_ATTENTION_MAX) == fused)
+    # Paths: the separate attention kernels switch at 512 cached positions,
+    # the fused QKV + attention kernel at 256 (every workgroup attending its
+    # head over all positions up to there, 64-position passes beyond).
+    limit = FULL_ATTENTION_MAX if kernel == 'qkv_attention' else FUSED_ATTENTION_MAX
+    same = sorted(p for p in points if (p[0] <= limit) == (position <= limit))
     if any(p[0] == position for p in same):
         return dict(same)[position], f'measured at position {position}'
     if len(same) < 2:
