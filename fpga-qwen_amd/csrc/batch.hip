@@ -369,6 +369,7 @@ __global__ __launch_bounds__(K / SPLITK / 4) void bgemv_kernel(const BatchGemvAr
 struct BatchResults {
     ArgmaxResult* device[kMaxBatch];
     ArgmaxResult* host[kMaxBatch];
+    int* stall[kMaxBatch];  // the sequence's stall flag: copied to its result, then cleared
 };
 
 __global__ __launch_bounds__(1024) void batch_argmax_kernel(const float* __restrict__ value,
@@ -398,12 +399,14 @@ __global__ __launch_bounds__(1024) void batch_argmax_kernel(const float* __restr
             bad |= wb[k];
             if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
         }
+        const int stalled = *out.stall[b];
+        *out.stall[b] = 0;
         out.device[b]->token = bi;
         out.device[b]->nonfinite = bad;
-        out.device[b]->stalled = 0;
+        out.device[b]->stalled = stalled;
         out.host[b]->token = bi;
         out.host[b]->nonfinite = bad;
-        out.host[b]->stalled = 0;
+        out.host[b]->stalled = stalled;
     }
 }
 
@@ -456,8 +459,8 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
         AttnSeq as[kMaxBatch];
         for (int b = 0; b < count; ++b) {
             const DecodeScratch& s = seqs[b].s;
-            as[b] = AttnSeq{s.qkv,          seqs[b].layers[l].keys, seqs[b].layers[l].values, s.attn_partial,
-                            s.attended,     seqs[b].pos,            seqs[b].context};
+            as[b] = AttnSeq{s.qkv,   seqs[b].layers[l].keys, seqs[b].layers[l].values, s.xpart,
+                            s.attended, s.stall, seqs[b].pos, seqs[b].context, seqs[b].tags[l]};
         }
         launch_attention_batch(as, count, W.q_norm, W.k_norm, cosines, sines, stream);
 
@@ -511,6 +514,7 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
         lm.hidden[b] = seqs[b].s.hidden;
         res.device[b] = seqs[b].s.result;
         res.host[b] = seqs[b].host_out;
+        res.stall[b] = seqs[b].s.stall;
     }
     bgemv<kHidden, kBLmHead, kBatchLmTiles>(lm, kVocab, stream);
     batch_argmax_kernel<<<count, 1024, 0, stream>>>(s0.lm_value, s0.lm_index, s0.lm_bad, res);

@@ -17,6 +17,7 @@ struct BatchSeq {
     int token;                  // id consumed at pos
     int context;                // K/V cache capacity
     ArgmaxResult* host_out;     // pinned slot for the greedy selection
+    uint32_t tags[kLayers];     // per layer: the attention exchange tag (nonzero, unique per launch)
 };
 
 // One decode step for each sequence: 28 x (norm+QKV skinny GEMM, batched

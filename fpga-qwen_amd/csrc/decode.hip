@@ -808,18 +808,6 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     attn_split_body(a, blockIdx.x, blockIdx.y);
 }
 
-// Several sequences in one launch (blockIdx.z = sequence); each has its own
-// position, K/V cache and buffers.
-struct AttnBatch {
-    AttnArgs seq[kMaxBatch];
-};
-
-// At most 80 VGPRs (6 waves per SIMD): three workgroups share a CU, so the
-// 8-sequence grids (over a thousand workgroups) take fewer rounds.
-__global__ __launch_bounds__(512, 6) void attn_decode_batch_kernel(const AttnBatch b) {
-    attn_split_body(b.seq[blockIdx.z], blockIdx.x, blockIdx.y);
-}
-
 // Merge of the position splits of one query head (flash-decoding, fixed
 // split order): o = sum_s w_s o_s / sum_s w_s l_s with w_s = exp(m_s - max).
 // One split: attention already wrote the normalized output.
@@ -916,11 +904,6 @@ __global__ __launch_bounds__(512) void attn_merge_o_kernel(const AttnArgs a) {
     y += xor_lanes<2>(y);
     y += xor_lanes<4>(y);
     if (opart_id == 0) a.o_part[h * kHidden + orow] = y;
-}
-
-__global__ __launch_bounds__(512) void attn_merge_batch_kernel(const AttnBatch b) {
-    const AttnArgs& a = b.seq[blockIdx.y];
-    attn_merge_body(a, blockIdx.x, a.attended + blockIdx.x * 128, [] {});
 }
 
 // Fused attention + O projection for n <= kFusedMaxPositions. Workgroup
@@ -1162,6 +1145,30 @@ __device__ __forceinline__ bool exchange_gather(const uint64_t* const (&p)[N], u
 #pragma unroll
         for (int k = 0; k < N; ++k)
             u[k] = (want >> k) & 1 ? __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
+                out[k] = __uint_as_float(uint32_t(u[k]));
+                want &= ~(1u << k);
+            }
+    }
+    return want == 0;
+}
+
+// The same for words base + k STRIDE + off (k < N, bit k of `want`) with
+// `base` uniform and `off` per lane, so every address is a scalar base plus
+// one 32-bit lane offset; with `extra` non-null, bit N - 1 is the word at
+// `extra` instead.
+template <int N, int STRIDE>
+__device__ __forceinline__ bool exchange_gather_strided(const uint64_t* base, unsigned off, const uint64_t* extra,
+                                                        uint32_t tag, float (&out)[N], unsigned want) {
+    for (unsigned spin = 0; spin < kExchangeSpins && __any(want != 0); ++spin) {
+        uint64_t u[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            const uint64_t* w = k == N - 1 && extra ? extra : base + k * STRIDE + off;
+            u[k] = (want >> k) & 1 ? __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        }
 #pragma unroll
         for (int k = 0; k < N; ++k)
             if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
@@ -1716,6 +1723,378 @@ __global__ __launch_bounds__(512) void qkv_attn_kernel(const QkvAttnArgs a) {
     if (opart_id == 0) a.o_part[h * kHidden + orow] = y;
 }
 
+// Batched decode attention with the merge of the position splits in the
+// same launch (up to kMaxBatch sequences, each with its own position and
+// cache). Workgroup w = g + 8 (b + B p): KV head g of sequence b, piece p of
+// its positions. All pieces of one (sequence, head) have the same w % 8 and
+// therefore run on one XCD. The grid holds one workgroup per CU: a CU serves
+// its loads in order, so a single workgroup per CU that keeps its own stream
+// of K/V rows in flight (kInFlight 64-position blocks, the loads of block
+// i + kInFlight issued once block i is consumed) overlaps its arithmetic with
+// the stream, where several workgroups per CU would each wait behind the
+// others' loads. Block layout as in the single-sequence split kernel: the 8
+// lanes of position t score it (lane c = chain c of the reference dot,
+// engine/core.cpp:612, key values converted once for both heads), and the
+// wave that scored 8 positions multiplies their V rows (4 positions x 16
+// channel groups per load). Softmax (613-620) runs online per wave: each wave
+// keeps its own running maximum, rescaling its sums when it rises, and the 8
+// waves' sums are combined with weights exp(m_w - max) in a fixed tree.
+// Pieces p > 0 post (output, max, sum) of both query heads as tagged words
+// in the sequence's exchange; piece 0 computes its own partial, gathers the
+// others from L2 and merges them in groups of 8 against their own maximum,
+// then the groups, in fixed order (all pieces are resident, so every poll
+// ends). The last piece writes the new K/V row.
+struct AttnBatchSeq {
+    const float* qkv;   // raw projections [4096]
+    uint16_t* keys;     // layer base [8][context][128]
+    uint16_t* values;
+    uint64_t* xpart;    // [8][32][2][kXPart] tagged partials
+    float* attended;    // [2048]
+    int* stall;         // set if the merge gave up waiting
+    int pos;
+    int context;
+    uint32_t tag;       // this launch's tag for the sequence's exchange
+};
+
+struct AttnBatchArgs {
+    AttnBatchSeq seq[kMaxBatch];
+    const float* q_norm;
+    const float* k_norm;
+    const float* cosines;
+    const float* sines;
+    float scale;
+    int batch;
+    int pieces;  // pieces per (sequence, head)
+};
+
+static_assert(kXPartWords == kKVHeads * kAttnSplits * 2 * kXPart, "exchange layout of the split partials");
+// Third descriptor word of a raw buffer (gfx9 family: 32-bit data format),
+// and the non-temporal cache policy for rows that are read once.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kLoadNT = 2;
+constexpr int kInFlight = 4;
+
+// NB = the largest number of 64-position blocks a piece of this launch holds.
+template <int NB>
+__global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs args) {
+    const int w = blockIdx.x, g = w & 7, b = (w >> 3) % args.batch, p = (w >> 3) / args.batch;
+    const AttnBatchSeq a = args.seq[b];  // by value: loaded once, ahead of the cache rows
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = a.pos, n = pos + 1;
+    const int blocks = (n + 63) / 64, per = (blocks + args.pieces - 1) / args.pieces;
+    const int ns = (blocks + per - 1) / per;  // pieces with positions
+    if (p >= ns) return;
+    const int t_begin = p * per * 64, t_end = min(n, t_begin + per * 64);
+    // The block holding row pos (the last piece's last block), or -1.
+    const int i_pos = p == ns - 1 ? (pos - t_begin) >> 6 : -1;
+    const size_t head_base = size_t(g) * a.context;
+    const int quarter = tid >> 7, j = tid & 127, c = tid & 7, grp = tid >> 3;
+    const int vsub = lane >> 4, vcg = lane & 15;
+
+    // Loads in the order the phases need them: this step's q/k/v with norm
+    // weights and rotation, then the first K/V blocks. Row pos is taken from
+    // LDS, not from the cache.
+    const float raw = quarter < 2 ? a.qkv[(2 * g + quarter) * 128 + j] : a.qkv[2048 + g * 128 + j];
+    const float raw_v = a.qkv[3072 + g * 128 + j];
+    const float nw = (__builtin_amdgcn_readfirstlane(quarter) < 2 ? args.q_norm : args.k_norm)[j];
+    const float rc = args.cosines[size_t(pos) * 64 + (j & 63)], rs = args.sines[size_t(pos) * 64 + (j & 63)];
+    // K/V rows through buffer loads: one descriptor per matrix covering this
+    // piece's rows (reads past them return zeros without touching memory),
+    // per-lane offsets fixed for the piece, the block in the scalar offset.
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(a.keys + head_base * 128, 0, t_end * 256, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(a.values + head_base * 128, 0, t_end * 256, kBufferWord3);
+    const int koff = (t_begin + grp) * 256 + 16 * c;
+    const int voff = (t_begin + 8 * wave + vsub) * 256 + 16 * vcg;
+    auto load_block = [&](u32x4 (&k)[2], u32x4 (&v)[2], int i) {
+        k[0] = __builtin_amdgcn_raw_buffer_load_b128(krs, koff, 16384 * i, kLoadNT);
+        k[1] = __builtin_amdgcn_raw_buffer_load_b128(krs, koff + 128, 16384 * i, kLoadNT);
+        v[0] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, 16384 * i, kLoadNT);
+        v[1] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + 1024, 16384 * i, kLoadNT);
+    };
+    u32x4 kr[kInFlight][2], vr[kInFlight][2];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kInFlight && i < NB; ++i) load_block(kr[i], vr[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+
+    __shared__ float qp[2][128];
+    __shared__ float buf[4][128];
+    __shared__ float prob[2][64];
+    __shared__ __align__(16) float opart[8][2][128];
+    __shared__ uint16_t kcur[128], vcur[128];
+    __shared__ double red[4][2];
+    __shared__ float wm[8][2], wl[8][2];
+    __shared__ float mlv[2][kAttnSplits][2];
+    __shared__ float ovl[kAttnSplits][2][128];
+
+    // QK-norm + RoPE (engine/core.cpp:395-402); the last piece writes the
+    // new K/V row (403-406).
+    {
+        const float r = head_norm_rope(raw, nw, rc, rs, red[quarter], buf[quarter], j);
+        const bool owner = p == ns - 1;
+        if (quarter < 2) {
+            qp[quarter][kperm(j)] = r;
+        } else if (quarter == 2) {
+            const uint16_t bits = f2h(r);
+            kcur[kperm(j)] = bits;
+            if (owner) a.keys[(head_base + pos) * 128 + kperm(j)] = bits;
+        } else {
+            const uint16_t bits = f2h(raw_v);
+            vcur[j] = bits;
+            if (owner) a.values[(head_base + pos) * 128 + j] = bits;
+        }
+    }
+    __syncthreads();
+    // Lane c's query values in chain order: q[h][2i + e] multiplies half e
+    // of key word i (see key_chain).
+    float q[2][16];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int base = (i < 4 ? 8 * c : 64 + 8 * c) + 2 * (i & 3);
+            q[h][2 * i] = qp[h][base];
+            q[h][2 * i + 1] = qp[h][base + 1];
+        }
+
+    // Per-wave online softmax over the blocks: running maxima m (uniform in
+    // the wave), per-lane probability sums l (one position per block) and
+    // P.V sums acc, all rescaled by exp(m_old - m_new) when the maximum rises.
+    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
+    float acc[2][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[0][e] = acc[1][e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        u32x4(&k)[2] = kr[i % kInFlight];
+        u32x4(&v)[2] = vr[i % kInFlight];
+        if (64 * i < t_end - t_begin) {  // uniform: blocks past the piece hold no position
+            const int t = t_begin + 64 * i + grp;
+            uint32_t kw[8] = {k[0].x, k[0].y, k[0].z, k[0].w, k[1].x, k[1].y, k[1].z, k[1].w};
+            if (i == i_pos && t == pos) key_pieces_lds(kcur, c, kw);  // i == i_pos is uniform
+            float kf[16];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                kf[2 * e] = h2f(kw[e] & 0xffffu);
+                kf[2 * e + 1] = h2f(kw[e] >> 16);
+            }
+            float d[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float chain = 0.f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) chain = __builtin_fmaf(q[h][e], kf[e], chain);
+                d[h] = combine_chains(chain) * args.scale;
+            }
+            const bool valid = t < t_end;
+            const float s0 = valid ? d[0] : -INFINITY, s1 = valid ? d[1] : -INFINITY;
+            float b0 = fmaxf(s0, xor_lanes<8>(s0)), b1 = fmaxf(s1, xor_lanes<8>(s1));
+            b0 = fmaxf(b0, xor_lanes<16>(b0));
+            b1 = fmaxf(b1, xor_lanes<16>(b1));
+            b0 = fmaxf(b0, xor_lanes<32>(b0));
+            b1 = fmaxf(b1, xor_lanes<32>(b1));
+            const float n0 = fmaxf(m0, b0), n1 = fmaxf(m1, b1);
+            // A wave with no valid position yet keeps m = -inf and scale 1.
+            const float a0 = n0 == -INFINITY ? 1.f : expf(m0 - n0);
+            const float a1 = n1 == -INFINITY ? 1.f : expf(m1 - n1);
+            m0 = n0;
+            m1 = n1;
+            const float p0 = valid ? expf(s0 - n0) : 0.f;
+            const float p1 = valid ? expf(s1 - n1) : 0.f;
+            l0 = l0 * a0 + p0;
+            l1 = l1 * a1 + p1;
+            if (c == 0) {
+                prob[0][grp] = p0;
+                prob[1][grp] = p1;
+            }
+            // prob[][] of this wave's positions is written and read by this wave only.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                acc[0][e] *= a0;
+                acc[1][e] *= a1;
+            }
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int tl = 8 * wave + 4 * hf + vsub, tv = t_begin + 64 * i + tl;
+                if (tv < t_end) {
+                    const float q0 = prob[0][tl], q1 = prob[1][tl];
+                    uint32_t vw[4] = {v[hf].x, v[hf].y, v[hf].z, v[hf].w};
+                    if (i == i_pos && tv == pos) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            vw[e] = uint32_t(vcur[vcg * 8 + 2 * e]) | (uint32_t(vcur[vcg * 8 + 2 * e + 1]) << 16);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float v0 = h2f(vw[e] & 0xffffu), v1 = h2f(vw[e] >> 16);
+                        acc[0][2 * e] = __builtin_fmaf(v0, q0, acc[0][2 * e]);
+                        acc[0][2 * e + 1] = __builtin_fmaf(v1, q0, acc[0][2 * e + 1]);
+                        acc[1][2 * e] = __builtin_fmaf(v0, q1, acc[1][2 * e]);
+                        acc[1][2 * e + 1] = __builtin_fmaf(v1, q1, acc[1][2 * e + 1]);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        if (i + kInFlight < NB) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_block(k, v, i + kInFlight);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // Wave sums: the 8 position lanes of l, the 4 position groups of acc.
+    l0 += xor_lanes<8>(l0);
+    l1 += xor_lanes<8>(l1);
+    l0 += xor_lanes<16>(l0);
+    l1 += xor_lanes<16>(l1);
+    l0 += xor_lanes<32>(l0);
+    l1 += xor_lanes<32>(l1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            acc[h][e] += xor_lanes<16>(acc[h][e]);
+            acc[h][e] += xor_lanes<32>(acc[h][e]);
+        }
+    if (vsub == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; e += 4)
+                *reinterpret_cast<float4*>(&opart[wave][h][vcg * 8 + e]) =
+                    make_float4(acc[h][e], acc[h][e + 1], acc[h][e + 2], acc[h][e + 3]);
+    }
+    if (lane == 0) {
+        wm[wave][0] = m0;
+        wm[wave][1] = m1;
+        wl[wave][0] = l0;
+        wl[wave][1] = l1;
+    }
+    __syncthreads();
+    // Thread (half, j) of the first 256: output j of query head 2g + half,
+    // the 8 waves combined with weights exp(m_w - max) (0 for a wave that
+    // saw no position) in a fixed tree.
+    const int half = (tid >> 7) & 1;
+    float mx = wm[0][half];
+#pragma unroll
+    for (int v8 = 1; v8 < 8; ++v8) mx = fmaxf(mx, wm[v8][half]);
+    float wt[8];
+#pragma unroll
+    for (int v8 = 0; v8 < 8; ++v8) wt[v8] = wm[v8][half] == -INFINITY ? 0.f : expf(wm[v8][half] - mx);
+    auto tree = [&](auto f) {
+        return ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
+    };
+    const float o = tree([&](int v8) { return wt[v8] * opart[v8][half][j]; });
+    const float l = tree([&](int v8) { return wt[v8] * wl[v8][half]; });
+    float* out = a.attended + (2 * g + half) * 128;
+    if (ns == 1) {  // nothing to merge: normalize here
+        if (tid < 256) out[j] = o / l;
+        return;
+    }
+    auto part_of = [&](int split) { return a.xpart + ((size_t(g) * kAttnSplits + split) * 2 + half) * kXPart; };
+    if (p > 0) {
+        if (tid < 256) {
+            uint64_t* part = part_of(p);
+            exchange_put(part + j, o, a.tag);
+            if (j == 0) {
+                exchange_put(part + 128, mx, a.tag);
+                exchange_put(part + 129, l, a.tag);
+            }
+        }
+        return;
+    }
+
+    // Piece 0 merges. Output j of split k, head half, sits at
+    // head0 + k * kSplitWords + lane_word. Each poll gathers 8 splits per
+    // thread: threads 0-255 splits 1-8 (and every split's max or sum),
+    // threads 256-511 splits 9-16; a second poll takes splits 17-24 and
+    // 25-31. The outputs go to LDS, then threads 0-255 merge.
+    constexpr int kSplitWords = 2 * kXPart;
+    const uint64_t* head0 = a.xpart + size_t(g) * kAttnSplits * kSplitWords;
+    const unsigned lane_word = half * kXPart + j;
+    const bool upper = tid >= 256;
+    const int ms = j < 2 * kAttnSplits ? j >> 1 : 0;
+    const bool fetch_ml = !upper && j < 2 * kAttnSplits && ms > 0 && ms < ns;
+    bool ok = true;
+#pragma unroll
+    for (int round = 0; round < 2; ++round) {
+        const int first = 1 + 16 * round + (upper ? 8 : 0);
+        if (round == 1 && ns <= 17) break;  // uniform: no split past 16
+        float got[9];
+        unsigned want = 0;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            got[k] = 0.f;
+            if (k < 8 && first + k < min(ns, kAttnSplits)) want |= 1u << k;
+        }
+        const bool ml = round == 0 && fetch_ml;
+        if (ml) want |= 1u << 8;
+        // After a give-up, stop polling (the step is reported as stalled).
+        if (ok)
+            ok = exchange_gather_strided<9, kSplitWords>(head0 + first * kSplitWords, lane_word,
+                                                         ml ? part_of(ms) + 128 + (j & 1) : nullptr, a.tag, got, want);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (first + k < min(ns, kAttnSplits)) ovl[first + k][half][j] = got[k];
+        if (ml) mlv[half][ms][j & 1] = got[8];
+    }
+    if (!ok) *a.stall = 1;
+    if (tid == 0 || tid == 128) {
+        mlv[half][0][0] = mx;
+        mlv[half][0][1] = l;
+    }
+    if (!upper) ovl[0][half][j] = o;
+    __syncthreads();
+    if (upper) return;
+    // Groups of 8 splits against their own maximum, then the groups.
+    float gm[4], gl[4], go[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (8 * q + k < ns) m = fmaxf(m, mlv[half][8 * q + k][0]);
+        float ls = 0.f, os = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (8 * q + k < ns) {
+                const float wk = expf(mlv[half][8 * q + k][0] - m);
+                ls += wk * mlv[half][8 * q + k][1];
+                os += wk * ovl[8 * q + k][half][j];
+            }
+        gm[q] = m;
+        gl[q] = ls;
+        go[q] = os;
+    }
+    const float m2 = fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3]));
+    float lt = 0.f, ot = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (gm[q] != -INFINITY) {  // a group without splits adds nothing
+            const float wq = expf(gm[q] - m2);
+            lt += wq * gl[q];
+            ot += wq * go[q];
+        }
+    out[j] = ot / lt;
+}
+
+// Pieces per (sequence, head) and blocks per piece for a launch: one
+// workgroup per CU (256 / (8 count) pieces, at most kAttnSplits), each piece
+// an equal share of the longest sequence's blocks.
+inline void attn_batch_shape(int max_positions, int count, int& pieces, int& per) {
+    const int blocks = (max_positions + 63) / 64;
+    pieces = std::min(kAttnSplits, std::max(1, 256 / (kKVHeads * count)));
+    per = (blocks + pieces - 1) / pieces;
+}
+static_assert((kMaxContext + 63) / 64 <= 16 * 4, "16 blocks per piece cover the longest context at 4 pieces");
+
 __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* __restrict__ second,
                             uint16_t* __restrict__ dst, int rows, int cols) {
     const int nb = cols / 64;
@@ -2123,29 +2502,43 @@ void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const De
 void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
                             const float* cosines, const float* sines, hipStream_t stream) {
     require(count >= 1 && count <= kMaxBatch, "attention batch: 1..8 sequences");
-    AttnBatch b{};
-    int max_splits = 1;
+    AttnBatchArgs b{};
+    int max_positions = 1;
     for (int i = 0; i < count; ++i) {
-        AttnArgs& a = b.seq[i];
+        AttnBatchSeq& a = b.seq[i];
         a.qkv = seqs[i].qkv;
-        a.q_norm = q_norm;
-        a.k_norm = k_norm;
-        a.cosines = cosines;
-        a.sines = sines;
         a.keys = seqs[i].keys;
         a.values = seqs[i].values;
-        a.pos = seqs[i].pos;
-        a.partial = seqs[i].partial;
+        a.xpart = seqs[i].xpart;
         a.attended = seqs[i].attended;
+        a.stall = seqs[i].stall;
+        a.pos = seqs[i].pos;
         a.context = seqs[i].context;
-        a.scale = 1.0f / std::sqrt(128.0f);
+        a.tag = seqs[i].tag;
         require(a.pos >= 0 && a.pos < a.context, "attention batch: position outside the cache");
-        int chunk, splits;
-        attn_split(a.pos + 1, chunk, splits);
-        max_splits = std::max(max_splits, splits);
+        require(a.tag != 0, "attention batch: exchange tags are nonzero");
+        max_positions = std::max(max_positions, a.pos + 1);
     }
-    attn_decode_batch_kernel<<<dim3(max_splits, kKVHeads, count), 512, 0, stream>>>(b);
-    if (max_splits > 1) attn_merge_batch_kernel<<<dim3(kQHeads, count), 512, 0, stream>>>(b);
+    b.q_norm = q_norm;
+    b.k_norm = k_norm;
+    b.cosines = cosines;
+    b.sines = sines;
+    b.scale = 1.0f / std::sqrt(128.0f);
+    b.batch = count;
+    int pieces, per;
+    attn_batch_shape(max_positions, count, pieces, per);
+    require(pieces <= kAttnSplits, "attention batch: more pieces than the exchange holds");
+    b.pieces = pieces;
+    const dim3 grid(kKVHeads * count * pieces);
+    if (per <= 2) attn_batch_kernel<2><<<grid, 512, 0, stream>>>(b);
+    else if (per <= 4) attn_batch_kernel<4><<<grid, 512, 0, stream>>>(b);
+    else if (per <= 6) attn_batch_kernel<6><<<grid, 512, 0, stream>>>(b);
+    else if (per <= 9) attn_batch_kernel<9><<<grid, 512, 0, stream>>>(b);
+    else if (per <= 12) attn_batch_kernel<12><<<grid, 512, 0, stream>>>(b);
+    else {
+        require(per <= 16, "attention batch: more than 16 blocks per piece");
+        attn_batch_kernel<16><<<grid, 512, 0, stream>>>(b);
+    }
 }
 
 void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,

@@ -209,12 +209,8 @@ void Engine::init_state() {
     pair_.xm = device_alloc<float>(2 * kHidden);
     pair_.dparts = device_alloc<float>(size_t(2) * kFfnSlices * kHidden);
     pair_.exchange = device_alloc<uint64_t>(2 * kFFN);
-    // Exchange words start with tag 0, which no launch uses.
-    HIP_CHECK(hipMemsetAsync(s.exchange, 0, kFFN * sizeof(uint64_t), stream_));
-    HIP_CHECK(hipMemsetAsync(pair_.exchange, 0, 2 * kFFN * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(s.stall, 0, sizeof(int), stream_));
-    HIP_CHECK(hipMemsetAsync(s.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
-    HIP_CHECK(hipMemsetAsync(s.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
+    clear_exchanges();
 
     if (const char* env = std::getenv("QWEN_HIP_FUSED_FFN")) fused_ffn_ = std::string(env) != "0";
     if (const char* env = std::getenv("QWEN_HIP_FUSED_ATTENTION")) fused_attn_ = std::string(env) != "0";
@@ -294,9 +290,23 @@ void Engine::truncate(int position) {
 // `result_slot`. The step scalars are kernel arguments.
 // Exchange tags: every launch of a fused kernel takes the next one (never 0,
 // the cleared exchange), so no launch reads a word an earlier one wrote.
+// When the counter wraps, the exchanges are cleared again (on the engine's
+// stream, ahead of any launch that uses the new tags), so a word written
+// 2^32 launches earlier can never carry a reused tag.
 uint32_t Engine::next_tag() {
-    if (++ffn_tag_ == 0) ++ffn_tag_;
+    if (++ffn_tag_ == 0) {
+        clear_exchanges();
+        ffn_tag_ = 1;
+    }
     return ffn_tag_;
+}
+
+// Exchange words start with tag 0, which no launch uses.
+void Engine::clear_exchanges() {
+    HIP_CHECK(hipMemsetAsync(scratch_.exchange, 0, kFFN * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(pair_.exchange, 0, 2 * kFFN * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(scratch_.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(scratch_.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
 }
 
 LayerFlow Engine::layer_flow(int layer, bool pair) {
@@ -310,11 +320,11 @@ LayerFlow Engine::layer_flow(int layer, bool pair) {
     return f;
 }
 
-// A fused FFN launch whose exchange poll gave up leaves garbage in the
-// residual stream; the argmax of the step reports it.
+// A launch whose exchange poll gave up leaves garbage in the residual
+// stream; the argmax of the step reports it.
 void Engine::check_stall(int slot) const {
     if (result_host_[slot].stalled)
-        throw std::runtime_error("Decode step stalled: a fused FFN exchange did not complete");
+        throw std::runtime_error("Decode step stalled: an exchange between workgroups did not complete");
 }
 
 void Engine::run_token(int token, bool head, int result_slot) {
@@ -427,17 +437,19 @@ void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
     for (int i = 0; i < count; ++i) {
         Engine& e = *seqs[i];
         e.invalidate();
+        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_, {}};
+        // Tags come from each sequence's own counter: its exchange buffers
+        // are written by its single-sequence launches too.
+        for (int l = 0; l < kLayers; ++l) bs[i].tags[l] = e.next_tag();
         HIP_CHECK(hipStreamSynchronize(e.stream_));
-        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_};
     }
     Engine& lead = *seqs[0];
     launch_decode_batch(bs, count, lead.embed_, lead.final_norm_, lead.cosines_, lead.sines_, lead.stream_);
     HIP_CHECK(hipGetLastError());
     lead.sync();
-    for (int i = 0; i < count; ++i) {
-        ++seqs[i]->pos_;
-        seqs[i]->has_logits_ = true;
-    }
+    for (int i = 0; i < count; ++i) ++seqs[i]->pos_;
+    for (int i = 0; i < count; ++i) seqs[i]->check_stall(0);  // as append: no logits after a stall
+    for (int i = 0; i < count; ++i) seqs[i]->has_logits_ = true;
 }
 
 int Engine::greedy() {

@@ -95,6 +95,7 @@ private:
     void run_pair(int first, int second);
     LayerFlow layer_flow(int layer, bool pair = false);
     uint32_t next_tag();
+    void clear_exchanges();
     void check_stall(int slot) const;
     void release();
     void sync();

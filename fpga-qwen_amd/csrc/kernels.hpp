@@ -206,16 +206,17 @@ struct AttnSeq {
     const float* qkv;   // raw projections [4096]
     uint16_t* keys;     // this layer's cache [8][context][128]
     uint16_t* values;
-    float* partial;     // [8][kAttnSplits][kAttnPartial]
+    uint64_t* xpart;    // [kXPartWords] tagged split partials
     float* attended;    // [2048] normalized output
+    int* stall;         // set if a merge gave up waiting for a split's partial
     int pos;            // position being written
     int context;
+    uint32_t tag;       // nonzero, unique per launch for this sequence's exchange
 };
 
 // Decode attention of up to kMaxBatch sequences in one launch (split
-// attention for every context length) plus the merge of their splits into
-// `attended`; per sequence the same arithmetic as the split path of one
-// sequence.
+// attention for every context length, the splits of each sequence and KV
+// head merged inside the launch) into `attended`.
 void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
                             const float* cosines, const float* sines, hipStream_t stream);
 
