@@ -37,27 +37,23 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;  // waves of the K = 1024 kernels (norm prologues, lm_head)
+using dev::exchange_gather;
+using dev::exchange_put;
 using dev::xor_lanes;
-
-__device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-enum BatchMode { kBPlain, kBQKV, kBO, kBGateUp, kBDown, kBLmHead };
+enum BatchMode { kBPlain, kBGateUp, kBLmHead };
 
 struct BatchGemvArgs {
     const uint16_t* w;                 // natural [rows x K]; gate/up: 3072 gate rows then 3072 up rows
-    const float* norm_w;               // RMSNorm weights (QKV, gate/up, lm_head)
-    const float* in[kMaxBatch];        // input rows: x (norm modes), attention output (O), activation (down)
-    const uint16_t* embed[kMaxBatch];  // QKV of the first layer: embedding rows instead of x
-    float* out[kMaxBatch];             // output rows (plain, QKV, gate/up: activation, lm_head: logits)
-    float* x[kMaxBatch];               // residual rows (O and down add; first layer stores E[token])
+    const float* norm_w;               // RMSNorm weights (gate/up, lm_head)
+    const float* in[kMaxBatch];        // input rows: x (norm modes), activation (down)
+    float* out[kMaxBatch];             // output rows (plain, gate/up: activation, lm_head: logits)
     float* hidden[kMaxBatch];          // lm_head: final normalized rows
     float* lm_value;                   // lm_head argmax partials [groups][kMaxBatch]
     int* lm_index;
     int* lm_bad;
-    float* slices[kMaxBatch];          // down with K slices: [3][1024] partial sums per sequence (output)
-    const float* pending[kMaxBatch];   // QKV, O: the previous layer's down slices still to add, or null
     int batch;
 };
 
@@ -67,22 +63,15 @@ struct BatchGemvArgs {
 // pass (one barrier for the 8 norms) and stages FP16 hi / lo with 8-byte LDS
 // stores; the weights are issued right after the inputs, so their HBM round
 // trip overlaps the prologue.
-// SPLITK > 1 (down): workgroup (tile, blockIdx.y) multiplies one slice of
-// K / SPLITK = 1024 columns and stores its partial sums in the sequence's
-// slice buffer; the next layer's QKV prologue adds them to the residual it
-// normalizes, and its O epilogue adds them into the residual stream (both in
-// slice order), so no workgroup waits for another.
-template <int K, int MODE, int RT = 1, int SPLITK = 1>
-__global__ __launch_bounds__(K / SPLITK / 4) void bgemv_kernel(const BatchGemvArgs a) {
-    constexpr bool kNorm = MODE == kBQKV || MODE == kBGateUp || MODE == kBLmHead;
+template <int K, int MODE, int RT = 1>
+__global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
+    constexpr bool kNorm = MODE == kBGateUp || MODE == kBLmHead;
     constexpr int kTiles = MODE == kBGateUp ? 2 : RT;
     static_assert(MODE == kBGateUp ? RT == 1 : RT >= 1, "gate/up pairs one gate tile with one up tile");
-    static_assert(SPLITK == 1 || (MODE == kBDown && SPLITK == kBatchSplitMax && RT == 1),
-                  "K slices for the down projection");
-    constexpr int KS = K / SPLITK;  // this workgroup's columns
+    constexpr int KS = K;
     constexpr int WAVES = KS / 256, THREADS = 64 * WAVES, KW = 256, kBlocks = KW / 128, F4 = 1;
     static_assert(KS % 1024 == 0 && (!kNorm || WAVES == kWaves), "one wave per 256 columns; norms with 4 waves");
-    const int k0 = KS * int(blockIdx.y);
+    constexpr int k0 = 0;
     __shared__ __align__(16) _Float16 xh[kMaxBatch][KS + 8];
     __shared__ __align__(16) _Float16 xl[kMaxBatch][KS + 8];
     __shared__ double red[kWaves][kMaxBatch];
@@ -104,53 +93,13 @@ __global__ __launch_bounds__(K / SPLITK / 4) void bgemv_kernel(const BatchGemvAr
 #pragma unroll
         for (int i = 0; i < F4; ++i) {
             const int j4 = tid + THREADS * i;
-            if constexpr (MODE == kBQKV) {
-                if (a.embed[bb]) {
-                    const uint2 e = reinterpret_cast<const uint2*>(a.embed[bb])[j4];
-                    v[b][i] = make_float4(h2f(e.x & 0xffffu), h2f(e.x >> 16), h2f(e.y & 0xffffu), h2f(e.y >> 16));
-                    continue;
-                }
-            }
             v[b][i] = reinterpret_cast<const float4*>(a.in[bb] + k0)[j4];
-        }
-    }
-    if constexpr (MODE == kBQKV) {
-        // The residual the norm sees: x plus the previous layer's down slices
-        // (((s0 + s1) + s2), added as the O epilogue will add them).
-        float4 sl[kMaxBatch][kBatchSplitMax];
-#pragma unroll
-        for (int b = 0; b < kMaxBatch; ++b) {
-            const int bb = min(b, B - 1);
-            if (a.pending[bb]) {
-#pragma unroll
-                for (int z = 0; z < kBatchSplitMax; ++z)
-                    sl[b][z] = reinterpret_cast<const float4*>(a.pending[bb] + z * kHidden)[tid];
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < kMaxBatch; ++b) {
-            const int bb = min(b, B - 1);
-            if (a.pending[bb]) {
-                const float4 s01 = make_float4(sl[b][0].x + sl[b][1].x, sl[b][0].y + sl[b][1].y,
-                                               sl[b][0].z + sl[b][1].z, sl[b][0].w + sl[b][1].w);
-                v[b][0] = make_float4(v[b][0].x + (s01.x + sl[b][2].x), v[b][0].y + (s01.y + sl[b][2].y),
-                                      v[b][0].z + (s01.z + sl[b][2].z), v[b][0].w + (s01.w + sl[b][2].w));
-            }
         }
     }
     float4 wn[F4];
     if constexpr (kNorm) {
 #pragma unroll
         for (int i = 0; i < F4; ++i) wn[i] = reinterpret_cast<const float4*>(a.norm_w)[tid + THREADS * i];
-    }
-    float xres = 0.f, pend[kBatchSplitMax] = {};
-    if constexpr (MODE == kBO || (MODE == kBDown && SPLITK == 1)) xres = a.x[min(eb, B - 1)][o0 + erow];
-    if constexpr (MODE == kBO) {
-        const float* pb = a.pending[min(eb, B - 1)];
-        if (pb) {
-#pragma unroll
-            for (int z = 0; z < kBatchSplitMax; ++z) pend[z] = pb[z * kHidden + o0 + erow];
-        }
     }
     u32x4 wa[kTiles][kBlocks][4];
     __builtin_amdgcn_sched_barrier(0);
@@ -209,16 +158,6 @@ __global__ __launch_bounds__(K / SPLITK / 4) void bgemv_kernel(const BatchGemvAr
         if (tid < kMaxBatch) {
             const double total = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
             inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(K) + 1e-6f);
-        }
-        if constexpr (MODE == kBQKV) {
-            if (blockIdx.x == 0) {  // first layer: keep fp32(E[token]) as the residual stream
-#pragma unroll
-                for (int b = 0; b < kMaxBatch; ++b)
-                    if (b < B && a.embed[b]) {
-#pragma unroll
-                        for (int i = 0; i < F4; ++i) reinterpret_cast<float4*>(a.x[b])[tid + THREADS * i] = v[b][i];
-                    }
-            }
         }
         __syncthreads();
 #pragma unroll
@@ -305,18 +244,8 @@ __global__ __launch_bounds__(K / SPLITK / 4) void bgemv_kernel(const BatchGemvAr
     }
     const bool live = eb < B;
     const int eo = o0 + erow;
-    if constexpr (MODE == kBPlain || MODE == kBQKV) {
+    if constexpr (MODE == kBPlain) {
         if (live) a.out[eb][eo] = y[0];
-    } else if constexpr (MODE == kBO) {
-        if (live) {
-            const float base = a.pending[eb] ? xres + ((pend[0] + pend[1]) + pend[2]) : xres;
-            a.x[eb][eo] = base + y[0];
-        }
-    } else if constexpr (MODE == kBDown) {
-        if (live) {
-            if constexpr (SPLITK == 1) a.x[eb][eo] = xres + y[0];
-            else a.slices[eb][blockIdx.y * kHidden + eo] = y[0];
-        }
     } else if constexpr (MODE == kBGateUp) {
         if (live) {  // SwiGLU (engine/core.cpp:636-639)
             const float gate = y[0], up = y[1];
@@ -365,6 +294,184 @@ __global__ __launch_bounds__(K / SPLITK / 4) void bgemv_kernel(const BatchGemvAr
     }
 }
 
+// Residual projections of the batched step, x += W in, as 256 workgroups,
+// one per CU: workgroup w = x + 8 (4 t + q) computes output rows
+// 16 (x + 8 t) .. + 15 over the K quarter q, so the 4 quarters of a row tile
+// share XCD x. The inputs enter the matrix cores as FP16 hi + lo, as in
+// bgemv_kernel (v_mfma_f32_16x16x32_f16, A = 16 weight rows, B = the
+// sequences; each of the 4 waves takes a quarter of the quarter's columns,
+// summed in fixed order). Quarters 1-3 post their 16 x 8 sums as tagged
+// words in the XCD's L2; quarter 0 adds them in fixed order
+// ((q0 + q1) + (q2 + q3)) to the residual and writes the residual stream.
+//   kRO: the O projection (engine/core.cpp:625-626), K = 2048, quarter q =
+//        query heads 4q .. 4q + 3, with the merge of the attention pieces in
+//        the prologue: each (sequence, head) is merged by 8 threads (16
+//        channels each) from the pieces' (output, max, sum): out =
+//        sum_p e_p o_p / sum_p e_p l_p with e_p = exp(m_p - max), pieces in
+//        order, in chunks of 4 (a later chunk rescales the running sums).
+//   kRDown: the down projection (engine/core.cpp:640-641), K = 3072, input
+//        the SwiGLU activations.
+enum ResidualMode { kRO, kRDown };
+
+struct ResidualArgs {
+    const uint16_t* w;                 // natural [1024 x K]
+    const float* in[kMaxBatch];        // kRO: attention pieces [8][kAttnSplits][kAttnPartial]; kRDown: act [3072]
+    float* x[kMaxBatch];               // residual rows
+    uint64_t* exchange;                // [64 tiles][3][128] tagged quarter sums
+    int* stall;
+    int pieces[kMaxBatch];             // kRO: pieces with positions per sequence
+    int batch;
+    uint32_t tag;
+};
+
+constexpr int kResidualExchangeWords = 64 * 3 * 128;  // 64 row tiles x quarters 1-3 x 16 rows x 8 sequences
+static_assert(kHidden / kBatchRows == 64 && kQDim / 4 == 4 * kHeadDim, "64 row tiles; O quarters of 4 heads");
+
+template <int MODE>
+__global__ __launch_bounds__(256) void residual_kernel(const ResidualArgs a) {
+    constexpr int K = MODE == kRO ? kQDim : kFFN, KQ = K / 4, CW = KQ / 4, STEPS = CW / 32;
+    static_assert(CW % 32 == 0, "whole MFMA steps per wave");
+    const int xcd = blockIdx.x & 7, i = blockIdx.x >> 3, qk = i & 3;
+    const int o0 = kBatchRows * (xcd + 8 * (i >> 2)), k0 = KQ * qk;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, quad = lane >> 4;
+    const int B = a.batch;
+    // Epilogue element of this thread: row o0 + erow, sequence eb.
+    const int eb = lane & 15, erow = 4 * (lane >> 4) + wave;
+    const bool live = eb < B;
+    __shared__ __align__(16) _Float16 xh[kMaxBatch][KQ + 8];
+    __shared__ __align__(16) _Float16 xl[kMaxBatch][KQ + 8];
+    // Stages 8 input values of sequence bb at quarter column kk as hi / lo.
+    auto stage8 = [&](int bb, int kk, const float (&v)[8]) {
+        half8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 h, l;
+            split_half(v[e], h, l);
+            hi[e] = h;
+            lo[e] = l;
+        }
+        *reinterpret_cast<half8*>(&xh[bb][kk]) = hi;
+        *reinterpret_cast<half8*>(&xl[bb][kk]) = lo;
+    };
+
+    // Loads complete in issue order per wave: the inputs, then the weights,
+    // then the residual entries of quarter 0.
+    u32x4 wa[STEPS];
+    auto load_weights = [&] {
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(o0 + col) * K + k0 + CW * wave) + quad;
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) wa[st] = __builtin_nontemporal_load(wp + 4 * st);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    float xres = 0.f;
+    if constexpr (MODE == kRO) {
+        // Merge layout: sequence mb, head 4 qk + mh, channels 16 mc .. 16 mc + 15.
+        const int mb = tid >> 5, mh = (tid >> 3) & 3, mc = tid & 7;
+        const int head = 4 * qk + mh;
+        const int np = mb < B ? a.pieces[mb] : 0;
+        const float* pbase = a.in[min(mb, B - 1)] + size_t(head >> 1) * kAttnSplits * kAttnPartial + (head & 1) * 132;
+        float4 ov[4][4];
+        float mv[4], lv[4];
+        auto load_chunk = [&](int p0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float* e = pbase + size_t(min(p0 + k, max(np - 1, 0))) * kAttnPartial;
+                if (np > 0) {
+                    mv[k] = e[128];
+                    lv[k] = e[129];
+#pragma unroll
+                    for (int c4 = 0; c4 < 4; ++c4) ov[k][c4] = reinterpret_cast<const float4*>(e + 16 * mc)[c4];
+                }
+            }
+        };
+        load_chunk(0);
+        load_weights();
+        if (qk == 0 && live) xres = a.x[eb][o0 + erow];
+        // Online merge over chunks of 4 pieces (one chunk when there are at most 4).
+        float run_m = -INFINITY, run_l = 0.f, run_o[16] = {};
+        for (int p0 = 0; p0 < np; p0 += 4) {
+            if (p0 > 0) load_chunk(p0);
+            float cm = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (p0 + k < np) cm = fmaxf(cm, mv[k]);
+            const float nm = fmaxf(run_m, cm);
+            const float sc = run_m == -INFINITY ? 0.f : expf(run_m - nm);
+            run_l *= sc;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) run_o[c] *= sc;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (p0 + k < np) {
+                    const float e = expf(mv[k] - nm);
+                    run_l += e * lv[k];
+                    const float o16[16] = {ov[k][0].x, ov[k][0].y, ov[k][0].z, ov[k][0].w, ov[k][1].x, ov[k][1].y,
+                                           ov[k][1].z, ov[k][1].w, ov[k][2].x, ov[k][2].y, ov[k][2].z, ov[k][2].w,
+                                           ov[k][3].x, ov[k][3].y, ov[k][3].z, ov[k][3].w};
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) run_o[c] += e * o16[c];
+                }
+            run_m = nm;
+        }
+#pragma unroll
+        for (int z = 0; z < 2; ++z) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = np > 0 ? run_o[8 * z + e] / run_l : 0.f;
+            stage8(mb, 128 * mh + 16 * mc + 8 * z, v);
+        }
+    } else {
+        // Activation layout: sequence tid / 32, columns 24 (tid % 32) .. + 23.
+        const int bb = tid >> 5, c0 = 24 * (tid & 31);
+        const float4* src = reinterpret_cast<const float4*>(a.in[min(bb, B - 1)] + k0 + c0);
+        float4 av[6];
+#pragma unroll
+        for (int z = 0; z < 6; ++z) av[z] = src[z];
+        load_weights();
+        if (qk == 0 && live) xres = a.x[eb][o0 + erow];
+#pragma unroll
+        for (int z = 0; z < 3; ++z) {
+            const float v[8] = {av[2 * z].x,     av[2 * z].y,     av[2 * z].z,     av[2 * z].w,
+                                av[2 * z + 1].x, av[2 * z + 1].y, av[2 * z + 1].z, av[2 * z + 1].w};
+            stage8(bb, c0 + 8 * z, v);
+        }
+    }
+    __syncthreads();
+
+    // 16 output rows x 8 sequences over this wave's CW columns (k slot
+    // (quad, e) of step st holds column CW wave + 32 st + 8 quad + e).
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+        const int k = CW * wave + 32 * st + 8 * quad;
+        const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
+        const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+        const half8 w8 = __builtin_bit_cast(half8, wa[st]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);
+    }
+    __shared__ float part[4][64][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[wave][lane][r] = acc[r];
+    __syncthreads();
+    const float y = (part[0][lane][wave] + part[1][lane][wave]) + (part[2][lane][wave] + part[3][lane][wave]);
+
+    uint64_t* tile_words = a.exchange + size_t(o0 / kBatchRows) * 3 * 128;
+    const int word = erow * kMaxBatch + eb;
+    if (qk > 0) {
+        if (live) exchange_put(tile_words + (qk - 1) * 128 + word, y, a.tag);
+        return;
+    }
+    const uint64_t* const words[3] = {tile_words + word, tile_words + 128 + word, tile_words + 256 + word};
+    float got[3] = {0.f, 0.f, 0.f};
+    const bool ok = exchange_gather<3>(words, a.tag, got, live ? 7u : 0u);
+    if (!ok) *a.stall = 1;
+    if (live) a.x[eb][o0 + erow] = xres + ((y + got[0]) + (got[1] + got[2]));
+}
+
 // Second pass of the per-sequence greedy selection.
 struct BatchResults {
     ArgmaxResult* device[kMaxBatch];
@@ -410,12 +517,11 @@ __global__ __launch_bounds__(1024) void batch_argmax_kernel(const float* __restr
     }
 }
 
-template <int K, int MODE, int RT = 1, int SPLITK = 1>
+template <int K, int MODE, int RT = 1>
 void bgemv(const BatchGemvArgs& a, int rows, hipStream_t stream) {
     require(a.batch >= 1 && a.batch <= kMaxBatch, "batched GEMV: 1..8 rows");
     require(rows % (kBatchRows * RT) == 0 && rows > 0, "batched GEMV: rows must be a positive multiple of the tile rows");
-    require(SPLITK == 1 || rows == kHidden, "batched GEMV: K slices for the down projection only");
-    bgemv_kernel<K, MODE, RT, SPLITK><<<dim3(rows / (kBatchRows * RT), SPLITK), K / SPLITK / 4, 0, stream>>>(a);
+    bgemv_kernel<K, MODE, RT><<<rows / (kBatchRows * RT), K / 4, 0, stream>>>(a);
 }
 
 }  // namespace
@@ -438,41 +544,43 @@ void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, 
 }
 
 void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const float* final_norm,
-                         const float* cosines, const float* sines, hipStream_t stream) {
+                         const float* cosines, const float* sines, const uint32_t* tags, hipStream_t stream) {
     require(count >= 1 && count <= kMaxBatch, "batched decode: 1..8 sequences");
+    for (int l = 0; l < kBatchTagsPerLayer * kLayers; ++l) require(tags[l] != 0, "batched decode: exchange tags are nonzero");
+    static_assert(kXPartWords >= kResidualExchangeWords + kKVHeads * kMaxBatch * 512,
+                  "the residual quarter and q/k/v exchanges fit the lead sequence's partial words");
     for (int l = 0; l < kLayers; ++l) {
         const LayerDevice& W = seqs[0].layers[l];  // weights are shared; K/V are per sequence
-        BatchGemvArgs q{};
-        q.w = W.qkv_n;
-        q.norm_w = W.in_norm;
-        q.batch = count;
-        for (int b = 0; b < count; ++b) {
-            const DecodeScratch& s = seqs[b].s;
-            q.in[b] = s.x;
-            q.embed[b] = l == 0 ? embed + size_t(seqs[b].token) * kHidden : nullptr;
-            q.out[b] = s.qkv;
-            q.x[b] = s.x;
-            q.pending[b] = l > 0 ? s.o_part : nullptr;  // the previous layer's down slices
-        }
-        bgemv<kHidden, kBQKV>(q, kQKVRows, stream);
-
         AttnSeq as[kMaxBatch];
+        int positions[kMaxBatch];
         for (int b = 0; b < count; ++b) {
             const DecodeScratch& s = seqs[b].s;
-            as[b] = AttnSeq{s.qkv,   seqs[b].layers[l].keys, seqs[b].layers[l].values, s.xpart,
-                            s.attended, s.stall, seqs[b].pos, seqs[b].context, seqs[b].tags[l]};
+            as[b] = AttnSeq{s.x,
+                            l == 0 ? embed + size_t(seqs[b].token) * kHidden : nullptr,
+                            s.x,
+                            seqs[b].layers[l].keys,
+                            seqs[b].layers[l].values,
+                            s.attn_partial,
+                            seqs[b].pos,
+                            seqs[b].context};
+            positions[b] = seqs[b].pos + 1;
         }
-        launch_attention_batch(as, count, W.q_norm, W.k_norm, cosines, sines, stream);
+        launch_qkv_attention_batch(as, count, W.qkv_n, W.in_norm, W.q_norm, W.k_norm, cosines, sines,
+                                   seqs[0].s.xpart + kResidualExchangeWords, seqs[0].s.stall, tags[3 * l], stream);
 
-        BatchGemvArgs o{};
+        ResidualArgs o{};
         o.w = W.o_n;
         o.batch = count;
+        o.exchange = seqs[0].s.xpart;
+        o.stall = seqs[0].s.stall;
+        o.tag = tags[3 * l + 1];
+        int per;
+        attn_batch_pieces(positions, count, o.pieces, per);
         for (int b = 0; b < count; ++b) {
-            o.in[b] = seqs[b].s.attended;
+            o.in[b] = seqs[b].s.attn_partial;
             o.x[b] = seqs[b].s.x;
-            o.pending[b] = l > 0 ? seqs[b].s.o_part : nullptr;
         }
-        bgemv<kQDim, kBO>(o, kHidden, stream);
+        residual_kernel<kRO><<<256, 256, 0, stream>>>(o);
 
         BatchGemvArgs gu{};
         gu.w = W.gateup_n;
@@ -484,20 +592,17 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
         }
         bgemv<kHidden, kBGateUp>(gu, kFFN, stream);
 
-        BatchGemvArgs d{};
+        ResidualArgs d{};
         d.w = W.down_n;
         d.batch = count;
+        d.exchange = seqs[0].s.xpart;
+        d.stall = seqs[0].s.stall;
+        d.tag = tags[3 * l + 2];
         for (int b = 0; b < count; ++b) {
             d.in[b] = seqs[b].s.act;
             d.x[b] = seqs[b].s.x;
-            d.slices[b] = seqs[b].s.o_part;  // [3][1024] of the sequence's partial buffer
         }
-        // K slices leave their partial sums for the next layer; the last
-        // layer's down adds into the residual itself (the lm_head reads it).
-        if (l + 1 < kLayers)
-            bgemv<kFFN, kBDown, 1, kBatchSplitMax>(d, kHidden, stream);
-        else
-            bgemv<kFFN, kBDown>(d, kHidden, stream);
+        residual_kernel<kRDown><<<256, 256, 0, stream>>>(d);
     }
     BatchGemvArgs lm{};
     lm.w = embed;  // tied head (engine/core.cpp:643-645)

@@ -17,15 +17,19 @@ struct BatchSeq {
     int token;                  // id consumed at pos
     int context;                // K/V cache capacity
     ArgmaxResult* host_out;     // pinned slot for the greedy selection
-    uint32_t tags[kLayers];     // per layer: the attention exchange tag (nonzero, unique per launch)
 };
 
-// One decode step for each sequence: 28 x (norm+QKV skinny GEMM, batched
-// attention, O skinny GEMM + residual, norm+gate/up skinny GEMM + SwiGLU,
-// down skinny GEMM + residual), final norm + tied lm_head + per-sequence
-// argmax. Logits, hidden and selections land in each sequence's buffers.
+// Exchange tags a batched step takes per layer (attention, O, down).
+inline constexpr int kBatchTagsPerLayer = 3;
+
+// One decode step for each sequence: 28 x (norm + QKV + attention pieces in
+// one launch, piece merge + O + residual, norm + gate/up + SwiGLU, down +
+// residual), final norm + tied lm_head + per-sequence argmax. Logits, hidden
+// and selections land in each sequence's buffers. tags[3 l .. 3 l + 2]
+// (nonzero, unique per launch) tag layer l's exchanges between workgroups,
+// which use the first sequence's buffers.
 void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const float* final_norm,
-                         const float* cosines, const float* sines, hipStream_t stream);
+                         const float* cosines, const float* sines, const uint32_t* tags, hipStream_t stream);
 
 // Y[b] = W X[b] for b < batch on the matrix cores (W natural row-major
 // [rows x cols] FP16, X [batch x cols] FP32, Y [batch x rows] FP32); rows a

@@ -32,6 +32,10 @@ namespace {
 
 using namespace dev;
 
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 // Residual stream entry x + the 16 per-query-head partial O projections of
 // the fused attention kernel, summed in a fixed tree order (every kernel
 // that reads the entry gets the same value).
@@ -362,46 +366,6 @@ __global__ __launch_bounds__(SEG * 32) void gemv_seg_kernel(const GemvArgs a) {
             else a.x[row] = xres + y;
         }
     }
-}
-
-// Exchange between the workgroups of one XCD. A launch's workgroups are
-// dispatched round-robin over the 8 XCDs (workgroup w on XCD w % 8, measured
-// on this chip also right after launches of odd sizes), whose CUs share the
-// XCD's L2. A plain store reaches that L2 (the vector L1 is write-through),
-// and an agent-scope load skips the reader's L1 and finds the line there.
-// (Invalidating L1 with buffer_inv sc0 does not work here: outside
-// thread-group-split mode it leaves the stale line in place.) Each value
-// travels with its launch's tag in one 8-byte store, so a word left by an
-// earlier launch is never taken for a fresh one: placement decides only
-// whether a value arrives, never which value is read. Polls are bounded; a
-// consumer that gives up raises the stall flag, which the step's argmax
-// copies to the host. Measured: 0.40 us per exchange inside an XCD, against
-// 2.37 us per dependent kernel launch.
-constexpr unsigned kExchangeSpins = 1u << 18;  // ~0.1 s of polling; an exchange takes about a microsecond
-
-__device__ __forceinline__ void exchange_put(uint64_t* p, float v, uint32_t tag) {
-    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// Two consecutive tagged words; false if they did not both carry `tag`
-// within kExchangeSpins polls. The loop runs while any lane of the wave still
-// waits (a wave-uniform exit), and each lane's result comes from its own
-// flag: lanes leaving a loop at different iterations would otherwise hand the
-// compiler a divergent loop exit for the result.
-__device__ __forceinline__ bool exchange_get2(const uint64_t* p, uint32_t tag, float& a, float& b) {
-    unsigned missing = 1;
-    for (unsigned spin = 0; spin < kExchangeSpins && __any(missing); ++spin) {
-        if (missing) {
-            const uint64_t u = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint64_t w = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (uint32_t(u >> 32) == tag && uint32_t(w >> 32) == tag) {
-                a = __uint_as_float(uint32_t(u));
-                b = __uint_as_float(uint32_t(w));
-                missing = 0;
-            }
-        }
-    }
-    return missing == 0;
 }
 
 struct FfnArgs {
@@ -1132,53 +1096,6 @@ __global__ __launch_bounds__(512) void attn_o_kernel(const AttnArgs a) {
     }
 }
 
-// N tagged words at once: every round issues the loads of all words still
-// missing (bit k of `want`), then checks them, so a round costs one L2 round
-// trip however many words there are. False if some word did not carry `tag`
-// within kExchangeSpins rounds.
-template <int N>
-__device__ __forceinline__ bool exchange_gather(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N],
-                                                unsigned want) {
-    // Wave-uniform loop exit, per-lane result from `want` (see exchange_get2).
-    for (unsigned spin = 0; spin < kExchangeSpins && __any(want != 0); ++spin) {
-        uint64_t u[N];
-#pragma unroll
-        for (int k = 0; k < N; ++k)
-            u[k] = (want >> k) & 1 ? __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-#pragma unroll
-        for (int k = 0; k < N; ++k)
-            if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
-                out[k] = __uint_as_float(uint32_t(u[k]));
-                want &= ~(1u << k);
-            }
-    }
-    return want == 0;
-}
-
-// The same for words base + k STRIDE + off (k < N, bit k of `want`) with
-// `base` uniform and `off` per lane, so every address is a scalar base plus
-// one 32-bit lane offset; with `extra` non-null, bit N - 1 is the word at
-// `extra` instead.
-template <int N, int STRIDE>
-__device__ __forceinline__ bool exchange_gather_strided(const uint64_t* base, unsigned off, const uint64_t* extra,
-                                                        uint32_t tag, float (&out)[N], unsigned want) {
-    for (unsigned spin = 0; spin < kExchangeSpins && __any(want != 0); ++spin) {
-        uint64_t u[N];
-#pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const uint64_t* w = k == N - 1 && extra ? extra : base + k * STRIDE + off;
-            u[k] = (want >> k) & 1 ? __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-        }
-#pragma unroll
-        for (int k = 0; k < N; ++k)
-            if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
-                out[k] = __uint_as_float(uint32_t(u[k]));
-                want &= ~(1u << k);
-            }
-    }
-    return want == 0;
-}
-
 // Contexts of up to this many 64-position passes take the fused kernel's
 // FULL form (every workgroup attends its head over all positions).
 constexpr int kFullAttnPasses = 4;
@@ -1723,51 +1640,60 @@ __global__ __launch_bounds__(512) void qkv_attn_kernel(const QkvAttnArgs a) {
     if (opart_id == 0) a.o_part[h * kHidden + orow] = y;
 }
 
-// Batched decode attention with the merge of the position splits in the
-// same launch (up to kMaxBatch sequences, each with its own position and
-// cache). Workgroup w = g + 8 (b + B p): KV head g of sequence b, piece p of
-// its positions. All pieces of one (sequence, head) have the same w % 8 and
-// therefore run on one XCD. The grid holds one workgroup per CU: a CU serves
-// its loads in order, so a single workgroup per CU that keeps its own stream
-// of K/V rows in flight (kInFlight 64-position blocks, the loads of block
-// i + kInFlight issued once block i is consumed) overlaps its arithmetic with
-// the stream, where several workgroups per CU would each wait behind the
-// others' loads. Block layout as in the single-sequence split kernel: the 8
-// lanes of position t score it (lane c = chain c of the reference dot,
-// engine/core.cpp:612, key values converted once for both heads), and the
-// wave that scored 8 positions multiplies their V rows (4 positions x 16
-// channel groups per load). Softmax (613-620) runs online per wave: each wave
-// keeps its own running maximum, rescaling its sums when it rises, and the 8
-// waves' sums are combined with weights exp(m_w - max) in a fixed tree.
-// Pieces p > 0 post (output, max, sum) of both query heads as tagged words
-// in the sequence's exchange; piece 0 computes its own partial, gathers the
-// others from L2 and merges them in groups of 8 against their own maximum,
-// then the groups, in fixed order (all pieces are resident, so every poll
-// ends). The last piece writes the new K/V row.
+// Batched decode: norm + QKV projection + attention of one layer for up to
+// kMaxBatch sequences, each with its own position and cache. Workgroup w =
+// g + 8 (b + B p): KV head g of sequence b, piece p of its positions; the
+// W = B x pieces workgroups of KV head g share XCD g.
+//
+// QKV: every workgroup forms RMSNorm(x) of all sequences (engine/core.cpp
+// 207-215, 390; FP32 squares summed in FP64; x is the embedding row in the
+// first layer) as FP16 hi + lo in LDS, and computes 16 of the 512 q/k/v rows of KV head g (query
+// heads 2g and 2g + 1, key g, value g) on the matrix cores
+// (v_mfma_f32_16x16x32_f16, A = weight rows, B = the sequences, the 8 waves
+// splitting K, summed in a fixed tree); the rows travel as tagged words
+// through the XCD's L2 to the workgroups that attend with them.
+//
+// Attention: one workgroup per CU. A CU serves its loads in order, so a
+// single workgroup per CU that keeps its own stream of K/V rows in flight
+// (kInFlight 64-position blocks, the loads of block i + kInFlight issued
+// once block i is consumed) overlaps the q/k/v exchange and its arithmetic
+// with the stream. Block layout as in the single-sequence
+// split kernel: the 8 lanes of position t score it (lane c = chain c of the
+// reference dot, engine/core.cpp:612, key values converted once for both
+// heads), and the wave that scored 8 positions multiplies their V rows (4
+// positions x 16 channel groups per load). Softmax (613-620) runs online per
+// wave: each wave keeps its own running maximum, rescaling its sums when it
+// rises, and the 8 waves' sums are combined with weights exp(m_w - max) in a
+// fixed tree. Every piece writes (unnormalized output, max, sum) of both
+// query heads to the sequence's partial buffer; the batched O projection
+// merges the pieces in its prologue. The last piece writes the new K/V row.
 struct AttnBatchSeq {
-    const float* qkv;   // raw projections [4096]
-    uint16_t* keys;     // layer base [8][context][128]
+    const float* x;          // residual stream the layer starts from [1024]
+    const uint16_t* embed;   // first layer: the token's embedding row, else null
+    float* x_store;          // first layer: receives fp32 of the embedding row (the residual)
+    uint16_t* keys;          // layer base [8][context][128]
     uint16_t* values;
-    uint64_t* xpart;    // [8][32][2][kXPart] tagged partials
-    float* attended;    // [2048]
-    int* stall;         // set if the merge gave up waiting
+    float* partial;          // [8][kAttnSplits][kAttnPartial]
     int pos;
     int context;
-    uint32_t tag;       // this launch's tag for the sequence's exchange
 };
 
 struct AttnBatchArgs {
     AttnBatchSeq seq[kMaxBatch];
+    const uint16_t* w_qkv;   // natural [4096 x 1024]: q rows, k rows, v rows
+    const float* in_norm;    // input RMSNorm weights
     const float* q_norm;
     const float* k_norm;
     const float* cosines;
     const float* sines;
+    uint64_t* exchange;      // [8 KV heads][kMaxBatch][512] tagged q/k/v rows
+    int* stall;
     float scale;
     int batch;
     int pieces;  // pieces per (sequence, head)
+    uint32_t tag;
 };
 
-static_assert(kXPartWords == kKVHeads * kAttnSplits * 2 * kXPart, "exchange layout of the split partials");
 // Third descriptor word of a raw buffer (gfx9 family: 32-bit data format),
 // and the non-temporal cache policy for rows that are read once.
 constexpr int kBufferWord3 = 0x00020000;
@@ -1777,13 +1703,15 @@ constexpr int kInFlight = 4;
 // NB = the largest number of 64-position blocks a piece of this launch holds.
 template <int NB>
 __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs args) {
-    const int w = blockIdx.x, g = w & 7, b = (w >> 3) % args.batch, p = (w >> 3) / args.batch;
+    const int w = blockIdx.x, g = w & 7, r = w >> 3, B = args.batch, b = r % B, p = r / B;
+    const int W = B * args.pieces;  // workgroups of this XCD
     const AttnBatchSeq a = args.seq[b];  // by value: loaded once, ahead of the cache rows
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, quad = lane >> 4;
     const int pos = a.pos, n = pos + 1;
     const int blocks = (n + 63) / 64, per = (blocks + args.pieces - 1) / args.pieces;
     const int ns = (blocks + per - 1) / per;  // pieces with positions
-    if (p >= ns) return;
+    // A piece past ns has t_end < t_begin: its buffer loads are all out of range.
     const int t_begin = p * per * 64, t_end = min(n, t_begin + per * 64);
     // The block holding row pos (the last piece's last block), or -1.
     const int i_pos = p == ns - 1 ? (pos - t_begin) >> 6 : -1;
@@ -1791,11 +1719,36 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     const int quarter = tid >> 7, j = tid & 127, c = tid & 7, grp = tid >> 3;
     const int vsub = lane >> 4, vcg = lane & 15;
 
-    // Loads in the order the phases need them: this step's q/k/v with norm
-    // weights and rotation, then the first K/V blocks. Row pos is taken from
-    // LDS, not from the cache.
-    const float raw = quarter < 2 ? a.qkv[(2 * g + quarter) * 128 + j] : a.qkv[2048 + g * 128 + j];
-    const float raw_v = a.qkv[3072 + g * 128 + j];
+    // Loads complete in issue order per wave, so they are issued in the order
+    // the phases need them: the residual inputs (elements 2 tid, 2 tid + 1 of
+    // every sequence; rows past the batch repeat row B - 1), norm weights,
+    // this workgroup's QKV weight tile, rotation.
+    // The loads are unconditional (without an embedding row the residual row
+    // is read twice), so none waits behind a branch.
+    float2 xv[kMaxBatch];
+    uint32_t ev[kMaxBatch];
+#pragma unroll
+    for (int bb = 0; bb < kMaxBatch; ++bb) {
+        const AttnBatchSeq& s2 = args.seq[min(bb, B - 1)];
+        xv[bb] = reinterpret_cast<const float2*>(s2.x)[tid];
+        ev[bb] = reinterpret_cast<const uint32_t*>(s2.embed ? static_cast<const void*>(s2.embed) : s2.x)[tid];
+    }
+    const float2 wn = reinterpret_cast<const float2*>(args.in_norm)[tid];
+    // QKV tile tr (16 of the 512 rows of KV head g): query rows 256 g + 16 tr
+    // for tr < 16, key rows 2048 + 128 g + 16 (tr - 16) for tr < 24, value
+    // rows 3072 + 128 g + 16 (tr - 24) after.
+    auto tile_row = [&](int tr) {
+        return tr < 16 ? 256 * g + 16 * tr : (tr < 24 ? 2048 + 128 * g + 16 * (tr - 16) : 3072 + 128 * g + 16 * (tr - 24));
+    };
+    auto load_tile = [&](u32x4 (&wt)[4], int tr) {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(args.w_qkv + size_t(tile_row(tr) + col) * kHidden + 128 * wave) + quad;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 4 * st);
+    };
+    u32x4 wq[4];
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(wq, r);
+    __builtin_amdgcn_sched_barrier(0);
     const float nw = (__builtin_amdgcn_readfirstlane(quarter) < 2 ? args.q_norm : args.k_norm)[j];
     const float rc = args.cosines[size_t(pos) * 64 + (j & 63)], rs = args.sines[size_t(pos) * 64 + (j & 63)];
     // K/V rows through buffer loads: one descriptor per matrix covering this
@@ -1814,11 +1767,12 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         v[1] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + 1024, 16384 * i, kLoadNT);
     };
     u32x4 kr[kInFlight][2], vr[kInFlight][2];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < kInFlight && i < NB; ++i) load_block(kr[i], vr[i], i);
-    __builtin_amdgcn_sched_barrier(0);
 
+    __shared__ __align__(16) _Float16 xh[kMaxBatch][kHidden + 8];
+    __shared__ __align__(16) _Float16 xl[kMaxBatch][kHidden + 8];
+    __shared__ double nred[8][kMaxBatch];
+    __shared__ float inv_row[kMaxBatch];
+    __shared__ float qpart[8][64][4];
     __shared__ float qp[2][128];
     __shared__ float buf[4][128];
     __shared__ float prob[2][64];
@@ -1826,8 +1780,123 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     __shared__ uint16_t kcur[128], vcur[128];
     __shared__ double red[4][2];
     __shared__ float wm[8][2], wl[8][2];
-    __shared__ float mlv[2][kAttnSplits][2];
-    __shared__ float ovl[kAttnSplits][2][128];
+
+#pragma unroll
+    for (int bb = 0; bb < kMaxBatch; ++bb)
+        if (args.seq[min(bb, B - 1)].embed) xv[bb] = make_float2(h2f(ev[bb] & 0xffffu), h2f(ev[bb] >> 16));
+
+    // RMSNorm of every sequence's row: per-thread FP64 sums of the FP32
+    // squares, a reduce-scatter inside each wave (exchanges over lane bits
+    // 5, 4 and 3 halve the rows a lane carries, then bits 2..0 are summed, so
+    // lane l ends with its wave's total of row (l >> 3) & 7), then the 8 wave
+    // totals of a row in fixed order.
+    {
+        double sq[kMaxBatch];
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float q0 = xv[bb].x * xv[bb].x, q1 = xv[bb].y * xv[bb].y;
+            sq[bb] = static_cast<double>(q0) + static_cast<double>(q1);
+        }
+        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+        double r4[4], r2[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const double keep = b5 ? sq[4 + i] : sq[i], send = b5 ? sq[i] : sq[4 + i];
+            r4[i] = keep + xor_lanes<32>(send);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const double keep = b4 ? r4[2 + i] : r4[i], send = b4 ? r4[i] : r4[2 + i];
+            r2[i] = keep + xor_lanes<16>(send);
+        }
+        double r1 = (b3 ? r2[1] : r2[0]) + xor_lanes<8>(b3 ? r2[0] : r2[1]);
+        r1 += xor_lanes<4>(r1);
+        r1 += xor_lanes<2>(r1);
+        r1 += xor_lanes<1>(r1);
+        if ((lane & 7) == 0) nred[wave][lane >> 3] = r1;
+        if (w == 0) {  // first layer: the residual is fp32 of the embedding row
+#pragma unroll
+            for (int bb = 0; bb < kMaxBatch; ++bb)
+                if (bb < B && args.seq[bb].embed) reinterpret_cast<float2*>(args.seq[bb].x_store)[tid] = xv[bb];
+        }
+        __syncthreads();
+        if (tid < kMaxBatch) {
+            const double total = ((nred[0][tid] + nred[1][tid]) + (nred[2][tid] + nred[3][tid])) +
+                                 ((nred[4][tid] + nred[5][tid]) + (nred[6][tid] + nred[7][tid]));
+            inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(kHidden) + 1e-6f);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float inv = inv_row[bb];
+            const float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
+            _Float16 h0, l0, h1, l1;
+            split_half(n0, h0, l0);
+            split_half(n1, h1, l1);
+            *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
+            *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
+        }
+        __syncthreads();
+    }
+
+    // QKV tiles of this workgroup: r, then r + W, ... when W < 32 (the first
+    // outside the loop, so that its weights are waited for without the K/V
+    // loads issued after them).
+    auto project_tile = [&](int tr) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            // k slot (quad, e) of step st holds column 128 wave + 32 st + 8 quad + e.
+            const int k = 128 * wave + 32 * st + 8 * quad;
+            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
+            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+            const half8 w8 = __builtin_bit_cast(half8, wq[st]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qpart[wave][lane][e] = acc[e];
+        __syncthreads();
+        if (wave < 4) {  // element (row 4 (lane / 16) + wave, sequence lane % 16)
+            const auto f = [&](int v8) { return qpart[v8][lane][wave]; };
+            const float y = ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
+            const int seq = lane & 15, row = 16 * tr + 4 * (lane >> 4) + wave;
+            if (seq < B) exchange_put(args.exchange + (size_t(g) * kMaxBatch + seq) * 512 + row, y, args.tag);
+        }
+        __syncthreads();
+    };
+    project_tile(r);
+    for (int tr = r + W; tr < 32; tr += W) {
+        load_tile(wq, tr);
+        project_tile(tr);
+    }
+    if (p >= ns) return;  // no positions: this workgroup only projected
+
+    // This workgroup's q/k/v rows (query heads 2g, 2g + 1, key, value) are
+    // gathered by wave 0 into LDS before it issues any K/V load: loads return
+    // in order, so a poll issued behind the stream would wait for it. The
+    // other waves start the stream right away (a wave issuing loads into a
+    // full memory queue stalls, so the stream starts only after the
+    // projection, whose inputs and weights would otherwise queue behind it).
+    __shared__ float rawq[512];
+    if (wave == 0) {
+        const uint64_t* base = args.exchange + (size_t(g) * kMaxBatch + b) * 512 + lane;
+        const uint64_t* const words[8] = {base, base + 64, base + 128, base + 192,
+                                          base + 256, base + 320, base + 384, base + 448};
+        float got[8] = {};
+        if (!exchange_gather<8>(words, args.tag, got, 0xffu)) *args.stall = 1;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) rawq[lane + 64 * k] = got[k];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kInFlight && i < NB; ++i) load_block(kr[i], vr[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    // Thread tid's row: quarter 0/1 query heads, 2 key, 3 value.
+    const float raw = rawq[tid];
+    const float raw_v = raw;
 
     // QK-norm + RoPE (engine/core.cpp:395-402); the last piece writes the
     // new K/V row (403-406).
@@ -1993,107 +2062,16 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     };
     const float o = tree([&](int v8) { return wt[v8] * opart[v8][half][j]; });
     const float l = tree([&](int v8) { return wt[v8] * wl[v8][half]; });
-    float* out = a.attended + (2 * g + half) * 128;
-    if (ns == 1) {  // nothing to merge: normalize here
-        if (tid < 256) out[j] = o / l;
-        return;
-    }
-    auto part_of = [&](int split) { return a.xpart + ((size_t(g) * kAttnSplits + split) * 2 + half) * kXPart; };
-    if (p > 0) {
-        if (tid < 256) {
-            uint64_t* part = part_of(p);
-            exchange_put(part + j, o, a.tag);
-            if (j == 0) {
-                exchange_put(part + 128, mx, a.tag);
-                exchange_put(part + 129, l, a.tag);
-            }
+    if (tid < 256) {
+        float* part = a.partial + (size_t(g) * kAttnSplits + p) * kAttnPartial + half * 132;
+        part[j] = o;
+        if (j == 0) {
+            part[128] = mx;
+            part[129] = l;
         }
-        return;
     }
-
-    // Piece 0 merges. Output j of split k, head half, sits at
-    // head0 + k * kSplitWords + lane_word. Each poll gathers 8 splits per
-    // thread: threads 0-255 splits 1-8 (and every split's max or sum),
-    // threads 256-511 splits 9-16; a second poll takes splits 17-24 and
-    // 25-31. The outputs go to LDS, then threads 0-255 merge.
-    constexpr int kSplitWords = 2 * kXPart;
-    const uint64_t* head0 = a.xpart + size_t(g) * kAttnSplits * kSplitWords;
-    const unsigned lane_word = half * kXPart + j;
-    const bool upper = tid >= 256;
-    const int ms = j < 2 * kAttnSplits ? j >> 1 : 0;
-    const bool fetch_ml = !upper && j < 2 * kAttnSplits && ms > 0 && ms < ns;
-    bool ok = true;
-#pragma unroll
-    for (int round = 0; round < 2; ++round) {
-        const int first = 1 + 16 * round + (upper ? 8 : 0);
-        if (round == 1 && ns <= 17) break;  // uniform: no split past 16
-        float got[9];
-        unsigned want = 0;
-#pragma unroll
-        for (int k = 0; k < 9; ++k) {
-            got[k] = 0.f;
-            if (k < 8 && first + k < min(ns, kAttnSplits)) want |= 1u << k;
-        }
-        const bool ml = round == 0 && fetch_ml;
-        if (ml) want |= 1u << 8;
-        // After a give-up, stop polling (the step is reported as stalled).
-        if (ok)
-            ok = exchange_gather_strided<9, kSplitWords>(head0 + first * kSplitWords, lane_word,
-                                                         ml ? part_of(ms) + 128 + (j & 1) : nullptr, a.tag, got, want);
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (first + k < min(ns, kAttnSplits)) ovl[first + k][half][j] = got[k];
-        if (ml) mlv[half][ms][j & 1] = got[8];
-    }
-    if (!ok) *a.stall = 1;
-    if (tid == 0 || tid == 128) {
-        mlv[half][0][0] = mx;
-        mlv[half][0][1] = l;
-    }
-    if (!upper) ovl[0][half][j] = o;
-    __syncthreads();
-    if (upper) return;
-    // Groups of 8 splits against their own maximum, then the groups.
-    float gm[4], gl[4], go[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float m = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (8 * q + k < ns) m = fmaxf(m, mlv[half][8 * q + k][0]);
-        float ls = 0.f, os = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (8 * q + k < ns) {
-                const float wk = expf(mlv[half][8 * q + k][0] - m);
-                ls += wk * mlv[half][8 * q + k][1];
-                os += wk * ovl[8 * q + k][half][j];
-            }
-        gm[q] = m;
-        gl[q] = ls;
-        go[q] = os;
-    }
-    const float m2 = fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3]));
-    float lt = 0.f, ot = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        if (gm[q] != -INFINITY) {  // a group without splits adds nothing
-            const float wq = expf(gm[q] - m2);
-            lt += wq * gl[q];
-            ot += wq * go[q];
-        }
-    out[j] = ot / lt;
 }
 
-// Pieces per (sequence, head) and blocks per piece for a launch: one
-// workgroup per CU (256 / (8 count) pieces, at most kAttnSplits), each piece
-// an equal share of the longest sequence's blocks.
-inline void attn_batch_shape(int max_positions, int count, int& pieces, int& per) {
-    const int blocks = (max_positions + 63) / 64;
-    pieces = std::min(kAttnSplits, std::max(1, 256 / (kKVHeads * count)));
-    per = (blocks + pieces - 1) / pieces;
-}
-static_assert((kMaxContext + 63) / 64 <= 16 * 4, "16 blocks per piece cover the longest context at 4 pieces");
 
 __global__ void tile_kernel(const uint16_t* __restrict__ first, const uint16_t* __restrict__ second,
                             uint16_t* __restrict__ dst, int rows, int cols) {
@@ -2499,46 +2477,61 @@ void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const De
                                               host_out + row, s.stall);
 }
 
-void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
-                            const float* cosines, const float* sines, hipStream_t stream) {
+int attn_batch_pieces(const int* positions, int count, int* pieces_out, int& per) {
     require(count >= 1 && count <= kMaxBatch, "attention batch: 1..8 sequences");
+    int longest = 1;
+    for (int i = 0; i < count; ++i) longest = std::max(longest, positions[i]);
+    const int pieces = std::min(kAttnSplits, std::max(1, 256 / (kKVHeads * count)));
+    per = ((longest + 63) / 64 + pieces - 1) / pieces;
+    require(per <= 16, "attention batch: more than 16 blocks per piece");
+    for (int i = 0; i < count; ++i) {  // as the kernel splits each sequence
+        const int blocks = (positions[i] + 63) / 64, own = (blocks + pieces - 1) / pieces;
+        pieces_out[i] = (blocks + own - 1) / own;
+    }
+    return pieces;
+}
+
+void launch_qkv_attention_batch(const AttnSeq* seqs, int count, const uint16_t* w_qkv, const float* in_norm,
+                                const float* q_norm, const float* k_norm, const float* cosines, const float* sines,
+                                uint64_t* exchange, int* stall, uint32_t tag, hipStream_t stream) {
+    require(count >= 1 && count <= kMaxBatch, "attention batch: 1..8 sequences");
+    require(tag != 0, "attention batch: exchange tags are nonzero");
     AttnBatchArgs b{};
-    int max_positions = 1;
+    int positions[kMaxBatch];
     for (int i = 0; i < count; ++i) {
         AttnBatchSeq& a = b.seq[i];
-        a.qkv = seqs[i].qkv;
+        a.x = seqs[i].x;
+        a.embed = seqs[i].embed;
+        a.x_store = seqs[i].x_store;
         a.keys = seqs[i].keys;
         a.values = seqs[i].values;
-        a.xpart = seqs[i].xpart;
-        a.attended = seqs[i].attended;
-        a.stall = seqs[i].stall;
+        a.partial = seqs[i].partial;
         a.pos = seqs[i].pos;
         a.context = seqs[i].context;
-        a.tag = seqs[i].tag;
         require(a.pos >= 0 && a.pos < a.context, "attention batch: position outside the cache");
-        require(a.tag != 0, "attention batch: exchange tags are nonzero");
-        max_positions = std::max(max_positions, a.pos + 1);
+        require(a.x != nullptr, "attention batch: a residual row per sequence");
+        positions[i] = a.pos + 1;
     }
+    b.w_qkv = w_qkv;
+    b.in_norm = in_norm;
     b.q_norm = q_norm;
     b.k_norm = k_norm;
     b.cosines = cosines;
     b.sines = sines;
+    b.exchange = exchange;
+    b.stall = stall;
     b.scale = 1.0f / std::sqrt(128.0f);
     b.batch = count;
-    int pieces, per;
-    attn_batch_shape(max_positions, count, pieces, per);
-    require(pieces <= kAttnSplits, "attention batch: more pieces than the exchange holds");
-    b.pieces = pieces;
-    const dim3 grid(kKVHeads * count * pieces);
+    b.tag = tag;
+    int pieces[kMaxBatch], per;
+    b.pieces = attn_batch_pieces(positions, count, pieces, per);
+    const dim3 grid(kKVHeads * count * b.pieces);
     if (per <= 2) attn_batch_kernel<2><<<grid, 512, 0, stream>>>(b);
     else if (per <= 4) attn_batch_kernel<4><<<grid, 512, 0, stream>>>(b);
     else if (per <= 6) attn_batch_kernel<6><<<grid, 512, 0, stream>>>(b);
     else if (per <= 9) attn_batch_kernel<9><<<grid, 512, 0, stream>>>(b);
     else if (per <= 12) attn_batch_kernel<12><<<grid, 512, 0, stream>>>(b);
-    else {
-        require(per <= 16, "attention batch: more than 16 blocks per piece");
-        attn_batch_kernel<16><<<grid, 512, 0, stream>>>(b);
-    }
+    else attn_batch_kernel<16><<<grid, 512, 0, stream>>>(b);
 }
 
 void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,

@@ -176,5 +176,68 @@ __device__ __forceinline__ float head_norm_rope(float raw, float w, float cs, fl
     return out;
 }
 
+// Exchange between the workgroups of one XCD. A launch's workgroups are
+// dispatched round-robin over the 8 XCDs (workgroup w on XCD w % 8, measured
+// on this chip also right after launches of odd sizes), whose CUs share the
+// XCD's L2. A plain store reaches that L2 (the vector L1 is write-through),
+// and an agent-scope load skips the reader's L1 and finds the line there.
+// (Invalidating L1 with buffer_inv sc0 does not work here: outside
+// thread-group-split mode it leaves the stale line in place.) Each value
+// travels with its launch's tag in one 8-byte store, so a word left by an
+// earlier launch is never taken for a fresh one: placement decides only
+// whether a value arrives, never which value is read. Polls are bounded; a
+// consumer that gives up raises the stall flag, which the step's argmax
+// copies to the host. Measured: 0.40 us per exchange inside an XCD, against
+// 2.37 us per dependent kernel launch.
+constexpr unsigned kExchangeSpins = 1u << 18;  // ~0.1 s of polling; an exchange takes about a microsecond
+
+__device__ __forceinline__ void exchange_put(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Two consecutive tagged words; false if they did not both carry `tag`
+// within kExchangeSpins polls. The loop runs while any lane of the wave still
+// waits (a wave-uniform exit), and each lane's result comes from its own
+// flag: lanes leaving a loop at different iterations would otherwise hand the
+// compiler a divergent loop exit for the result.
+__device__ __forceinline__ bool exchange_get2(const uint64_t* p, uint32_t tag, float& a, float& b) {
+    unsigned missing = 1;
+    for (unsigned spin = 0; spin < kExchangeSpins && __any(missing); ++spin) {
+        if (missing) {
+            const uint64_t u = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t w = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (uint32_t(u >> 32) == tag && uint32_t(w >> 32) == tag) {
+                a = __uint_as_float(uint32_t(u));
+                b = __uint_as_float(uint32_t(w));
+                missing = 0;
+            }
+        }
+    }
+    return missing == 0;
+}
+
+// N tagged words at once: every round issues the loads of all words still
+// missing (bit k of `want`), then checks them, so a round costs one L2 round
+// trip however many words there are. False if some word did not carry `tag`
+// within kExchangeSpins rounds.
+template <int N>
+__device__ __forceinline__ bool exchange_gather(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N],
+                                                unsigned want) {
+    // Wave-uniform loop exit, per-lane result from `want` (see exchange_get2).
+    for (unsigned spin = 0; spin < kExchangeSpins && __any(want != 0); ++spin) {
+        uint64_t u[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            u[k] = (want >> k) & 1 ? __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
+                out[k] = __uint_as_float(uint32_t(u[k]));
+                want &= ~(1u << k);
+            }
+    }
+    return want == 0;
+}
+
 }  // namespace dev
 }  // namespace qwen_hip

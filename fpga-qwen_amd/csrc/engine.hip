@@ -434,17 +434,18 @@ void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
         require(tokens[i] >= 0 && tokens[i] < kVocab, "Token ID out of range");
     }
     BatchSeq bs[kMaxBatch];
+    Engine& lead = *seqs[0];
+    // The batched launches exchange through the first sequence's buffers,
+    // which its single-sequence launches use too: tags from its counter.
+    uint32_t tags[kBatchTagsPerLayer * kLayers];
+    for (uint32_t& t : tags) t = lead.next_tag();
     for (int i = 0; i < count; ++i) {
         Engine& e = *seqs[i];
         e.invalidate();
-        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_, {}};
-        // Tags come from each sequence's own counter: its exchange buffers
-        // are written by its single-sequence launches too.
-        for (int l = 0; l < kLayers; ++l) bs[i].tags[l] = e.next_tag();
+        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_};
         HIP_CHECK(hipStreamSynchronize(e.stream_));
     }
-    Engine& lead = *seqs[0];
-    launch_decode_batch(bs, count, lead.embed_, lead.final_norm_, lead.cosines_, lead.sines_, lead.stream_);
+    launch_decode_batch(bs, count, lead.embed_, lead.final_norm_, lead.cosines_, lead.sines_, tags, lead.stream_);
     HIP_CHECK(hipGetLastError());
     lead.sync();
     for (int i = 0; i < count; ++i) ++seqs[i]->pos_;

@@ -63,7 +63,6 @@ inline constexpr int kAttnOGroups = kQHeads * (kHidden / kAttnORows);  // 256 wo
 __host__ __device__ inline bool attn_fused(int n) { return n <= kFusedMaxPositions; }
 
 inline constexpr int kMaxBatch = 8;             // sequences per batched decode step
-inline constexpr int kBatchSplitMax = 3;        // K slices of 1024 columns in a batched down projection
 inline constexpr int kBatchRows = 16;           // output rows of one batched-GEMV MFMA tile
 inline constexpr int kBatchLmTiles = 4;         // MFMA tiles per batched lm_head workgroup
 inline constexpr int kBatchLmGroups = kVocab / (kBatchRows * kBatchLmTiles);  // 2374 lm_head workgroups
@@ -201,24 +200,36 @@ void launch_decode_layer_pair(const LayerDevice& layer, const uint16_t* embed, i
 void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
                          const PairScratch& pair, ArgmaxResult* host_out, hipStream_t stream);
 
-// One sequence of a batched attention launch.
+// One sequence of a batched norm + QKV + attention launch.
 struct AttnSeq {
-    const float* qkv;   // raw projections [4096]
-    uint16_t* keys;     // this layer's cache [8][context][128]
+    const float* x;          // residual stream the layer starts from
+    const uint16_t* embed;   // first layer: the token's embedding row (x is then overwritten), else null
+    float* x_store;          // first layer: receives fp32 of the embedding row
+    uint16_t* keys;          // this layer's cache [8][context][128]
     uint16_t* values;
-    uint64_t* xpart;    // [kXPartWords] tagged split partials
-    float* attended;    // [2048] normalized output
-    int* stall;         // set if a merge gave up waiting for a split's partial
-    int pos;            // position being written
+    float* partial;          // [8][kAttnSplits][kAttnPartial]: per piece and head (o[128], max, sum)
+    int pos;                 // position being written
     int context;
-    uint32_t tag;       // nonzero, unique per launch for this sequence's exchange
 };
 
-// Decode attention of up to kMaxBatch sequences in one launch (split
-// attention for every context length, the splits of each sequence and KV
-// head merged inside the launch) into `attended`.
-void launch_attention_batch(const AttnSeq* seqs, int count, const float* q_norm, const float* k_norm,
-                            const float* cosines, const float* sines, hipStream_t stream);
+// Pieces per (sequence, KV head) of a batched attention launch over
+// sequences with `positions` cached rows (the one being written included):
+// returns the grid's pieces per sequence (one workgroup per CU), sets `per`
+// (the most 64-position blocks a piece holds; each sequence's blocks are
+// shared evenly by the pieces) and pieces_out[i] (pieces of sequence i that
+// hold positions; the partials the merge reads).
+int attn_batch_pieces(const int* positions, int count, int* pieces_out, int& per);
+
+// RMSNorm + QKV projection + decode attention of one layer for up to
+// kMaxBatch sequences in one launch: each piece of each sequence and KV head
+// writes its (unnormalized output, max, sum) per query head to the
+// sequence's partial buffer, at piece index p. exchange ([8][kMaxBatch][512]
+// words) carries the q/k/v rows between the workgroups of an XCD under
+// `tag` (nonzero, unique per launch for that buffer); stall is set if a
+// workgroup gave up waiting for them.
+void launch_qkv_attention_batch(const AttnSeq* seqs, int count, const uint16_t* w_qkv, const float* in_norm,
+                                const float* q_norm, const float* k_norm, const float* cosines, const float* sines,
+                                uint64_t* exchange, int* stall, uint32_t tag, hipStream_t stream);
 
 // The batch-1 decode projections of one layer as the step runs them, on
 // caller buffers (parity-test entries):
