@@ -33,6 +33,7 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -324,7 +325,7 @@ struct ResidualArgs {
     uint32_t tag;
 };
 
-constexpr int kResidualExchangeWords = 64 * 3 * 128;  // 64 row tiles x quarters 1-3 x 16 rows x 8 sequences
+static_assert(kBatchQuarterWords == 64 * 3 * 128, "64 row tiles x quarters 1-3 x 16 rows x 8 sequences");
 static_assert(kHidden / kBatchRows == 64 && kQDim / 4 == 4 * kHeadDim, "64 row tiles; O quarters of 4 heads");
 
 template <int MODE>
@@ -472,6 +473,246 @@ __global__ __launch_bounds__(256) void residual_kernel(const ResidualArgs a) {
     if (live) a.x[eb][o0 + erow] = xres + ((y + got[0]) + (got[1] + got[2]));
 }
 
+// Norm + gate/up + SwiGLU + down + residual of one layer for the batched
+// step in one launch (engine/core.cpp:627-641). 256 workgroups of 512
+// threads, one per CU; XCD x owns activation columns 384 x .. 384 x + 383:
+//  1. every workgroup forms RMSNorm(x) of all sequences (FP32 squares summed
+//     in FP64) as FP16 hi + lo in LDS;
+//  2. workgroup r of XCD x computes the 12 gate and 12 up rows of columns
+//     384 x + 12 r .. + 11 on the matrix cores (two 16-row tiles, 4 rows of
+//     each unused; the 8 waves split K, summed in a fixed tree), applies
+//     SwiGLU (636-639) and posts the activations as tagged words in the
+//     XCD's L2;
+//  3. it gathers the XCD's 384 x 8 activations and multiplies them by down
+//     rows 32 r .. 32 r + 31, columns 384 x .. + 383 (this XCD's share of K);
+//  4. the 8 shares of a row, one per XCD, travel through memory (stores that
+//     write through the L2, loads that bypass it), and workgroup (r, x)
+//     adds rows 32 r + 4 x .. + 3 in fixed order ((s0 + s1) + (s2 + s3)) +
+//     ((s4 + s5) + (s6 + s7)) to the residual.
+// Every workgroup reads all of the input residual, so the output goes to a
+// second buffer (the layers alternate between the two).
+struct BatchFfnArgs {
+    const uint16_t* gateup;            // natural [6144 x 1024]: gate rows, then up rows
+    const uint16_t* down;              // natural [1024 x 3072]
+    const float* norm_w;               // post-attention RMSNorm weights
+    const float* x[kMaxBatch];         // residual in
+    float* x_out[kMaxBatch];           // residual out
+    uint64_t* act_words;               // [8 XCDs][kMaxBatch][384] tagged activations
+    uint64_t* share_words;             // [1024][kMaxBatch][8] tagged down shares
+    int* stall;
+    int batch;
+    uint32_t tag;
+};
+
+constexpr int kFfnOctant = kFFN / 8;  // 384 activation columns per XCD
+static_assert(kBatchActWords == 8 * kMaxBatch * kFfnOctant, "activation words per XCD octant");
+
+__device__ __forceinline__ void exchange_put_through(uint64_t* p, float v, uint32_t tag) {
+    // Agent scope: the store writes through the L2 so the other XCDs see it.
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
+    const int xo = blockIdx.x & 7, r = blockIdx.x >> 3;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, quad = lane >> 4;
+    const int B = a.batch;
+
+    // Loads complete in issue order per wave: residual elements 2 tid,
+    // 2 tid + 1 of every sequence (rows past the batch repeat row B - 1),
+    // norm weights, gate/up weights, down weights.
+    float2 xv[kMaxBatch];
+#pragma unroll
+    for (int bb = 0; bb < kMaxBatch; ++bb) xv[bb] = reinterpret_cast<const float2*>(a.x[min(bb, B - 1)])[tid];
+    const float2 wn = reinterpret_cast<const float2*>(a.norm_w)[tid];
+    // Gate/up tiles: rows 12 r + col (col < 12) of the octant's gate and up
+    // rows; wave w takes columns 128 w .. 128 w + 127.
+    const int c0 = kFfnOctant * xo + 12 * r;
+    u32x4 wg[4], wu[4];
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const int rr = c0 + min(col, 11);
+        const u32x4* gp = reinterpret_cast<const u32x4*>(a.gateup + size_t(rr) * kHidden + 128 * wave) + quad;
+        const u32x4* up = reinterpret_cast<const u32x4*>(a.gateup + size_t(kFFN + rr) * kHidden + 128 * wave) + quad;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            wg[st] = col < 12 ? __builtin_nontemporal_load(gp + 4 * st) : zero4;
+            wu[st] = col < 12 ? __builtin_nontemporal_load(up + 4 * st) : zero4;
+        }
+    }
+    // Down tile tt = wave & 1 (rows 32 r + 16 tt + col), K range
+    // 384 xo + 96 (wave >> 1) .. + 95 in 3 steps.
+    const int tt = wave & 1, kq = wave >> 1;
+    u32x4 wd[3];
+    {
+        const u32x4* dp = reinterpret_cast<const u32x4*>(a.down + size_t(32 * r + 16 * tt + col) * kFFN +
+                                                         kFfnOctant * xo + 96 * kq) + quad;
+#pragma unroll
+        for (int st = 0; st < 3; ++st) wd[st] = __builtin_nontemporal_load(dp + 4 * st);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    __shared__ __align__(16) _Float16 xh[kMaxBatch][kHidden + 8];
+    __shared__ __align__(16) _Float16 xl[kMaxBatch][kHidden + 8];
+    __shared__ double nred[8][kMaxBatch];
+    __shared__ float inv_row[kMaxBatch];
+    __shared__ float part[8][2][64][4];
+    __shared__ __align__(16) _Float16 ah[kMaxBatch][kFfnOctant + 8];
+    __shared__ __align__(16) _Float16 al[kMaxBatch][kFfnOctant + 8];
+
+    // 1. RMSNorm of every row (reduce-scatter inside each wave: lane l ends
+    // with its wave's total of row (l >> 3) & 7; then the 8 waves in order).
+    {
+        double sq[kMaxBatch];
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float q0 = xv[bb].x * xv[bb].x, q1 = xv[bb].y * xv[bb].y;
+            sq[bb] = static_cast<double>(q0) + static_cast<double>(q1);
+        }
+        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+        double r4[4], r2[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const double keep = b5 ? sq[4 + i] : sq[i], send = b5 ? sq[i] : sq[4 + i];
+            r4[i] = keep + xor_lanes<32>(send);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const double keep = b4 ? r4[2 + i] : r4[i], send = b4 ? r4[i] : r4[2 + i];
+            r2[i] = keep + xor_lanes<16>(send);
+        }
+        double r1 = (b3 ? r2[1] : r2[0]) + xor_lanes<8>(b3 ? r2[0] : r2[1]);
+        r1 += xor_lanes<4>(r1);
+        r1 += xor_lanes<2>(r1);
+        r1 += xor_lanes<1>(r1);
+        if ((lane & 7) == 0) nred[wave][lane >> 3] = r1;
+        __syncthreads();
+        if (tid < kMaxBatch) {
+            const double total = ((nred[0][tid] + nred[1][tid]) + (nred[2][tid] + nred[3][tid])) +
+                                 ((nred[4][tid] + nred[5][tid]) + (nred[6][tid] + nred[7][tid]));
+            inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(kHidden) + 1e-6f);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float inv = inv_row[bb];
+            const float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
+            _Float16 h0, l0, h1, l1;
+            split_half(n0, h0, l0);
+            split_half(n1, h1, l1);
+            *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
+            *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
+        }
+        __syncthreads();
+    }
+
+    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    // 2. Gate/up and SwiGLU.
+    {
+        floatx4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            // k slot (quad, e) of step st holds column 128 wave + 32 st + 8 quad + e.
+            const int k = 128 * wave + 32 * st + 8 * quad;
+            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
+            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+            const half8 g8 = __builtin_bit_cast(half8, wg[st]), u8 = __builtin_bit_cast(half8, wu[st]);
+            accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(g8, bh, accg, 0, 0, 0);
+            accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(g8, bl, accg, 0, 0, 0);
+            accu = __builtin_amdgcn_mfma_f32_16x16x32_f16(u8, bh, accu, 0, 0, 0);
+            accu = __builtin_amdgcn_mfma_f32_16x16x32_f16(u8, bl, accu, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            part[wave][0][lane][e] = accg[e];
+            part[wave][1][lane][e] = accu[e];
+        }
+        __syncthreads();
+        if (wave < 4) {  // element (row 4 (lane / 16) + wave, sequence lane % 16)
+            auto tree = [&](int t) {
+                return ((part[0][t][lane][wave] + part[1][t][lane][wave]) +
+                        (part[2][t][lane][wave] + part[3][t][lane][wave])) +
+                       ((part[4][t][lane][wave] + part[5][t][lane][wave]) +
+                        (part[6][t][lane][wave] + part[7][t][lane][wave]));
+            };
+            const float gate = tree(0), up = tree(1);
+            const int row = 4 * (lane >> 4) + wave, seq = lane & 15;
+            if (row < 12 && seq < B) {
+                const float half_gate = gate * 0.5f;
+                const float th = tanhf(half_gate);
+                const float act = gate * (0.5f + 0.5f * th) * up;
+                exchange_put(a.act_words + (size_t(xo) * kMaxBatch + seq) * kFfnOctant + 12 * r + row, act, a.tag);
+            }
+        }
+    }
+
+    // 3. The XCD's activations (6 words per thread), staged as hi / lo.
+    bool ok;
+    {
+        const uint64_t* words[6];
+        float got[6];
+        unsigned want = 0;
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const int idx = tid + 512 * k, seq = idx / kFfnOctant;
+            words[k] = a.act_words + size_t(xo) * kMaxBatch * kFfnOctant + idx;
+            got[k] = 0.f;
+            if (seq < B) want |= 1u << k;
+        }
+        ok = exchange_gather<6>(words, a.tag, got, want);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const int idx = tid + 512 * k, seq = idx / kFfnOctant, c = idx % kFfnOctant;
+            _Float16 h, l;
+            split_half(got[k], h, l);
+            ah[seq][c] = h;
+            al[seq][c] = l;
+        }
+        __syncthreads();
+    }
+    // Down share of rows 32 r .. 32 r + 31 over this XCD's columns.
+    {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 3; ++st) {
+            const int k = 96 * kq + 32 * st + 8 * quad;
+            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&ah[col & 7][k]) : zero;
+            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&al[col & 7][k]) : zero;
+            const half8 d8 = __builtin_bit_cast(half8, wd[st]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(d8, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(d8, bl, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[wave][0][lane][e] = acc[e];
+        __syncthreads();
+        // Thread of waves 0-3 and 4-7: tile tt2 = wave >> 2, element (row
+        // 4 (lane / 16) + (wave & 3), sequence lane % 16); the 4 K ranges of
+        // the tile (waves tt2, tt2 + 2, tt2 + 4, tt2 + 6) in fixed order.
+        const int tt2 = wave >> 2, e4 = wave & 3;
+        const float y = (part[tt2][0][lane][e4] + part[tt2 + 2][0][lane][e4]) +
+                        (part[tt2 + 4][0][lane][e4] + part[tt2 + 6][0][lane][e4]);
+        const int row = 32 * r + 16 * tt2 + 4 * (lane >> 4) + e4, seq = lane & 15;
+        if (seq < B) exchange_put_through(a.share_words + (size_t(row) * kMaxBatch + seq) * 8 + xo, y, a.tag);
+    }
+
+    // 4. Rows 32 r + 4 xo .. + 3 of every sequence: threads 0..31 (row
+    // 4 xo + tid / 8, sequence tid % 8) add the 8 shares to the residual.
+    if (tid < 32) {
+        const int row = 32 * r + 4 * xo + (tid >> 3), seq = tid & 7;
+        const bool live = seq < B;
+        const uint64_t* base = a.share_words + (size_t(row) * kMaxBatch + seq) * 8;
+        const uint64_t* const words[8] = {base, base + 1, base + 2, base + 3, base + 4, base + 5, base + 6, base + 7};
+        float s8[8] = {};
+        if (ok) ok = exchange_gather<8>(words, a.tag, s8, live ? 0xffu : 0u);
+        if (live) {
+            const float down = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+            a.x_out[seq][row] = a.x[seq][row] + down;
+        }
+    }
+    if (!ok) *a.stall = 1;
+}
+
 // Second pass of the per-sequence greedy selection.
 struct BatchResults {
     ArgmaxResult* device[kMaxBatch];
@@ -547,17 +788,24 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
                          const float* cosines, const float* sines, const uint32_t* tags, hipStream_t stream) {
     require(count >= 1 && count <= kMaxBatch, "batched decode: 1..8 sequences");
     for (int l = 0; l < kBatchTagsPerLayer * kLayers; ++l) require(tags[l] != 0, "batched decode: exchange tags are nonzero");
-    static_assert(kXPartWords >= kResidualExchangeWords + kKVHeads * kMaxBatch * 512,
-                  "the residual quarter and q/k/v exchanges fit the lead sequence's partial words");
+    static_assert(kLayers % 2 == 0, "the residual alternates between two buffers and ends in x");
+    uint64_t* const qkv_words = seqs[0].s.bexchange;
+    uint64_t* const quarter_words = qkv_words + kBatchQkvWords;
+    uint64_t* const act_words = quarter_words + kBatchQuarterWords;
+    uint64_t* const share_words = act_words + kBatchActWords;
     for (int l = 0; l < kLayers; ++l) {
         const LayerDevice& W = seqs[0].layers[l];  // weights are shared; K/V are per sequence
+        // The layer's residual is in x (even layers) or xm (odd layers); its
+        // FFN writes the other.
+        auto res_in = [&](int b) { return (l & 1) ? seqs[b].s.xm : seqs[b].s.x; };
+        auto res_out = [&](int b) { return (l & 1) ? seqs[b].s.x : seqs[b].s.xm; };
         AttnSeq as[kMaxBatch];
         int positions[kMaxBatch];
         for (int b = 0; b < count; ++b) {
             const DecodeScratch& s = seqs[b].s;
-            as[b] = AttnSeq{s.x,
+            as[b] = AttnSeq{res_in(b),
                             l == 0 ? embed + size_t(seqs[b].token) * kHidden : nullptr,
-                            s.x,
+                            res_in(b),
                             seqs[b].layers[l].keys,
                             seqs[b].layers[l].values,
                             s.attn_partial,
@@ -565,44 +813,37 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
                             seqs[b].context};
             positions[b] = seqs[b].pos + 1;
         }
-        launch_qkv_attention_batch(as, count, W.qkv_n, W.in_norm, W.q_norm, W.k_norm, cosines, sines,
-                                   seqs[0].s.xpart + kResidualExchangeWords, seqs[0].s.stall, tags[3 * l], stream);
+        launch_qkv_attention_batch(as, count, W.qkv_n, W.in_norm, W.q_norm, W.k_norm, cosines, sines, qkv_words,
+                                   seqs[0].s.stall, tags[kBatchTagsPerLayer * l], stream);
 
         ResidualArgs o{};
         o.w = W.o_n;
         o.batch = count;
-        o.exchange = seqs[0].s.xpart;
+        o.exchange = quarter_words;
         o.stall = seqs[0].s.stall;
-        o.tag = tags[3 * l + 1];
+        o.tag = tags[kBatchTagsPerLayer * l + 1];
         int per;
         attn_batch_pieces(positions, count, o.pieces, per);
         for (int b = 0; b < count; ++b) {
             o.in[b] = seqs[b].s.attn_partial;
-            o.x[b] = seqs[b].s.x;
+            o.x[b] = res_in(b);
         }
         residual_kernel<kRO><<<256, 256, 0, stream>>>(o);
 
-        BatchGemvArgs gu{};
-        gu.w = W.gateup_n;
-        gu.norm_w = W.post_norm;
-        gu.batch = count;
+        BatchFfnArgs f{};
+        f.gateup = W.gateup_n;
+        f.down = W.down_n;
+        f.norm_w = W.post_norm;
+        f.act_words = act_words;
+        f.share_words = share_words;
+        f.stall = seqs[0].s.stall;
+        f.batch = count;
+        f.tag = tags[kBatchTagsPerLayer * l + 2];
         for (int b = 0; b < count; ++b) {
-            gu.in[b] = seqs[b].s.x;
-            gu.out[b] = seqs[b].s.act;
+            f.x[b] = res_in(b);
+            f.x_out[b] = res_out(b);
         }
-        bgemv<kHidden, kBGateUp>(gu, kFFN, stream);
-
-        ResidualArgs d{};
-        d.w = W.down_n;
-        d.batch = count;
-        d.exchange = seqs[0].s.xpart;
-        d.stall = seqs[0].s.stall;
-        d.tag = tags[3 * l + 2];
-        for (int b = 0; b < count; ++b) {
-            d.in[b] = seqs[b].s.act;
-            d.x[b] = seqs[b].s.x;
-        }
-        residual_kernel<kRDown><<<256, 256, 0, stream>>>(d);
+        ffn_batch_kernel<<<256, 512, 0, stream>>>(f);
     }
     BatchGemvArgs lm{};
     lm.w = embed;  // tied head (engine/core.cpp:643-645)

@@ -1656,15 +1656,16 @@ __global__ __launch_bounds__(512) void qkv_attn_kernel(const QkvAttnArgs a) {
 // Attention: one workgroup per CU. A CU serves its loads in order, so a
 // single workgroup per CU that keeps its own stream of K/V rows in flight
 // (kInFlight 64-position blocks, the loads of block i + kInFlight issued
-// once block i is consumed) overlaps the q/k/v exchange and its arithmetic
-// with the stream. Block layout as in the single-sequence
+// once block i is consumed) overlaps the projection, the q/k/v exchange and
+// its arithmetic with the stream. Block layout as in the single-sequence
 // split kernel: the 8 lanes of position t score it (lane c = chain c of the
 // reference dot, engine/core.cpp:612, key values converted once for both
 // heads), and the wave that scored 8 positions multiplies their V rows (4
 // positions x 16 channel groups per load). Softmax (613-620) runs online per
 // wave: each wave keeps its own running maximum, rescaling its sums when it
 // rises, and the 8 waves' sums are combined with weights exp(m_w - max) in a
-// fixed tree. Every piece writes (unnormalized output, max, sum) of both
+// fixed tree; the exponentials are the hardware exp2 of x log2(e) (the
+// batched path is held to the reference's tolerance gate). Every piece writes (unnormalized output, max, sum) of both
 // query heads to the sequence's partial buffer; the batched O projection
 // merges the pieces in its prologue. The last piece writes the new K/V row.
 struct AttnBatchSeq {
@@ -1874,11 +1875,12 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     if (p >= ns) return;  // no positions: this workgroup only projected
 
     // This workgroup's q/k/v rows (query heads 2g, 2g + 1, key, value) are
-    // gathered by wave 0 into LDS before it issues any K/V load: loads return
-    // in order, so a poll issued behind the stream would wait for it. The
-    // other waves start the stream right away (a wave issuing loads into a
-    // full memory queue stalls, so the stream starts only after the
-    // projection, whose inputs and weights would otherwise queue behind it).
+    // gathered by wave 0 into LDS before it issues any K/V load; the other
+    // waves start the stream right away. (A CU returns loads in the order it
+    // received them, and the memory system serves a flood of stream misses
+    // ahead of later ones: issued before the projection, the stream would
+    // hold up its inputs; issued before the poll, it holds up the poll. Wave
+    // 0's poll still waits behind the other waves' first blocks.)
     __shared__ float rawq[512];
     if (wave == 0) {
         const uint64_t* base = args.exchange + (size_t(g) * kMaxBatch + b) * 512 + lane;
@@ -1965,15 +1967,25 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
             b0 = fmaxf(b0, xor_lanes<32>(b0));
             b1 = fmaxf(b1, xor_lanes<32>(b1));
             const float n0 = fmaxf(m0, b0), n1 = fmaxf(m1, b1);
-            // A wave with no valid position yet keeps m = -inf and scale 1.
-            const float a0 = n0 == -INFINITY ? 1.f : expf(m0 - n0);
-            const float a1 = n1 == -INFINITY ? 1.f : expf(m1 - n1);
-            m0 = n0;
-            m1 = n1;
-            const float p0 = valid ? expf(s0 - n0) : 0.f;
-            const float p1 = valid ? expf(s1 - n1) : 0.f;
-            l0 = l0 * a0 + p0;
-            l1 = l1 * a1 + p1;
+            // The sums are rescaled only when the wave's running maximum rises
+            // (uniform in the wave; from -inf the scale is 0, on empty sums).
+            if (n0 != m0 || n1 != m1) {
+                const float a0 = n0 == m0 ? 1.f : __expf(m0 - n0);
+                const float a1 = n1 == m1 ? 1.f : __expf(m1 - n1);
+                l0 *= a0;
+                l1 *= a1;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    acc[0][e] *= a0;
+                    acc[1][e] *= a1;
+                }
+                m0 = n0;
+                m1 = n1;
+            }
+            const float p0 = valid ? __expf(s0 - n0) : 0.f;
+            const float p1 = valid ? __expf(s1 - n1) : 0.f;
+            l0 += p0;
+            l1 += p1;
             if (c == 0) {
                 prob[0][grp] = p0;
                 prob[1][grp] = p1;
@@ -1982,11 +1994,6 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                acc[0][e] *= a0;
-                acc[1][e] *= a1;
-            }
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
                 const int tl = 8 * wave + 4 * hf + vsub, tv = t_begin + 64 * i + tl;

@@ -194,6 +194,7 @@ void Engine::init_state() {
     s.stall = device_alloc<int>(1);
     s.xqkv = device_alloc<uint64_t>(kXqkvWords);
     s.xpart = device_alloc<uint64_t>(kXPartWords);
+    s.bexchange = device_alloc<uint64_t>(kBatchExchangeWords);
 
     ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
     ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
@@ -307,6 +308,7 @@ void Engine::clear_exchanges() {
     HIP_CHECK(hipMemsetAsync(pair_.exchange, 0, 2 * kFFN * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(scratch_.bexchange, 0, kBatchExchangeWords * sizeof(uint64_t), stream_));
 }
 
 LayerFlow Engine::layer_flow(int layer, bool pair) {

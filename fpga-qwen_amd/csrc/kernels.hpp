@@ -107,7 +107,17 @@ struct DecodeScratch {
     int* stall;           // nonzero once an exchange poll gave up (cleared by the argmax kernel)
     uint64_t* xqkv;       // [8][512] q/k/v rows of each KV head group (fused QKV + attention kernel)
     uint64_t* xpart;      // [kXPartWords] attention partials of its workgroups
+    uint64_t* bexchange;  // [kBatchExchangeWords] batched step exchanges (when this sequence leads a batch)
 };
+
+// Exchange words of a batched step, in the first sequence's buffers:
+// q/k/v rows [8 KV heads][kMaxBatch][512], O quarter sums [64 tiles][3][128],
+// activations [8 XCDs][kMaxBatch][384], down shares [1024][kMaxBatch][8 XCDs].
+inline constexpr int kBatchQkvWords = kKVHeads * kMaxBatch * 512;
+inline constexpr int kBatchQuarterWords = 64 * 3 * 128;
+inline constexpr int kBatchActWords = 8 * kMaxBatch * (kFFN / 8);
+inline constexpr int kBatchShareWords = kHidden * kMaxBatch * 8;
+inline constexpr int kBatchExchangeWords = kBatchQkvWords + kBatchQuarterWords + kBatchActWords + kBatchShareWords;
 
 // The fused FFN kernel (norm + gate/up + SwiGLU + down in one launch): XCD
 // g computes activations 384 g .. 384 g + 383 and their share of the down
