@@ -40,6 +40,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 4;  // waves of the K = 1024 kernels (norm prologues, lm_head)
 using dev::exchange_gather;
 using dev::exchange_put;
+using dev::exchange_put_through;
 using dev::xor_lanes;
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
@@ -295,184 +296,6 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
     }
 }
 
-// Residual projections of the batched step, x += W in, as 256 workgroups,
-// one per CU: workgroup w = x + 8 (4 t + q) computes output rows
-// 16 (x + 8 t) .. + 15 over the K quarter q, so the 4 quarters of a row tile
-// share XCD x. The inputs enter the matrix cores as FP16 hi + lo, as in
-// bgemv_kernel (v_mfma_f32_16x16x32_f16, A = 16 weight rows, B = the
-// sequences; each of the 4 waves takes a quarter of the quarter's columns,
-// summed in fixed order). Quarters 1-3 post their 16 x 8 sums as tagged
-// words in the XCD's L2; quarter 0 adds them in fixed order
-// ((q0 + q1) + (q2 + q3)) to the residual and writes the residual stream.
-//   kRO: the O projection (engine/core.cpp:625-626), K = 2048, quarter q =
-//        query heads 4q .. 4q + 3, with the merge of the attention pieces in
-//        the prologue: each (sequence, head) is merged by 8 threads (16
-//        channels each) from the pieces' (output, max, sum): out =
-//        sum_p e_p o_p / sum_p e_p l_p with e_p = exp(m_p - max), pieces in
-//        order, in chunks of 4 (a later chunk rescales the running sums).
-//   kRDown: the down projection (engine/core.cpp:640-641), K = 3072, input
-//        the SwiGLU activations.
-enum ResidualMode { kRO, kRDown };
-
-struct ResidualArgs {
-    const uint16_t* w;                 // natural [1024 x K]
-    const float* in[kMaxBatch];        // kRO: attention pieces [8][kAttnSplits][kAttnPartial]; kRDown: act [3072]
-    float* x[kMaxBatch];               // residual rows
-    uint64_t* exchange;                // [64 tiles][3][128] tagged quarter sums
-    int* stall;
-    int pieces[kMaxBatch];             // kRO: pieces with positions per sequence
-    int batch;
-    uint32_t tag;
-};
-
-static_assert(kBatchQuarterWords == 64 * 3 * 128, "64 row tiles x quarters 1-3 x 16 rows x 8 sequences");
-static_assert(kHidden / kBatchRows == 64 && kQDim / 4 == 4 * kHeadDim, "64 row tiles; O quarters of 4 heads");
-
-template <int MODE>
-__global__ __launch_bounds__(256) void residual_kernel(const ResidualArgs a) {
-    constexpr int K = MODE == kRO ? kQDim : kFFN, KQ = K / 4, CW = KQ / 4, STEPS = CW / 32;
-    static_assert(CW % 32 == 0, "whole MFMA steps per wave");
-    const int xcd = blockIdx.x & 7, i = blockIdx.x >> 3, qk = i & 3;
-    const int o0 = kBatchRows * (xcd + 8 * (i >> 2)), k0 = KQ * qk;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int col = lane & 15, quad = lane >> 4;
-    const int B = a.batch;
-    // Epilogue element of this thread: row o0 + erow, sequence eb.
-    const int eb = lane & 15, erow = 4 * (lane >> 4) + wave;
-    const bool live = eb < B;
-    __shared__ __align__(16) _Float16 xh[kMaxBatch][KQ + 8];
-    __shared__ __align__(16) _Float16 xl[kMaxBatch][KQ + 8];
-    // Stages 8 input values of sequence bb at quarter column kk as hi / lo.
-    auto stage8 = [&](int bb, int kk, const float (&v)[8]) {
-        half8 hi, lo;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            _Float16 h, l;
-            split_half(v[e], h, l);
-            hi[e] = h;
-            lo[e] = l;
-        }
-        *reinterpret_cast<half8*>(&xh[bb][kk]) = hi;
-        *reinterpret_cast<half8*>(&xl[bb][kk]) = lo;
-    };
-
-    // Loads complete in issue order per wave: the inputs, then the weights,
-    // then the residual entries of quarter 0.
-    u32x4 wa[STEPS];
-    auto load_weights = [&] {
-        __builtin_amdgcn_sched_barrier(0);
-        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(o0 + col) * K + k0 + CW * wave) + quad;
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) wa[st] = __builtin_nontemporal_load(wp + 4 * st);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    float xres = 0.f;
-    if constexpr (MODE == kRO) {
-        // Merge layout: sequence mb, head 4 qk + mh, channels 16 mc .. 16 mc + 15.
-        const int mb = tid >> 5, mh = (tid >> 3) & 3, mc = tid & 7;
-        const int head = 4 * qk + mh;
-        const int np = mb < B ? a.pieces[mb] : 0;
-        const float* pbase = a.in[min(mb, B - 1)] + size_t(head >> 1) * kAttnSplits * kAttnPartial + (head & 1) * 132;
-        float4 ov[4][4];
-        float mv[4], lv[4];
-        auto load_chunk = [&](int p0) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float* e = pbase + size_t(min(p0 + k, max(np - 1, 0))) * kAttnPartial;
-                if (np > 0) {
-                    mv[k] = e[128];
-                    lv[k] = e[129];
-#pragma unroll
-                    for (int c4 = 0; c4 < 4; ++c4) ov[k][c4] = reinterpret_cast<const float4*>(e + 16 * mc)[c4];
-                }
-            }
-        };
-        load_chunk(0);
-        load_weights();
-        if (qk == 0 && live) xres = a.x[eb][o0 + erow];
-        // Online merge over chunks of 4 pieces (one chunk when there are at most 4).
-        float run_m = -INFINITY, run_l = 0.f, run_o[16] = {};
-        for (int p0 = 0; p0 < np; p0 += 4) {
-            if (p0 > 0) load_chunk(p0);
-            float cm = -INFINITY;
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (p0 + k < np) cm = fmaxf(cm, mv[k]);
-            const float nm = fmaxf(run_m, cm);
-            const float sc = run_m == -INFINITY ? 0.f : expf(run_m - nm);
-            run_l *= sc;
-#pragma unroll
-            for (int c = 0; c < 16; ++c) run_o[c] *= sc;
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (p0 + k < np) {
-                    const float e = expf(mv[k] - nm);
-                    run_l += e * lv[k];
-                    const float o16[16] = {ov[k][0].x, ov[k][0].y, ov[k][0].z, ov[k][0].w, ov[k][1].x, ov[k][1].y,
-                                           ov[k][1].z, ov[k][1].w, ov[k][2].x, ov[k][2].y, ov[k][2].z, ov[k][2].w,
-                                           ov[k][3].x, ov[k][3].y, ov[k][3].z, ov[k][3].w};
-#pragma unroll
-                    for (int c = 0; c < 16; ++c) run_o[c] += e * o16[c];
-                }
-            run_m = nm;
-        }
-#pragma unroll
-        for (int z = 0; z < 2; ++z) {
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = np > 0 ? run_o[8 * z + e] / run_l : 0.f;
-            stage8(mb, 128 * mh + 16 * mc + 8 * z, v);
-        }
-    } else {
-        // Activation layout: sequence tid / 32, columns 24 (tid % 32) .. + 23.
-        const int bb = tid >> 5, c0 = 24 * (tid & 31);
-        const float4* src = reinterpret_cast<const float4*>(a.in[min(bb, B - 1)] + k0 + c0);
-        float4 av[6];
-#pragma unroll
-        for (int z = 0; z < 6; ++z) av[z] = src[z];
-        load_weights();
-        if (qk == 0 && live) xres = a.x[eb][o0 + erow];
-#pragma unroll
-        for (int z = 0; z < 3; ++z) {
-            const float v[8] = {av[2 * z].x,     av[2 * z].y,     av[2 * z].z,     av[2 * z].w,
-                                av[2 * z + 1].x, av[2 * z + 1].y, av[2 * z + 1].z, av[2 * z + 1].w};
-            stage8(bb, c0 + 8 * z, v);
-        }
-    }
-    __syncthreads();
-
-    // 16 output rows x 8 sequences over this wave's CW columns (k slot
-    // (quad, e) of step st holds column CW wave + 32 st + 8 quad + e).
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int st = 0; st < STEPS; ++st) {
-        const int k = CW * wave + 32 * st + 8 * quad;
-        const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
-        const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
-        const half8 w8 = __builtin_bit_cast(half8, wa[st]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);
-    }
-    __shared__ float part[4][64][4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) part[wave][lane][r] = acc[r];
-    __syncthreads();
-    const float y = (part[0][lane][wave] + part[1][lane][wave]) + (part[2][lane][wave] + part[3][lane][wave]);
-
-    uint64_t* tile_words = a.exchange + size_t(o0 / kBatchRows) * 3 * 128;
-    const int word = erow * kMaxBatch + eb;
-    if (qk > 0) {
-        if (live) exchange_put(tile_words + (qk - 1) * 128 + word, y, a.tag);
-        return;
-    }
-    const uint64_t* const words[3] = {tile_words + word, tile_words + 128 + word, tile_words + 256 + word};
-    float got[3] = {0.f, 0.f, 0.f};
-    const bool ok = exchange_gather<3>(words, a.tag, got, live ? 7u : 0u);
-    if (!ok) *a.stall = 1;
-    if (live) a.x[eb][o0 + erow] = xres + ((y + got[0]) + (got[1] + got[2]));
-}
-
 // Norm + gate/up + SwiGLU + down + residual of one layer for the batched
 // step in one launch (engine/core.cpp:627-641). 256 workgroups of 512
 // threads, one per CU; XCD x owns activation columns 384 x .. 384 x + 383:
@@ -506,11 +329,6 @@ struct BatchFfnArgs {
 
 constexpr int kFfnOctant = kFFN / 8;  // 384 activation columns per XCD
 static_assert(kBatchActWords == 8 * kMaxBatch * kFfnOctant, "activation words per XCD octant");
-
-__device__ __forceinline__ void exchange_put_through(uint64_t* p, float v, uint32_t tag) {
-    // Agent scope: the store writes through the L2 so the other XCDs see it.
-    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
     const int xo = blockIdx.x & 7, r = blockIdx.x >> 3;
@@ -788,60 +606,37 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
                          const float* cosines, const float* sines, const uint32_t* tags, hipStream_t stream) {
     require(count >= 1 && count <= kMaxBatch, "batched decode: 1..8 sequences");
     for (int l = 0; l < kBatchTagsPerLayer * kLayers; ++l) require(tags[l] != 0, "batched decode: exchange tags are nonzero");
-    static_assert(kLayers % 2 == 0, "the residual alternates between two buffers and ends in x");
-    uint64_t* const qkv_words = seqs[0].s.bexchange;
-    uint64_t* const quarter_words = qkv_words + kBatchQkvWords;
-    uint64_t* const act_words = quarter_words + kBatchQuarterWords;
-    uint64_t* const share_words = act_words + kBatchActWords;
+    uint64_t* const words = seqs[0].s.bexchange;
     for (int l = 0; l < kLayers; ++l) {
         const LayerDevice& W = seqs[0].layers[l];  // weights are shared; K/V are per sequence
-        // The layer's residual is in x (even layers) or xm (odd layers); its
-        // FFN writes the other.
-        auto res_in = [&](int b) { return (l & 1) ? seqs[b].s.xm : seqs[b].s.x; };
-        auto res_out = [&](int b) { return (l & 1) ? seqs[b].s.x : seqs[b].s.xm; };
+        // The residual is in x at each layer's start; attention + O leave it
+        // in xm, the FFN brings it back to x.
         AttnSeq as[kMaxBatch];
-        int positions[kMaxBatch];
         for (int b = 0; b < count; ++b) {
             const DecodeScratch& s = seqs[b].s;
-            as[b] = AttnSeq{res_in(b),
+            as[b] = AttnSeq{s.x,
                             l == 0 ? embed + size_t(seqs[b].token) * kHidden : nullptr,
-                            res_in(b),
+                            s.xm,
                             seqs[b].layers[l].keys,
                             seqs[b].layers[l].values,
-                            s.attn_partial,
                             seqs[b].pos,
                             seqs[b].context};
-            positions[b] = seqs[b].pos + 1;
         }
-        launch_qkv_attention_batch(as, count, W.qkv_n, W.in_norm, W.q_norm, W.k_norm, cosines, sines, qkv_words,
-                                   seqs[0].s.stall, tags[kBatchTagsPerLayer * l], stream);
-
-        ResidualArgs o{};
-        o.w = W.o_n;
-        o.batch = count;
-        o.exchange = quarter_words;
-        o.stall = seqs[0].s.stall;
-        o.tag = tags[kBatchTagsPerLayer * l + 1];
-        int per;
-        attn_batch_pieces(positions, count, o.pieces, per);
-        for (int b = 0; b < count; ++b) {
-            o.in[b] = seqs[b].s.attn_partial;
-            o.x[b] = res_in(b);
-        }
-        residual_kernel<kRO><<<256, 256, 0, stream>>>(o);
+        launch_attention_o_batch(as, count, W.qkv_n, W.o_n, W.in_norm, W.q_norm, W.k_norm, cosines, sines, words,
+                                 seqs[0].s.stall, tags[kBatchTagsPerLayer * l], stream);
 
         BatchFfnArgs f{};
         f.gateup = W.gateup_n;
         f.down = W.down_n;
         f.norm_w = W.post_norm;
-        f.act_words = act_words;
-        f.share_words = share_words;
+        f.act_words = words + kBatchActOffset;
+        f.share_words = words + kBatchShareOffset;
         f.stall = seqs[0].s.stall;
         f.batch = count;
-        f.tag = tags[kBatchTagsPerLayer * l + 2];
+        f.tag = tags[kBatchTagsPerLayer * l + 1];
         for (int b = 0; b < count; ++b) {
-            f.x[b] = res_in(b);
-            f.x_out[b] = res_out(b);
+            f.x[b] = seqs[b].s.xm;
+            f.x_out[b] = seqs[b].s.x;
         }
         ffn_batch_kernel<<<256, 512, 0, stream>>>(f);
     }

@@ -19,15 +19,15 @@ struct BatchSeq {
     ArgmaxResult* host_out;     // pinned slot for the greedy selection
 };
 
-// Exchange tags a batched step takes per layer (attention, O, down).
-inline constexpr int kBatchTagsPerLayer = 3;
+// Exchange tags a batched step takes per layer (attention + O, FFN).
+inline constexpr int kBatchTagsPerLayer = 2;
 
-// One decode step for each sequence: 28 x (norm + QKV + attention pieces in
-// one launch, piece merge + O + residual, norm + gate/up + SwiGLU, down +
-// residual), final norm + tied lm_head + per-sequence argmax. Logits, hidden
-// and selections land in each sequence's buffers. tags[3 l .. 3 l + 2]
-// (nonzero, unique per launch) tag layer l's exchanges between workgroups,
-// which use the first sequence's buffers.
+// One decode step for each sequence: 28 x (norm + QKV + attention + piece
+// merge + O + residual in one launch, norm + gate/up + SwiGLU + down +
+// residual in another), final norm + tied lm_head + per-sequence argmax.
+// Logits, hidden and selections land in each sequence's buffers.
+// tags[2 l], tags[2 l + 1] (nonzero, unique per launch) tag layer l's
+// exchanges between workgroups, which use the first sequence's buffers.
 void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const float* final_norm,
                          const float* cosines, const float* sines, const uint32_t* tags, hipStream_t stream);
 

@@ -1670,11 +1670,10 @@ __global__ __launch_bounds__(512) void qkv_attn_kernel(const QkvAttnArgs a) {
 // merges the pieces in its prologue. The last piece writes the new K/V row.
 struct AttnBatchSeq {
     const float* x;          // residual stream the layer starts from [1024]
-    const uint16_t* embed;   // first layer: the token's embedding row, else null
-    float* x_store;          // first layer: receives fp32 of the embedding row (the residual)
+    const uint16_t* embed;   // first layer: the token's embedding row (the residual is fp32 of it), else null
     uint16_t* keys;          // layer base [8][context][128]
     uint16_t* values;
-    float* partial;          // [8][kAttnSplits][kAttnPartial]
+    float* x_out;            // residual after the O projection
     int pos;
     int context;
 };
@@ -1682,12 +1681,16 @@ struct AttnBatchSeq {
 struct AttnBatchArgs {
     AttnBatchSeq seq[kMaxBatch];
     const uint16_t* w_qkv;   // natural [4096 x 1024]: q rows, k rows, v rows
+    const uint16_t* w_o;     // natural [1024 x 2048]
     const float* in_norm;    // input RMSNorm weights
     const float* q_norm;
     const float* k_norm;
     const float* cosines;
     const float* sines;
     uint64_t* exchange;      // [8 KV heads][kMaxBatch][512] tagged q/k/v rows
+    uint64_t* piece_words;   // [8 KV heads][32 workgroups][2][kXPart] tagged piece partials
+    uint64_t* att_words;     // [8 KV heads][kMaxBatch][256] tagged merged attention rows
+    uint64_t* share_words;   // [1024][kMaxBatch][8 XCDs] tagged O shares
     int* stall;
     float scale;
     int batch;
@@ -1705,7 +1708,7 @@ constexpr int kInFlight = 4;
 template <int NB>
 __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs args) {
     const int w = blockIdx.x, g = w & 7, r = w >> 3, B = args.batch, b = r % B, p = r / B;
-    const int W = B * args.pieces;  // workgroups of this XCD
+    const int W = B * args.pieces;  // attention workgroups of this XCD (the grid holds 32 per XCD)
     const AttnBatchSeq a = args.seq[b];  // by value: loaded once, ahead of the cache rows
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, quad = lane >> 4;
@@ -1815,11 +1818,6 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         r1 += xor_lanes<2>(r1);
         r1 += xor_lanes<1>(r1);
         if ((lane & 7) == 0) nred[wave][lane >> 3] = r1;
-        if (w == 0) {  // first layer: the residual is fp32 of the embedding row
-#pragma unroll
-            for (int bb = 0; bb < kMaxBatch; ++bb)
-                if (bb < B && args.seq[bb].embed) reinterpret_cast<float2*>(args.seq[bb].x_store)[tid] = xv[bb];
-        }
         __syncthreads();
         if (tid < kMaxBatch) {
             const double total = ((nred[0][tid] + nred[1][tid]) + (nred[2][tid] + nred[3][tid])) +
@@ -1868,11 +1866,19 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         __syncthreads();
     };
     project_tile(r);
-    for (int tr = r + W; tr < 32; tr += W) {
-        load_tile(wq, tr);
-        project_tile(tr);
+    // O weights of this workgroup (rows 32 r + 16 (wave & 1) + col, columns
+    // 256 g + 64 (wave >> 1) + 32 st + 8 quad .. + 7), issued ahead of the
+    // K/V stream and used after it.
+    u32x4 wo[2];
+    {
+        const u32x4* op = reinterpret_cast<const u32x4*>(args.w_o + size_t(32 * r + 16 * (wave & 1) + col) * kQDim +
+                                                         256 * g + 64 * (wave >> 1)) + quad;
+        wo[0] = __builtin_nontemporal_load(op);
+        wo[1] = __builtin_nontemporal_load(op + 4);
     }
-    if (p >= ns) return;  // no positions: this workgroup only projected
+    // Workgroups past the batch's pieces, or whose piece holds no position,
+    // only project.
+    if (r < W && p < ns) {
 
     // This workgroup's q/k/v rows (query heads 2g, 2g + 1, key, value) are
     // gathered by wave 0 into LDS before it issues any K/V load; the other
@@ -2069,14 +2075,126 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     };
     const float o = tree([&](int v8) { return wt[v8] * opart[v8][half][j]; });
     const float l = tree([&](int v8) { return wt[v8] * wl[v8][half]; });
-    if (tid < 256) {
-        float* part = a.partial + (size_t(g) * kAttnSplits + p) * kAttnPartial + half * 132;
-        part[j] = o;
-        if (j == 0) {
-            part[128] = mx;
-            part[129] = l;
+    // Pieces p > 0 post (output, max, sum); piece 0 merges its sequence's
+    // pieces in order (out = sum_p e_p o_p / sum_p e_p l_p, e_p =
+    // exp(m_p - max)) and posts the merged rows of both query heads.
+    uint64_t* const my_piece = args.piece_words + ((size_t(g) * 32 + r) * 2 + half) * kXPart;
+    if (p > 0) {
+        if (tid < 256) {
+            exchange_put(my_piece + j, o, args.tag);
+            if (j == 0) {
+                exchange_put(my_piece + 128, mx, args.tag);
+                exchange_put(my_piece + 129, l, args.tag);
+            }
+        }
+    } else if (tid < 256) {
+        float run_m = mx, run_l = l, run_o = o;
+        bool ok = true;
+        for (int p0 = 1; p0 < ns; p0 += 4) {
+            const uint64_t* words[12];
+            float got[12];
+            unsigned want = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int pk = min(p0 + k, ns - 1);
+                const uint64_t* e = args.piece_words + ((size_t(g) * 32 + b + B * pk) * 2 + half) * kXPart;
+                words[k] = e + j;
+                words[4 + k] = e + 128;
+                words[8 + k] = e + 129;
+                got[k] = got[4 + k] = got[8 + k] = 0.f;
+                if (p0 + k < ns) want |= 0x111u << k;
+            }
+            if (ok) ok = exchange_gather<12>(words, args.tag, got, want);
+            float cm = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (p0 + k < ns) cm = fmaxf(cm, got[4 + k]);
+            const float nm = fmaxf(run_m, cm), sc = expf(run_m - nm);
+            run_l *= sc;
+            run_o *= sc;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (p0 + k < ns) {
+                    const float e = expf(got[4 + k] - nm);
+                    run_l += e * got[8 + k];
+                    run_o += e * got[k];
+                }
+            run_m = nm;
+        }
+        if (!ok) *args.stall = 1;
+        exchange_put(args.att_words + (size_t(g) * kMaxBatch + b) * 256 + half * 128 + j, run_o / run_l, args.tag);
+    }
+    }  // attention workgroups
+
+    // O projection of this XCD's two query heads (columns 256 g .. + 255)
+    // for rows 32 r .. 32 r + 31: the merged rows of every sequence, staged
+    // as FP16 hi + lo.
+    bool ok = true;
+    {
+        const uint64_t* words[4];
+        float got[4];
+        unsigned want = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int idx = tid + 512 * k;  // sequence idx / 256, column idx % 256
+            words[k] = args.att_words + size_t(g) * kMaxBatch * 256 + idx;
+            got[k] = 0.f;
+            if ((idx >> 8) < B) want |= 1u << k;
+        }
+        ok = exchange_gather<4>(words, args.tag, got, want);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int idx = tid + 512 * k;
+            _Float16 h, lo;
+            split_half(got[k], h, lo);
+            xh[idx >> 8][idx & 255] = h;
+            xl[idx >> 8][idx & 255] = lo;
+        }
+        __syncthreads();
+    }
+    {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int k = 64 * (wave >> 1) + 32 * st + 8 * quad;
+            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
+            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+            const half8 w8 = __builtin_bit_cast(half8, wo[st]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qpart[wave][lane][e] = acc[e];
+        __syncthreads();
+        // Waves 0-3 take tile 0, waves 4-7 tile 1: element (row 4 (lane / 16)
+        // + (wave & 3), sequence lane % 16), the tile's 4 column ranges
+        // (waves tt, tt + 2, tt + 4, tt + 6) in fixed order; the share goes
+        // through the L2 to the XCD that adds the row.
+        const int tt = wave >> 2, e4 = wave & 3;
+        const float y = (qpart[tt][lane][e4] + qpart[tt + 2][lane][e4]) +
+                        (qpart[tt + 4][lane][e4] + qpart[tt + 6][lane][e4]);
+        const int row = 32 * r + 16 * tt + 4 * (lane >> 4) + e4, seq = lane & 15;
+        if (seq < B) exchange_put_through(args.share_words + (size_t(row) * kMaxBatch + seq) * 8 + g, y, args.tag);
+    }
+    // Rows 32 r + 4 g .. + 3 of every sequence: threads 0..31 (row
+    // 4 g + tid / 8, sequence tid % 8) add the 8 XCD shares to the residual
+    // in fixed order, into the second residual buffer (every workgroup read
+    // the first one).
+    if (tid < 32) {
+        const int row = 32 * r + 4 * g + (tid >> 3), seq = tid & 7;
+        const bool live = seq < B;
+        const uint64_t* base = args.share_words + (size_t(row) * kMaxBatch + seq) * 8;
+        const uint64_t* const words[8] = {base, base + 1, base + 2, base + 3, base + 4, base + 5, base + 6, base + 7};
+        float s8[8] = {};
+        if (ok) ok = exchange_gather<8>(words, args.tag, s8, live ? 0xffu : 0u);
+        if (live) {
+            const float y = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+            const AttnBatchSeq& sq = args.seq[seq];
+            sq.x_out[row] = (sq.embed ? h2f(sq.embed[row]) : sq.x[row]) + y;
         }
     }
+    if (!ok) *args.stall = 1;
 }
 
 
@@ -2498,9 +2616,9 @@ int attn_batch_pieces(const int* positions, int count, int* pieces_out, int& per
     return pieces;
 }
 
-void launch_qkv_attention_batch(const AttnSeq* seqs, int count, const uint16_t* w_qkv, const float* in_norm,
-                                const float* q_norm, const float* k_norm, const float* cosines, const float* sines,
-                                uint64_t* exchange, int* stall, uint32_t tag, hipStream_t stream) {
+void launch_attention_o_batch(const AttnSeq* seqs, int count, const uint16_t* w_qkv, const uint16_t* w_o,
+                              const float* in_norm, const float* q_norm, const float* k_norm, const float* cosines,
+                              const float* sines, uint64_t* words, int* stall, uint32_t tag, hipStream_t stream) {
     require(count >= 1 && count <= kMaxBatch, "attention batch: 1..8 sequences");
     require(tag != 0, "attention batch: exchange tags are nonzero");
     AttnBatchArgs b{};
@@ -2509,36 +2627,40 @@ void launch_qkv_attention_batch(const AttnSeq* seqs, int count, const uint16_t* 
         AttnBatchSeq& a = b.seq[i];
         a.x = seqs[i].x;
         a.embed = seqs[i].embed;
-        a.x_store = seqs[i].x_store;
+        a.x_out = seqs[i].x_out;
         a.keys = seqs[i].keys;
         a.values = seqs[i].values;
-        a.partial = seqs[i].partial;
         a.pos = seqs[i].pos;
         a.context = seqs[i].context;
         require(a.pos >= 0 && a.pos < a.context, "attention batch: position outside the cache");
-        require(a.x != nullptr, "attention batch: a residual row per sequence");
+        require(a.x != nullptr && a.x_out != nullptr && a.x_out != a.x, "attention batch: two residual buffers per sequence");
         positions[i] = a.pos + 1;
     }
     b.w_qkv = w_qkv;
+    b.w_o = w_o;
     b.in_norm = in_norm;
     b.q_norm = q_norm;
     b.k_norm = k_norm;
     b.cosines = cosines;
     b.sines = sines;
-    b.exchange = exchange;
+    b.exchange = words;
+    b.piece_words = words + kBatchPieceOffset;
+    b.att_words = words + kBatchAttOffset;
+    b.share_words = words + kBatchShareOffset;
     b.stall = stall;
     b.scale = 1.0f / std::sqrt(128.0f);
     b.batch = count;
     b.tag = tag;
     int pieces[kMaxBatch], per;
     b.pieces = attn_batch_pieces(positions, count, pieces, per);
-    const dim3 grid(kKVHeads * count * b.pieces);
-    if (per <= 2) attn_batch_kernel<2><<<grid, 512, 0, stream>>>(b);
-    else if (per <= 4) attn_batch_kernel<4><<<grid, 512, 0, stream>>>(b);
-    else if (per <= 6) attn_batch_kernel<6><<<grid, 512, 0, stream>>>(b);
-    else if (per <= 9) attn_batch_kernel<9><<<grid, 512, 0, stream>>>(b);
-    else if (per <= 12) attn_batch_kernel<12><<<grid, 512, 0, stream>>>(b);
-    else attn_batch_kernel<16><<<grid, 512, 0, stream>>>(b);
+    require(count * b.pieces <= 32, "attention batch: at most 32 attention workgroups per XCD");
+    constexpr int kGrid = 256;  // 32 workgroups per XCD: one per QKV tile and per 32 O rows
+    if (per <= 2) attn_batch_kernel<2><<<kGrid, 512, 0, stream>>>(b);
+    else if (per <= 4) attn_batch_kernel<4><<<kGrid, 512, 0, stream>>>(b);
+    else if (per <= 6) attn_batch_kernel<6><<<kGrid, 512, 0, stream>>>(b);
+    else if (per <= 9) attn_batch_kernel<9><<<kGrid, 512, 0, stream>>>(b);
+    else if (per <= 12) attn_batch_kernel<12><<<kGrid, 512, 0, stream>>>(b);
+    else attn_batch_kernel<16><<<kGrid, 512, 0, stream>>>(b);
 }
 
 void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,

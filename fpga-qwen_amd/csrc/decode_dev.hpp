@@ -195,6 +195,12 @@ __device__ __forceinline__ void exchange_put(uint64_t* p, float v, uint32_t tag)
     __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// For a reader on another XCD: an agent-scope store writes through the L2
+// (such a reader's agent-scope load then finds it in memory).
+__device__ __forceinline__ void exchange_put_through(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Two consecutive tagged words; false if they did not both carry `tag`
 // within kExchangeSpins polls. The loop runs while any lane of the wave still
 // waits (a wave-uniform exit), and each lane's result comes from its own

@@ -110,14 +110,23 @@ struct DecodeScratch {
     uint64_t* bexchange;  // [kBatchExchangeWords] batched step exchanges (when this sequence leads a batch)
 };
 
-// Exchange words of a batched step, in the first sequence's buffers:
-// q/k/v rows [8 KV heads][kMaxBatch][512], O quarter sums [64 tiles][3][128],
-// activations [8 XCDs][kMaxBatch][384], down shares [1024][kMaxBatch][8 XCDs].
+// Exchange words of a batched step, in the first sequence's buffers. The
+// attention launch uses q/k/v rows [8 KV heads][kMaxBatch][512], piece
+// partials [8][32 workgroups][2 heads][130], merged rows [8][kMaxBatch][256]
+// and O shares [1024][kMaxBatch][8 XCDs]; the FFN launch activations
+// [8 XCDs][kMaxBatch][384] (over the q/k/v rows: another launch, another
+// tag) and down shares (over the O shares).
 inline constexpr int kBatchQkvWords = kKVHeads * kMaxBatch * 512;
-inline constexpr int kBatchQuarterWords = 64 * 3 * 128;
-inline constexpr int kBatchActWords = 8 * kMaxBatch * (kFFN / 8);
+inline constexpr int kBatchPieceWords = kKVHeads * 32 * 2 * (kHeadDim + 2);
+inline constexpr int kBatchAttWords = kKVHeads * kMaxBatch * 256;
 inline constexpr int kBatchShareWords = kHidden * kMaxBatch * 8;
-inline constexpr int kBatchExchangeWords = kBatchQkvWords + kBatchQuarterWords + kBatchActWords + kBatchShareWords;
+inline constexpr int kBatchActWords = 8 * kMaxBatch * (kFFN / 8);
+inline constexpr int kBatchPieceOffset = kBatchQkvWords;
+inline constexpr int kBatchAttOffset = kBatchPieceOffset + kBatchPieceWords;
+inline constexpr int kBatchShareOffset = kBatchAttOffset + kBatchAttWords;
+inline constexpr int kBatchActOffset = 0;
+static_assert(kBatchActWords <= kBatchQkvWords, "the FFN activations fit the q/k/v words");
+inline constexpr int kBatchExchangeWords = kBatchShareOffset + kBatchShareWords;
 
 // The fused FFN kernel (norm + gate/up + SwiGLU + down in one launch): XCD
 // g computes activations 384 g .. 384 g + 383 and their share of the down
@@ -210,14 +219,13 @@ void launch_decode_layer_pair(const LayerDevice& layer, const uint16_t* embed, i
 void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
                          const PairScratch& pair, ArgmaxResult* host_out, hipStream_t stream);
 
-// One sequence of a batched norm + QKV + attention launch.
+// One sequence of a batched norm + QKV + attention + O launch.
 struct AttnSeq {
     const float* x;          // residual stream the layer starts from
-    const uint16_t* embed;   // first layer: the token's embedding row (x is then overwritten), else null
-    float* x_store;          // first layer: receives fp32 of the embedding row
+    const uint16_t* embed;   // first layer: the token's embedding row (the residual is then fp32 of it), else null
+    float* x_out;            // residual after the O projection (a buffer other than x)
     uint16_t* keys;          // this layer's cache [8][context][128]
     uint16_t* values;
-    float* partial;          // [8][kAttnSplits][kAttnPartial]: per piece and head (o[128], max, sum)
     int pos;                 // position being written
     int context;
 };
@@ -230,16 +238,13 @@ struct AttnSeq {
 // hold positions; the partials the merge reads).
 int attn_batch_pieces(const int* positions, int count, int* pieces_out, int& per);
 
-// RMSNorm + QKV projection + decode attention of one layer for up to
-// kMaxBatch sequences in one launch: each piece of each sequence and KV head
-// writes its (unnormalized output, max, sum) per query head to the
-// sequence's partial buffer, at piece index p. exchange ([8][kMaxBatch][512]
-// words) carries the q/k/v rows between the workgroups of an XCD under
-// `tag` (nonzero, unique per launch for that buffer); stall is set if a
-// workgroup gave up waiting for them.
-void launch_qkv_attention_batch(const AttnSeq* seqs, int count, const uint16_t* w_qkv, const float* in_norm,
-                                const float* q_norm, const float* k_norm, const float* cosines, const float* sines,
-                                uint64_t* exchange, int* stall, uint32_t tag, hipStream_t stream);
+// RMSNorm + QKV projection + decode attention + O projection + residual of
+// one layer for up to kMaxBatch sequences in one launch (256 workgroups).
+// words: the batched exchange buffer (kBatchExchangeWords), used under `tag`
+// (nonzero, unique per launch); stall is set if a workgroup gave up waiting.
+void launch_attention_o_batch(const AttnSeq* seqs, int count, const uint16_t* w_qkv, const uint16_t* w_o,
+                              const float* in_norm, const float* q_norm, const float* k_norm, const float* cosines,
+                              const float* sines, uint64_t* words, int* stall, uint32_t tag, hipStream_t stream);
 
 // The batch-1 decode projections of one layer as the step runs them, on
 // caller buffers (parity-test entries):
