@@ -39,6 +39,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;  // waves of the K = 1024 kernels (norm prologues, lm_head)
 using dev::exchange_gather;
+using dev::masked_b;
 using dev::exchange_put;
 using dev::exchange_put_through;
 using dev::xor_lanes;
@@ -206,7 +207,6 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
     floatx4 acc[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
@@ -214,8 +214,8 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
             // k slot (quad, i) of step s holds k = 128 blk + 32 s + 8 quad + i of this wave's range
             // (each weight load reads 64 contiguous bytes of every tile row).
             const int k = wave * KW + 128 * blk + 32 * s + 8 * quad;
-            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
-            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+            const half8 bh = masked_b<half8>(&xh[col & 7][k], col < kMaxBatch);
+            const half8 bl = masked_b<half8>(&xl[col & 7][k], col < kMaxBatch);
 #pragma unroll
             for (int t = 0; t < kTiles; ++t) {
                 const half8 w8 = __builtin_bit_cast(half8, wa[t][blk][s]);
@@ -425,7 +425,6 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
         __syncthreads();
     }
 
-    const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
     // 2. Gate/up and SwiGLU.
     {
         floatx4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
@@ -433,8 +432,8 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
         for (int st = 0; st < 4; ++st) {
             // k slot (quad, e) of step st holds column 128 wave + 32 st + 8 quad + e.
             const int k = 128 * wave + 32 * st + 8 * quad;
-            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
-            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+            const half8 bh = masked_b<half8>(&xh[col & 7][k], col < kMaxBatch);
+            const half8 bl = masked_b<half8>(&xl[col & 7][k], col < kMaxBatch);
             const half8 g8 = __builtin_bit_cast(half8, wg[st]), u8 = __builtin_bit_cast(half8, wu[st]);
             accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(g8, bh, accg, 0, 0, 0);
             accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(g8, bl, accg, 0, 0, 0);
@@ -495,8 +494,8 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
 #pragma unroll
         for (int st = 0; st < 3; ++st) {
             const int k = 96 * kq + 32 * st + 8 * quad;
-            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&ah[col & 7][k]) : zero;
-            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&al[col & 7][k]) : zero;
+            const half8 bh = masked_b<half8>(&ah[col & 7][k], col < kMaxBatch);
+            const half8 bl = masked_b<half8>(&al[col & 7][k], col < kMaxBatch);
             const half8 d8 = __builtin_bit_cast(half8, wd[st]);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(d8, bh, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(d8, bl, acc, 0, 0, 0);
@@ -529,6 +528,187 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
         }
     }
     if (!ok) *a.stall = 1;
+}
+
+// Final norm + tied lm_head + first pass of the per-sequence greedy
+// selection for the batched step (engine/core.cpp:642-645, main.cpp:51-59)
+// as one workgroup per CU: every workgroup forms RMSNorm(x) of all
+// sequences as FP16 hi + lo in LDS, then streams the 16-row tiles
+// w, w + 256, ... of the embedding matrix with kLmInFlight tiles in flight
+// (the 8 waves split K, summed in a fixed tree per tile), writes the logits
+// and keeps each sequence's best (largest value, lowest id among equals,
+// nonfinite flagged) for the second pass.
+constexpr int kLmInFlight = 4;
+constexpr int kLmTiles = kVocab / kBatchRows;  // 9496
+constexpr int kLmTilesPerGroup = (kLmTiles + kBatchLmGroups - 1) / kBatchLmGroups;
+static_assert(kVocab % kBatchRows == 0, "whole 16-row tiles");
+
+struct BatchLmArgs {
+    const uint16_t* w;         // embedding matrix [kVocab x 1024] (tied head)
+    const float* norm_w;       // final RMSNorm weights
+    const float* x[kMaxBatch];
+    float* hidden[kMaxBatch];  // final normalized rows
+    float* logits[kMaxBatch];
+    float* lm_value;           // [kBatchLmGroups][kMaxBatch] per-group best
+    int* lm_index;
+    int* lm_bad;
+    int batch;
+};
+
+__global__ __launch_bounds__(512) void lm_head_batch_kernel(const BatchLmArgs a) {
+    const int w = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, quad = lane >> 4;
+    const int B = a.batch;
+    float2 xv[kMaxBatch];
+#pragma unroll
+    for (int bb = 0; bb < kMaxBatch; ++bb) xv[bb] = reinterpret_cast<const float2*>(a.x[min(bb, B - 1)])[tid];
+    const float2 wn = reinterpret_cast<const float2*>(a.norm_w)[tid];
+
+    __shared__ __align__(16) _Float16 xh[kMaxBatch][kHidden + 8];
+    __shared__ __align__(16) _Float16 xl[kMaxBatch][kHidden + 8];
+    __shared__ double nred[8][kMaxBatch];
+    __shared__ float inv_row[kMaxBatch];
+    __shared__ float part[2][8][64][4];
+    // RMSNorm of every row (as in ffn_batch_kernel).
+    {
+        double sq[kMaxBatch];
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float q0 = xv[bb].x * xv[bb].x, q1 = xv[bb].y * xv[bb].y;
+            sq[bb] = static_cast<double>(q0) + static_cast<double>(q1);
+        }
+        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+        double r4[4], r2[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const double keep = b5 ? sq[4 + i] : sq[i], send = b5 ? sq[i] : sq[4 + i];
+            r4[i] = keep + xor_lanes<32>(send);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const double keep = b4 ? r4[2 + i] : r4[i], send = b4 ? r4[i] : r4[2 + i];
+            r2[i] = keep + xor_lanes<16>(send);
+        }
+        double r1 = (b3 ? r2[1] : r2[0]) + xor_lanes<8>(b3 ? r2[0] : r2[1]);
+        r1 += xor_lanes<4>(r1);
+        r1 += xor_lanes<2>(r1);
+        r1 += xor_lanes<1>(r1);
+        if ((lane & 7) == 0) nred[wave][lane >> 3] = r1;
+        __syncthreads();
+        if (tid < kMaxBatch) {
+            const double total = ((nred[0][tid] + nred[1][tid]) + (nred[2][tid] + nred[3][tid])) +
+                                 ((nred[4][tid] + nred[5][tid]) + (nred[6][tid] + nred[7][tid]));
+            inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(kHidden) + 1e-6f);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float inv = inv_row[bb];
+            const float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
+            if (w == 0 && bb < B) reinterpret_cast<float2*>(a.hidden[bb])[tid] = make_float2(n0, n1);
+            _Float16 h0, l0, h1, l1;
+            split_half(n0, h0, l0);
+            split_half(n1, h1, l1);
+            *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
+            *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
+        }
+        __syncthreads();
+    }
+
+    // Tile k of this workgroup: rows 16 (w + 256 k) ..; loads past the last
+    // tile repeat it and are not used.
+    const int ntiles = (kLmTiles - w + kBatchLmGroups - 1) / kBatchLmGroups;
+    auto load_tile = [&](u32x4 (&wt)[4], int k) {
+        const int t = min(w + kBatchLmGroups * k, kLmTiles - 1);
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(kBatchRows * t + col) * kHidden + 128 * wave) + quad;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 4 * st);
+    };
+    // Epilogue element of threads 0..255: row 4 (lane / 16) + wave of the
+    // tile, sequence lane % 16; its running best over the tiles.
+    const int eb = lane & 15, erow = 4 * (lane >> 4) + (wave & 3);
+    // Loaded (and waited for, by the empty asm that uses it) before the
+    // stream: a pointer still pending inside the loop would wait behind the
+    // tiles in flight.
+    float* out = a.logits[min(eb, B - 1)];
+    asm volatile("" : "+v"(out));
+    u32x4 ring[kLmInFlight][4];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kLmInFlight; ++u) load_tile(ring[u], u);
+    __builtin_amdgcn_sched_barrier(0);
+    float bv = -INFINITY, lg[kLmTilesPerGroup];
+    int bi = INT_MAX, bad = 0;
+    // Fully unrolled (compile-time ring slots and tile counts, so every wait
+    // covers exactly the oldest tile).
+#pragma unroll
+    for (int k0 = 0; k0 < kLmTilesPerGroup; k0 += kLmInFlight) {
+#pragma unroll
+        for (int u = 0; u < kLmInFlight; ++u) {
+            const int k = k0 + u;
+            if (k >= kLmTilesPerGroup) break;
+            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int kk = 128 * wave + 32 * st + 8 * quad;
+                const half8 bh = masked_b<half8>(&xh[col & 7][kk], col < kMaxBatch);
+                const half8 bl = masked_b<half8>(&xl[col & 7][kk], col < kMaxBatch);
+                const half8 w8 = __builtin_bit_cast(half8, ring[u][st]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);
+            }
+            if (k + kLmInFlight < kLmTilesPerGroup) load_tile(ring[u], k + kLmInFlight);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part[k & 1][wave][lane][e] = acc[e];
+            __syncthreads();
+            if (wave < 4) {
+                const auto f = [&](int v8) { return part[k & 1][v8][lane][wave]; };
+                const float y = ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
+                const int row = kBatchRows * (w + kBatchLmGroups * k) + erow;
+                lg[k] = y;
+                const bool use = k < ntiles && eb < B;
+                bad |= use && !__builtin_isfinite(y);
+                if (use && better(y, row, bv, bi)) { bv = y; bi = row; }
+            }
+        }
+    }
+    // The logits are stored after the stream: on this GPU a store counts
+    // among the outstanding loads, and conditional stores inside the loop
+    // would make every wait cover all the tiles in flight.
+    if (wave < 4 && eb < B) {
+#pragma unroll
+        for (int k = 0; k < kLmTilesPerGroup; ++k)
+            if (k < ntiles) out[kBatchRows * (w + kBatchLmGroups * k) + erow] = lg[k];
+    }
+    // Best per sequence over the 16 rows' threads (lanes l, l ^ 16, l ^ 32,
+    // l ^ 48 of waves 0-3), then this group's entry.
+    __shared__ float mv[4][16];
+    __shared__ int mi[4][16], mb[4][16];
+    if (wave < 4) {
+#pragma unroll
+        for (int off = 16; off < 64; off <<= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            bad |= __shfl_xor(bad, off);
+            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        if (lane < 16) { mv[wave][lane] = bv; mi[wave][lane] = bi; mb[wave][lane] = bad; }
+    }
+    __syncthreads();
+    if (tid < B) {
+        float v0 = mv[0][tid];
+        int i0 = mi[0][tid], b0 = mb[0][tid];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) {
+            b0 |= mb[q][tid];
+            if (better(mv[q][tid], mi[q][tid], v0, i0)) { v0 = mv[q][tid]; i0 = mi[q][tid]; }
+        }
+        const size_t slot = size_t(w) * kMaxBatch + tid;
+        a.lm_value[slot] = v0;
+        a.lm_index[slot] = i0;
+        a.lm_bad[slot] = b0;
+    }
 }
 
 // Second pass of the per-sequence greedy selection.
@@ -640,7 +820,7 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
         }
         ffn_batch_kernel<<<256, 512, 0, stream>>>(f);
     }
-    BatchGemvArgs lm{};
+    BatchLmArgs lm{};
     lm.w = embed;  // tied head (engine/core.cpp:643-645)
     lm.norm_w = final_norm;
     lm.batch = count;
@@ -650,14 +830,14 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
     lm.lm_bad = s0.lm_bad;
     BatchResults res{};
     for (int b = 0; b < count; ++b) {
-        lm.in[b] = seqs[b].s.x;
-        lm.out[b] = seqs[b].s.logits;
+        lm.x[b] = seqs[b].s.x;
+        lm.logits[b] = seqs[b].s.logits;
         lm.hidden[b] = seqs[b].s.hidden;
         res.device[b] = seqs[b].s.result;
         res.host[b] = seqs[b].host_out;
         res.stall[b] = seqs[b].s.stall;
     }
-    bgemv<kHidden, kBLmHead, kBatchLmTiles>(lm, kVocab, stream);
+    lm_head_batch_kernel<<<kBatchLmGroups, 512, 0, stream>>>(lm);
     batch_argmax_kernel<<<count, 1024, 0, stream>>>(s0.lm_value, s0.lm_index, s0.lm_bad, res);
 }
 

@@ -1843,13 +1843,12 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     // loads issued after them).
     auto project_tile = [&](int tr) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-        const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             // k slot (quad, e) of step st holds column 128 wave + 32 st + 8 quad + e.
             const int k = 128 * wave + 32 * st + 8 * quad;
-            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
-            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+            const half8 bh = masked_b<half8>(&xh[col & 7][k], col < kMaxBatch);
+            const half8 bl = masked_b<half8>(&xl[col & 7][k], col < kMaxBatch);
             const half8 w8 = __builtin_bit_cast(half8, wq[st]);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);
@@ -2154,12 +2153,11 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     }
     {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-        const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const int k = 64 * (wave >> 1) + 32 * st + 8 * quad;
-            const half8 bh = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xh[col & 7][k]) : zero;
-            const half8 bl = col < kMaxBatch ? *reinterpret_cast<const half8*>(&xl[col & 7][k]) : zero;
+            const half8 bh = masked_b<half8>(&xh[col & 7][k], col < kMaxBatch);
+            const half8 bl = masked_b<half8>(&xl[col & 7][k], col < kMaxBatch);
             const half8 w8 = __builtin_bit_cast(half8, wo[st]);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);

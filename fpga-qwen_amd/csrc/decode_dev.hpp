@@ -120,6 +120,16 @@ __device__ __forceinline__ void norm_to_lds(const float (&v)[N / THREADS], const
     }
 }
 
+// 8 FP16 values of an MFMA B operand from LDS, zeroed for lanes whose column
+// is not a live sequence. Read unconditionally and masked (no branch): a
+// branch around the read makes the next wait cover every load in flight.
+template <class H8>
+__device__ __forceinline__ H8 masked_b(const _Float16* p, bool live) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    const unsigned m = live ? 0xffffffffu : 0u;
+    return __builtin_bit_cast(H8, u32x4{v.x & m, v.y & m, v.z & m, v.w & m});
+}
+
 // Two 16-byte pieces of a chain-permuted key row as the 8 chain steps each
 // of lane c: pieces c and c + 8 (see kperm).
 __device__ __forceinline__ void key_pieces(const uint16_t* row, int c, u32x4& lo, u32x4& hi) {

@@ -184,9 +184,9 @@ void Engine::init_state() {
     s.hidden = device_alloc<float>(kHidden);
     s.attn_partial = device_alloc<float>(size_t(kKVHeads) * kAttnSplits * kAttnPartial);
     s.o_part = device_alloc<float>(size_t(kOParts) * kHidden);
-    s.lm_value = device_alloc<float>(size_t(kBatchLmGroups) * kMaxBatch);
-    s.lm_index = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
-    s.lm_bad = device_alloc<int>(size_t(kBatchLmGroups) * kMaxBatch);
+    s.lm_value = device_alloc<float>(kLmPartials);
+    s.lm_index = device_alloc<int>(kLmPartials);
+    s.lm_bad = device_alloc<int>(kLmPartials);
     s.result = device_alloc<ArgmaxResult>(1);
     s.xm = device_alloc<float>(kHidden);
     s.dparts = device_alloc<float>(size_t(kFfnSlices) * kHidden);

@@ -64,12 +64,13 @@ __host__ __device__ inline bool attn_fused(int n) { return n <= kFusedMaxPositio
 
 inline constexpr int kMaxBatch = 8;             // sequences per batched decode step
 inline constexpr int kBatchRows = 16;           // output rows of one batched-GEMV MFMA tile
-inline constexpr int kBatchLmTiles = 4;         // MFMA tiles per batched lm_head workgroup
-inline constexpr int kBatchLmGroups = kVocab / (kBatchRows * kBatchLmTiles);  // 2374 lm_head workgroups
-static_assert(kVocab % (kBatchRows * kBatchLmTiles) == 0, "batched lm_head tiles must cover the vocabulary");
+inline constexpr int kBatchLmGroups = 256;       // batched lm_head workgroups (one per CU)
 
 inline constexpr int kLmWaves = 8;              // lm_head workgroup waves
 inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 2374 workgroups
+// Entries of the lm_head partial buffers: the batched head's groups x sequences,
+// or two verification rows of the single-sequence head.
+inline constexpr int kLmPartials = kBatchLmGroups * kMaxBatch > 2 * kLmGroups ? kBatchLmGroups * kMaxBatch : 2 * kLmGroups;
 static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
 
 struct LayerDevice {
@@ -97,7 +98,7 @@ struct DecodeScratch {
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
     float* o_part;        // [16][1024]: per-query-head partial O projections (batched decode: down K slices)
-    float* lm_value;      // [kBatchLmGroups x kMaxBatch] argmax partials (batch-1 uses kLmGroups)
+    float* lm_value;      // [kLmPartials] argmax partials: [kBatchLmGroups][kMaxBatch] (batched), [2][kLmGroups] (pair)
     int* lm_index;
     int* lm_bad;
     ArgmaxResult* result; // [1] device copy of the selection
