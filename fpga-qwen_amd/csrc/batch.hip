@@ -787,6 +787,12 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
     require(count >= 1 && count <= kMaxBatch, "batched decode: 1..8 sequences");
     for (int l = 0; l < kBatchTagsPerLayer * kLayers; ++l) require(tags[l] != 0, "batched decode: exchange tags are nonzero");
     uint64_t* const words = seqs[0].s.bexchange;
+    for (int b = 0; b < count; ++b) {
+        const BatchSeq& q = seqs[b];
+        require(q.shared_seq >= 0 && q.shared_seq < count && q.shared >= 0 && q.shared % 64 == 0 &&
+                    q.shared <= q.pos && q.shared <= seqs[q.shared_seq].pos,
+                "batched decode: shared rows outside both caches");
+    }
     for (int l = 0; l < kLayers; ++l) {
         const LayerDevice& W = seqs[0].layers[l];  // weights are shared; K/V are per sequence
         // The residual is in x at each layer's start; attention + O leave it
@@ -800,7 +806,11 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
                             seqs[b].layers[l].keys,
                             seqs[b].layers[l].values,
                             seqs[b].pos,
-                            seqs[b].context};
+                            seqs[b].context,
+                            seqs[seqs[b].shared_seq].layers[l].keys,
+                            seqs[seqs[b].shared_seq].layers[l].values,
+                            seqs[seqs[b].shared_seq].context,
+                            seqs[b].shared};
         }
         launch_attention_o_batch(as, count, W.qkv_n, W.o_n, W.in_norm, W.q_norm, W.k_norm, cosines, sines, words,
                                  seqs[0].s.stall, tags[kBatchTagsPerLayer * l], stream);

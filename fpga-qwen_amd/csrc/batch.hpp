@@ -17,6 +17,8 @@ struct BatchSeq {
     int token;                  // id consumed at pos
     int context;                // K/V cache capacity
     ArgmaxResult* host_out;     // pinned slot for the greedy selection
+    int shared_seq;             // batch index of the sequence whose K/V rows [0, shared) equal this one's
+    int shared;                 // multiple of 64, at most pos (0: none)
 };
 
 // Exchange tags a batched step takes per layer (attention + O, FFN).

@@ -1676,6 +1676,10 @@ struct AttnBatchSeq {
     float* x_out;            // residual after the O projection
     int pos;
     int context;
+    const uint16_t* shared_keys;    // layer base of a cache whose rows [0, shared) equal these
+    const uint16_t* shared_values;
+    int shared_context;
+    int shared;                     // multiple of 64, at most pos
 };
 
 struct AttnBatchArgs {
@@ -1762,13 +1766,25 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         __builtin_amdgcn_make_buffer_rsrc(a.keys + head_base * 128, 0, t_end * 256, kBufferWord3);
     const __amdgpu_buffer_rsrc_t vrs =
         __builtin_amdgcn_make_buffer_rsrc(a.values + head_base * 128, 0, t_end * 256, kBufferWord3);
+    // Blocks below a.shared come from the shared copy, whose descriptors
+    // cover the rows of this piece below a.shared; every sequence of the
+    // batch with that copy reads the same addresses, on this XCD (KV head g),
+    // so all but the first reads hit in its L2.
+    const size_t shared_base = size_t(g) * a.shared_context;
+    const int shared_end = min(a.shared, t_end);
+    const __amdgpu_buffer_rsrc_t skrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.shared_keys) + shared_base * 128, 0, max(shared_end, 0) * 256, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t svrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.shared_values) + shared_base * 128, 0, max(shared_end, 0) * 256, kBufferWord3);
     const int koff = (t_begin + grp) * 256 + 16 * c;
     const int voff = (t_begin + 8 * wave + vsub) * 256 + 16 * vcg;
     auto load_block = [&](u32x4 (&k)[2], u32x4 (&v)[2], int i) {
-        k[0] = __builtin_amdgcn_raw_buffer_load_b128(krs, koff, 16384 * i, kLoadNT);
-        k[1] = __builtin_amdgcn_raw_buffer_load_b128(krs, koff + 128, 16384 * i, kLoadNT);
-        v[0] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, 16384 * i, kLoadNT);
-        v[1] = __builtin_amdgcn_raw_buffer_load_b128(vrs, voff + 1024, 16384 * i, kLoadNT);
+        const bool shared = t_begin + 64 * i < a.shared;  // uniform; a.shared is a multiple of 64
+        const __amdgpu_buffer_rsrc_t kb = shared ? skrs : krs, vb = shared ? svrs : vrs;
+        k[0] = __builtin_amdgcn_raw_buffer_load_b128(kb, koff, 16384 * i, kLoadNT);
+        k[1] = __builtin_amdgcn_raw_buffer_load_b128(kb, koff + 128, 16384 * i, kLoadNT);
+        v[0] = __builtin_amdgcn_raw_buffer_load_b128(vb, voff, 16384 * i, kLoadNT);
+        v[1] = __builtin_amdgcn_raw_buffer_load_b128(vb, voff + 1024, 16384 * i, kLoadNT);
     };
     u32x4 kr[kInFlight][2], vr[kInFlight][2];
 
@@ -2630,7 +2646,14 @@ void launch_attention_o_batch(const AttnSeq* seqs, int count, const uint16_t* w_
         a.values = seqs[i].values;
         a.pos = seqs[i].pos;
         a.context = seqs[i].context;
+        a.shared_keys = seqs[i].shared_keys;
+        a.shared_values = seqs[i].shared_values;
+        a.shared_context = seqs[i].shared_context;
+        a.shared = seqs[i].shared;
         require(a.pos >= 0 && a.pos < a.context, "attention batch: position outside the cache");
+        require(a.shared >= 0 && a.shared % 64 == 0 && a.shared <= a.pos && a.shared <= a.shared_context &&
+                    (a.shared == 0 || (a.shared_keys != nullptr && a.shared_values != nullptr)),
+                "attention batch: shared rows outside the caches");
         require(a.x != nullptr && a.x_out != nullptr && a.x_out != a.x, "attention batch: two residual buffers per sequence");
         positions[i] = a.pos + 1;
     }

@@ -3,6 +3,7 @@
 #include "engine.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -215,6 +216,8 @@ void Engine::init_state() {
 
     if (const char* env = std::getenv("QWEN_HIP_FUSED_FFN")) fused_ffn_ = std::string(env) != "0";
     if (const char* env = std::getenv("QWEN_HIP_FUSED_ATTENTION")) fused_attn_ = std::string(env) != "0";
+    if (const char* env = std::getenv("QWEN_HIP_SHARED_PREFIX")) share_prefix_ = std::string(env) != "0";
+    renew_content();
 
     penalized_ = device_alloc<uint8_t>(kVocab);
     top_scratch_ = device_alloc<uint8_t>(top_scores_scratch_bytes());
@@ -271,17 +274,26 @@ void Engine::invalidate() {
     host_logits_valid_ = host_hidden_valid_ = false;
 }
 
+void Engine::renew_content() {
+    static std::atomic<uint64_t> next_id{1};
+    content_id_ = next_id.fetch_add(1);
+}
+
 // engine/core.cpp:718-721
 void Engine::reset() {
     pos_ = 0;
     pending_ = false;
+    prefix_len_ = 0;
+    renew_content();
     invalidate();
 }
 
 // engine/core.cpp:722-727
 void Engine::truncate(int position) {
     require(position >= 0 && position <= pos_, "Rewind position out of range");
+    if (position < pos_) renew_content();  // rows from position on will be rewritten
     pos_ = position;
+    prefix_len_ = std::min(prefix_len_, position);
     pending_ = false;
     invalidate();
 }
@@ -407,9 +419,15 @@ void Engine::copy_prefix(const Engine& src, int positions) {
     require(positions >= 0 && positions <= src.pos_, "Rewind position out of range");
     require(positions <= options_.context, "Context capacity exceeded");
     invalidate();
+    if (&src == this) {  // a rewind of this sequence
+        truncate(positions);
+        return;
+    }
     pos_ = 0;
+    prefix_len_ = 0;
+    renew_content();
     const size_t row = size_t(kHeadDim) * sizeof(uint16_t);
-    if (positions > 0 && &src != this) {
+    if (positions > 0) {
         HIP_CHECK(hipStreamSynchronize(src.stream_));
         for (int l = 0; l < kLayers; ++l) {
             HIP_CHECK(hipMemcpy2DAsync(layers_[l].keys, row * options_.context, src.layers_[l].keys,
@@ -422,6 +440,14 @@ void Engine::copy_prefix(const Engine& src, int positions) {
         sync();
     }
     pos_ = positions;
+    // The copied rows are src's content; rows src itself copied are that
+    // copy's source's content, so a copy of a copy joins the first copies.
+    if (positions <= src.prefix_len_) {
+        prefix_id_ = src.prefix_id_;
+    } else {
+        prefix_id_ = src.content_id_;
+    }
+    prefix_len_ = positions;
 }
 
 // Validates every sequence before running any (as append does for one).
@@ -437,6 +463,27 @@ void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
     }
     BatchSeq bs[kMaxBatch];
     Engine& lead = *seqs[0];
+    // Sequences holding copies of the same rows read them from the first
+    // such sequence of the batch, up to the shorter of the two copies (whole
+    // 64-row blocks).
+    int shared_seq[kMaxBatch], shared[kMaxBatch];
+    for (int i = 0; i < count; ++i) {
+        const Engine& e = *seqs[i];
+        shared_seq[i] = i;
+        shared[i] = 0;
+        if (!e.share_prefix_ || e.prefix_len_ < 64) continue;
+        for (int j = 0; j < i; ++j) {
+            const Engine& f = *seqs[j];
+            if (f.share_prefix_ && f.prefix_id_ == e.prefix_id_ && f.prefix_len_ >= 64 && shared_seq[j] == j) {
+                shared_seq[i] = j;
+                break;
+            }
+        }
+    }
+    for (int i = 0; i < count; ++i) {
+        if (shared_seq[i] == i) continue;
+        shared[i] = std::min(seqs[i]->prefix_len_, seqs[shared_seq[i]]->prefix_len_) / 64 * 64;
+    }
     // The batched launches exchange through the first sequence's buffers,
     // which its single-sequence launches use too: tags from its counter.
     uint32_t tags[kBatchTagsPerLayer * kLayers];
@@ -444,7 +491,8 @@ void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
     for (int i = 0; i < count; ++i) {
         Engine& e = *seqs[i];
         e.invalidate();
-        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_};
+        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_,
+                         shared_seq[i], shared[i]};
         HIP_CHECK(hipStreamSynchronize(e.stream_));
     }
     launch_decode_batch(bs, count, lead.embed_, lead.final_norm_, lead.cosines_, lead.sines_, tags, lead.stream_);

@@ -137,6 +137,17 @@ private:
     // QWEN_HIP_FUSED_ATTENTION=0; its launches take tags from the same counter.
     bool fused_attn_ = true;
     uint32_t ffn_tag_ = 0;
+    // Identity of this sequence's K/V rows [0, pos_): a new process-unique
+    // id whenever rows below pos_ may be rewritten (construction, reset,
+    // rewind, copy_prefix). A copy records its source's id and length: rows
+    // [0, prefix_len_) are that content, so sequences of one batched step
+    // with the same prefix_id_ read those rows from one cache (unless
+    // QWEN_HIP_SHARED_PREFIX=0).
+    uint64_t content_id_ = 0;
+    uint64_t prefix_id_ = 0;
+    int prefix_len_ = 0;
+    bool share_prefix_ = true;
+    void renew_content();
     bool has_logits_ = false;
     bool pending_ = false;
     std::vector<float> host_logits_, host_hidden_;

@@ -229,6 +229,14 @@ struct AttnSeq {
     uint16_t* values;
     int pos;                 // position being written
     int context;
+    // Rows [0, shared) hold the same values in this cache and in the cache at
+    // shared_keys / shared_values (capacity shared_context), which the other
+    // sequences of the batch with that copy read too, so the rows come from
+    // HBM once per batch. shared is a multiple of 64 and at most pos.
+    const uint16_t* shared_keys;
+    const uint16_t* shared_values;
+    int shared_context;
+    int shared;
 };
 
 // Pieces per (sequence, KV head) of a batched attention launch over

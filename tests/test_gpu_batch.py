@@ -124,6 +124,62 @@ def test_copy_prefix_equals_truncate(qpkg, pack0):
             b.close()
 
 
+def _prefix_family(qpkg, pack0):
+    """A base sequence and five sequences built from copies of its rows:
+    copies of 700 and 520 rows, a 650-row copy rewound to 200 and refilled
+    with other tokens, a copy of the first copy (600 rows), and a copy taken
+    after the base was rewound to 100 and refilled (its rows 100.. differ)."""
+    prompt = PROMPTS['long_3968']
+    base = qpkg.Model(pack0, context=4096)
+    base.prefill(prompt[:700])
+    seqs = []
+    for source_index, rows, rewind, suffix in ((None, 700, None, prompt[1000:1010]),
+                                               (None, 520, None, prompt[1100:1150]),
+                                               (None, 650, 200, prompt[1200:1500]),
+                                               (0, 600, None, prompt[1300:1330])):
+        m = base.share(context=2048)
+        m.copy_prefix(base if source_index is None else seqs[source_index], rows)
+        if rewind is not None:
+            m.truncate(rewind)
+        m.prefill(suffix)
+        seqs.append(m)
+    base.truncate(100)
+    base.prefill(prompt[2000:2500])
+    m = base.share()
+    m.copy_prefix(base, 450)
+    m.prefill(prompt[2600:2620])
+    seqs.append(m)
+    return seqs + [base]
+
+
+@pytest.mark.gpu
+def test_shared_prefix_rows_bit_identical(qpkg, pack0, monkeypatch):
+    """Sequences of a batched step that hold copies of the same rows read
+    them from one cache (whole 64-row blocks up to the shorter copy). The
+    rows are equal, so every step's logits must equal, bit for bit, those of
+    the same sequences each reading its own cache (QWEN_HIP_SHARED_PREFIX=0
+    when they are created). A copy rewound below its prefix, or one of a
+    source that was rewound and refilled, would read wrong rows if it were
+    still grouped: those sequences' logits would then differ."""
+    monkeypatch.setenv('QWEN_HIP_SHARED_PREFIX', '0')
+    own = _prefix_family(qpkg, pack0)
+    monkeypatch.delenv('QWEN_HIP_SHARED_PREFIX')
+    shared = _prefix_family(qpkg, pack0)
+    try:
+        tokens = [m.greedy() for m in shared]
+        assert tokens == [m.greedy() for m in own]
+        for _ in range(4):
+            qpkg.step_batch(shared, tokens)
+            qpkg.step_batch(own, tokens)
+            for i, (a, b) in enumerate(zip(shared, own)):
+                assert a.position() == b.position()
+                assert np.array_equal(a.logits().view(np.uint32), b.logits().view(np.uint32)), i
+            tokens = [m.greedy() for m in shared]
+    finally:
+        for m in shared + own:
+            m.close()
+
+
 @pytest.mark.gpu
 def test_step_batch_validates_before_running(qpkg, pack0):
     prompt = PROMPTS['long_3968']
