@@ -2,22 +2,27 @@
 // weights (the prefix-reuse serving workload). The reference is
 // single-stream; per sequence this computes what qwen_cpu::Model::step does
 // (engine/core.cpp:353-646, 707-714), but every projection reads each weight
-// matrix once for all rows: a skinny GEMM on the matrix cores instead of one
-// GEMV per sequence.
+// matrix once for all sequences, on the matrix cores.
 //
-// Skinny GEMM (bgemv_kernel): Y[b][o] = sum_k X[b][k] W[o][k], W natural
-// row-major FP16, b < 8. Workgroup = 16 output rows per MFMA tile (one
-// 16x16x32 tile, A = W rows, B = X^T with the 8 sequences in columns 0..7;
-// the lm_head takes 4 tiles per workgroup) and one wave per 256 columns of K
-// (4, 8 or 12 waves: a wave retires about one 1 KiB load per 100 ns, so the
-// inputs and weights a workgroup streams are spread over that many waves);
-// the waves' parts are summed in LDS in a fixed order. X enters the matrix cores
-// as FP16 hi + lo (hi = fp16(x), lo = fp16(x - hi)), so the products are
-// exact and the sums FP32, as in the prefill GEMMs. In each weight load the 4
-// lanes of a tile row read 64 contiguous bytes (the summation order inside a
-// 128-wide K block is a fixed permutation of k, applied to A and B alike).
-// RMSNorm prologues (FP32 squares, FP64 sums per row) and the residual /
-// SwiGLU / argmax epilogues are fused as in the batch-1 kernels.
+// A step is 28 pairs of launches of 256 workgroups (one per CU), then the
+// head:
+//  * attention (decode.hip, attn_batch_kernel): RMSNorm + QKV + QK-norm /
+//    RoPE + attention over 64-position blocks + merge of the position pieces
+//    + O + residual;
+//  * FFN (ffn_batch_kernel, below): RMSNorm + gate/up + SwiGLU + down +
+//    residual;
+//  * lm_head_batch_kernel (final norm + tied head + per-workgroup best) and
+//    batch_argmax_kernel (per-sequence greedy selection).
+// Workgroup w runs on XCD w % 8; values move between workgroups as tagged
+// words inside an XCD (its L2) or, for the residual shares, between XCDs.
+// Every matrix product is v_mfma_f32_16x16x32_f16 with A = 16 weight rows
+// (the 4 lanes of a row reading 64 contiguous bytes per load) and B = the 8
+// sequences' inputs as FP16 hi + lo (hi = fp16(x), lo = fp16(x - hi)) in
+// columns 0..7, so the products are exact and the sums FP32; a kernel's
+// waves split K and their parts are added in a fixed order.
+//
+// bgemv_kernel is the plain skinny GEMM (Y[b] = W X[b], b < 8) behind the
+// batched-GEMV parity entry.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -37,7 +42,6 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;  // waves of the K = 1024 kernels (norm prologues, lm_head)
 using dev::exchange_gather;
 using dev::masked_b;
 using dev::exchange_put;
@@ -46,167 +50,61 @@ using dev::xor_lanes;
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
-enum BatchMode { kBPlain, kBGateUp, kBLmHead };
-
 struct BatchGemvArgs {
-    const uint16_t* w;                 // natural [rows x K]; gate/up: 3072 gate rows then 3072 up rows
-    const float* norm_w;               // RMSNorm weights (gate/up, lm_head)
-    const float* in[kMaxBatch];        // input rows: x (norm modes), activation (down)
-    float* out[kMaxBatch];             // output rows (plain, gate/up: activation, lm_head: logits)
-    float* hidden[kMaxBatch];          // lm_head: final normalized rows
-    float* lm_value;                   // lm_head argmax partials [groups][kMaxBatch]
-    int* lm_index;
-    int* lm_bad;
+    const uint16_t* w;                 // natural [rows x K]
+    const float* in[kMaxBatch];        // input rows
+    float* out[kMaxBatch];             // output rows
     int batch;
 };
 
-// RT = 16-row MFMA tiles per workgroup (gate/up: the gate tile and the
-// matching up tile). The prologue loads every input row as float4 (thread t
-// holds elements 4 t .. 4 t + 3), sums the squares of all rows in one
-// pass (one barrier for the 8 norms) and stages FP16 hi / lo with 8-byte LDS
-// stores; the weights are issued right after the inputs, so their HBM round
-// trip overlaps the prologue.
-template <int K, int MODE, int RT = 1>
+// Y[b] = W X[b] on the matrix cores: one 16-row tile per workgroup, one
+// wave per 256 columns. Every input row is loaded as float4 (thread t holds
+// elements 4 t .. 4 t + 3) and staged in LDS as FP16 hi / lo; the weights
+// are issued right after the inputs, so their HBM round trip overlaps the
+// staging, and the waves' K parts are summed in a fixed order.
+template <int K>
 __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
-    constexpr bool kNorm = MODE == kBGateUp || MODE == kBLmHead;
-    constexpr int kTiles = MODE == kBGateUp ? 2 : RT;
-    static_assert(MODE == kBGateUp ? RT == 1 : RT >= 1, "gate/up pairs one gate tile with one up tile");
-    constexpr int KS = K;
-    constexpr int WAVES = KS / 256, THREADS = 64 * WAVES, KW = 256, kBlocks = KW / 128, F4 = 1;
-    static_assert(KS % 1024 == 0 && (!kNorm || WAVES == kWaves), "one wave per 256 columns; norms with 4 waves");
-    constexpr int k0 = 0;
-    __shared__ __align__(16) _Float16 xh[kMaxBatch][KS + 8];
-    __shared__ __align__(16) _Float16 xl[kMaxBatch][KS + 8];
-    __shared__ double red[kWaves][kMaxBatch];
-    __shared__ float part[WAVES][kTiles][64][4];
+    constexpr int WAVES = K / 256, KW = 256, kBlocks = KW / 128;
+    static_assert(WAVES == 4 || WAVES == 8 || WAVES == 12, "4, 8 or 12 waves");
+    __shared__ __align__(16) _Float16 xh[kMaxBatch][K + 8];
+    __shared__ __align__(16) _Float16 xl[kMaxBatch][K + 8];
+    __shared__ float part[WAVES][64][4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, quad = lane >> 4;
-    const int B = a.batch, o0 = blockIdx.x * (kBatchRows * RT);
-    // Epilogue elements of this thread: row o0 + 16 t + 4 (l / 16) + r,
-    // sequence l % 16 of each 16x16 accumulator (r = wave, l = lane).
-    const int eb = lane & 15, erow = 4 * (lane >> 4) + (wave & 3);  // waves 0..3 run the epilogue
+    const int B = a.batch, o0 = blockIdx.x * kBatchRows;
 
     // Loads complete in issue order per wave: inputs first (rows past the
-    // batch repeat row B - 1 and are never stored), then norm weights and
-    // residual entries, then the weights.
-    float4 v[kMaxBatch][F4];
+    // batch repeat row B - 1 and are never stored), then the weights.
+    float4 v[kMaxBatch];
 #pragma unroll
-    for (int b = 0; b < kMaxBatch; ++b) {
-        const int bb = min(b, B - 1);
-#pragma unroll
-        for (int i = 0; i < F4; ++i) {
-            const int j4 = tid + THREADS * i;
-            v[b][i] = reinterpret_cast<const float4*>(a.in[bb] + k0)[j4];
-        }
-    }
-    float4 wn[F4];
-    if constexpr (kNorm) {
-#pragma unroll
-        for (int i = 0; i < F4; ++i) wn[i] = reinterpret_cast<const float4*>(a.norm_w)[tid + THREADS * i];
-    }
-    u32x4 wa[kTiles][kBlocks][4];
+    for (int b = 0; b < kMaxBatch; ++b) v[b] = reinterpret_cast<const float4*>(a.in[min(b, B - 1)])[tid];
+    u32x4 wa[kBlocks][4];
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-        const int row = MODE == kBGateUp ? o0 + col + (t ? kFFN : 0) : o0 + kBatchRows * t + col;
-        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(row) * K + k0 + wave * KW) + quad;
+    {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(o0 + col) * K + wave * KW) + quad;
 #pragma unroll
         for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) wa[t][blk][s] = __builtin_nontemporal_load(wp + 16 * blk + 4 * s);
+            for (int s = 0; s < 4; ++s) wa[blk][s] = __builtin_nontemporal_load(wp + 16 * blk + 4 * s);
     }
     __builtin_amdgcn_sched_barrier(0);
-
-    if constexpr (kNorm) {
-        // RMSNorm per row (engine/core.cpp:207-215): FP32 squares summed in
-        // FP64. A reduce-scatter inside each wave halves the rows a lane
-        // carries at each of the exchanges over lane bits 5, 4 and 3, then
-        // sums over bits 2..0, so lane l ends with the wave's total of row
-        // (l >> 3) & 7; the 4 wave totals of a row are added by one thread,
-        // which also forms the row's scale once.
-        double sq[kMaxBatch];
 #pragma unroll
-        for (int b = 0; b < kMaxBatch; ++b) {
-            double s = 0.0;
+    for (int b = 0; b < kMaxBatch; ++b) {
+        const float e[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+        half4 hi, lo;
 #pragma unroll
-            for (int i = 0; i < F4; ++i) {
-                const float e[4] = {v[b][i].x, v[b][i].y, v[b][i].z, v[b][i].w};
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const float square = e[k] * e[k];
-                    s += static_cast<double>(square);
-                }
-            }
-            sq[b] = s;
+        for (int k = 0; k < 4; ++k) {
+            _Float16 h, l;
+            split_half(e[k], h, l);
+            hi[k] = h;
+            lo[k] = l;
         }
-        const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
-        double r4[4], r2[2];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // keep rows 4 b5 + i, send the others
-            const double keep = b5 ? sq[4 + i] : sq[i], send = b5 ? sq[i] : sq[4 + i];
-            r4[i] = keep + xor_lanes<32>(send);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {  // rows 4 b5 + 2 b4 + i
-            const double keep = b4 ? r4[2 + i] : r4[i], send = b4 ? r4[i] : r4[2 + i];
-            r2[i] = keep + xor_lanes<16>(send);
-        }
-        double r1 = (b3 ? r2[1] : r2[0]) + xor_lanes<8>(b3 ? r2[0] : r2[1]);  // row (lane >> 3) & 7
-        r1 += xor_lanes<4>(r1);
-        r1 += xor_lanes<2>(r1);
-        r1 += xor_lanes<1>(r1);
-        if ((lane & 7) == 0) red[wave][lane >> 3] = r1;
-        __syncthreads();
-        __shared__ float inv_row[kMaxBatch];
-        if (tid < kMaxBatch) {
-            const double total = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
-            inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(K) + 1e-6f);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int b = 0; b < kMaxBatch; ++b) {
-            const float inv = inv_row[b];
-#pragma unroll
-            for (int i = 0; i < F4; ++i) {
-                v[b][i].x = (v[b][i].x * inv) * wn[i].x;
-                v[b][i].y = (v[b][i].y * inv) * wn[i].y;
-                v[b][i].z = (v[b][i].z * inv) * wn[i].z;
-                v[b][i].w = (v[b][i].w * inv) * wn[i].w;
-            }
-        }
-        if constexpr (MODE == kBLmHead) {
-            if (blockIdx.x == 0) {
-#pragma unroll
-                for (int b = 0; b < kMaxBatch; ++b)
-                    if (b < B) {
-#pragma unroll
-                        for (int i = 0; i < F4; ++i) reinterpret_cast<float4*>(a.hidden[b])[tid + THREADS * i] = v[b][i];
-                    }
-            }
-        }
+        *reinterpret_cast<half4*>(&xh[b][4 * tid]) = hi;
+        *reinterpret_cast<half4*>(&xl[b][4 * tid]) = lo;
     }
-#pragma unroll
-    for (int b = 0; b < kMaxBatch; ++b)
-#pragma unroll
-        for (int i = 0; i < F4; ++i) {
-            const float e[4] = {v[b][i].x, v[b][i].y, v[b][i].z, v[b][i].w};
-            half4 hi, lo;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                _Float16 h, l;
-                split_half(e[k], h, l);
-                hi[k] = h;
-                lo[k] = l;
-            }
-            const int j = 4 * (tid + THREADS * i);
-            *reinterpret_cast<half4*>(&xh[b][j]) = hi;
-            *reinterpret_cast<half4*>(&xl[b][j]) = lo;
-        }
     __syncthreads();
 
-    floatx4 acc[kTiles];
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int blk = 0; blk < kBlocks; ++blk)
 #pragma unroll
@@ -216,84 +114,26 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
             const int k = wave * KW + 128 * blk + 32 * s + 8 * quad;
             const half8 bh = masked_b<half8>(&xh[col & 7][k], col < kMaxBatch);
             const half8 bl = masked_b<half8>(&xl[col & 7][k], col < kMaxBatch);
-#pragma unroll
-            for (int t = 0; t < kTiles; ++t) {
-                const half8 w8 = __builtin_bit_cast(half8, wa[t][blk][s]);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc[t], 0, 0, 0);
-            }
+            const half8 w8 = __builtin_bit_cast(half8, wa[blk][s]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w8, bl, acc, 0, 0, 0);
         }
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) part[wave][t][lane][r] = acc[t][r];
+    for (int r = 0; r < 4; ++r) part[wave][lane][r] = acc[r];
     __syncthreads();
 
-    // The waves' K parts of each output, summed in a fixed order (pairs,
-    // then pairs of pairs; a third group of four comes last).
+    // Element (row o0 + 4 (lane / 16) + wave, sequence lane % 16) for
+    // waves 0..3: the waves' K parts in fixed order (pairs, then pairs of
+    // pairs; further groups of four after).
     if (wave >= 4) return;
-    float y[kTiles];
-#pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-        auto quad_sum = [&](int w0) {
-            return (part[w0][t][lane][wave] + part[w0 + 1][t][lane][wave]) +
-                   (part[w0 + 2][t][lane][wave] + part[w0 + 3][t][lane][wave]);
-        };
-        y[t] = quad_sum(0);
-        if constexpr (WAVES >= 8) y[t] = y[t] + quad_sum(4);
-        if constexpr (WAVES >= 12) y[t] = y[t] + quad_sum(8);
-        static_assert(WAVES == 4 || WAVES == 8 || WAVES == 12, "4, 8 or 12 waves");
-    }
-    const bool live = eb < B;
-    const int eo = o0 + erow;
-    if constexpr (MODE == kBPlain) {
-        if (live) a.out[eb][eo] = y[0];
-    } else if constexpr (MODE == kBGateUp) {
-        if (live) {  // SwiGLU (engine/core.cpp:636-639)
-            const float gate = y[0], up = y[1];
-            const float half_gate = gate * 0.5f;
-            const float th = tanhf(half_gate);
-            a.out[eb][eo] = gate * (0.5f + 0.5f * th) * up;
-        }
-    } else if constexpr (MODE == kBLmHead) {
-        // Per-sequence argmax over this workgroup's rows: lowest id among
-        // maxima, nonfinite values flagged (engine/main.cpp:51-59).
-        float bv = -INFINITY;
-        int bi = INT_MAX, bad = 0;
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) {
-            const int row = eo + kBatchRows * t;
-            if (live) {
-                a.out[eb][row] = y[t];
-                bad |= !__builtin_isfinite(y[t]);
-                if (better(y[t], row, bv, bi)) { bv = y[t]; bi = row; }
-            }
-        }
-#pragma unroll
-        for (int off = 16; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            bad |= __shfl_xor(bad, off);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-        }
-        __shared__ float mv[kWaves][16];
-        __shared__ int mi[kWaves][16], mb[kWaves][16];
-        if (lane < 16) { mv[wave][lane] = bv; mi[wave][lane] = bi; mb[wave][lane] = bad; }
-        __syncthreads();
-        if (tid < B) {
-            float v0 = mv[0][tid];
-            int i0 = mi[0][tid], b0 = mb[0][tid];
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) {
-                b0 |= mb[w][tid];
-                if (better(mv[w][tid], mi[w][tid], v0, i0)) { v0 = mv[w][tid]; i0 = mi[w][tid]; }
-            }
-            const size_t slot = size_t(blockIdx.x) * kMaxBatch + tid;
-            a.lm_value[slot] = v0;
-            a.lm_index[slot] = i0;
-            a.lm_bad[slot] = b0;
-        }
-    }
+    auto quad_sum = [&](int w0) {
+        return (part[w0][lane][wave] + part[w0 + 1][lane][wave]) + (part[w0 + 2][lane][wave] + part[w0 + 3][lane][wave]);
+    };
+    float y = quad_sum(0);
+    if constexpr (WAVES >= 8) y = y + quad_sum(4);
+    if constexpr (WAVES >= 12) y = y + quad_sum(8);
+    const int eb = lane & 15;
+    if (eb < B) a.out[eb][o0 + 4 * (lane >> 4) + wave] = y;
 }
 
 // Norm + gate/up + SwiGLU + down + residual of one layer for the batched
@@ -756,11 +596,11 @@ __global__ __launch_bounds__(1024) void batch_argmax_kernel(const float* __restr
     }
 }
 
-template <int K, int MODE, int RT = 1>
+template <int K>
 void bgemv(const BatchGemvArgs& a, int rows, hipStream_t stream) {
     require(a.batch >= 1 && a.batch <= kMaxBatch, "batched GEMV: 1..8 rows");
-    require(rows % (kBatchRows * RT) == 0 && rows > 0, "batched GEMV: rows must be a positive multiple of the tile rows");
-    bgemv_kernel<K, MODE, RT><<<rows / (kBatchRows * RT), K / 4, 0, stream>>>(a);
+    require(rows % kBatchRows == 0 && rows > 0, "batched GEMV: rows must be a positive multiple of 16");
+    bgemv_kernel<K><<<rows / kBatchRows, K / 4, 0, stream>>>(a);
 }
 
 }  // namespace
@@ -775,9 +615,9 @@ void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, 
         a.out[b] = y + size_t(b) * rows;
     }
     switch (cols) {
-        case 1024: bgemv<1024, kBPlain>(a, rows, stream); break;
-        case 2048: bgemv<2048, kBPlain>(a, rows, stream); break;
-        case 3072: bgemv<3072, kBPlain>(a, rows, stream); break;
+        case 1024: bgemv<1024>(a, rows, stream); break;
+        case 2048: bgemv<2048>(a, rows, stream); break;
+        case 3072: bgemv<3072>(a, rows, stream); break;
         default: throw std::runtime_error("batched GEMV: cols must be 1024, 2048 or 3072");
     }
 }

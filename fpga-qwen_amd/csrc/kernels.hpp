@@ -92,12 +92,12 @@ struct LayerDevice {
 struct DecodeScratch {
     float* x;             // [1024] residual stream
     float* qkv;           // [4096] raw projections
-    float* attended;      // [2048] normalized attention output (batched decode)
+    float* attended;      // [2048] normalized attention output (split attention with one split)
     float* act;           // [3072]
     float* logits;        // [151936]
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
-    float* o_part;        // [16][1024]: per-query-head partial O projections (batched decode: down K slices)
+    float* o_part;        // [16][1024]: per-query-head partial O projections
     float* lm_value;      // [kLmPartials] argmax partials: [kBatchLmGroups][kMaxBatch] (batched), [2][kLmGroups] (pair)
     int* lm_index;
     int* lm_bad;
