@@ -1801,9 +1801,14 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     __shared__ double red[4][2];
     __shared__ float wm[8][2], wl[8][2];
 
+    // Selects, not branches: a branch here would make the compiler wait for
+    // every load in flight (the QKV weights too) before the norm.
 #pragma unroll
-    for (int bb = 0; bb < kMaxBatch; ++bb)
-        if (args.seq[min(bb, B - 1)].embed) xv[bb] = make_float2(h2f(ev[bb] & 0xffffu), h2f(ev[bb] >> 16));
+    for (int bb = 0; bb < kMaxBatch; ++bb) {
+        const bool embedded = args.seq[min(bb, B - 1)].embed != nullptr;
+        const float e0 = h2f(ev[bb] & 0xffffu), e1 = h2f(ev[bb] >> 16);
+        xv[bb] = make_float2(embedded ? e0 : xv[bb].x, embedded ? e1 : xv[bb].y);
+    }
 
     // RMSNorm of every sequence's row: per-thread FP64 sums of the FP32
     // squares, a reduce-scatter inside each wave (exchanges over lane bits
