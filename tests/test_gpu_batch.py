@@ -214,8 +214,9 @@ def test_prefix_reuse_workload_matches_oracle(qpkg, pack0, oracle_lib):
     canonical 512-token prefix is prefilled once; 8 sequences take a device
     copy of its K/V (the 512-token rewind), prefill their own 1536-token
     suffix (positions 512..2047) and decode 8 greedy steps together through
-    step_batch (contexts 2049..2056: 17 position splits per KV head, a grid
-    of 8 sequences). Teacher-forced against the oracle (rewind to 512, prefill
+    step_batch (contexts 2049..2056: each sequence's 33 blocks of 64
+    positions split into 4 pieces per KV head, its first 512 rows read from
+    one shared copy). Teacher-forced against the oracle (rewind to 512, prefill
     the suffix, step the same tokens), every sequence's logits after its
     prefill and after each batched step pass the reference gate; then each
     sequence re-steps the same tokens alone from position 2048 (batch-1
