@@ -384,7 +384,7 @@ constexpr int kLmTilesPerGroup = (kLmTiles + kBatchLmGroups - 1) / kBatchLmGroup
 static_assert(kVocab % kBatchRows == 0, "whole 16-row tiles");
 
 struct BatchLmArgs {
-    const uint16_t* w;         // embedding matrix [kVocab x 1024] (tied head)
+    const uint16_t* w;         // embedding matrix (tied head) in matrix-core order (launch_mfma_order)
     const float* norm_w;       // final RMSNorm weights
     const float* x[kMaxBatch];
     float* hidden[kMaxBatch];  // final normalized rows
@@ -461,9 +461,11 @@ __global__ __launch_bounds__(512) void lm_head_batch_kernel(const BatchLmArgs a)
     const int ntiles = (kLmTiles - w + kBatchLmGroups - 1) / kBatchLmGroups;
     auto load_tile = [&](u32x4 (&wt)[4], int k) {
         const int t = min(w + kBatchLmGroups * k, kLmTiles - 1);
-        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w + size_t(kBatchRows * t + col) * kHidden + 128 * wave) + quad;
+        // Piece (t, wave, st) of the matrix-core copy: 64 lanes x 16 bytes
+        // in a row, so that every load reads 1 KiB contiguous.
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w) + (size_t(t) * 8 + wave) * 256 + lane;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 4 * st);
+        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 64 * st);
     };
     // Epilogue element of threads 0..255: row 4 (lane / 16) + wave of the
     // tile, sequence lane % 16; its running best over the tiles.
@@ -603,7 +605,29 @@ void bgemv(const BatchGemvArgs& a, int rows, hipStream_t stream) {
     bgemv_kernel<K><<<rows / kBatchRows, K / 4, 0, stream>>>(a);
 }
 
+// dst in matrix-core order of W (natural [rows x K], rows % 16 == 0,
+// K % 128 == 0): 16-byte piece u = ((t (K / 128) + w) 4 + st) 64 + l holds
+// W[16 t + l % 16][128 w + 32 st + 8 (l / 16) .. + 7], the A operand of lane
+// l in step st of the wave that takes columns 128 w .. + 127 of tile t.
+__global__ void mfma_order_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int rows, int K) {
+    const size_t u = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int blocks = K / 128;
+    if (u >= size_t(rows) / 16 * blocks * 256) return;
+    const int l = int(u & 63), st = int((u >> 6) & 3);
+    const size_t tw = u >> 8;
+    const int w = int(tw % blocks);
+    const size_t t = tw / blocks;
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src + (16 * t + (l & 15)) * size_t(K) + 128 * w + 32 * st + 8 * (l >> 4));
+    reinterpret_cast<u32x4*>(dst)[u] = *s4;
+}
+
 }  // namespace
+
+void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, hipStream_t stream) {
+    require(rows > 0 && rows % 16 == 0 && K > 0 && K % 128 == 0, "mfma order: rows % 16 == 0 and K % 128 == 0");
+    const size_t pieces = size_t(rows) / 16 * (K / 128) * 256;
+    mfma_order_kernel<<<unsigned((pieces + 255) / 256), 256, 0, stream>>>(src, dst, rows, K);
+}
 
 void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols,
                         hipStream_t stream) {
@@ -622,8 +646,9 @@ void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, 
     }
 }
 
-void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const float* final_norm,
-                         const float* cosines, const float* sines, const uint32_t* tags, hipStream_t stream) {
+void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const uint16_t* embed_mfma,
+                         const float* final_norm, const float* cosines, const float* sines, const uint32_t* tags,
+                         hipStream_t stream) {
     require(count >= 1 && count <= kMaxBatch, "batched decode: 1..8 sequences");
     for (int l = 0; l < kBatchTagsPerLayer * kLayers; ++l) require(tags[l] != 0, "batched decode: exchange tags are nonzero");
     uint64_t* const words = seqs[0].s.bexchange;
@@ -671,7 +696,7 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
         ffn_batch_kernel<<<256, 512, 0, stream>>>(f);
     }
     BatchLmArgs lm{};
-    lm.w = embed;  // tied head (engine/core.cpp:643-645)
+    lm.w = embed_mfma;  // tied head (engine/core.cpp:643-645)
     lm.norm_w = final_norm;
     lm.batch = count;
     const DecodeScratch& s0 = seqs[0].s;

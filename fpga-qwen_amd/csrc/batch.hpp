@@ -30,8 +30,15 @@ inline constexpr int kBatchTagsPerLayer = 2;
 // Logits, hidden and selections land in each sequence's buffers.
 // tags[2 l], tags[2 l + 1] (nonzero, unique per launch) tag layer l's
 // exchanges between workgroups, which use the first sequence's buffers.
-void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const float* final_norm,
-                         const float* cosines, const float* sines, const uint32_t* tags, hipStream_t stream);
+// embed_mfma: the embedding in matrix-core order (launch_mfma_order).
+void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed, const uint16_t* embed_mfma,
+                         const float* final_norm, const float* cosines, const float* sines, const uint32_t* tags,
+                         hipStream_t stream);
+
+// dst = W (natural [rows x K] FP16, rows % 16 == 0, K % 128 == 0) in the
+// order the batched kernels' matrix-core loads read it: each 16-row tile, per
+// 128-column block and 32-column step, as 64 lanes x 16 bytes.
+void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, hipStream_t stream);
 
 // Y[b] = W X[b] for b < batch on the matrix cores (W natural row-major
 // [rows x cols] FP16, X [batch x cols] FP32, Y [batch x rows] FP32); rows a

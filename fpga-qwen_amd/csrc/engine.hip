@@ -35,8 +35,9 @@ Weights::~Weights() {
 }
 
 // Uploads a validated pack: natural copies of every matrix (gather, prefill
-// GEMMs, batched decode), chain-tiled copies (batch-1 GEMVs), norms and the
-// RoPE tables for the full 4096-position range.
+// GEMMs, batched decode), chain-tiled copies (batch-1 GEMVs), the embedding
+// in matrix-core order (batched head), norms and the RoPE tables for the
+// full 4096-position range.
 static std::shared_ptr<Weights> load_weights(const Pack& pack, hipStream_t stream) {
     auto w = std::make_shared<Weights>();
     auto alloc = [&](size_t bytes) {
@@ -61,6 +62,8 @@ static std::shared_ptr<Weights> load_weights(const Pack& pack, hipStream_t strea
     HIP_CHECK(hipMemcpy(w->embed, emb.half, size_t(kVocab) * kHidden * 2, hipMemcpyHostToDevice));
     w->lm_t = alloc_half(size_t(kVocab) * kHidden);
     launch_tile_matrix(w->embed, nullptr, w->lm_t, kVocab, kHidden, stream);
+    w->embed_mfma = alloc_half(size_t(kVocab) * kHidden);
+    launch_mfma_order(w->embed, w->embed_mfma, kVocab, kHidden, stream);
     w->final_norm = upload_norm(pack.tensor("model.norm.weight"));
 
     w->layers.resize(kLayers);
@@ -495,7 +498,8 @@ void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
                          shared_seq[i], shared[i]};
         HIP_CHECK(hipStreamSynchronize(e.stream_));
     }
-    launch_decode_batch(bs, count, lead.embed_, lead.final_norm_, lead.cosines_, lead.sines_, tags, lead.stream_);
+    launch_decode_batch(bs, count, lead.embed_, lead.weights_->embed_mfma, lead.final_norm_, lead.cosines_, lead.sines_,
+                        tags, lead.stream_);
     HIP_CHECK(hipGetLastError());
     lead.sync();
     for (int i = 0; i < count; ++i) ++seqs[i]->pos_;

@@ -31,6 +31,7 @@ struct Weights {
     std::vector<PrefillLayer> prefill;  // keys/values unset
     uint16_t* embed = nullptr;          // natural [vocab x 1024]
     uint16_t* lm_t = nullptr;           // chain-tiled embedding
+    uint16_t* embed_mfma = nullptr;     // embedding in matrix-core order (batched head)
     float* final_norm = nullptr;
     float* cosines = nullptr;           // [4096][64]
     float* sines = nullptr;
