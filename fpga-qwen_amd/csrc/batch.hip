@@ -155,8 +155,8 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
 // Every workgroup reads all of the input residual, so the output goes to a
 // second buffer (the layers alternate between the two).
 struct BatchFfnArgs {
-    const uint16_t* gateup;            // natural [6144 x 1024]: gate rows, then up rows
-    const uint16_t* down;              // natural [1024 x 3072]
+    const uint16_t* gateup;            // gate / up tiles in matrix-core order (launch_gateup_order)
+    const uint16_t* down;              // [1024 x 3072] in matrix-core order, 96-column blocks
     const float* norm_w;               // post-attention RMSNorm weights
     const float* x[kMaxBatch];         // residual in
     float* x_out[kMaxBatch];           // residual out
@@ -183,31 +183,31 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
 #pragma unroll
     for (int bb = 0; bb < kMaxBatch; ++bb) xv[bb] = reinterpret_cast<const float2*>(a.x[min(bb, B - 1)])[tid];
     const float2 wn = reinterpret_cast<const float2*>(a.norm_w)[tid];
-    // Gate/up tiles: rows 12 r + col (col < 12) of the octant's gate and up
-    // rows; wave w takes columns 128 w .. 128 w + 127.
-    const int c0 = kFfnOctant * xo + 12 * r;
+    // Gate/up tiles 32 xo + r (rows 384 xo + 12 r + col of the gate and up
+    // halves, col < 12; lanes col >= 12 repeat row 11 and are masked at
+    // use); wave w takes columns 128 w .. 128 w + 127. 1 KiB contiguous per
+    // load.
+    const int tile = 32 * xo + r;
     u32x4 wg[4], wu[4];
-    const u32x4 zero4 = {0u, 0u, 0u, 0u};
     __builtin_amdgcn_sched_barrier(0);
     {
-        const int rr = c0 + min(col, 11);
-        const u32x4* gp = reinterpret_cast<const u32x4*>(a.gateup + size_t(rr) * kHidden + 128 * wave) + quad;
-        const u32x4* up = reinterpret_cast<const u32x4*>(a.gateup + size_t(kFFN + rr) * kHidden + 128 * wave) + quad;
+        const u32x4* gp = reinterpret_cast<const u32x4*>(a.gateup) + (size_t(2 * tile) * 8 + wave) * 256 + lane;
+        const u32x4* up = reinterpret_cast<const u32x4*>(a.gateup) + (size_t(2 * tile + 1) * 8 + wave) * 256 + lane;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            wg[st] = col < 12 ? __builtin_nontemporal_load(gp + 4 * st) : zero4;
-            wu[st] = col < 12 ? __builtin_nontemporal_load(up + 4 * st) : zero4;
+            wg[st] = __builtin_nontemporal_load(gp + 64 * st);
+            wu[st] = __builtin_nontemporal_load(up + 64 * st);
         }
     }
     // Down tile tt = wave & 1 (rows 32 r + 16 tt + col), K range
-    // 384 xo + 96 (wave >> 1) .. + 95 in 3 steps.
+    // 384 xo + 96 (wave >> 1) .. + 95 in 3 steps (96-column block
+    // 4 xo + (wave >> 1)).
     const int tt = wave & 1, kq = wave >> 1;
     u32x4 wd[3];
     {
-        const u32x4* dp = reinterpret_cast<const u32x4*>(a.down + size_t(32 * r + 16 * tt + col) * kFFN +
-                                                         kFfnOctant * xo + 96 * kq) + quad;
+        const u32x4* dp = reinterpret_cast<const u32x4*>(a.down) + ((size_t(2 * r + tt) * 32 + 4 * xo + kq) * 3) * 64 + lane;
 #pragma unroll
-        for (int st = 0; st < 3; ++st) wd[st] = __builtin_nontemporal_load(dp + 4 * st);
+        for (int st = 0; st < 3; ++st) wd[st] = __builtin_nontemporal_load(dp + 64 * st);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -274,7 +274,9 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
             const int k = 128 * wave + 32 * st + 8 * quad;
             const half8 bh = masked_b<half8>(&xh[col & 7][k], col < kMaxBatch);
             const half8 bl = masked_b<half8>(&xl[col & 7][k], col < kMaxBatch);
-            const half8 g8 = __builtin_bit_cast(half8, wg[st]), u8 = __builtin_bit_cast(half8, wu[st]);
+            const u32x4 zero4 = {0u, 0u, 0u, 0u};
+            const half8 g8 = __builtin_bit_cast(half8, col < 12 ? wg[st] : zero4);
+            const half8 u8 = __builtin_bit_cast(half8, col < 12 ? wu[st] : zero4);
             accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(g8, bh, accg, 0, 0, 0);
             accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(g8, bl, accg, 0, 0, 0);
             accu = __builtin_amdgcn_mfma_f32_16x16x32_f16(u8, bh, accu, 0, 0, 0);
@@ -606,27 +608,49 @@ void bgemv(const BatchGemvArgs& a, int rows, hipStream_t stream) {
 }
 
 // dst in matrix-core order of W (natural [rows x K], rows % 16 == 0,
-// K % 128 == 0): 16-byte piece u = ((t (K / 128) + w) 4 + st) 64 + l holds
-// W[16 t + l % 16][128 w + 32 st + 8 (l / 16) .. + 7], the A operand of lane
-// l in step st of the wave that takes columns 128 w .. + 127 of tile t.
-__global__ void mfma_order_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int rows, int K) {
+// K % BW == 0, BW % 32 == 0): 16-byte piece
+// u = ((t (K / BW) + b) (BW / 32) + st) 64 + l holds
+// W[16 t + l % 16][BW b + 32 st + 8 (l / 16) .. + 7], the A operand of lane
+// l in step st of the wave that takes columns BW b .. + BW - 1 of tile t.
+__global__ void mfma_order_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int rows, int K,
+                                  int BW) {
     const size_t u = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int blocks = K / 128;
-    if (u >= size_t(rows) / 16 * blocks * 256) return;
-    const int l = int(u & 63), st = int((u >> 6) & 3);
-    const size_t tw = u >> 8;
-    const int w = int(tw % blocks);
-    const size_t t = tw / blocks;
-    const u32x4* s4 = reinterpret_cast<const u32x4*>(src + (16 * t + (l & 15)) * size_t(K) + 128 * w + 32 * st + 8 * (l >> 4));
+    const int blocks = K / BW, steps = BW / 32;
+    if (u >= size_t(rows) / 16 * blocks * steps * 64) return;
+    const int l = int(u & 63);
+    const size_t q = u >> 6;
+    const int st = int(q % steps), b = int((q / steps) % blocks);
+    const size_t t = q / steps / blocks;
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src + (16 * t + (l & 15)) * size_t(K) + BW * b + 32 * st + 8 * (l >> 4));
+    reinterpret_cast<u32x4*>(dst)[u] = *s4;
+}
+
+// Gate / up rows of the batched FFN in matrix-core order: tile T holds gate
+// (h = 0) or up (h = 1) rows 12 T .. 12 T + 11 (lanes with l % 16 >= 12
+// repeat row 12 T + 11); piece u = (((2 T + h) 8 + w) 4 + st) 64 + l holds
+// W[h 3072 + 12 T + min(l % 16, 11)][128 w + 32 st + 8 (l / 16) .. + 7].
+__global__ void gateup_order_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst) {
+    const size_t u = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (u >= size_t(256) * 2 * 8 * 4 * 64) return;
+    const int l = int(u & 63), st = int((u >> 6) & 3), w = int((u >> 8) & 7), h = int((u >> 11) & 1);
+    const int T = int(u >> 12);
+    const int row = h * kFFN + 12 * T + min(l & 15, 11);
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src + size_t(row) * kHidden + 128 * w + 32 * st + 8 * (l >> 4));
     reinterpret_cast<u32x4*>(dst)[u] = *s4;
 }
 
 }  // namespace
 
-void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, hipStream_t stream) {
-    require(rows > 0 && rows % 16 == 0 && K > 0 && K % 128 == 0, "mfma order: rows % 16 == 0 and K % 128 == 0");
-    const size_t pieces = size_t(rows) / 16 * (K / 128) * 256;
-    mfma_order_kernel<<<unsigned((pieces + 255) / 256), 256, 0, stream>>>(src, dst, rows, K);
+void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, int BW, hipStream_t stream) {
+    require(rows > 0 && rows % 16 == 0 && BW > 0 && BW % 32 == 0 && K > 0 && K % BW == 0,
+            "mfma order: rows % 16 == 0, K % BW == 0, BW % 32 == 0");
+    const size_t pieces = size_t(rows) / 16 * (K / BW) * (BW / 32) * 64;
+    mfma_order_kernel<<<unsigned((pieces + 255) / 256), 256, 0, stream>>>(src, dst, rows, K, BW);
+}
+
+void launch_gateup_order(const uint16_t* gateup, uint16_t* dst, hipStream_t stream) {
+    const size_t pieces = size_t(256) * 2 * 8 * 4 * 64;
+    gateup_order_kernel<<<unsigned(pieces / 256), 256, 0, stream>>>(gateup, dst);
 }
 
 void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols,
@@ -677,12 +701,12 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
                             seqs[seqs[b].shared_seq].context,
                             seqs[b].shared};
         }
-        launch_attention_o_batch(as, count, W.qkv_n, W.o_n, W.in_norm, W.q_norm, W.k_norm, cosines, sines, words,
+        launch_attention_o_batch(as, count, W.qkv_m, W.o_m, W.in_norm, W.q_norm, W.k_norm, cosines, sines, words,
                                  seqs[0].s.stall, tags[kBatchTagsPerLayer * l], stream);
 
         BatchFfnArgs f{};
-        f.gateup = W.gateup_n;
-        f.down = W.down_n;
+        f.gateup = W.gateup_m;
+        f.down = W.down_m;
         f.norm_w = W.post_norm;
         f.act_words = words + kBatchActOffset;
         f.share_words = words + kBatchShareOffset;

@@ -35,10 +35,15 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
                          const float* final_norm, const float* cosines, const float* sines, const uint32_t* tags,
                          hipStream_t stream);
 
-// dst = W (natural [rows x K] FP16, rows % 16 == 0, K % 128 == 0) in the
+// dst = W (natural [rows x K] FP16, rows % 16 == 0, K % BW == 0) in the
 // order the batched kernels' matrix-core loads read it: each 16-row tile, per
-// 128-column block and 32-column step, as 64 lanes x 16 bytes.
-void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, hipStream_t stream);
+// BW-column block and 32-column step, as 64 lanes x 16 bytes (one load of
+// 1 KiB contiguous per wave).
+void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, int BW, hipStream_t stream);
+// The same for the batched FFN's gate / up tiles (12 rows each, natural
+// [6144 x 1024] gate rows then up rows in; 16 MiB out).
+void launch_gateup_order(const uint16_t* gateup, uint16_t* dst, hipStream_t stream);
+inline constexpr size_t kGateupOrderHalves = size_t(256) * 2 * 8 * 4 * 64 * 8;
 
 // Y[b] = W X[b] for b < batch on the matrix cores (W natural row-major
 // [rows x cols] FP16, X [batch x cols] FP32, Y [batch x rows] FP32); rows a

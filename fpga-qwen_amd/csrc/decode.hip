@@ -1684,8 +1684,8 @@ struct AttnBatchSeq {
 
 struct AttnBatchArgs {
     AttnBatchSeq seq[kMaxBatch];
-    const uint16_t* w_qkv;   // natural [4096 x 1024]: q rows, k rows, v rows
-    const uint16_t* w_o;     // natural [1024 x 2048]
+    const uint16_t* w_qkv;   // [4096 x 1024] (q rows, k rows, v rows) in matrix-core order, 128-column blocks
+    const uint16_t* w_o;     // [1024 x 2048] in matrix-core order, 64-column blocks
     const float* in_norm;    // input RMSNorm weights
     const float* q_norm;
     const float* k_norm;
@@ -1749,9 +1749,11 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         return tr < 16 ? 256 * g + 16 * tr : (tr < 24 ? 2048 + 128 * g + 16 * (tr - 16) : 3072 + 128 * g + 16 * (tr - 24));
     };
     auto load_tile = [&](u32x4 (&wt)[4], int tr) {
-        const u32x4* wp = reinterpret_cast<const u32x4*>(args.w_qkv + size_t(tile_row(tr) + col) * kHidden + 128 * wave) + quad;
+        // 16-row tile tile_row(tr) / 16, wave's 128-column block, step st:
+        // 1 KiB contiguous per load.
+        const u32x4* wp = reinterpret_cast<const u32x4*>(args.w_qkv) + (size_t(tile_row(tr) / 16) * 8 + wave) * 256 + lane;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 4 * st);
+        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 64 * st);
     };
     u32x4 wq[4];
     __builtin_amdgcn_sched_barrier(0);
@@ -1891,10 +1893,11 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     // K/V stream and used after it.
     u32x4 wo[2];
     {
-        const u32x4* op = reinterpret_cast<const u32x4*>(args.w_o + size_t(32 * r + 16 * (wave & 1) + col) * kQDim +
-                                                         256 * g + 64 * (wave >> 1)) + quad;
+        // Tile 2 r + (wave & 1), 64-column block 4 g + (wave >> 1), steps 0, 1.
+        const u32x4* op = reinterpret_cast<const u32x4*>(args.w_o) +
+                          ((size_t(2 * r + (wave & 1)) * 32 + 4 * g + (wave >> 1)) * 2) * 64 + lane;
         wo[0] = __builtin_nontemporal_load(op);
-        wo[1] = __builtin_nontemporal_load(op + 4);
+        wo[1] = __builtin_nontemporal_load(op + 64);
     }
     // Workgroups past the batch's pieces, or whose piece holds no position,
     // only project.

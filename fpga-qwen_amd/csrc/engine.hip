@@ -63,7 +63,7 @@ static std::shared_ptr<Weights> load_weights(const Pack& pack, hipStream_t strea
     w->lm_t = alloc_half(size_t(kVocab) * kHidden);
     launch_tile_matrix(w->embed, nullptr, w->lm_t, kVocab, kHidden, stream);
     w->embed_mfma = alloc_half(size_t(kVocab) * kHidden);
-    launch_mfma_order(w->embed, w->embed_mfma, kVocab, kHidden, stream);
+    launch_mfma_order(w->embed, w->embed_mfma, kVocab, kHidden, 128, stream);
     w->final_norm = upload_norm(pack.tensor("model.norm.weight"));
 
     w->layers.resize(kLayers);
@@ -87,6 +87,17 @@ static std::shared_ptr<Weights> load_weights(const Pack& pack, hipStream_t strea
         launch_tile_matrix(gu_n, gu_n + size_t(kFFN) * kHidden, gu_t, kFFN, kHidden, stream);
         uint16_t* down_t = alloc_half(size_t(kHidden) * kFFN);
         launch_tile_matrix(down_n, nullptr, down_t, kHidden, kFFN, stream);
+        // Matrix-core order for the batched step: QKV tiles and the lm_head
+        // take 128-column blocks per wave, O 64, down 96; gate / up tiles
+        // of 12 rows.
+        L.qkv_m = alloc_half(size_t(kQKVRows) * kHidden);
+        launch_mfma_order(qkv_n, L.qkv_m, kQKVRows, kHidden, 128, stream);
+        L.o_m = alloc_half(size_t(kHidden) * kQDim);
+        launch_mfma_order(o_n, L.o_m, kHidden, kQDim, 64, stream);
+        L.down_m = alloc_half(size_t(kHidden) * kFFN);
+        launch_mfma_order(down_n, L.down_m, kHidden, kFFN, 96, stream);
+        L.gateup_m = alloc_half(kGateupOrderHalves);
+        launch_gateup_order(gu_n, L.gateup_m, stream);
         L.qkv_t = qkv_t;
         L.o_n = o_n;
         L.qkv_n = qkv_n;

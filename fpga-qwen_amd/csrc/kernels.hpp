@@ -81,6 +81,10 @@ struct LayerDevice {
     const uint16_t* down_n;    // natural [1024 x 3072] (batched decode)
     const uint16_t* gateup_t;  // tiled [6144 x 1024]: tile T = gate rows 4T..4T+3, up rows 4T..4T+3
     const uint16_t* down_t;    // tiled [1024 x 3072]
+    uint16_t* qkv_m;           // matrix-core orders (launch_mfma_order) for the batched step
+    uint16_t* o_m;
+    uint16_t* gateup_m;
+    uint16_t* down_m;
     const float* in_norm;      // [1024]
     const float* post_norm;    // [1024]
     const float* q_norm;       // [128]
