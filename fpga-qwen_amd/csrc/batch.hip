@@ -184,19 +184,20 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
     for (int bb = 0; bb < kMaxBatch; ++bb) xv[bb] = reinterpret_cast<const float2*>(a.x[min(bb, B - 1)])[tid];
     const float2 wn = reinterpret_cast<const float2*>(a.norm_w)[tid];
     // Gate/up tiles 32 xo + r (rows 384 xo + 12 r + col of the gate and up
-    // halves, col < 12; lanes col >= 12 repeat row 11 and are masked at
-    // use); wave w takes columns 128 w .. 128 w + 127. 1 KiB contiguous per
-    // load.
+    // halves, col < 12; lanes col >= 12 read row 11 again and are masked
+    // at use); wave w takes columns 128 w .. 128 w + 127. 768 bytes
+    // contiguous per load.
     const int tile = 32 * xo + r;
     u32x4 wg[4], wu[4];
     __builtin_amdgcn_sched_barrier(0);
     {
-        const u32x4* gp = reinterpret_cast<const u32x4*>(a.gateup) + (size_t(2 * tile) * 8 + wave) * 256 + lane;
-        const u32x4* up = reinterpret_cast<const u32x4*>(a.gateup) + (size_t(2 * tile + 1) * 8 + wave) * 256 + lane;
+        const int l48 = 12 * quad + min(col, 11);
+        const u32x4* gp = reinterpret_cast<const u32x4*>(a.gateup) + (size_t(2 * tile) * 8 + wave) * 4 * 48 + l48;
+        const u32x4* up = reinterpret_cast<const u32x4*>(a.gateup) + (size_t(2 * tile + 1) * 8 + wave) * 4 * 48 + l48;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            wg[st] = __builtin_nontemporal_load(gp + 64 * st);
-            wu[st] = __builtin_nontemporal_load(up + 64 * st);
+            wg[st] = __builtin_nontemporal_load(gp + 48 * st);
+            wu[st] = __builtin_nontemporal_load(up + 48 * st);
         }
     }
     // Down tile tt = wave & 1 (rows 32 r + 16 tt + col), K range
@@ -626,16 +627,20 @@ __global__ void mfma_order_kernel(const uint16_t* __restrict__ src, uint16_t* __
 }
 
 // Gate / up rows of the batched FFN in matrix-core order: tile T holds gate
-// (h = 0) or up (h = 1) rows 12 T .. 12 T + 11 (lanes with l % 16 >= 12
-// repeat row 12 T + 11); piece u = (((2 T + h) 8 + w) 4 + st) 64 + l holds
-// W[h 3072 + 12 T + min(l % 16, 11)][128 w + 32 st + 8 (l / 16) .. + 7].
+// (h = 0) or up (h = 1) rows 12 T .. 12 T + 11; piece
+// u = (((2 T + h) 8 + w) 4 + st) 48 + 12 q + c (c < 12) holds
+// W[h 3072 + 12 T + c][128 w + 32 st + 8 q .. + 7], the A operand of lane
+// 16 q + c in step st of wave w (lanes with l % 16 >= 12 read piece c = 11
+// again and are masked).
 __global__ void gateup_order_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst) {
     const size_t u = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (u >= size_t(256) * 2 * 8 * 4 * 64) return;
-    const int l = int(u & 63), st = int((u >> 6) & 3), w = int((u >> 8) & 7), h = int((u >> 11) & 1);
-    const int T = int(u >> 12);
-    const int row = h * kFFN + 12 * T + min(l & 15, 11);
-    const u32x4* s4 = reinterpret_cast<const u32x4*>(src + size_t(row) * kHidden + 128 * w + 32 * st + 8 * (l >> 4));
+    if (u >= kGateupOrderHalves / 8) return;
+    const int l48 = int(u % 48), q = l48 / 12, c = l48 % 12;
+    const size_t rest = u / 48;
+    const int st = int(rest & 3), w = int((rest >> 2) & 7), h = int((rest >> 5) & 1);
+    const int T = int(rest >> 6);
+    const int row = h * kFFN + 12 * T + c;
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src + size_t(row) * kHidden + 128 * w + 32 * st + 8 * q);
     reinterpret_cast<u32x4*>(dst)[u] = *s4;
 }
 
@@ -649,8 +654,8 @@ void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, int 
 }
 
 void launch_gateup_order(const uint16_t* gateup, uint16_t* dst, hipStream_t stream) {
-    const size_t pieces = size_t(256) * 2 * 8 * 4 * 64;
-    gateup_order_kernel<<<unsigned(pieces / 256), 256, 0, stream>>>(gateup, dst);
+    const size_t pieces = kGateupOrderHalves / 8;
+    gateup_order_kernel<<<unsigned((pieces + 255) / 256), 256, 0, stream>>>(gateup, dst);
 }
 
 void launch_bgemv_plain(const uint16_t* w, const float* x, float* y, int batch, int rows, int cols,

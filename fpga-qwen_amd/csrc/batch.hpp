@@ -40,10 +40,10 @@ void launch_decode_batch(const BatchSeq* seqs, int count, const uint16_t* embed,
 // BW-column block and 32-column step, as 64 lanes x 16 bytes (one load of
 // 1 KiB contiguous per wave).
 void launch_mfma_order(const uint16_t* src, uint16_t* dst, int rows, int K, int BW, hipStream_t stream);
-// The same for the batched FFN's gate / up tiles (12 rows each, natural
-// [6144 x 1024] gate rows then up rows in; 16 MiB out).
+// The same for the batched FFN's gate / up tiles (12 rows each, 48 pieces
+// per wave and step; natural [6144 x 1024] gate rows then up rows in).
 void launch_gateup_order(const uint16_t* gateup, uint16_t* dst, hipStream_t stream);
-inline constexpr size_t kGateupOrderHalves = size_t(256) * 2 * 8 * 4 * 64 * 8;
+inline constexpr size_t kGateupOrderHalves = size_t(256) * 2 * 8 * 4 * 48 * 8;
 
 // Y[b] = W X[b] for b < batch on the matrix cores (W natural row-major
 // [rows x cols] FP16, X [batch x cols] FP32, Y [batch x rows] FP32); rows a
