@@ -197,7 +197,8 @@ def prefix_reuse_batch(model, prompts, steps=128):
     8 sequences on the same weights reuse its K/V (device copy of the rewound
     prefix), prefill their own 1536-token suffix (positions 512..2047) and
     decode 128 greedy tokens each as one batch of 8 (skinny GEMMs on the
-    matrix cores). Also times one sequence stepping alone at that context."""
+    matrix cores; each step returns the 8 selections). Also times one
+    sequence stepping alone at that context."""
     prefix, suffixes = prompts['prefix_512'], prompts['suffix_1536']
     base = model.share()
     seqs = [model.share() for _ in suffixes]
@@ -213,12 +214,10 @@ def prefix_reuse_batch(model, prompts, steps=128):
             m.prefill(suffix)
             suffix_s.append(time.perf_counter() - t0)
         tokens = [m.greedy() for m in seqs]
-        q.step_batch(seqs, tokens)  # warmup step
-        tokens = [m.greedy() for m in seqs]
+        tokens = q.step_batch_greedy(seqs, tokens)  # warmup step
         start = time.perf_counter()
         for _ in range(steps - 1):
-            q.step_batch(seqs, tokens)
-            tokens = [m.greedy() for m in seqs]
+            tokens = q.step_batch_greedy(seqs, tokens)
         elapsed = time.perf_counter() - start
         aggregate = len(seqs) * (steps - 1) / elapsed
         # The same context stepped one sequence at a time (batch-1 path).

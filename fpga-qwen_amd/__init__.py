@@ -72,6 +72,7 @@ SIGNATURES = {
                                                ctypes.POINTER(ctypes.c_void_p)]),
     'qwen_gpu_copy_prefix': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
     'qwen_gpu_step_batch': (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _c_int_p, ctypes.c_int]),
+    'qwen_gpu_step_batch_greedy': (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p), _c_int_p, ctypes.c_int, _c_int_p]),
     'qwen_gpu_op_attention_prefill': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                                      ctypes.c_int, ctypes.c_void_p]),
@@ -263,6 +264,26 @@ def step_batch(models, tokens):
     if toks.size != len(models):
         raise ValueError('one token per model')
     _check(_LIB.qwen_gpu_step_batch(handles, toks.ctypes.data_as(_c_int_p), len(models)))
+
+
+_BATCH_ARRAYS = {}  # handles of a model list -> its ctypes argument arrays, reused across steps
+
+
+def step_batch_greedy(models, tokens):
+    """step_batch, then each model's greedy selection, in one call; returns
+    the selections (the next tokens of a greedy decode loop)."""
+    n = len(models)
+    if len(tokens) != n:
+        raise ValueError('one token per model')
+    key = tuple(m._handle.value if m._handle else 0 for m in models)  # a closed model passes null
+    arrays = _BATCH_ARRAYS.get(key)
+    if arrays is None:
+        if len(_BATCH_ARRAYS) > 64:
+            _BATCH_ARRAYS.clear()
+        arrays = _BATCH_ARRAYS[key] = ((ctypes.c_void_p * n)(*key), ctypes.c_int * n, (ctypes.c_int * n)())
+    handles, token_type, out = arrays
+    _check(_LIB.qwen_gpu_step_batch_greedy(handles, token_type(*tokens), n, out))
+    return out[:]
 
 
 def write_random_pack(path, seed=0, stddev=0.02, threads=None):

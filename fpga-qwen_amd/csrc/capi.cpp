@@ -94,6 +94,22 @@ int qwen_gpu_step_batch(qwen_gpu_model* const* models, const int* tokens, int co
     });
 }
 
+int qwen_gpu_step_batch_greedy(qwen_gpu_model* const* models, const int* tokens, int count, int* next) {
+    return guarded([&] {
+        need(models, "models");
+        need(tokens, "tokens");
+        need(next, "next");
+        if (count < 1 || count > 8) throw std::runtime_error("Batch must hold 1..8 sequences");
+        qwen_hip::Engine* engines[8];
+        for (int i = 0; i < count; ++i) {
+            need(models[i], "model");
+            engines[i] = &models[i]->engine;
+        }
+        qwen_hip::Engine::step_batch(engines, tokens, count);
+        for (int i = 0; i < count; ++i) next[i] = engines[i]->greedy();
+    });
+}
+
 int qwen_gpu_reset(qwen_gpu_model* m) {
     return guarded([&] {
         need(m, "model");

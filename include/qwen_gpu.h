@@ -59,12 +59,18 @@ int qwen_gpu_copy_prefix(qwen_gpu_model* dst, const qwen_gpu_model* src, int pos
 /* One decode step for each of `count` (1..8) distinct models that share
  * weights: models[i] consumes tokens[i] (Model::step, engine/core.hpp:38),
  * with every projection reading each weight matrix once for all rows (FP16
- * matrix cores, FP32 activations split into FP16 hi + lo, FP32 sums) and the
- * same attention arithmetic as a batch-1 step past 512 positions. Every model
- * is validated (pending verification, capacity, token range) before any
- * runs. Afterwards each model has current logits and qwen_gpu_greedy works
- * as after a step. No reference counterpart. */
+ * matrix cores, FP32 activations split into FP16 hi + lo, FP32 sums) and an
+ * online-softmax attention over position pieces (held to the reference's
+ * tolerance gate, not bit-equal to a batch-1 step). Rows that models hold as
+ * copies of the same prefix (qwen_gpu_copy_prefix) are read from one of
+ * them. Every model is validated (pending verification, capacity, token
+ * range) before any runs. Afterwards each model has current logits and
+ * qwen_gpu_greedy works as after a step. No reference counterpart. */
 int qwen_gpu_step_batch(qwen_gpu_model* const* models, const int* tokens, int count);
+/* qwen_gpu_step_batch, then next[i] = qwen_gpu_greedy(models[i]) in the same
+ * call (one host round trip per step for a greedy decode loop). Fails as
+ * either would; on failure next is unspecified. No reference counterpart. */
+int qwen_gpu_step_batch_greedy(qwen_gpu_model* const* models, const int* tokens, int count, int* next);
 
 /* Model::reset, engine/core.hpp:32; engine/core.cpp:718-721. */
 int qwen_gpu_reset(qwen_gpu_model* model);

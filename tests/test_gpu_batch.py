@@ -181,6 +181,27 @@ def test_shared_prefix_rows_bit_identical(qpkg, pack0, monkeypatch):
 
 
 @pytest.mark.gpu
+def test_step_batch_greedy_returns_the_selections(qpkg, pack0):
+    """step_batch_greedy = step_batch followed by each model's greedy():
+    same selections and bit-identical logits along a 4-step trajectory."""
+    base, batch, alone = _seed_sequences(qpkg, pack0)
+    try:
+        tokens = [m.greedy() for m in batch]
+        for _ in range(4):
+            nxt = qpkg.step_batch_greedy(batch, tokens)
+            qpkg.step_batch(alone, tokens)
+            assert nxt == [m.greedy() for m in alone] == [m.greedy() for m in batch]
+            for b, a in zip(batch, alone):
+                assert np.array_equal(b.logits().view(np.uint32), a.logits().view(np.uint32))
+            tokens = nxt
+        with pytest.raises(RuntimeError, match='Token ID out of range'):
+            qpkg.step_batch_greedy(batch[:2], [1, 151936])
+    finally:
+        for m in batch + alone + [base]:
+            m.close()
+
+
+@pytest.mark.gpu
 def test_step_batch_validates_before_running(qpkg, pack0):
     prompt = PROMPTS['long_3968']
     with qpkg.Model(pack0) as a, qpkg.Model(pack0) as stranger:
