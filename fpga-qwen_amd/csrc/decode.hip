@@ -1708,8 +1708,9 @@ constexpr int kBufferWord3 = 0x00020000;
 constexpr int kLoadNT = 2;
 constexpr int kInFlight = 4;
 
-// NB = the largest number of 64-position blocks a piece of this launch holds.
-template <int NB>
+// NB = the largest number of 64-position blocks a piece of this launch
+// holds; EMBED: the first layer (the residual is the embedding row).
+template <int NB, bool EMBED>
 __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs args) {
     const int w = blockIdx.x, g = w & 7, r = w >> 3, B = args.batch, b = r % B, p = r / B;
     const int W = B * args.pieces;  // attention workgroups of this XCD (the grid holds 32 per XCD)
@@ -1731,15 +1732,16 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     // the phases need them: the residual inputs (elements 2 tid, 2 tid + 1 of
     // every sequence; rows past the batch repeat row B - 1), norm weights,
     // this workgroup's QKV weight tile, rotation.
-    // The loads are unconditional (without an embedding row the residual row
-    // is read twice), so none waits behind a branch.
+    // The first layer (EMBED) reads every sequence's embedding row instead.
     float2 xv[kMaxBatch];
     uint32_t ev[kMaxBatch];
 #pragma unroll
     for (int bb = 0; bb < kMaxBatch; ++bb) {
         const AttnBatchSeq& s2 = args.seq[min(bb, B - 1)];
-        xv[bb] = reinterpret_cast<const float2*>(s2.x)[tid];
-        ev[bb] = reinterpret_cast<const uint32_t*>(s2.embed ? static_cast<const void*>(s2.embed) : s2.x)[tid];
+        if constexpr (EMBED)
+            ev[bb] = reinterpret_cast<const uint32_t*>(s2.embed)[tid];
+        else
+            xv[bb] = reinterpret_cast<const float2*>(s2.x)[tid];
     }
     const float2 wn = reinterpret_cast<const float2*>(args.in_norm)[tid];
     // QKV tile tr (16 of the 512 rows of KV head g): query rows 256 g + 16 tr
@@ -1803,13 +1805,9 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     __shared__ double red[4][2];
     __shared__ float wm[8][2], wl[8][2];
 
-    // Selects, not branches: a branch here would make the compiler wait for
-    // every load in flight (the QKV weights too) before the norm.
+    if constexpr (EMBED) {
 #pragma unroll
-    for (int bb = 0; bb < kMaxBatch; ++bb) {
-        const bool embedded = args.seq[min(bb, B - 1)].embed != nullptr;
-        const float e0 = h2f(ev[bb] & 0xffffu), e1 = h2f(ev[bb] >> 16);
-        xv[bb] = make_float2(embedded ? e0 : xv[bb].x, embedded ? e1 : xv[bb].y);
+        for (int bb = 0; bb < kMaxBatch; ++bb) xv[bb] = make_float2(h2f(ev[bb] & 0xffffu), h2f(ev[bb] >> 16));
     }
 
     // RMSNorm of every sequence's row: per-thread FP64 sums of the FP32
@@ -2213,7 +2211,7 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         if (live) {
             const float y = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
             const AttnBatchSeq& sq = args.seq[seq];
-            sq.x_out[row] = (sq.embed ? h2f(sq.embed[row]) : sq.x[row]) + y;
+            sq.x_out[row] = (EMBED ? h2f(sq.embed[row]) : sq.x[row]) + y;
         }
     }
     if (!ok) *args.stall = 1;
@@ -2684,12 +2682,25 @@ void launch_attention_o_batch(const AttnSeq* seqs, int count, const uint16_t* w_
     b.pieces = attn_batch_pieces(positions, count, pieces, per);
     require(count * b.pieces <= 32, "attention batch: at most 32 attention workgroups per XCD");
     constexpr int kGrid = 256;  // 32 workgroups per XCD: one per QKV tile and per 32 O rows
-    if (per <= 2) attn_batch_kernel<2><<<kGrid, 512, 0, stream>>>(b);
-    else if (per <= 4) attn_batch_kernel<4><<<kGrid, 512, 0, stream>>>(b);
-    else if (per <= 6) attn_batch_kernel<6><<<kGrid, 512, 0, stream>>>(b);
-    else if (per <= 9) attn_batch_kernel<9><<<kGrid, 512, 0, stream>>>(b);
-    else if (per <= 12) attn_batch_kernel<12><<<kGrid, 512, 0, stream>>>(b);
-    else attn_batch_kernel<16><<<kGrid, 512, 0, stream>>>(b);
+    bool embed = b.seq[0].embed != nullptr;
+    for (int i = 1; i < count; ++i)
+        require((b.seq[i].embed != nullptr) == embed, "attention batch: embedding rows for all sequences or none");
+    auto launch = [&](auto kernel) { kernel<<<kGrid, 512, 0, stream>>>(b); };
+    if (embed) {
+        if (per <= 2) launch(attn_batch_kernel<2, true>);
+        else if (per <= 4) launch(attn_batch_kernel<4, true>);
+        else if (per <= 6) launch(attn_batch_kernel<6, true>);
+        else if (per <= 9) launch(attn_batch_kernel<9, true>);
+        else if (per <= 12) launch(attn_batch_kernel<12, true>);
+        else launch(attn_batch_kernel<16, true>);
+    } else {
+        if (per <= 2) launch(attn_batch_kernel<2, false>);
+        else if (per <= 4) launch(attn_batch_kernel<4, false>);
+        else if (per <= 6) launch(attn_batch_kernel<6, false>);
+        else if (per <= 9) launch(attn_batch_kernel<9, false>);
+        else if (per <= 12) launch(attn_batch_kernel<12, false>);
+        else launch(attn_batch_kernel<16, false>);
+    }
 }
 
 void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, int token, const float* cosines,
