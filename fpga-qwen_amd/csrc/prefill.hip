@@ -154,13 +154,19 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
     __shared__ __align__(16) unsigned char smem[kSmem];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Tile of this workgroup: workgroup w runs on XCD w % 8 (round-robin
-    // dispatch), which takes row tiles xcd, xcd + 8, ... and walks the column
-    // tiles, so each XCD keeps only its eighth of A resident in its L2 while
-    // W streams through. The grid is rounded up to whole XCD rows; the extra
-    // workgroups have no tile.
-    const int mtiles = (M + BM - 1) / BM, per = (mtiles + 7) / 8;
-    const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-    const int mt = xcd + 8 * (slot % per), nt = slot / per;
+    // dispatch). With 4 or more row tiles per XCD, XCD x takes row tiles
+    // x, x + 8, ... and walks the column tiles (its 32 CUs hold 4 row tiles
+    // x 8 column tiles at a time). With fewer (prompts up to 3 x 8 x BM
+    // rows), f = 4 or 2 XCDs pool their row tiles and split the column tiles
+    // by residue mod f, so that the tiles an XCD runs at once still share
+    // A and W rows in its L2: at 1024 rows 4 x 8 tiles per XCD instead of
+    // 1 x 32 (each W tile fetched by 2 XCDs instead of 8). The grid is
+    // rounded up to whole XCD rows; the extra workgroups have no tile.
+    const int mtiles = (M + BM - 1) / BM, per = (mtiles + 7) / 8, ntiles = N / BN;
+    const int f = per >= 4 ? 1 : per == 1 && ntiles % 4 == 0 ? 4 : ntiles % 2 == 0 ? 2 : 1;
+    const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8, rows = f * per;
+    const int rr = slot % rows, cc = slot / rows;
+    const int mt = (xcd / f) * f + rr % f + 8 * (rr / f), nt = xcd % f + f * cc;
     if (mt >= mtiles) return;
     const int m0 = mt * BM, n0 = nt * BN;
     const bool mma = wave < S::kMma;
@@ -394,17 +400,23 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
                                                            uint16_t* __restrict__ out_lo,
                                                            const float* __restrict__ parts, int rows) {
     const int b = blockIdx.x, tid = threadIdx.x;
-    float* x = X + size_t(b) * kHidden;
-    float v[4];
+    // Thread t holds columns 4t .. 4t + 3 (16-byte accesses).
+    float4* xr = reinterpret_cast<float4*>(X + size_t(b) * kHidden) + tid;
+    float4 v4 = *xr;
+    if constexpr (SPLITS > 0) {
+        const size_t stride = size_t(rows) * kHidden / 4;
+        const float4* pr = reinterpret_cast<const float4*>(parts + size_t(b) * kHidden) + tid;
+        const float4 p0 = pr[0], p1 = pr[stride], p2 = pr[2 * stride], p3 = pr[3 * stride];
+        v4.x = v4.x + ((p0.x + p1.x) + (p2.x + p3.x));
+        v4.y = v4.y + ((p0.y + p1.y) + (p2.y + p3.y));
+        v4.z = v4.z + ((p0.z + p1.z) + (p2.z + p3.z));
+        v4.w = v4.w + ((p0.w + p1.w) + (p2.w + p3.w));
+        *xr = v4;
+    }
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     double part = 0.0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int j = tid + 256 * k;
-        v[k] = x[j];
-        if constexpr (SPLITS > 0) {
-            v[k] = fold_splits<SPLITS>(v[k], parts + size_t(b) * kHidden + j, size_t(rows) * kHidden);
-            x[j] = v[k];
-        }
         const float square = v[k] * v[k];
         part += static_cast<double>(square);
     }
@@ -414,11 +426,19 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
     __syncthreads();
     const float sum = static_cast<float>((red[0] + red[1]) + (red[2] + red[3]));
     const float inv = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
+    const float4 w4 = reinterpret_cast<const float4*>(w)[tid];
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+    uint16_t hi[4], lo[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int j = tid + 256 * k;
-        split_store((v[k] * inv) * w[j], out_hi, out_lo, size_t(b) * kHidden + j);
+        _Float16 h, l;
+        split_half((v[k] * inv) * wv[k], h, l);
+        hi[k] = __builtin_bit_cast(uint16_t, h);
+        lo[k] = __builtin_bit_cast(uint16_t, l);
     }
+    const size_t at = size_t(b) * kHidden + 4 * tid;
+    *reinterpret_cast<uint2*>(out_hi + at) = make_uint2(hi[0] | (unsigned(hi[1]) << 16), hi[2] | (unsigned(hi[3]) << 16));
+    *reinterpret_cast<uint2*>(out_lo + at) = make_uint2(lo[0] | (unsigned(lo[1]) << 16), lo[2] | (unsigned(lo[3]) << 16));
 }
 
 // Causal attention for a prefill chunk on the matrix cores (engine/core.cpp:
