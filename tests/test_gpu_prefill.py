@@ -23,8 +23,11 @@ PROMPTS = json.loads((Path(__file__).parent / 'golden' / 'prompts.json').read_te
 @pytest.mark.gpu
 @pytest.mark.parametrize('m,n,k', [(1, 1024, 1024), (37, 4096, 1024), (85, 1024, 2048), (512, 6144, 1024),
                                    (129, 1024, 3072), (1000, 4096, 1024), (1100, 6144, 1024),
-                                   (1024, 6144, 1024)])
+                                   (1024, 6144, 1024), (2500, 4096, 1024)])
 def test_gemm_against_fp64(qpkg, m, n, k):
+    """Row counts cover each tile-to-XCD mapping of 128-row tiles: 1000 /
+    1024 rows (4 XCDs pool their row tiles), 1100 (2 XCDs pool 2 row tiles
+    each), 2500 (2 XCDs pool 3 each), plus the narrower 32 / 64-row tiles."""
     rng = np.random.default_rng(21)
     a = rng.standard_normal((m, k), dtype=np.float32) * 3
     w = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float16)
