@@ -125,19 +125,22 @@ def test_copy_prefix_equals_truncate(qpkg, pack0):
 
 
 def _prefix_family(qpkg, pack0):
-    """A base sequence and five sequences built from copies of its rows:
+    """A base sequence and six sequences built from copies of its rows:
     copies of 700 and 520 rows, a 650-row copy rewound to 200 and refilled
-    with other tokens, a copy of the first copy (600 rows), and a copy taken
-    after the base was rewound to 100 and refilled (its rows 100.. differ)."""
+    with other tokens, a copy of the first copy (600 rows), a 640-row copy
+    with a larger cache than the copy it reads its rows from (another row
+    stride), and a copy taken after the base was rewound to 100 and refilled
+    (its rows 100.. differ)."""
     prompt = PROMPTS['long_3968']
     base = qpkg.Model(pack0, context=4096)
     base.prefill(prompt[:700])
     seqs = []
-    for source_index, rows, rewind, suffix in ((None, 700, None, prompt[1000:1010]),
-                                               (None, 520, None, prompt[1100:1150]),
-                                               (None, 650, 200, prompt[1200:1500]),
-                                               (0, 600, None, prompt[1300:1330])):
-        m = base.share(context=2048)
+    for source_index, rows, rewind, suffix, context in ((None, 700, None, prompt[1000:1010], 2048),
+                                                        (None, 520, None, prompt[1100:1150], 2048),
+                                                        (None, 650, 200, prompt[1200:1500], 2048),
+                                                        (0, 600, None, prompt[1300:1330], 2048),
+                                                        (None, 640, None, prompt[1400:1420], 3000)):
+        m = base.share(context=context)
         m.copy_prefix(base if source_index is None else seqs[source_index], rows)
         if rewind is not None:
             m.truncate(rewind)
