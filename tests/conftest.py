@@ -12,7 +12,7 @@ PACK_CACHE = Path(os.environ.get('QWEN_GPU_PACK_CACHE', '/tmp/qwen_gpu_packs'))
 
 
 def pytest_configure(config):
-    config.addinivalue_line('markers', 'gpu: needs an MI355X (runs on the GPU box)')
+    config.addinivalue_line('markers', 'gpu: needs an MI355X GPU')
 
 
 def load_package():
