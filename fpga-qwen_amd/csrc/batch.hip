@@ -407,6 +407,32 @@ __global__ __launch_bounds__(512) void lm_head_batch_kernel(const BatchLmArgs a)
 #pragma unroll
     for (int bb = 0; bb < kMaxBatch; ++bb) xv[bb] = reinterpret_cast<const float2*>(a.x[min(bb, B - 1)])[tid];
     const float2 wn = reinterpret_cast<const float2*>(a.norm_w)[tid];
+    // Tile k of this workgroup: rows 16 (w + 256 k) ..; loads past the last
+    // tile repeat it and are not used.
+    const int ntiles = (kLmTiles - w + kBatchLmGroups - 1) / kBatchLmGroups;
+    auto load_tile = [&](u32x4 (&wt)[4], int k) {
+        const int t = min(w + kBatchLmGroups * k, kLmTiles - 1);
+        // Piece (t, wave, st) of the matrix-core copy: 64 lanes x 16 bytes
+        // in a row, so that every load reads 1 KiB contiguous.
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w) + (size_t(t) * 8 + wave) * 256 + lane;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 64 * st);
+    };
+    // Epilogue element of threads 0..255: row 4 (lane / 16) + wave of the
+    // tile, sequence lane % 16; its running best over the tiles.
+    const int eb = lane & 15, erow = 4 * (lane >> 4) + (wave & 3);
+    // Loaded before the stream and waited for (by the empty asm that uses
+    // it) right after the first tiles are issued: a pointer still pending
+    // inside the loop would wait behind the tiles in flight.
+    float* out = a.logits[min(eb, B - 1)];
+    // The first tiles do not depend on the norm: issued behind the residual
+    // rows (which return first), they stream while the norm is formed.
+    u32x4 ring[kLmInFlight][4];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kLmInFlight; ++u) load_tile(ring[u], u);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(out));
 
     __shared__ __align__(16) _Float16 xh[kMaxBatch][kHidden + 8];
     __shared__ __align__(16) _Float16 xl[kMaxBatch][kHidden + 8];
@@ -459,30 +485,6 @@ __global__ __launch_bounds__(512) void lm_head_batch_kernel(const BatchLmArgs a)
         __syncthreads();
     }
 
-    // Tile k of this workgroup: rows 16 (w + 256 k) ..; loads past the last
-    // tile repeat it and are not used.
-    const int ntiles = (kLmTiles - w + kBatchLmGroups - 1) / kBatchLmGroups;
-    auto load_tile = [&](u32x4 (&wt)[4], int k) {
-        const int t = min(w + kBatchLmGroups * k, kLmTiles - 1);
-        // Piece (t, wave, st) of the matrix-core copy: 64 lanes x 16 bytes
-        // in a row, so that every load reads 1 KiB contiguous.
-        const u32x4* wp = reinterpret_cast<const u32x4*>(a.w) + (size_t(t) * 8 + wave) * 256 + lane;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) wt[st] = __builtin_nontemporal_load(wp + 64 * st);
-    };
-    // Epilogue element of threads 0..255: row 4 (lane / 16) + wave of the
-    // tile, sequence lane % 16; its running best over the tiles.
-    const int eb = lane & 15, erow = 4 * (lane >> 4) + (wave & 3);
-    // Loaded (and waited for, by the empty asm that uses it) before the
-    // stream: a pointer still pending inside the loop would wait behind the
-    // tiles in flight.
-    float* out = a.logits[min(eb, B - 1)];
-    asm volatile("" : "+v"(out));
-    u32x4 ring[kLmInFlight][4];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < kLmInFlight; ++u) load_tile(ring[u], u);
-    __builtin_amdgcn_sched_barrier(0);
     float bv = -INFINITY, lg[kLmTilesPerGroup];
     int bi = INT_MAX, bad = 0;
     // Fully unrolled (compile-time ring slots and tile counts, so every wait
