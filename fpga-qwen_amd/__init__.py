@@ -57,6 +57,7 @@ SIGNATURES = {
     'qwen_gpu_update_penalized': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _c_int_p, ctypes.c_size_t]),
     'qwen_gpu_verify_two_greedy': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _c_int_p, _c_int_p]),
     'qwen_gpu_write_random_pack': (ctypes.c_int, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_double, ctypes.c_int]),
+    'qwen_gpu_validate_pack': (ctypes.c_int, [ctypes.c_char_p]),
     'qwen_gpu_device_malloc': (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
     'qwen_gpu_device_free': (ctypes.c_int, [ctypes.c_void_p]),
     'qwen_gpu_memcpy_to_device': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
@@ -286,6 +287,12 @@ def step_batch_greedy(models, tokens):
     return out[:]
 
 
+def validate_pack(path):
+    """The engine's pack checks (no device needed); raises RuntimeError with
+    the reference's message on a malformed pack."""
+    _check(_LIB.qwen_gpu_validate_pack(str(path).encode()))
+
+
 def write_random_pack(path, seed=0, stddev=0.02, threads=None):
     """Seeded QWCPU01 pack: matrices N(0, stddev) in FP16, norm gains 1.0."""
     threads = threads or min(16, os.cpu_count() or 1)
@@ -434,13 +441,27 @@ def attention_prefill(qkv, keys, values, pos0):
     return (h + l).reshape(rows, 2048)
 
 
+def _gemm_operands(a, w, c):
+    """A FP32 [M, K], W FP16 [N, K] with N % 128 == 0 and K % 64 == 0, C (if
+    given) [M, N]: checked before anything reaches the device, since the
+    kernel reads and writes whole tiles of these shapes."""
+    a = np.ascontiguousarray(a, np.float32)
+    w = np.ascontiguousarray(w, np.float16)
+    if a.ndim != 2 or w.ndim != 2:
+        raise ValueError(f'gemm: a and w must be matrices, got {a.shape} and {w.shape}')
+    m, k = a.shape
+    n = w.shape[0]
+    if m < 1 or w.shape[1] != k or n % 128 or k % 64 or n < 128 or k < 64:
+        raise ValueError(f'gemm: w must be [N, {k}] with N % 128 == 0 and K % 64 == 0, got a {a.shape}, w {w.shape}')
+    if c is not None and np.shape(c) != (m, n):
+        raise ValueError(f'gemm: c must be [{m}, {n}], got {np.shape(c)}')
+    return a, w, m, n, k
+
+
 def gemm(a, w, c=None):
     """C = A W^T (or C += A W^T when C is given) on the matrix cores: A FP32
     [M, K], W FP16 [N, K] natural layout. Returns C as a NumPy array."""
-    a = np.ascontiguousarray(a, np.float32)
-    w = np.ascontiguousarray(w, np.float16)
-    m, k = a.shape
-    n = w.shape[0]
+    a, w, m, n, k = _gemm_operands(a, w, c)
     ad, wd = DeviceBuffer.from_array(a), DeviceBuffer.from_array(w)
     cd = DeviceBuffer.from_array(np.ascontiguousarray(c, np.float32)) if c is not None else DeviceBuffer(m * n * 4)
     _check(_LIB.qwen_gpu_op_gemm(ad.ptr, wd.ptr, cd.ptr, m, n, k, int(c is not None), None))
@@ -558,10 +579,7 @@ def norm_qkv_folded(tiled, norm_weight, xm, dparts):
 def gemm_static(a, w, c=None):
     """gemm() through the entry point that allocates nothing (operand planes
     in the library's static device array; M x K at most 1048576)."""
-    a = np.ascontiguousarray(a, np.float32)
-    w = np.ascontiguousarray(w, np.float16)
-    m, k = a.shape
-    n = w.shape[0]
+    a, w, m, n, k = _gemm_operands(a, w, c)
     ad, wd = DeviceBuffer.from_array(a), DeviceBuffer.from_array(w)
     cd = DeviceBuffer.from_array(np.ascontiguousarray(c, np.float32)) if c is not None else DeviceBuffer(m * n * 4)
     _check(_LIB.qwen_gpu_op_gemm_static(ad.ptr, wd.ptr, cd.ptr, m, n, k, int(c is not None), None))

@@ -246,6 +246,14 @@ int qwen_gpu_write_random_pack(const char* path, uint64_t seed, double stddev, i
     });
 }
 
+int qwen_gpu_validate_pack(const char* path) {
+    return guarded([&] {
+        need(path, "path");
+        qwen_hip::Pack pack(path);
+        pack.validate();
+    });
+}
+
 static void hip_ok(hipError_t e) {
     if (e != hipSuccess) throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(e));
 }

@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "batch.hpp"
@@ -21,6 +22,19 @@
     } while (0)
 
 namespace qwen_hip {
+
+// The fused decode kernels and the batched step hand values between the
+// workgroups of one launch, so each launch needs all of its 256 workgroups
+// resident at once (one per CU). Two such launches in flight together, from
+// engines stepped on different host threads, could split the CUs between
+// them and both give up polling ("Decode step stalled"). Every call that
+// launches them holds this process-wide lock (the engine runs on device 0)
+// until its stream has drained, so such calls from several threads run one
+// after another.
+static std::mutex& launch_lock() {
+    static std::mutex lock;
+    return lock;
+}
 
 template <class T>
 T* Engine::device_alloc(size_t count) {
@@ -312,6 +326,19 @@ void Engine::truncate(int position) {
     invalidate();
 }
 
+// A call that fails after launching its kernels (an exchange that gave up,
+// a HIP error) leaves the K/V rows from its start position on written from
+// garbage or not at all: the sequence returns to that position without
+// current logits, and its content identity is renewed since those rows will
+// be rewritten.
+void Engine::roll_back(int position) {
+    pos_ = position;
+    prefix_len_ = std::min(prefix_len_, position);
+    pending_ = false;
+    renew_content();
+    invalidate();
+}
+
 // One token through the 28 layers (5 kernels each) and, when `head`, the
 // final norm, tied lm_head and greedy argmax into host result slot
 // `result_slot`. The step scalars are kernel arguments.
@@ -371,6 +398,17 @@ void Engine::append(const int* ids, size_t count) {
     require(count > 0, "Empty token input");
     require(count <= size_t(options_.context - pos_), "Context capacity exceeded");
     for (size_t i = 0; i < count; ++i) require(ids[i] >= 0 && ids[i] < kVocab, "Token ID out of range");
+    const int start = pos_;
+    std::lock_guard<std::mutex> hold(launch_lock());
+    try {
+        run_append(ids, count);
+    } catch (...) {
+        roll_back(start);
+        throw;
+    }
+}
+
+void Engine::run_append(const int* ids, size_t count) {
     invalidate();
     // The reference splits a call into 512-row chunks counted from its start
     // and runs a one-row chunk on the batch-1 path (engine/core.cpp:712). Every
@@ -500,21 +538,30 @@ void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
     }
     // The batched launches exchange through the first sequence's buffers,
     // which its single-sequence launches use too: tags from its counter.
-    uint32_t tags[kBatchTagsPerLayer * kLayers];
-    for (uint32_t& t : tags) t = lead.next_tag();
-    for (int i = 0; i < count; ++i) {
-        Engine& e = *seqs[i];
-        e.invalidate();
-        bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_,
-                         shared_seq[i], shared[i]};
-        HIP_CHECK(hipStreamSynchronize(e.stream_));
+    int starts[kMaxBatch];
+    for (int i = 0; i < count; ++i) starts[i] = seqs[i]->pos_;
+    std::lock_guard<std::mutex> hold(launch_lock());
+    try {
+        uint32_t tags[kBatchTagsPerLayer * kLayers];
+        for (uint32_t& t : tags) t = lead.next_tag();
+        for (int i = 0; i < count; ++i) {
+            Engine& e = *seqs[i];
+            e.invalidate();
+            bs[i] = BatchSeq{e.layers_.data(), e.scratch_, e.pos_, tokens[i], e.options_.context, e.result_host_,
+                             shared_seq[i], shared[i]};
+            HIP_CHECK(hipStreamSynchronize(e.stream_));
+        }
+        launch_decode_batch(bs, count, lead.embed_, lead.weights_->embed_mfma, lead.final_norm_, lead.cosines_,
+                            lead.sines_, tags, lead.stream_);
+        HIP_CHECK(hipGetLastError());
+        lead.sync();
+        for (int i = 0; i < count; ++i) ++seqs[i]->pos_;
+        for (int i = 0; i < count; ++i) seqs[i]->check_stall(0);  // as append: no logits after a stall
+    } catch (...) {
+        // Every sequence of the batch wrote its K/V rows at its position.
+        for (int i = 0; i < count; ++i) seqs[i]->roll_back(starts[i]);
+        throw;
     }
-    launch_decode_batch(bs, count, lead.embed_, lead.weights_->embed_mfma, lead.final_norm_, lead.cosines_, lead.sines_,
-                        tags, lead.stream_);
-    HIP_CHECK(hipGetLastError());
-    lead.sync();
-    for (int i = 0; i < count; ++i) ++seqs[i]->pos_;
-    for (int i = 0; i < count; ++i) seqs[i]->check_stall(0);  // as append: no logits after a stall
     for (int i = 0; i < count; ++i) seqs[i]->has_logits_ = true;
 }
 
@@ -543,6 +590,7 @@ void Engine::verify_two(int first, int second) {
     require(first >= 0 && first < kVocab && second >= 0 && second < kVocab, "Token ID out of range");
     require(pos_ <= options_.context - 2, "Context capacity exceeded");
     const int start = pos_;
+    std::lock_guard<std::mutex> hold(launch_lock());
     try {
         if (fused_attn_ || pair_supported(start)) {
             run_pair(first, second);
@@ -658,6 +706,7 @@ void Engine::commit_verified(int count) {
 
 float Engine::time_kernel(int which, int iterations) {
     require(pos_ > 0 && !pending_, "time_kernel needs a current position");
+    std::lock_guard<std::mutex> hold(launch_lock());
     HIP_CHECK(hipStreamSynchronize(stream_));
     require(which >= 0 && which <= 7 && iterations > 0, "time_kernel: bad arguments");
     if (which == 2) return 0.f;  // O runs with the attention (1)

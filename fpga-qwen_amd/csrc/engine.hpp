@@ -92,6 +92,8 @@ public:
 private:
     void init_state();
     void append(const int* ids, size_t count);
+    void run_append(const int* ids, size_t count);
+    void roll_back(int position);
     void run_token(int token, bool head, int result_slot);
     void run_pair(int first, int second);
     LayerFlow layer_flow(int layer, bool pair = false);

@@ -7,6 +7,19 @@
  * QWEN_GPU_ERROR and qwen_gpu_last_error() (per calling thread) holds the
  * message, using the reference's wording (engine/core.cpp:235-276, 707-752).
  * One caller at a time per model (engine/core.hpp:23).
+ *
+ * Decode kernels hand values between the workgroups of one launch, so a
+ * launch needs the whole GPU (all 256 CUs) to itself. Calls that run them on
+ * models stepped from different threads of one process take a process-wide
+ * lock and run one after another; another process decoding on the same GPU
+ * at the same time can make a step fail with "Decode step stalled" (a
+ * bounded wait that gave up, never a hang).
+ *
+ * A prefill, step or batched step that fails after validation (a stalled
+ * exchange, a HIP error) returns each model to its position before the call,
+ * without current logits; K/V rows from that position on are rewritten by
+ * the next call. A failed verification resets the model
+ * (engine/core.cpp:740).
  */
 #ifndef QWEN_GPU_H
 #define QWEN_GPU_H
@@ -133,6 +146,11 @@ int qwen_gpu_update_penalized(qwen_gpu_model* model, int clear, const int* ids, 
  * FP16 from a counter-based splitmix64 Box-Muller stream, norm gains 1.0.
  * Writes PATH, PATH.index and PATH.manifest.json; refuses existing outputs. */
 int qwen_gpu_write_random_pack(const char* path, uint64_t seed, double stddev, int threads);
+/* The pack checks of Model::Model without a device: maps PATH and runs the
+ * header, index, shape, range, overlap and finiteness checks of
+ * engine/core.cpp:235-276 with the same messages (what qwen_gpu_create runs
+ * before touching the GPU). For exporters and tools on hosts without one. */
+int qwen_gpu_validate_pack(const char* path);
 
 /* Device memory plumbing for callers that hold no other GPU runtime (the
  * op-level entry points below take device pointers). No reference counterpart:

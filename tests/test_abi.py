@@ -6,6 +6,7 @@ import re
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -63,3 +64,20 @@ def test_create_errors_are_reported(qpkg, pack0):
     else:
         model.close()
         pytest.skip('a GPU is present')
+
+
+@pytest.mark.parametrize('name', ['gemm', 'gemm_static'])
+def test_gemm_shapes_checked_before_the_device(qpkg, name):
+    """The GEMM wrappers reject operands the kernel's whole-tile reads and
+    writes would overrun before any device buffer exists (so on a host
+    without a GPU too)."""
+    call = getattr(qpkg, name)
+    a = np.zeros((4, 64), np.float32)
+    for w, c, message in ((np.zeros((128, 128), np.float16), None, 'w must be'),
+                          (np.zeros((100, 64), np.float16), None, 'w must be'),
+                          (np.zeros((128, 64), np.float16), np.zeros((4, 100), np.float32), 'c must be'),
+                          (np.zeros(128, np.float16), None, 'matrices')):
+        with pytest.raises(ValueError, match=message):
+            call(a, w, c)
+    with pytest.raises(ValueError, match='w must be'):
+        call(np.zeros((4, 96), np.float32), np.zeros((128, 96), np.float16))

@@ -154,13 +154,13 @@ def test_rejections(tmp_path, case, message):
     assert not (tmp_path / 'out' / 'weights.bin').exists()
 
 
-def test_full_shape_export_passes_engine_validation(tmp_path, qpkg):
-    """A synthetic BF16 checkpoint with the exact Qwen3-0.6B tensor set: the
-    exported pack must pass the engine's validator (on a host without a GPU
-    the constructor then stops at the device check)."""
+def write_full_checkpoint(path, seed=7):
+    """A synthetic BF16 checkpoint with the exact Qwen3-0.6B tensor set: each
+    matrix a differently rotated window of one N(0, 0.02) BF16 pattern, norm
+    gains 1.0, lm_head a copy of the embedding."""
     shapes = export_pack.qwen3_tensor_table()
-    rng = np.random.default_rng(7)
-    wide = rng.standard_normal(1 << 19).astype(np.float32) * 0.02
+    rng = np.random.default_rng(seed)
+    wide = rng.standard_normal(1 << 21).astype(np.float32) * 0.02
     pattern = bf16((wide.view(np.uint32) & 0xffff0000).view(np.float32))
     ones = bf16(np.ones(1, np.float32))[0]
     names = list(shapes) + ['lm_head.weight']
@@ -171,26 +171,68 @@ def test_full_shape_export_passes_engine_validation(tmp_path, qpkg):
         header[name] = dict(dtype='BF16', shape=list(shape), data_offsets=[cursor, cursor + size])
         cursor += size
     raw = json.dumps(header).encode()
-    path = tmp_path / 'model.safetensors'
     with path.open('wb') as f:
         f.write(struct.pack('<Q', len(raw)) + raw)
-        for name in names:
-            shape = shapes['model.embed_tokens.weight'] if name == 'lm_head.weight' else shapes[name]
+        for index, name in enumerate(names):
+            tied = name == 'lm_head.weight'
+            shape = shapes['model.embed_tokens.weight'] if tied else shapes[name]
             count = int(np.prod(shape))
             if len(shape) == 1:
                 f.write(np.full(count, ones, '<u2').tobytes())
                 continue
-            reps = -(-count // pattern.size)
-            f.write(np.tile(pattern, reps)[:count].tobytes())
+            window = np.roll(pattern, 7919 * (0 if tied else index))
+            reps = -(-count // window.size)
+            f.write(np.tile(window, reps)[:count].tobytes())
+    return path
+
+
+def test_full_shape_export_passes_engine_validation(tmp_path, qpkg):
+    """The exported pack of a full-shape synthetic checkpoint passes the
+    engine's own pack checks (qwen_gpu_validate_pack: the checks the engine
+    runs before it touches a device, so the test is the same with or
+    without one)."""
+    path = write_full_checkpoint(tmp_path / 'model.safetensors')
     out = tmp_path / 'pack' / 'weights.bin'
     export_pack.write_pack(path, out)
     index = out.with_name('weights.bin.index').read_text().splitlines()
     assert index[0] == 'QWCPU01 310' and len(index) == 311
+    qpkg.validate_pack(out)
+    data = bytearray(out.read_bytes()[:64])
+    assert data[:7] == b'QWCPU01'
+    broken = tmp_path / 'broken' / 'weights.bin'
+    broken.parent.mkdir()
+    broken.with_name('weights.bin.index').write_text(
+        out.with_name('weights.bin.index').read_text().replace('QWCPU01 310', 'QWCPU01 309', 1))
+    broken.write_bytes(out.read_bytes())
+    with pytest.raises(RuntimeError):
+        qpkg.validate_pack(broken)
+
+
+@pytest.mark.gpu
+def test_exported_pack_runs_on_gpu_against_oracle(tmp_path, qpkg, oracle_lib):
+    """An exported full-shape pack served by the engine on the GPU: the
+    85-token prompt and 4 greedy steps, every position's logits against the
+    oracle on the same exported file under the reference gate (max-abs 1e-2,
+    RMS 2e-3, greedy identity)."""
+    from oracle_binding import compare_logits
+    path = write_full_checkpoint(tmp_path / 'model.safetensors')
+    out = tmp_path / 'pack' / 'weights.bin'
+    export_pack.write_pack(path, out)
+    path.unlink()
+    prompt = json.loads((ROOT / 'tests' / 'golden' / 'prompts.json').read_text())['decode_85']
+    model = qpkg.Model(out, context=256)
+    oracle = oracle_lib.model(out, 16, 16, 256)
     try:
-        model = qpkg.Model(out, context=64)
-    except RuntimeError as error:
-        assert 'No HIP device available' in str(error), error
-    else:
-        with model:
-            model.prefill([9707])
-            assert model.logits().size == 151936
+        model.prefill(prompt)
+        oracle.prefill(prompt)
+        for step in range(5):
+            result = compare_logits(model.logits(), oracle.logits())
+            print('exported pack, position', model.position(), result, flush=True)
+            assert result['passed'], (step, result)
+            token = model.greedy()
+            if step < 4:
+                model.step(token)
+                oracle.step(token)
+    finally:
+        model.close()
+        oracle.close()

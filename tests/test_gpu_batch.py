@@ -288,3 +288,57 @@ def test_prefix_reuse_workload_matches_oracle(qpkg, pack0, oracle_lib):
     finally:
         oracle.close()
     print('max_abs vs oracle', worst, 'alone vs batched', worst_alone)
+
+
+@pytest.mark.gpu
+def test_step_batch_long_pieces(qpkg, pack0, oracle_lib):
+    """8 sequences at 2,900-3,043 and at 3,884-4,062 positions: each
+    sequence's 64-position blocks, split into 4 pieces per KV head, give 12
+    and 16 blocks per piece (the batched attention kernel's two largest
+    forms, past what the 2,048-position prefix-reuse workload reaches). Every
+    batched row passes the reference gate against the same sequence
+    re-stepped alone, and sequence 0's rows against the oracle."""
+    prompt, other = PROMPTS['long_3968'], PROMPTS['prefill_1024']
+    steps = 3
+    base = qpkg.Model(pack0, context=4096)
+    seqs = [base.share() for _ in range(8)]
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    worst_alone = worst_oracle = 0.0
+    oracle_valid = 0
+    try:
+        for shared, lengths in ((2816, [2900 + 20 * i for i in range(8)]), (3584, [3884 + 25 * i for i in range(8)])):
+            base.reset()
+            base.prefill(prompt[:shared])
+            starts = []
+            for i, (m, n) in enumerate(zip(seqs, lengths)):
+                suffix = prompt[shared:n] if i == 0 else other[37 * i:37 * i + n - shared]
+                assert len(suffix) == n - shared
+                m.copy_prefix(base, shared)
+                m.prefill(suffix)
+                starts.append(m.position())
+            rows = [[(m.logits(), m.greedy())] for m in seqs]
+            for _ in range(steps):
+                qpkg.step_batch(seqs, [r[-1][1] for r in rows])
+                for r, m in zip(rows, seqs):
+                    r.append((m.logits(), m.greedy()))
+            for r, m, start in zip(rows, seqs, starts):
+                m.truncate(start)
+                for k in range(1, steps + 1):
+                    m.step(r[k - 1][1])
+                    result = compare_logits(m.logits(), r[k][0])
+                    assert result['passed'], ('alone vs batched', start, k, result)
+                    worst_alone = max(worst_alone, result['max_abs'])
+            oracle.truncate(min(oracle_valid, lengths[0]))
+            oracle.prefill(prompt[min(oracle_valid, lengths[0]):lengths[0]])
+            for k, (logits, _) in enumerate(rows[0]):
+                if k:
+                    oracle.step(rows[0][k - 1][1])
+                result = compare_logits(logits, oracle.logits())
+                assert result['passed'], ('sequence 0', lengths[0], k, result)
+                worst_oracle = max(worst_oracle, result['max_abs'])
+            oracle_valid = lengths[0]
+    finally:
+        for m in seqs + [base]:
+            m.close()
+        oracle.close()
+    print('max_abs vs oracle', worst_oracle, 'alone vs batched', worst_alone)

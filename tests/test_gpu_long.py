@@ -1,12 +1,13 @@
 """Long-context decode parity (the 3968-token workload, seed 3).
 
-Up to 512 cached positions decode attention runs fused with the O
-projection (one workgroup per KV head and block of O rows, partial
-projections folded into the residual stream by the next kernels); beyond
-that it splits the positions into up to 32 chunks of 128 whose partial
-softmax statistics a merge kernel combines before the O projection. These tests
-cover the switch between the two paths, many splits and the 512-row prefill
-chunk boundaries against the oracle's sequential softmax
+Decode attention runs inside one kernel per layer with the QKV and O
+projections. Up to 256 cached positions every workgroup attends its query
+head over all positions in 64-position passes (FULL form, 1 to 4 passes);
+beyond, the 32 workgroups of a KV head each take passes s and s + 32 and
+merge their (output, max, sum) partials in a fixed order. These tests cover
+every pass count of the FULL form, the switch to the split form (256 -> 257
+positions), many passes, the capacity limit and the 512-row prefill chunk
+boundaries against the oracle's sequential softmax
 (engine/core.cpp:606-624), teacher-forced like tools/check_native_logits.py,
 under the gate of tools/check_native_saved_oracle.py:36.
 """
@@ -40,9 +41,25 @@ def check_trajectory(gpu, oracle, prompt, steps):
 
 
 @pytest.mark.gpu
+def test_full_form_passes_and_split_switch_match_oracle(qpkg, pack0, oracle_lib):
+    """Steps at n = 125 .. 264 cached positions: the FULL form with 2, 3 and 4
+    passes (switches at 129 and 193 positions), then the split form from 257
+    on; every row against the oracle."""
+    gpu = qpkg.Model(pack0, context=4096)
+    oracle = oracle_lib.model(pack0, 16, 16, 4096)
+    try:
+        results = check_trajectory(gpu, oracle, PROMPTS['long_3968'][:124], 141)
+        assert gpu.position() == 264
+        print('max_abs', max(r['max_abs'] for r in results), 'rms', max(r['rms'] for r in results))
+    finally:
+        gpu.close()
+        oracle.close()
+
+
+@pytest.mark.gpu
 def test_fused_to_split_attention_matches_oracle(qpkg, pack0, oracle_lib):
-    # Steps at n = 506 .. 517 cached positions: fused attention + O up to 512,
-    # split attention with the O-prologue merge from 513 on.
+    # Steps at n = 506 .. 517 cached positions (the split form, 8 passes; the
+    # separate kernels' switch from attention + O to split + merge at 512/513).
     gpu = qpkg.Model(pack0, context=4096)
     oracle = oracle_lib.model(pack0, 16, 16, 4096)
     try:

@@ -84,8 +84,9 @@ def test_fused_kernels_match_separate_kernels(qpkg, pack0, gpu_model, monkeypatc
     layer. QWEN_HIP_FUSED_ATTENTION=0: the QKV kernel and the fused (up to 512
     positions) or split + merge attention kernels, instead of one kernel whose
     workgroups attend over 64-position passes and merge their partials. Along
-    greedy trajectories after the 85-token prompt and after 1100- and
-    3000-token prompts both paths choose the same tokens and their logits
+    greedy trajectories after the 85-, 200-, 1100- and 3000-token prompts
+    (the 200-token one crosses from 3 to 4 passes of the FULL form and on to
+    the split form at 257 positions) both paths choose the same tokens and their logits
     agree to 1e-4: the different summation orders move outputs by a few FP32
     ulps, nothing more (a wrong slice, row, head, pass or fold moves them by
     ~1e-1)."""
@@ -93,9 +94,10 @@ def test_fused_kernels_match_separate_kernels(qpkg, pack0, gpu_model, monkeypatc
     plain = qpkg.Model(pack0, context=4096)
     monkeypatch.delenv(switch)
     try:
-        for prompt in (PROMPTS['decode_85'], PROMPTS['long_3968'][:1100], PROMPTS['long_3968'][:3000]):
-            fused_rows = greedy_trajectory(gpu_model, prompt, 12)
-            plain_rows = greedy_trajectory(plain, prompt, 12)
+        for prompt, steps in ((PROMPTS['decode_85'], 12), (PROMPTS['long_3968'][:190], 70),
+                              (PROMPTS['long_3968'][:1100], 12), (PROMPTS['long_3968'][:3000], 12)):
+            fused_rows = greedy_trajectory(gpu_model, prompt, steps)
+            plain_rows = greedy_trajectory(plain, prompt, steps)
             worst = 0.0
             for (lf, tf), (lp, tp) in zip(fused_rows, plain_rows):
                 assert tf == tp
@@ -104,6 +106,42 @@ def test_fused_kernels_match_separate_kernels(qpkg, pack0, gpu_model, monkeypatc
             assert worst <= 1e-4
     finally:
         plain.close()
+
+
+@pytest.mark.gpu
+def test_models_stepped_from_two_threads(qpkg, pack0):
+    """Two independent models (own weights, caches and streams) decoding at
+    the same time from two host threads: the library runs their decode
+    launches one after another (each needs every CU), so no step stalls and
+    each trajectory is bit-identical to the same model run alone."""
+    import threading
+    prompt = PROMPTS['decode_85']
+    models = [qpkg.Model(pack0, context=512) for _ in range(2)]
+    try:
+        lengths = (40, 60)
+        expected = [greedy_trajectory(m, prompt[:n], 30) for m, n in zip(models, lengths)]
+        got, errors = [None, None], []
+
+        def run(i):
+            try:
+                got[i] = greedy_trajectory(models[i], prompt[:lengths[i]], 30)
+            except Exception as error:  # reported by the main thread
+                errors.append(error)
+
+        threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=100)
+        assert not any(t.is_alive() for t in threads), 'a decode thread did not finish'
+        assert not errors, errors
+        for exp, rows in zip(expected, got):
+            for (le, te), (lg, tg) in zip(exp, rows):
+                assert te == tg
+                assert np.array_equal(le.view(np.uint32), lg.view(np.uint32))
+    finally:
+        for m in models:
+            m.close()
 
 
 @pytest.mark.gpu
