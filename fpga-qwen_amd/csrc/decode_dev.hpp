@@ -216,9 +216,10 @@ __device__ __forceinline__ void exchange_put_through(uint64_t* p, float v, uint3
 // waits (a wave-uniform exit), and each lane's result comes from its own
 // flag: lanes leaving a loop at different iterations would otherwise hand the
 // compiler a divergent loop exit for the result.
-__device__ __forceinline__ bool exchange_get2(const uint64_t* p, uint32_t tag, float& a, float& b) {
+__device__ __forceinline__ bool exchange_get2(const uint64_t* p, uint32_t tag, float& a, float& b,
+                                              unsigned limit = kExchangeSpins) {
     unsigned missing = 1;
-    for (unsigned spin = 0; spin < kExchangeSpins && __any(missing); ++spin) {
+    for (unsigned spin = 0; spin < limit && __any(missing); ++spin) {
         if (missing) {
             const uint64_t u = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const uint64_t w = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -238,9 +239,9 @@ __device__ __forceinline__ bool exchange_get2(const uint64_t* p, uint32_t tag, f
 // within kExchangeSpins rounds.
 template <int N>
 __device__ __forceinline__ bool exchange_gather(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N],
-                                                unsigned want) {
+                                                unsigned want, unsigned limit = kExchangeSpins) {
     // Wave-uniform loop exit, per-lane result from `want` (see exchange_get2).
-    for (unsigned spin = 0; spin < kExchangeSpins && __any(want != 0); ++spin) {
+    for (unsigned spin = 0; spin < limit && __any(want != 0); ++spin) {
         uint64_t u[N];
 #pragma unroll
         for (int k = 0; k < N; ++k)

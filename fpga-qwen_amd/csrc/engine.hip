@@ -123,6 +123,12 @@ static std::shared_ptr<Weights> load_weights(const Pack& pack, hipStream_t strea
         L.post_norm = upload_norm(pack.layer(l, "post_attention_layernorm.weight"));
         L.q_norm = upload_norm(pack.layer(l, "self_attn.q_norm.weight"));
         L.k_norm = upload_norm(pack.layer(l, "self_attn.k_norm.weight"));
+        {
+            float* qk = static_cast<float*>(alloc(2 * kHeadDim * 4));
+            HIP_CHECK(hipMemcpy(qk, L.q_norm, kHeadDim * 4, hipMemcpyDeviceToDevice));
+            HIP_CHECK(hipMemcpy(qk + kHeadDim, L.k_norm, kHeadDim * 4, hipMemcpyDeviceToDevice));
+            L.qk_norm = qk;
+        }
         w->prefill[l] = PrefillLayer{qkv_n, o_n, gu_n, down_n, L.in_norm, L.post_norm, L.q_norm, L.k_norm,
                                      nullptr, nullptr};
     }
@@ -198,8 +204,10 @@ void Engine::init_state() {
     layers_ = w.layers;
     prefill_layers_ = w.prefill;
     for (int l = 0; l < kLayers; ++l) {
-        layers_[l].keys = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
-        layers_[l].values = device_alloc<uint16_t>(size_t(kKVHeads) * ctx * kHeadDim);
+        // Keys then values of a layer in one allocation (the token kernel
+        // addresses both from the keys).
+        layers_[l].keys = device_alloc<uint16_t>(2 * size_t(kKVHeads) * ctx * kHeadDim);
+        layers_[l].values = layers_[l].keys + size_t(kKVHeads) * ctx * kHeadDim;
         prefill_layers_[l].keys = layers_[l].keys;
         prefill_layers_[l].values = layers_[l].values;
     }
@@ -239,12 +247,18 @@ void Engine::init_state() {
     pair_.xm = device_alloc<float>(2 * kHidden);
     pair_.dparts = device_alloc<float>(size_t(2) * kFfnSlices * kHidden);
     pair_.exchange = device_alloc<uint64_t>(2 * kFFN);
+    token_words_ = device_alloc<uint64_t>(kTokWords);
     HIP_CHECK(hipMemsetAsync(s.stall, 0, sizeof(int), stream_));
     clear_exchanges();
 
     if (const char* env = std::getenv("QWEN_HIP_FUSED_FFN")) fused_ffn_ = std::string(env) != "0";
     if (const char* env = std::getenv("QWEN_HIP_FUSED_ATTENTION")) fused_attn_ = std::string(env) != "0";
     if (const char* env = std::getenv("QWEN_HIP_SHARED_PREFIX")) share_prefix_ = std::string(env) != "0";
+    if (const char* env = std::getenv("QWEN_HIP_TOKEN_KERNEL")) token_kernel_ = std::string(env) != "0";
+    if (const char* env = std::getenv("QWEN_HIP_TOKEN_PREFETCH")) token_prefetch_ = std::string(env) != "0";
+    if (const char* env = std::getenv("QWEN_HIP_TEST_WITHHOLD")) token_withhold_ = std::atoi(env);
+    if (const char* env = std::getenv("QWEN_HIP_TEST_SPINS")) token_spins_ = unsigned(std::max(1, std::atoi(env)));
+    token_kernel_ = token_kernel_ && fused_ffn_ && fused_attn_;
     renew_content();
 
     penalized_ = device_alloc<uint8_t>(kVocab);
@@ -362,6 +376,17 @@ void Engine::clear_exchanges() {
     HIP_CHECK(hipMemsetAsync(scratch_.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.bexchange, 0, kBatchExchangeWords * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(token_words_, 0, kTokWords * sizeof(uint64_t), stream_));
+}
+
+uint32_t Engine::reserve_tags(int count) {
+    if (ffn_tag_ > 0xFFFFFFFFu - uint32_t(count)) {
+        clear_exchanges();
+        ffn_tag_ = 0;
+    }
+    const uint32_t first = ffn_tag_ + 1;
+    ffn_tag_ += uint32_t(count);
+    return first;
 }
 
 LayerFlow Engine::layer_flow(int layer, bool pair) {
@@ -383,6 +408,33 @@ void Engine::check_stall(int slot) const {
 }
 
 void Engine::run_token(int token, bool head, int result_slot) {
+    if (token_kernel_) {
+        TokenLaunch t{};
+        for (int l = 0; l < kLayers; ++l) {
+            const LayerDevice& L = layers_[l];
+            t.layers[l] = TokenLayer{L.qkv_t, L.o_n, L.gateup_t, L.down_t, L.in_norm, L.post_norm, L.qk_norm, L.keys};
+        }
+        t.layer_count = kLayers;
+        t.embed = embed_;
+        t.token = token;
+        t.pos = pos_;
+        t.context = options_.context;
+        t.cosines = cosines_;
+        t.sines = sines_;
+        t.x_out = scratch_.x;
+        t.words = token_words_;
+        t.stall = scratch_.stall;
+        t.scale = 1.0f / std::sqrt(128.0f);
+        t.tag = reserve_tags(kLayers);
+        t.spins = token_spins_;
+        t.withhold = token_withhold_;
+        t.prefetch = token_prefetch_ ? 1 : 0;
+        launch_token_layers(t, stream_);
+        if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
+        HIP_CHECK(hipGetLastError());
+        ++pos_;
+        return;
+    }
     for (int l = 0; l < kLayers; ++l)
         launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, pos_, token, cosines_, sines_, options_.context,
                             scratch_, layer_flow(l), stream_);

@@ -10,6 +10,7 @@
 #include "kernels.hpp"
 #include "prefill.hpp"
 #include "sampler.hpp"
+#include "token.hpp"
 
 namespace qwen_hip {
 
@@ -98,6 +99,8 @@ private:
     void run_pair(int first, int second);
     LayerFlow layer_flow(int layer, bool pair = false);
     uint32_t next_tag();
+    // `count` consecutive tags (none of them 0) for one launch.
+    uint32_t reserve_tags(int count);
     void clear_exchanges();
     void check_stall(int slot) const;
     void release();
@@ -140,6 +143,15 @@ private:
     // QWEN_HIP_FUSED_ATTENTION=0; its launches take tags from the same counter.
     bool fused_attn_ = true;
     uint32_t ffn_tag_ = 0;
+    // A single-row step runs its 28 layers as one persistent launch
+    // (launch_token_layers) unless QWEN_HIP_TOKEN_KERNEL=0 (or either fused
+    // kernel is switched off): exchange words, poll limit and the test-only
+    // withheld post (QWEN_HIP_TEST_WITHHOLD / _SPINS).
+    bool token_kernel_ = true;
+    uint64_t* token_words_ = nullptr;
+    unsigned token_spins_ = kTokenSpins;
+    int token_withhold_ = -1;
+    bool token_prefetch_ = true;
     // Identity of this sequence's K/V rows [0, pos_): a new process-unique
     // id whenever rows below pos_ may be rewritten (construction, reset,
     // rewind, copy_prefix). A copy records its source's id and length: rows

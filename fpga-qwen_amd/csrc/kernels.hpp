@@ -89,6 +89,7 @@ struct LayerDevice {
     const float* post_norm;    // [1024]
     const float* q_norm;       // [128]
     const float* k_norm;       // [128]
+    const float* qk_norm;      // [256]: q_norm then k_norm in one allocation (token kernel)
     uint16_t* keys;            // [8][context][128], chain-permuted rows
     uint16_t* values;          // [8][context][128]
 };

@@ -1,0 +1,897 @@
+// One launch per decode token for gfx950 (CDNA4, wave64): the 28 layers of
+// a batch-1 step (engine/core.cpp:353-646 for one row) in one persistent
+// kernel.
+//
+// Why one launch: between two dependent kernels the GPU spends ~1.2 us of
+// launch gap and ~2.5 us until the next kernel's first data arrives (its
+// inputs were just written on other XCDs, and every workgroup starts by
+// loading them together with its weights), 57 times per token. Inside one
+// launch the two residual hand-overs of a layer are exchanges through memory
+// (~1.1-1.5 us each), and each phase's weights are already in LDS when it
+// starts.
+//
+// Workgroup w = g + 8 s (XCD g, slot s), 12 waves:
+// * waves 0-7 (compute) run the phases of the fused QKV + attention + O
+//   kernel and of the fused FFN kernel (decode.hip) with the same thread
+//   layouts and arithmetic, so every row is bit-identical to that path, and
+//   do every exchange poll;
+// * waves 8-11 (load) copy the layer's weight tiles into LDS with direct
+//   global -> LDS loads, one region per phase (QKV tiles with the input and
+//   QK norm weights, O rows, gate/up tiles with the post-attention norm
+//   weights, down tiles). A region is refilled with the next layer's tiles
+//   as soon as its phase is done, so the weights stream a layer ahead of the
+//   arithmetic. Load waves never poll: a wave's loads complete in issue
+//   order, so a poll issued behind weight loads would wait for them.
+// All 12 waves pass the same barriers (s_barrier without a memory fence).
+// Compute waves wait for their own LDS accesses before each barrier; load
+// waves wait for the region the next phase reads with an exact vmcnt (the
+// loads they issued after it may stay in flight).
+//
+// Residual hand-overs across XCDs (the O projection's 16 head partials, the
+// FFN's 8 down slices): producers post their rows with write-through stores;
+// the 8 workgroups of slot s (one per XCD) each gather rows 32 s .. 32 s +
+// 31, fold them in the fixed tree order of the two-kernel path, and post
+// the 32 sums inside their XCD, where every workgroup gathers all 1024.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+
+#include "decode_dev.hpp"
+#include "token.hpp"
+
+namespace qwen_hip {
+namespace {
+
+using namespace dev;
+
+constexpr int kComputeWaves = 8, kLoadWaves = 4;
+constexpr int kTokenThreads = 64 * (kComputeWaves + kLoadWaves);
+
+// LDS regions (bytes) and the direct loads (1 KiB each) each load wave issues for them.
+constexpr int kRegQkv = 2 * 16384;   // QKV tiles li = 2s, 2s + 1 of the head group
+constexpr int kRegO = 64 * 256;       // O rows 64 (s / 2) .. + 63 over head h's 128 columns
+constexpr int kRegGu = 3 * 16384;     // gate/up tiles 96 g + 3 s .. + 2
+constexpr int kRegDown = 4 * 6144;    // down tiles 4 s .. 4 s + 3 over slice g's 6 column blocks
+constexpr int kLoadsQkv = 10;         // 8 tile blocks, a quarter of the input norm, the QK norms
+constexpr int kLoadsO = 4;
+constexpr int kLoadsGu = 13;          // 12 tile blocks, a quarter of the post-attention norm
+constexpr int kLoadsDown = 6;
+constexpr int kLoadsPrefetch = 2;     // next layer's K/V lines into L2
+static_assert(kRegQkv / 1024 == 8 * kLoadWaves && kRegO / 1024 == kLoadsO * kLoadWaves &&
+                  kRegGu / 1024 == 12 * kLoadWaves && kRegDown / 1024 == kLoadsDown * kLoadWaves,
+              "every load wave issues the same loads");
+// When each region's loads are issued. A CU returns loads in issue order, so
+// an exchange poll issued behind weight loads waits for them, and a load
+// wave that issues a long burst holds up the next barrier (the issue rate is
+// bound by HBM when every CU streams). So each region's loads are spread
+// over several barrier intervals, a few per interval, in intervals without
+// polls where possible. Interval k runs from barrier Bk to Bk+1 (B0: the
+// previous layer's last barrier). Per layer l, per load wave:
+//   k = 0: gate/up(l) loads 0-4        k = 5: QKV(l + 1) 3-4
+//   k = 1: gate/up(l) 5-8              k = 6: QKV(l + 1) 5-6
+//   k = 3: gate/up(l) 9-12, prefetch 0 k = 8: O(l + 1) 0-2
+//   k = 4: down(l) 0-5, prefetch 1,    k = 9: O(l + 1) 3, QKV(l + 1) 7-9
+//          QKV(l + 1) 0-2
+// At the start: QKV(0) and O(0) in the order of intervals 4-9. A region's
+// wait comes after its interval's loads; it allows the loads issued after
+// the region (the same count for every layer but the last, which waits for
+// all):
+//   QKV(l) in interval 0: gate/up(l) 0-4                          = 5
+//   O(l) in interval 4: QKV(l) 7-9, gate/up(l), prefetch, down(l),
+//     QKV(l + 1) 0-2                                               = 27
+//   gate/up(l) in interval 8: prefetch 0-1, down, QKV(l + 1) 0-6,
+//     O(l + 1) 0-2 (less prefetch 0, issued with gate/up 9-12)     = 18
+//   down(l) in interval 10: prefetch 1, QKV(l + 1), O(l + 1)       = 15
+constexpr int kAfterQkv = 5;
+constexpr int kAfterO = 3 + kLoadsGu + kLoadsPrefetch + kLoadsDown + 3;
+constexpr int kAfterGu = 1 + kLoadsDown + 1 + 7 + 3;
+constexpr int kAfterDown = 1 + kLoadsQkv + kLoadsO;
+static_assert(kAfterO == 27 && kAfterGu == 18 && kAfterDown == 15, "wait counts of the load plan");
+
+constexpr int kXPart = kHeadDim + 2;  // attention partial: 128 outputs, max, sum
+
+// 16 bytes per lane from global memory into LDS at lds + 16 lane (lds
+// wave-uniform), counted by vmcnt.
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
+// vmcnt <= n (expcnt and lgkmcnt unconstrained).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Barrier of all 12 waves without a memory fence (a fenced barrier would
+// make the load waves wait for every load in flight). Each wave first waits
+// for its own LDS accesses, so what it wrote is visible after the barrier;
+// the empty asm statements keep the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Exchange polls that also give up as soon as another workgroup raised the
+// step's stall word (so one missing post costs one poll limit, not one per
+// waiting workgroup and phase).
+template <int N>
+__device__ __forceinline__ bool tok_gather(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N], unsigned want,
+                                           const int* stall, unsigned limit) {
+    for (unsigned spin = 0; spin < limit && __any(want != 0); ++spin) {
+        uint64_t u[N];
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            u[k] = (want >> k) & 1 ? __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        const int raised = __hip_atomic_load(stall, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
+                out[k] = __uint_as_float(uint32_t(u[k]));
+                want &= ~(1u << k);
+            }
+        if (__any(raised != 0)) break;
+    }
+    // A give-up raises the stall word at once: the other workgroups stop
+    // polling and the step's argmax reports it.
+    if (want != 0) __hip_atomic_store(const_cast<int*>(stall), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return want == 0;
+}
+
+__device__ __forceinline__ bool tok_get2(const uint64_t* p, uint32_t tag, float& a, float& b, const int* stall,
+                                         unsigned limit) {
+    const uint64_t* const words[2] = {p, p + 1};
+    float got[2] = {0.f, 0.f};
+    const bool ok = tok_gather<2>(words, tag, got, 3u, stall, limit);
+    a = got[0];
+    b = got[1];
+    return ok;
+}
+
+// Global-memory views of the K/V cache pointers (which the kernel reads from
+// its arguments, so the compiler cannot infer their address space and would
+// use flat accesses, which also count in lgkmcnt).
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+typedef __attribute__((address_space(1))) uint16_t global_u16;
+__device__ __forceinline__ const global_u32x4* global_rows(const uint16_t* p) {
+    return (const global_u32x4*)(p);
+}
+__device__ __forceinline__ global_u16* global_halves(uint16_t* p) { return (global_u16*)(p); }
+
+__device__ __forceinline__ float fold_slices(float xm, const float (&d)[kFfnSlices]) {
+    return xm + (((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7])));
+}
+
+// QKV tile of local index li (0..63) of head group g: q tiles 32 g + li,
+// k tiles 256 + 16 g + li - 32, v tiles 384 + 16 g + li - 48.
+__device__ __forceinline__ int qkv_tile(int g, int li) {
+    return li < 32 ? 32 * g + li : li < 48 ? 256 + 16 * g + (li - 32) : 384 + 16 * g + (li - 48);
+}
+
+struct Lds {
+    unsigned char wq[kRegQkv];
+    unsigned char wo[kRegO];
+    unsigned char wgu[kRegGu];
+    unsigned char wdn[kRegDown];
+    float nin[kHidden];      // input RMSNorm weights
+    float npost[kHidden];    // post-attention RMSNorm weights
+    float nqk[2 * kHeadDim];  // q norm, k norm
+    unsigned char junk[1024];  // target of the K/V prefetch loads
+    float x[kHidden];        // residual the layer starts from
+    float xm[kHidden];       // residual after the attention block
+    float4 xs4[kHidden / 4];  // normalized input, chain-permuted
+    float4 as4[kFfnSlice / 4];  // this XCD's activations, chain-permuted
+    double red[4];
+    float qp[2][128];
+    float prob[2][128];
+    float opart[8][2][128];
+    uint16_t kcur[128], vcur[128];
+    float wmax[8][2], wsum[8][2];
+    float gm[4], gl[4], go[4][128];
+    float att[128];
+    float rope[2][64];  // cos, sin of this position's 64 rotation pairs
+};
+
+// Load waves: one region's loads for layer `layer` (lw = load wave 0..3).
+struct Loader {
+    const TokenLaunch& a;  // the kernel arguments (layer pointers read with scalar loads)
+    int g, s, lw, lane, context, pos;
+
+    // Load i (0-9) of the QKV region: 8 tile blocks, a quarter of the input
+    // norm weights, the QK norm weights.
+    __device__ void qkv(Lds& m, int layer, int i) const {
+        const TokenLayer& L = a.layers[layer];
+        if (i < 8) {
+            const int k = 8 * lw + i, t = k >> 4, b = k & 15;
+            const int tile = qkv_tile(g, 2 * s + t);
+            dma16(L.qkv_t + (size_t(tile) * 16 + b) * 512 + 8 * lane, m.wq + 1024 * k);
+        } else if (i == 8) {
+            dma16(L.in_norm + 256 * lw + 4 * lane, reinterpret_cast<unsigned char*>(m.nin) + 1024 * lw);
+        } else {
+            dma16(L.qk_norm + 4 * lane, m.nqk);
+        }
+    }
+    __device__ void o(Lds& m, int layer, int i) const {
+        const TokenLayer& L = a.layers[layer];
+        const int h = 2 * g + (s & 1), rb = s >> 1;
+        const int k = kLoadsO * lw + i, r = 4 * k + (lane >> 4), piece = lane & 15;
+        dma16(L.o_n + size_t(64 * rb + r) * kQDim + 128 * h + 8 * piece, m.wo + 1024 * k);
+    }
+    // Load i (0-12) of the gate/up region: 12 tile blocks, a quarter of the
+    // post-attention norm weights.
+    __device__ void gu(Lds& m, int layer, int i) const {
+        const TokenLayer& L = a.layers[layer];
+        if (i < 12) {
+            const int k = 12 * lw + i;
+            dma16(L.gateup_t + (size_t(96 * g + 3 * s) * 16 + k) * 512 + 8 * lane, m.wgu + 1024 * k);
+        } else {
+            dma16(L.post_norm + 256 * lw + 4 * lane, reinterpret_cast<unsigned char*>(m.npost) + 1024 * lw);
+        }
+    }
+    __device__ void down(Lds& m, int layer, int b) const {
+        const TokenLayer& L = a.layers[layer];
+        const int tile = 4 * s + lw;
+        dma16(L.down_t + (size_t(tile) * (kFFN / 64) + 6 * g + b) * 512 + 8 * lane, m.wdn + 1024 * (6 * lw + b));
+    }
+    // Lines of the K/V rows [0, pos) of head g in layer `layer`, a 1/32
+    // share per workgroup of the XCD (128-byte lines, one lane each; lanes
+    // past the rows read line 0), into L2 ahead of the compute waves' loads.
+    // With `on` false the same load re-reads the QK norm weights into the
+    // junk area (the waits count loads).
+    __device__ void prefetch(Lds& m, int layer, int i, bool on) const {
+        const TokenLayer& L = a.layers[layer];
+        if (!on) {
+            dma16(L.qk_norm + 4 * lane, m.junk);
+            return;
+        }
+        const size_t base = size_t(g) * context * 128;     // halves
+        const size_t kv = size_t(kKVHeads) * context * 128;  // values after the keys
+        const int lines = 2 * pos;                         // per matrix
+        const int q = 512 * s + 64 * (kLoadsPrefetch * lw + i) + lane;
+        // Key lines, then the value lines (kv halves further on).
+        const size_t at = q < lines ? base + 64 * size_t(q) : q < 2 * lines ? kv + base + 64 * size_t(q - lines) : base;
+        dma16(L.keys + at, m.junk);
+    }
+};
+
+// The chain dot of NB 16-byte LDS blocks (block b at w[64 b]) against the
+// permuted LDS vector (block b's 8 values at x4[16 b], x4[16 b + 1]) in the
+// reference's FMA order. The next two blocks are read while the chain steps
+// of the current two run, which bounds the registers the dot holds (about
+// 50 instead of the ~190 of all 16 blocks read up front).
+template <int NB>
+__device__ __forceinline__ float lds_chain(const u32x4* w, const float4* x4) {
+    static_assert(NB % 2 == 0, "pairs of blocks");
+    u32x4 w0 = w[0], w1 = w[64];
+    float4 a0 = x4[0], b0 = x4[1], a1 = x4[16], b1 = x4[17];
+    float acc = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; b += 2) {
+        u32x4 nw0 = w0, nw1 = w1;
+        float4 na0 = a0, nb0 = b0, na1 = a1, nb1 = b1;
+        if (b + 2 < NB) {
+            nw0 = w[64 * (b + 2)];
+            nw1 = w[64 * (b + 3)];
+            na0 = x4[16 * (b + 2)];
+            nb0 = x4[16 * (b + 2) + 1];
+            na1 = x4[16 * (b + 3)];
+            nb1 = x4[16 * (b + 3) + 1];
+        }
+        acc = chain8(acc, w0, a0, b0);
+        acc = chain8(acc, w1, a1, b1);
+        w0 = nw0; w1 = nw1; a0 = na0; b0 = nb0; a1 = na1; b1 = nb1;
+        // Orders the chain steps before the next reads (a scheduling barrier
+        // alone leaves the arithmetic free to sink below every read).
+        asm volatile("" : "+v"(acc));
+    }
+    return acc;
+}
+
+// FULL (PASSES <= 4 passes of 64 positions, n <= 256): every workgroup
+// attends its query head over all positions; else the split form (passes s
+// and s + 32 of both heads, partials merged inside the XCD).
+//
+// The load waves and the compute waves run separate loops that pass the
+// same barriers, numbered B0 .. B13 below (the split form adds B6b).
+template <int PASSES, bool FULL>
+__global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch a) {
+    __shared__ Lds m;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = int(blockIdx.x & 7), s = int(blockIdx.x >> 3);
+    const int L = a.layer_count;
+
+    if (wave >= kComputeWaves) {
+        // lw in a scalar register: every load below must be one instruction
+        // executed by the whole wave (the waits count them), never a load
+        // under a divergent branch.
+        const int lw = __builtin_amdgcn_readfirstlane(wave - kComputeWaves);
+        const Loader ld{a, g, s, lw, lane, a.context, a.pos};
+        auto qkv = [&](int layer, int first, int count) {
+            for (int i = first; i < first + count; ++i) ld.qkv(m, layer, i);
+        };
+        auto o = [&](int layer, int first, int count) {
+            for (int i = first; i < first + count; ++i) ld.o(m, layer, i);
+        };
+        auto gu = [&](int layer, int first, int count) {
+            for (int i = first; i < first + count; ++i) ld.gu(m, layer, i);
+        };
+        const bool pf = a.prefetch != 0;
+        // QKV(0) and O(0) in the order of intervals 4-9 of a layer.
+        qkv(0, 0, 3);
+        qkv(0, 3, 2);
+        qkv(0, 5, 2);
+        o(0, 0, 3);
+        o(0, 3, 1);
+        qkv(0, 7, 3);
+        barrier();  // B0
+        for (int l = 0; l < L; ++l) {
+            const bool last = l + 1 == L;
+            gu(l, 0, 5);
+            wait_vmcnt<kAfterQkv>();  // QKV(l) and the input / QK norm weights
+            barrier();  // B1
+            gu(l, 5, 4);
+            barrier();  // B2
+            barrier();  // B3
+            gu(l, 9, 4);
+            if (!last) ld.prefetch(m, l + 1, 0, pf);
+            barrier();  // B4
+#pragma unroll
+            for (int b = 0; b < kLoadsDown; ++b) ld.down(m, l, b);
+            if (!last) {
+                ld.prefetch(m, l + 1, 1, pf);
+                qkv(l + 1, 0, 3);
+            }
+            if (last) wait_vmcnt<0>();
+            else wait_vmcnt<kAfterO>();  // O(l)
+            barrier();  // B5
+            if (!last) qkv(l + 1, 3, 2);
+            barrier();  // B6
+            if (!FULL) barrier();  // B6b
+            if (!last) qkv(l + 1, 5, 2);
+            barrier();  // B7
+            barrier();  // B8
+            if (!last) o(l + 1, 0, 3);
+            if (last) wait_vmcnt<0>();
+            else wait_vmcnt<kAfterGu>();  // gate/up(l) and the post-attention norm weights
+            barrier();  // B9
+            if (!last) {
+                o(l + 1, 3, 1);
+                qkv(l + 1, 7, 3);
+            }
+            barrier();  // B10
+            if (last) wait_vmcnt<0>();
+            else wait_vmcnt<kAfterDown>();  // down(l)
+            barrier();  // B11
+            barrier();  // B12
+            barrier();  // B13
+        }
+        return;
+    }
+
+    // Compute waves.
+    const int pos = a.pos, n = pos + 1, npasses = (n + 63) >> 6;
+    const int active = min(npasses, 32);
+    const bool mine = FULL || s < active;
+    const size_t head_base = size_t(g) * a.context;
+    const int hq = s & 1, h = 2 * g + hq, rb = s >> 1;
+    const unsigned spins = a.spins;
+    bool ok = true;
+    auto pass_base = [&](int p) { return FULL ? 64 * p : 64 * (s + 32 * p); };
+
+    // Layer 0 starts from the embedding row (engine/core.cpp:354-356).
+    if (tid < 256) {
+        const uint2 e = *reinterpret_cast<const uint2*>(a.embed + size_t(a.token) * kHidden + 4 * tid);
+        *reinterpret_cast<float4*>(&m.x[4 * tid]) =
+            make_float4(h2f(e.x & 0xffffu), h2f(e.x >> 16), h2f(e.y & 0xffffu), h2f(e.y >> 16));
+    }
+    if (wave == 0) {
+        m.rope[0][lane] = a.cosines[size_t(pos) * 64 + lane];
+        m.rope[1][lane] = a.sines[size_t(pos) * 64 + lane];
+    }
+    barrier();  // B0
+
+    for (int l = 0; l < L; ++l) {
+        const TokenLayer& TL = a.layers[l];
+        uint16_t* const values = TL.keys + size_t(kKVHeads) * a.context * 128;
+        const uint32_t tag = a.tag + uint32_t(l);
+        // The thread index, opaque to the compiler in each iteration:
+        // otherwise it hoists every per-thread address out of the layer loop
+        // and spills them.
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        uint64_t* const W = a.words;
+        const int lane = tid & 63, wave = tid >> 6;
+        const int j = tid & 127, c = tid & 7, grp = tid >> 3;
+        const int vsub = lane >> 4, vcg = lane & 15;
+        const int orow_local = tid >> 3, opart_id = tid & 7;
+        const int orow = 64 * rb + orow_local;
+        const int gu_tile = 96 * g + 3 * s + min(wave, 2);
+        const int down_tile = 4 * s + wave;
+
+        // ---- attention block (engine/core.cpp:384-406, 606-626) ----
+        // K/V rows of this workgroup's passes (positions past n, the current
+        // one, and all of an inactive workgroup's read row 0).
+        u32x4 kreg[PASSES][2], vreg[PASSES][2];
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = pass_base(p) + grp;
+            const int tl = mine && t < n && t != pos ? t : 0;
+            const global_u32x4* kp = global_rows(TL.keys + (head_base + tl) * 128);
+            kreg[p][0] = kp[c];
+            kreg[p][1] = kp[c + 8];
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int t = pass_base(p) + 8 * wave + 4 * hf + vsub;
+                const int tl = mine && t < n && t != pos ? t : 0;
+                vreg[p][hf] = global_rows(values + (head_base + tl) * 128)[vcg];
+            }
+        // RMSNorm of the residual (engine/core.cpp:207-215; FP32 squares
+        // summed in FP64): waves 0-3 hold entries 4 tid .. 4 tid + 3.
+        float v[4];
+        if (tid < 256) {
+            const float4 f = *reinterpret_cast<const float4*>(&m.x[4 * tid]);
+            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+            double part = 0.0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float square = v[k] * v[k];
+                part += static_cast<double>(square);
+            }
+            part = wave_sum(part);
+            if (lane == 0) m.red[wave] = part;
+        }
+        barrier();  // B1
+        if (tid < 256) {
+            const float sum = static_cast<float>(((m.red[0] + m.red[1]) + m.red[2]) + m.red[3]);
+            const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(kHidden) + 1e-6f);
+            float* xs = reinterpret_cast<float*>(m.xs4);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xs[xperm(4 * tid + k)] = (v[k] * inv) * m.nin[4 * tid + k];
+        }
+        barrier();  // B2
+
+        // QKV rows (the reference's chain-ordered dot): wave t < 2 runs tile
+        // li = 2 s + t over all 16 column blocks and posts its 8 rows.
+        if (wave < 2) {
+            const float y = combine_chains(
+                lds_chain<16>(reinterpret_cast<const u32x4*>(m.wq + 16384 * wave) + lane, m.xs4 + 2 * c));
+            const int li = 2 * s + wave;
+            if (c == 0 && !(l == 0 && int(blockIdx.x) == a.withhold))
+                exchange_put(W + kTokQkvOffset + g * 512 + 8 * li + (lane >> 3), y, tag);
+        }
+        // Wave w < 4 takes head-group rows 128 w + lane and 128 w + 64 + lane
+        // (q0, q1, k, v): QK-norm (engine/core.cpp:397-398) and rotate-half
+        // RoPE (216-218) inside the wave; the workgroup holding pos's pass
+        // writes the new K/V row (403-406).
+        if (tid < 256) {
+            const uint64_t* const words[2] = {W + kTokQkvOffset + g * 512 + 128 * wave + lane,
+                                              W + kTokQkvOffset + g * 512 + 128 * wave + 64 + lane};
+            float got[2] = {0.f, 0.f};
+            if (ok) ok = tok_gather<2>(words, tag, got, 3u, a.stall, spins);
+            const float x0 = got[0], x1 = got[1];
+            const bool owner = ((pos >> 6) & 31) == s;
+            if (wave < 3) {
+                const float* hw = m.nqk + (wave == 2 ? kHeadDim : 0);
+                const float sq0 = x0 * x0, sq1 = x1 * x1;
+                const double lo = wave_sum(static_cast<double>(sq0)), hi = wave_sum(static_cast<double>(sq1));
+                const float sum = static_cast<float>(lo + hi);
+                const float inv = 1.0f / __builtin_sqrtf(sum / 128.0f + 1e-6f);
+                const float n0 = (x0 * inv) * hw[lane], n1 = (x1 * inv) * hw[lane + 64];
+                const float rc = m.rope[0][lane], rs = m.rope[1][lane];
+                const float r0 = n0 * rc - n1 * rs, r1 = n1 * rc + n0 * rs;
+                if (wave < 2) {
+                    m.qp[wave][kperm(lane)] = r0;
+                    m.qp[wave][kperm(lane + 64)] = r1;
+                } else {
+                    const uint16_t b0 = f2h(r0), b1 = f2h(r1);
+                    m.kcur[kperm(lane)] = b0;
+                    m.kcur[kperm(lane + 64)] = b1;
+                    if (owner) {
+                        global_halves(TL.keys)[(head_base + pos) * 128 + kperm(lane)] = b0;
+                        global_halves(TL.keys)[(head_base + pos) * 128 + kperm(lane + 64)] = b1;
+                    }
+                }
+            } else {
+                const uint16_t b0 = f2h(x0), b1 = f2h(x1);
+                m.vcur[lane] = b0;
+                m.vcur[lane + 64] = b1;
+                if (owner) {
+                    global_halves(values)[(head_base + pos) * 128 + lane] = b0;
+                    global_halves(values)[(head_base + pos) * 128 + lane + 64] = b1;
+                }
+            }
+        }
+        barrier();  // B3
+
+        // Scores (engine/core.cpp:606-612): the 8 lanes of a position run its
+        // chains; each head's maximum over this workgroup's positions.
+        float s0[PASSES], s1[PASSES];
+        float m0 = -INFINITY, m1 = -INFINITY;
+        if (mine) {
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) {
+                const int t = pass_base(p) + grp;
+                uint32_t kw[8];
+                if (t == pos) {
+                    key_pieces_lds(m.kcur, c, kw);
+                } else {
+                    kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
+                    kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
+                }
+                if constexpr (FULL) {
+                    const float d0 = combine_chains(key_chain(m.qp[hq], c, kw, 0.f)) * a.scale;
+                    s0[p] = t < n ? d0 : -INFINITY;
+                    m0 = fmaxf(m0, s0[p]);
+                } else {
+                    const float d0 = combine_chains(key_chain(m.qp[0], c, kw, 0.f)) * a.scale;
+                    const float d1 = combine_chains(key_chain(m.qp[1], c, kw, 0.f)) * a.scale;
+                    s0[p] = t < n ? d0 : -INFINITY;
+                    s1[p] = t < n ? d1 : -INFINITY;
+                    m0 = fmaxf(m0, s0[p]);
+                    m1 = fmaxf(m1, s1[p]);
+                }
+            }
+            m0 = fmaxf(m0, xor_lanes<8>(m0));
+            m0 = fmaxf(m0, xor_lanes<16>(m0));
+            m0 = fmaxf(m0, xor_lanes<32>(m0));
+            if constexpr (!FULL) {
+                m1 = fmaxf(m1, xor_lanes<8>(m1));
+                m1 = fmaxf(m1, xor_lanes<16>(m1));
+                m1 = fmaxf(m1, xor_lanes<32>(m1));
+            }
+            if (lane == 0) {
+                m.wmax[wave][0] = m0;
+                m.wmax[wave][1] = m1;
+            }
+        }
+        barrier();  // B4
+
+        // Probabilities and P.V (engine/core.cpp:613-624): one maximum per
+        // head over the workgroup (so the waves' sums add without
+        // rescaling), each wave's sums over its positions.
+        if (mine) {
+            m0 = m.wmax[0][0];
+            m1 = m.wmax[0][1];
+#pragma unroll
+            for (int w = 1; w < 8; ++w) {
+                m0 = fmaxf(m0, m.wmax[w][0]);
+                m1 = fmaxf(m1, m.wmax[w][1]);
+            }
+            float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) {
+                const int t = pass_base(p) + grp;
+                const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
+                l0 += p0;
+                if constexpr (FULL) {
+                    if (c == 0) m.prob[t >> 7][t & 127] = p0;
+                } else {
+                    const float p1 = t < n ? expf(s1[p] - m1) : 0.f;
+                    l1 += p1;
+                    if (c == 0) {
+                        m.prob[0][p * 64 + grp] = p0;
+                        m.prob[1][p * 64 + grp] = p1;
+                    }
+                }
+            }
+            l0 += xor_lanes<8>(l0);
+            l0 += xor_lanes<16>(l0);
+            l0 += xor_lanes<32>(l0);
+            if constexpr (!FULL) {
+                l1 += xor_lanes<8>(l1);
+                l1 += xor_lanes<16>(l1);
+                l1 += xor_lanes<32>(l1);
+            }
+            // prob of this wave's positions is written and read by this wave only.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            constexpr int kHeads = FULL ? 1 : 2;
+            float acc[kHeads][8];
+#pragma unroll
+            for (int hh = 0; hh < kHeads; ++hh)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[hh][i] = 0.f;
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int t = pass_base(p) + 8 * wave + 4 * hf + vsub;
+                    if (t < n) {
+                        uint32_t vw[4];
+                        if (t == pos) {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                vw[i] = uint32_t(m.vcur[vcg * 8 + 2 * i]) | (uint32_t(m.vcur[vcg * 8 + 2 * i + 1]) << 16);
+                        } else {
+                            vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
+                        }
+                        if constexpr (FULL) {
+                            const float p0 = m.prob[t >> 7][t & 127];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                acc[0][2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p0, acc[0][2 * i]);
+                                acc[0][2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p0, acc[0][2 * i + 1]);
+                            }
+                        } else {
+                            const int tl = p * 64 + 8 * wave + 4 * hf + vsub;
+                            const float p0 = m.prob[0][tl], p1 = m.prob[1][tl];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
+                                acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
+                                acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
+                                acc[kHeads - 1][2 * i] = __builtin_fmaf(v0, p1, acc[kHeads - 1][2 * i]);
+                                acc[kHeads - 1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[kHeads - 1][2 * i + 1]);
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+            for (int hh = 0; hh < kHeads; ++hh)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    acc[hh][i] += xor_lanes<16>(acc[hh][i]);
+                    acc[hh][i] += xor_lanes<32>(acc[hh][i]);
+                }
+            if (vsub == 0) {
+#pragma unroll
+                for (int hh = 0; hh < kHeads; ++hh)
+#pragma unroll
+                    for (int i = 0; i < 8; i += 4)
+                        *reinterpret_cast<float4*>(&m.opart[wave][hh][vcg * 8 + i]) =
+                            make_float4(acc[hh][i], acc[hh][i + 1], acc[hh][i + 2], acc[hh][i + 3]);
+            }
+            if (lane == 0) {
+                m.wsum[wave][0] = l0;
+                m.wsum[wave][1] = l1;
+            }
+        }
+        barrier();  // B5
+
+        if constexpr (FULL) {
+            if (tid < 128) {  // the 8 waves' sums in a fixed tree
+                const float o = ((m.opart[0][0][tid] + m.opart[1][0][tid]) + (m.opart[2][0][tid] + m.opart[3][0][tid])) +
+                                ((m.opart[4][0][tid] + m.opart[5][0][tid]) + (m.opart[6][0][tid] + m.opart[7][0][tid]));
+                const float lsum = ((m.wsum[0][0] + m.wsum[1][0]) + (m.wsum[2][0] + m.wsum[3][0])) +
+                                   ((m.wsum[4][0] + m.wsum[5][0]) + (m.wsum[6][0] + m.wsum[7][0]));
+                m.att[tid] = o / lsum;
+            }
+            barrier();  // B6
+        } else {
+            // Each workgroup with positions posts (output, max, sum) of both
+            // heads; workgroup (g, s) merges head h over the active partials
+            // (4 groups of 8 against their own maximum, then combined).
+            if (mine && tid < 256) {
+                const int hh = tid >> 7;
+                const float o = ((m.opart[0][hh][j] + m.opart[1][hh][j]) + (m.opart[2][hh][j] + m.opart[3][hh][j])) +
+                                ((m.opart[4][hh][j] + m.opart[5][hh][j]) + (m.opart[6][hh][j] + m.opart[7][hh][j]));
+                const float lsum = ((m.wsum[0][hh] + m.wsum[1][hh]) + (m.wsum[2][hh] + m.wsum[3][hh])) +
+                                   ((m.wsum[4][hh] + m.wsum[5][hh]) + (m.wsum[6][hh] + m.wsum[7][hh]));
+                uint64_t* part = W + kTokPartOffset + ((size_t(g) * 32 + s) * 2 + hh) * kXPart;
+                exchange_put(part + j, o, tag);
+                if (j == 0) {
+                    exchange_put(part + 128, hh ? m1 : m0, tag);
+                    exchange_put(part + 129, lsum, tag);
+                }
+            }
+            {
+                const int q = tid >> 7;
+                float mv[8], lv[8], ovl[8];
+                {
+                    const uint64_t* words[24];
+                    float got[24];
+                    unsigned want = 0;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const uint64_t* part = W + kTokPartOffset + ((size_t(g) * 32 + 8 * q + k) * 2 + hq) * kXPart;
+                        words[k] = part + j;
+                        words[8 + k] = part + 128;
+                        words[16 + k] = part + 129;
+                        got[k] = got[8 + k] = got[16 + k] = 0.f;
+                        if (8 * q + k < active) want |= 0x10101u << k;
+                    }
+                    if (ok) ok = tok_gather<24>(words, tag, got, want, a.stall, spins);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        ovl[k] = got[k];
+                        mv[k] = 8 * q + k < active ? got[8 + k] : -INFINITY;
+                        lv[k] = got[16 + k];
+                    }
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (8 * q + k < active) mx = fmaxf(mx, mv[k]);
+                float lsum = 0.f, o = 0.f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (8 * q + k < active) {
+                        const float w = expf(mv[k] - mx);
+                        lsum += w * lv[k];
+                        o += w * ovl[k];
+                    }
+                if (j == 0) {
+                    m.gm[q] = mx;
+                    m.gl[q] = lsum;
+                }
+                m.go[q][j] = o;
+            }
+            barrier();  // B6
+            if (tid < 128) {
+                float m2 = m.gm[0];
+#pragma unroll
+                for (int q = 1; q < 4; ++q) m2 = fmaxf(m2, m.gm[q]);
+                float lt = 0.f, ot = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (m.gm[q] != -INFINITY) {  // a group without partials adds nothing
+                        const float w = expf(m.gm[q] - m2);
+                        lt += w * m.gl[q];
+                        ot += w * m.go[q][tid];
+                    }
+                m.att[tid] = ot / lt;
+            }
+            barrier();  // B6b
+        }
+
+        // O rows 64 rb .. + 63 against head h's attention output; each row's
+        // partial goes to the fold across XCDs.
+        {
+            const u32x4* wrow = reinterpret_cast<const u32x4*>(m.wo + 256 * orow_local) + opart_id;
+            const float4* at4 = reinterpret_cast<const float4*>(m.att) + 2 * opart_id;
+            float y = 0.f;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) y = chain8(y, wrow[8 * i], at4[16 * i], at4[16 * i + 1]);
+            y += xor_lanes<1>(y);
+            y += xor_lanes<2>(y);
+            y += xor_lanes<4>(y);
+            if (opart_id == 0) exchange_put_through(W + kTokOCrossOffset + size_t(h) * kHidden + orow, y, tag);
+        }
+        barrier();  // B7
+
+        // Fold 1 (engine/core.cpp:626): wave 0 forms rows 32 s .. + 31 of x +
+        // the 16 head partials (lane = row, half: heads 8 half .. + 7; the
+        // tree of the two-kernel path) and posts them inside the XCD; every
+        // thread then gathers two of the XCD's 1024 sums.
+        if (wave == 0) {
+            const int row = 32 * s + (lane >> 1), half = lane & 1;
+            const uint64_t* base = W + kTokOCrossOffset + size_t(8 * half) * kHidden + row;
+            const uint64_t* const words[8] = {base, base + kHidden, base + 2 * kHidden, base + 3 * kHidden,
+                                              base + 4 * kHidden, base + 5 * kHidden, base + 6 * kHidden,
+                                              base + 7 * kHidden};
+            float p8[8] = {};
+            if (ok) ok = tok_gather<8>(words, tag, p8, 0xffu, a.stall, spins);
+            const float part = ((p8[0] + p8[1]) + (p8[2] + p8[3])) + ((p8[4] + p8[5]) + (p8[6] + p8[7]));
+            const float other = xor_lanes<1>(part);
+            const float lo = half ? other : part, hi = half ? part : other;
+            const float xm = m.x[row] + (lo + hi);
+            if (half == 0) exchange_put(W + kTokXmOffset + g * kHidden + row, xm, tag);
+        }
+        {
+            float x0 = 0.f, x1 = 0.f;
+            if (ok) ok = tok_get2(W + kTokXmOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
+            m.xm[2 * tid] = x0;
+            m.xm[2 * tid + 1] = x1;
+        }
+        barrier();  // B8
+
+        // ---- FFN block (engine/core.cpp:627-641) ----
+        if (tid < 256) {
+            const float4 f = *reinterpret_cast<const float4*>(&m.xm[4 * tid]);
+            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+            double part = 0.0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float square = v[k] * v[k];
+                part += static_cast<double>(square);
+            }
+            part = wave_sum(part);
+            if (lane == 0) m.red[wave] = part;
+        }
+        barrier();  // B9
+        if (tid < 256) {
+            double total = 0.0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) total += m.red[i];
+            const float sum = static_cast<float>(total);
+            const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(kHidden) + 1e-6f);
+            float* xs = reinterpret_cast<float*>(m.xs4);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xs[xperm(4 * tid + k)] = (v[k] * inv) * m.npost[4 * tid + k];
+        }
+        barrier();  // B10
+
+        // Gate/up tile 96 g + 3 s + w (waves 0-2; rows 0-3 gate, 4-7 up),
+        // SwiGLU (engine/core.cpp:636-639), the XCD's 384 activations
+        // exchanged.
+        if (wave < 3) {
+            const float y = combine_chains(
+                lds_chain<16>(reinterpret_cast<const u32x4*>(m.wgu + 16384 * wave) + lane, m.xs4 + 2 * c));
+            const float up = __shfl(y, (lane + 32) & 63);
+            if (lane < 32 && c == 0) {
+                const float gate = y;
+                const float half_gate = gate * 0.5f;
+                const float t = tanhf(half_gate);
+                exchange_put(W + kTokActOffset + 4 * gu_tile + (lane >> 3), gate * (0.5f + 0.5f * t) * up, tag);
+            }
+        }
+        if (tid < kFfnSlice / 2) {
+            float a0 = 0.f, a1 = 0.f;
+            if (ok) ok = tok_get2(W + kTokActOffset + kFfnSlice * g + 2 * tid, tag, a0, a1, a.stall, spins);
+            float* as = reinterpret_cast<float*>(m.as4);
+            as[xperm(2 * tid)] = a0;
+            as[xperm(2 * tid + 1)] = a1;
+        }
+        barrier();  // B11
+
+        // Down tile 4 s + w (waves 0-3) over the slice's 384 columns; the
+        // rows go to the fold across XCDs.
+        if (wave < 4) {
+            const float y = combine_chains(
+                lds_chain<6>(reinterpret_cast<const u32x4*>(m.wdn + 6144 * wave) + lane, m.as4 + 2 * c));
+            if (c == 0)
+                exchange_put_through(W + kTokDCrossOffset + size_t(g) * kHidden + 8 * down_tile + (lane >> 3), y, tag);
+        }
+        barrier();  // B12
+
+        // Fold 2: rows 32 s .. + 31 of xm + the 8 down slices (the tree of
+        // the two-kernel path), posted inside the XCD; every thread gathers
+        // two entries of the next layer's residual.
+        if (wave == 0 && lane < 32) {
+            const int row = 32 * s + lane;
+            const uint64_t* base = W + kTokDCrossOffset + row;
+            const uint64_t* const words[8] = {base, base + kHidden, base + 2 * kHidden, base + 3 * kHidden,
+                                              base + 4 * kHidden, base + 5 * kHidden, base + 6 * kHidden,
+                                              base + 7 * kHidden};
+            float d8[8] = {};
+            if (ok) ok = tok_gather<8>(words, tag, d8, 0xffu, a.stall, spins);
+            exchange_put(W + kTokXOffset + g * kHidden + row, fold_slices(m.xm[row], d8), tag);
+        }
+        {
+            float x0 = 0.f, x1 = 0.f;
+            if (ok) ok = tok_get2(W + kTokXOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
+            m.x[2 * tid] = x0;
+            m.x[2 * tid + 1] = x1;
+        }
+        barrier();  // B13
+    }
+
+    if (blockIdx.x == 0) {
+        a.x_out[2 * tid] = m.x[2 * tid];
+        a.x_out[2 * tid + 1] = m.x[2 * tid + 1];
+    }
+}
+
+}  // namespace
+
+void launch_token_layers(const TokenLaunch& t, hipStream_t stream) {
+    require(t.layer_count >= 1 && t.layer_count <= kLayers, "token kernel: bad layer table");
+    require(t.pos >= 0 && t.pos < t.context && t.context <= kMaxContext, "token kernel: position outside the cache");
+    require(t.token >= 0 && t.token < kVocab, "token kernel: token out of range");
+    require(t.tag != 0 && uint64_t(t.tag) + uint64_t(t.layer_count) - 1 <= 0xFFFFFFFFull,
+            "token kernel: tags must be nonzero and not wrap");
+    require(t.spins >= 1, "token kernel: poll limit must be positive");
+    const int passes = (t.pos + 1 + 63) / 64;
+    auto go = [&](auto kernel) { kernel<<<256, kTokenThreads, 0, stream>>>(t); };
+    switch (passes <= 4 ? passes : 0) {
+        case 1: go(token_kernel<1, true>); break;
+        case 2: go(token_kernel<2, true>); break;
+        case 3: go(token_kernel<3, true>); break;
+        case 4: go(token_kernel<4, true>); break;
+        default:
+            if (passes > 32) go(token_kernel<2, false>);
+            else go(token_kernel<1, false>);
+    }
+}
+
+}  // namespace qwen_hip

@@ -109,6 +109,30 @@ def test_fused_kernels_match_separate_kernels(qpkg, pack0, gpu_model, monkeypatc
 
 
 @pytest.mark.gpu
+def test_token_kernel_equals_two_kernel_path(qpkg, pack0, gpu_model, monkeypatch):
+    """The one-launch step (all 28 layers in one persistent kernel, weights
+    streamed into LDS a layer ahead, residual folds across XCDs inside the
+    launch) against the two fused kernels per layer it replaces
+    (QWEN_HIP_TOKEN_KERNEL=0): the same dots, norms, folds and attention
+    order, so the logits of every step must be bit-identical. Contexts cover
+    the FULL attention form with 1, 2, 3 and 4 passes and the split form with
+    one and two passes per workgroup."""
+    monkeypatch.setenv('QWEN_HIP_TOKEN_KERNEL', '0')
+    plain = qpkg.Model(pack0, context=4096)
+    monkeypatch.delenv('QWEN_HIP_TOKEN_KERNEL')
+    try:
+        for length in (20, 85, 150, 200, 300, 2100, 3000):
+            prompt = (PROMPTS['decode_85'] if length <= 85 else PROMPTS['long_3968'])[:length]
+            fused_rows = greedy_trajectory(gpu_model, prompt, 3)
+            plain_rows = greedy_trajectory(plain, prompt, 3)
+            for (lt, tt), (lp, tp) in zip(fused_rows, plain_rows):
+                assert tt == tp
+                assert np.array_equal(lt.view(np.uint32), lp.view(np.uint32)), length
+    finally:
+        plain.close()
+
+
+@pytest.mark.gpu
 def test_models_stepped_from_two_threads(qpkg, pack0):
     """Two independent models (own weights, caches and streams) decoding at
     the same time from two host threads: the library runs their decode
