@@ -48,6 +48,7 @@ SIGNATURES = {
     'qwen_gpu_logits': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_c_float_p), _c_size_p]),
     'qwen_gpu_hidden': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(_c_float_p), _c_size_p]),
     'qwen_gpu_position': (ctypes.c_int, [ctypes.c_void_p]),
+    'qwen_gpu_decode_kernels': (ctypes.c_int, [ctypes.c_void_p]),
     'qwen_gpu_lossless_bf16_cache_bytes': (ctypes.c_size_t, [ctypes.c_void_p]),
     'qwen_gpu_get_options': (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Options)]),
     'qwen_gpu_greedy': (ctypes.c_int, [ctypes.c_void_p, _c_int_p]),
@@ -207,6 +208,10 @@ class Model:
         data, count = _c_float_p(), ctypes.c_size_t()
         _check(_LIB.qwen_gpu_hidden(self._handle, ctypes.byref(data), ctypes.byref(count)))
         return np.ctypeslib.as_array(data, (count.value,)).copy()
+
+    def decode_kernels(self):
+        """2: one launch per token, 1: two fused launches per layer, 0: separate kernels."""
+        return _LIB.qwen_gpu_decode_kernels(self._handle)
 
     def position(self):
         return _LIB.qwen_gpu_position(self._handle)

@@ -190,6 +190,10 @@ int qwen_gpu_hidden(qwen_gpu_model* m, const float** data, size_t* count) {
     });
 }
 
+int qwen_gpu_decode_kernels(const qwen_gpu_model* model) {
+    return model ? model->engine.decode_kernels() : -1;
+}
+
 int qwen_gpu_position(const qwen_gpu_model* m) { return m ? m->engine.position() : 0; }
 
 size_t qwen_gpu_lossless_bf16_cache_bytes(const qwen_gpu_model*) { return 0; }

@@ -36,6 +36,51 @@ static std::mutex& launch_lock() {
     return lock;
 }
 
+// The decode kernels that exchange values between the workgroups of one
+// launch assume what the dispatcher does on this chip: 256 CUs, and the
+// workgroups of a launch dealt round-robin to the 8 XCDs, so that all
+// workgroups w with the same w % 8 share one XCD (and its L2) and the 8
+// residues sit on 8 different XCDs. A probe launch records each workgroup's
+// XCD (HW_REG_XCC_ID) once per process; if the mapping or the CU count
+// differs, the engine runs the separate kernels (no exchanges inside a
+// launch) and refuses the batched step.
+__global__ void placement_probe_kernel(unsigned* xcc) {
+    if (threadIdx.x == 0) {
+        unsigned v;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+        xcc[blockIdx.x] = v & 15u;
+    }
+}
+
+static bool probe_placement() {
+    hipDeviceProp_t prop{};
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess || prop.multiProcessorCount != 256) return false;
+    unsigned* d = nullptr;
+    if (hipMalloc(&d, 256 * sizeof(unsigned)) != hipSuccess) return false;
+    unsigned h[256] = {};
+    placement_probe_kernel<<<256, 64>>>(d);
+    const bool ran = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+                     hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(d);
+    if (!ran) return false;
+    unsigned seen = 0;
+    for (int r = 0; r < 8; ++r) {
+        for (int w = r; w < 256; w += 8)
+            if (h[w] != h[r]) return false;
+        if (seen & (1u << h[r])) return false;
+        seen |= 1u << h[r];
+    }
+    return true;
+}
+
+bool placement_ok() {
+    static const bool ok = [] {
+        const char* env = std::getenv("QWEN_HIP_ASSUME_NO_PLACEMENT");  // tests: act as if the probe failed
+        return !(env && std::string(env) != "0") && probe_placement();
+    }();
+    return ok;
+}
+
 template <class T>
 T* Engine::device_alloc(size_t count) {
     void* p = nullptr;
@@ -258,6 +303,7 @@ void Engine::init_state() {
     if (const char* env = std::getenv("QWEN_HIP_TOKEN_PREFETCH")) token_prefetch_ = std::string(env) != "0";
     if (const char* env = std::getenv("QWEN_HIP_TEST_WITHHOLD")) token_withhold_ = std::atoi(env);
     if (const char* env = std::getenv("QWEN_HIP_TEST_SPINS")) token_spins_ = unsigned(std::max(1, std::atoi(env)));
+    if (!placement_ok()) fused_ffn_ = fused_attn_ = false;
     token_kernel_ = token_kernel_ && fused_ffn_ && fused_attn_;
     renew_content();
 
@@ -428,6 +474,7 @@ void Engine::run_token(int token, bool head, int result_slot) {
         t.tag = reserve_tags(kLayers);
         t.spins = token_spins_;
         t.withhold = token_withhold_;
+        token_withhold_ = -1;  // the test knob withholds one post, once
         t.prefetch = token_prefetch_ ? 1 : 0;
         launch_token_layers(t, stream_);
         if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
@@ -557,6 +604,7 @@ void Engine::copy_prefix(const Engine& src, int positions) {
 // Validates every sequence before running any (as append does for one).
 void Engine::step_batch(Engine* const* seqs, const int* tokens, int count) {
     require(count >= 1 && count <= kMaxBatch, "Batch must hold 1..8 sequences");
+    require(placement_ok(), "Batched decode needs 256 CUs with workgroups dealt round-robin over 8 XCDs");
     for (int i = 0; i < count; ++i) {
         require(seqs[i] != nullptr, "Null sequence in batch");
         for (int j = 0; j < i; ++j) require(seqs[j] != seqs[i], "Sequence repeated in batch");

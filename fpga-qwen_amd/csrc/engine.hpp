@@ -38,6 +38,11 @@ struct Weights {
     float* sines = nullptr;
 };
 
+// True when the dispatcher deals a launch's workgroups round-robin over the
+// 8 XCDs of a 256-CU device (probed once per process), which the decode
+// kernels that exchange values inside a launch rely on.
+bool placement_ok();
+
 class Engine {
 public:
     Engine(const std::string& weights, Options options);
@@ -64,6 +69,9 @@ public:
     const float* logits();
     const float* hidden();
     int position() const { return pos_; }
+    // 2: one persistent launch per token, 1: two fused launches per layer,
+    // 0: separate kernels.
+    int decode_kernels() const { return token_kernel_ ? 2 : (fused_ffn_ && fused_attn_) ? 1 : 0; }
     // Device greedy selection of the current logits (engine/main.cpp:51-59).
     int greedy();
     // Greedy selections of the pending verification rows.
@@ -146,7 +154,7 @@ private:
     // A single-row step runs its 28 layers as one persistent launch
     // (launch_token_layers) unless QWEN_HIP_TOKEN_KERNEL=0 (or either fused
     // kernel is switched off): exchange words, poll limit and the test-only
-    // withheld post (QWEN_HIP_TEST_WITHHOLD / _SPINS).
+    // withheld post of the next launch (QWEN_HIP_TEST_WITHHOLD / _SPINS).
     bool token_kernel_ = true;
     uint64_t* token_words_ = nullptr;
     unsigned token_spins_ = kTokenSpins;

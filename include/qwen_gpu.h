@@ -110,6 +110,11 @@ int qwen_gpu_hidden(qwen_gpu_model* model, const float** data, size_t* count);
 int qwen_gpu_position(const qwen_gpu_model* model);
 /* Model::lossless_bf16_cache_bytes(), engine/core.hpp:53; always 0 (engine/core.cpp:759). */
 size_t qwen_gpu_lossless_bf16_cache_bytes(const qwen_gpu_model* model);
+/* Which batch-1 decode kernels the model runs (no reference counterpart;
+ * for tests and benchmarks): 2 one persistent launch per token, 1 two fused
+ * launches per layer, 0 separate kernels (no exchanges inside a launch, as
+ * when the device does not deal workgroups round-robin over 8 XCDs). */
+int qwen_gpu_decode_kernels(const qwen_gpu_model* model);
 /* Options actually in effect (echoed by the protocol handshake, engine/main.cpp:71-79). */
 int qwen_gpu_get_options(const qwen_gpu_model* model, qwen_gpu_options* options);
 

@@ -121,6 +121,7 @@ def test_token_kernel_equals_two_kernel_path(qpkg, pack0, gpu_model, monkeypatch
     plain = qpkg.Model(pack0, context=4096)
     monkeypatch.delenv('QWEN_HIP_TOKEN_KERNEL')
     try:
+        assert gpu_model.decode_kernels() == 2 and plain.decode_kernels() == 1
         for length in (20, 85, 150, 200, 300, 2100, 3000):
             prompt = (PROMPTS['decode_85'] if length <= 85 else PROMPTS['long_3968'])[:length]
             fused_rows = greedy_trajectory(gpu_model, prompt, 3)
@@ -130,6 +131,83 @@ def test_token_kernel_equals_two_kernel_path(qpkg, pack0, gpu_model, monkeypatch
                 assert np.array_equal(lt.view(np.uint32), lp.view(np.uint32)), length
     finally:
         plain.close()
+
+
+@pytest.mark.gpu
+def test_stalled_step_is_reported_and_rolled_back(qpkg, pack0, monkeypatch):
+    """A decode launch whose exchange cannot complete fails cleanly instead
+    of hanging. A test-only knob makes workgroup 5 withhold its q/k/v rows in
+    layer 0 of the next launch, and a short poll limit (2048 rounds) makes
+    the workgroups waiting for them give up; their give-up raises the step's
+    stall word, which ends every other workgroup's polls, so the launch
+    exits. The step raises 'Decode step stalled' and leaves the model at its
+    position before the call, without logits; the next step (the knob acts
+    once) is bit-identical to the same step on a clean model, and so are the
+    steps after it (engine/core.cpp:740; engine/main.cpp:190-193)."""
+    monkeypatch.setenv('QWEN_HIP_TEST_WITHHOLD', '5')
+    monkeypatch.setenv('QWEN_HIP_TEST_SPINS', '2048')
+    m = qpkg.Model(pack0, context=512)
+    monkeypatch.delenv('QWEN_HIP_TEST_WITHHOLD')
+    monkeypatch.delenv('QWEN_HIP_TEST_SPINS')
+    clean = qpkg.Model(pack0, context=512)
+    try:
+        assert m.decode_kernels() == 2
+        prompt = PROMPTS['decode_85'][:40]
+        m.prefill(prompt)
+        clean.prefill(prompt)
+        token = clean.greedy()
+        with pytest.raises(RuntimeError, match='Decode step stalled'):
+            m.step(token)
+        assert m.position() == 40 and m.logits().size == 0
+        for _ in range(3):
+            m.step(token)
+            clean.step(token)
+            assert np.array_equal(m.logits().view(np.uint32), clean.logits().view(np.uint32))
+            token = clean.greedy()
+    finally:
+        m.close()
+        clean.close()
+
+
+@pytest.mark.gpu
+def test_separate_kernels_when_placement_cannot_be_assumed(qpkg, pack0, gpu_model, tmp_path):
+    """When the placement probe fails (forced here in a fresh process) the
+    engine runs the separate kernels, which exchange nothing inside a launch:
+    the same greedy tokens and logits within 1e-4 of the one-launch step, and
+    the batched step, which needs the placement, is refused."""
+    import os
+    import subprocess
+    import sys
+    out = tmp_path / 'logits.npy'
+    code = f"""
+import sys, numpy as np
+sys.path.insert(0, {str(Path(__file__).parent)!r})
+from conftest import load_package
+q = load_package()
+m = q.Model({str(pack0)!r}, context=512)
+assert m.decode_kernels() == 0, m.decode_kernels()
+m.prefill({PROMPTS['decode_85'][:60]!r})
+rows = [m.logits()]
+for _ in range(3):
+    m.step(m.greedy())
+    rows.append(m.logits())
+np.save({str(out)!r}, np.stack(rows))
+b = m.share()
+try:
+    q.step_batch([m, b], [1, 2])
+except RuntimeError as error:
+    assert 'round-robin' in str(error), error
+else:
+    raise AssertionError('batched step ran without the placement')
+print('separate kernels ok', flush=True)
+"""
+    env = {**os.environ, 'QWEN_HIP_ASSUME_NO_PLACEMENT': '1'}
+    subprocess.run([sys.executable, '-c', code], env=env, check=True, timeout=300)
+    separate = np.load(out)
+    rows = greedy_trajectory(gpu_model, PROMPTS['decode_85'][:60], 4)
+    for (logits, _), other in zip(rows, separate):
+        assert int(np.argmax(logits)) == int(np.argmax(other))
+        assert float(np.max(np.abs(logits - other))) <= 1e-4
 
 
 @pytest.mark.gpu
