@@ -2495,112 +2495,6 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
     }
 }
 
-bool pair_supported(int pos) { return attn_fused(pos + 2) || !attn_fused(pos + 1); }
-
-// The pair's QKV (shared weight loads) and attention kernels (fused for both
-// rows, or split + merge/O per row).
-static void launch_pair_qkv_attention(const LayerDevice& L, const uint16_t* embed, int pos, const int (&tokens)[2],
-                               const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                               const PairScratch& pr, LayerFlow flow, hipStream_t stream) {
-    require(pair_supported(pos) && pos >= 0 && pos + 2 <= context, "verification pair: unsupported position");
-    const bool fused = attn_fused(pos + 2);
-    GemvArgs q{};
-    q.w = L.qkv_t;
-    q.in = pr.x;
-    q.norm_w = L.in_norm;
-    q.embed = embed;
-    q.token[0] = tokens[0];
-    q.token[1] = tokens[1];
-    q.out = pr.qkv;
-    q.out_stride = kQKVRows;
-    q.x = pr.x;
-    if (flow.fold_input && !embed) {
-        q.in = pr.xm;
-        q.parts = pr.dparts;
-    }
-    launch_gemv_pair<kHidden, kQKV>(q, kQKVRows, stream);
-
-    AttnArgs at{};
-    at.qkv = pr.qkv;
-    at.q_norm = L.q_norm;
-    at.k_norm = L.k_norm;
-    at.cosines = cosines;
-    at.sines = sines;
-    at.keys = L.keys;
-    at.values = L.values;
-    at.pos = pos;
-    at.partial = s.attn_partial;
-    at.context = context;
-    at.scale = 1.0f / std::sqrt(128.0f);
-    at.o_n = L.o_n;
-    at.o_part = pr.o_part;
-    if (fused) {
-        switch ((pos + 2 + 63) / 64) {  // passes of 64 positions over n = pos + 2
-            case 1: attn_o_kernel<1, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            case 2: attn_o_kernel<2, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            case 3: attn_o_kernel<3, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            case 4: attn_o_kernel<4, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            case 5: attn_o_kernel<5, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            case 6: attn_o_kernel<6, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            case 7: attn_o_kernel<7, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            case 8: attn_o_kernel<8, 2><<<kAttnOGroups, 512, 0, stream>>>(at); break;
-            default: throw std::runtime_error("fused attention: context beyond 512 positions");
-        }
-    } else {
-        // Both rows past the fused range: the single-row split and merge + O
-        // kernels, row 0 first (it writes the K/V row that row 1 reads from
-        // the cache).
-        for (int row = 0; row < 2; ++row) {
-            AttnArgs ar = at;
-            ar.qkv = pr.qkv + row * kQKVRows;
-            ar.pos = pos + row;
-            ar.o_part = pr.o_part + size_t(row) * kOParts * kHidden;
-            int chunk, splits;
-            attn_split(ar.pos + 1, chunk, splits);
-            attn_decode_kernel<<<dim3(splits, kKVHeads), 512, 0, stream>>>(ar);
-            attn_merge_o_kernel<<<kAttnOGroups, 512, 0, stream>>>(ar);
-        }
-    }
-}
-
-void launch_decode_layer_pair(const LayerDevice& L, const uint16_t* embed, int pos, const int (&tokens)[2],
-                              const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                              const PairScratch& pr, LayerFlow flow, hipStream_t stream) {
-    if (flow.attn_tag) {
-        // Each row through the fused QKV + attention kernel at its position
-        // (row 0 first: it writes the K/V row that row 1 reads), then the
-        // FFN for both rows with shared weight loads.
-        require(pos >= 0 && pos + 2 <= context, "verification pair: unsupported position");
-        const bool fold = flow.fold_input && !embed;
-        for (int row = 0; row < 2; ++row)
-            launch_qkv_attn(L, embed, tokens[row], pos + row, cosines, sines, context, pr.x + row * kHidden,
-                            pr.xm + row * kHidden, fold ? pr.dparts + size_t(row) * kFfnSlices * kHidden : nullptr,
-                            pr.o_part + size_t(row) * kOParts * kHidden, s, row ? flow.attn_tag2 : flow.attn_tag,
-                            stream);
-    } else {
-        launch_pair_qkv_attention(L, embed, pos, tokens, cosines, sines, context, s, pr, flow, stream);
-    }
-    if (flow.ffn_tag) {
-        launch_ffn<2>(L, pr.x, pr.o_part, pr.xm, pr.dparts, pr.exchange, s.stall, flow.ffn_tag, stream);
-        return;
-    }
-    GemvArgs gu{};
-    gu.w = L.gateup_t;
-    gu.in = pr.x;
-    gu.norm_w = L.post_norm;
-    gu.parts = pr.o_part;
-    gu.out = pr.act;
-    gu.out_stride = kFFN;
-    launch_gemv_pair<kHidden, kGateUp>(gu, 2 * kFFN, stream);
-
-    GemvArgs d{};
-    d.w = L.down_t;
-    d.in = pr.act;
-    d.parts = pr.o_part;
-    d.x = pr.x;
-    launch_gemv_pair<kFFN, kDown>(d, kHidden, stream);
-}
-
 void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
                          const PairScratch& pr, ArgmaxResult* host_out, hipStream_t stream) {
     GemvArgs a{};

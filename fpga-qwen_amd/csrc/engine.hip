@@ -283,16 +283,10 @@ void Engine::init_state() {
     base_logits_ = device_alloc<float>(kVocab);
     base_hidden_ = device_alloc<float>(kHidden);
     pair_.x = device_alloc<float>(2 * kHidden);
-    pair_.qkv = device_alloc<float>(2 * kQKVRows);
-    pair_.act = device_alloc<float>(2 * kFFN);
-    pair_.o_part = device_alloc<float>(size_t(2) * kOParts * kHidden);
     pair_.logits = ver_logits_;
     pair_.hidden = ver_hidden_;
     pair_.result = device_alloc<ArgmaxResult>(2);
-    pair_.xm = device_alloc<float>(2 * kHidden);
-    pair_.dparts = device_alloc<float>(size_t(2) * kFfnSlices * kHidden);
-    pair_.exchange = device_alloc<uint64_t>(2 * kFFN);
-    token_words_ = device_alloc<uint64_t>(kTokWords);
+    token_words_ = device_alloc<uint64_t>(2 * size_t(kTokWords));  // a block per verification row
     HIP_CHECK(hipMemsetAsync(s.stall, 0, sizeof(int), stream_));
     clear_exchanges();
 
@@ -418,7 +412,6 @@ uint32_t Engine::next_tag() {
 // Exchange words start with tag 0, which no launch uses.
 void Engine::clear_exchanges() {
     HIP_CHECK(hipMemsetAsync(scratch_.exchange, 0, kFFN * sizeof(uint64_t), stream_));
-    HIP_CHECK(hipMemsetAsync(pair_.exchange, 0, 2 * kFFN * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.bexchange, 0, kBatchExchangeWords * sizeof(uint64_t), stream_));
@@ -435,13 +428,10 @@ uint32_t Engine::reserve_tags(int count) {
     return first;
 }
 
-LayerFlow Engine::layer_flow(int layer, bool pair) {
+LayerFlow Engine::layer_flow(int layer) {
     LayerFlow f{};
     f.fold_input = fused_ffn_ && layer > 0;
-    if (fused_attn_) {
-        f.attn_tag = next_tag();
-        if (pair) f.attn_tag2 = next_tag();
-    }
+    if (fused_attn_) f.attn_tag = next_tag();
     if (fused_ffn_) f.ffn_tag = next_tag();
     return f;
 }
@@ -462,7 +452,8 @@ void Engine::run_token(int token, bool head, int result_slot) {
         }
         t.layer_count = kLayers;
         t.embed = embed_;
-        t.token = token;
+        t.token[0] = token;
+        t.rows = 1;
         t.pos = pos_;
         t.context = options_.context;
         t.cosines = cosines_;
@@ -671,14 +662,34 @@ int Engine::greedy() {
     return result_host_[0].token;
 }
 
-// Both verification rows through the 28 layers and the head in one pass
-// over the weights; K/V rows written at pos_ and pos_ + 1, pos_ unchanged.
+// Both verification rows through the 28 layers in one launch that reads
+// every weight once for both (the token kernel's two-row form: row 1 attends
+// to row 0's new K/V, each row with a single step's arithmetic), then the
+// head for both; K/V rows written at pos_ and pos_ + 1, pos_ unchanged.
 void Engine::run_pair(int first, int second) {
-    const int tokens[2] = {first, second};
-    for (int l = 0; l < kLayers; ++l)
-        launch_decode_layer_pair(layers_[l], l == 0 ? embed_ : nullptr, pos_, tokens, cosines_, sines_,
-                                 options_.context, scratch_, pair_, layer_flow(l, true), stream_);
-    if (fused_ffn_) launch_fold_residual(pair_.xm, pair_.dparts, pair_.x, 2, stream_);
+    TokenLaunch t{};
+    for (int l = 0; l < kLayers; ++l) {
+        const LayerDevice& L = layers_[l];
+        t.layers[l] = TokenLayer{L.qkv_t, L.o_n, L.gateup_t, L.down_t, L.in_norm, L.post_norm, L.qk_norm, L.keys};
+    }
+    t.layer_count = kLayers;
+    t.embed = embed_;
+    t.token[0] = first;
+    t.token[1] = second;
+    t.rows = 2;
+    t.pos = pos_;
+    t.context = options_.context;
+    t.cosines = cosines_;
+    t.sines = sines_;
+    t.x_out = pair_.x;
+    t.words = token_words_;
+    t.stall = scratch_.stall;
+    t.scale = 1.0f / std::sqrt(128.0f);
+    t.tag = reserve_tags(kLayers);
+    t.spins = token_spins_;
+    t.withhold = -1;
+    t.prefetch = token_prefetch_ ? 1 : 0;
+    launch_token_layers(t, stream_);
     launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, stream_);
     HIP_CHECK(hipGetLastError());
 }
@@ -692,11 +703,13 @@ void Engine::verify_two(int first, int second) {
     const int start = pos_;
     std::lock_guard<std::mutex> hold(launch_lock());
     try {
-        if (fused_attn_ || pair_supported(start)) {
+        if (token_kernel_ && token_pair_supported(start)) {
             run_pair(first, second);
         } else {
-            // The two positions straddle the fused-attention limit: two single
-            // steps, with the public logits saved and restored around them.
+            // Without the token kernel, or where the two rows would take
+            // different attention forms (256 and 257 cached positions): two
+            // single steps, with the public logits saved and restored around
+            // them.
             if (has_logits_) {
                 HIP_CHECK(hipMemcpyAsync(base_logits_, scratch_.logits, size_t(kVocab) * 4,
                                          hipMemcpyDeviceToDevice, stream_));

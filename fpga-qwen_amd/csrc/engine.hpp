@@ -58,8 +58,10 @@ public:
     void prefill(const int* ids, size_t count);
     void step(int token);
     // Two consumed ids with B1 arithmetic; rows stay pending until commit.
-    // Both rows run as one pass over the weights when the two positions take
-    // the same attention path (pair_supported), else as two single steps.
+    // Both rows run as one launch that reads every weight once for both
+    // (the token kernel's two-row form) unless the two positions take
+    // different attention forms or the token kernel is off; then as two
+    // single steps.
     void verify_two(int first, int second);
     // Host copies of the pending rows ([2 x vocab] logits, [2 x 1024]
     // hidden), copied on first access, and the base position.
@@ -105,7 +107,7 @@ private:
     void roll_back(int position);
     void run_token(int token, bool head, int result_slot);
     void run_pair(int first, int second);
-    LayerFlow layer_flow(int layer, bool pair = false);
+    LayerFlow layer_flow(int layer);
     uint32_t next_tag();
     // `count` consecutive tags (none of them 0) for one launch.
     uint32_t reserve_tags(int count);

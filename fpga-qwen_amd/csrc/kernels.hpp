@@ -170,13 +170,11 @@ void launch_gemv_plain(const uint16_t* w_t, const float* x, float* y, int rows, 
 // after the last layer the caller folds s.xm and the slices into s.x);
 // 0: the norm+gate/up and down kernels.
 // attn_tag != 0: norm + QKV + attention + O run as one kernel with that
-// tag (pairs: attn_tag for row 0, attn_tag2 for row 1); 0: the QKV and
-// attention kernels.
+// tag; 0: the QKV and attention kernels.
 struct LayerFlow {
     bool fold_input;
     uint32_t ffn_tag;
     uint32_t attn_tag;
-    uint32_t attn_tag2;
 };
 
 void launch_decode_layer(const LayerDevice& layer, const uint16_t* embed, int pos, int token,
@@ -195,30 +193,11 @@ void launch_layer_kernel(int which, const LayerDevice& layer, const uint16_t* em
 
 // Buffers of a two-token verification (rows at positions pos and pos + 1).
 struct PairScratch {
-    float* x;             // [2][1024] residual streams
-    float* qkv;           // [2][4096]
-    float* act;           // [2][3072]
-    float* o_part;        // [2][16][1024]
+    float* x;             // [2][1024] residual streams after the last layer
     float* logits;        // [2][151936]
     float* hidden;        // [2][1024]
     ArgmaxResult* result; // [2] device copies of the selections
-    float* xm;            // [2][1024]
-    float* dparts;        // [2][8][1024]
-    uint64_t* exchange;   // [2][3072]
 };
-
-// True when the steps at pos and pos + 1 take the same attention path
-// (both fused or both split), which the pair launch requires.
-bool pair_supported(int pos);
-
-// Verification (engine/core.cpp:729-741): one decode layer for the steps at
-// positions pos and pos + 1 with tokens[0], tokens[1], every weight matrix
-// read once for both rows; each row gets the arithmetic of
-// launch_decode_layer at its position, so results are bit-identical to two
-// single steps. Writes K/V at pos and pos + 1.
-void launch_decode_layer_pair(const LayerDevice& layer, const uint16_t* embed, int pos, const int (&tokens)[2],
-                              const float* cosines, const float* sines, int context, const DecodeScratch& s,
-                              const PairScratch& pair, LayerFlow flow, hipStream_t stream);
 
 // Final norm + lm_head + greedy argmax of both verification rows (uses the
 // lm partial buffers of s); selections to pair.result and host_out[0..1].

@@ -36,6 +36,7 @@
 
 #include <cfloat>
 #include <cmath>
+#include <type_traits>
 
 #include "decode_dev.hpp"
 #include "token.hpp"
@@ -174,77 +175,105 @@ __device__ __forceinline__ int qkv_tile(int g, int li) {
     return li < 32 ? 32 * g + li : li < 48 ? 256 + 16 * g + (li - 32) : 384 + 16 * g + (li - 48);
 }
 
+// LDS of a workgroup. Weight regions (bytes): one row: QKV, O, gate/up,
+// down; two rows (verification): O shares the down region (O rows are used
+// before the down tiles are loaded, and the next layer's O rows are loaded
+// after them), which leaves room for the second row's state.
+template <int ROWS>
 struct Lds {
-    unsigned char wq[kRegQkv];
-    unsigned char wo[kRegO];
-    unsigned char wgu[kRegGu];
-    unsigned char wdn[kRegDown];
-    float nin[kHidden];      // input RMSNorm weights
-    float npost[kHidden];    // post-attention RMSNorm weights
+    static constexpr int kQkvAt = 0;
+    static constexpr int kGuAt = kQkvAt + kRegQkv;
+    static constexpr int kDownAt = kGuAt + kRegGu;
+    static constexpr int kOAt = ROWS == 1 ? kDownAt + kRegDown : kDownAt;
+    static constexpr int kWeights = ROWS == 1 ? kOAt + kRegO : kDownAt + kRegDown;
+    static_assert(kRegO <= kRegDown, "O rows fit the down region");
+    unsigned char w[kWeights];
+    float nin[kHidden];       // input RMSNorm weights
+    float npost[kHidden];     // post-attention RMSNorm weights
     float nqk[2 * kHeadDim];  // q norm, k norm
     unsigned char junk[1024];  // target of the K/V prefetch loads
-    float x[kHidden];        // residual the layer starts from
-    float xm[kHidden];       // residual after the attention block
-    float4 xs4[kHidden / 4];  // normalized input, chain-permuted
-    float4 as4[kFfnSlice / 4];  // this XCD's activations, chain-permuted
-    double red[4];
-    float qp[2][128];
-    float prob[2][128];
-    float opart[8][2][128];
-    uint16_t kcur[128], vcur[128];
-    float wmax[8][2], wsum[8][2];
-    float gm[4], gl[4], go[4][128];
-    float att[128];
-    float rope[2][64];  // cos, sin of this position's 64 rotation pairs
+    float rope[ROWS][2][64];  // cos, sin of each row's position
+    // Per row. Buffers whose lifetimes do not overlap share storage: the
+    // attention partials (between the scores and the O rows) with the
+    // normalized input and the post-attention residual, the probabilities
+    // with the activations.
+    struct Row {
+        float x[kHidden];  // residual the layer starts from
+        union {
+            struct {
+                float4 xs4[kHidden / 4];  // normalized input, chain-permuted
+                float xm[kHidden];        // residual after the attention block
+            } n;
+            float opart[8][2][128];
+        } u;
+        union {
+            float4 as4[kFfnSlice / 4];  // this XCD's activations, chain-permuted
+            float prob[2][128];
+        } v;
+        double red[4];
+        float qp[2][128];
+        uint16_t kcur[128], vcur[128];
+        float wmax[8][2], wsum[8][2];
+        float gm[4], gl[4], go[4][128];
+        float att[128];
+    } r[ROWS];
+    __device__ unsigned char* wq() { return w + kQkvAt; }
+    __device__ unsigned char* wo() { return w + kOAt; }
+    __device__ unsigned char* wgu() { return w + kGuAt; }
+    __device__ unsigned char* wdn() { return w + kDownAt; }
 };
+static_assert(sizeof(Lds<1>) <= 163840 && sizeof(Lds<2>) <= 163840, "LDS of one workgroup per CU");
 
-// Load waves: one region's loads for layer `layer` (lw = load wave 0..3).
+// Load waves: one load of a region for layer `layer` (lw = load wave 0..3).
+template <int ROWS>
 struct Loader {
     const TokenLaunch& a;  // the kernel arguments (layer pointers read with scalar loads)
+    Lds<ROWS>& m;
     int g, s, lw, lane, context, pos;
 
     // Load i (0-9) of the QKV region: 8 tile blocks, a quarter of the input
     // norm weights, the QK norm weights.
-    __device__ void qkv(Lds& m, int layer, int i) const {
+    __device__ void qkv(int layer, int i) const {
         const TokenLayer& L = a.layers[layer];
         if (i < 8) {
             const int k = 8 * lw + i, t = k >> 4, b = k & 15;
             const int tile = qkv_tile(g, 2 * s + t);
-            dma16(L.qkv_t + (size_t(tile) * 16 + b) * 512 + 8 * lane, m.wq + 1024 * k);
+            dma16(L.qkv_t + (size_t(tile) * 16 + b) * 512 + 8 * lane, m.wq() + 1024 * k);
         } else if (i == 8) {
             dma16(L.in_norm + 256 * lw + 4 * lane, reinterpret_cast<unsigned char*>(m.nin) + 1024 * lw);
         } else {
             dma16(L.qk_norm + 4 * lane, m.nqk);
         }
     }
-    __device__ void o(Lds& m, int layer, int i) const {
+    __device__ void o(int layer, int i) const {
         const TokenLayer& L = a.layers[layer];
         const int h = 2 * g + (s & 1), rb = s >> 1;
         const int k = kLoadsO * lw + i, r = 4 * k + (lane >> 4), piece = lane & 15;
-        dma16(L.o_n + size_t(64 * rb + r) * kQDim + 128 * h + 8 * piece, m.wo + 1024 * k);
+        dma16(L.o_n + size_t(64 * rb + r) * kQDim + 128 * h + 8 * piece, m.wo() + 1024 * k);
     }
     // Load i (0-12) of the gate/up region: 12 tile blocks, a quarter of the
     // post-attention norm weights.
-    __device__ void gu(Lds& m, int layer, int i) const {
+    __device__ void gu(int layer, int i) const {
         const TokenLayer& L = a.layers[layer];
         if (i < 12) {
             const int k = 12 * lw + i;
-            dma16(L.gateup_t + (size_t(96 * g + 3 * s) * 16 + k) * 512 + 8 * lane, m.wgu + 1024 * k);
+            dma16(L.gateup_t + (size_t(96 * g + 3 * s) * 16 + k) * 512 + 8 * lane, m.wgu() + 1024 * k);
         } else {
             dma16(L.post_norm + 256 * lw + 4 * lane, reinterpret_cast<unsigned char*>(m.npost) + 1024 * lw);
         }
     }
-    __device__ void down(Lds& m, int layer, int b) const {
+    __device__ void down(int layer, int b) const {
         const TokenLayer& L = a.layers[layer];
         const int tile = 4 * s + lw;
-        dma16(L.down_t + (size_t(tile) * (kFFN / 64) + 6 * g + b) * 512 + 8 * lane, m.wdn + 1024 * (6 * lw + b));
+        dma16(L.down_t + (size_t(tile) * (kFFN / 64) + 6 * g + b) * 512 + 8 * lane,
+              m.wdn() + 1024 * (6 * lw + b));
     }
     // Lines of the K/V rows [0, pos) of head g in layer `layer`, a 1/32
     // share per workgroup of the XCD (128-byte lines, one lane each; lanes
     // past the rows read line 0), into L2 ahead of the compute waves' loads.
     // With `on` false the same load re-reads the QK norm weights into the
     // junk area (the waits count loads).
-    __device__ void prefetch(Lds& m, int layer, int i, bool on) const {
+    __device__ void prefetch(int layer, int i, bool on) const {
         const TokenLayer& L = a.layers[layer];
         if (!on) {
             dma16(L.qk_norm + 4 * lane, m.junk);
@@ -258,50 +287,131 @@ struct Loader {
         const size_t at = q < lines ? base + 64 * size_t(q) : q < 2 * lines ? kv + base + 64 * size_t(q - lines) : base;
         dma16(L.keys + at, m.junk);
     }
+    __device__ void qkv_range(int layer, int first, int count) const {
+        for (int i = first; i < first + count; ++i) qkv(layer, i);
+    }
+    __device__ void o_range(int layer, int first, int count) const {
+        for (int i = first; i < first + count; ++i) o(layer, i);
+    }
+    __device__ void gu_range(int layer, int first, int count) const {
+        for (int i = first; i < first + count; ++i) gu(layer, i);
+    }
+    __device__ void down_range(int layer, int first, int count) const {
+        for (int b = first; b < first + count; ++b) down(layer, b);
+    }
 };
 
+// The load plan of two rows, where O shares the down region: down(l) is
+// loaded after O(l) is used (B7), O(l + 1) after down(l) is used (B12). Per
+// layer l, per load wave:
+//   k = 0: gate/up(l) 0-4           k = 6: QKV(l + 1) 5-6
+//   k = 1: gate/up(l) 5-8           k = 7: down(l) 0-2
+//   k = 3: gate/up(l) 9-12,         k = 8: down(l) 3-5
+//          prefetch 0               k = 9: QKV(l + 1) 7-9
+//   k = 4: prefetch 1, QKV(l + 1)   k = 12: O(l + 1) 0-3
+//          0-2
+//   k = 5: QKV(l + 1) 3-4
+// At the start: QKV(0), then O(0). Waits (loads issued after the region):
+//   QKV(l) in interval 0: O(l), gate/up(l) 0-4                     = 9
+//   O(l) in interval 4: gate/up(l), prefetch, QKV(l + 1) 0-2       = 18
+//   gate/up(l) in interval 8: prefetch, QKV(l + 1) 0-6, down(l)    = 15
+//   down(l) in interval 10: QKV(l + 1) 7-9                         = 3
+constexpr int kPairAfterQkv = kLoadsO + 5;
+constexpr int kPairAfterO = kLoadsGu + kLoadsPrefetch + 3;
+constexpr int kPairAfterGu = kLoadsPrefetch + 7 + kLoadsDown;
+constexpr int kPairAfterDown = 3;
+static_assert(kPairAfterQkv == 9 && kPairAfterO == 18 && kPairAfterGu == 15, "wait counts of the two-row plan");
+
 // The chain dot of NB 16-byte LDS blocks (block b at w[64 b]) against the
-// permuted LDS vector (block b's 8 values at x4[16 b], x4[16 b + 1]) in the
-// reference's FMA order. The next two blocks are read while the chain steps
-// of the current two run, which bounds the registers the dot holds (about
-// 50 instead of the ~190 of all 16 blocks read up front).
-template <int NB>
-__device__ __forceinline__ float lds_chain(const u32x4* w, const float4* x4) {
+// permuted LDS vector of each row (block b's 8 values at x4[16 b],
+// x4[16 b + 1]) in the reference's FMA order; the rows share every weight
+// read. The next two blocks are read while the chain steps of the current
+// two run, which bounds the registers the dot holds (about 50 per row
+// instead of the ~190 of all 16 blocks read up front).
+template <int NB, int ROWS>
+__device__ __forceinline__ void lds_chain(const u32x4* w, const float4* const (&x4)[ROWS], float (&acc)[ROWS]) {
     static_assert(NB % 2 == 0, "pairs of blocks");
     u32x4 w0 = w[0], w1 = w[64];
-    float4 a0 = x4[0], b0 = x4[1], a1 = x4[16], b1 = x4[17];
-    float acc = 0.f;
+    float4 a0[ROWS], b0[ROWS], a1[ROWS], b1[ROWS];
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        a0[q] = x4[q][0];
+        b0[q] = x4[q][1];
+        a1[q] = x4[q][16];
+        b1[q] = x4[q][17];
+        acc[q] = 0.f;
+    }
 #pragma unroll
     for (int b = 0; b < NB; b += 2) {
         u32x4 nw0 = w0, nw1 = w1;
-        float4 na0 = a0, nb0 = b0, na1 = a1, nb1 = b1;
+        float4 na0[ROWS], nb0[ROWS], na1[ROWS], nb1[ROWS];
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            na0[q] = a0[q];
+            nb0[q] = b0[q];
+            na1[q] = a1[q];
+            nb1[q] = b1[q];
+        }
         if (b + 2 < NB) {
             nw0 = w[64 * (b + 2)];
             nw1 = w[64 * (b + 3)];
-            na0 = x4[16 * (b + 2)];
-            nb0 = x4[16 * (b + 2) + 1];
-            na1 = x4[16 * (b + 3)];
-            nb1 = x4[16 * (b + 3) + 1];
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                na0[q] = x4[q][16 * (b + 2)];
+                nb0[q] = x4[q][16 * (b + 2) + 1];
+                na1[q] = x4[q][16 * (b + 3)];
+                nb1[q] = x4[q][16 * (b + 3) + 1];
+            }
         }
-        acc = chain8(acc, w0, a0, b0);
-        acc = chain8(acc, w1, a1, b1);
-        w0 = nw0; w1 = nw1; a0 = na0; b0 = nb0; a1 = na1; b1 = nb1;
-        // Orders the chain steps before the next reads (a scheduling barrier
-        // alone leaves the arithmetic free to sink below every read).
-        asm volatile("" : "+v"(acc));
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            acc[q] = chain8(acc[q], w0, a0[q], b0[q]);
+            acc[q] = chain8(acc[q], w1, a1[q], b1[q]);
+        }
+        w0 = nw0;
+        w1 = nw1;
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            a0[q] = na0[q];
+            b0[q] = nb0[q];
+            a1[q] = na1[q];
+            b1[q] = nb1[q];
+            // Orders the chain steps before the next reads (a scheduling
+            // barrier alone leaves the arithmetic free to sink below every read).
+            asm volatile("" : "+v"(acc[q]));
+        }
     }
-    return acc;
+}
+
+// RMSNorm sums of one row (engine/core.cpp:207-215: FP32 squares summed in
+// FP64): thread tid < 256 holds entries 4 tid .. 4 tid + 3 in v; wave w's
+// sum goes to red[w].
+__device__ __forceinline__ void norm_sums(const float (&v)[4], double* red, int wave, int lane) {
+    double part = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float square = v[k] * v[k];
+        part += static_cast<double>(square);
+    }
+    part = wave_sum(part);
+    if (lane == 0) red[wave] = part;
 }
 
 // FULL (PASSES <= 4 passes of 64 positions, n <= 256): every workgroup
 // attends its query head over all positions; else the split form (passes s
-// and s + 32 of both heads, partials merged inside the XCD).
+// and s + 32 of both heads, partials merged inside the XCD). ROWS = 2: the
+// two rows of a verification at positions pos and pos + 1 (row 1 attends to
+// row 0's new K/V from LDS), every weight read once for both, each row with
+// the arithmetic of a single step; the attention form and pass count are
+// row 1's (extra passes add nothing to row 0: its positions past pos + 1
+// score -inf and weigh 0).
 //
 // The load waves and the compute waves run separate loops that pass the
 // same barriers, numbered B0 .. B13 below (the split form adds B6b).
-template <int PASSES, bool FULL>
+template <int PASSES, bool FULL, int ROWS>
 __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch a) {
-    __shared__ Lds m;
+    static_assert(ROWS == 1 || ROWS == 2, "one or two rows");
+    __shared__ Lds<ROWS> m;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = int(blockIdx.x & 7), s = int(blockIdx.x >> 3);
     const int L = a.layer_count;
@@ -311,88 +421,99 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         // executed by the whole wave (the waits count them), never a load
         // under a divergent branch.
         const int lw = __builtin_amdgcn_readfirstlane(wave - kComputeWaves);
-        const Loader ld{a, g, s, lw, lane, a.context, a.pos};
-        auto qkv = [&](int layer, int first, int count) {
-            for (int i = first; i < first + count; ++i) ld.qkv(m, layer, i);
-        };
-        auto o = [&](int layer, int first, int count) {
-            for (int i = first; i < first + count; ++i) ld.o(m, layer, i);
-        };
-        auto gu = [&](int layer, int first, int count) {
-            for (int i = first; i < first + count; ++i) ld.gu(m, layer, i);
-        };
+        const Loader<ROWS> ld{a, m, g, s, lw, lane, a.context, a.pos};
         const bool pf = a.prefetch != 0;
-        // QKV(0) and O(0) in the order of intervals 4-9 of a layer.
-        qkv(0, 0, 3);
-        qkv(0, 3, 2);
-        qkv(0, 5, 2);
-        o(0, 0, 3);
-        o(0, 3, 1);
-        qkv(0, 7, 3);
+        if constexpr (ROWS == 1) {
+            // QKV(0) and O(0) in the order of intervals 4-9 of a layer.
+            ld.qkv_range(0, 0, 3);
+            ld.qkv_range(0, 3, 2);
+            ld.qkv_range(0, 5, 2);
+            ld.o_range(0, 0, 3);
+            ld.o_range(0, 3, 1);
+            ld.qkv_range(0, 7, 3);
+        } else {
+            ld.qkv_range(0, 0, kLoadsQkv);
+            ld.o_range(0, 0, kLoadsO);
+        }
         barrier();  // B0
         for (int l = 0; l < L; ++l) {
             const bool last = l + 1 == L;
-            gu(l, 0, 5);
-            wait_vmcnt<kAfterQkv>();  // QKV(l) and the input / QK norm weights
+            ld.gu_range(l, 0, 5);
+            wait_vmcnt<ROWS == 1 ? kAfterQkv : kPairAfterQkv>();  // QKV(l) and the input / QK norm weights
             barrier();  // B1
-            gu(l, 5, 4);
+            ld.gu_range(l, 5, 4);
             barrier();  // B2
             barrier();  // B3
-            gu(l, 9, 4);
-            if (!last) ld.prefetch(m, l + 1, 0, pf);
+            ld.gu_range(l, 9, 4);
+            if (!last) ld.prefetch(l + 1, 0, pf);
             barrier();  // B4
-#pragma unroll
-            for (int b = 0; b < kLoadsDown; ++b) ld.down(m, l, b);
+            if constexpr (ROWS == 1) ld.down_range(l, 0, kLoadsDown);
             if (!last) {
-                ld.prefetch(m, l + 1, 1, pf);
-                qkv(l + 1, 0, 3);
+                ld.prefetch(l + 1, 1, pf);
+                ld.qkv_range(l + 1, 0, 3);
             }
             if (last) wait_vmcnt<0>();
-            else wait_vmcnt<kAfterO>();  // O(l)
+            else wait_vmcnt<ROWS == 1 ? kAfterO : kPairAfterO>();  // O(l)
             barrier();  // B5
-            if (!last) qkv(l + 1, 3, 2);
+            if (!last) ld.qkv_range(l + 1, 3, 2);
             barrier();  // B6
             if (!FULL) barrier();  // B6b
-            if (!last) qkv(l + 1, 5, 2);
-            barrier();  // B7
+            if (!last) ld.qkv_range(l + 1, 5, 2);
+            barrier();  // B7: O(l) is used
+            if constexpr (ROWS == 2) ld.down_range(l, 0, 3);
             barrier();  // B8
-            if (!last) o(l + 1, 0, 3);
+            if constexpr (ROWS == 1) {
+                if (!last) ld.o_range(l + 1, 0, 3);
+            } else {
+                ld.down_range(l, 3, 3);
+            }
             if (last) wait_vmcnt<0>();
-            else wait_vmcnt<kAfterGu>();  // gate/up(l) and the post-attention norm weights
+            else wait_vmcnt<ROWS == 1 ? kAfterGu : kPairAfterGu>();  // gate/up(l), post-attention norm weights
             barrier();  // B9
             if (!last) {
-                o(l + 1, 3, 1);
-                qkv(l + 1, 7, 3);
+                if constexpr (ROWS == 1) ld.o_range(l + 1, 3, 1);
+                ld.qkv_range(l + 1, 7, 3);
             }
             barrier();  // B10
             if (last) wait_vmcnt<0>();
-            else wait_vmcnt<kAfterDown>();  // down(l)
+            else wait_vmcnt<ROWS == 1 ? kAfterDown : kPairAfterDown>();  // down(l)
             barrier();  // B11
-            barrier();  // B12
+            barrier();  // B12: down(l) is used
+            if constexpr (ROWS == 2) {
+                if (!last) ld.o_range(l + 1, 0, kLoadsO);
+            }
             barrier();  // B13
         }
         return;
     }
 
     // Compute waves.
-    const int pos = a.pos, n = pos + 1, npasses = (n + 63) >> 6;
-    const int active = min(npasses, 32);
-    const bool mine = FULL || s < active;
+    const int pos = a.pos;
+    int n[ROWS], active[ROWS];
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        n[q] = pos + 1 + q;
+        active[q] = min((n[q] + 63) >> 6, 32);
+    }
+    const bool mine = FULL || s < active[ROWS - 1];
     const size_t head_base = size_t(g) * a.context;
     const int hq = s & 1, h = 2 * g + hq, rb = s >> 1;
     const unsigned spins = a.spins;
     bool ok = true;
     auto pass_base = [&](int p) { return FULL ? 64 * p : 64 * (s + 32 * p); };
 
-    // Layer 0 starts from the embedding row (engine/core.cpp:354-356).
-    if (tid < 256) {
-        const uint2 e = *reinterpret_cast<const uint2*>(a.embed + size_t(a.token) * kHidden + 4 * tid);
-        *reinterpret_cast<float4*>(&m.x[4 * tid]) =
-            make_float4(h2f(e.x & 0xffffu), h2f(e.x >> 16), h2f(e.y & 0xffffu), h2f(e.y >> 16));
-    }
-    if (wave == 0) {
-        m.rope[0][lane] = a.cosines[size_t(pos) * 64 + lane];
-        m.rope[1][lane] = a.sines[size_t(pos) * 64 + lane];
+    // Layer 0 starts from the embedding rows (engine/core.cpp:354-356).
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        if (tid < 256) {
+            const uint2 e = *reinterpret_cast<const uint2*>(a.embed + size_t(a.token[q]) * kHidden + 4 * tid);
+            *reinterpret_cast<float4*>(&m.r[q].x[4 * tid]) =
+                make_float4(h2f(e.x & 0xffffu), h2f(e.x >> 16), h2f(e.y & 0xffffu), h2f(e.y >> 16));
+        }
+        if (wave == 0) {
+            m.rope[q][0][lane] = a.cosines[size_t(pos + q) * 64 + lane];
+            m.rope[q][1][lane] = a.sines[size_t(pos + q) * 64 + lane];
+        }
     }
     barrier();  // B0
 
@@ -405,7 +526,9 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         // and spills them.
         int tid = threadIdx.x;
         asm volatile("" : "+v"(tid));
-        uint64_t* const W = a.words;
+        uint64_t* W[ROWS];
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) W[q] = a.words + size_t(q) * kTokWords;
         const int lane = tid & 63, wave = tid >> 6;
         const int j = tid & 127, c = tid & 7, grp = tid >> 3;
         const int vsub = lane >> 4, vcg = lane & 15;
@@ -415,13 +538,14 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         const int down_tile = 4 * s + wave;
 
         // ---- attention block (engine/core.cpp:384-406, 606-626) ----
-        // K/V rows of this workgroup's passes (positions past n, the current
-        // one, and all of an inactive workgroup's read row 0).
+        // K/V rows of this workgroup's passes from the cache (the rows at pos
+        // and pos + 1 come from LDS; positions past them, and all of an
+        // inactive workgroup's, read row 0).
         u32x4 kreg[PASSES][2], vreg[PASSES][2];
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int t = pass_base(p) + grp;
-            const int tl = mine && t < n && t != pos ? t : 0;
+            const int tl = mine && t < pos ? t : 0;
             const global_u32x4* kp = global_rows(TL.keys + (head_base + tl) * 128);
             kreg[p][0] = kp[c];
             kreg[p][1] = kp[c + 8];
@@ -431,82 +555,98 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
                 const int t = pass_base(p) + 8 * wave + 4 * hf + vsub;
-                const int tl = mine && t < n && t != pos ? t : 0;
+                const int tl = mine && t < pos ? t : 0;
                 vreg[p][hf] = global_rows(values + (head_base + tl) * 128)[vcg];
             }
-        // RMSNorm of the residual (engine/core.cpp:207-215; FP32 squares
-        // summed in FP64): waves 0-3 hold entries 4 tid .. 4 tid + 3.
-        float v[4];
+        // RMSNorm of the residual: waves 0-3 hold entries 4 tid .. 4 tid + 3.
+        float v[ROWS][4];
         if (tid < 256) {
-            const float4 f = *reinterpret_cast<const float4*>(&m.x[4 * tid]);
-            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-            double part = 0.0;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float square = v[k] * v[k];
-                part += static_cast<double>(square);
+            for (int q = 0; q < ROWS; ++q) {
+                const float4 f = *reinterpret_cast<const float4*>(&m.r[q].x[4 * tid]);
+                v[q][0] = f.x; v[q][1] = f.y; v[q][2] = f.z; v[q][3] = f.w;
+                norm_sums(v[q], m.r[q].red, wave, lane);
             }
-            part = wave_sum(part);
-            if (lane == 0) m.red[wave] = part;
         }
         barrier();  // B1
         if (tid < 256) {
-            const float sum = static_cast<float>(((m.red[0] + m.red[1]) + m.red[2]) + m.red[3]);
-            const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(kHidden) + 1e-6f);
-            float* xs = reinterpret_cast<float*>(m.xs4);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) xs[xperm(4 * tid + k)] = (v[k] * inv) * m.nin[4 * tid + k];
+            for (int q = 0; q < ROWS; ++q) {
+                const double* red = m.r[q].red;
+                const float sum = static_cast<float>(((red[0] + red[1]) + red[2]) + red[3]);
+                const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(kHidden) + 1e-6f);
+                float* xs = reinterpret_cast<float*>(m.r[q].u.n.xs4);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) xs[xperm(4 * tid + k)] = (v[q][k] * inv) * m.nin[4 * tid + k];
+            }
         }
         barrier();  // B2
 
         // QKV rows (the reference's chain-ordered dot): wave t < 2 runs tile
         // li = 2 s + t over all 16 column blocks and posts its 8 rows.
         if (wave < 2) {
-            const float y = combine_chains(
-                lds_chain<16>(reinterpret_cast<const u32x4*>(m.wq + 16384 * wave) + lane, m.xs4 + 2 * c));
+            const float4* x4[ROWS];
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) x4[q] = m.r[q].u.n.xs4 + 2 * c;
+            float acc[ROWS];
+            lds_chain<16, ROWS>(reinterpret_cast<const u32x4*>(m.wq() + 16384 * wave) + lane, x4, acc);
             const int li = 2 * s + wave;
-            if (c == 0 && !(l == 0 && int(blockIdx.x) == a.withhold))
-                exchange_put(W + kTokQkvOffset + g * 512 + 8 * li + (lane >> 3), y, tag);
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                const float y = combine_chains(acc[q]);
+                if (c == 0 && !(q == 0 && l == 0 && int(blockIdx.x) == a.withhold))
+                    exchange_put(W[q] + kTokQkvOffset + g * 512 + 8 * li + (lane >> 3), y, tag);
+            }
         }
         // Wave w < 4 takes head-group rows 128 w + lane and 128 w + 64 + lane
-        // (q0, q1, k, v): QK-norm (engine/core.cpp:397-398) and rotate-half
-        // RoPE (216-218) inside the wave; the workgroup holding pos's pass
-        // writes the new K/V row (403-406).
+        // (q0, q1, k, v) of each row: QK-norm (engine/core.cpp:397-398) and
+        // rotate-half RoPE (216-218) inside the wave; the workgroup holding
+        // the pass of a row's position writes its new K/V row (403-406).
         if (tid < 256) {
-            const uint64_t* const words[2] = {W + kTokQkvOffset + g * 512 + 128 * wave + lane,
-                                              W + kTokQkvOffset + g * 512 + 128 * wave + 64 + lane};
-            float got[2] = {0.f, 0.f};
-            if (ok) ok = tok_gather<2>(words, tag, got, 3u, a.stall, spins);
-            const float x0 = got[0], x1 = got[1];
-            const bool owner = ((pos >> 6) & 31) == s;
-            if (wave < 3) {
-                const float* hw = m.nqk + (wave == 2 ? kHeadDim : 0);
-                const float sq0 = x0 * x0, sq1 = x1 * x1;
-                const double lo = wave_sum(static_cast<double>(sq0)), hi = wave_sum(static_cast<double>(sq1));
-                const float sum = static_cast<float>(lo + hi);
-                const float inv = 1.0f / __builtin_sqrtf(sum / 128.0f + 1e-6f);
-                const float n0 = (x0 * inv) * hw[lane], n1 = (x1 * inv) * hw[lane + 64];
-                const float rc = m.rope[0][lane], rs = m.rope[1][lane];
-                const float r0 = n0 * rc - n1 * rs, r1 = n1 * rc + n0 * rs;
-                if (wave < 2) {
-                    m.qp[wave][kperm(lane)] = r0;
-                    m.qp[wave][kperm(lane + 64)] = r1;
-                } else {
-                    const uint16_t b0 = f2h(r0), b1 = f2h(r1);
-                    m.kcur[kperm(lane)] = b0;
-                    m.kcur[kperm(lane + 64)] = b1;
-                    if (owner) {
-                        global_halves(TL.keys)[(head_base + pos) * 128 + kperm(lane)] = b0;
-                        global_halves(TL.keys)[(head_base + pos) * 128 + kperm(lane + 64)] = b1;
+            const uint64_t* words[2 * ROWS];
+            float got[2 * ROWS];
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                words[2 * q] = W[q] + kTokQkvOffset + g * 512 + 128 * wave + lane;
+                words[2 * q + 1] = W[q] + kTokQkvOffset + g * 512 + 128 * wave + 64 + lane;
+                got[2 * q] = got[2 * q + 1] = 0.f;
+            }
+            if (ok) ok = tok_gather<2 * ROWS>(words, tag, got, (1u << (2 * ROWS)) - 1, a.stall, spins);
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                const int at = pos + q;
+                const float x0 = got[2 * q], x1 = got[2 * q + 1];
+                const bool owner = ((at >> 6) & 31) == s;
+                auto& R = m.r[q];
+                if (wave < 3) {
+                    const float* hw = m.nqk + (wave == 2 ? kHeadDim : 0);
+                    const float sq0 = x0 * x0, sq1 = x1 * x1;
+                    const double lo = wave_sum(static_cast<double>(sq0)), hi = wave_sum(static_cast<double>(sq1));
+                    const float sum = static_cast<float>(lo + hi);
+                    const float inv = 1.0f / __builtin_sqrtf(sum / 128.0f + 1e-6f);
+                    const float n0 = (x0 * inv) * hw[lane], n1 = (x1 * inv) * hw[lane + 64];
+                    const float rc = m.rope[q][0][lane], rs = m.rope[q][1][lane];
+                    const float r0 = n0 * rc - n1 * rs, r1 = n1 * rc + n0 * rs;
+                    if (wave < 2) {
+                        R.qp[wave][kperm(lane)] = r0;
+                        R.qp[wave][kperm(lane + 64)] = r1;
+                    } else {
+                        const uint16_t b0 = f2h(r0), b1 = f2h(r1);
+                        R.kcur[kperm(lane)] = b0;
+                        R.kcur[kperm(lane + 64)] = b1;
+                        if (owner) {
+                            global_halves(TL.keys)[(head_base + at) * 128 + kperm(lane)] = b0;
+                            global_halves(TL.keys)[(head_base + at) * 128 + kperm(lane + 64)] = b1;
+                        }
                     }
-                }
-            } else {
-                const uint16_t b0 = f2h(x0), b1 = f2h(x1);
-                m.vcur[lane] = b0;
-                m.vcur[lane + 64] = b1;
-                if (owner) {
-                    global_halves(values)[(head_base + pos) * 128 + lane] = b0;
-                    global_halves(values)[(head_base + pos) * 128 + lane + 64] = b1;
+                } else {
+                    const uint16_t b0 = f2h(x0), b1 = f2h(x1);
+                    R.vcur[lane] = b0;
+                    R.vcur[lane + 64] = b1;
+                    if (owner) {
+                        global_halves(values)[(head_base + at) * 128 + lane] = b0;
+                        global_halves(values)[(head_base + at) * 128 + lane + 64] = b1;
+                    }
                 }
             }
         }
@@ -514,43 +654,53 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
 
         // Scores (engine/core.cpp:606-612): the 8 lanes of a position run its
         // chains; each head's maximum over this workgroup's positions.
-        float s0[PASSES], s1[PASSES];
-        float m0 = -INFINITY, m1 = -INFINITY;
+        float s0[ROWS][PASSES], s1[ROWS][PASSES];
+        float m0[ROWS], m1[ROWS];
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) m0[q] = m1[q] = -INFINITY;
         if (mine) {
 #pragma unroll
             for (int p = 0; p < PASSES; ++p) {
                 const int t = pass_base(p) + grp;
                 uint32_t kw[8];
                 if (t == pos) {
-                    key_pieces_lds(m.kcur, c, kw);
+                    key_pieces_lds(m.r[0].kcur, c, kw);
+                } else if (ROWS == 2 && t == pos + 1) {
+                    key_pieces_lds(m.r[ROWS - 1].kcur, c, kw);
                 } else {
                     kw[0] = kreg[p][0].x; kw[1] = kreg[p][0].y; kw[2] = kreg[p][0].z; kw[3] = kreg[p][0].w;
                     kw[4] = kreg[p][1].x; kw[5] = kreg[p][1].y; kw[6] = kreg[p][1].z; kw[7] = kreg[p][1].w;
                 }
-                if constexpr (FULL) {
-                    const float d0 = combine_chains(key_chain(m.qp[hq], c, kw, 0.f)) * a.scale;
-                    s0[p] = t < n ? d0 : -INFINITY;
-                    m0 = fmaxf(m0, s0[p]);
-                } else {
-                    const float d0 = combine_chains(key_chain(m.qp[0], c, kw, 0.f)) * a.scale;
-                    const float d1 = combine_chains(key_chain(m.qp[1], c, kw, 0.f)) * a.scale;
-                    s0[p] = t < n ? d0 : -INFINITY;
-                    s1[p] = t < n ? d1 : -INFINITY;
-                    m0 = fmaxf(m0, s0[p]);
-                    m1 = fmaxf(m1, s1[p]);
+#pragma unroll
+                for (int q = 0; q < ROWS; ++q) {
+                    if constexpr (FULL) {
+                        const float d0 = combine_chains(key_chain(m.r[q].qp[hq], c, kw, 0.f)) * a.scale;
+                        s0[q][p] = t < n[q] ? d0 : -INFINITY;
+                        m0[q] = fmaxf(m0[q], s0[q][p]);
+                    } else {
+                        const float d0 = combine_chains(key_chain(m.r[q].qp[0], c, kw, 0.f)) * a.scale;
+                        const float d1 = combine_chains(key_chain(m.r[q].qp[1], c, kw, 0.f)) * a.scale;
+                        s0[q][p] = t < n[q] ? d0 : -INFINITY;
+                        s1[q][p] = t < n[q] ? d1 : -INFINITY;
+                        m0[q] = fmaxf(m0[q], s0[q][p]);
+                        m1[q] = fmaxf(m1[q], s1[q][p]);
+                    }
                 }
             }
-            m0 = fmaxf(m0, xor_lanes<8>(m0));
-            m0 = fmaxf(m0, xor_lanes<16>(m0));
-            m0 = fmaxf(m0, xor_lanes<32>(m0));
-            if constexpr (!FULL) {
-                m1 = fmaxf(m1, xor_lanes<8>(m1));
-                m1 = fmaxf(m1, xor_lanes<16>(m1));
-                m1 = fmaxf(m1, xor_lanes<32>(m1));
-            }
-            if (lane == 0) {
-                m.wmax[wave][0] = m0;
-                m.wmax[wave][1] = m1;
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                m0[q] = fmaxf(m0[q], xor_lanes<8>(m0[q]));
+                m0[q] = fmaxf(m0[q], xor_lanes<16>(m0[q]));
+                m0[q] = fmaxf(m0[q], xor_lanes<32>(m0[q]));
+                if constexpr (!FULL) {
+                    m1[q] = fmaxf(m1[q], xor_lanes<8>(m1[q]));
+                    m1[q] = fmaxf(m1[q], xor_lanes<16>(m1[q]));
+                    m1[q] = fmaxf(m1[q], xor_lanes<32>(m1[q]));
+                }
+                if (lane == 0) {
+                    m.r[q].wmax[wave][0] = m0[q];
+                    m.r[q].wmax[wave][1] = m1[q];
+                }
             }
         }
         barrier();  // B4
@@ -559,133 +709,163 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         // head over the workgroup (so the waves' sums add without
         // rescaling), each wave's sums over its positions.
         if (mine) {
-            m0 = m.wmax[0][0];
-            m1 = m.wmax[0][1];
+            float l0[ROWS], l1[ROWS];
 #pragma unroll
-            for (int w = 1; w < 8; ++w) {
-                m0 = fmaxf(m0, m.wmax[w][0]);
-                m1 = fmaxf(m1, m.wmax[w][1]);
-            }
-            float l0 = 0.f, l1 = 0.f;
+            for (int q = 0; q < ROWS; ++q) {
+                auto& R = m.r[q];
+                m0[q] = R.wmax[0][0];
+                m1[q] = R.wmax[0][1];
 #pragma unroll
-            for (int p = 0; p < PASSES; ++p) {
-                const int t = pass_base(p) + grp;
-                const float p0 = t < n ? expf(s0[p] - m0) : 0.f;
-                l0 += p0;
-                if constexpr (FULL) {
-                    if (c == 0) m.prob[t >> 7][t & 127] = p0;
-                } else {
-                    const float p1 = t < n ? expf(s1[p] - m1) : 0.f;
-                    l1 += p1;
-                    if (c == 0) {
-                        m.prob[0][p * 64 + grp] = p0;
-                        m.prob[1][p * 64 + grp] = p1;
+                for (int w = 1; w < 8; ++w) {
+                    m0[q] = fmaxf(m0[q], R.wmax[w][0]);
+                    m1[q] = fmaxf(m1[q], R.wmax[w][1]);
+                }
+                l0[q] = l1[q] = 0.f;
+#pragma unroll
+                for (int p = 0; p < PASSES; ++p) {
+                    const int t = pass_base(p) + grp;
+                    const float p0 = t < n[q] ? expf(s0[q][p] - m0[q]) : 0.f;
+                    l0[q] += p0;
+                    if constexpr (FULL) {
+                        if (c == 0) R.v.prob[t >> 7][t & 127] = p0;
+                    } else {
+                        const float p1 = t < n[q] ? expf(s1[q][p] - m1[q]) : 0.f;
+                        l1[q] += p1;
+                        if (c == 0) {
+                            R.v.prob[0][p * 64 + grp] = p0;
+                            R.v.prob[1][p * 64 + grp] = p1;
+                        }
                     }
                 }
-            }
-            l0 += xor_lanes<8>(l0);
-            l0 += xor_lanes<16>(l0);
-            l0 += xor_lanes<32>(l0);
-            if constexpr (!FULL) {
-                l1 += xor_lanes<8>(l1);
-                l1 += xor_lanes<16>(l1);
-                l1 += xor_lanes<32>(l1);
+                l0[q] += xor_lanes<8>(l0[q]);
+                l0[q] += xor_lanes<16>(l0[q]);
+                l0[q] += xor_lanes<32>(l0[q]);
+                if constexpr (!FULL) {
+                    l1[q] += xor_lanes<8>(l1[q]);
+                    l1[q] += xor_lanes<16>(l1[q]);
+                    l1[q] += xor_lanes<32>(l1[q]);
+                }
             }
             // prob of this wave's positions is written and read by this wave only.
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             constexpr int kHeads = FULL ? 1 : 2;
-            float acc[kHeads][8];
+            float acc[ROWS][kHeads][8];
 #pragma unroll
-            for (int hh = 0; hh < kHeads; ++hh)
+            for (int q = 0; q < ROWS; ++q)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[hh][i] = 0.f;
+                for (int hh = 0; hh < kHeads; ++hh)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[q][hh][i] = 0.f;
 #pragma unroll
             for (int p = 0; p < PASSES; ++p)
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
                     const int t = pass_base(p) + 8 * wave + 4 * hf + vsub;
-                    if (t < n) {
+                    if (t < n[ROWS - 1]) {
                         uint32_t vw[4];
                         if (t == pos) {
 #pragma unroll
                             for (int i = 0; i < 4; ++i)
-                                vw[i] = uint32_t(m.vcur[vcg * 8 + 2 * i]) | (uint32_t(m.vcur[vcg * 8 + 2 * i + 1]) << 16);
+                                vw[i] = uint32_t(m.r[0].vcur[vcg * 8 + 2 * i]) |
+                                        (uint32_t(m.r[0].vcur[vcg * 8 + 2 * i + 1]) << 16);
+                        } else if (ROWS == 2 && t == pos + 1) {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                vw[i] = uint32_t(m.r[ROWS - 1].vcur[vcg * 8 + 2 * i]) |
+                                        (uint32_t(m.r[ROWS - 1].vcur[vcg * 8 + 2 * i + 1]) << 16);
                         } else {
                             vw[0] = vreg[p][hf].x; vw[1] = vreg[p][hf].y; vw[2] = vreg[p][hf].z; vw[3] = vreg[p][hf].w;
                         }
-                        if constexpr (FULL) {
-                            const float p0 = m.prob[t >> 7][t & 127];
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                acc[0][2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p0, acc[0][2 * i]);
-                                acc[0][2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p0, acc[0][2 * i + 1]);
-                            }
-                        } else {
-                            const int tl = p * 64 + 8 * wave + 4 * hf + vsub;
-                            const float p0 = m.prob[0][tl], p1 = m.prob[1][tl];
+                        for (int q = 0; q < ROWS; ++q) {
+                            if (t < n[q]) {
+                                if constexpr (FULL) {
+                                    const float p0 = m.r[q].v.prob[t >> 7][t & 127];
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
-                                acc[0][2 * i] = __builtin_fmaf(v0, p0, acc[0][2 * i]);
-                                acc[0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[0][2 * i + 1]);
-                                acc[kHeads - 1][2 * i] = __builtin_fmaf(v0, p1, acc[kHeads - 1][2 * i]);
-                                acc[kHeads - 1][2 * i + 1] = __builtin_fmaf(v1, p1, acc[kHeads - 1][2 * i + 1]);
+                                    for (int i = 0; i < 4; ++i) {
+                                        acc[q][0][2 * i] = __builtin_fmaf(h2f(vw[i] & 0xffffu), p0, acc[q][0][2 * i]);
+                                        acc[q][0][2 * i + 1] = __builtin_fmaf(h2f(vw[i] >> 16), p0, acc[q][0][2 * i + 1]);
+                                    }
+                                } else {
+                                    const int tl = p * 64 + 8 * wave + 4 * hf + vsub;
+                                    const float p0 = m.r[q].v.prob[0][tl], p1 = m.r[q].v.prob[1][tl];
+#pragma unroll
+                                    for (int i = 0; i < 4; ++i) {
+                                        const float v0 = h2f(vw[i] & 0xffffu), v1 = h2f(vw[i] >> 16);
+                                        acc[q][0][2 * i] = __builtin_fmaf(v0, p0, acc[q][0][2 * i]);
+                                        acc[q][0][2 * i + 1] = __builtin_fmaf(v1, p0, acc[q][0][2 * i + 1]);
+                                        acc[q][kHeads - 1][2 * i] = __builtin_fmaf(v0, p1, acc[q][kHeads - 1][2 * i]);
+                                        acc[q][kHeads - 1][2 * i + 1] =
+                                            __builtin_fmaf(v1, p1, acc[q][kHeads - 1][2 * i + 1]);
+                                    }
+                                }
                             }
                         }
                     }
                 }
 #pragma unroll
-            for (int hh = 0; hh < kHeads; ++hh)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    acc[hh][i] += xor_lanes<16>(acc[hh][i]);
-                    acc[hh][i] += xor_lanes<32>(acc[hh][i]);
-                }
-            if (vsub == 0) {
+            for (int q = 0; q < ROWS; ++q) {
 #pragma unroll
                 for (int hh = 0; hh < kHeads; ++hh)
 #pragma unroll
-                    for (int i = 0; i < 8; i += 4)
-                        *reinterpret_cast<float4*>(&m.opart[wave][hh][vcg * 8 + i]) =
-                            make_float4(acc[hh][i], acc[hh][i + 1], acc[hh][i + 2], acc[hh][i + 3]);
-            }
-            if (lane == 0) {
-                m.wsum[wave][0] = l0;
-                m.wsum[wave][1] = l1;
+                    for (int i = 0; i < 8; ++i) {
+                        acc[q][hh][i] += xor_lanes<16>(acc[q][hh][i]);
+                        acc[q][hh][i] += xor_lanes<32>(acc[q][hh][i]);
+                    }
+                if (vsub == 0) {
+#pragma unroll
+                    for (int hh = 0; hh < kHeads; ++hh)
+#pragma unroll
+                        for (int i = 0; i < 8; i += 4)
+                            *reinterpret_cast<float4*>(&m.r[q].u.opart[wave][hh][vcg * 8 + i]) =
+                                make_float4(acc[q][hh][i], acc[q][hh][i + 1], acc[q][hh][i + 2], acc[q][hh][i + 3]);
+                }
+                if (lane == 0) {
+                    m.r[q].wsum[wave][0] = l0[q];
+                    m.r[q].wsum[wave][1] = l1[q];
+                }
             }
         }
         barrier();  // B5
 
         if constexpr (FULL) {
-            if (tid < 128) {  // the 8 waves' sums in a fixed tree
-                const float o = ((m.opart[0][0][tid] + m.opart[1][0][tid]) + (m.opart[2][0][tid] + m.opart[3][0][tid])) +
-                                ((m.opart[4][0][tid] + m.opart[5][0][tid]) + (m.opart[6][0][tid] + m.opart[7][0][tid]));
-                const float lsum = ((m.wsum[0][0] + m.wsum[1][0]) + (m.wsum[2][0] + m.wsum[3][0])) +
-                                   ((m.wsum[4][0] + m.wsum[5][0]) + (m.wsum[6][0] + m.wsum[7][0]));
-                m.att[tid] = o / lsum;
+            if (tid < 128 * ROWS) {  // the 8 waves' sums in a fixed tree
+                auto& R = m.r[tid >> 7];
+                const float o = ((R.u.opart[0][0][j] + R.u.opart[1][0][j]) + (R.u.opart[2][0][j] + R.u.opart[3][0][j])) +
+                                ((R.u.opart[4][0][j] + R.u.opart[5][0][j]) + (R.u.opart[6][0][j] + R.u.opart[7][0][j]));
+                const float lsum = ((R.wsum[0][0] + R.wsum[1][0]) + (R.wsum[2][0] + R.wsum[3][0])) +
+                                   ((R.wsum[4][0] + R.wsum[5][0]) + (R.wsum[6][0] + R.wsum[7][0]));
+                R.att[j] = o / lsum;
             }
             barrier();  // B6
         } else {
             // Each workgroup with positions posts (output, max, sum) of both
             // heads; workgroup (g, s) merges head h over the active partials
             // (4 groups of 8 against their own maximum, then combined).
-            if (mine && tid < 256) {
-                const int hh = tid >> 7;
-                const float o = ((m.opart[0][hh][j] + m.opart[1][hh][j]) + (m.opart[2][hh][j] + m.opart[3][hh][j])) +
-                                ((m.opart[4][hh][j] + m.opart[5][hh][j]) + (m.opart[6][hh][j] + m.opart[7][hh][j]));
-                const float lsum = ((m.wsum[0][hh] + m.wsum[1][hh]) + (m.wsum[2][hh] + m.wsum[3][hh])) +
-                                   ((m.wsum[4][hh] + m.wsum[5][hh]) + (m.wsum[6][hh] + m.wsum[7][hh]));
-                uint64_t* part = W + kTokPartOffset + ((size_t(g) * 32 + s) * 2 + hh) * kXPart;
-                exchange_put(part + j, o, tag);
-                if (j == 0) {
-                    exchange_put(part + 128, hh ? m1 : m0, tag);
-                    exchange_put(part + 129, lsum, tag);
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                if (s < active[q] && tid < 256) {
+                    auto& R = m.r[q];
+                    const int hh = tid >> 7;
+                    const float o = ((R.u.opart[0][hh][j] + R.u.opart[1][hh][j]) +
+                                     (R.u.opart[2][hh][j] + R.u.opart[3][hh][j])) +
+                                    ((R.u.opart[4][hh][j] + R.u.opart[5][hh][j]) +
+                                     (R.u.opart[6][hh][j] + R.u.opart[7][hh][j]));
+                    const float lsum = ((R.wsum[0][hh] + R.wsum[1][hh]) + (R.wsum[2][hh] + R.wsum[3][hh])) +
+                                       ((R.wsum[4][hh] + R.wsum[5][hh]) + (R.wsum[6][hh] + R.wsum[7][hh]));
+                    uint64_t* part = W[q] + kTokPartOffset + ((size_t(g) * 32 + s) * 2 + hh) * kXPart;
+                    exchange_put(part + j, o, tag);
+                    if (j == 0) {
+                        exchange_put(part + 128, hh ? m1[q] : m0[q], tag);
+                        exchange_put(part + 129, lsum, tag);
+                    }
                 }
             }
-            {
-                const int q = tid >> 7;
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                const int gq = tid >> 7;
                 float mv[8], lv[8], ovl[8];
                 {
                     const uint64_t* words[24];
@@ -693,79 +873,85 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                     unsigned want = 0;
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
-                        const uint64_t* part = W + kTokPartOffset + ((size_t(g) * 32 + 8 * q + k) * 2 + hq) * kXPart;
+                        const uint64_t* part =
+                            W[q] + kTokPartOffset + ((size_t(g) * 32 + 8 * gq + k) * 2 + hq) * kXPart;
                         words[k] = part + j;
                         words[8 + k] = part + 128;
                         words[16 + k] = part + 129;
                         got[k] = got[8 + k] = got[16 + k] = 0.f;
-                        if (8 * q + k < active) want |= 0x10101u << k;
+                        if (8 * gq + k < active[q]) want |= 0x10101u << k;
                     }
                     if (ok) ok = tok_gather<24>(words, tag, got, want, a.stall, spins);
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
                         ovl[k] = got[k];
-                        mv[k] = 8 * q + k < active ? got[8 + k] : -INFINITY;
+                        mv[k] = 8 * gq + k < active[q] ? got[8 + k] : -INFINITY;
                         lv[k] = got[16 + k];
                     }
                 }
                 float mx = -INFINITY;
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
-                    if (8 * q + k < active) mx = fmaxf(mx, mv[k]);
+                    if (8 * gq + k < active[q]) mx = fmaxf(mx, mv[k]);
                 float lsum = 0.f, o = 0.f;
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
-                    if (8 * q + k < active) {
+                    if (8 * gq + k < active[q]) {
                         const float w = expf(mv[k] - mx);
                         lsum += w * lv[k];
                         o += w * ovl[k];
                     }
+                auto& R = m.r[q];
                 if (j == 0) {
-                    m.gm[q] = mx;
-                    m.gl[q] = lsum;
+                    R.gm[gq] = mx;
+                    R.gl[gq] = lsum;
                 }
-                m.go[q][j] = o;
+                R.go[gq][j] = o;
             }
             barrier();  // B6
-            if (tid < 128) {
-                float m2 = m.gm[0];
+            if (tid < 128 * ROWS) {
+                auto& R = m.r[tid >> 7];
+                float m2 = R.gm[0];
 #pragma unroll
-                for (int q = 1; q < 4; ++q) m2 = fmaxf(m2, m.gm[q]);
+                for (int gq = 1; gq < 4; ++gq) m2 = fmaxf(m2, R.gm[gq]);
                 float lt = 0.f, ot = 0.f;
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (m.gm[q] != -INFINITY) {  // a group without partials adds nothing
-                        const float w = expf(m.gm[q] - m2);
-                        lt += w * m.gl[q];
-                        ot += w * m.go[q][tid];
+                for (int gq = 0; gq < 4; ++gq)
+                    if (R.gm[gq] != -INFINITY) {  // a group without partials adds nothing
+                        const float w = expf(R.gm[gq] - m2);
+                        lt += w * R.gl[gq];
+                        ot += w * R.go[gq][j];
                     }
-                m.att[tid] = ot / lt;
+                R.att[j] = ot / lt;
             }
             barrier();  // B6b
         }
 
-        // O rows 64 rb .. + 63 against head h's attention output; each row's
-        // partial goes to the fold across XCDs.
+        // O rows 64 rb .. + 63 against head h's attention output of each row;
+        // each row's partial goes to the fold across XCDs.
         {
-            const u32x4* wrow = reinterpret_cast<const u32x4*>(m.wo + 256 * orow_local) + opart_id;
-            const float4* at4 = reinterpret_cast<const float4*>(m.att) + 2 * opart_id;
-            float y = 0.f;
+            const u32x4* wrow = reinterpret_cast<const u32x4*>(m.wo() + 256 * orow_local) + opart_id;
+            const u32x4 w0 = wrow[0], w1 = wrow[8];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) y = chain8(y, wrow[8 * i], at4[16 * i], at4[16 * i + 1]);
-            y += xor_lanes<1>(y);
-            y += xor_lanes<2>(y);
-            y += xor_lanes<4>(y);
-            if (opart_id == 0) exchange_put_through(W + kTokOCrossOffset + size_t(h) * kHidden + orow, y, tag);
+            for (int q = 0; q < ROWS; ++q) {
+                const float4* at4 = reinterpret_cast<const float4*>(m.r[q].att) + 2 * opart_id;
+                float y = chain8(0.f, w0, at4[0], at4[1]);
+                y = chain8(y, w1, at4[16], at4[17]);
+                y += xor_lanes<1>(y);
+                y += xor_lanes<2>(y);
+                y += xor_lanes<4>(y);
+                if (opart_id == 0) exchange_put_through(W[q] + kTokOCrossOffset + size_t(h) * kHidden + orow, y, tag);
+            }
         }
         barrier();  // B7
 
-        // Fold 1 (engine/core.cpp:626): wave 0 forms rows 32 s .. + 31 of x +
-        // the 16 head partials (lane = row, half: heads 8 half .. + 7; the
-        // tree of the two-kernel path) and posts them inside the XCD; every
-        // thread then gathers two of the XCD's 1024 sums.
-        if (wave == 0) {
+        // Fold 1 (engine/core.cpp:626): wave q forms rows 32 s .. + 31 of row
+        // q's x + the 16 head partials (lane = row, half: heads 8 half .. + 7;
+        // the tree of the two-kernel path) and posts them inside the XCD;
+        // every thread then gathers two of the XCD's 1024 sums of each row.
+        if (wave < ROWS) {
             const int row = 32 * s + (lane >> 1), half = lane & 1;
-            const uint64_t* base = W + kTokOCrossOffset + size_t(8 * half) * kHidden + row;
+            const uint64_t* base = W[wave] + kTokOCrossOffset + size_t(8 * half) * kHidden + row;
             const uint64_t* const words[8] = {base, base + kHidden, base + 2 * kHidden, base + 3 * kHidden,
                                               base + 4 * kHidden, base + 5 * kHidden, base + 6 * kHidden,
                                               base + 7 * kHidden};
@@ -774,40 +960,40 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             const float part = ((p8[0] + p8[1]) + (p8[2] + p8[3])) + ((p8[4] + p8[5]) + (p8[6] + p8[7]));
             const float other = xor_lanes<1>(part);
             const float lo = half ? other : part, hi = half ? part : other;
-            const float xm = m.x[row] + (lo + hi);
-            if (half == 0) exchange_put(W + kTokXmOffset + g * kHidden + row, xm, tag);
+            const float xm = m.r[wave].x[row] + (lo + hi);
+            if (half == 0) exchange_put(W[wave] + kTokXmOffset + g * kHidden + row, xm, tag);
         }
-        {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
             float x0 = 0.f, x1 = 0.f;
-            if (ok) ok = tok_get2(W + kTokXmOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
-            m.xm[2 * tid] = x0;
-            m.xm[2 * tid + 1] = x1;
+            if (ok) ok = tok_get2(W[q] + kTokXmOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
+            m.r[q].u.n.xm[2 * tid] = x0;
+            m.r[q].u.n.xm[2 * tid + 1] = x1;
         }
         barrier();  // B8
 
         // ---- FFN block (engine/core.cpp:627-641) ----
         if (tid < 256) {
-            const float4 f = *reinterpret_cast<const float4*>(&m.xm[4 * tid]);
-            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-            double part = 0.0;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float square = v[k] * v[k];
-                part += static_cast<double>(square);
+            for (int q = 0; q < ROWS; ++q) {
+                const float4 f = *reinterpret_cast<const float4*>(&m.r[q].u.n.xm[4 * tid]);
+                v[q][0] = f.x; v[q][1] = f.y; v[q][2] = f.z; v[q][3] = f.w;
+                norm_sums(v[q], m.r[q].red, wave, lane);
             }
-            part = wave_sum(part);
-            if (lane == 0) m.red[wave] = part;
         }
         barrier();  // B9
         if (tid < 256) {
-            double total = 0.0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) total += m.red[i];
-            const float sum = static_cast<float>(total);
-            const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(kHidden) + 1e-6f);
-            float* xs = reinterpret_cast<float*>(m.xs4);
+            for (int q = 0; q < ROWS; ++q) {
+                double total = 0.0;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) xs[xperm(4 * tid + k)] = (v[k] * inv) * m.npost[4 * tid + k];
+                for (int i = 0; i < 4; ++i) total += m.r[q].red[i];
+                const float sum = static_cast<float>(total);
+                const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(kHidden) + 1e-6f);
+                float* xs = reinterpret_cast<float*>(m.r[q].u.n.xs4);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) xs[xperm(4 * tid + k)] = (v[q][k] * inv) * m.npost[4 * tid + k];
+            }
         }
         barrier();  // B10
 
@@ -815,83 +1001,120 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         // SwiGLU (engine/core.cpp:636-639), the XCD's 384 activations
         // exchanged.
         if (wave < 3) {
-            const float y = combine_chains(
-                lds_chain<16>(reinterpret_cast<const u32x4*>(m.wgu + 16384 * wave) + lane, m.xs4 + 2 * c));
-            const float up = __shfl(y, (lane + 32) & 63);
-            if (lane < 32 && c == 0) {
-                const float gate = y;
-                const float half_gate = gate * 0.5f;
-                const float t = tanhf(half_gate);
-                exchange_put(W + kTokActOffset + 4 * gu_tile + (lane >> 3), gate * (0.5f + 0.5f * t) * up, tag);
+            const float4* x4[ROWS];
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) x4[q] = m.r[q].u.n.xs4 + 2 * c;
+            float acc[ROWS];
+            lds_chain<16, ROWS>(reinterpret_cast<const u32x4*>(m.wgu() + 16384 * wave) + lane, x4, acc);
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                const float y = combine_chains(acc[q]);
+                const float up = __shfl(y, (lane + 32) & 63);
+                if (lane < 32 && c == 0) {
+                    const float gate = y;
+                    const float half_gate = gate * 0.5f;
+                    const float t = tanhf(half_gate);
+                    exchange_put(W[q] + kTokActOffset + 4 * gu_tile + (lane >> 3), gate * (0.5f + 0.5f * t) * up, tag);
+                }
             }
         }
         if (tid < kFfnSlice / 2) {
-            float a0 = 0.f, a1 = 0.f;
-            if (ok) ok = tok_get2(W + kTokActOffset + kFfnSlice * g + 2 * tid, tag, a0, a1, a.stall, spins);
-            float* as = reinterpret_cast<float*>(m.as4);
-            as[xperm(2 * tid)] = a0;
-            as[xperm(2 * tid + 1)] = a1;
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                float a0 = 0.f, a1 = 0.f;
+                if (ok) ok = tok_get2(W[q] + kTokActOffset + kFfnSlice * g + 2 * tid, tag, a0, a1, a.stall, spins);
+                float* as = reinterpret_cast<float*>(m.r[q].v.as4);
+                as[xperm(2 * tid)] = a0;
+                as[xperm(2 * tid + 1)] = a1;
+            }
         }
         barrier();  // B11
 
         // Down tile 4 s + w (waves 0-3) over the slice's 384 columns; the
         // rows go to the fold across XCDs.
         if (wave < 4) {
-            const float y = combine_chains(
-                lds_chain<6>(reinterpret_cast<const u32x4*>(m.wdn + 6144 * wave) + lane, m.as4 + 2 * c));
-            if (c == 0)
-                exchange_put_through(W + kTokDCrossOffset + size_t(g) * kHidden + 8 * down_tile + (lane >> 3), y, tag);
+            const float4* x4[ROWS];
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) x4[q] = m.r[q].v.as4 + 2 * c;
+            float acc[ROWS];
+            lds_chain<6, ROWS>(reinterpret_cast<const u32x4*>(m.wdn() + 6144 * wave) + lane, x4, acc);
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                const float y = combine_chains(acc[q]);
+                if (c == 0)
+                    exchange_put_through(W[q] + kTokDCrossOffset + size_t(g) * kHidden + 8 * down_tile + (lane >> 3), y,
+                                         tag);
+            }
         }
         barrier();  // B12
 
-        // Fold 2: rows 32 s .. + 31 of xm + the 8 down slices (the tree of
-        // the two-kernel path), posted inside the XCD; every thread gathers
-        // two entries of the next layer's residual.
-        if (wave == 0 && lane < 32) {
+        // Fold 2: wave q forms rows 32 s .. + 31 of row q's xm + the 8 down
+        // slices (the tree of the two-kernel path), posted inside the XCD;
+        // every thread gathers two entries of each row's next residual.
+        if (wave < ROWS && lane < 32) {
             const int row = 32 * s + lane;
-            const uint64_t* base = W + kTokDCrossOffset + row;
+            const uint64_t* base = W[wave] + kTokDCrossOffset + row;
             const uint64_t* const words[8] = {base, base + kHidden, base + 2 * kHidden, base + 3 * kHidden,
                                               base + 4 * kHidden, base + 5 * kHidden, base + 6 * kHidden,
                                               base + 7 * kHidden};
             float d8[8] = {};
             if (ok) ok = tok_gather<8>(words, tag, d8, 0xffu, a.stall, spins);
-            exchange_put(W + kTokXOffset + g * kHidden + row, fold_slices(m.xm[row], d8), tag);
+            exchange_put(W[wave] + kTokXOffset + g * kHidden + row, fold_slices(m.r[wave].u.n.xm[row], d8), tag);
         }
-        {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
             float x0 = 0.f, x1 = 0.f;
-            if (ok) ok = tok_get2(W + kTokXOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
-            m.x[2 * tid] = x0;
-            m.x[2 * tid + 1] = x1;
+            if (ok) ok = tok_get2(W[q] + kTokXOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
+            m.r[q].x[2 * tid] = x0;
+            m.r[q].x[2 * tid + 1] = x1;
         }
         barrier();  // B13
     }
 
     if (blockIdx.x == 0) {
-        a.x_out[2 * tid] = m.x[2 * tid];
-        a.x_out[2 * tid + 1] = m.x[2 * tid + 1];
+        int t = threadIdx.x;  // opaque: keeps the address from being formed (and held) before the loop
+        asm volatile("" : "+v"(t));
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            a.x_out[q * kHidden + 2 * t] = m.r[q].x[2 * t];
+            a.x_out[q * kHidden + 2 * t + 1] = m.r[q].x[2 * t + 1];
+        }
     }
 }
 
 }  // namespace
 
+bool token_pair_supported(int pos) {
+    const int n0 = pos + 1, n1 = pos + 2;
+    return (n0 <= 256) == (n1 <= 256);  // the same attention form for both rows
+}
+
 void launch_token_layers(const TokenLaunch& t, hipStream_t stream) {
     require(t.layer_count >= 1 && t.layer_count <= kLayers, "token kernel: bad layer table");
-    require(t.pos >= 0 && t.pos < t.context && t.context <= kMaxContext, "token kernel: position outside the cache");
-    require(t.token >= 0 && t.token < kVocab, "token kernel: token out of range");
+    require(t.rows == 1 || t.rows == 2, "token kernel: one or two rows");
+    require(t.pos >= 0 && t.pos + t.rows <= t.context && t.context <= kMaxContext,
+            "token kernel: position outside the cache");
+    for (int q = 0; q < t.rows; ++q) require(t.token[q] >= 0 && t.token[q] < kVocab, "token kernel: token out of range");
+    require(t.rows == 1 || token_pair_supported(t.pos), "token kernel: the two rows take different attention forms");
     require(t.tag != 0 && uint64_t(t.tag) + uint64_t(t.layer_count) - 1 <= 0xFFFFFFFFull,
             "token kernel: tags must be nonzero and not wrap");
     require(t.spins >= 1, "token kernel: poll limit must be positive");
-    const int passes = (t.pos + 1 + 63) / 64;
-    auto go = [&](auto kernel) { kernel<<<256, kTokenThreads, 0, stream>>>(t); };
-    switch (passes <= 4 ? passes : 0) {
-        case 1: go(token_kernel<1, true>); break;
-        case 2: go(token_kernel<2, true>); break;
-        case 3: go(token_kernel<3, true>); break;
-        case 4: go(token_kernel<4, true>); break;
-        default:
-            if (passes > 32) go(token_kernel<2, false>);
-            else go(token_kernel<1, false>);
-    }
+    const int passes = (t.pos + t.rows + 63) / 64;  // of the last row
+    auto go = [&](auto rows_tag) {
+        constexpr int R = decltype(rows_tag)::value;
+        auto launch = [&](auto kernel) { kernel<<<256, kTokenThreads, 0, stream>>>(t); };
+        switch (passes <= 4 ? passes : 0) {
+            case 1: launch(token_kernel<1, true, R>); break;
+            case 2: launch(token_kernel<2, true, R>); break;
+            case 3: launch(token_kernel<3, true, R>); break;
+            case 4: launch(token_kernel<4, true, R>); break;
+            default:
+                if (passes > 32) launch(token_kernel<2, false, R>);
+                else launch(token_kernel<1, false, R>);
+        }
+    };
+    if (t.rows == 1) go(std::integral_constant<int, 1>{});
+    else go(std::integral_constant<int, 2>{});
 }
 
 }  // namespace qwen_hip

@@ -46,14 +46,15 @@ inline constexpr unsigned kTokenSpins = 1u << 18;
 struct TokenLaunch {
     TokenLayer layers[kLayers];  // layers 0 .. layer_count - 1 (kernel arguments: read with scalar loads)
     int layer_count;
-    const uint16_t* embed;     // natural embedding (layer 0 starts from row `token`)
-    int token;
-    int pos;                   // position written (n = pos + 1 cached positions)
+    const uint16_t* embed;     // natural embedding (layer 0 of row q starts from row token[q])
+    int token[2];
+    int rows;                  // 1, or 2: the rows of a verification at pos and pos + 1
+    int pos;                   // position written by row 0 (n = pos + 1 cached positions)
     int context;
     const float* cosines;      // [4096][64]
     const float* sines;
-    float* x_out;              // [1024] residual after the last layer
-    uint64_t* words;           // kTokWords exchange words
+    float* x_out;              // [rows][1024] residual after the last layer
+    uint64_t* words;           // [rows][kTokWords] exchange words
     int* stall;                // raised when a poll gave up (cleared by the argmax kernel)
     float scale;               // 1 / sqrt(128), the attention score scale
     uint32_t tag;              // layer l uses tag + l (never 0, unique since the words were cleared)
@@ -62,7 +63,12 @@ struct TokenLaunch {
     int prefetch;              // nonzero: load waves pull the next layer's K/V rows into L2
 };
 
-// Runs layers 0 .. layer_count - 1 of one decode row at position pos:
+// True when the verification rows at pos and pos + 1 take the same
+// attention form (which one launch of two rows requires).
+bool token_pair_supported(int pos);
+
+// Runs layers 0 .. layer_count - 1 of one decode row at position pos (or of
+// the two verification rows at pos and pos + 1):
 // 256 workgroups, one per CU (all resident together: the caller holds the
 // GPU), workgroup w on XCD w % 8. Compute waves 0-7 keep the arithmetic of
 // the fused QKV + attention and FFN kernels (bit-identical results); waves

@@ -291,12 +291,12 @@ def oracle_prefix(oracle_lib, pack0):
 
 
 @pytest.mark.gpu
-# Prefixes cover the one-pass pair kernels (fused attention: 0, 1, 62, 63
-# where row 1 needs one more 64-position pass than row 0, 510 at the fused
-# limit; split attention: 513, 700) and the two-step fallback (511: row 0
-# fused, row 1 split).
-@pytest.mark.parametrize('prefix,commit', [(0, 1), (0, 2), (1, 1), (1, 2), (62, 2), (63, 1), (510, 2), (511, 2),
-                                           (513, 2), (700, 1)])
+# Prefixes cover the two-row launch of the token kernel (fused attention:
+# 0, 1, 62, 63 where row 1 needs one more 64-position pass than row 0, 254
+# with both rows at the fused limit of 256 positions; split attention: 510,
+# 511, 513, 700) and the two-step fallback (255: row 0 fused, row 1 split).
+@pytest.mark.parametrize('prefix,commit', [(0, 1), (0, 2), (1, 1), (1, 2), (62, 2), (63, 1), (254, 2), (255, 1),
+                                           (510, 2), (511, 2), (513, 2), (700, 1)])
 def test_verify_two_equals_two_steps(qpkg, pack0, gpu_model, oracle_prefix, prefix, commit):
     """tools/native_verify_check.cpp normal_case, against a second model:
     every row bit-identical to single steps; and both rows (logits and
