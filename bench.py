@@ -22,13 +22,17 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / 'tests'))
 
 HBM_PEAK_GBS = 8000.0
-# Engine kernel ids (time_kernel). A decode step runs 'qkv_attention' (norm
-# + QKV + attention + O in one kernel) and 'ffn' (norm + gate/up + SwiGLU +
-# down) in every layer; 'qkv', 'attention', 'gate_up' and 'down' are the
-# separate kernels those replace (timed for comparison, not run by a step).
-KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head', 'ffn', 'qkv_attention']
+# Engine kernel ids (time_kernel). A decode step runs 'token' (all 28 layers
+# in one launch) and 'lm_head' (+ the argmax). 'qkv_attention' (norm + QKV +
+# attention + O) and 'ffn' (norm + gate/up + SwiGLU + down) are the two
+# per-layer kernels of the engine's two-kernel step, and 'qkv', 'attention',
+# 'gate_up' and 'down' the separate kernels those replace (timed for
+# comparison, not run by a step).
+KERNELS = ['qkv', 'attention', 'o', 'gate_up', 'down', 'lm_head', 'ffn', 'qkv_attention', 'token']
 # Launches of each kernel per decode token.
-PER_TOKEN = {'qkv_attention': 28, 'ffn': 28, 'lm_head': 1}
+PER_TOKEN = {'token': 1, 'lm_head': 1}
+# One layer's weights: QKV, O, gate/up, down (FP16).
+LAYER_WEIGHT_BYTES = (4096 * 1024 + 1024 * 2048 + 6144 * 1024 + 1024 * 3072) * 2
 # Algorithmic bytes per launch: FP16 weights + FP32 vectors read/written.
 KERNEL_BYTES = {
     'qkv': 4096 * 1024 * 2 + 1024 * 4 * 2 + 4096 * 4 + 8 * 1024 * 4,  # + the 8 down slices folded in
@@ -67,6 +71,12 @@ def kernel_bytes(kernel, n):
     """Algorithmic bytes of one launch with n cached positions."""
     if kernel == 'attention':
         return attention_bytes(n)
+    if kernel == 'token':
+        # Per layer: the weights, the K/V rows of n positions (one of them
+        # written), the two norm weights and the QK-norm weights; once: the
+        # embedding row read and the final residual written. The exchange
+        # words between workgroups stay in the L2s and are not counted.
+        return 28 * (LAYER_WEIGHT_BYTES + 8 * n * 128 * 2 * 2 + 2 * 1024 * 4 + 256 * 4) + 1024 * 2 + 1024 * 4
     if kernel == 'qkv_attention':
         # QKV and O weights, K/V rows, residual (+ the 8 down slices) in and
         # out, norm weights, the 16 partial O projections written.
@@ -77,14 +87,17 @@ def kernel_bytes(kernel, n):
 
 def kernel_replays(model, history, iterations=224):
     """Average duration of each decode kernel at the model's position (HIP
-    events on the engine stream, launches rotating over the layers). Timing
-    an attention kernel rewrites cached K/V and resets the model, so the
-    context `history` is prefilled again before the fused one."""
+    events on the engine stream; layer kernels rotate over the layers, the
+    token kernel replays whole steps). Timing an attention kernel or the
+    token kernel rewrites cached K/V and resets the model, so the context
+    `history` is prefilled again before each of those."""
     kernel_ms = {}
     for which in (0, 6, 3, 4, 5, 1):
         kernel_ms[KERNELS[which]] = model.time_kernel(which, iterations)
     model.prefill(history)
     kernel_ms['qkv_attention'] = model.time_kernel(7, iterations)
+    model.prefill(history)
+    kernel_ms['token'] = model.time_kernel(8, max(8, iterations // 28))
     return kernel_ms
 
 
@@ -107,12 +120,13 @@ def measured_traffic(kernel, position):
         parts = line.split()
         if len(parts) == 4 and parts[0] == 'traffic' and parts[1] == kernel:
             points.append((int(parts[2]), float(parts[3])))
-    if kernel not in ('attention', 'qkv_attention'):  # no dependence on the context
+    if kernel not in ('attention', 'qkv_attention', 'token'):  # no dependence on the context
         return (points[0][1], f'measured at position {points[0][0]}') if points else (None, 'not measured')
     # Paths: the separate attention kernels switch at 512 cached positions,
-    # the fused QKV + attention kernel at 256 (every workgroup attending its
-    # head over all positions up to there, 64-position passes beyond).
-    limit = FULL_ATTENTION_MAX if kernel == 'qkv_attention' else FUSED_ATTENTION_MAX
+    # the fused QKV + attention kernel and the token kernel at 256 (every
+    # workgroup attending its head over all positions up to there, passes of
+    # 64 positions split over the workgroups beyond).
+    limit = FUSED_ATTENTION_MAX if kernel == 'attention' else FULL_ATTENTION_MAX
     same = sorted(p for p in points if (p[0] <= limit) == (position <= limit))
     if any(p[0] == position for p in same):
         return dict(same)[position], f'measured at position {position}'
@@ -336,7 +350,8 @@ def main():
     parser.add_argument('--no-gemv', action='store_true', help='skip the isolated GEMV microbenchmark')
     parser.add_argument('--no-batch', action='store_true', help='skip the 8-sequence prefix-reuse workload')
     parser.add_argument('--pmc-kernel', choices=KERNELS,
-                        help='only run 29 launches of one decode kernel (hardware-counter passes)')
+                        help='only replay one decode kernel (28 + 28 layer launches, or 2 + 8 token-kernel '
+                             'steps) at one position (hardware-counter passes)')
     parser.add_argument('--pmc-positions', type=int,
                         help='cached positions for --pmc-kernel (default: where the timed region ends)')
     parser.add_argument('--pmc-prefill', type=int, nargs='?', const=1024, choices=(1024, 3968),
@@ -351,8 +366,8 @@ def main():
     if args.pmc_kernel:
         # Light run for hardware-counter passes (each profiled dispatch is
         # slow): one batched prefill up to the position the timed region of
-        # the default run ends at, then 28 launches of one decode kernel
-        # there (the same context the per-kernel timings below use).
+        # the default run ends at, then replays of one decode kernel there
+        # (the same context the per-kernel timings below use).
         from conftest import GOLDEN, PACK_CACHE, load_package
         q = load_package()
         prompts = json.loads((GOLDEN / 'prompts.json').read_text())
@@ -361,9 +376,12 @@ def main():
         prompt = (prompts['long_3968'] + prompts['prefill_1024'])[:position]
         model.prefill(prompt)
         which = KERNELS.index(args.pmc_kernel)
-        ms = model.time_kernel(which, 28)
+        launches = 8 if args.pmc_kernel == 'token' else 28
+        ms = model.time_kernel(which, launches)
         model.close()
-        print(json.dumps({'pmc_kernel': args.pmc_kernel, 'position': position, 'launches': 29, 'avg_ms': ms}))
+        warm = 2 if args.pmc_kernel == 'token' else 28
+        print(json.dumps({'pmc_kernel': args.pmc_kernel, 'position': position, 'launches': launches + warm,
+                          'avg_ms': ms}))
         return 0
     if args.pmc_prefill:
         from conftest import GOLDEN, PACK_CACHE, load_package

@@ -81,7 +81,8 @@ SIGNATURES = {
     'qwen_gpu_op_gemm_static': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     'qwen_gpu_op_gemm_swiglu': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                                               ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+                                               ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_void_p]),
     'qwen_gpu_op_norm_qkv': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p]),
     'qwen_gpu_op_norm_gate_up': (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -474,10 +475,12 @@ def gemm(a, w, c=None):
     return cd.to_array(np.float32, m * n).reshape(m, n)
 
 
-def gemm_swiglu(a, w):
+def gemm_swiglu(a, w, exponents=False):
     """Prefill gate/up GEMM with its SwiGLU epilogue: A FP32 [M, K], W FP16
     [N, K] holding N / 2 gate rows then N / 2 up rows. Returns the FP32
-    activation [M, N / 2] (the kernel's FP16 hi + lo planes summed)."""
+    activation [M, N / 2] (the kernel's FP16 hi + lo planes summed and scaled
+    by 2^exponent of each group of 8), and with exponents=True also those
+    exponents [M, N / 16]."""
     a = np.ascontiguousarray(a, np.float32)
     w = np.ascontiguousarray(w, np.float16)
     m, k = a.shape
@@ -486,11 +489,14 @@ def gemm_swiglu(a, w):
         raise ValueError(f'need W [N, K] with N % 256 == 0 and K % 64 == 0, got A {a.shape} W {w.shape}')
     ad, wd = DeviceBuffer.from_array(a), DeviceBuffer.from_array(w)
     hi, lo = DeviceBuffer(m * n // 2 * 2), DeviceBuffer(m * n // 2 * 2)
-    _check(_LIB.qwen_gpu_op_gemm_swiglu(ad.ptr, wd.ptr, hi.ptr, lo.ptr, m, n, k, None))
+    ex = DeviceBuffer(m * n // 16)
+    _check(_LIB.qwen_gpu_op_gemm_swiglu(ad.ptr, wd.ptr, hi.ptr, lo.ptr, ex.ptr, m, n, k, None))
     synchronize()
     h = hi.to_array(np.float16, m * n // 2).astype(np.float32)
     l = lo.to_array(np.float16, m * n // 2).astype(np.float32)
-    return (h + l).reshape(m, n // 2)
+    e = ex.to_array(np.uint8, m * n // 16).reshape(m, n // 16)
+    act = ((h + l).reshape(m, n // 16, 8) * np.exp2(e.astype(np.float32))[:, :, None]).reshape(m, n // 2)
+    return (act, e) if exponents else act
 
 
 def _vector(values, size, name):

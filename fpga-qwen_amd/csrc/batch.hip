@@ -69,9 +69,11 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
     __shared__ __align__(16) _Float16 xh[kMaxBatch][K + 8];
     __shared__ __align__(16) _Float16 xl[kMaxBatch][K + 8];
     __shared__ float part[WAVES][64][4];
+    __shared__ dev::SplitGuard guard;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, quad = lane >> 4;
     const int B = a.batch, o0 = blockIdx.x * kBatchRows;
+    guard.init(tid);
 
     // Loads complete in issue order per wave: inputs first (rows past the
     // batch repeat row B - 1 and are never stored), then the weights.
@@ -88,21 +90,38 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
             for (int s = 0; s < 4; ++s) wa[blk][s] = __builtin_nontemporal_load(wp + 16 * blk + 4 * s);
     }
     __builtin_amdgcn_sched_barrier(0);
+    auto split_rows = [&](bool scaled) {
+        float big = 0.f;
 #pragma unroll
-    for (int b = 0; b < kMaxBatch; ++b) {
-        const float e[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
-        half4 hi, lo;
+        for (int b = 0; b < kMaxBatch; ++b) {
+            const float down = scaled ? pow2(-guard.seq_e[b]) : 1.f;
+            const float e[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+            half4 hi, lo;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            _Float16 h, l;
-            split_half(e[k], h, l);
-            hi[k] = h;
-            lo[k] = l;
+            for (int k = 0; k < 4; ++k) {
+                big = fmaxf(big, fabsf(e[k]));
+                _Float16 h, l;
+                split_half(e[k] * down, h, l);
+                hi[k] = h;
+                lo[k] = l;
+            }
+            *reinterpret_cast<half4*>(&xh[b][4 * tid]) = hi;
+            *reinterpret_cast<half4*>(&xl[b][4 * tid]) = lo;
         }
-        *reinterpret_cast<half4*>(&xh[b][4 * tid]) = hi;
-        *reinterpret_cast<half4*>(&xl[b][4 * tid]) = lo;
-    }
+        return big;
+    };
+    guard.post(split_rows(false), lane, wave);
     __syncthreads();
+    if (guard.needed(WAVES)) {
+#pragma unroll
+        for (int b = 0; b < kMaxBatch; ++b)
+            guard.offer(b, fmaxf(fmaxf(fabsf(v[b].x), fabsf(v[b].y)), fmaxf(fabsf(v[b].z), fabsf(v[b].w))));
+        __syncthreads();
+        if (tid < kMaxBatch) guard.seq_e[tid] = guard.exponent(tid);
+        __syncthreads();
+        split_rows(true);
+        __syncthreads();
+    }
 
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -133,7 +152,7 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
     if constexpr (WAVES >= 8) y = y + quad_sum(4);
     if constexpr (WAVES >= 12) y = y + quad_sum(8);
     const int eb = lane & 15;
-    if (eb < B) a.out[eb][o0 + 4 * (lane >> 4) + wave] = y;
+    if (eb < B) a.out[eb][o0 + 4 * (lane >> 4) + wave] = y * guard.up(eb & 7);
 }
 
 // Norm + gate/up + SwiGLU + down + residual of one layer for the batched
@@ -169,6 +188,54 @@ struct BatchFfnArgs {
 
 constexpr int kFfnOctant = kFFN / 8;  // 384 activation columns per XCD
 static_assert(kBatchActWords == 8 * kMaxBatch * kFfnOctant, "activation words per XCD octant");
+
+// The normalized rows (x * inv) * w of every sequence (elements 2 tid and
+// 2 tid + 1) as FP16 hi / lo in LDS under the range guard; with `hidden`,
+// also the unscaled FP32 rows of the first `batch` sequences. Ends with a
+// barrier.
+__device__ __forceinline__ void split_normalized(const float2 (&xv)[kMaxBatch], float2 wn,
+                                                 const float (&inv_row)[kMaxBatch],
+                                                 _Float16 (&xh)[kMaxBatch][kHidden + 8],
+                                                 _Float16 (&xl)[kMaxBatch][kHidden + 8], dev::SplitGuard& guard,
+                                                 int tid, float* const* hidden, int batch = 0) {
+    const int lane = tid & 63, wave = tid >> 6;
+    auto split_rows = [&](bool scaled) {
+        float big = 0.f;
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float inv = inv_row[bb];
+            float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
+            if (!scaled && hidden != nullptr && bb < batch)
+                reinterpret_cast<float2*>(hidden[bb])[tid] = make_float2(n0, n1);
+            big = fmaxf(big, fmaxf(fabsf(n0), fabsf(n1)));
+            if (scaled) {
+                const float down = pow2(-guard.seq_e[bb]);
+                n0 = n0 * down;
+                n1 = n1 * down;
+            }
+            _Float16 h0, l0, h1, l1;
+            split_half(n0, h0, l0);
+            split_half(n1, h1, l1);
+            *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
+            *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
+        }
+        return big;
+    };
+    guard.post(split_rows(false), lane, wave);
+    __syncthreads();
+    if (guard.needed(8)) {
+#pragma unroll
+        for (int bb = 0; bb < kMaxBatch; ++bb) {
+            const float inv = inv_row[bb];
+            guard.offer(bb, fmaxf(fabsf((xv[bb].x * inv) * wn.x), fabsf((xv[bb].y * inv) * wn.y)));
+        }
+        __syncthreads();
+        if (tid < kMaxBatch) guard.seq_e[tid] = guard.exponent(tid);
+        __syncthreads();
+        split_rows(true);
+        __syncthreads();
+    }
+}
 
 __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
     const int xo = blockIdx.x & 7, r = blockIdx.x >> 3;
@@ -219,6 +286,11 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
     __shared__ float part[8][2][64][4];
     __shared__ __align__(16) _Float16 ah[kMaxBatch][kFfnOctant + 8];
     __shared__ __align__(16) _Float16 al[kMaxBatch][kFfnOctant + 8];
+    // Range guards (decode_dev.hpp): the normalized rows, then the XCD's
+    // activations of each sequence.
+    __shared__ dev::SplitGuard guard, act_guard;
+    guard.init(tid);
+    act_guard.init(tid);
 
     // 1. RMSNorm of every row (reduce-scatter inside each wave: lane l ends
     // with its wave's total of row (l >> 3) & 7; then the 8 waves in order).
@@ -253,17 +325,7 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
             inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(kHidden) + 1e-6f);
         }
         __syncthreads();
-#pragma unroll
-        for (int bb = 0; bb < kMaxBatch; ++bb) {
-            const float inv = inv_row[bb];
-            const float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
-            _Float16 h0, l0, h1, l1;
-            split_half(n0, h0, l0);
-            split_half(n1, h1, l1);
-            *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
-            *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
-        }
-        __syncthreads();
+        split_normalized(xv, wn, inv_row, xh, xl, guard, tid, nullptr);
     }
 
     // 2. Gate/up and SwiGLU.
@@ -296,8 +358,8 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
                        ((part[4][t][lane][wave] + part[5][t][lane][wave]) +
                         (part[6][t][lane][wave] + part[7][t][lane][wave]));
             };
-            const float gate = tree(0), up = tree(1);
             const int row = 4 * (lane >> 4) + wave, seq = lane & 15;
+            const float gate = tree(0) * guard.up(seq & 7), up = tree(1) * guard.up(seq & 7);
             if (row < 12 && seq < B) {
                 const float half_gate = gate * 0.5f;
                 const float th = tanhf(half_gate);
@@ -321,15 +383,30 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
             if (seq < B) want |= 1u << k;
         }
         ok = exchange_gather<6>(words, a.tag, got, want);
+        auto split_acts = [&](bool scaled) {
+            float big = 0.f;
 #pragma unroll
-        for (int k = 0; k < 6; ++k) {
-            const int idx = tid + 512 * k, seq = idx / kFfnOctant, c = idx % kFfnOctant;
-            _Float16 h, l;
-            split_half(got[k], h, l);
-            ah[seq][c] = h;
-            al[seq][c] = l;
-        }
+            for (int k = 0; k < 6; ++k) {
+                const int idx = tid + 512 * k, seq = idx / kFfnOctant, c = idx % kFfnOctant;
+                big = fmaxf(big, fabsf(got[k]));
+                _Float16 h, l;
+                split_half(scaled ? got[k] * pow2(-act_guard.seq_e[seq]) : got[k], h, l);
+                ah[seq][c] = h;
+                al[seq][c] = l;
+            }
+            return big;
+        };
+        act_guard.post(split_acts(false), lane, wave);
         __syncthreads();
+        if (act_guard.needed(8)) {
+#pragma unroll
+            for (int k = 0; k < 6; ++k) act_guard.offer((tid + 512 * k) / kFfnOctant, fabsf(got[k]));
+            __syncthreads();
+            if (tid < kMaxBatch) act_guard.seq_e[tid] = act_guard.exponent(tid);
+            __syncthreads();
+            split_acts(true);
+            __syncthreads();
+        }
     }
     // Down share of rows 32 r .. 32 r + 31 over this XCD's columns.
     {
@@ -350,9 +427,10 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
         // 4 (lane / 16) + (wave & 3), sequence lane % 16); the 4 K ranges of
         // the tile (waves tt2, tt2 + 2, tt2 + 4, tt2 + 6) in fixed order.
         const int tt2 = wave >> 2, e4 = wave & 3;
-        const float y = (part[tt2][0][lane][e4] + part[tt2 + 2][0][lane][e4]) +
-                        (part[tt2 + 4][0][lane][e4] + part[tt2 + 6][0][lane][e4]);
         const int row = 32 * r + 16 * tt2 + 4 * (lane >> 4) + e4, seq = lane & 15;
+        const float y = ((part[tt2][0][lane][e4] + part[tt2 + 2][0][lane][e4]) +
+                         (part[tt2 + 4][0][lane][e4] + part[tt2 + 6][0][lane][e4])) *
+                        act_guard.up(seq & 7);
         if (seq < B) exchange_put_through(a.share_words + (size_t(row) * kMaxBatch + seq) * 8 + xo, y, a.tag);
     }
 
@@ -439,6 +517,8 @@ __global__ __launch_bounds__(512) void lm_head_batch_kernel(const BatchLmArgs a)
     __shared__ double nred[8][kMaxBatch];
     __shared__ float inv_row[kMaxBatch];
     __shared__ float part[2][8][64][4];
+    __shared__ dev::SplitGuard guard;
+    guard.init(tid);
     // RMSNorm of every row (as in ffn_batch_kernel).
     {
         double sq[kMaxBatch];
@@ -471,18 +551,7 @@ __global__ __launch_bounds__(512) void lm_head_batch_kernel(const BatchLmArgs a)
             inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(kHidden) + 1e-6f);
         }
         __syncthreads();
-#pragma unroll
-        for (int bb = 0; bb < kMaxBatch; ++bb) {
-            const float inv = inv_row[bb];
-            const float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
-            if (w == 0 && bb < B) reinterpret_cast<float2*>(a.hidden[bb])[tid] = make_float2(n0, n1);
-            _Float16 h0, l0, h1, l1;
-            split_half(n0, h0, l0);
-            split_half(n1, h1, l1);
-            *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
-            *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
-        }
-        __syncthreads();
+        split_normalized(xv, wn, inv_row, xh, xl, guard, tid, w == 0 ? a.hidden : nullptr, B);
     }
 
     float bv = -INFINITY, lg[kLmTilesPerGroup];
@@ -511,7 +580,8 @@ __global__ __launch_bounds__(512) void lm_head_batch_kernel(const BatchLmArgs a)
             __syncthreads();
             if (wave < 4) {
                 const auto f = [&](int v8) { return part[k & 1][v8][lane][wave]; };
-                const float y = ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
+                const float y = (((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)))) *
+                                guard.up(eb & 7);
                 const int row = kBatchRows * (w + kBatchLmGroups * k) + erow;
                 lg[k] = y;
                 const bool use = k < ntiles && eb < B;

@@ -326,14 +326,15 @@ int qwen_gpu_op_gemm_static(const float* a, const uint16_t* w, float* c, int m, 
     });
 }
 
-int qwen_gpu_op_gemm_swiglu(const float* a, const uint16_t* w, uint16_t* act_hi, uint16_t* act_lo, int m, int n,
-                            int k, void* stream) {
+int qwen_gpu_op_gemm_swiglu(const float* a, const uint16_t* w, uint16_t* act_hi, uint16_t* act_lo, uint8_t* act_exp,
+                            int m, int n, int k, void* stream) {
     return guarded([&] {
         need(a, "a");
         need(w, "w");
         need(act_hi, "act_hi");
         need(act_lo, "act_lo");
-        qwen_hip::launch_gemm_swiglu(a, w, act_hi, act_lo, m, n, k, static_cast<hipStream_t>(stream));
+        need(act_exp, "act_exp");
+        qwen_hip::launch_gemm_swiglu(a, w, act_hi, act_lo, act_exp, m, n, k, static_cast<hipStream_t>(stream));
         hip_ok(hipGetLastError());
     });
 }

@@ -1804,6 +1804,8 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     __shared__ uint16_t kcur[128], vcur[128];
     __shared__ double red[4][2];
     __shared__ float wm[8][2], wl[8][2];
+    __shared__ dev::SplitGuard guard;
+    guard.init(tid);
 
     if constexpr (EMBED) {
 #pragma unroll
@@ -1846,17 +1848,42 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
             inv_row[tid] = 1.0f / __builtin_sqrtf(static_cast<float>(total) / static_cast<float>(kHidden) + 1e-6f);
         }
         __syncthreads();
+        // Normalized rows as FP16 hi / lo, scaled by 2^-e per sequence only
+        // when a row reaches the FP16 limit (the guard's slow path).
+        auto split_rows = [&](bool scaled) {
+            float big = 0.f;
 #pragma unroll
-        for (int bb = 0; bb < kMaxBatch; ++bb) {
-            const float inv = inv_row[bb];
-            const float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
-            _Float16 h0, l0, h1, l1;
-            split_half(n0, h0, l0);
-            split_half(n1, h1, l1);
-            *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
-            *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
-        }
+            for (int bb = 0; bb < kMaxBatch; ++bb) {
+                const float inv = inv_row[bb];
+                float n0 = (xv[bb].x * inv) * wn.x, n1 = (xv[bb].y * inv) * wn.y;
+                big = fmaxf(big, fmaxf(fabsf(n0), fabsf(n1)));
+                if (scaled) {
+                    const float down = pow2(-guard.seq_e[bb]);
+                    n0 = n0 * down;
+                    n1 = n1 * down;
+                }
+                _Float16 h0, l0, h1, l1;
+                split_half(n0, h0, l0);
+                split_half(n1, h1, l1);
+                *reinterpret_cast<half2_t*>(&xh[bb][2 * tid]) = half2_t{h0, h1};
+                *reinterpret_cast<half2_t*>(&xl[bb][2 * tid]) = half2_t{l0, l1};
+            }
+            return big;
+        };
+        guard.post(split_rows(false), lane, wave);
         __syncthreads();
+        if (guard.needed(8)) {
+#pragma unroll
+            for (int bb = 0; bb < kMaxBatch; ++bb) {
+                const float inv = inv_row[bb];
+                guard.offer(bb, fmaxf(fabsf((xv[bb].x * inv) * wn.x), fabsf((xv[bb].y * inv) * wn.y)));
+            }
+            __syncthreads();
+            if (tid < kMaxBatch) guard.seq_e[tid] = guard.exponent(tid);
+            __syncthreads();
+            split_rows(true);
+            __syncthreads();
+        }
     }
 
     // QKV tiles of this workgroup: r, then r + W, ... when W < 32 (the first
@@ -1879,8 +1906,8 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         __syncthreads();
         if (wave < 4) {  // element (row 4 (lane / 16) + wave, sequence lane % 16)
             const auto f = [&](int v8) { return qpart[v8][lane][wave]; };
-            const float y = ((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)));
             const int seq = lane & 15, row = 16 * tr + 4 * (lane >> 4) + wave;
+            const float y = (((f(0) + f(1)) + (f(2) + f(3))) + ((f(4) + f(5)) + (f(6) + f(7)))) * guard.up(seq & 7);
             if (seq < B) exchange_put(args.exchange + (size_t(g) * kMaxBatch + seq) * 512 + row, y, args.tag);
         }
         __syncthreads();
@@ -2163,6 +2190,8 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
             if ((idx >> 8) < B) want |= 1u << k;
         }
         ok = exchange_gather<4>(words, args.tag, got, want);
+        // Attention rows are convex combinations of FP16 values: they fit
+        // FP16 without the range guard.
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int idx = tid + 512 * k;

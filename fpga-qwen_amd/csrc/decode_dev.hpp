@@ -85,6 +85,52 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, xor_lanes<32>(v));
+    v = fmaxf(v, xor_lanes<16>(v));
+    v = fmaxf(v, xor_lanes<8>(v));
+    v = fmaxf(v, xor_lanes<4>(v));
+    v = fmaxf(v, xor_lanes<2>(v));
+    return fmaxf(v, xor_lanes<1>(v));
+}
+
+// Range guard of the batched matrix-core inputs (split_exponent): a launch
+// first splits every sequence's values unscaled and each wave records the
+// largest magnitude it split (wave_big). Only if one of them reaches the FP16
+// limit (rare: every wave sees the same LDS, so all take the same branch)
+// does the workgroup find each sequence's exact maximum and split again as
+// v * 2^-e; the products of sequence s are scaled back by 2^e[s]
+// (SplitGuard::up, 1 while no sequence was scaled).
+struct SplitGuard {
+    float wave_big[16];
+    unsigned seq_big[kMaxBatch];
+    int seq_e[kMaxBatch];
+
+    // Before the first barrier of the launch.
+    __device__ void init(int tid) {
+        if (tid < kMaxBatch) {
+            seq_big[tid] = 0u;
+            seq_e[tid] = 0;
+        }
+    }
+    // Every wave after its unscaled splits, before the barrier that ends them.
+    __device__ void post(float big, int lane, int wave) {
+        big = wave_max(big);
+        if (lane == 0) wave_big[wave] = big;
+    }
+    // After that barrier.
+    __device__ bool needed(int waves) const {
+        float big = 0.f;
+        for (int w = 0; w < waves; ++w) big = fmaxf(big, wave_big[w]);
+        return big >= kSplitLimit;
+    }
+    // Slow path: every thread offers the maximum of its values of sequence
+    // s; after a barrier, exponent(s) is that sequence's exponent.
+    __device__ void offer(int s, float big) { atomicMax(&seq_big[s], __float_as_uint(big)); }
+    __device__ int exponent(int s) const { return split_exponent(__uint_as_float(seq_big[s])); }
+    __device__ float up(int s) const { return pow2(seq_e[s]); }
+};
+
 // Position of activation j in the permuted LDS vector: j = 64b + 8i + c is
 // stored at 64b + 8c + i, so chain c reads its 8 values contiguously.
 __device__ __forceinline__ int xperm(int j) { return (j & ~63) | ((j & 7) << 3) | ((j >> 3) & 7); }

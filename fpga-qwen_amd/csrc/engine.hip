@@ -323,6 +323,9 @@ void Engine::init_state() {
     ps.act_hi = device_alloc<uint16_t>(prows * kFFN);
     ps.act_lo = device_alloc<uint16_t>(prows * kFFN);
     ps.part = device_alloc<float>(4 * prows * kHidden);
+    ps.row_exp = device_alloc<int>(prows);
+    ps.act_flag = device_alloc<int>(4 * prows);
+    ps.act_exp = device_alloc<uint8_t>(prows * (kFFN / 8));
     ids_dev_ = device_alloc<int>(size_t(ctx));
     HIP_CHECK(hipHostMalloc(&pinned, sizeof(int) * size_t(ctx), hipHostMallocDefault));
     ids_host_ = static_cast<int*>(pinned);
@@ -445,28 +448,9 @@ void Engine::check_stall(int slot) const {
 
 void Engine::run_token(int token, bool head, int result_slot) {
     if (token_kernel_) {
-        TokenLaunch t{};
-        for (int l = 0; l < kLayers; ++l) {
-            const LayerDevice& L = layers_[l];
-            t.layers[l] = TokenLayer{L.qkv_t, L.o_n, L.gateup_t, L.down_t, L.in_norm, L.post_norm, L.qk_norm, L.keys};
-        }
-        t.layer_count = kLayers;
-        t.embed = embed_;
-        t.token[0] = token;
-        t.rows = 1;
-        t.pos = pos_;
-        t.context = options_.context;
-        t.cosines = cosines_;
-        t.sines = sines_;
-        t.x_out = scratch_.x;
-        t.words = token_words_;
-        t.stall = scratch_.stall;
-        t.scale = 1.0f / std::sqrt(128.0f);
-        t.tag = reserve_tags(kLayers);
-        t.spins = token_spins_;
+        TokenLaunch t = token_launch(1, pos_, token, 0, scratch_.x);
         t.withhold = token_withhold_;
         token_withhold_ = -1;  // the test knob withholds one post, once
-        t.prefetch = token_prefetch_ ? 1 : 0;
         launch_token_layers(t, stream_);
         if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
         HIP_CHECK(hipGetLastError());
@@ -666,7 +650,9 @@ int Engine::greedy() {
 // every weight once for both (the token kernel's two-row form: row 1 attends
 // to row 0's new K/V, each row with a single step's arithmetic), then the
 // head for both; K/V rows written at pos_ and pos_ + 1, pos_ unchanged.
-void Engine::run_pair(int first, int second) {
+// The token kernel's launch record: every layer, `rows` rows from position
+// pos, fresh tags.
+TokenLaunch Engine::token_launch(int rows, int pos, int first, int second, float* x_out) {
     TokenLaunch t{};
     for (int l = 0; l < kLayers; ++l) {
         const LayerDevice& L = layers_[l];
@@ -676,12 +662,12 @@ void Engine::run_pair(int first, int second) {
     t.embed = embed_;
     t.token[0] = first;
     t.token[1] = second;
-    t.rows = 2;
-    t.pos = pos_;
+    t.rows = rows;
+    t.pos = pos;
     t.context = options_.context;
     t.cosines = cosines_;
     t.sines = sines_;
-    t.x_out = pair_.x;
+    t.x_out = x_out;
     t.words = token_words_;
     t.stall = scratch_.stall;
     t.scale = 1.0f / std::sqrt(128.0f);
@@ -689,7 +675,11 @@ void Engine::run_pair(int first, int second) {
     t.spins = token_spins_;
     t.withhold = -1;
     t.prefetch = token_prefetch_ ? 1 : 0;
-    launch_token_layers(t, stream_);
+    return t;
+}
+
+void Engine::run_pair(int first, int second) {
+    launch_token_layers(token_launch(2, pos_, first, second, pair_.x), stream_);
     launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, stream_);
     HIP_CHECK(hipGetLastError());
 }
@@ -821,31 +811,35 @@ float Engine::time_kernel(int which, int iterations) {
     require(pos_ > 0 && !pending_, "time_kernel needs a current position");
     std::lock_guard<std::mutex> hold(launch_lock());
     HIP_CHECK(hipStreamSynchronize(stream_));
-    require(which >= 0 && which <= 7 && iterations > 0, "time_kernel: bad arguments");
+    require(which >= 0 && which <= 8 && iterations > 0, "time_kernel: bad arguments");
     if (which == 2) return 0.f;  // O runs with the attention (1)
     require(which != 6 || fused_ffn_, "time_kernel: the fused FFN kernel is switched off");
     require(which != 7 || fused_attn_, "time_kernel: the fused QKV + attention kernel is switched off");
+    require(which != 8 || token_kernel_, "time_kernel: the token kernel is switched off");
     // Replays kernels of the last processed position; the state is reset
     // afterwards. Layer kernels rotate over all 28 layers so that, as in a
     // real step, their weights (about 880 MB in total) stream from HBM rather
     // than from the 256 MB Infinity Cache.
     // 0, 1, 3 and 4 time the separate norm+QKV, attention, norm+gate/up and
     // down kernels (with the fused kernels on, a step runs none of them), 6
-    // the fused FFN kernel, 7 the fused QKV + attention + O kernel.
+    // the fused FFN kernel, 7 the fused QKV + attention + O kernel, 8 the
+    // token kernel (all 28 layers in one launch).
     const int layers = kLayers;
     int layer = 0;
     auto launch = [&] {
         LayerFlow flow = layer_flow(layer);
         if (which == 3 || which == 4) flow.ffn_tag = 0;
         if (which == 0 || which == 1) flow.attn_tag = 0;
-        if (which == 5)
+        if (which == 8)
+            launch_token_layers(token_launch(1, pos_ - 1, 0, 0, scratch_.x), stream_);
+        else if (which == 5)
             launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
         else
             launch_layer_kernel(which == 6 ? 3 : which == 7 ? 0 : which, layers_[layer], nullptr, pos_ - 1, 0,
                                 cosines_, sines_, options_.context, scratch_, flow, stream_);
         layer = (layer + 1) % layers;
     };
-    for (int i = 0; i < layers; ++i) launch();
+    for (int i = 0; i < (which == 8 ? 2 : layers); ++i) launch();
     hipEvent_t start, stop;
     HIP_CHECK(hipEventCreate(&start));
     HIP_CHECK(hipEventCreate(&stop));
@@ -858,8 +852,9 @@ float Engine::time_kernel(int which, int iterations) {
     (void)hipEventDestroy(start);
     (void)hipEventDestroy(stop);
     // The replayed kernels overwrite the residual stream and logits; the
-    // attention kernel also rewrites cached K/V, so it resets the model.
-    if (which == 1 || which == 7)
+    // attention and token kernels also rewrite cached K/V, so they reset the
+    // model.
+    if (which == 1 || which == 7 || which == 8)
         reset();
     else
         invalidate();

@@ -89,7 +89,8 @@ public:
 
     // Average duration (ms) of one standalone launch of a decode kernel,
     // timed with HIP events on the engine stream. which: 0 qkv, 1 attention,
-    // 2 o, 3 gate/up, 4 down, 5 lm_head. Requires position() > 0.
+    // 2 o, 3 gate/up, 4 down, 5 lm_head, 6 fused FFN, 7 fused QKV +
+    // attention + O, 8 token kernel (all layers). Requires position() > 0.
     float time_kernel(int which, int iterations);
     hipStream_t stream() const { return stream_; }
 
@@ -107,6 +108,7 @@ private:
     void roll_back(int position);
     void run_token(int token, bool head, int result_slot);
     void run_pair(int first, int second);
+    TokenLaunch token_launch(int rows, int pos, int first, int second, float* x_out);
     LayerFlow layer_flow(int layer);
     uint32_t next_tag();
     // `count` consecutive tags (none of them 0) for one launch.

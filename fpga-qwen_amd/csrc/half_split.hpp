@@ -31,4 +31,24 @@ __device__ __forceinline__ void split_half(float v, _Float16& hi, _Float16& lo) 
     lo = to_half(v - static_cast<float>(hi));
 }
 
+// Range guard of the split. FP32 values from 65520 up round to an infinite
+// FP16 hi (and a NaN lo), where the FP32 reference carries on. A group of
+// values that feeds one dot product (a row of a GEMM operand, or a slice of
+// one) is therefore split as v * 2^-e with e the smallest exponent that
+// brings its largest magnitude below 65504, and the FP32 product is scaled
+// back by 2^e: both scalings are exact, so the result is the unscaled
+// product's, and e = 0 (no scaling at all) wherever the group fits, which
+// leaves those bits unchanged. Non-finite maxima keep e = 0: they propagate
+// as the reference's FP32 arithmetic would.
+inline constexpr float kSplitLimit = 65504.f;
+
+__device__ __forceinline__ int split_exponent(float max_abs) {
+    if (!(max_abs >= kSplitLimit) || max_abs == __builtin_huge_valf()) return 0;
+    // max_abs in [2^k, 2^(k+1)), k >= 15: v * 2^-(k - 14) lies below 2^15.
+    return ((__builtin_bit_cast(int, max_abs) >> 23) - 127) - 14;
+}
+
+// 2^e as an FP32 value, e in [-126, 127].
+__device__ __forceinline__ float pow2(int e) { return __builtin_bit_cast(float, (127 + e) << 23); }
+
 }  // namespace qwen_hip

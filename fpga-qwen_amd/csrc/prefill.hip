@@ -86,6 +86,17 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ ((r & 1) << 2)) &
 // Work fused into the epilogue. QKV (EPI 4): QK-norm, RoPE and the K/V cache
 // writes of engine/core.cpp:395-406. Gate/up (EPI 3): SwiGLU, written as the
 // FP16 hi / lo planes the down GEMM reads.
+//
+// Range guard of the FP16 split (split_exponent): A row m that its producer
+// split as a * 2^-row_exp[m] has its products scaled back by 2^row_exp[m]
+// (EPI 0, 1, 3, 4; row_exp null: no row was scaled). The SwiGLU epilogue
+// splits each group of 8 activations with its own exponent, stored in
+// act_exp [M][N / 16], and raises act_flag [M][4] (one word per K range of
+// the down GEMM, cleared by the kernel before the gate/up GEMM) to the
+// largest exponent in the range. The down GEMM (EPI 2 with act_flag) runs
+// its plain K loop, and a workgroup whose rows saw a nonzero flag runs the
+// loop again with every group rescaled in LDS to its row's flag exponent
+// and the products scaled back: a row that fits keeps its bits.
 struct GemmEpilogue {
     const float* q_norm;
     const float* k_norm;
@@ -97,7 +108,15 @@ struct GemmEpilogue {
     int context;
     uint16_t* act_hi;
     uint16_t* act_lo;
+    const int* row_exp;
+    int* act_flag;
+    uint8_t* act_exp;
 };
+
+// Exponent of row m in row_exp (0 without one).
+__device__ __forceinline__ float row_scale(const int* row_exp, int m) {
+    return row_exp ? pow2(row_exp[m]) : 1.f;
+}
 
 // FP32 value -> the FP16 hi / lo pair the GEMMs read (hi = fp16(v), lo = fp16(v - hi)).
 __device__ __forceinline__ void split_store(float v, uint16_t* hi, uint16_t* lo, size_t i) {
@@ -121,6 +140,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(n >= 0 && n < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+
+// lgkmcnt == 0 (this wave's LDS accesses have completed).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
 
 // Workgroup barrier without a memory fence: the waits before it already
 // cover the direct-to-LDS loads (a fenced barrier would wait for every load
@@ -197,53 +219,105 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
                 load_lds16(src[j] + kt * kTileK, stage + 1024 * (wave + S::kWaves * j));
     };
 
-    floatx16 acc[TI][TJ];
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int jt = 0; jt < TJ; ++jt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][jt][r] = 0.f;
+    // Range guard of the down GEMM (EPI 2 with act_flag): the flags of this
+    // workgroup's rows in its K range (lane l: rows m0 + l and m0 + 64 + l),
+    // loaded before the stream so that they have arrived when the loop ends.
+    int flag0 = 0, flag1 = 0;
+    if constexpr (EPI == 2) {
+        if (ep.act_flag != nullptr && lane < BM) {
+            flag0 = ep.act_flag[size_t(min(m0 + lane, M - 1)) * 4 + blockIdx.z];
+            if (BM > 64) flag1 = ep.act_flag[size_t(min(m0 + 64 + lane, M - 1)) * 4 + blockIdx.z];
+        }
+    }
 
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s)
-        if (s < nk) issue(s);
+    floatx16 acc[TI][TJ];
     const int fr = lane & 31;
-    for (int kt = 0; kt < nk; ++kt) {
-        // Step kt has landed once no more than the later steps' loads are
-        // pending; the barrier then also tells every wave that all waves are
-        // done reading the stage the next issue overwrites.
-        if (kt + kStages - 2 < nk)
-            wait_vmcnt<(kStages - 2) * kLoads>();
-        else
-            wait_vmcnt<0>();
-        stage_barrier();
-        if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
-        if (mma) {
-            const unsigned char* stage = smem + (kt % kStages) * kStageBytes;
+    // Rescales the A groups of stage kt in LDS to their row's flag
+    // exponent (the second pass of a guarded down GEMM): exact, being
+    // multiplications of FP16 values by powers of two no greater than 1.
+    auto rescale_stage = [&](int kt) {
+        unsigned char* stage = smem + (kt % kStages) * kStageBytes;
+        for (int q = tid; q < kASlots; q += kThreads) {
+            const int r = q >> 3, p = (q & 7) ^ swz(r), m = min(m0 + r, M - 1);
+            const int er = ep.act_flag[size_t(m) * 4 + blockIdx.z];
+            if (er != 0) {
+                const int e8 = ep.act_exp[size_t(m) * (K / 8) + (kz + kt * kTileK) / 8 + p];
+                const float sc = pow2(e8 - er);
+                half8* h = reinterpret_cast<half8*>(stage + 16 * q);
+                half8* l = reinterpret_cast<half8*>(stage + 16 * (kASlots + q));
+                half8 hv = *h, lv = *l;
 #pragma unroll
-            for (int sub = 0; sub < 4; ++sub) {
-                const int p = 2 * sub + (lane >> 5);  // k = 16 sub + 8 (lane / 32) .. + 7 of the step
-                half8 ah[TI], al[TI], bb[TJ];
-#pragma unroll
-                for (int i = 0; i < TI; ++i) {
-                    const int ra = (wm * TI + i) * 32 + fr, sa = 8 * ra + (p ^ swz(ra));
-                    ah[i] = *reinterpret_cast<const half8*>(stage + 16 * sa);
-                    al[i] = *reinterpret_cast<const half8*>(stage + 16 * (kASlots + sa));
+                for (int e = 0; e < 8; ++e) {
+                    hv[e] = static_cast<_Float16>(static_cast<float>(hv[e]) * sc);
+                    lv[e] = static_cast<_Float16>(static_cast<float>(lv[e]) * sc);
                 }
+                *h = hv;
+                *l = lv;
+            }
+        }
+    };
+    auto k_loop = [&](auto rescale_tag) {
+        constexpr bool kRescale = decltype(rescale_tag)::value;
 #pragma unroll
-                for (int jt = 0; jt < TJ; ++jt) {
-                    const int rb = wn * (BN / S::WC) + 32 * jt + fr;
-                    bb[jt] = *reinterpret_cast<const half8*>(stage + 16 * (2 * kASlots + 8 * rb + (p ^ swz(rb))));
-                }
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int i = 0; i < TI; ++i)
+            for (int jt = 0; jt < TJ; ++jt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][jt][r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < kStages - 1; ++s)
+            if (s < nk) issue(s);
+        for (int kt = 0; kt < nk; ++kt) {
+            // Step kt has landed once no more than the later steps' loads are
+            // pending; the barrier then also tells every wave that all waves are
+            // done reading the stage the next issue overwrites.
+            if (kt + kStages - 2 < nk)
+                wait_vmcnt<(kStages - 2) * kLoads>();
+            else
+                wait_vmcnt<0>();
+            stage_barrier();
+            if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
+            if constexpr (kRescale) {
+                rescale_stage(kt);
+                wait_lgkm0();
+                stage_barrier();
+            }
+            if (mma) {
+                const unsigned char* stage = smem + (kt % kStages) * kStageBytes;
+#pragma unroll
+                for (int sub = 0; sub < 4; ++sub) {
+                    const int p = 2 * sub + (lane >> 5);  // k = 16 sub + 8 (lane / 32) .. + 7 of the step
+                    half8 ah[TI], al[TI], bb[TJ];
+#pragma unroll
+                    for (int i = 0; i < TI; ++i) {
+                        const int ra = (wm * TI + i) * 32 + fr, sa = 8 * ra + (p ^ swz(ra));
+                        ah[i] = *reinterpret_cast<const half8*>(stage + 16 * sa);
+                        al[i] = *reinterpret_cast<const half8*>(stage + 16 * (kASlots + sa));
+                    }
 #pragma unroll
                     for (int jt = 0; jt < TJ; ++jt) {
-                        acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bb[jt], acc[i][jt], 0, 0, 0);
-                        acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bb[jt], acc[i][jt], 0, 0, 0);
+                        const int rb = wn * (BN / S::WC) + 32 * jt + fr;
+                        bb[jt] = *reinterpret_cast<const half8*>(stage + 16 * (2 * kASlots + 8 * rb + (p ^ swz(rb))));
                     }
+#pragma unroll
+                    for (int i = 0; i < TI; ++i)
+#pragma unroll
+                        for (int jt = 0; jt < TJ; ++jt) {
+                            acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bb[jt], acc[i][jt], 0, 0, 0);
+                            acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bb[jt], acc[i][jt], 0, 0, 0);
+                        }
+                }
             }
+        }
+    };
+    k_loop(std::false_type{});
+    // Every wave read the same flags, so every wave takes the same branch.
+    bool rescaled = false;
+    if constexpr (EPI == 2) {
+        if (ep.act_flag != nullptr && __builtin_amdgcn_ballot_w64(flag0 != 0 || flag1 != 0) != 0) {
+            rescaled = true;
+            stage_barrier();  // every wave is done with the stages (all loads were waited for)
+            k_loop(std::true_type{});
         }
     }
 
@@ -269,7 +343,14 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
             const int row = q / (BN / 4), c4 = q % (BN / 4), m = m0 + row;
             if (m < M) {
                 float4* c = reinterpret_cast<float4*>(C + (size_t(blockIdx.z) * M + m) * N + n0) + c4;
-                const float4 v = *reinterpret_cast<const float4*>(&ct[row][4 * c4]);
+                float4 v = *reinterpret_cast<const float4*>(&ct[row][4 * c4]);
+                float sc = 1.f;
+                if constexpr (EPI == 2) {
+                    if (rescaled) sc = pow2(ep.act_flag[size_t(m) * 4 + blockIdx.z]);
+                } else {
+                    sc = row_scale(ep.row_exp, m);
+                }
+                v = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
                 if constexpr (EPI == 1) {
                     const float4 o = *c;
                     *c = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
@@ -286,21 +367,32 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
         for (int q = tid; q < BM * (BN / 16); q += kThreads) {
             const int row = q / (BN / 16), c8 = 8 * (q % (BN / 16)), m = m0 + row;
             if (m < M) {
+                const float sc = row_scale(ep.row_exp, m);
+                float o[8], big = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float gate = ct[row][c8 + e] * sc, up = ct[row][BN / 2 + c8 + e] * sc;
+                    const float half_gate = gate * 0.5f;
+                    const float t = tanhf(half_gate);
+                    o[e] = gate * (0.5f + 0.5f * t) * up;
+                    big = fmaxf(big, fabsf(o[e]));
+                }
+                // This group's exponent; the K range's flag holds the largest.
+                const int e8 = split_exponent(big), col = n0 / 2 + c8;
+                const float down = pow2(-e8);
                 half8 hi, lo;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float gate = ct[row][c8 + e], up = ct[row][BN / 2 + c8 + e];
-                    const float half_gate = gate * 0.5f;
-                    const float t = tanhf(half_gate);
-                    const float o = gate * (0.5f + 0.5f * t) * up;
                     _Float16 h, l;
-                    split_half(o, h, l);
+                    split_half(o[e] * down, h, l);
                     hi[e] = h;
                     lo[e] = l;
                 }
-                const size_t at = size_t(m) * (N / 2) + n0 / 2 + c8;
+                const size_t at = size_t(m) * (N / 2) + col;
                 *reinterpret_cast<half8*>(ep.act_hi + at) = hi;
                 *reinterpret_cast<half8*>(ep.act_lo + at) = lo;
+                ep.act_exp[size_t(m) * (N / 16) + col / 8] = static_cast<uint8_t>(e8);
+                if (e8 != 0) atomicMax(ep.act_flag + size_t(m) * 4 + col / (N / 8), e8);
             }
         }
     } else {
@@ -316,8 +408,9 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
 #pragma unroll
             for (int k = 0; k < kRows; ++k) {
                 const int rr = wave + S::kWaves * k;
-                ht[rr][j] = f2h(ct[rr][j]);
-                ht[rr][j + 64] = f2h(ct[rr][j + 64]);
+                const float sc = row_scale(ep.row_exp, min(m0 + rr, M - 1));
+                ht[rr][j] = f2h(ct[rr][j] * sc);
+                ht[rr][j + 64] = f2h(ct[rr][j + 64] * sc);
             }
         } else {
             const float* w = is_q ? ep.q_norm : ep.k_norm;
@@ -332,7 +425,8 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
 #pragma unroll
             for (int k = 0; k < kRows; ++k) {
                 const int rr = wave + S::kWaves * k;
-                const float x0 = ct[rr][j], x1 = ct[rr][j + 64];
+                const float sc = row_scale(ep.row_exp, min(m0 + rr, M - 1));
+                const float x0 = ct[rr][j] * sc, x1 = ct[rr][j + 64] * sc;
                 const float s0 = x0 * x0, s1 = x1 * x1;
                 double part = static_cast<double>(s0) + static_cast<double>(s1);
 #pragma unroll
@@ -391,14 +485,18 @@ __device__ __forceinline__ float fold_splits(float x, const float* p, size_t str
 
 
 // out[b] = RMSNorm(x[b]) (engine/core.cpp:207-215): FP32 squares, FP64 sum,
-// written as the FP16 hi / lo planes of the next GEMM's A operand.
-// With SPLITS > 0 the residual first absorbs the pending partial products of
-// a K-split GEMM (parts[z][b], z < SPLITS) and is written back.
+// written as the FP16 hi / lo planes of the next GEMM's A operand, split as
+// out * 2^-row_exp[b] (split_exponent of the row's largest magnitude; 0
+// wherever the row fits FP16). With SPLITS > 0 the residual first absorbs the
+// pending partial products of a K-split GEMM (parts[z][b], z < SPLITS) and is
+// written back. clear_flags (optional) zeroes the row's 4 SwiGLU range flags
+// ahead of the gate/up GEMM.
 template <int SPLITS = 0>
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X, const float* __restrict__ w,
                                                            uint16_t* __restrict__ out_hi,
                                                            uint16_t* __restrict__ out_lo,
-                                                           const float* __restrict__ parts, int rows) {
+                                                           const float* __restrict__ parts, int rows,
+                                                           int* __restrict__ row_exp, int* __restrict__ clear_flags) {
     const int b = blockIdx.x, tid = threadIdx.x;
     // Thread t holds columns 4t .. 4t + 3 (16-byte accesses).
     float4* xr = reinterpret_cast<float4*>(X + size_t(b) * kHidden) + tid;
@@ -428,11 +526,26 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ X
     const float inv = 1.0f / __builtin_sqrtf(sum / 1024.0f + 1e-6f);
     const float4 w4 = reinterpret_cast<const float4*>(w)[tid];
     const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+    float n[4], big = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        n[k] = (v[k] * inv) * wv[k];
+        big = fmaxf(big, fabsf(n[k]));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+    __shared__ float bred[4];
+    if ((tid & 63) == 0) bred[tid >> 6] = big;
+    __syncthreads();
+    const int e = split_exponent(fmaxf(fmaxf(bred[0], bred[1]), fmaxf(bred[2], bred[3])));
+    const float down = pow2(-e);
+    if (tid == 0) row_exp[b] = e;
+    if (clear_flags != nullptr && tid < 4) clear_flags[size_t(b) * 4 + tid] = 0;
     uint16_t hi[4], lo[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         _Float16 h, l;
-        split_half((v[k] * inv) * wv[k], h, l);
+        split_half(n[k] * down, h, l);
         hi[k] = __builtin_bit_cast(uint16_t, h);
         lo[k] = __builtin_bit_cast(uint16_t, l);
     }
@@ -547,24 +660,38 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
     // Q^T operand: query b0 + col (rows past the chunk repeat its last row
     // and are never written), channels 16s + 8hf .. +7, scaled by
     // scale * log2(e) so that the scores come out in the exp2 domain.
+    // A query row whose largest magnitude reaches 65504 is split as
+    // q * 2^-eq (split_exponent) and its scores scaled back by 2^eq.
     half8 qh[8], ql[8];
+    int eq;
     {
         const float* qrow = QKV + size_t(b0 + min(col, nrows - 1)) * kQKVRows + head * kHeadDim + 8 * hf;
+        float v[8][8], big = 0.f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const float4 x0 = reinterpret_cast<const float4*>(qrow + 16 * s)[0];
             const float4 x1 = reinterpret_cast<const float4*>(qrow + 16 * s)[1];
-            const float v[8] = {x0.x * scale2, x0.y * scale2, x0.z * scale2, x0.w * scale2,
-                                x1.x * scale2, x1.y * scale2, x1.z * scale2, x1.w * scale2};
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[s][i] = x[i] * scale2;
+                big = fmaxf(big, fabsf(v[s][i]));
+            }
+        }
+        eq = split_exponent(fmaxf(big, __shfl_xor(big, 32)));
+        const float down = pow2(-eq);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 _Float16 hh, ll;
-                split_half(v[i], hh, ll);
+                split_half(v[s][i] * down, hh, ll);
                 qh[s][i] = hh;
                 ql[s][i] = ll;
             }
-        }
     }
+    const bool q_scaled = __builtin_amdgcn_ballot_w64(eq != 0) != 0;
+    const float q_up = pow2(eq);
     float m = -INFINITY, l = 0.f;
     floatx16 acc[4];
 #pragma unroll
@@ -593,6 +720,10 @@ __global__ __launch_bounds__(512) void attn_prefill_mfma_kernel(const float* __r
             const half8 ka = *reinterpret_cast<const half8*>(k_lds + 16 * fb_slot(col, 2 * s + hf));
             st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[s], st, 0, 0, 0);
             st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[s], st, 0, 0, 0);
+        }
+        if (q_scaled) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st[r] *= q_up;
         }
         // Online softmax; register r holds key t0 + 8(r/4) + 4hf + r%4. A
         // tile entirely at or before the block's first query needs no causal
@@ -766,18 +897,32 @@ void gemm(const uint16_t* Ah, const uint16_t* Al, const uint16_t* W, float* C, i
         launch(std::integral_constant<int, 32>{}, I128{});
 }
 
-// FP32 rows -> FP16 hi / lo planes (GEMM operands handed over as FP32).
+// FP32 rows [M x K] -> FP16 hi / lo planes (GEMM operands handed over as
+// FP32), one workgroup per row: the row is split as a * 2^-row_exp[m]
+// (split_exponent of its largest magnitude).
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ A, uint16_t* __restrict__ hi,
-                                                         uint16_t* __restrict__ lo, size_t n) {
-    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
-        split_store(A[i], hi, lo, i);
+                                                         uint16_t* __restrict__ lo, int* __restrict__ row_exp, int K) {
+    const size_t base = size_t(blockIdx.x) * K;
+    const int tid = threadIdx.x;
+    float big = 0.f;
+    for (int i = tid; i < K; i += 256) big = fmaxf(big, fabsf(A[base + i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+    __shared__ float bred[4];
+    if ((tid & 63) == 0) bred[tid >> 6] = big;
+    __syncthreads();
+    const int e = split_exponent(fmaxf(fmaxf(bred[0], bred[1]), fmaxf(bred[2], bred[3])));
+    const float down = pow2(-e);
+    if (tid == 0) row_exp[blockIdx.x] = e;
+    for (int i = tid; i < K; i += 256) split_store(A[base + i] * down, hi, lo, base + i);
 }
 
 }  // namespace
 
-// Runs fn(hi, lo) on FP16 hi / lo planes of the FP32 rows A[M x K], held in
-// device memory allocated for this call (an operator entry point for tests
-// and benchmarks, not on the inference path), then waits for the stream.
+// Runs fn(hi, lo, row_exp) on FP16 hi / lo planes of the FP32 rows
+// A[M x K] and their row exponents, held in device memory allocated for this
+// call (an operator entry point for tests and benchmarks, not on the
+// inference path), then waits for the stream.
 template <class F>
 static void with_planes(const float* A, int M, int K, hipStream_t stream, F&& fn) {
     require(M > 0 && K > 0, "gemm: unsupported shape");
@@ -786,9 +931,10 @@ static void with_planes(const float* A, int M, int K, hipStream_t stream, F&& fn
         require(e == hipSuccess, std::string("HIP error: ") + hipGetErrorString(e) + " (" + what + ")");
     };
     uint16_t* planes = nullptr;
-    check(hipMalloc(&planes, 2 * n * sizeof(uint16_t)), "hipMalloc");
-    split_rows_kernel<<<unsigned(std::min<size_t>((n + 255) / 256, 4096)), 256, 0, stream>>>(A, planes, planes + n, n);
-    fn(planes, planes + n);
+    check(hipMalloc(&planes, 2 * n * sizeof(uint16_t) + size_t(M) * sizeof(int)), "hipMalloc");
+    int* row_exp = reinterpret_cast<int*>(planes + 2 * n);
+    split_rows_kernel<<<M, 256, 0, stream>>>(A, planes, planes + n, row_exp, K);
+    fn(planes, planes + n, row_exp);
     const hipError_t launched = hipGetLastError();
     const hipError_t done = hipStreamSynchronize(stream);
     check(hipFree(planes), "hipFree");
@@ -798,30 +944,46 @@ static void with_planes(const float* A, int M, int K, hipStream_t stream, F&& fn
 
 void launch_gemm(const float* A, const uint16_t* W, float* C, int M, int N, int K, bool accumulate,
                  hipStream_t stream) {
-    with_planes(A, M, K, stream, [&](const uint16_t* hi, const uint16_t* lo) {
+    with_planes(A, M, K, stream, [&](const uint16_t* hi, const uint16_t* lo, const int* row_exp) {
+        GemmEpilogue ep{};
+        ep.row_exp = row_exp;
         if (accumulate)
-            gemm<1>(hi, lo, W, C, M, N, K, stream);
+            gemm<1>(hi, lo, W, C, M, N, K, stream, 1, ep);
         else
-            gemm<0>(hi, lo, W, C, M, N, K, stream);
+            gemm<0>(hi, lo, W, C, M, N, K, stream, 1, ep);
     });
 }
 
-void launch_gemm_swiglu(const float* A, const uint16_t* W, uint16_t* act_hi, uint16_t* act_lo, int M, int N, int K,
-                        hipStream_t stream) {
+void launch_gemm_swiglu(const float* A, const uint16_t* W, uint16_t* act_hi, uint16_t* act_lo, uint8_t* act_exp,
+                        int M, int N, int K, hipStream_t stream) {
     require(N % 256 == 0, "gemm swiglu: N must be a multiple of 256");
+    int* flags = nullptr;
+    require(hipMalloc(&flags, size_t(M) * 4 * sizeof(int)) == hipSuccess, "gemm swiglu: hipMalloc failed");
+    const hipError_t cleared = hipMemsetAsync(flags, 0, size_t(M) * 4 * sizeof(int), stream);
     GemmEpilogue ep{};
     ep.act_hi = act_hi;
     ep.act_lo = act_lo;
-    with_planes(A, M, K, stream, [&](const uint16_t* hi, const uint16_t* lo) {
-        gemm<3>(hi, lo, W, nullptr, M, N, K, stream, 1, ep);
-    });
+    ep.act_exp = act_exp;
+    ep.act_flag = flags;
+    try {
+        require(cleared == hipSuccess, "gemm swiglu: hipMemsetAsync failed");
+        with_planes(A, M, K, stream, [&](const uint16_t* hi, const uint16_t* lo, const int* row_exp) {
+            ep.row_exp = row_exp;
+            gemm<3>(hi, lo, W, nullptr, M, N, K, stream, 1, ep);
+        });
+    } catch (...) {
+        (void)hipFree(flags);
+        throw;
+    }
+    require(hipFree(flags) == hipSuccess, "gemm swiglu: hipFree failed");
 }
 
-// Operand planes of launch_gemm_static: a file-scope device array, so the
-// call allocates nothing. Each device holds its own copy at its own address
-// (from hipGetSymbolAddress, taken once per device); host code uses only that
-// address, never the array's name.
-static __device__ __align__(256) uint16_t scratch[2 * kStaticGemmElements];
+// Operand planes and row exponents of launch_gemm_static: a file-scope
+// device array, so the call allocates nothing. Each device holds its own copy
+// at its own address (from hipGetSymbolAddress, taken once per device); host
+// code uses only that address, never the array's name.
+inline constexpr size_t kStaticGemmRows = kStaticGemmElements / kTileK;  // K >= 64
+static __device__ __align__(256) uint16_t scratch[2 * kStaticGemmElements + 2 * kStaticGemmRows];
 
 static uint16_t* static_planes() {
     constexpr int kMaxDevices = 64;
@@ -849,12 +1011,14 @@ void launch_gemm_static(const float* A, const uint16_t* W, float* C, int M, int 
             "gemm static: M x K exceeds the 1048576 operand elements of the static planes");
     uint16_t* hi = static_planes();
     uint16_t* lo = hi + kStaticGemmElements;
-    const size_t n = size_t(M) * K;
-    split_rows_kernel<<<unsigned(std::min<size_t>((n + 255) / 256, 4096)), 256, 0, stream>>>(A, hi, lo, n);
+    int* row_exp = reinterpret_cast<int*>(hi + 2 * kStaticGemmElements);
+    split_rows_kernel<<<M, 256, 0, stream>>>(A, hi, lo, row_exp, K);
+    GemmEpilogue ep{};
+    ep.row_exp = row_exp;
     if (accumulate)
-        gemm<1>(hi, lo, W, C, M, N, K, stream);
+        gemm<1>(hi, lo, W, C, M, N, K, stream, 1, ep);
     else
-        gemm<0>(hi, lo, W, C, M, N, K, stream);
+        gemm<0>(hi, lo, W, C, M, N, K, stream, 1, ep);
 }
 
 void launch_attention_prefill(const float* qkv, const uint16_t* keys, const uint16_t* values, uint16_t* att_hi,
@@ -878,16 +1042,24 @@ void launch_prefill_chunk(const PrefillLayer* layers, const uint16_t* embed, con
     for (int l = 0; l < kLayers; ++l) {
         const PrefillLayer& L = layers[l];
         if (l == 0)
-            rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, nullptr, rows);
+            rmsnorm_rows_kernel<<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, nullptr, rows, s.row_exp,
+                                                          nullptr);
         else
-            rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, s.part, rows);
-        const GemmEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context, s.act_hi, s.act_lo};
+            rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.in_norm, s.h_hi, s.h_lo, s.part, rows,
+                                                                   s.row_exp, nullptr);
+        GemmEpilogue ep{L.q_norm, L.k_norm, cosines, sines, L.keys, L.values, pos0, context, s.act_hi, s.act_lo,
+                        s.row_exp, s.act_flag, s.act_exp};
         gemm<4>(s.h_hi, s.h_lo, L.qkv_n, s.qkv, rows, kQKVRows, kHidden, stream, 1, ep);
         launch_attention_prefill(s.qkv, L.keys, L.values, s.att_hi, s.att_lo, rows, pos0, context, stream);
+        // The attention output is a convex combination of FP16 values: it fits FP16 unscaled.
         gemm<2>(s.att_hi, s.att_lo, L.o_n, s.part, rows, kHidden, kQDim, stream, kSplits);
-        rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h_hi, s.h_lo, s.part, rows);
+        rmsnorm_rows_kernel<kSplits><<<rows, 256, 0, stream>>>(s.x, L.post_norm, s.h_hi, s.h_lo, s.part, rows,
+                                                               s.row_exp, s.act_flag);
         gemm<3>(s.h_hi, s.h_lo, L.gateup_n, nullptr, rows, 2 * kFFN, kHidden, stream, 1, ep);
-        gemm<2>(s.act_hi, s.act_lo, L.down_n, s.part, rows, kHidden, kFFN, stream, kSplits);
+        GemmEpilogue down{};
+        down.act_flag = s.act_flag;
+        down.act_exp = s.act_exp;
+        gemm<2>(s.act_hi, s.act_lo, L.down_n, s.part, rows, kHidden, kFFN, stream, kSplits, down);
     }
     fold_rows_kernel<kSplits><<<(rows * kHidden + 255) / 256, 256, 0, stream>>>(s.x, s.part, rows);
 }

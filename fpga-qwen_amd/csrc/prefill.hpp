@@ -34,6 +34,10 @@ struct PrefillScratch {
     uint16_t* act_hi;   // [rows x 3072] SwiGLU output
     uint16_t* act_lo;
     float* part;        // [4 x rows x 1024] K-split partial products of the O and down GEMMs
+    // Range guard of the FP16 split (values from 65504 up do not fit FP16):
+    int* row_exp;       // [rows] the normalized row was split as h * 2^-row_exp
+    int* act_flag;      // [rows x 4] largest SwiGLU group exponent per K range of the down GEMM
+    uint8_t* act_exp;   // [rows x 384] exponent of each group of 8 activations
 };
 
 // C[M x N] (+)= A[M x K] . W[N x K]^T; A FP32 split into FP16 hi + lo on the
@@ -51,10 +55,11 @@ void launch_gemm_static(const float* A, const uint16_t* W, float* C, int M, int 
 
 // Gate/up projection with the SwiGLU epilogue of the prefill path: W holds
 // N / 2 gate rows then N / 2 up rows (natural [N x K]); act[m][i] =
-// SwiGLU(gate_i, up_i) of row m, written as FP16 hi / lo planes [M x N / 2].
-// N a multiple of 256, K of 64.
-void launch_gemm_swiglu(const float* A, const uint16_t* W, uint16_t* act_hi, uint16_t* act_lo, int M, int N, int K,
-                        hipStream_t stream);
+// SwiGLU(gate_i, up_i) of row m, written as FP16 hi / lo planes [M x N / 2]
+// of act * 2^-act_exp[m][i / 8] (act_exp [M x N / 16]: 0 wherever the group
+// of 8 fits FP16). N a multiple of 256, K of 64.
+void launch_gemm_swiglu(const float* A, const uint16_t* W, uint16_t* act_hi, uint16_t* act_lo, uint8_t* act_exp,
+                        int M, int N, int K, hipStream_t stream);
 
 // Causal GQA attention of a prefill chunk (the layer step between the QKV
 // and O GEMMs): queries from qkv [rows x 4096] (columns 0..2047, 16 heads),

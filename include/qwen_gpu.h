@@ -197,11 +197,15 @@ int qwen_gpu_op_gemm_static(const float* a, const uint16_t* w, float* c, int m, 
  * (engine/core.cpp:630-639 with batch > 1: the gate and up projections, then
  * gate * (0.5 + 0.5 tanh(gate / 2)) * up): w natural FP16 [n x k] holding
  * n / 2 gate rows then n / 2 up rows, a FP32 [m x k]; act[m][i] is written
- * as FP16 hi and lo planes [m x n / 2] (hi + lo is the FP32 result to
- * 2^-22). n a multiple of 256, k of 64. Parity-test entry for the kernel the
- * prefill runs between the post-attention norm and the down GEMM. */
-int qwen_gpu_op_gemm_swiglu(const float* a, const uint16_t* w, uint16_t* act_hi, uint16_t* act_lo, int m, int n,
-                            int k, void* stream);
+ * as FP16 hi and lo planes [m x n / 2] and exponents act_exp [m x n / 16]
+ * (one byte per group of 8 activations), with
+ * act = (hi + lo) * 2^act_exp[m][i / 8] (the FP32 result to 2^-22; the
+ * exponent is 0 unless the group's largest magnitude reaches 65504, the
+ * FP16 limit). n a multiple of 256, k of 64. Parity-test entry for the
+ * kernel the prefill runs between the post-attention norm and the down
+ * GEMM. */
+int qwen_gpu_op_gemm_swiglu(const float* a, const uint16_t* w, uint16_t* act_hi, uint16_t* act_lo, uint8_t* act_exp,
+                            int m, int n, int k, void* stream);
 /* The batch-1 decode projections as a step runs them (parity-test entries;
  * all weights in the chain-tiled layout of qwen_gpu_op_tile_matrix):
  * qkv[4096] = W_qkv . RMSNorm(x, norm_weight) with W_qkv = q, k, v rows
@@ -270,13 +274,15 @@ int qwen_gpu_op_gemv_time(const uint16_t* tiled, size_t copy_stride, int copies,
 int qwen_gpu_op_copy(const void* src, void* dst, size_t bytes, void* stream);
 /* Average milliseconds of one standalone launch of a decode kernel on the
  * model's stream, timed with HIP events (which: 0 norm+QKV, 1 attention,
- * 2 O, 3 norm+gate/up, 4 down, 5 lm_head, 6 the fused FFN kernel that layers
- * 0-26 run in place of 3 and 4, 7 the fused norm + QKV + attention + O
- * kernel that every layer runs in place of 0 and 1). Needs position() > 0.
- * The O projection runs with the attention (timed as 1: one kernel up to 512
- * positions, split attention + merge/O beyond) and 2 reports 0. Afterwards
- * the current logits are invalid; timing the attention (1 or 7) also resets
- * the model, so time it last. */
+ * 2 O, 3 norm+gate/up, 4 down, 5 lm_head, 6 the fused FFN kernel and 7 the
+ * fused norm + QKV + attention + O kernel of the two-kernel step, 8 the
+ * token kernel that runs all 28 layers of a step in one launch). Needs
+ * position() > 0. The O projection runs with the attention (timed as 1: one
+ * kernel up to 512 positions, split attention + merge/O beyond) and 2
+ * reports 0. Kernels 0-7 replay layer by layer over all 28 layers, 8 replays
+ * whole steps. Afterwards the current logits are invalid; timing the
+ * attention or the token kernel (1, 7 or 8) also resets the model, so time
+ * them last. */
 int qwen_gpu_time_kernel(qwen_gpu_model* model, int which, int iterations, float* milliseconds);
 
 #ifdef __cplusplus

@@ -154,15 +154,17 @@ def test_rejections(tmp_path, case, message):
     assert not (tmp_path / 'out' / 'weights.bin').exists()
 
 
-def write_full_checkpoint(path, seed=7):
+def write_full_checkpoint(path, seed=7, gains=None):
     """A synthetic BF16 checkpoint with the exact Qwen3-0.6B tensor set: each
     matrix a differently rotated window of one N(0, 0.02) BF16 pattern, norm
-    gains 1.0, lm_head a copy of the embedding."""
+    gains 1.0 (gains: {norm name suffix: (channels, value)} overrides them in
+    every layer), lm_head a copy of the embedding."""
     shapes = export_pack.qwen3_tensor_table()
     rng = np.random.default_rng(seed)
     wide = rng.standard_normal(1 << 21).astype(np.float32) * 0.02
     pattern = bf16((wide.view(np.uint32) & 0xffff0000).view(np.float32))
     ones = bf16(np.ones(1, np.float32))[0]
+    gains = gains or {}
     names = list(shapes) + ['lm_head.weight']
     header, cursor = {}, 0
     for name in names:
@@ -178,7 +180,11 @@ def write_full_checkpoint(path, seed=7):
             shape = shapes['model.embed_tokens.weight'] if tied else shapes[name]
             count = int(np.prod(shape))
             if len(shape) == 1:
-                f.write(np.full(count, ones, '<u2').tobytes())
+                norm = np.full(count, ones, '<u2')
+                for suffix, (channels, value) in gains.items():
+                    if name.endswith(suffix + '.weight'):
+                        norm[list(channels)] = bf16(np.float32([value]))[0]
+                f.write(norm.tobytes())
                 continue
             window = np.roll(pattern, 7919 * (0 if tied else index))
             reps = -(-count // window.size)
@@ -236,3 +242,74 @@ def test_exported_pack_runs_on_gpu_against_oracle(tmp_path, qpkg, oracle_lib):
     finally:
         model.close()
         oracle.close()
+
+
+# Norm gains that drive the prefill and batched matrix-core inputs far past
+# FP16's range (65504): 32768 in 8 channels of every layer's input and
+# post-attention norms.
+LARGE_GAINS = {'input_layernorm': ((3, 200, 411, 517, 640, 777, 901, 1013), 32768.0),
+               'post_attention_layernorm': ((3, 200, 411, 517, 640, 777, 901, 1013), 32768.0)}
+
+
+@pytest.mark.gpu
+def test_large_activations_against_oracle(tmp_path, qpkg, oracle_lib):
+    """FP32 activations beyond FP16's range (engine/core.cpp:292-294 keeps
+    them FP32): an exported pack with norm gains of 32768 in 8 channels
+    (LARGE_GAINS) makes about a third of the normalized rows exceed 65504 in
+    layer 0 already (checked below from the pack's embedding rows), and the
+    SwiGLU activations reach the millions. The 1024-token prompt (two
+    512-row prefill chunks on the matrix cores, every input split under the
+    range guard), 2 decode steps, and one batched step of two sequences
+    sharing the weights, every row's logits against the oracle on the same
+    file under the reference gate (max-abs 1e-2, RMS 2e-3, greedy
+    identity)."""
+    from oracle_binding import compare_logits
+    path = write_full_checkpoint(tmp_path / 'model.safetensors', gains=LARGE_GAINS)
+    out = tmp_path / 'pack' / 'weights.bin'
+    export_pack.write_pack(path, out)
+    path.unlink()
+    prompts = json.loads((ROOT / 'tests' / 'golden' / 'prompts.json').read_text())
+    prompt, other = prompts['prefill_1024'], prompts['decode_85']
+    # Layer 0's normalized rows: the pack's FP16 embedding rows of the prompt
+    # times the input norm gains (FP32 norm of engine/core.cpp:207-215).
+    slots = {slot.name: slot for slot in export_pack.plan(export_pack.qwen3_tensor_table())[0]}
+    blob = np.memmap(out, np.uint8, 'r')
+    emb = slots['model.embed_tokens.weight']
+    table = blob[emb.offset:emb.offset + emb.length].view(np.float16).reshape(emb.shape)
+    rows = table[prompt].astype(np.float64)
+    gain = blob[slots['model.layers.0.input_layernorm.weight'].offset:][:4096].view(np.float32)
+    normed = rows / np.sqrt((rows ** 2).mean(axis=1, keepdims=True) + 1e-6) * gain
+    share = float((np.abs(normed).max(axis=1) >= 65504).mean())
+    print('rows of layer 0 past FP16 range', share, flush=True)
+    assert share > 0.1
+    del blob, table
+    model = qpkg.Model(out, context=1100)
+    second = model.share()
+    oracle = oracle_lib.model(out, 16, 16, 1100)
+    oracle2 = oracle_lib.model(out, 16, 16, 1100)
+    try:
+        model.prefill(prompt)
+        oracle.prefill(prompt)
+        second.prefill(other)
+        oracle2.prefill(other)
+        for step in range(3):
+            result = compare_logits(model.logits(), oracle.logits())
+            print('large gains, position', model.position(), result, flush=True)
+            assert result['passed'], (step, result)
+            if step < 2:
+                token = model.greedy()
+                model.step(token)
+                oracle.step(token)
+        tokens = [model.greedy(), second.greedy()]
+        qpkg.step_batch([model, second], tokens)
+        oracle.step(tokens[0])
+        oracle2.step(tokens[1])
+        for m, o in ((model, oracle), (second, oracle2)):
+            result = compare_logits(m.logits(), o.logits())
+            print('large gains, batched, position', m.position(), result, flush=True)
+            assert result['passed'], result
+    finally:
+        second.close()
+        model.close()
+        oracle.close()
+        oracle2.close()

@@ -42,30 +42,66 @@ def test_gemm_against_fp64(qpkg, m, n, k):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('m', [1024, 100, 3968])
-def test_gemm_swiglu_against_fp64(qpkg, m):
+def test_gemm_range_guard(qpkg):
+    """Rows holding values far beyond FP16's range (up to 3e6; FP16 ends at
+    65504) are split as a * 2^-e and scaled back (engine/core.cpp:292-294
+    multiplies FP32 activations): within the FP64 bound, while rows that fit
+    FP16 keep the bits they have in a call where no row is scaled, through
+    the allocating and the static entry points."""
+    rng = np.random.default_rng(31)
+    a = rng.standard_normal((300, 1024), dtype=np.float32)
+    big = np.arange(0, 300, 7)
+    a[big, 5] = 3e6
+    a[big[::2], 900] = -7e4
+    a[11, :] *= 40000.0
+    w = (rng.standard_normal((1024, 1024), dtype=np.float32) * 0.02).astype(np.float16)
+    ref = a.astype(np.float64) @ w.astype(np.float64).T
+    bound = 4e-6 * (np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T) + 1e-7
+    fits = np.setdiff1d(np.arange(300), np.r_[big, 11])
+    alone = qpkg.gemm(a[fits], w)
+    for got in (qpkg.gemm(a, w), qpkg.gemm_static(a, w)):
+        assert np.isfinite(got).all()
+        err = np.abs(got - ref)
+        assert np.all(err <= bound), float((err / bound).max())
+        assert np.array_equal(got[fits].view(np.uint32), alone.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('m,amp', [(1024, 1.0), (100, 1.0), (3968, 1.0), (1024, 200.0), (100, 200.0)])
+def test_gemm_swiglu_against_fp64(qpkg, m, amp):
     """The gate/up GEMM with its SwiGLU epilogue (engine/core.cpp:630-639 at
     batch > 1). 1024 rows take 128 x 192 tiles (256 workgroups in one round),
     100 rows narrower 32- or 64-row tiles and 3968 rows 128 x 256 tiles, so
     each epilogue's gate/up column mapping is exercised. Against FP64:
     g sigmoid(g) u with g, u the exact products, the GEMM error bound
     propagated through the activation's partial derivatives, plus the FP16
-    hi + lo rounding of the stored result."""
+    hi + lo rounding of the stored result. With amp = 200 many activations
+    lie beyond FP16's range: their groups of 8 carry exponents (the others
+    keep 0, and so does every group at amp = 1)."""
     rng = np.random.default_rng(23 + m)
-    a = rng.standard_normal((m, 1024), dtype=np.float32)
+    a = rng.standard_normal((m, 1024), dtype=np.float32) * np.float32(amp)
     w = (rng.standard_normal((6144, 1024), dtype=np.float32) * 0.02).astype(np.float16)
     # Every column, every third row plus the last (the FP64 products of all
     # 3968 rows would dominate the test's time).
     rows = np.r_[0:m:3, m - 1]
-    got = qpkg.gemm_swiglu(a, w).astype(np.float64)[rows]
+    got, exps = qpkg.gemm_swiglu(a, w, exponents=True)
+    got = got.astype(np.float64)[rows]
+    if amp == 1.0:
+        assert not exps.any()
+    else:
+        assert 0.005 < (exps > 0).mean() < 0.995, float((exps > 0).mean())
+        assert np.isfinite(got).all()
     a64, w64 = a[rows].astype(np.float64), w.astype(np.float64)
     g, u = a64 @ w64[:3072].T, a64 @ w64[3072:].T
     sig = 1.0 / (1.0 + np.exp(-g))
     ref = g * sig * u
     bg = 4e-6 * (np.abs(a64) @ np.abs(w64[:3072]).T) + 1e-7
     bu = 4e-6 * (np.abs(a64) @ np.abs(w64[3072:]).T) + 1e-7
+    # The last terms: the FP32 formula's own rounding, including 0.5 + 0.5 t
+    # for t near -1 (tanhf saturates to -1 below g ~ -17, where FP64 still
+    # has g sigmoid(g) u ~ 1e-8 g u): 2^-23 |g u| covers it.
     bound = (np.abs(sig * (1.0 + g * (1.0 - sig)) * u) * bg + np.abs(g * sig) * bu
-             + 1e-6 * np.abs(ref) + 1e-8)
+             + 1e-6 * np.abs(ref) + 2.0 ** -23 * np.abs(g * u) + 1e-8)
     # The epilogue itself: the plain GEMM accumulates every element in the
     # same K order, so its g and u are the ones the SwiGLU epilogue saw. The
     # activation must be the reference formula evaluated in FP32 on them, up
@@ -124,6 +160,31 @@ def test_attention_prefill_against_fp64(qpkg, rows, pos0, boost):
         for t, alpha in ((40, 10.0), (97, 20.0), (170, 30.0), (300, 40.0)):
             if t < pos0 + rows:
                 keys[:, t] = (alpha * u).astype(np.float16)
+    qkv = np.zeros((rows, 4096), np.float32)
+    qkv[:, :2048] = q.reshape(rows, 2048)
+    got = qpkg.attention_prefill(qkv, keys, values, pos0)
+    ref = causal_attention_fp64(q, keys, values, pos0)
+    err = np.abs(got - ref)
+    assert np.all(err <= 1e-4 + 1e-4 * np.abs(ref)), float(err.max())
+
+
+@pytest.mark.gpu
+def test_attention_prefill_range_guard(qpkg):
+    """Queries with a channel far beyond FP16's range (4e6 before the
+    kernel's scale * log2(e), against keys that are 0 in that channel, so the
+    scores stay moderate): the kernel splits such a query as q * 2^-e and
+    scales its scores back, within the same FP64 tolerance as plain
+    queries."""
+    rng = np.random.default_rng(77)
+    rows, pos0 = 70, 30
+    context = pos0 + rows
+    q = rng.standard_normal((rows, 16, 128)).astype(np.float32)
+    q[::3, :, 17] = 4e6
+    q[1::5, 2, 90] = -9e5
+    keys = (0.3 * rng.standard_normal((8, context, 128))).astype(np.float16)
+    keys[:, :, 17] = 0
+    keys[:, :, 90] = 0
+    values = rng.standard_normal((8, context, 128)).astype(np.float16)
     qkv = np.zeros((rows, 4096), np.float32)
     qkv[:, :2048] = q.reshape(rows, 2048)
     got = qpkg.attention_prefill(qkv, keys, values, pos0)
