@@ -868,25 +868,32 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                 const int gq = tid >> 7;
                 float mv[8], lv[8], ovl[8];
                 {
-                    const uint64_t* words[24];
-                    float got[24];
+                    // Every lane polls its output entry of the group's 8
+                    // partials; lane k < 8 of each wave also polls the
+                    // maximum of partial k and lane 8 + k its sum, which
+                    // every lane then reads from those lanes.
+                    auto part = [&](int k) {
+                        return W[q] + kTokPartOffset + ((size_t(g) * 32 + 8 * gq + k) * 2 + hq) * kXPart;
+                    };
+                    const uint64_t* words[9];
+                    float got[9];
                     unsigned want = 0;
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
-                        const uint64_t* part =
-                            W[q] + kTokPartOffset + ((size_t(g) * 32 + 8 * gq + k) * 2 + hq) * kXPart;
-                        words[k] = part + j;
-                        words[8 + k] = part + 128;
-                        words[16 + k] = part + 129;
-                        got[k] = got[8 + k] = got[16 + k] = 0.f;
-                        if (8 * gq + k < active[q]) want |= 0x10101u << k;
+                        words[k] = part(k) + j;
+                        got[k] = 0.f;
+                        if (8 * gq + k < active[q]) want |= 1u << k;
                     }
-                    if (ok) ok = tok_gather<24>(words, tag, got, want, a.stall, spins);
+                    const int kk = lane & 7;
+                    words[8] = part(kk) + (lane < 8 ? 128 : 129);
+                    got[8] = 0.f;
+                    if (lane < 16 && 8 * gq + kk < active[q]) want |= 1u << 8;
+                    if (ok) ok = tok_gather<9>(words, tag, got, want, a.stall, spins);
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
                         ovl[k] = got[k];
-                        mv[k] = 8 * gq + k < active[q] ? got[8 + k] : -INFINITY;
-                        lv[k] = got[16 + k];
+                        mv[k] = 8 * gq + k < active[q] ? __shfl(got[8], k) : -INFINITY;
+                        lv[k] = __shfl(got[8], 8 + k);
                     }
                 }
                 float mx = -INFINITY;
