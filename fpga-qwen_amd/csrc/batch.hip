@@ -168,9 +168,10 @@ __global__ __launch_bounds__(K / 4) void bgemv_kernel(const BatchGemvArgs a) {
 //  3. it gathers the XCD's 384 x 8 activations and multiplies them by down
 //     rows 32 r .. 32 r + 31, columns 384 x .. + 383 (this XCD's share of K);
 //  4. the 8 shares of a row, one per XCD, travel through memory (stores that
-//     write through the L2, loads that bypass it), and workgroup (r, x)
-//     adds rows 32 r + 4 x .. + 3 in fixed order ((s0 + s1) + (s2 + s3)) +
-//     ((s4 + s5) + (s6 + s7)) to the residual.
+//     write through the L2, loads that bypass it; each XCD's shares of a
+//     workgroup's rows fill whole lines), and workgroup (r, x) adds rows
+//     32 r .. 32 r + 31 of sequence x in fixed order ((s0 + s1) + (s2 + s3))
+//     + ((s4 + s5) + (s6 + s7)) to the residual (whole lines again).
 // Every workgroup reads all of the input residual, so the output goes to a
 // second buffer (the layers alternate between the two).
 struct BatchFfnArgs {
@@ -180,7 +181,7 @@ struct BatchFfnArgs {
     const float* x[kMaxBatch];         // residual in
     float* x_out[kMaxBatch];           // residual out
     uint64_t* act_words;               // [8 XCDs][kMaxBatch][384] tagged activations
-    uint64_t* share_words;             // [1024][kMaxBatch][8] tagged down shares
+    uint64_t* share_words;             // [32 row blocks][8 XCDs][kMaxBatch][32 rows] tagged down shares
     int* stall;
     int batch;
     uint32_t tag;
@@ -423,24 +424,31 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) part[wave][0][lane][e] = acc[e];
         __syncthreads();
-        // Thread of waves 0-3 and 4-7: tile tt2 = wave >> 2, element (row
-        // 4 (lane / 16) + (wave & 3), sequence lane % 16); the 4 K ranges of
-        // the tile (waves tt2, tt2 + 2, tt2 + 4, tt2 + 6) in fixed order.
-        const int tt2 = wave >> 2, e4 = wave & 3;
-        const int row = 32 * r + 16 * tt2 + 4 * (lane >> 4) + e4, seq = lane & 15;
-        const float y = ((part[tt2][0][lane][e4] + part[tt2 + 2][0][lane][e4]) +
-                         (part[tt2 + 4][0][lane][e4] + part[tt2 + 6][0][lane][e4])) *
-                        act_guard.up(seq & 7);
-        if (seq < B) exchange_put_through(a.share_words + (size_t(row) * kMaxBatch + seq) * 8 + xo, y, a.tag);
+        // Thread (wave w < 4, lane): sequence 2 w + lane / 32, row
+        // 32 r + rl (rl = lane % 32: tile rl / 16, element rl % 16 held by
+        // MFMA lane 16 (rl / 4 % 4) + sequence, register rl % 4); the 4 K
+        // ranges of the tile (waves tt, tt + 2, tt + 4, tt + 6) in fixed
+        // order. A wave posts 64 consecutive words: the XCD's shares fill
+        // whole lines (write-through stores of parts of a line cost far more).
+        if (wave < 4) {
+            const int seq = 2 * wave + (lane >> 5), rl = lane & 31;
+            const int tt2 = rl >> 4, e4 = rl & 3, el = 16 * ((rl >> 2) & 3) + seq;
+            const float y = ((part[tt2][0][el][e4] + part[tt2 + 2][0][el][e4]) +
+                             (part[tt2 + 4][0][el][e4] + part[tt2 + 6][0][el][e4])) *
+                            act_guard.up(seq);
+            if (seq < B)
+                exchange_put_through(a.share_words + ((size_t(r) * 8 + xo) * kMaxBatch + seq) * 32 + rl, y, a.tag);
+        }
     }
 
-    // 4. Rows 32 r + 4 xo .. + 3 of every sequence: threads 0..31 (row
-    // 4 xo + tid / 8, sequence tid % 8) add the 8 shares to the residual.
+    // 4. Rows 32 r .. 32 r + 31 of sequence xo (threads 0..31, one row
+    // each: a whole line of the residual): x + the 8 XCD shares.
     if (tid < 32) {
-        const int row = 32 * r + 4 * xo + (tid >> 3), seq = tid & 7;
+        const int row = 32 * r + tid, seq = xo;
         const bool live = seq < B;
-        const uint64_t* base = a.share_words + (size_t(row) * kMaxBatch + seq) * 8;
-        const uint64_t* const words[8] = {base, base + 1, base + 2, base + 3, base + 4, base + 5, base + 6, base + 7};
+        const uint64_t* words[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) words[k] = a.share_words + ((size_t(r) * 8 + k) * kMaxBatch + seq) * 32 + tid;
         float s8[8] = {};
         if (ok) ok = exchange_gather<8>(words, a.tag, s8, live ? 0xffu : 0u);
         if (live) {

@@ -1694,7 +1694,7 @@ struct AttnBatchArgs {
     uint64_t* exchange;      // [8 KV heads][kMaxBatch][512] tagged q/k/v rows
     uint64_t* piece_words;   // [8 KV heads][32 workgroups][2][kXPart] tagged piece partials
     uint64_t* att_words;     // [8 KV heads][kMaxBatch][256] tagged merged attention rows
-    uint64_t* share_words;   // [1024][kMaxBatch][8 XCDs] tagged O shares
+    uint64_t* share_words;   // [32 row blocks][8 XCDs][kMaxBatch][32 rows] tagged O shares
     int* stall;
     float scale;
     int batch;
@@ -2216,25 +2216,30 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
 #pragma unroll
         for (int e = 0; e < 4; ++e) qpart[wave][lane][e] = acc[e];
         __syncthreads();
-        // Waves 0-3 take tile 0, waves 4-7 tile 1: element (row 4 (lane / 16)
-        // + (wave & 3), sequence lane % 16), the tile's 4 column ranges
-        // (waves tt, tt + 2, tt + 4, tt + 6) in fixed order; the share goes
-        // through the L2 to the XCD that adds the row.
-        const int tt = wave >> 2, e4 = wave & 3;
-        const float y = (qpart[tt][lane][e4] + qpart[tt + 2][lane][e4]) +
-                        (qpart[tt + 4][lane][e4] + qpart[tt + 6][lane][e4]);
-        const int row = 32 * r + 16 * tt + 4 * (lane >> 4) + e4, seq = lane & 15;
-        if (seq < B) exchange_put_through(args.share_words + (size_t(row) * kMaxBatch + seq) * 8 + g, y, args.tag);
+        // Thread (wave w < 4, lane): sequence 2 w + lane / 32, row
+        // 32 r + rl (rl = lane % 32: tile rl / 16, element rl % 16 held by
+        // MFMA lane 16 (rl / 4 % 4) + sequence, register rl % 4), the tile's
+        // 4 column ranges (waves tt, tt + 2, tt + 4, tt + 6) in fixed order;
+        // the share goes through memory to the XCD that adds the row. A wave
+        // posts 64 consecutive words: the XCD's shares fill whole lines
+        // (write-through stores of parts of a line cost far more).
+        if (wave < 4) {
+            const int seq = 2 * wave + (lane >> 5), rl = lane & 31;
+            const int tt = rl >> 4, e4 = rl & 3, el = 16 * ((rl >> 2) & 3) + seq;
+            const float y = (qpart[tt][el][e4] + qpart[tt + 2][el][e4]) + (qpart[tt + 4][el][e4] + qpart[tt + 6][el][e4]);
+            if (seq < B)
+                exchange_put_through(args.share_words + ((size_t(r) * 8 + g) * kMaxBatch + seq) * 32 + rl, y, args.tag);
+        }
     }
-    // Rows 32 r + 4 g .. + 3 of every sequence: threads 0..31 (row
-    // 4 g + tid / 8, sequence tid % 8) add the 8 XCD shares to the residual
-    // in fixed order, into the second residual buffer (every workgroup read
-    // the first one).
+    // Rows 32 r .. 32 r + 31 of sequence g (threads 0..31, one row each: a
+    // whole line of the residual) add the 8 XCD shares in fixed order, into
+    // the second residual buffer (every workgroup read the first one).
     if (tid < 32) {
-        const int row = 32 * r + 4 * g + (tid >> 3), seq = tid & 7;
+        const int row = 32 * r + tid, seq = g;
         const bool live = seq < B;
-        const uint64_t* base = args.share_words + (size_t(row) * kMaxBatch + seq) * 8;
-        const uint64_t* const words[8] = {base, base + 1, base + 2, base + 3, base + 4, base + 5, base + 6, base + 7};
+        const uint64_t* words[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) words[k] = args.share_words + ((size_t(r) * 8 + k) * kMaxBatch + seq) * 32 + tid;
         float s8[8] = {};
         if (ok) ok = exchange_gather<8>(words, args.tag, s8, live ? 0xffu : 0u);
         if (live) {
