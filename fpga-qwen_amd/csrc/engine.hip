@@ -490,11 +490,13 @@ void Engine::run_append(const int* ids, size_t count) {
     // with it (GEMM rows, row kernels, and causal attention whose key split
     // follows absolute positions), so consecutive 512-row chunks run as one
     // batched pass; only a trailing one-row chunk takes the batch-1 path.
-    std::copy(ids, ids + count, ids_host_);
-    HIP_CHECK(hipMemcpyAsync(ids_dev_, ids_host_, count * sizeof(int), hipMemcpyHostToDevice, stream_));
     const size_t batched = count % kChunk == 1 ? count - 1 : count;
     require(batched <= size_t(kPrefillRows), "prefill: call longer than the batched pass");
     if (batched > 0) {
+        // Only the batched pass reads the ids from the device; a one-row
+        // chunk takes its token as a kernel argument.
+        std::copy(ids, ids + batched, ids_host_);
+        HIP_CHECK(hipMemcpyAsync(ids_dev_, ids_host_, batched * sizeof(int), hipMemcpyHostToDevice, stream_));
         const int rows = int(batched);
         launch_prefill_chunk(prefill_layers_.data(), embed_, ids_dev_, rows, pos_, cosines_, sines_,
                              options_.context, prefill_, stream_);

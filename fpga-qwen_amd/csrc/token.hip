@@ -41,6 +41,13 @@
 #include "decode_dev.hpp"
 #include "token.hpp"
 
+#ifndef QWEN_TOK_STAGGER_XCD
+#define QWEN_TOK_STAGGER_XCD 2
+#endif
+#ifndef QWEN_TOK_STAGGER_CROSS
+#define QWEN_TOK_STAGGER_CROSS 6
+#endif
+
 namespace qwen_hip {
 namespace {
 
@@ -122,22 +129,43 @@ __device__ __forceinline__ void barrier() {
 // Exchange polls that also give up as soon as another workgroup raised the
 // step's stall word (so one missing post costs one poll limit, not one per
 // waiting workgroup and phase).
-template <int N>
+//
+// Two rounds are in flight at once, the second issued about half a round
+// trip after the first (s_sleep D, D x 64 clocks), so memory is sampled twice
+// per round trip: a word that lands is seen about a quarter round trip
+// sooner on average than with one round at a time. Every round loads all N
+// words (every caller's addresses are valid for every lane), so each round is
+// the same N instructions and the compiler's waits count exactly one round.
+template <int N, int D>
 __device__ __forceinline__ bool tok_gather(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N], unsigned want,
                                            const int* stall, unsigned limit) {
-    for (unsigned spin = 0; spin < limit && __any(want != 0); ++spin) {
-        uint64_t u[N];
+    uint64_t a[N], b[N];
+    auto issue = [&](uint64_t(&u)[N]) {
 #pragma unroll
-        for (int k = 0; k < N; ++k)
-            u[k] = (want >> k) & 1 ? __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-        const int raised = __hip_atomic_load(stall, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 0; k < N; ++k) u[k] = __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto take = [&](const uint64_t(&u)[N]) {
 #pragma unroll
         for (int k = 0; k < N; ++k)
             if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
                 out[k] = __uint_as_float(uint32_t(u[k]));
                 want &= ~(1u << k);
             }
-        if (__any(raised != 0)) break;
+    };
+    issue(a);
+    __builtin_amdgcn_s_sleep(D);
+    for (unsigned spin = 0;;) {
+        issue(b);
+        take(a);
+        if (!__any(want != 0) || ++spin >= limit) break;
+        issue(a);
+        take(b);
+        if (!__any(want != 0) || ++spin >= limit) break;
+        // Every polling wave of the launch reads the one stall word: read it
+        // every 16th pair of rounds only.
+        if ((spin & 31) == 30 && __any(__hip_atomic_load(stall, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
+            break;
     }
     // A give-up raises the stall word at once: the other workgroups stop
     // polling and the step's argmax reports it.
@@ -145,11 +173,15 @@ __device__ __forceinline__ bool tok_gather(const uint64_t* const (&p)[N], uint32
     return want == 0;
 }
 
+// Stagger of the second round in flight (s_sleep units of 64 clocks): about
+// half the round trip of a poll inside an XCD (L2) and across XCDs (memory).
+constexpr int kStaggerXcd = QWEN_TOK_STAGGER_XCD, kStaggerCross = QWEN_TOK_STAGGER_CROSS;
+
 __device__ __forceinline__ bool tok_get2(const uint64_t* p, uint32_t tag, float& a, float& b, const int* stall,
                                          unsigned limit) {
     const uint64_t* const words[2] = {p, p + 1};
     float got[2] = {0.f, 0.f};
-    const bool ok = tok_gather<2>(words, tag, got, 3u, stall, limit);
+    const bool ok = tok_gather<2, kStaggerXcd>(words, tag, got, 3u, stall, limit);
     a = got[0];
     b = got[1];
     return ok;
@@ -611,7 +643,7 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                 words[2 * q + 1] = W[q] + kTokQkvOffset + g * 512 + 128 * wave + 64 + lane;
                 got[2 * q] = got[2 * q + 1] = 0.f;
             }
-            if (ok) ok = tok_gather<2 * ROWS>(words, tag, got, (1u << (2 * ROWS)) - 1, a.stall, spins);
+            if (ok) ok = tok_gather<2 * ROWS, kStaggerXcd>(words, tag, got, (1u << (2 * ROWS)) - 1, a.stall, spins);
 #pragma unroll
             for (int q = 0; q < ROWS; ++q) {
                 const int at = pos + q;
@@ -888,7 +920,7 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                     words[8] = part(kk) + (lane < 8 ? 128 : 129);
                     got[8] = 0.f;
                     if (lane < 16 && 8 * gq + kk < active[q]) want |= 1u << 8;
-                    if (ok) ok = tok_gather<9>(words, tag, got, want, a.stall, spins);
+                    if (ok) ok = tok_gather<9, kStaggerXcd>(words, tag, got, want, a.stall, spins);
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
                         ovl[k] = got[k];
@@ -963,7 +995,7 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                                               base + 4 * kHidden, base + 5 * kHidden, base + 6 * kHidden,
                                               base + 7 * kHidden};
             float p8[8] = {};
-            if (ok) ok = tok_gather<8>(words, tag, p8, 0xffu, a.stall, spins);
+            if (ok) ok = tok_gather<8, kStaggerCross>(words, tag, p8, 0xffu, a.stall, spins);
             const float part = ((p8[0] + p8[1]) + (p8[2] + p8[3])) + ((p8[4] + p8[5]) + (p8[6] + p8[7]));
             const float other = xor_lanes<1>(part);
             const float lo = half ? other : part, hi = half ? part : other;
@@ -1065,7 +1097,7 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                                               base + 4 * kHidden, base + 5 * kHidden, base + 6 * kHidden,
                                               base + 7 * kHidden};
             float d8[8] = {};
-            if (ok) ok = tok_gather<8>(words, tag, d8, 0xffu, a.stall, spins);
+            if (ok) ok = tok_gather<8, kStaggerCross>(words, tag, d8, 0xffu, a.stall, spins);
             exchange_put(W[wave] + kTokXOffset + g * kHidden + row, fold_slices(m.r[wave].u.n.xm[row], d8), tag);
         }
 #pragma unroll
