@@ -43,6 +43,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 using dev::exchange_gather;
+using dev::exchange_gather_pipe;
 using dev::masked_b;
 using dev::exchange_put;
 using dev::exchange_put_through;
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
             got[k] = 0.f;
             if (seq < B) want |= 1u << k;
         }
-        ok = exchange_gather<6>(words, a.tag, got, want);
+        ok = exchange_gather_pipe<6, 2>(words, a.tag, got, want);
         auto split_acts = [&](bool scaled) {
             float big = 0.f;
 #pragma unroll
@@ -450,7 +451,7 @@ __global__ __launch_bounds__(512) void ffn_batch_kernel(const BatchFfnArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) words[k] = a.share_words + ((size_t(r) * 8 + k) * kMaxBatch + seq) * 32 + tid;
         float s8[8] = {};
-        if (ok) ok = exchange_gather<8>(words, a.tag, s8, live ? 0xffu : 0u);
+        if (ok) ok = exchange_gather_pipe<8, 6>(words, a.tag, s8, live ? 0xffu : 0u);
         if (live) {
             const float down = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
             a.x_out[seq][row] = a.x[seq][row] + down;

@@ -1941,7 +1941,7 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
         const uint64_t* const words[8] = {base, base + 64, base + 128, base + 192,
                                           base + 256, base + 320, base + 384, base + 448};
         float got[8] = {};
-        if (!exchange_gather<8>(words, args.tag, got, 0xffu)) *args.stall = 1;
+        if (!exchange_gather_pipe<8, 2>(words, args.tag, got, 0xffu)) *args.stall = 1;
 #pragma unroll
         for (int k = 0; k < 8; ++k) rawq[lane + 64 * k] = got[k];
     }
@@ -2152,7 +2152,7 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
                 got[k] = got[4 + k] = got[8 + k] = 0.f;
                 if (p0 + k < ns) want |= 0x111u << k;
             }
-            if (ok) ok = exchange_gather<12>(words, args.tag, got, want);
+            if (ok) ok = exchange_gather_pipe<12, 2>(words, args.tag, got, want);
             float cm = -INFINITY;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
@@ -2189,7 +2189,7 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
             got[k] = 0.f;
             if ((idx >> 8) < B) want |= 1u << k;
         }
-        ok = exchange_gather<4>(words, args.tag, got, want);
+        ok = exchange_gather_pipe<4, 2>(words, args.tag, got, want);
         // Attention rows are convex combinations of FP16 values: they fit
         // FP16 without the range guard.
 #pragma unroll
@@ -2241,7 +2241,7 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
 #pragma unroll
         for (int k = 0; k < 8; ++k) words[k] = args.share_words + ((size_t(r) * 8 + k) * kMaxBatch + seq) * 32 + tid;
         float s8[8] = {};
-        if (ok) ok = exchange_gather<8>(words, args.tag, s8, live ? 0xffu : 0u);
+        if (ok) ok = exchange_gather_pipe<8, 6>(words, args.tag, s8, live ? 0xffu : 0u);
         if (live) {
             const float y = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
             const AttnBatchSeq& sq = args.seq[seq];

@@ -302,5 +302,39 @@ __device__ __forceinline__ bool exchange_gather(const uint64_t* const (&p)[N], u
     return want == 0;
 }
 
+// exchange_gather with two rounds in flight: every round loads all N words
+// (the caller's addresses must be valid for every lane, wanted or not), the
+// second round issued D x 64 clocks after the first, so memory is sampled
+// about twice per round trip and the compiler's waits count one round.
+template <int N, int D>
+__device__ __forceinline__ bool exchange_gather_pipe(const uint64_t* const (&p)[N], uint32_t tag, float (&out)[N],
+                                                     unsigned want, unsigned limit = kExchangeSpins) {
+    uint64_t a[N], b[N];
+    auto issue = [&](uint64_t(&u)[N]) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) u[k] = __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto take = [&](const uint64_t(&u)[N]) {
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (((want >> k) & 1) && uint32_t(u[k] >> 32) == tag) {
+                out[k] = __uint_as_float(uint32_t(u[k]));
+                want &= ~(1u << k);
+            }
+    };
+    issue(a);
+    __builtin_amdgcn_s_sleep(D);
+    for (unsigned spin = 0;;) {
+        issue(b);
+        take(a);
+        if (!__any(want != 0) || ++spin >= limit) break;
+        issue(a);
+        take(b);
+        if (!__any(want != 0) || ++spin >= limit) break;
+    }
+    return want == 0;
+}
+
 }  // namespace dev
 }  // namespace qwen_hip

@@ -418,7 +418,7 @@ void Engine::clear_exchanges() {
     HIP_CHECK(hipMemsetAsync(scratch_.xqkv, 0, kXqkvWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.bexchange, 0, kBatchExchangeWords * sizeof(uint64_t), stream_));
-    HIP_CHECK(hipMemsetAsync(token_words_, 0, kTokWords * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(token_words_, 0, 2 * kTokWords * sizeof(uint64_t), stream_));
 }
 
 uint32_t Engine::reserve_tags(int count) {
