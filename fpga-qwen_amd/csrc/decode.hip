@@ -500,7 +500,8 @@ __global__ __launch_bounds__(256) void ffn_kernel(const FfnArgs a) {
 // (max, lowest id, nonfinite) partials of the lm_head kernel.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ value, const int* __restrict__ index,
                                                       const int* __restrict__ bad_in, int groups,
-                                                      ArgmaxResult* result, ArgmaxResult* host_out, int* stall) {
+                                                      ArgmaxResult* result, ArgmaxResult* host_out, int* stall,
+                                                      unsigned seq) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float bv = -INFINITY;
     int bi = INT_MAX, bad = 0;
@@ -538,6 +539,10 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
         host_out->token = bi;
         host_out->nonfinite = bad;
         host_out->stalled = stalled;
+        const unsigned long long word = (static_cast<unsigned long long>(seq) << 32) |
+                                        (stalled ? 1ull << 31 : 0ull) | (bad ? 1ull << 30 : 0ull) |
+                                        (static_cast<unsigned>(bi) & 0x3fffffffu);
+        __hip_atomic_store(&host_out->done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -2547,7 +2552,7 @@ void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const De
     for (int row = 0; row < 2; ++row)
         argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value + row * kLmGroups, s.lm_index + row * kLmGroups,
                                               s.lm_bad + row * kLmGroups, kLmGroups, pr.result + row,
-                                              host_out + row, s.stall);
+                                              host_out + row, s.stall, 0u);
 }
 
 int attn_batch_pieces(const int* positions, int count, int* pieces_out, int& per) {
@@ -2639,7 +2644,7 @@ void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, i
 }
 
 void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, ArgmaxResult* host_out,
-                    hipStream_t stream) {
+                    hipStream_t stream, unsigned seq) {
     GemvArgs a{};
     a.w = lm_t;
     a.in = s.x;
@@ -2650,7 +2655,8 @@ void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeS
     a.lm_index = s.lm_index;
     a.lm_bad = s.lm_bad;
     gemv_kernel<kHidden, kLmWaves, kLmHead><<<kLmGroups, 64 * kLmWaves, 0, stream>>>(a);
-    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, host_out, s.stall);
+    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, host_out, s.stall,
+                                          seq);
 }
 
 void launch_norm_qkv(const uint16_t* qkv_t, const float* norm_w, const float* x, float* qkv, hipStream_t stream) {

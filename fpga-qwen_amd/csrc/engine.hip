@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -352,7 +353,37 @@ void Engine::release() {
 
 Engine::~Engine() { release(); }
 
-void Engine::sync() { HIP_CHECK(hipStreamSynchronize(stream_)); }
+void Engine::sync() {
+    HIP_CHECK(hipStreamSynchronize(stream_));
+    unsynced_ = false;
+}
+
+// Host reads of device memory and launches that read another engine's
+// buffers first let a step that returned early drain.
+void Engine::settle() {
+    if (unsynced_) sync();
+}
+
+// A decode step returns as soon as its argmax kernel has stored the result
+// word of this launch in pinned memory (the last store of the step's last
+// kernel), instead of waiting for the stream's completion signal. Bounded:
+// after ~20 ms it waits for the stream, which also reports a failed launch.
+void Engine::await_result(int slot) {
+    const unsigned long long* word = &result_host_[slot].done;
+    const auto start = std::chrono::steady_clock::now();
+    for (unsigned spin = 1;; ++spin) {
+        const unsigned long long w = __atomic_load_n(word, __ATOMIC_ACQUIRE);
+        if (uint32_t(w >> 32) == result_seq_) {
+            result_host_[slot].token = int(w & 0x3fffffffu);
+            result_host_[slot].nonfinite = int((w >> 30) & 1u);
+            result_host_[slot].stalled = int((w >> 31) & 1u);
+            unsynced_ = true;
+            return;
+        }
+        if ((spin & 1023u) == 0 && std::chrono::steady_clock::now() - start > std::chrono::milliseconds(20)) break;
+    }
+    sync();
+}
 
 void Engine::invalidate() {
     has_logits_ = false;
@@ -452,7 +483,7 @@ void Engine::run_token(int token, bool head, int result_slot) {
         t.withhold = token_withhold_;
         token_withhold_ = -1;  // the test knob withholds one post, once
         launch_token_layers(t, stream_);
-        if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
+        if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_, ++result_seq_);
         HIP_CHECK(hipGetLastError());
         ++pos_;
         return;
@@ -461,7 +492,7 @@ void Engine::run_token(int token, bool head, int result_slot) {
         launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, pos_, token, cosines_, sines_, options_.context,
                             scratch_, layer_flow(l), stream_);
     if (fused_ffn_) launch_fold_residual(scratch_.xm, scratch_.dparts, scratch_.x, 1, stream_);
-    if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_);
+    if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_, ++result_seq_);
     HIP_CHECK(hipGetLastError());
     ++pos_;
 }
@@ -509,7 +540,8 @@ void Engine::run_append(const int* ids, size_t count) {
     }
     if (batched < count) run_token(ids[count - 1], true, 0);
     HIP_CHECK(hipGetLastError());
-    sync();
+    if (batched == 0) await_result(0);  // one row: its argmax is the call's last kernel
+    else sync();
     check_stall(0);
     has_logits_ = true;
 }
@@ -520,6 +552,7 @@ void Engine::step(int token) { append(&token, 1); }
 const float* Engine::logits() {
     if (!has_logits_) return nullptr;
     if (!host_logits_valid_) {
+        settle();
         host_logits_.resize(kVocab);
         HIP_CHECK(hipMemcpy(host_logits_.data(), scratch_.logits, size_t(kVocab) * 4, hipMemcpyDeviceToHost));
         host_logits_valid_ = true;
@@ -530,6 +563,7 @@ const float* Engine::logits() {
 const float* Engine::hidden() {
     if (!has_logits_ || pos_ <= 0) return nullptr;
     if (!host_hidden_valid_) {
+        settle();
         host_hidden_.resize(kHidden);
         HIP_CHECK(hipMemcpy(host_hidden_.data(), scratch_.hidden, size_t(kHidden) * 4, hipMemcpyDeviceToHost));
         host_hidden_valid_ = true;

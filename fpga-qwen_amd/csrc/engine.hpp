@@ -117,6 +117,8 @@ private:
     void check_stall(int slot) const;
     void release();
     void sync();
+    void settle();
+    void await_result(int slot);
     void invalidate();
 
     Options options_;
@@ -155,6 +157,8 @@ private:
     // QWEN_HIP_FUSED_ATTENTION=0; its launches take tags from the same counter.
     bool fused_attn_ = true;
     uint32_t ffn_tag_ = 0;
+    uint32_t result_seq_ = 0;  // sequence number of the last single-row head launch
+    bool unsynced_ = false;    // a step returned on its result word; the stream may still be finishing
     // A single-row step runs its 28 layers as one persistent launch
     // (launch_token_layers) unless QWEN_HIP_TOKEN_KERNEL=0 (or either fused
     // kernel is switched off): exchange words, poll limit and the test-only

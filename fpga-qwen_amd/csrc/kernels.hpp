@@ -33,6 +33,11 @@ struct ArgmaxResult {
     int token;
     int nonfinite;
     int stalled;  // a fused FFN launch of this step gave up waiting for an exchange
+    int pad;
+    // The step's result in one word, stored last by the argmax kernel at
+    // system scope (host memory): seq << 32 | stalled << 31 | nonfinite << 30
+    // | token. A host that sees its step's seq has the whole result.
+    unsigned long long done;
 };
 
 inline constexpr int kAttnSplits = 32;          // max position splits per KV head
@@ -274,6 +279,6 @@ void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);
 // nonfinite flagged). Also writes the final hidden vector; the selection
 // goes to s.result and to `host_out` (pinned host memory).
 void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, ArgmaxResult* host_out,
-                    hipStream_t stream);
+                    hipStream_t stream, unsigned seq = 0);
 
 }  // namespace qwen_hip
