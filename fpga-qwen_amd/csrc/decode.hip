@@ -2643,20 +2643,191 @@ void launch_decode_layer(const LayerDevice& L, const uint16_t* embed, int pos, i
                             stream);
 }
 
+namespace {
+// Final RMSNorm + tied lm_head + greedy selection in one launch: one
+// workgroup per CU, 8 waves; wave v of workgroup w streams the chain-tiled
+// 8-row tiles 8 w + v + 2048 k, the next tile's loads in flight while it
+// forms the current tile's dots (the reference's chain order, the GEMV
+// path's arithmetic: logits bit-identical to it). Every workgroup forms the
+// norm itself and posts its best (value, lowest id, nonfinite) as two tagged
+// words; workgroup 0 gathers the 256 candidates (through memory: they come
+// from every XCD), selects, takes and clears the step's stall word and
+// writes the result (the argmax kernel's outputs). The selection does not
+// depend on the reduction order (greatest value, lowest id among equals).
+struct LmStreamArgs {
+    GemvArgs g;
+    uint64_t* words;  // [kLmStreamGroups][2]
+    uint32_t tag;
+    ArgmaxResult* result;
+    ArgmaxResult* host_out;
+    int* stall;
+    unsigned seq;
+};
+
+constexpr int kLmStreamWaves = 8, kLmTiles = kVocab / 8, kLmWaveCount = kLmStreamGroups * kLmStreamWaves;
+static_assert(kLmTiles > kLmWaveCount, "every wave streams at least one tile");
+
+__global__ __launch_bounds__(64 * kLmStreamWaves) void lm_head_stream_kernel(const LmStreamArgs a) {
+    constexpr int N = kHidden, THREADS = 64 * kLmStreamWaves, PER = N / THREADS;
+    __shared__ float4 xs4[N / 4];
+    __shared__ double red[kLmStreamWaves];
+    __shared__ float wbest[kLmStreamWaves];
+    __shared__ int wi[kLmStreamWaves], wb[kLmStreamWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 7, r = lane >> 3;
+    float v[PER], wn[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        v[k] = a.g.in[tid + k * THREADS];
+        wn[k] = a.g.norm_w[tid + k * THREADS];
+    }
+    // This wave's tiles first, first + 2048, ...; the first one's loads go
+    // out behind the norm inputs (loads complete in issue order). A rolling
+    // stream: as soon as block b of a tile has entered its dot, block b of
+    // the next tile is loaded into the same registers, so a whole tile stays
+    // in flight per wave and each dot step waits for exactly the oldest block.
+    constexpr int NB = N / 64;
+    const int first = kLmStreamWaves * int(blockIdx.x) + wave;
+    const int count = (kLmTiles - 1 - first) / kLmWaveCount + 1;
+    u32x4 wv[NB];
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        // In block order, as the loop reloads them (the waits count on it).
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.g.w) + size_t(first) * (NB * 64) + lane;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            wv[b] = __builtin_nontemporal_load(wp + b * 64);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    norm_to_lds<N, THREADS, false>(v, wn, reinterpret_cast<float*>(xs4), red,
+                                   blockIdx.x == 0 ? a.g.hidden : nullptr);
+    __syncthreads();
+    const float4* x4 = xs4;
+    float bv = -INFINITY;
+    int bi = INT_MAX, bad = 0;
+    // Every lane of a row holds its sum (combine_chains), so all 8 store it
+    // and take it into the selection: no divergent store, which keeps the
+    // compiler's load waits exact.
+    auto finish = [&](float acc, int tile) {
+        const float y = combine_chains(acc);
+        const int row = tile * 8 + r;
+        a.g.out[row] = y;
+        bad |= !__builtin_isfinite(y);
+        if (better(y, row, bv, bi)) { bv = y; bi = row; }
+    };
+    int tile = first;
+    for (int k = 0; k + 1 < count; ++k, tile += kLmWaveCount) {
+        const u32x4* wp = reinterpret_cast<const u32x4*>(a.g.w) + size_t(tile + kLmWaveCount) * (NB * 64) + lane;
+        float acc = 0.f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            acc = chain8(acc, wv[b], x4[16 * b + 2 * c], x4[16 * b + 2 * c + 1]);
+            wv[b] = __builtin_nontemporal_load(wp + b * 64);
+            __builtin_amdgcn_sched_barrier(0);  // each reload right behind its block's dot step
+        }
+        finish(acc, tile);
+    }
+    {
+        float acc = 0.f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc = chain8(acc, wv[b], x4[16 * b + 2 * c], x4[16 * b + 2 * c + 1]);
+        finish(acc, tile);
+    }
+    auto step = [&](auto off) {
+        constexpr int kOff = decltype(off)::value;
+        const float ov = xor_lanes<kOff>(bv);
+        const int oi = xor_lanes<kOff>(bi);
+        bad |= xor_lanes<kOff>(bad);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    };
+    step(std::integral_constant<int, 8>{});
+    step(std::integral_constant<int, 16>{});
+    step(std::integral_constant<int, 32>{});
+    if (lane == 0) { wbest[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int k = 1; k < kLmStreamWaves; ++k) {
+            bad |= wb[k];
+            if (better(wbest[k], wi[k], bv, bi)) { bv = wbest[k]; bi = wi[k]; }
+        }
+        uint64_t* mine = a.words + 2 * blockIdx.x;
+        exchange_put_through(mine, bv, a.tag);
+        exchange_put_through(mine + 1, __int_as_float((bi & 0x7fffffff) | (bad ? int(0x80000000u) : 0)), a.tag);
+    }
+    if (blockIdx.x != 0) return;
+
+    // Workgroup 0: thread t < 256 gathers workgroup t's candidate.
+    float cv = -INFINITY;
+    int ci = INT_MAX, cb = 0, lost = 0;
+    if (tid < kLmStreamGroups) {
+        const uint64_t* const words[2] = {a.words + 2 * tid, a.words + 2 * tid + 1};
+        float got[2] = {0.f, 0.f};
+        if (exchange_gather_pipe<2, 6>(words, a.tag, got, 3u)) {
+            const int packed = __float_as_int(got[1]);
+            cv = got[0];
+            ci = packed & 0x7fffffff;
+            cb = packed < 0;
+        } else {
+            lost = 1;
+        }
+    }
+    auto step2 = [&](auto off) {
+        constexpr int kOff = decltype(off)::value;
+        const float ov = xor_lanes<kOff>(cv);
+        const int oi = xor_lanes<kOff>(ci);
+        cb |= xor_lanes<kOff>(cb);
+        lost |= xor_lanes<kOff>(lost);
+        if (better(ov, oi, cv, ci)) { cv = ov; ci = oi; }
+    };
+    step2(std::integral_constant<int, 1>{});
+    step2(std::integral_constant<int, 2>{});
+    step2(std::integral_constant<int, 4>{});
+    step2(std::integral_constant<int, 8>{});
+    step2(std::integral_constant<int, 16>{});
+    step2(std::integral_constant<int, 32>{});
+    __syncthreads();  // wbest / wi / wb are reused
+    if (lane == 0) { wbest[wave] = cv; wi[wave] = ci; wb[wave] = cb | (lost << 1); }
+    __syncthreads();
+    if (tid == 0) {
+        int flags = wb[0];
+        for (int k = 1; k < kLmStreamWaves; ++k) {
+            flags |= wb[k];
+            if (better(wbest[k], wi[k], cv, ci)) { cv = wbest[k]; ci = wi[k]; }
+        }
+        const int nonfinite = flags & 1;
+        // A candidate that never arrived is reported as a stalled step.
+        const int stalled = *a.stall | (flags >> 1);
+        *a.stall = 0;
+        a.result->token = ci;
+        a.result->nonfinite = nonfinite;
+        a.result->stalled = stalled;
+        a.host_out->token = ci;
+        a.host_out->nonfinite = nonfinite;
+        a.host_out->stalled = stalled;
+        const unsigned long long word = (static_cast<unsigned long long>(a.seq) << 32) |
+                                        (stalled ? 1ull << 31 : 0ull) | (nonfinite ? 1ull << 30 : 0ull) |
+                                        (static_cast<unsigned>(ci) & 0x3fffffffu);
+        __hip_atomic_store(&a.host_out->done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+}  // namespace
+
 void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, ArgmaxResult* host_out,
-                    hipStream_t stream, unsigned seq) {
-    GemvArgs a{};
-    a.w = lm_t;
-    a.in = s.x;
-    a.norm_w = final_norm;
-    a.out = s.logits;
-    a.hidden = s.hidden;
-    a.lm_value = s.lm_value;
-    a.lm_index = s.lm_index;
-    a.lm_bad = s.lm_bad;
-    gemv_kernel<kHidden, kLmWaves, kLmHead><<<kLmGroups, 64 * kLmWaves, 0, stream>>>(a);
-    argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value, s.lm_index, s.lm_bad, kLmGroups, s.result, host_out, s.stall,
-                                          seq);
+                    uint32_t tag, hipStream_t stream, unsigned seq) {
+    LmStreamArgs a{};
+    a.g.w = lm_t;
+    a.g.in = s.x;
+    a.g.norm_w = final_norm;
+    a.g.out = s.logits;
+    a.g.hidden = s.hidden;
+    a.words = s.lm_words;
+    a.tag = tag;
+    a.result = s.result;
+    a.host_out = host_out;
+    a.stall = s.stall;
+    a.seq = seq;
+    lm_head_stream_kernel<<<kLmStreamGroups, 64 * kLmStreamWaves, 0, stream>>>(a);
 }
 
 void launch_norm_qkv(const uint16_t* qkv_t, const float* norm_w, const float* x, float* qkv, hipStream_t stream) {

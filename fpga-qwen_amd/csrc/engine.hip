@@ -278,6 +278,7 @@ void Engine::init_state() {
     s.xqkv = device_alloc<uint64_t>(kXqkvWords);
     s.xpart = device_alloc<uint64_t>(kXPartWords);
     s.bexchange = device_alloc<uint64_t>(kBatchExchangeWords);
+    s.lm_words = device_alloc<uint64_t>(2 * kLmStreamGroups);
 
     ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
     ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
@@ -450,6 +451,7 @@ void Engine::clear_exchanges() {
     HIP_CHECK(hipMemsetAsync(scratch_.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.bexchange, 0, kBatchExchangeWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(token_words_, 0, 2 * kTokWords * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(scratch_.lm_words, 0, 2 * kLmStreamGroups * sizeof(uint64_t), stream_));
 }
 
 uint32_t Engine::reserve_tags(int count) {
@@ -483,7 +485,7 @@ void Engine::run_token(int token, bool head, int result_slot) {
         t.withhold = token_withhold_;
         token_withhold_ = -1;  // the test knob withholds one post, once
         launch_token_layers(t, stream_);
-        if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_, ++result_seq_);
+        if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, next_tag(), stream_, ++result_seq_);
         HIP_CHECK(hipGetLastError());
         ++pos_;
         return;
@@ -492,7 +494,7 @@ void Engine::run_token(int token, bool head, int result_slot) {
         launch_decode_layer(layers_[l], l == 0 ? embed_ : nullptr, pos_, token, cosines_, sines_, options_.context,
                             scratch_, layer_flow(l), stream_);
     if (fused_ffn_) launch_fold_residual(scratch_.xm, scratch_.dparts, scratch_.x, 1, stream_);
-    if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, stream_, ++result_seq_);
+    if (head) launch_lm_head(lm_t_, final_norm_, scratch_, result_host_ + result_slot, next_tag(), stream_, ++result_seq_);
     HIP_CHECK(hipGetLastError());
     ++pos_;
 }
@@ -535,7 +537,7 @@ void Engine::run_append(const int* ids, size_t count) {
         if (batched == count) {
             HIP_CHECK(hipMemcpyAsync(scratch_.x, prefill_.x + size_t(rows - 1) * kHidden, kHidden * sizeof(float),
                                      hipMemcpyDeviceToDevice, stream_));
-            launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
+            launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, next_tag(), stream_);
         }
     }
     if (batched < count) run_token(ids[count - 1], true, 0);
@@ -869,7 +871,7 @@ float Engine::time_kernel(int which, int iterations) {
         if (which == 8)
             launch_token_layers(token_launch(1, pos_ - 1, 0, 0, scratch_.x), stream_);
         else if (which == 5)
-            launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, stream_);
+            launch_lm_head(lm_t_, final_norm_, scratch_, result_host_, next_tag(), stream_);
         else
             launch_layer_kernel(which == 6 ? 3 : which == 7 ? 0 : which, layers_[layer], nullptr, pos_ - 1, 0,
                                 cosines_, sines_, options_.context, scratch_, flow, stream_);

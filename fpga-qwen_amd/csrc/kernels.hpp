@@ -72,6 +72,7 @@ inline constexpr int kBatchRows = 16;           // output rows of one batched-GE
 inline constexpr int kBatchLmGroups = 256;       // batched lm_head workgroups (one per CU)
 
 inline constexpr int kLmWaves = 8;              // lm_head workgroup waves
+inline constexpr int kLmStreamGroups = 256;     // streaming lm_head: one workgroup per CU
 inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 2374 workgroups
 // Entries of the lm_head partial buffers: the batched head's groups x sequences,
 // or two verification rows of the single-sequence head.
@@ -119,6 +120,7 @@ struct DecodeScratch {
     uint64_t* xqkv;       // [8][512] q/k/v rows of each KV head group (fused QKV + attention kernel)
     uint64_t* xpart;      // [kXPartWords] attention partials of its workgroups
     uint64_t* bexchange;  // [kBatchExchangeWords] batched step exchanges (when this sequence leads a batch)
+    uint64_t* lm_words;   // [kLmStreamGroups][2] lm_head candidates (value, id | nonfinite) with the launch tag
 };
 
 // Exchange words of a batched step, in the first sequence's buffers. The
@@ -279,6 +281,6 @@ void launch_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);
 // nonfinite flagged). Also writes the final hidden vector; the selection
 // goes to s.result and to `host_out` (pinned host memory).
 void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s, ArgmaxResult* host_out,
-                    hipStream_t stream, unsigned seq = 0);
+                    uint32_t tag, hipStream_t stream, unsigned seq = 0);
 
 }  // namespace qwen_hip
