@@ -74,11 +74,11 @@ __device__ __forceinline__ float tile_dot(const u32x4 (&wv)[N / 64], const float
     return combine_chains(acc);
 }
 
-enum GemvMode { kPlain, kQKV, kGateUp, kDown, kLmHead };
+enum GemvMode { kPlain, kQKV, kGateUp, kDown };
 
 // With ROWS input vectors (two-token verification), row q of each per-row
 // buffer starts q strides in: in + q N, x / hidden + q 1024, parts +
-// q 16384, out + q out_stride, lm partials + q gridDim.x.
+// q 16384, out + q out_stride.
 struct GemvArgs {
     const uint16_t* w;        // chain-tiled weights
     const float* in;          // input vector (plain; O: attention output; down), residual x (norm modes)
@@ -109,7 +109,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { retur
 template <int N, int WAVES, int MODE, bool PARTS = false, int ROWS = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
     constexpr int THREADS = WAVES * 64, PER = N / THREADS;
-    constexpr bool kNorm = MODE == kQKV || MODE == kGateUp || MODE == kLmHead;
+    constexpr bool kNorm = MODE == kQKV || MODE == kGateUp;
     __shared__ float4 xs4[ROWS][N / 4];
     __shared__ double red[ROWS][WAVES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
                 }
             }
             norm_to_lds<N, THREADS, kContig>(v[q], wn, xs, red[q],
-                                             MODE == kLmHead && blockIdx.x == 0 ? a.hidden + q * kHidden : nullptr);
+                                             nullptr);
         } else {
 #pragma unroll
             for (int k = 0; k < PER; ++k) xs[xperm(jbase + k * kStride)] = v[q][k];
@@ -256,39 +256,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const GemvArgs a) {
                 const float half_gate = gate * 0.5f;
                 const float t = tanhf(half_gate);
                 out[int(tile) * 4 + r] = gate * (0.5f + 0.5f * t) * up;
-            }
-        } else if constexpr (MODE == kLmHead) {
-            if (c == 0) out[row] = y[q];
-            // Workgroup argmax: lowest id among maxima; any nonfinite value flagged.
-            float bv = -INFINITY;
-            int bi = INT_MAX, bad = 0;
-            if (c == 0) {
-                bad = !__builtin_isfinite(y[q]);
-                if (better(y[q], row, bv, bi)) { bv = y[q]; bi = row; }
-            }
-            auto step = [&](auto off) {
-                constexpr int kOff = decltype(off)::value;
-                const float ov = xor_lanes<kOff>(bv);
-                const int oi = xor_lanes<kOff>(bi);
-                bad |= xor_lanes<kOff>(bad);
-                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            };
-            step(std::integral_constant<int, 8>{});
-            step(std::integral_constant<int, 16>{});
-            step(std::integral_constant<int, 32>{});
-            __shared__ float wbest[ROWS][WAVES];
-            __shared__ int wi[ROWS][WAVES], wb[ROWS][WAVES];
-            if (lane == 0) { wbest[q][wave] = bv; wi[q][wave] = bi; wb[q][wave] = bad; }
-            __syncthreads();
-            if (tid == 0) {
-                for (int k = 1; k < WAVES; ++k) {
-                    bad |= wb[q][k];
-                    if (better(wbest[q][k], wi[q][k], bv, bi)) { bv = wbest[q][k]; bi = wi[q][k]; }
-                }
-                const int slot = q * gridDim.x + blockIdx.x;
-                a.lm_value[slot] = bv;
-                a.lm_index[slot] = bi;
-                a.lm_bad[slot] = bad;
             }
         }
     }
@@ -493,56 +460,6 @@ __global__ __launch_bounds__(256) void ffn_kernel(const FfnArgs a) {
         for (int b = 0; b < kSliceBlocks; ++b) acc = chain8(acc, dw[b], as[16 * b + 2 * c], as[16 * b + 2 * c + 1]);
         const float y = combine_chains(acc);
         if (c == 0) a.dparts[(q * kFfnSlices + g) * kHidden + 8 * down_tile + r] = y;
-    }
-}
-
-// Second pass of the greedy selection: one workgroup reduces the per-group
-// (max, lowest id, nonfinite) partials of the lm_head kernel.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ value, const int* __restrict__ index,
-                                                      const int* __restrict__ bad_in, int groups,
-                                                      ArgmaxResult* result, ArgmaxResult* host_out, int* stall,
-                                                      unsigned seq) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float bv = -INFINITY;
-    int bi = INT_MAX, bad = 0;
-    for (int k = tid; k < groups; k += 1024) {
-        bad |= bad_in[k];
-        if (better(value[k], index[k], bv, bi)) { bv = value[k]; bi = index[k]; }
-    }
-    auto step = [&](auto off) {
-        constexpr int kOff = decltype(off)::value;
-        const float ov = xor_lanes<kOff>(bv);
-        const int oi = xor_lanes<kOff>(bi);
-        bad |= xor_lanes<kOff>(bad);
-        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    };
-    step(std::integral_constant<int, 1>{});
-    step(std::integral_constant<int, 2>{});
-    step(std::integral_constant<int, 4>{});
-    step(std::integral_constant<int, 8>{});
-    step(std::integral_constant<int, 16>{});
-    step(std::integral_constant<int, 32>{});
-    __shared__ float wv[16];
-    __shared__ int wi[16], wb[16];
-    if (lane == 0) { wv[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int k = 1; k < 16; ++k) {
-            bad |= wb[k];
-            if (better(wv[k], wi[k], bv, bi)) { bv = wv[k]; bi = wi[k]; }
-        }
-        const int stalled = *stall;
-        *stall = 0;
-        result->token = bi;
-        result->nonfinite = bad;
-        result->stalled = stalled;
-        host_out->token = bi;
-        host_out->nonfinite = bad;
-        host_out->stalled = stalled;
-        const unsigned long long word = (static_cast<unsigned long long>(seq) << 32) |
-                                        (stalled ? 1ull << 31 : 0ull) | (bad ? 1ull << 30 : 0ull) |
-                                        (static_cast<unsigned>(bi) & 0x3fffffffu);
-        __hip_atomic_store(&host_out->done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -2314,8 +2231,7 @@ void launch_gemv(const GemvArgs& a, int rows, hipStream_t stream) {
 // Two-row launches (verification pairs): waves per workgroup of each mode.
 template <int MODE>
 constexpr int gemv_pair_waves() {
-    if constexpr (MODE == kLmHead) return kLmWaves;
-    else if constexpr (MODE == kGateUp) return 4;
+    if constexpr (MODE == kGateUp) return 4;
     else if constexpr (MODE == kDown) return 1;
     else return 2;
 }
@@ -2534,26 +2450,6 @@ void launch_layer_kernel(int which, const LayerDevice& L, const uint16_t* embed,
     }
 }
 
-void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
-                         const PairScratch& pr, ArgmaxResult* host_out, hipStream_t stream) {
-    GemvArgs a{};
-    a.w = lm_t;
-    a.in = pr.x;
-    a.norm_w = final_norm;
-    a.out = pr.logits;
-    a.out_stride = kVocab;
-    a.hidden = pr.hidden;
-    a.lm_value = s.lm_value;
-    a.lm_index = s.lm_index;
-    a.lm_bad = s.lm_bad;
-    constexpr int W = gemv_pair_waves<kLmHead>();
-    static_assert(W == kLmWaves, "pair lm_head partials use the single-row group count");
-    gemv_kernel<kHidden, W, kLmHead, false, 2><<<kLmGroups, 64 * W, 0, stream>>>(a);
-    for (int row = 0; row < 2; ++row)
-        argmax_kernel<<<1, 1024, 0, stream>>>(s.lm_value + row * kLmGroups, s.lm_index + row * kLmGroups,
-                                              s.lm_bad + row * kLmGroups, kLmGroups, pr.result + row,
-                                              host_out + row, s.stall, 0u);
-}
 
 int attn_batch_pieces(const int* positions, int count, int* pieces_out, int& per) {
     require(count >= 1 && count <= kMaxBatch, "attention batch: 1..8 sequences");
@@ -2654,12 +2550,14 @@ namespace {
 // from every XCD), selects, takes and clears the step's stall word and
 // writes the result (the argmax kernel's outputs). The selection does not
 // depend on the reduction order (greatest value, lowest id among equals).
+// ROWS = 2: the two verification rows, every weight block read once for
+// both (each row with a single row's arithmetic).
 struct LmStreamArgs {
-    GemvArgs g;
-    uint64_t* words;  // [kLmStreamGroups][2]
+    GemvArgs g;       // in / hidden: row q at + q * 1024; out: row q at + q * out_stride
+    uint64_t* words;  // [ROWS][kLmStreamGroups][2]
     uint32_t tag;
-    ArgmaxResult* result;
-    ArgmaxResult* host_out;
+    ArgmaxResult* result;    // [ROWS]
+    ArgmaxResult* host_out;  // [ROWS]
     int* stall;
     unsigned seq;
 };
@@ -2667,23 +2565,26 @@ struct LmStreamArgs {
 constexpr int kLmStreamWaves = 8, kLmTiles = kVocab / 8, kLmWaveCount = kLmStreamGroups * kLmStreamWaves;
 static_assert(kLmTiles > kLmWaveCount, "every wave streams at least one tile");
 
+template <int ROWS>
 __global__ __launch_bounds__(64 * kLmStreamWaves) void lm_head_stream_kernel(const LmStreamArgs a) {
+    static_assert(ROWS == 1 || ROWS == 2, "one or two rows");
     constexpr int N = kHidden, THREADS = 64 * kLmStreamWaves, PER = N / THREADS;
-    __shared__ float4 xs4[N / 4];
-    __shared__ double red[kLmStreamWaves];
-    __shared__ float wbest[kLmStreamWaves];
-    __shared__ int wi[kLmStreamWaves], wb[kLmStreamWaves];
+    __shared__ float4 xs4[ROWS][N / 4];
+    __shared__ double red[ROWS][kLmStreamWaves];
+    __shared__ float wbest[ROWS][kLmStreamWaves];
+    __shared__ int wi[ROWS][kLmStreamWaves], wb[ROWS][kLmStreamWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = lane & 7, r = lane >> 3;
-    float v[PER], wn[PER];
+    float v[ROWS][PER], wn[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        v[k] = a.g.in[tid + k * THREADS];
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) v[q][k] = a.g.in[q * N + tid + k * THREADS];
         wn[k] = a.g.norm_w[tid + k * THREADS];
     }
     // This wave's tiles first, first + 2048, ...; the first one's loads go
     // out behind the norm inputs (loads complete in issue order). A rolling
-    // stream: as soon as block b of a tile has entered its dot, block b of
+    // stream: as soon as block b of a tile has entered its dots, block b of
     // the next tile is loaded into the same registers, so a whole tile stays
     // in flight per wave and each dot step waits for exactly the oldest block.
     constexpr int NB = N / 64;
@@ -2700,67 +2601,90 @@ __global__ __launch_bounds__(64 * kLmStreamWaves) void lm_head_stream_kernel(con
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    norm_to_lds<N, THREADS, false>(v, wn, reinterpret_cast<float*>(xs4), red,
-                                   blockIdx.x == 0 ? a.g.hidden : nullptr);
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q)
+        norm_to_lds<N, THREADS, false>(v[q], wn, reinterpret_cast<float*>(xs4[q]), red[q],
+                                       blockIdx.x == 0 ? a.g.hidden + q * N : nullptr);
     __syncthreads();
-    const float4* x4 = xs4;
-    float bv = -INFINITY;
-    int bi = INT_MAX, bad = 0;
+    float bv[ROWS];
+    int bi[ROWS], bad[ROWS];
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        bv[q] = -INFINITY;
+        bi[q] = INT_MAX;
+        bad[q] = 0;
+    }
     // Every lane of a row holds its sum (combine_chains), so all 8 store it
     // and take it into the selection: no divergent store, which keeps the
     // compiler's load waits exact.
-    auto finish = [&](float acc, int tile) {
-        const float y = combine_chains(acc);
+    auto finish = [&](const float (&acc)[ROWS], int tile) {
         const int row = tile * 8 + r;
-        a.g.out[row] = y;
-        bad |= !__builtin_isfinite(y);
-        if (better(y, row, bv, bi)) { bv = y; bi = row; }
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            const float y = combine_chains(acc[q]);
+            a.g.out[size_t(q) * a.g.out_stride + row] = y;
+            bad[q] |= !__builtin_isfinite(y);
+            if (better(y, row, bv[q], bi[q])) { bv[q] = y; bi[q] = row; }
+        }
+    };
+    auto dot_step = [&](float (&acc)[ROWS], int b) {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q)
+            acc[q] = chain8(acc[q], wv[b], xs4[q][16 * b + 2 * c], xs4[q][16 * b + 2 * c + 1]);
     };
     int tile = first;
     for (int k = 0; k + 1 < count; ++k, tile += kLmWaveCount) {
         const u32x4* wp = reinterpret_cast<const u32x4*>(a.g.w) + size_t(tile + kLmWaveCount) * (NB * 64) + lane;
-        float acc = 0.f;
+        float acc[ROWS] = {};
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            acc = chain8(acc, wv[b], x4[16 * b + 2 * c], x4[16 * b + 2 * c + 1]);
+            dot_step(acc, b);
             wv[b] = __builtin_nontemporal_load(wp + b * 64);
-            __builtin_amdgcn_sched_barrier(0);  // each reload right behind its block's dot step
+            __builtin_amdgcn_sched_barrier(0);  // each reload right behind its block's dot steps
         }
         finish(acc, tile);
     }
     {
-        float acc = 0.f;
+        float acc[ROWS] = {};
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc = chain8(acc, wv[b], x4[16 * b + 2 * c], x4[16 * b + 2 * c + 1]);
+        for (int b = 0; b < NB; ++b) dot_step(acc, b);
         finish(acc, tile);
     }
-    auto step = [&](auto off) {
-        constexpr int kOff = decltype(off)::value;
-        const float ov = xor_lanes<kOff>(bv);
-        const int oi = xor_lanes<kOff>(bi);
-        bad |= xor_lanes<kOff>(bad);
-        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    };
-    step(std::integral_constant<int, 8>{});
-    step(std::integral_constant<int, 16>{});
-    step(std::integral_constant<int, 32>{});
-    if (lane == 0) { wbest[wave] = bv; wi[wave] = bi; wb[wave] = bad; }
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        auto step = [&](auto off) {
+            constexpr int kOff = decltype(off)::value;
+            const float ov = xor_lanes<kOff>(bv[q]);
+            const int oi = xor_lanes<kOff>(bi[q]);
+            bad[q] |= xor_lanes<kOff>(bad[q]);
+            if (better(ov, oi, bv[q], bi[q])) { bv[q] = ov; bi[q] = oi; }
+        };
+        step(std::integral_constant<int, 8>{});
+        step(std::integral_constant<int, 16>{});
+        step(std::integral_constant<int, 32>{});
+        if (lane == 0) { wbest[q][wave] = bv[q]; wi[q][wave] = bi[q]; wb[q][wave] = bad[q]; }
+    }
     __syncthreads();
-    if (tid == 0) {
+    if (tid < ROWS) {
+        const int q = tid;
+        float cv = wbest[q][0];
+        int ci = wi[q][0], cb = wb[q][0];
         for (int k = 1; k < kLmStreamWaves; ++k) {
-            bad |= wb[k];
-            if (better(wbest[k], wi[k], bv, bi)) { bv = wbest[k]; bi = wi[k]; }
+            cb |= wb[q][k];
+            if (better(wbest[q][k], wi[q][k], cv, ci)) { cv = wbest[q][k]; ci = wi[q][k]; }
         }
-        uint64_t* mine = a.words + 2 * blockIdx.x;
-        exchange_put_through(mine, bv, a.tag);
-        exchange_put_through(mine + 1, __int_as_float((bi & 0x7fffffff) | (bad ? int(0x80000000u) : 0)), a.tag);
+        uint64_t* mine = a.words + 2 * (size_t(q) * kLmStreamGroups + blockIdx.x);
+        exchange_put_through(mine, cv, a.tag);
+        exchange_put_through(mine + 1, __int_as_float((ci & 0x7fffffff) | (cb ? int(0x80000000u) : 0)), a.tag);
     }
     if (blockIdx.x != 0) return;
 
-    // Workgroup 0: thread t < 256 gathers workgroup t's candidate.
+    // Workgroup 0: thread t < ROWS x 256 gathers row t / 256's candidate of
+    // workgroup t % 256 (waves 0-3: row 0, waves 4-7: row 1).
+    static_assert(ROWS * kLmStreamGroups <= THREADS, "one candidate per thread");
     float cv = -INFINITY;
     int ci = INT_MAX, cb = 0, lost = 0;
-    if (tid < kLmStreamGroups) {
+    if (tid < ROWS * kLmStreamGroups) {
         const uint64_t* const words[2] = {a.words + 2 * tid, a.words + 2 * tid + 1};
         float got[2] = {0.f, 0.f};
         if (exchange_gather_pipe<2, 6>(words, a.tag, got, 3u)) {
@@ -2787,28 +2711,35 @@ __global__ __launch_bounds__(64 * kLmStreamWaves) void lm_head_stream_kernel(con
     step2(std::integral_constant<int, 16>{});
     step2(std::integral_constant<int, 32>{});
     __syncthreads();  // wbest / wi / wb are reused
-    if (lane == 0) { wbest[wave] = cv; wi[wave] = ci; wb[wave] = cb | (lost << 1); }
+    if (lane == 0) { wbest[0][wave] = cv; wi[0][wave] = ci; wb[0][wave] = cb | (lost << 1); }
     __syncthreads();
     if (tid == 0) {
-        int flags = wb[0];
-        for (int k = 1; k < kLmStreamWaves; ++k) {
-            flags |= wb[k];
-            if (better(wbest[k], wi[k], cv, ci)) { cv = wbest[k]; ci = wi[k]; }
-        }
-        const int nonfinite = flags & 1;
-        // A candidate that never arrived is reported as a stalled step.
-        const int stalled = *a.stall | (flags >> 1);
+        // The step's stall word covers both rows (one launch wrote them).
+        int flags_all = 0;
+        for (int k = 0; k < kLmStreamWaves; ++k) flags_all |= wb[0][k] & 2;
+        const int stalled = *a.stall | (flags_all >> 1);
         *a.stall = 0;
-        a.result->token = ci;
-        a.result->nonfinite = nonfinite;
-        a.result->stalled = stalled;
-        a.host_out->token = ci;
-        a.host_out->nonfinite = nonfinite;
-        a.host_out->stalled = stalled;
-        const unsigned long long word = (static_cast<unsigned long long>(a.seq) << 32) |
-                                        (stalled ? 1ull << 31 : 0ull) | (nonfinite ? 1ull << 30 : 0ull) |
-                                        (static_cast<unsigned>(ci) & 0x3fffffffu);
-        __hip_atomic_store(&a.host_out->done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        for (int q = 0; q < ROWS; ++q) {
+            constexpr int kWavesPerRow = kLmStreamGroups / 64;
+            float qv = wbest[0][q * kWavesPerRow];
+            int qi = wi[0][q * kWavesPerRow], flags = wb[0][q * kWavesPerRow];
+            for (int k = 1; k < kWavesPerRow; ++k) {
+                const int w = q * kWavesPerRow + k;
+                flags |= wb[0][w];
+                if (better(wbest[0][w], wi[0][w], qv, qi)) { qv = wbest[0][w]; qi = wi[0][w]; }
+            }
+            const int nonfinite = flags & 1;
+            a.result[q].token = qi;
+            a.result[q].nonfinite = nonfinite;
+            a.result[q].stalled = stalled;
+            a.host_out[q].token = qi;
+            a.host_out[q].nonfinite = nonfinite;
+            a.host_out[q].stalled = stalled;
+            const unsigned long long word = (static_cast<unsigned long long>(a.seq) << 32) |
+                                            (stalled ? 1ull << 31 : 0ull) | (nonfinite ? 1ull << 30 : 0ull) |
+                                            (static_cast<unsigned>(qi) & 0x3fffffffu);
+            __hip_atomic_store(&a.host_out[q].done, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 }  // namespace
@@ -2820,6 +2751,7 @@ void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeS
     a.g.in = s.x;
     a.g.norm_w = final_norm;
     a.g.out = s.logits;
+    a.g.out_stride = kVocab;
     a.g.hidden = s.hidden;
     a.words = s.lm_words;
     a.tag = tag;
@@ -2827,7 +2759,26 @@ void launch_lm_head(const uint16_t* lm_t, const float* final_norm, const DecodeS
     a.host_out = host_out;
     a.stall = s.stall;
     a.seq = seq;
-    lm_head_stream_kernel<<<kLmStreamGroups, 64 * kLmStreamWaves, 0, stream>>>(a);
+    lm_head_stream_kernel<1><<<kLmStreamGroups, 64 * kLmStreamWaves, 0, stream>>>(a);
+}
+
+void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
+                         const PairScratch& pr, ArgmaxResult* host_out, uint32_t tag, hipStream_t stream,
+                         unsigned seq) {
+    LmStreamArgs a{};
+    a.g.w = lm_t;
+    a.g.in = pr.x;
+    a.g.norm_w = final_norm;
+    a.g.out = pr.logits;
+    a.g.out_stride = kVocab;
+    a.g.hidden = pr.hidden;
+    a.words = s.lm_words;
+    a.tag = tag;
+    a.result = pr.result;
+    a.host_out = host_out;
+    a.stall = s.stall;
+    a.seq = seq;
+    lm_head_stream_kernel<2><<<kLmStreamGroups, 64 * kLmStreamWaves, 0, stream>>>(a);
 }
 
 void launch_norm_qkv(const uint16_t* qkv_t, const float* norm_w, const float* x, float* qkv, hipStream_t stream) {

@@ -278,7 +278,7 @@ void Engine::init_state() {
     s.xqkv = device_alloc<uint64_t>(kXqkvWords);
     s.xpart = device_alloc<uint64_t>(kXPartWords);
     s.bexchange = device_alloc<uint64_t>(kBatchExchangeWords);
-    s.lm_words = device_alloc<uint64_t>(2 * kLmStreamGroups);
+    s.lm_words = device_alloc<uint64_t>(4 * kLmStreamGroups);
 
     ver_logits_ = device_alloc<float>(size_t(2) * kVocab);
     ver_hidden_ = device_alloc<float>(size_t(2) * kHidden);
@@ -451,7 +451,7 @@ void Engine::clear_exchanges() {
     HIP_CHECK(hipMemsetAsync(scratch_.xpart, 0, kXPartWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(scratch_.bexchange, 0, kBatchExchangeWords * sizeof(uint64_t), stream_));
     HIP_CHECK(hipMemsetAsync(token_words_, 0, 2 * kTokWords * sizeof(uint64_t), stream_));
-    HIP_CHECK(hipMemsetAsync(scratch_.lm_words, 0, 2 * kLmStreamGroups * sizeof(uint64_t), stream_));
+    HIP_CHECK(hipMemsetAsync(scratch_.lm_words, 0, 4 * kLmStreamGroups * sizeof(uint64_t), stream_));
 }
 
 uint32_t Engine::reserve_tags(int count) {
@@ -718,7 +718,7 @@ TokenLaunch Engine::token_launch(int rows, int pos, int first, int second, float
 
 void Engine::run_pair(int first, int second) {
     launch_token_layers(token_launch(2, pos_, first, second, pair_.x), stream_);
-    launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, stream_);
+    launch_lm_head_pair(lm_t_, final_norm_, scratch_, pair_, result_host_ + 1, next_tag(), stream_, ++result_seq_);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -731,7 +731,8 @@ void Engine::verify_two(int first, int second) {
     const int start = pos_;
     std::lock_guard<std::mutex> hold(launch_lock());
     try {
-        if (token_kernel_ && token_pair_supported(start)) {
+        const bool pair = token_kernel_ && token_pair_supported(start);
+        if (pair) {
             run_pair(first, second);
         } else {
             // Without the token kernel, or where the two rows would take
@@ -759,7 +760,12 @@ void Engine::verify_two(int first, int second) {
                                          hipMemcpyDeviceToDevice, stream_));
             }
         }
-        sync();
+        if (pair) {  // both rows' result words, stored last by the one head launch
+            await_result(1);
+            await_result(2);
+        } else {
+            sync();
+        }
         check_stall(1);
         check_stall(2);
         pos_ = start;

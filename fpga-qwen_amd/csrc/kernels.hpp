@@ -71,13 +71,10 @@ inline constexpr int kMaxBatch = 8;             // sequences per batched decode 
 inline constexpr int kBatchRows = 16;           // output rows of one batched-GEMV MFMA tile
 inline constexpr int kBatchLmGroups = 256;       // batched lm_head workgroups (one per CU)
 
-inline constexpr int kLmWaves = 8;              // lm_head workgroup waves
-inline constexpr int kLmStreamGroups = 256;     // streaming lm_head: one workgroup per CU
-inline constexpr int kLmGroups = kVocab / (8 * kLmWaves);  // 2374 workgroups
-// Entries of the lm_head partial buffers: the batched head's groups x sequences,
-// or two verification rows of the single-sequence head.
-inline constexpr int kLmPartials = kBatchLmGroups * kMaxBatch > 2 * kLmGroups ? kBatchLmGroups * kMaxBatch : 2 * kLmGroups;
-static_assert(kVocab % (8 * kLmWaves) == 0, "lm_head tiles must cover the vocabulary");
+inline constexpr int kLmStreamGroups = 256;     // single-sequence lm_head: one workgroup per CU
+// Entries of the lm_head partial buffers: the batched head's groups x sequences.
+inline constexpr int kLmPartials = kBatchLmGroups * kMaxBatch;
+static_assert(kVocab % 8 == 0, "lm_head tiles of 8 rows must cover the vocabulary");
 
 struct LayerDevice {
     const uint16_t* qkv_t;     // tiled [4096 x 1024]: q rows, k rows, v rows
@@ -109,7 +106,7 @@ struct DecodeScratch {
     float* hidden;        // [1024] final normalized hidden
     float* attn_partial;  // [8][kAttnSplits][kAttnPartial]: unnormalized o, max, sum per split
     float* o_part;        // [16][1024]: per-query-head partial O projections
-    float* lm_value;      // [kLmPartials] argmax partials: [kBatchLmGroups][kMaxBatch] (batched), [2][kLmGroups] (pair)
+    float* lm_value;      // [kLmPartials] argmax partials of the batched head: [kBatchLmGroups][kMaxBatch]
     int* lm_index;
     int* lm_bad;
     ArgmaxResult* result; // [1] device copy of the selection
@@ -120,7 +117,7 @@ struct DecodeScratch {
     uint64_t* xqkv;       // [8][512] q/k/v rows of each KV head group (fused QKV + attention kernel)
     uint64_t* xpart;      // [kXPartWords] attention partials of its workgroups
     uint64_t* bexchange;  // [kBatchExchangeWords] batched step exchanges (when this sequence leads a batch)
-    uint64_t* lm_words;   // [kLmStreamGroups][2] lm_head candidates (value, id | nonfinite) with the launch tag
+    uint64_t* lm_words;   // [2 rows][kLmStreamGroups][2] lm_head candidates (value, id | nonfinite) with the launch tag
 };
 
 // Exchange words of a batched step, in the first sequence's buffers. The
@@ -206,10 +203,12 @@ struct PairScratch {
     ArgmaxResult* result; // [2] device copies of the selections
 };
 
-// Final norm + lm_head + greedy argmax of both verification rows (uses the
-// lm partial buffers of s); selections to pair.result and host_out[0..1].
+// Final norm + lm_head + greedy selection of both verification rows in one
+// launch (each weight block read once for both; candidate words of s);
+// selections to pair.result and host_out[0..1], each with its result word.
 void launch_lm_head_pair(const uint16_t* lm_t, const float* final_norm, const DecodeScratch& s,
-                         const PairScratch& pair, ArgmaxResult* host_out, hipStream_t stream);
+                         const PairScratch& pair, ArgmaxResult* host_out, uint32_t tag, hipStream_t stream,
+                         unsigned seq);
 
 // One sequence of a batched norm + QKV + attention + O launch.
 struct AttnSeq {
