@@ -169,6 +169,10 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
     static_assert(EPI != 4 || BN == kTileN, "the QKV epilogue takes one head per tile");
     constexpr int kStages = S::kStages, kLoads = S::kLoads, kStageBytes = S::kStageBytes;
     constexpr int kASlots = S::kASlots, WR = S::WR, TI = S::TI, TJ = S::TJ;
+    // Overlapped operand reads (below) for 2 x 2 MFMA tiles per wave; the
+    // K-split 192-column instance keeps the plain order (8 more registers
+    // would spill there).
+    constexpr bool kPipelined = TI == 2 && TJ == 2 && !(EPI == 2 && BN == 192);
     constexpr int kThreads = S::kWaves * 64;
     constexpr int kCPitch = BN + 4;  // floats per row of the staged C tile
     constexpr int kEpiBytes = BM * kCPitch * 4 + (EPI == 4 ? BM * kHeadDim * 2 : 0);
@@ -283,29 +287,81 @@ __global__ __launch_bounds__((GemmShape<BM, BN>::kWaves * 64)) void gemm_kernel(
                 stage_barrier();
             }
             if (mma) {
-                const unsigned char* stage = smem + (kt % kStages) * kStageBytes;
-#pragma unroll
-                for (int sub = 0; sub < 4; ++sub) {
-                    const int p = 2 * sub + (lane >> 5);  // k = 16 sub + 8 (lane / 32) .. + 7 of the step
-                    half8 ah[TI], al[TI], bb[TJ];
-#pragma unroll
-                    for (int i = 0; i < TI; ++i) {
+                if constexpr (kPipelined) {
+                    // Operand reads of sub-step sub + 1 overlap the MFMAs of sub:
+                    // the B pair and row tile 0 of sub + 1 are read while row tile
+                    // 1 of sub multiplies, row tile 1 of sub + 1 while row tile 0
+                    // of sub + 1 does. Each accumulator still takes hi then lo of
+                    // sub 0, 1, 2, 3 in turn.
+                    const unsigned char* stage = smem + (kt % kStages) * kStageBytes;
+                    auto read_a = [&](int sub, int i, half8& h, half8& l) {
+                        const int p = 2 * sub + (lane >> 5);
                         const int ra = (wm * TI + i) * 32 + fr, sa = 8 * ra + (p ^ swz(ra));
-                        ah[i] = *reinterpret_cast<const half8*>(stage + 16 * sa);
-                        al[i] = *reinterpret_cast<const half8*>(stage + 16 * (kASlots + sa));
-                    }
-#pragma unroll
-                    for (int jt = 0; jt < TJ; ++jt) {
-                        const int rb = wn * (BN / S::WC) + 32 * jt + fr;
-                        bb[jt] = *reinterpret_cast<const half8*>(stage + 16 * (2 * kASlots + 8 * rb + (p ^ swz(rb))));
-                    }
-#pragma unroll
-                    for (int i = 0; i < TI; ++i)
+                        h = *reinterpret_cast<const half8*>(stage + 16 * sa);
+                        l = *reinterpret_cast<const half8*>(stage + 16 * (kASlots + sa));
+                    };
+                    auto read_b = [&](int sub, half8 (&b)[TJ]) {
+                        const int p = 2 * sub + (lane >> 5);
 #pragma unroll
                         for (int jt = 0; jt < TJ; ++jt) {
-                            acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bb[jt], acc[i][jt], 0, 0, 0);
-                            acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bb[jt], acc[i][jt], 0, 0, 0);
+                            const int rb = wn * (BN / S::WC) + 32 * jt + fr;
+                            b[jt] = *reinterpret_cast<const half8*>(stage + 16 * (2 * kASlots + 8 * rb + (p ^ swz(rb))));
                         }
+                    };
+                    half8 a0h, a0l, a1h, a1l, bb[2][TJ];
+                    read_a(0, 0, a0h, a0l);
+                    read_b(0, bb[0]);
+                    read_a(0, 1, a1h, a1l);
+#pragma unroll
+                    for (int sub = 0; sub < 4; ++sub) {
+                        half8(&cur)[TJ] = bb[sub & 1];
+#pragma unroll
+                        for (int jt = 0; jt < TJ; ++jt)
+                            acc[0][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, cur[jt], acc[0][jt], 0, 0, 0);
+#pragma unroll
+                        for (int jt = 0; jt < TJ; ++jt)
+                            acc[0][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0l, cur[jt], acc[0][jt], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (sub < 3) {
+                            read_b(sub + 1, bb[(sub + 1) & 1]);
+                            read_a(sub + 1, 0, a0h, a0l);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int jt = 0; jt < TJ; ++jt)
+                            acc[1][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, cur[jt], acc[1][jt], 0, 0, 0);
+#pragma unroll
+                        for (int jt = 0; jt < TJ; ++jt)
+                            acc[1][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1l, cur[jt], acc[1][jt], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (sub < 3) read_a(sub + 1, 1, a1h, a1l);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else {
+                    const unsigned char* stage = smem + (kt % kStages) * kStageBytes;
+#pragma unroll
+                    for (int sub = 0; sub < 4; ++sub) {
+                        const int p = 2 * sub + (lane >> 5);  // k = 16 sub + 8 (lane / 32) .. + 7 of the step
+                        half8 ah[TI], al[TI], bb[TJ];
+#pragma unroll
+                        for (int i = 0; i < TI; ++i) {
+                            const int ra = (wm * TI + i) * 32 + fr, sa = 8 * ra + (p ^ swz(ra));
+                            ah[i] = *reinterpret_cast<const half8*>(stage + 16 * sa);
+                            al[i] = *reinterpret_cast<const half8*>(stage + 16 * (kASlots + sa));
+                        }
+#pragma unroll
+                        for (int jt = 0; jt < TJ; ++jt) {
+                            const int rb = wn * (BN / S::WC) + 32 * jt + fr;
+                            bb[jt] = *reinterpret_cast<const half8*>(stage + 16 * (2 * kASlots + 8 * rb + (p ^ swz(rb))));
+                        }
+#pragma unroll
+                        for (int i = 0; i < TI; ++i)
+#pragma unroll
+                            for (int jt = 0; jt < TJ; ++jt) {
+                                acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bb[jt], acc[i][jt], 0, 0, 0);
+                                acc[i][jt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bb[jt], acc[i][jt], 0, 0, 0);
+                            }
+                    }
                 }
             }
         }
