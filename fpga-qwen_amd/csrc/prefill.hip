@@ -56,16 +56,18 @@ __device__ __forceinline__ double wave_sum(double v) {
 constexpr int kTileN = 128, kTileK = 64;
 
 // BN = 192 or 256 (only with BM = 128): 1.5x or 2x the columns per
-// workgroup, so every A byte streamed feeds more MFMA work; 6 or 8 MFMA waves
-// on 64x64 tiles and 2 stages of 56 or 64 KiB (the LDS holds no third). At
+// workgroup, so every A byte streamed feeds more MFMA work; 8 MFMA waves, two
+// per SIMD, on 32x96 (BN = 192) or 64x64 tiles (6 waves of 64x64 put two
+// SIMDs' worth of MFMAs on two of the four), and 2 stages of 56 or 64 KiB
+// (the LDS holds no third). At
 // BN = 192 a stage is 56 loads of 1 KiB, so half of the 16 waves issue 4 and
 // half 3 (with two stages every wait is for all of a wave's loads).
 template <int BM, int BN = kTileN>
 struct GemmShape {
     static_assert(BN == kTileN || ((BN == 192 || BN == 256) && BM == 128), "wide tiles with 128 rows only");
     static constexpr int kWaves = BM == 128 ? 16 : 8;            // waves per workgroup (all load)
-    static constexpr int kMma = BN == 192 ? 6 : BM == 64 || BN == 256 ? 8 : 4;  // waves running the MFMAs
-    static constexpr int TI = BM == 128 ? 2 : 1;                 // 32-row tiles per MFMA wave
+    static constexpr int kMma = BM == 64 || BN == 192 || BN == 256 ? 8 : 4;  // waves running the MFMAs
+    static constexpr int TI = BM == 128 && BN != 192 ? 2 : 1;    // 32-row tiles per MFMA wave
     static constexpr int WR = BM / 32 / TI, WC = kMma / WR;      // MFMA wave grid
     static constexpr int TJ = BN / WC / 32;                      // 32-column tiles per MFMA wave
     static constexpr int kASlots = BM * 8, kBSlots = BN * 8;     // 16-byte slots per stage
@@ -922,7 +924,7 @@ void gemm(const uint16_t* Ah, const uint16_t* Al, const uint16_t* W, float* C, i
             Ah, Al, W, C, M, N, K, ep);
     };
     using I128 = std::integral_constant<int, 128>;
-    // 128-row tiles of 128, 192 or 256 columns (the QKV epilogue takes one
+        // 128-row tiles of 128, 192 or 256 columns (the QKV epilogue takes one
     // head per tile): the fewest rounds of 256 workgroups, each round priced
     // at the measured time of one workgroup of that width relative to 128.
     if constexpr (EPI != 4) {
