@@ -1707,10 +1707,12 @@ __global__ __launch_bounds__(512) void attn_batch_kernel(const AttnBatchArgs arg
     auto load_block = [&](u32x4 (&k)[2], u32x4 (&v)[2], int i) {
         const bool shared = t_begin + 64 * i < a.shared;  // uniform; a.shared is a multiple of 64
         const __amdgpu_buffer_rsrc_t kb = shared ? skrs : krs, vb = shared ? svrs : vrs;
-        k[0] = __builtin_amdgcn_raw_buffer_load_b128(kb, koff, 16384 * i, kLoadNT);
-        k[1] = __builtin_amdgcn_raw_buffer_load_b128(kb, koff + 128, 16384 * i, kLoadNT);
-        v[0] = __builtin_amdgcn_raw_buffer_load_b128(vb, voff, 16384 * i, kLoadNT);
-        v[1] = __builtin_amdgcn_raw_buffer_load_b128(vb, voff + 1024, 16384 * i, kLoadNT);
+        // The block offset goes into the per-lane offset, which the range
+        // check covers, so rows past the piece are never read.
+        k[0] = __builtin_amdgcn_raw_buffer_load_b128(kb, koff + 16384 * i, 0, kLoadNT);
+        k[1] = __builtin_amdgcn_raw_buffer_load_b128(kb, koff + 128 + 16384 * i, 0, kLoadNT);
+        v[0] = __builtin_amdgcn_raw_buffer_load_b128(vb, voff + 16384 * i, 0, kLoadNT);
+        v[1] = __builtin_amdgcn_raw_buffer_load_b128(vb, voff + 1024 + 16384 * i, 0, kLoadNT);
     };
     u32x4 kr[kInFlight][2], vr[kInFlight][2];
 
