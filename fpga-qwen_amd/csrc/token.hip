@@ -873,9 +873,13 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             }
             barrier();  // B6
         } else {
-            // Each workgroup with positions posts (output, max, sum) of both
-            // heads; workgroup (g, s) merges head h over the active partials
-            // (4 groups of 8 against their own maximum, then combined).
+            // Each workgroup with positions writes (output, max, sum) of both
+            // heads as plain floats and, once a wave's stores are in the
+            // XCD's L2, posts that wave's flag; workgroup (g, s) polls the
+            // flags of the active partials, reads them in one pass and merges
+            // head h (4 groups of 8 against their own maximum, then
+            // combined). Polling the 32 x 130 tagged words themselves cost
+            // 2-3 us per layer of rounds that re-read all of them.
 #pragma unroll
             for (int q = 0; q < ROWS; ++q) {
                 if (s < active[q] && tid < 256) {
@@ -887,45 +891,52 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                                      (R.u.opart[6][hh][j] + R.u.opart[7][hh][j]));
                     const float lsum = ((R.wsum[0][hh] + R.wsum[1][hh]) + (R.wsum[2][hh] + R.wsum[3][hh])) +
                                        ((R.wsum[4][hh] + R.wsum[5][hh]) + (R.wsum[6][hh] + R.wsum[7][hh]));
-                    uint64_t* part = W[q] + kTokPartOffset + ((size_t(g) * 32 + s) * 2 + hh) * kXPart;
-                    exchange_put(part + j, o, tag);
+                    float* pay = reinterpret_cast<float*>(W[q] + kTokPartOffset) + ((size_t(g) * 32 + s) * 2 + hh) * kXPart;
+                    pay[j] = o;
                     if (j == 0) {
-                        exchange_put(part + 128, hh ? m1[q] : m0[q], tag);
-                        exchange_put(part + 129, lsum, tag);
+                        pay[128] = hh ? m1[q] : m0[q];
+                        pay[129] = lsum;
                     }
                 }
+            }
+            // The floats of this wave are in the XCD's L2 once its stores
+            // have completed; then its flag tells the readers.
+            if (tid < 256) {
+                __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+#pragma unroll
+                for (int q = 0; q < ROWS; ++q)
+                    if (s < active[q] && lane == 0)
+                        exchange_put(W[q] + kTokPartFlagOffset + (size_t(g) * 32 + s) * 4 + wave, 0.f, tag);
             }
 #pragma unroll
             for (int q = 0; q < ROWS; ++q) {
                 const int gq = tid >> 7;
                 float mv[8], lv[8], ovl[8];
                 {
-                    // Every lane polls its output entry of the group's 8
-                    // partials; lane k < 8 of each wave also polls the
-                    // maximum of partial k and lane 8 + k its sum, which
-                    // every lane then reads from those lanes.
-                    auto part = [&](int k) {
-                        return W[q] + kTokPartOffset + ((size_t(g) * 32 + 8 * gq + k) * 2 + hq) * kXPart;
-                    };
-                    const uint64_t* words[9];
-                    float got[9];
-                    unsigned want = 0;
+                    // Lanes 0-15 of each wave poll the flags of the group's
+                    // 8 partials (the two posting waves of head hq); then
+                    // every lane reads its output entry of the 8 partials,
+                    // lane k < 8 the maximum of partial k and lane 8 + k its
+                    // sum, which every lane then reads from those lanes.
+                    const int kf = lane & 7;
+                    const uint64_t* const flag[1] = {W[q] + kTokPartFlagOffset + (size_t(g) * 32 + 8 * gq + kf) * 4 +
+                                                     2 * hq + ((lane >> 3) & 1)};
+                    float unused[1] = {0.f};
+                    const unsigned want = lane < 16 && 8 * gq + kf < active[q] ? 1u : 0u;
+                    if (ok) ok = tok_gather<1, kStaggerXcd>(flag, tag, unused, want, a.stall, spins);
+                    const uint32_t* pay = reinterpret_cast<const uint32_t*>(W[q] + kTokPartOffset) +
+                                          (size_t(g) * 32 + 8 * gq) * 2 * kXPart + hq * kXPart;
+                    uint32_t raw[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        raw[k] = __hip_atomic_load(pay + k * 2 * kXPart + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const uint32_t ml = __hip_atomic_load(pay + kf * 2 * kXPart + (lane < 8 ? 128 : 129),
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
                     for (int k = 0; k < 8; ++k) {
-                        words[k] = part(k) + j;
-                        got[k] = 0.f;
-                        if (8 * gq + k < active[q]) want |= 1u << k;
-                    }
-                    const int kk = lane & 7;
-                    words[8] = part(kk) + (lane < 8 ? 128 : 129);
-                    got[8] = 0.f;
-                    if (lane < 16 && 8 * gq + kk < active[q]) want |= 1u << 8;
-                    if (ok) ok = tok_gather<9, kStaggerXcd>(words, tag, got, want, a.stall, spins);
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        ovl[k] = got[k];
-                        mv[k] = 8 * gq + k < active[q] ? __shfl(got[8], k) : -INFINITY;
-                        lv[k] = __shfl(got[8], 8 + k);
+                        ovl[k] = 8 * gq + k < active[q] ? __uint_as_float(raw[k]) : 0.f;
+                        mv[k] = 8 * gq + k < active[q] ? __uint_as_float(__shfl(ml, k)) : -INFINITY;
+                        lv[k] = __uint_as_float(__shfl(ml, 8 + k));
                     }
                 }
                 float mx = -INFINITY;

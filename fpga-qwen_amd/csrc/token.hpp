@@ -23,7 +23,10 @@ struct TokenLayer {
 };
 
 // Exchange words of the token kernel (uint64: tag << 32 | FP32 bits): q/k/v
-// rows [8][512], attention partials [8][32][2][130], O partials posted across
+// rows [8][512], the split form's attention partials as plain FP32
+// [8][32][2][130] (two per word) with one tagged flag per posting wave
+// [8][32][4] (posted once the wave's partial floats are in the XCD's L2),
+// O partials posted across
 // XCDs [16 heads][1024 rows], the post-attention residual broadcast in each
 // XCD [8][1024], activations [3072], down slices posted across XCDs
 // [8 slices][1024 rows], the next layer's residual broadcast in each XCD
@@ -32,7 +35,8 @@ struct TokenLayer {
 // more).
 inline constexpr int kTokQkvOffset = 0;
 inline constexpr int kTokPartOffset = kTokQkvOffset + kKVHeads * 512;
-inline constexpr int kTokOCrossOffset = kTokPartOffset + kKVHeads * 32 * 2 * (kHeadDim + 2);
+inline constexpr int kTokPartFlagOffset = kTokPartOffset + kKVHeads * 32 * 2 * (kHeadDim + 2) / 2;
+inline constexpr int kTokOCrossOffset = kTokPartFlagOffset + kKVHeads * 32 * 4;
 inline constexpr int kTokXmOffset = kTokOCrossOffset + kHidden * kQHeads;
 inline constexpr int kTokActOffset = kTokXmOffset + 8 * kHidden;
 inline constexpr int kTokDCrossOffset = kTokActOffset + kFFN;
