@@ -547,6 +547,39 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             m.rope[q][1][lane] = a.sines[size_t(pos + q) * 64 + lane];
         }
     }
+    // K/V rows of this workgroup's passes in layer `layer` from the cache
+    // (the rows at pos and pos + 1 come from LDS; positions past them, and
+    // all of an inactive workgroup's, read row 0).
+    auto load_kv = [&](int layer, int t_id, u32x4 (&kreg)[PASSES][2], u32x4 (&vreg)[PASSES][2]) {
+        const TokenLayer& KL = a.layers[layer];
+        const uint16_t* kv_values = KL.keys + size_t(kKVHeads) * a.context * 128;
+        const int kl = t_id & 63, kw = t_id >> 6, kc = t_id & 7, kg = t_id >> 3;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int t = pass_base(p) + kg;
+            const int tl = mine && t < pos ? t : 0;
+            const global_u32x4* kp = global_rows(KL.keys + (head_base + tl) * 128);
+            kreg[p][0] = kp[kc];
+            kreg[p][1] = kp[kc + 8];
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int t = pass_base(p) + 8 * kw + 4 * hf + (kl >> 4);
+                const int tl = mine && t < pos ? t : 0;
+                vreg[p][hf] = global_rows(kv_values + (head_base + tl) * 128)[kl & 15];
+            }
+    };
+    // One row with up to 3 passes: each layer's K/V loads are issued at the
+    // end of the layer before (the first layer's here), after its last
+    // gather, so that they land under the barrier and the norm instead of
+    // holding up the norm waves at the layer start (token kernel 329 -> 327
+    // us at 109 positions, 477 -> 466 at 4034, the same bits); more passes,
+    // or two rows, would spill, and load at the layer start.
+    constexpr bool kEarlyKv = ROWS == 1 && PASSES <= 3;
+    u32x4 knext[PASSES][2], vnext[PASSES][2];
+    if constexpr (kEarlyKv) load_kv(0, int(threadIdx.x), knext, vnext);
     barrier();  // B0
 
     for (int l = 0; l < L; ++l) {
@@ -570,26 +603,33 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         const int down_tile = 4 * s + wave;
 
         // ---- attention block (engine/core.cpp:384-406, 606-626) ----
-        // K/V rows of this workgroup's passes from the cache (the rows at pos
-        // and pos + 1 come from LDS; positions past them, and all of an
-        // inactive workgroup's, read row 0).
         u32x4 kreg[PASSES][2], vreg[PASSES][2];
+        if constexpr (kEarlyKv) {
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int t = pass_base(p) + grp;
-            const int tl = mine && t < pos ? t : 0;
-            const global_u32x4* kp = global_rows(TL.keys + (head_base + tl) * 128);
-            kreg[p][0] = kp[c];
-            kreg[p][1] = kp[c + 8];
-        }
+            for (int p = 0; p < PASSES; ++p)
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p)
+                for (int e = 0; e < 2; ++e) {
+                    kreg[p][e] = knext[p][e];
+                    vreg[p][e] = vnext[p][e];
+                }
+        } else {
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const int t = pass_base(p) + 8 * wave + 4 * hf + vsub;
+            for (int p = 0; p < PASSES; ++p) {
+                const int t = pass_base(p) + grp;
                 const int tl = mine && t < pos ? t : 0;
-                vreg[p][hf] = global_rows(values + (head_base + tl) * 128)[vcg];
+                const global_u32x4* kp = global_rows(TL.keys + (head_base + tl) * 128);
+                kreg[p][0] = kp[c];
+                kreg[p][1] = kp[c + 8];
             }
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int t = pass_base(p) + 8 * wave + 4 * hf + vsub;
+                    const int tl = mine && t < pos ? t : 0;
+                    vreg[p][hf] = global_rows(values + (head_base + tl) * 128)[vcg];
+                }
+        }
         // RMSNorm of the residual: waves 0-3 hold entries 4 tid .. 4 tid + 3.
         float v[ROWS][4];
         if (tid < 256) {
@@ -1117,6 +1157,9 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             if (ok) ok = tok_get2(W[q] + kTokXOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
             m.r[q].x[2 * tid] = x0;
             m.r[q].x[2 * tid + 1] = x1;
+        }
+        if constexpr (kEarlyKv) {
+            if (l + 1 < L) load_kv(l + 1, tid, knext, vnext);
         }
         barrier();  // B13
     }
