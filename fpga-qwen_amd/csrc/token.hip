@@ -571,12 +571,13 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
                 vreg[p][hf] = global_rows(kv_values + (head_base + tl) * 128)[kl & 15];
             }
     };
-    // One row with up to 3 passes: each layer's K/V loads are issued at the
-    // end of the layer before (the first layer's here), after its last
-    // gather, so that they land under the barrier and the norm instead of
-    // holding up the norm waves at the layer start (token kernel 329 -> 327
-    // us at 109 positions, 477 -> 466 at 4034, the same bits); more passes,
-    // or two rows, would spill, and load at the layer start.
+    // One row with up to 3 passes: each layer's K/V loads are issued in the
+    // last interval of the layer before (the first layer's here): by the
+    // waves that do not fold as it starts, by the folding waves after their
+    // fold, so that they land while the fold is gathered and under the norm
+    // instead of holding up the norm waves at the layer start (token kernel
+    // 329 -> 325 us at 109 positions, 477 -> 457 at 4034, the same bits);
+    // more passes, or two rows, would spill, and load at the layer start.
     constexpr bool kEarlyKv = ROWS == 1 && PASSES <= 3;
     u32x4 knext[PASSES][2], vnext[PASSES][2];
     if constexpr (kEarlyKv) load_kv(0, int(threadIdx.x), knext, vnext);
@@ -1141,6 +1142,12 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         // Fold 2: wave q forms rows 32 s .. + 31 of row q's xm + the 8 down
         // slices (the tree of the two-kernel path), posted inside the XCD;
         // every thread gathers two entries of each row's next residual.
+        // The waves that do not fold issue the next layer's K/V loads first
+        // (their polls cannot succeed before the folds are posted anyway);
+        // the folding waves after their fold.
+        if constexpr (kEarlyKv) {
+            if (l + 1 < L && wave >= ROWS) load_kv(l + 1, tid, knext, vnext);
+        }
         if (wave < ROWS && lane < 32) {
             const int row = 32 * s + lane;
             const uint64_t* base = W[wave] + kTokDCrossOffset + row;
@@ -1151,15 +1158,15 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             if (ok) ok = tok_gather<8, kStaggerCross>(words, tag, d8, 0xffu, a.stall, spins);
             exchange_put(W[wave] + kTokXOffset + g * kHidden + row, fold_slices(m.r[wave].u.n.xm[row], d8), tag);
         }
+        if constexpr (kEarlyKv) {
+            if (l + 1 < L && wave < ROWS) load_kv(l + 1, tid, knext, vnext);
+        }
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
             float x0 = 0.f, x1 = 0.f;
             if (ok) ok = tok_get2(W[q] + kTokXOffset + g * kHidden + 2 * tid, tag, x0, x1, a.stall, spins);
             m.r[q].x[2 * tid] = x0;
             m.r[q].x[2 * tid + 1] = x1;
-        }
-        if constexpr (kEarlyKv) {
-            if (l + 1 < L) load_kv(l + 1, tid, knext, vnext);
         }
         barrier();  // B13
     }
