@@ -91,8 +91,16 @@ static_assert(kRegQkv / 1024 == 8 * kLoadWaves && kRegO / 1024 == kLoadsO * kLoa
 //   gate/up(l) in interval 8: prefetch 0-1, down, QKV(l + 1) 0-6,
 //     O(l + 1) 0-2 (less prefetch 0, issued with gate/up 9-12)     = 18
 //   down(l) in interval 10: prefetch 1, QKV(l + 1), O(l + 1)       = 15
+// In the split form the partial merge (interval 5) stores and polls behind
+// whatever the CU still has in flight, and beyond ~1000 positions the
+// prefetch makes intervals 3-4 ask for more than HBM delivers in them: so
+// there prefetch 1 goes out in interval 8 (before O(l + 1) 0-2) and
+// QKV(l + 1) 3-4 after B6b, and the O(l) wait allows one load fewer (the
+// other counts stay: prefetch 1 is still issued after down(l) and before
+// the gate/up wait).
 constexpr int kAfterQkv = 5;
 constexpr int kAfterO = 3 + kLoadsGu + kLoadsPrefetch + kLoadsDown + 3;
+constexpr int kAfterOSplit = kAfterO - 1;
 constexpr int kAfterGu = 1 + kLoadsDown + 1 + 7 + 3;
 constexpr int kAfterDown = 1 + kLoadsQkv + kLoadsO;
 static_assert(kAfterO == 27 && kAfterGu == 18 && kAfterDown == 15, "wait counts of the load plan");
@@ -455,6 +463,7 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         const int lw = __builtin_amdgcn_readfirstlane(wave - kComputeWaves);
         const Loader<ROWS> ld{a, m, g, s, lw, lane, a.context, a.pos};
         const bool pf = a.prefetch != 0;
+        constexpr bool kSplitPlan = ROWS == 1 && !FULL;  // the split form's moved loads (above)
         if constexpr (ROWS == 1) {
             // QKV(0) and O(0) in the order of intervals 4-9 of a layer.
             ld.qkv_range(0, 0, 3);
@@ -481,21 +490,25 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             barrier();  // B4
             if constexpr (ROWS == 1) ld.down_range(l, 0, kLoadsDown);
             if (!last) {
-                ld.prefetch(l + 1, 1, pf);
+                if (!kSplitPlan) ld.prefetch(l + 1, 1, pf);
                 ld.qkv_range(l + 1, 0, 3);
             }
             if (last) wait_vmcnt<0>();
-            else wait_vmcnt<ROWS == 1 ? kAfterO : kPairAfterO>();  // O(l)
+            else wait_vmcnt<ROWS == 2 ? kPairAfterO : kSplitPlan ? kAfterOSplit : kAfterO>();  // O(l)
             barrier();  // B5
-            if (!last) ld.qkv_range(l + 1, 3, 2);
+            if (!kSplitPlan && !last) ld.qkv_range(l + 1, 3, 2);
             barrier();  // B6
             if (!FULL) barrier();  // B6b
+            if (kSplitPlan && !last) ld.qkv_range(l + 1, 3, 2);
             if (!last) ld.qkv_range(l + 1, 5, 2);
             barrier();  // B7: O(l) is used
             if constexpr (ROWS == 2) ld.down_range(l, 0, 3);
             barrier();  // B8
             if constexpr (ROWS == 1) {
-                if (!last) ld.o_range(l + 1, 0, 3);
+                if (!last) {
+                    if (kSplitPlan) ld.prefetch(l + 1, 1, pf);
+                    ld.o_range(l + 1, 0, 3);
+                }
             } else {
                 ld.down_range(l, 3, 3);
             }
