@@ -33,13 +33,16 @@ __device__ __forceinline__ float chain8(float acc, u32x4 w, float4 xa, float4 xb
     return acc;
 }
 
-// The value of lane (this lane ^ OFF). Inside a 16-lane row the exchange
-// uses DPP row moves (quad_perm for 1 and 2; row_shl / row_shr plus a lane
-// select for 4 and 8) at register speed instead of the cross-lane permute
-// through the LDS unit; 16 and 32 use the permute. Every lane receives the
-// same value as from __shfl_xor, so reductions keep their exact order. The
-// lane select reads threadIdx.x, so callers run one-dimensional workgroups
-// (threadIdx.x % 64 is the lane), as every decode kernel does.
+// The value of lane (this lane ^ OFF), at register speed instead of the
+// cross-lane permute through the LDS unit (a round trip of 100+ clocks on
+// the dependent chains of the reductions): inside a 16-lane row DPP row
+// moves (quad_perm for 1 and 2; row_shl / row_shr plus a lane select for 4
+// and 8), across rows the gfx950 row swaps (v_permlane16_swap,
+// v_permlane32_swap; token kernel 324.5 -> 322.6 us at 109 positions, 353.5
+// -> 348.3 at 201). Every lane receives the same value as from __shfl_xor,
+// so reductions keep their exact order. The lane select reads threadIdx.x,
+// so callers run one-dimensional workgroups (threadIdx.x % 64 is the lane),
+// as every decode kernel does.
 template <int OFF>
 __device__ __forceinline__ int xor_lanes_bits(int v) {
     static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "power-of-two lane offset");
@@ -51,8 +54,17 @@ __device__ __forceinline__ int xor_lanes_bits(int v) {
         const int up = __builtin_amdgcn_update_dpp(v, v, 0x100 + OFF, 0xF, 0xF, false);  // row_shl: lane + OFF
         const int down = __builtin_amdgcn_update_dpp(v, v, 0x110 + OFF, 0xF, 0xF, false);  // row_shr: lane - OFF
         return (threadIdx.x & OFF) ? down : up;
+    } else if constexpr (OFF == 16) {
+        // Odd 16-lane rows of the first operand trade places with even rows
+        // of the second: with v in both, the first holds lane - 16 in the
+        // odd rows and the second lane + 16 in the even rows.
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return int((threadIdx.x & 16) ? r[0] : r[1]);
     } else {
-        return __shfl_xor(v, OFF);
+        // The upper half of the first operand trades places with the lower
+        // half of the second.
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return int((threadIdx.x & 32) ? r[0] : r[1]);
     }
 }
 template <int OFF>
