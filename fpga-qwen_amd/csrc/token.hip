@@ -97,7 +97,9 @@ static_assert(kRegQkv / 1024 == 8 * kLoadWaves && kRegO / 1024 == kLoadsO * kLoa
 // there prefetch 1 goes out in interval 8 (before O(l + 1) 0-2) and
 // QKV(l + 1) 3-4 after B6b, and the O(l) wait allows one load fewer (the
 // other counts stay: prefetch 1 is still issued after down(l) and before
-// the gate/up wait).
+// the gate/up wait). With two passes (beyond 2048 positions) only load
+// waves 2-3 move their prefetch 1; waves 0-1 keep it in interval 4, so the
+// two windows share it (each wave's waits count its own loads).
 constexpr int kAfterQkv = 5;
 constexpr int kAfterO = 3 + kLoadsGu + kLoadsPrefetch + kLoadsDown + 3;
 constexpr int kAfterOSplit = kAfterO - 1;
@@ -464,6 +466,7 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
         const Loader<ROWS> ld{a, m, g, s, lw, lane, a.context, a.pos};
         const bool pf = a.prefetch != 0;
         constexpr bool kSplitPlan = ROWS == 1 && !FULL;  // the split form's moved loads (above)
+        const bool late_pf = kSplitPlan && (PASSES == 1 || lw >= 2);  // prefetch 1 after fold 1
         if constexpr (ROWS == 1) {
             // QKV(0) and O(0) in the order of intervals 4-9 of a layer.
             ld.qkv_range(0, 0, 3);
@@ -490,11 +493,12 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             barrier();  // B4
             if constexpr (ROWS == 1) ld.down_range(l, 0, kLoadsDown);
             if (!last) {
-                if (!kSplitPlan) ld.prefetch(l + 1, 1, pf);
+                if (!late_pf) ld.prefetch(l + 1, 1, pf);
                 ld.qkv_range(l + 1, 0, 3);
             }
             if (last) wait_vmcnt<0>();
-            else wait_vmcnt<ROWS == 2 ? kPairAfterO : kSplitPlan ? kAfterOSplit : kAfterO>();  // O(l)
+            else if (late_pf) wait_vmcnt<kAfterOSplit>();
+            else wait_vmcnt<ROWS == 2 ? kPairAfterO : kAfterO>();  // O(l)
             barrier();  // B5
             if (!kSplitPlan && !last) ld.qkv_range(l + 1, 3, 2);
             barrier();  // B6
@@ -506,7 +510,7 @@ __global__ __launch_bounds__(kTokenThreads) void token_kernel(const TokenLaunch 
             barrier();  // B8
             if constexpr (ROWS == 1) {
                 if (!last) {
-                    if (kSplitPlan) ld.prefetch(l + 1, 1, pf);
+                    if (late_pf) ld.prefetch(l + 1, 1, pf);
                     ld.o_range(l + 1, 0, 3);
                 }
             } else {
